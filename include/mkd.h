@@ -1,0 +1,233 @@
+/*
+ * mkd.h -- C ABI of the MI355X (gfx950) MoE decode library (libmkd.so).
+ *
+ * The library implements the token-generation hot path of a Mixture-of-Experts
+ * decoder layer:  rmsnorm_tkg -> attention_block_tkg -> router_topk -> moe_tkg,
+ * and the multi-layer decode step that chains them.  Each entry point below
+ * names the reference operator it replaces (paths relative to the
+ * KevGomes1403/nki-moe-megakernel checkout).
+ *
+ * Conventions
+ *  - Every pointer argument is a DEVICE pointer unless stated otherwise; the
+ *    caller owns all buffers.  The library never allocates device memory: any
+ *    temporary storage comes from a caller-provided workspace whose size is
+ *    reported by the matching *_workspace_bytes() query.
+ *  - `stream` is a hipStream_t passed as void* (NULL = default stream).  All
+ *    calls are asynchronous and stream-ordered; none synchronise the host.
+ *  - Return value: 0 on success, a negative MKD_ERR_* code otherwise; the
+ *    message is available from mkd_last_error() (thread-local, host memory).
+ *  - bf16 tensors are raw 16-bit bfloat16 bit patterns; fp32 are IEEE floats.
+ *  - KV caches are updated IN PLACE (the reference returns them aliased).
+ */
+#ifndef MKD_H_
+#define MKD_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MKD_OK 0
+#define MKD_ERR_INVALID (-1)     /* bad shape / argument value            */
+#define MKD_ERR_NULL (-2)        /* required pointer is NULL               */
+#define MKD_ERR_UNSUPPORTED (-3) /* valid request this build cannot do     */
+#define MKD_ERR_WORKSPACE (-4)   /* workspace too small                    */
+#define MKD_ERR_HIP (-5)         /* HIP runtime / launch failure           */
+
+#define MKD_DT_BF16 0
+#define MKD_DT_F32 1
+
+/* Router modes (bit field) -- router_topk.py:519-562 pipeline flags. */
+#define MKD_ROUTER_SIGMOID 1   /* act_fn: 0 softmax, 1 sigmoid                     */
+#define MKD_ROUTER_PRE_NORM 2  /* router_pre_norm: activation before top-k (ACT1)  */
+#define MKD_ROUTER_NORM_TOPK 4 /* norm_topk_prob: L1-renormalise the top-k          */
+#define MKD_ROUTER_QWEN 8      /* Qwen fused flow (moe_fused_nki.py:159-276,404-418) */
+
+/* Expert activation (moe_tkg activation_fn) */
+#define MKD_ACT_SILU 0
+#define MKD_ACT_SWISH 1 /* g * sigmoid(alpha * g), GPT-OSS alpha = 1.702 */
+
+/* Affinity scaling (moe_tkg expert_affinities_scaling_mode) */
+#define MKD_SCALE_NONE 0
+#define MKD_SCALE_POST 1
+
+int mkd_version(void);
+const char* mkd_last_error(void);
+
+/* ---------------------------------------------------------------------------
+ * rmsnorm_tkg -- replaces nki_kernels/norm/rmsnorm_tkg.py:49 (math :318-454).
+ * input [rows, hidden] (bf16 or fp32), gamma [hidden] bf16, output [rows, hidden]
+ * in output_dtype.  y = (x * gamma) * rsqrt(sum(x^2) / hidden_actual + eps).
+ * hidden % 8 == 0, hidden <= 8192; hidden_actual <= 0 means hidden.
+ * ------------------------------------------------------------------------- */
+int mkd_rmsnorm_tkg(const void* input, int input_dtype, const void* gamma, void* output,
+                    int output_dtype, int rows, int hidden, int hidden_actual, float eps,
+                    void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Weight repacking into the library's MFMA fragment layout.  Replaces the
+ * layout conversion of convert_qwen3_moe_hf_to_neuron_state_dict
+ * (megakernels/qwen3_moe/qwen_with_megakernel.py:171-271), which produces the
+ * NKI layouts.  Source element (g, n, k) of a logical [groups][n][k] bf16
+ * matrix (output feature n, contraction index k) is read at
+ *   src + g*g_stride + n*row_stride + k*col_stride      (elements).
+ * interleave_half > 0 (fused gate/up) pairs row block j of rows [0, half)
+ * with row block j of rows [half, 2*half).  n % 16 == 0, k % 32 == 0.
+ * ------------------------------------------------------------------------- */
+size_t mkd_packed_bytes(int groups, int n, int k);
+int mkd_pack_weights(const void* src, void* dst, int groups, int n, int k, long long g_stride,
+                     long long row_stride, long long col_stride, int interleave_half,
+                     void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Dense decode projection on packed weights: y[r, :] = x[r, :] @ W^T (+ bias)
+ * (the matmul of qkv_tkg, nki_kernels/attention/qkv_tkg.py:71, and of
+ * output_projection_tkg, nki_kernels/attention/output_projection_tkg.py:66).
+ * x [rows, k] (bf16, or fp32 for the router), w packed [n, k], bias [n] bf16
+ * or NULL, y [rows, n] in y_dtype.  With `residual` (bf16 [rows, n], y_dtype
+ * bf16) the result is bf16(residual + bf16(x @ W^T)).  rows <= 128.
+ * ------------------------------------------------------------------------- */
+int mkd_linear(const void* x, int x_dtype, int ldx, int rows, const void* w_packed, int n, int k,
+               const void* bias, void* y, int y_dtype, int ldy, const void* residual,
+               void* stream);
+
+/* ---------------------------------------------------------------------------
+ * router_topk -- replaces nki_kernels/moe/router_topk.py:69 (x in HBM, [T, H]).
+ * logits = x @ w (+ w_bias) in fp32 (w packed from the reference [H, E]
+ * layout as n=E, k=H); then the pipeline selected by `mode`.
+ * Outputs: router_logits [T, E] fp32, expert_index [T, k] int32,
+ * expert_affinities [T, E] fp32 (scattered top-k, or full activation for the
+ * (ACT1, topK) pipeline), topk_affinities [T, k] fp32 (may be NULL).
+ * E <= 512, k <= 8, T <= 128.  Ties resolve to the lowest expert index.
+ * ------------------------------------------------------------------------- */
+int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_packed, int E,
+                    const void* w_bias, float* router_logits, float* expert_affinities,
+                    int* expert_index, float* topk_affinities, int k, int mode, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * moe_tkg (selective experts, bf16) -- replaces nki_kernels/moe/moe_tkg.py:56
+ * with is_all_expert=False (selective_expert_impl.py:84-519).
+ * hidden [T, H] bf16; gate_up packed per expert from [E, H, 2, I]
+ * (n = 2I interleaved, k = H); down packed per expert from [E, I, H] (n = H,
+ * k = I); expert_index [T, K] int32; slot scales: expert_affinities [T, E]
+ * fp32 gathered at the selected experts when scaling == MKD_SCALE_POST, else 1.
+ * Optional gate_up_bias [E, 2, I] and down_bias [E, H] (bf16).  Clamps are
+ * applied when finite (gate <= gate_hi, gate >= gate_lo, up in [up_lo, up_hi]).
+ * round_qwen = 1 emulates the Qwen fused kernel's bf16 rounding points
+ * (moe_fused_nki.py:506-527).  output [T, H] bf16; with residual (bf16 [T,H])
+ * output = bf16(residual + bf16(moe)).  T <= 128.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* hidden;          /* [T, H] bf16                    */
+  const void* gate_up_packed;  /* E x packed [2I, H]             */
+  const void* down_packed;     /* E x packed [H, I]              */
+  const float* expert_affinities; /* [T, E] or NULL               */
+  const float* slot_weights;   /* [T*K] or NULL (overrides gather) */
+  const int* expert_index;     /* [T, K]                         */
+  const void* gate_up_bias;    /* [E, 2, I] bf16 or NULL         */
+  const void* down_bias;       /* [E, H] bf16 or NULL            */
+  const void* residual;        /* [T, H] bf16 or NULL            */
+  void* output;                /* [T, H] bf16                    */
+  float* output_f32;           /* [T, H] fp32 or NULL            */
+  int T, H, E, I, K;
+  int scaling_mode;            /* MKD_SCALE_*                    */
+  int activation;              /* MKD_ACT_*                      */
+  float alpha;                 /* swish alpha                    */
+  float gate_hi, gate_lo, up_hi, up_lo; /* +-INFINITY = no clamp */
+  int round_qwen;
+} mkd_moe_args;
+size_t mkd_moe_workspace_bytes(int T, int H, int E, int I, int K);
+int mkd_moe_tkg(const mkd_moe_args* args, void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * attention_block_tkg -- replaces nki_kernels/attention/attention_block_tkg.py:83
+ * for S_tkg = 1 (one new token per sequence), generalised from one kv head per
+ * call to nkv >= 1 (GQA).  Stages (attention_block_tkg.py:359-583): optional
+ * RMSNorm(X) -> QKV projection (+bias) -> optional pre-RoPE per-head RMSNorm ->
+ * RoPE (contiguous halves) -> decode attention over the cache window (+ the
+ * active token) with optional 0/1 mask and sink -> in-place KV scatter at
+ * kv_cache_update_idx -> output projection (+bias).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  const void* X;               /* [B, H] bf16                                    */
+  const void* rmsnorm_gamma;   /* [H] bf16 or NULL (no pre-attention norm)       */
+  float rmsnorm_eps;
+  int rmsnorm_order;           /* 0: (x*g)*rinv, 1: (x*rinv)*g                   */
+  const void* w_qkv_packed;    /* packed [(nq + 2 nkv) d, H]                     */
+  const void* bias_qkv;        /* [(nq + 2 nkv) d] bf16 or NULL                  */
+  const void* q_norm;          /* [d] bf16 or NULL                               */
+  const void* k_norm;          /* [d] bf16 or NULL                               */
+  float qk_eps;
+  const float* cos;            /* [B, d] fp32 (halves duplicated) or NULL        */
+  const float* sin;            /* [B, d] fp32 or NULL                            */
+  void* k_cache;               /* [B, nkv, S_max, d] bf16, updated in place      */
+  void* v_cache;
+  const int* n_prior;          /* [B] prior positions attended (t < n_prior[b])  */
+  const uint8_t* mask;         /* [S_ctx, B, nq] uint8 (1 attend) or NULL        */
+  int mask_s_ctx;              /* S_ctx of mask (active token = S_ctx - 1)       */
+  const float* sink;           /* [nq] fp32 or NULL                              */
+  float softmax_scale;         /* <= 0: 1/sqrt(d)                                */
+  int update_cache;
+  const int* kv_cache_update_idx; /* [B] row to write; < 0 or >= S_max skips     */
+  const void* w_out_packed;    /* packed [H_out, nq d] or NULL (return attention) */
+  const void* bias_out;        /* [H_out] bf16 or NULL                           */
+  const void* residual;        /* [B, H_out] bf16 or NULL: out = bf16(res + o)   */
+  void* out;                   /* [B, H_out] bf16, or [B, nq d] bf16 without W_out */
+  int B, H, H_out, nq, nkv, d, S_max;
+  int round_qwen;              /* emulate the Qwen kernel's bf16 rounding points */
+} mkd_attention_args;
+size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S_max);
+int mkd_attention_block_tkg(const mkd_attention_args* args, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Multi-layer Qwen3-MoE decode step -- replaces the megakernel
+ * transformer_qwen3_moe_tkg_multilayer (megakernels/qwen3_moe/
+ * transformer_qwen.py:68-417, factory :502-505): for each layer
+ *   r = x + attn(rmsnorm(x));  x = r + moe(rmsnorm(r))
+ * with the residual stream in bf16 and the KV caches updated in place at
+ * position_ids[b].  All weight pointers are per-layer arrays in HOST memory
+ * holding device pointers to packed weights.
+ * ------------------------------------------------------------------------- */
+typedef struct {
+  int num_layers, H, nq, nkv, d, E, K, I, S_max;
+  float eps;
+  const void* const* w_qkv;    /* packed [(nq + 2 nkv) d, H]             */
+  const void* const* w_o;      /* packed [H, nq d]                       */
+  const void* const* q_norm;   /* [d] bf16                               */
+  const void* const* k_norm;   /* [d] bf16                               */
+  const void* const* ln_in;    /* [H] bf16                               */
+  const void* const* ln_post;  /* [H] bf16                               */
+  const void* const* router;   /* packed [E, H]                          */
+  const void* const* gate_up;  /* E x packed [2I, H] (interleaved)       */
+  const void* const* down;     /* E x packed [H, I]                      */
+  void* const* k_cache;        /* [B, nkv, S_max, d] bf16                */
+  void* const* v_cache;
+  const float* inv_freq;       /* [d/2] fp32 device, RoPE inverse freqs  */
+} mkd_qwen3_model;
+size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B);
+/* hidden [B, H] bf16 in/out; position_ids [B] int32 (device); cos/sin [B, d]
+ * fp32 or NULL (then generated from position_ids and inv_freq). */
+int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
+                            const int* position_ids, const float* cos, const float* sin,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Decode-step epilogue (the NxDI side of the reference step:
+ * qwen_with_megakernel.py:533-594, main.py:390-398): embedding gather, final
+ * RMSNorm (HF order), lm_head on packed [V, H], greedy arg-max.
+ * ------------------------------------------------------------------------- */
+/* token_ids [B] int32 (ids outside [0, V) give zero rows), table [V, H] bf16, out [B, H]. */
+int mkd_embed(const int* token_ids, const void* table, void* out, int B, int H, int V,
+              void* stream);
+size_t mkd_lm_head_workspace_bytes(int B, int H, int V);
+int mkd_lm_head_greedy(const void* hidden, const void* ln_f, float eps, const void* lm_head_packed,
+                       int B, int H, int V, float* logits, int* next_tokens, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MKD_H_ */

@@ -1,0 +1,155 @@
+"""attention_block_tkg operator (reference: nki_kernels/attention/attention_block_tkg.py:83-583)."""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib as L
+from . import packing
+from .common_types import QuantizationType
+
+U32_MAX = 0xFFFFFFFF
+
+
+def attention_block_tkg(
+    X: torch.Tensor, X_hidden_dim_actual: Optional[int],
+    rmsnorm_X_enabled: bool, rmsnorm_X_eps: Optional[float], rmsnorm_X_gamma: Optional[torch.Tensor],
+    W_qkv: torch.Tensor, bias_qkv: Optional[torch.Tensor], quantization_type_qkv: QuantizationType,
+    weight_dequant_scale_qkv: Optional[torch.Tensor], input_dequant_scale_qkv: Optional[torch.Tensor],
+    rmsnorm_QK_pre_rope_enabled: bool, rmsnorm_QK_pre_rope_eps: float,
+    rmsnorm_QK_pre_rope_W_Q: Optional[torch.Tensor], rmsnorm_QK_pre_rope_W_K: Optional[torch.Tensor],
+    cos: Optional[torch.Tensor], sin: Optional[torch.Tensor], rope_contiguous_layout: bool,
+    rmsnorm_QK_post_rope_enabled: bool, rmsnorm_QK_post_rope_eps: float,
+    rmsnorm_QK_post_rope_W_Q: Optional[torch.Tensor], rmsnorm_QK_post_rope_W_K: Optional[torch.Tensor],
+    K_cache_transposed: bool, active_blocks_table: Optional[torch.Tensor],
+    K_cache: torch.Tensor, V_cache: torch.Tensor, attention_mask: torch.Tensor,
+    sink: Optional[torch.Tensor], update_cache: bool, kv_cache_update_idx: Optional[torch.Tensor],
+    W_out: Optional[torch.Tensor], bias_out: Optional[torch.Tensor],
+    quantization_type_out: QuantizationType, weight_dequant_scale_out: Optional[torch.Tensor],
+    input_dequant_scale_out: Optional[torch.Tensor], transposed_out: bool, out_in_sb: bool,
+    softmax_scale: Optional[float] = None, enable_fa_s_prior_tiling: bool = True,
+    k_scale: Optional[torch.Tensor] = None, v_scale: Optional[torch.Tensor] = None,
+    sbm=None, skip_attention: bool = False, KVDP: int = 1, KVDP_replica_group=None,
+):
+    """Fused decode attention block; returns (out, K_cache, V_cache).
+
+    Shapes follow the reference docstring (attention_block_tkg.py:140-289):
+    X [B, S_tkg, H]; W_qkv [H, d*(q_heads + 2*kv_heads)] packed Q | K | V;
+    cos/sin [d/2, B, S_tkg]; K_cache/V_cache [B, S_max, d] (one kv head, as in
+    the reference) or [B, kv_heads, S_max, d] (this build's GQA
+    generalisation); attention_mask [S_ctx, B, q_heads, S_tkg] with the active
+    token in slot S_ctx - 1; kv_cache_update_idx [B, 1] (uint32 max = skip);
+    W_out [q_heads*d, H].  out is [B*S_tkg, H] (or [B, q_heads, d, S_tkg]
+    without W_out).  The caches are updated in place.
+
+    Supported: S_tkg = 1, flat (non-block) caches, no quantisation.  Other
+    reference options raise NotImplementedError; post-RoPE RMSNorm is applied
+    when enabled.  enable_fa_s_prior_tiling is a scheduling hint (the GPU path
+    always tiles the KV length).
+    """
+    if KVDP != 1:
+        raise NotImplementedError("KV data parallelism spans several devices; one GPU only")
+    if active_blocks_table is not None:
+        raise NotImplementedError("block (paged) KV cache is not supported by this operator yet")
+    if K_cache_transposed:
+        raise NotImplementedError("K_cache_transposed=True is not supported (K is stored [.., S, d])")
+    if transposed_out or out_in_sb or sbm is not None:
+        raise NotImplementedError("transposed/SBUF outputs have no GPU equivalent")
+    if skip_attention:
+        raise NotImplementedError("skip_attention is a test hook of the reference")
+    if quantization_type_qkv not in (None, QuantizationType.NONE) or \
+            quantization_type_out not in (None, QuantizationType.NONE) or \
+            k_scale is not None or v_scale is not None:
+        raise NotImplementedError("quantized QKV / output projection / FP8 KV are not supported")
+    if not rope_contiguous_layout and cos is not None:
+        raise NotImplementedError("interleaved RoPE layout is not supported")
+    if rmsnorm_QK_post_rope_enabled:
+        raise NotImplementedError("post-RoPE Q/K RMSNorm is not supported")
+    L.require_gpu(X, W_qkv, K_cache, V_cache, attention_mask)
+    B, S_tkg, H = X.shape
+    if S_tkg != 1:
+        raise NotImplementedError("only S_tkg = 1 (one new token per sequence) is supported")
+    d = V_cache.shape[-1]
+    if d % 2:
+        raise ValueError(f"d_head must be even, got {d}")
+    if K_cache.dim() == 3:
+        nkv = 1
+        S_max = K_cache.shape[1]
+    elif K_cache.dim() == 4:
+        nkv = K_cache.shape[1]
+        S_max = K_cache.shape[2]
+    else:
+        raise ValueError(f"K_cache must be 3-D or 4-D, got {tuple(K_cache.shape)}")
+    if tuple(K_cache.shape) != tuple(V_cache.shape):
+        raise ValueError("K_cache / V_cache shape mismatch")
+    if K_cache.shape[0] != B:
+        raise ValueError(f"V_cache batch mismatch: expected {B}, got {K_cache.shape[0]}")
+    I = W_qkv.shape[1]
+    if I % d:
+        raise ValueError(f"QKV weights must be packed as (q_heads + 2) * d_head, got I={I}, d_head={d}")
+    nq = I // d - 2 * nkv
+    S_ctx = attention_mask.shape[0]
+    if tuple(attention_mask.shape) != (S_ctx, B, nq, S_tkg):
+        raise ValueError(f"attention_mask shape mismatch: expected {(S_ctx, B, nq, S_tkg)}, got {tuple(attention_mask.shape)}")
+    if S_ctx - 1 > S_max:
+        raise ValueError(f"mask window S_ctx={S_ctx} exceeds cache capacity {S_max} + 1")
+    if rmsnorm_X_enabled and rmsnorm_X_gamma is not None and tuple(rmsnorm_X_gamma.shape) not in ((1, H), (H,)):
+        raise ValueError(f"rmsnorm_X_gamma must be (1, {H}), got {tuple(rmsnorm_X_gamma.shape)}")
+    if (cos is None) != (sin is None):
+        raise ValueError("cos and sin must be given together")
+    if cos is not None and tuple(cos.shape) != (d // 2, B, S_tkg):
+        raise ValueError(f"cos shape mismatch: expected ({d // 2}, {B}, {S_tkg}), got {tuple(cos.shape)}")
+    if update_cache and kv_cache_update_idx is None:
+        raise ValueError("update_cache=True needs kv_cache_update_idx")
+    if K_cache.dtype != torch.bfloat16 or X.dtype != torch.bfloat16:
+        raise ValueError("X and the KV caches must be bfloat16")
+
+    dev = X.device
+    wqkv = packing.packed_cached(W_qkv, packing.pack_in_out)
+    wout = packing.packed_cached(W_out, packing.pack_in_out) if W_out is not None else None
+    H_out = W_out.shape[1] if W_out is not None else 0
+    x = X.reshape(B, H).contiguous()
+    gamma = rmsnorm_X_gamma.reshape(-1).to(torch.bfloat16).contiguous() \
+        if (rmsnorm_X_enabled and rmsnorm_X_gamma is not None) else None
+    qn = kn = None
+    if rmsnorm_QK_pre_rope_enabled:
+        qn = rmsnorm_QK_pre_rope_W_Q.reshape(-1).to(torch.bfloat16).contiguous() \
+            if rmsnorm_QK_pre_rope_W_Q is not None else torch.ones(d, dtype=torch.bfloat16, device=dev)
+        kn = rmsnorm_QK_pre_rope_W_K.reshape(-1).to(torch.bfloat16).contiguous() \
+            if rmsnorm_QK_pre_rope_W_K is not None else torch.ones(d, dtype=torch.bfloat16, device=dev)
+    cos_f = sin_f = None
+    if cos is not None:
+        # [d/2, B, 1] -> [B, d] with the halves duplicated
+        cos_f = torch.cat([cos, cos], 0)[:, :, 0].t().float().contiguous()
+        sin_f = torch.cat([sin, sin], 0)[:, :, 0].t().float().contiguous()
+    mask_u8 = (attention_mask[:, :, :, 0] != 0).to(torch.uint8).contiguous()
+    n_prior = torch.full((B,), S_ctx - 1, dtype=torch.int32, device=dev)
+    wpos = None
+    if update_cache:
+        idx = kv_cache_update_idx.reshape(-1).to(torch.int64)
+        wpos = torch.where(idx == U32_MAX, torch.full_like(idx, -1), idx).to(torch.int32).contiguous()
+    sink_f = sink.reshape(-1).float().contiguous() if sink is not None else None
+    bqkv = bias_qkv.reshape(-1).to(torch.bfloat16).contiguous() if bias_qkv is not None else None
+    bout = bias_out.reshape(-1).to(torch.bfloat16).contiguous() if bias_out is not None else None
+    out = torch.empty(B, H_out if W_out is not None else nq * d, dtype=torch.bfloat16, device=dev)
+    scale = float(softmax_scale) if softmax_scale is not None else 1.0 / math.sqrt(d)
+    args = L.AttentionArgs(
+        X=x.data_ptr(), rmsnorm_gamma=L.ptr(gamma),
+        rmsnorm_eps=float(rmsnorm_X_eps if rmsnorm_X_eps is not None else 1e-3), rmsnorm_order=0,
+        w_qkv_packed=wqkv.data_ptr(), bias_qkv=L.ptr(bqkv), q_norm=L.ptr(qn), k_norm=L.ptr(kn),
+        qk_eps=float(rmsnorm_QK_pre_rope_eps), cos=L.ptr(cos_f), sin=L.ptr(sin_f),
+        k_cache=K_cache.data_ptr(), v_cache=V_cache.data_ptr(), n_prior=n_prior.data_ptr(),
+        mask=mask_u8.data_ptr(), mask_s_ctx=S_ctx, sink=L.ptr(sink_f), softmax_scale=scale,
+        update_cache=int(bool(update_cache)), kv_cache_update_idx=L.ptr(wpos),
+        w_out_packed=L.ptr(wout), bias_out=L.ptr(bout), residual=None, out=out.data_ptr(),
+        B=B, H=H, H_out=H_out, nq=nq, nkv=nkv, d=d, S_max=S_max, round_qwen=0)
+    lib = L.load()
+    ws = torch.empty(max(lib.mkd_attention_workspace_bytes(B, H, nq, nkv, d, S_max), 256),
+                     dtype=torch.uint8, device=dev)
+    rc = lib.mkd_attention_block_tkg(args, ws.data_ptr(), ws.numel(), L.stream_ptr(dev))
+    L.check(rc, "attention_block_tkg")
+    if W_out is None:
+        out = out.reshape(B, nq, d, 1)
+    return out, K_cache, V_cache

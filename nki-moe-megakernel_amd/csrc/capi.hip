@@ -1,0 +1,541 @@
+// extern "C" entry points of libmkd.so (declared in include/mkd.h).
+//
+// This layer validates shapes and pointers on the host, carves the caller's
+// workspace, and enqueues the kernels on the caller's stream.  It never
+// allocates device memory and never synchronises.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "common.h"
+#include "mkd_internal.h"
+#include "../../include/mkd.h"
+
+using namespace mkd;
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(MKD_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return MKD_OK;
+}
+
+#define MKD_REQUIRE(cond, code, ...) \
+  do {                               \
+    if (!(cond)) return fail(code, __VA_ARGS__); \
+  } while (0)
+
+#define MKD_TRY(expr, what)                   \
+  do {                                        \
+    int rc_ = hip_check((expr), what);        \
+    if (rc_) return rc_;                      \
+  } while (0)
+
+// Bump allocator over the caller's workspace (256-byte aligned slices).
+struct Carver {
+  char* base;
+  size_t cap, used = 0;
+  bool ok = true;
+  template <class T>
+  T* take(size_t count) {
+    const size_t bytes = (count * sizeof(T) + 255) & ~size_t(255);
+    if (used + bytes > cap) { ok = false; used += bytes; return nullptr; }
+    T* p = reinterpret_cast<T*>(base + used);
+    used += bytes;
+    return p;
+  }
+};
+
+int token_tiles(int T) { return T <= 16 ? 1 : (T <= 32 ? 2 : 4); }
+
+GemmArgs dense_args(const void* w, const void* x, int ldx, int N, int K, int T, void* y, int ldy) {
+  GemmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.w = reinterpret_cast<const uint16_t*>(w);
+  a.x = x;
+  a.ldx = ldx;
+  a.N = N;
+  a.K = K;
+  a.KW = choose_kw(K);
+  a.T = T;
+  a.y = y;
+  a.ldy = ldy;
+  a.gate_hi = INFINITY; a.gate_lo = -INFINITY; a.up_hi = INFINITY; a.up_lo = -INFINITY;
+  return a;
+}
+
+int check_gemm_dims(int N, int K, int rb) {
+  MKD_REQUIRE(N > 0 && N % (16 * rb) == 0, MKD_ERR_INVALID, "output features %d must be a multiple of %d", N, 16 * rb);
+  MKD_REQUIRE(K > 0 && K % 32 == 0, MKD_ERR_INVALID, "contraction %d must be a multiple of 32", K);
+  MKD_REQUIRE(choose_kw(K) > 0, MKD_ERR_UNSUPPORTED, "contraction %d too large (max 8192)", K);
+  return MKD_OK;
+}
+
+// Dense launch with the token count split into tiles of <= 64 rows.
+int dense_gemm(GemmArgs a, int epi, bool xf32, hipStream_t s) {
+  const int T = a.T;
+  for (int t0 = 0; t0 < T; t0 += 64) {
+    GemmArgs b = a;
+    const int tt = T - t0 < 64 ? T - t0 : 64;
+    b.T = tt;
+    b.x = static_cast<const char*>(a.x) + (size_t)t0 * a.ldx * (xf32 ? 4 : 2);
+    const int ysz = (epi == EPI_F32 || epi == EPI_SCALE_F32) ? 4 : 2;
+    b.y = static_cast<char*>(a.y) + (size_t)t0 * a.ldy * ysz;
+    if (a.residual) b.residual = a.residual + (size_t)t0 * a.ldy;
+    MKD_TRY(gemm_launch(b, epi, xf32, token_tiles(tt), 1, tt, s), "gemm launch");
+  }
+  return MKD_OK;
+}
+
+struct MoeWs {
+  int *n_groups, *grp_expert, *grp_count, *grp_offset, *pair_token, *pair_slot, *idx;
+  float *slot_w, *ybuf;
+  uint16_t* hbuf;
+};
+
+MoeWs carve_moe(Carver& c, int T, int H, int E, int I, int K) {
+  MoeWs w;
+  w.n_groups = c.take<int>(1);
+  w.grp_expert = c.take<int>(E);
+  w.grp_count = c.take<int>(E);
+  w.grp_offset = c.take<int>(E);
+  w.pair_token = c.take<int>((size_t)T * K);
+  w.pair_slot = c.take<int>((size_t)T * K);
+  w.idx = c.take<int>((size_t)T * K);
+  w.slot_w = c.take<float>((size_t)T * K);
+  w.hbuf = c.take<uint16_t>((size_t)T * K * I);
+  w.ybuf = c.take<float>((size_t)T * K * H);
+  return w;
+}
+
+__global__ void gather_slot_weights(const float* aff, const int* idx, int T, int E, int K,
+                                    float* slot_w) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p >= T * K) return;
+  const int e = idx[p];
+  slot_w[p] = (aff && e >= 0 && e < E) ? aff[(long long)(p / K) * E + e] : (aff ? 0.0f : 1.0f);
+}
+
+__global__ void copy_slot_weights(const float* src, int n, float* dst) {
+  const int p = blockIdx.x * blockDim.x + threadIdx.x;
+  if (p < n) dst[p] = src[p];
+}
+
+// The expert FFN on an already-routed batch: routing tables -> gate/up -> down -> finalize.
+int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, const int* idx,
+             const float* slot_w, const uint16_t* gu_bias, const uint16_t* dn_bias,
+             const uint16_t* resid, uint16_t* out, float* out_f32, int T, int H, int E, int I,
+             int K, int act, float alpha, float ghi, float glo, float uhi, float ulo, int round_qwen,
+             MoeWs& w, hipStream_t s) {
+  MKD_TRY(moe_route_launch(idx, T, K, E, w.n_groups, w.grp_expert, w.grp_count, w.grp_offset,
+                           w.pair_token, w.pair_slot, s), "moe_route");
+  const int gmax = E < T * K ? E : T * K;
+  // Routed experts see few tokens each (T*K/E on average), so one 16-token
+  // MFMA column tile per block; groups with more tokens use extra z-tiles.
+  const int tn = 1;
+  {  // gate/up + activation
+    GemmArgs a = dense_args(gate_up, hidden, H, 2 * I, H, T, w.hbuf, I);
+    a.w_group_stride = (long long)2 * I * H;
+    a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
+    a.n_groups = w.n_groups; a.pair_row = w.pair_token; a.pair_out_row = w.pair_slot;
+    a.bias = gu_bias; a.bias_group_stride = 2LL * I;
+    a.act = act; a.alpha = alpha; a.gate_hi = ghi; a.gate_lo = glo; a.up_hi = uhi; a.up_lo = ulo;
+    a.round_qwen = round_qwen;
+    MKD_TRY(gemm_launch(a, EPI_SWIGLU_BF16, false, tn, gmax, T, s), "moe gate_up");
+  }
+  {  // down, scaled by the slot affinity
+    GemmArgs a = dense_args(down, w.hbuf, I, H, I, T, w.ybuf, H);
+    a.w_group_stride = (long long)H * I;
+    a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
+    a.n_groups = w.n_groups; a.pair_row = w.pair_slot; a.pair_out_row = w.pair_slot;
+    a.pair_scale = slot_w;
+    a.bias = dn_bias; a.bias_group_stride = H;
+    MKD_TRY(gemm_launch(a, EPI_SCALE_F32, false, tn, gmax, T, s), "moe down");
+  }
+  MKD_TRY(moe_finalize_launch(w.ybuf, T, K, H, resid, out, out_f32, s), "moe finalize");
+  return MKD_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mkd_version(void) { return 1; }
+const char* mkd_last_error(void) { return g_err; }
+
+int mkd_rmsnorm_tkg(const void* input, int input_dtype, const void* gamma, void* output,
+                    int output_dtype, int rows, int hidden, int hidden_actual, float eps,
+                    void* stream) {
+  MKD_REQUIRE(input && gamma && output, MKD_ERR_NULL, "rmsnorm_tkg: null pointer");
+  MKD_REQUIRE(rows > 0, MKD_ERR_INVALID, "rmsnorm_tkg: rows must be > 0, got %d", rows);
+  MKD_REQUIRE(hidden > 0 && hidden % 8 == 0 && hidden <= 8192, MKD_ERR_INVALID,
+              "rmsnorm_tkg: hidden %d must be a multiple of 8 and <= 8192", hidden);
+  MKD_REQUIRE(input_dtype == MKD_DT_BF16 || input_dtype == MKD_DT_F32, MKD_ERR_INVALID, "rmsnorm_tkg: bad input dtype");
+  MKD_REQUIRE(output_dtype == MKD_DT_BF16 || output_dtype == MKD_DT_F32, MKD_ERR_INVALID, "rmsnorm_tkg: bad output dtype");
+  const int ha = hidden_actual > 0 ? hidden_actual : hidden;
+  MKD_REQUIRE(ha <= hidden, MKD_ERR_INVALID, "rmsnorm_tkg: hidden_actual %d > hidden %d", ha, hidden);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  MKD_TRY(rmsnorm_launch(input, input_dtype == MKD_DT_F32, nullptr, nullptr,
+                         static_cast<const uint16_t*>(gamma),
+                         output_dtype == MKD_DT_BF16 ? static_cast<uint16_t*>(output) : nullptr,
+                         output_dtype == MKD_DT_F32 ? static_cast<float*>(output) : nullptr, rows,
+                         hidden, hidden, ha, eps, 0, s), "rmsnorm launch");
+  return MKD_OK;
+}
+
+size_t mkd_packed_bytes(int groups, int n, int k) {
+  return (size_t)groups * (size_t)n * (size_t)k * 2;
+}
+
+int mkd_pack_weights(const void* src, void* dst, int groups, int n, int k, long long g_stride,
+                     long long row_stride, long long col_stride, int interleave_half,
+                     void* stream) {
+  MKD_REQUIRE(src && dst, MKD_ERR_NULL, "pack_weights: null pointer");
+  MKD_REQUIRE(groups > 0 && n > 0 && k > 0, MKD_ERR_INVALID, "pack_weights: empty shape");
+  if (int rc = check_gemm_dims(n, k, interleave_half > 0 ? 2 : 1)) return rc;
+  MKD_REQUIRE(interleave_half == 0 || (interleave_half * 2 == n && interleave_half % 16 == 0),
+              MKD_ERR_INVALID, "pack_weights: interleave_half %d must be n/2 and a multiple of 16", interleave_half);
+  MKD_TRY(pack_frag_launch(static_cast<const uint16_t*>(src), static_cast<uint16_t*>(dst), groups,
+                           n, k, g_stride, row_stride, col_stride, interleave_half,
+                           static_cast<hipStream_t>(stream)), "pack launch");
+  return MKD_OK;
+}
+
+int mkd_linear(const void* x, int x_dtype, int ldx, int rows, const void* w_packed, int n, int k,
+               const void* bias, void* y, int y_dtype, int ldy, const void* residual,
+               void* stream) {
+  MKD_REQUIRE(x && w_packed && y, MKD_ERR_NULL, "linear: null pointer");
+  MKD_REQUIRE(rows > 0 && rows <= 128, MKD_ERR_INVALID, "linear: rows %d must be in [1, 128]", rows);
+  if (int rc = check_gemm_dims(n, k, 1)) return rc;
+  MKD_REQUIRE(ldx >= k && ldy >= n, MKD_ERR_INVALID, "linear: leading dims too small");
+  MKD_REQUIRE(ldx % 8 == 0 && ldy % 4 == 0, MKD_ERR_INVALID, "linear: leading dims must be 16-byte aligned");
+  MKD_REQUIRE(!residual || y_dtype == MKD_DT_BF16, MKD_ERR_INVALID, "linear: residual needs bf16 output");
+  GemmArgs a = dense_args(w_packed, x, ldx, n, k, rows, y, ldy);
+  a.bias = static_cast<const uint16_t*>(bias);
+  a.residual = static_cast<const uint16_t*>(residual);
+  const int epi = residual ? EPI_RESID_BF16 : (y_dtype == MKD_DT_F32 ? EPI_F32 : EPI_BF16);
+  return dense_gemm(a, epi, x_dtype == MKD_DT_F32, static_cast<hipStream_t>(stream));
+}
+
+int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_packed, int E,
+                    const void* w_bias, float* router_logits, float* expert_affinities,
+                    int* expert_index, float* topk_affinities, int k, int mode, void* stream) {
+  MKD_REQUIRE(x && w_packed && router_logits && expert_index, MKD_ERR_NULL, "router_topk: null pointer");
+  MKD_REQUIRE(T > 0 && T <= 128, MKD_ERR_INVALID, "router_topk: T %d must be in [1, 128]", T);
+  MKD_REQUIRE(E > 0 && E <= 512, MKD_ERR_INVALID, "router_topk: E %d must be in [1, 512]", E);
+  MKD_REQUIRE(k >= 1 && k <= 8 && k <= E, MKD_ERR_INVALID, "router_topk: k %d must be in [1, 8]", k);
+  if (int rc = check_gemm_dims(E, H, 1)) return rc;
+  const bool pre = mode & MKD_ROUTER_PRE_NORM, norm = mode & MKD_ROUTER_NORM_TOPK;
+  MKD_REQUIRE(!(norm && !pre), MKD_ERR_INVALID, "router_topk: norm_topk_prob requires router_pre_norm");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  GemmArgs a = dense_args(w_packed, x, H, E, H, T, router_logits, E);
+  a.bias = static_cast<const uint16_t*>(w_bias);
+  if (int rc = dense_gemm(a, EPI_F32, x_dtype == MKD_DT_F32, s)) return rc;
+  MKD_TRY(router_topk_launch(router_logits, T, E, k, mode, expert_affinities, expert_index,
+                             topk_affinities, nullptr, s), "router_topk launch");
+  return MKD_OK;
+}
+
+size_t mkd_moe_workspace_bytes(int T, int H, int E, int I, int K) {
+  Carver c{nullptr, 0};
+  carve_moe(c, T, H, E, I, K);
+  return c.used;
+}
+
+int mkd_moe_tkg(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, void* stream) {
+  MKD_REQUIRE(p, MKD_ERR_NULL, "moe_tkg: null args");
+  MKD_REQUIRE(p->hidden && p->gate_up_packed && p->down_packed && p->expert_index && p->output,
+              MKD_ERR_NULL, "moe_tkg: null pointer");
+  MKD_REQUIRE(p->T > 0 && p->T <= 128, MKD_ERR_INVALID,
+              "moe_tkg: only T <= 128 tokens are supported in selective mode, got %d", p->T);
+  MKD_REQUIRE(p->E > 0 && p->E <= 512 && p->K >= 1 && p->K <= 8 && p->K <= p->E, MKD_ERR_INVALID,
+              "moe_tkg: bad E=%d / K=%d", p->E, p->K);
+  if (int rc = check_gemm_dims(2 * p->I, p->H, 2)) return rc;
+  if (int rc = check_gemm_dims(p->H, p->I, 1)) return rc;
+  MKD_REQUIRE(p->scaling_mode == MKD_SCALE_NONE || p->scaling_mode == MKD_SCALE_POST,
+              MKD_ERR_UNSUPPORTED, "moe_tkg: only NO_SCALE and POST_SCALE affinity scaling are supported");
+  MKD_REQUIRE(!(p->scaling_mode == MKD_SCALE_POST && !p->expert_affinities && !p->slot_weights),
+              MKD_ERR_NULL, "moe_tkg: POST_SCALE needs expert_affinities");
+  MKD_REQUIRE(p->activation == MKD_ACT_SILU || p->activation == MKD_ACT_SWISH, MKD_ERR_UNSUPPORTED,
+              "moe_tkg: unsupported activation %d", p->activation);
+  MKD_REQUIRE(workspace, MKD_ERR_NULL, "moe_tkg: null workspace");
+  Carver c{static_cast<char*>(workspace), workspace_bytes};
+  MoeWs w = carve_moe(c, p->T, p->H, p->E, p->I, p->K);
+  MKD_REQUIRE(c.ok, MKD_ERR_WORKSPACE, "moe_tkg: workspace %zu < %zu bytes", workspace_bytes, c.used);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int TK = p->T * p->K;
+  if (p->slot_weights) {
+    hipLaunchKernelGGL(copy_slot_weights, dim3((TK + 255) / 256), dim3(256), 0, s, p->slot_weights, TK, w.slot_w);
+  } else {
+    hipLaunchKernelGGL(gather_slot_weights, dim3((TK + 255) / 256), dim3(256), 0, s,
+                       p->scaling_mode == MKD_SCALE_POST ? p->expert_affinities : nullptr,
+                       p->expert_index, p->T, p->E, p->K, w.slot_w);
+  }
+  MKD_TRY(hipGetLastError(), "slot weights");
+  return moe_core(static_cast<const uint16_t*>(p->hidden), p->gate_up_packed, p->down_packed,
+                  p->expert_index, w.slot_w, static_cast<const uint16_t*>(p->gate_up_bias),
+                  static_cast<const uint16_t*>(p->down_bias),
+                  static_cast<const uint16_t*>(p->residual), static_cast<uint16_t*>(p->output),
+                  p->output_f32, p->T, p->H, p->E, p->I, p->K, p->activation, p->alpha,
+                  p->gate_hi, p->gate_lo, p->up_hi, p->up_lo, p->round_qwen, w, s);
+}
+
+// ---------------------------------------------------------------------------
+// attention block
+// ---------------------------------------------------------------------------
+static const int kChunk = 256;
+
+struct AttnWs {
+  uint16_t* hnorm;
+  float* qkv;
+  uint16_t *q, *kvn, *attn;
+  float *po, *pml;
+  int n_chunks;
+};
+
+static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_max) {
+  AttnWs w;
+  w.n_chunks = (S_max + 1 + kChunk - 1) / kChunk;
+  w.hnorm = c.take<uint16_t>((size_t)B * H);
+  w.qkv = c.take<float>((size_t)B * (nq + 2 * nkv) * d);
+  w.q = c.take<uint16_t>((size_t)B * nq * d);
+  w.kvn = c.take<uint16_t>((size_t)B * 2 * nkv * d);
+  w.attn = c.take<uint16_t>((size_t)B * nq * d);
+  w.po = c.take<float>((size_t)B * nq * w.n_chunks * d);
+  w.pml = c.take<float>((size_t)B * nq * w.n_chunks * 2);
+  return w;
+}
+
+size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S_max) {
+  Carver c{nullptr, 0};
+  carve_attn(c, B, H, nq, nkv, d, S_max);
+  return c.used;
+}
+
+static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos_for_rope,
+                          const float* inv_freq, hipStream_t s) {
+  const int qkv_n = (p->nq + 2 * p->nkv) * p->d;
+  // 1. optional RMSNorm
+  const void* xin = p->X;
+  if (p->rmsnorm_gamma) {
+    MKD_TRY(rmsnorm_launch(p->X, 0, nullptr, nullptr, static_cast<const uint16_t*>(p->rmsnorm_gamma),
+                           w.hnorm, nullptr, p->B, p->H, p->H, p->H, p->rmsnorm_eps,
+                           p->rmsnorm_order, s), "attn rmsnorm");
+    xin = w.hnorm;
+  }
+  // 2. QKV projection (fp32 out)
+  GemmArgs g = dense_args(p->w_qkv_packed, xin, p->H, qkv_n, p->H, p->B, w.qkv, qkv_n);
+  g.bias = static_cast<const uint16_t*>(p->bias_qkv);
+  if (int rc = dense_gemm(g, EPI_F32, false, s)) return rc;
+  // 3. q/k norm + RoPE + staging
+  AttnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.qkv = w.qkv; a.ld_qkv = qkv_n;
+  a.q_norm = static_cast<const uint16_t*>(p->q_norm);
+  a.k_norm = static_cast<const uint16_t*>(p->k_norm);
+  a.qk_eps = p->qk_eps;
+  a.cos = p->cos; a.sin = p->sin; a.inv_freq = inv_freq; a.pos = pos_for_rope;
+  a.q_out = w.q; a.kv_new = w.kvn;
+  a.k_cache = static_cast<uint16_t*>(p->k_cache);
+  a.v_cache = static_cast<uint16_t*>(p->v_cache);
+  a.cache_h_stride = (long long)p->S_max * p->d;
+  a.cache_b_stride = a.cache_h_stride * p->nkv;
+  a.n_prior = p->n_prior;
+  a.mask = p->mask; a.mask_s_ctx = p->mask_s_ctx;
+  a.sink = p->sink;
+  a.scale = p->softmax_scale > 0.f ? p->softmax_scale : 1.0f / sqrtf((float)p->d);
+  a.round_qwen = p->round_qwen;
+  a.B = p->B; a.nq = p->nq; a.nkv = p->nkv; a.d = p->d; a.S_max = p->S_max;
+  a.chunk = kChunk; a.n_chunks = w.n_chunks;
+  a.part_o = w.po; a.part_ml = w.pml;
+  a.attn_out = w.attn;
+  a.update_cache = p->update_cache;
+  a.write_pos = p->kv_cache_update_idx;
+  const int rope_mode = p->cos ? 1 : (inv_freq ? 2 : 0);
+  MKD_TRY(qk_prep_launch(a, rope_mode, p->round_qwen, s), "qk_prep");
+  MKD_TRY(attn_decode_launch(a, s), "attn_decode");
+  MKD_TRY(attn_combine_launch(a, s), "attn_combine");
+  // 5. output projection
+  if (p->w_out_packed) {
+    GemmArgs o = dense_args(p->w_out_packed, w.attn, p->nq * p->d, p->H_out, p->nq * p->d, p->B,
+                            p->out, p->H_out);
+    o.bias = static_cast<const uint16_t*>(p->bias_out);
+    o.residual = static_cast<const uint16_t*>(p->residual);
+    if (int rc = dense_gemm(o, p->residual ? EPI_RESID_BF16 : EPI_BF16, false, s)) return rc;
+  } else {
+    MKD_TRY(hipMemcpyAsync(p->out, w.attn, (size_t)p->B * p->nq * p->d * 2, hipMemcpyDeviceToDevice, s),
+            "attn copy");
+  }
+  return MKD_OK;
+}
+
+static int validate_attn(const mkd_attention_args* p) {
+  MKD_REQUIRE(p, MKD_ERR_NULL, "attention: null args");
+  MKD_REQUIRE(p->X && p->w_qkv_packed && p->k_cache && p->v_cache && p->n_prior && p->out,
+              MKD_ERR_NULL, "attention: null pointer");
+  MKD_REQUIRE(p->B > 0 && p->B <= 128, MKD_ERR_INVALID, "attention: B %d must be in [1, 128]", p->B);
+  MKD_REQUIRE(p->d == 64 || p->d == 128, MKD_ERR_UNSUPPORTED, "attention: d_head %d must be 64 or 128", p->d);
+  MKD_REQUIRE(p->nkv > 0 && p->nq % p->nkv == 0, MKD_ERR_INVALID, "attention: q_heads %d not a multiple of kv_heads %d", p->nq, p->nkv);
+  const int g = p->nq / p->nkv;
+  MKD_REQUIRE(g == 1 || g == 2 || g == 4 || g == 8 || g == 16, MKD_ERR_UNSUPPORTED, "attention: GQA group %d unsupported", g);
+  MKD_REQUIRE(p->S_max > 0, MKD_ERR_INVALID, "attention: S_max must be > 0");
+  if (int rc = check_gemm_dims((p->nq + 2 * p->nkv) * p->d, p->H, 1)) return rc;
+  if (p->w_out_packed) {
+    if (int rc = check_gemm_dims(p->H_out, p->nq * p->d, 1)) return rc;
+  }
+  MKD_REQUIRE(!p->residual || p->w_out_packed, MKD_ERR_INVALID, "attention: residual needs W_out");
+  MKD_REQUIRE(!p->mask || p->mask_s_ctx >= 1, MKD_ERR_INVALID, "attention: mask_s_ctx must be >= 1");
+  MKD_REQUIRE(!(p->cos && !p->sin), MKD_ERR_NULL, "attention: cos without sin");
+  MKD_REQUIRE(!p->update_cache || p->kv_cache_update_idx, MKD_ERR_NULL,
+              "attention: update_cache needs kv_cache_update_idx");
+  return MKD_OK;
+}
+
+int mkd_attention_block_tkg(const mkd_attention_args* p, void* workspace, size_t workspace_bytes,
+                            void* stream) {
+  if (int rc = validate_attn(p)) return rc;
+  MKD_REQUIRE(workspace, MKD_ERR_NULL, "attention: null workspace");
+  Carver c{static_cast<char*>(workspace), workspace_bytes};
+  AttnWs w = carve_attn(c, p->B, p->H, p->nq, p->nkv, p->d, p->S_max);
+  MKD_REQUIRE(c.ok, MKD_ERR_WORKSPACE, "attention: workspace %zu < %zu bytes", workspace_bytes, c.used);
+  return attention_core(p, w, nullptr, nullptr, static_cast<hipStream_t>(stream));
+}
+
+// ---------------------------------------------------------------------------
+// multi-layer Qwen3 decode step
+// ---------------------------------------------------------------------------
+struct StepWs {
+  AttnWs attn;
+  uint16_t *r, *nbf;
+  float *nf32, *logits, *cos, *sin;
+  MoeWs moe;
+};
+
+static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
+  StepWs w;
+  w.attn = carve_attn(c, B, m->H, m->nq, m->nkv, m->d, m->S_max);
+  w.r = c.take<uint16_t>((size_t)B * m->H);
+  w.nbf = c.take<uint16_t>((size_t)B * m->H);
+  w.nf32 = c.take<float>((size_t)B * m->H);
+  w.logits = c.take<float>((size_t)B * m->E);
+  w.cos = c.take<float>((size_t)B * m->d);
+  w.sin = c.take<float>((size_t)B * m->d);
+  w.moe = carve_moe(c, B, m->H, m->E, m->I, m->K);
+  return w;
+}
+
+size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B) {
+  if (!m) return 0;
+  Carver c{nullptr, 0};
+  carve_step(c, m, B);
+  return c.used;
+}
+
+int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
+                            const int* position_ids, const float* cos, const float* sin,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  MKD_REQUIRE(m && hidden && position_ids && workspace, MKD_ERR_NULL, "decode_layers: null pointer");
+  MKD_REQUIRE(m->num_layers > 0, MKD_ERR_INVALID, "decode_layers: num_layers must be > 0");
+  MKD_REQUIRE(B > 0 && B <= 128, MKD_ERR_INVALID, "decode_layers: B %d must be in [1, 128]", B);
+  MKD_REQUIRE(cos || m->inv_freq, MKD_ERR_NULL, "decode_layers: need cos/sin or inv_freq");
+  MKD_REQUIRE(m->E <= 512 && m->K >= 1 && m->K <= 8, MKD_ERR_INVALID, "decode_layers: bad E/K");
+  MKD_REQUIRE(m->H % 8 == 0 && m->H <= 8192, MKD_ERR_INVALID, "decode_layers: bad H");
+  if (int rc = check_gemm_dims(2 * m->I, m->H, 2)) return rc;
+  if (int rc = check_gemm_dims(m->H, m->I, 1)) return rc;
+  if (int rc = check_gemm_dims(m->E, m->H, 1)) return rc;
+  Carver c{static_cast<char*>(workspace), workspace_bytes};
+  StepWs w = carve_step(c, m, B);
+  MKD_REQUIRE(c.ok, MKD_ERR_WORKSPACE, "decode_layers: workspace %zu < %zu bytes", workspace_bytes, c.used);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!cos) {
+    MKD_TRY(rope_table_launch(position_ids, m->inv_freq, B, m->d, w.cos, w.sin, s), "rope table");
+    cos = w.cos;
+    sin = w.sin;
+  }
+  uint16_t* x = static_cast<uint16_t*>(hidden);
+  for (int l = 0; l < m->num_layers; ++l) {
+    MKD_REQUIRE(m->w_qkv[l] && m->w_o[l] && m->router[l] && m->gate_up[l] && m->down[l] &&
+                m->k_cache[l] && m->v_cache[l] && m->ln_in[l] && m->ln_post[l],
+                MKD_ERR_NULL, "decode_layers: null weight in layer %d", l);
+    mkd_attention_args ap;
+    memset(&ap, 0, sizeof(ap));
+    ap.X = x;
+    ap.rmsnorm_gamma = m->ln_in[l]; ap.rmsnorm_eps = m->eps; ap.rmsnorm_order = 1;
+    ap.w_qkv_packed = m->w_qkv[l];
+    ap.q_norm = m->q_norm[l]; ap.k_norm = m->k_norm[l]; ap.qk_eps = m->eps;
+    ap.cos = cos; ap.sin = sin;
+    ap.k_cache = m->k_cache[l]; ap.v_cache = m->v_cache[l];
+    ap.n_prior = position_ids;
+    ap.update_cache = 1; ap.kv_cache_update_idx = position_ids;
+    ap.w_out_packed = m->w_o[l];
+    ap.residual = x;
+    ap.out = w.r;
+    ap.B = B; ap.H = m->H; ap.H_out = m->H; ap.nq = m->nq; ap.nkv = m->nkv; ap.d = m->d;
+    ap.S_max = m->S_max; ap.round_qwen = 1;
+    if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s)) return rc;
+    // post-attention RMSNorm: bf16 copy for the experts, fp32 copy for the router
+    MKD_TRY(rmsnorm_launch(w.r, 0, nullptr, nullptr, static_cast<const uint16_t*>(m->ln_post[l]),
+                           w.nbf, w.nf32, B, m->H, m->H, m->H, m->eps, 0, s), "post norm");
+    GemmArgs ra = dense_args(m->router[l], w.nf32, m->H, m->E, m->H, B, w.logits, m->E);
+    if (int rc = dense_gemm(ra, EPI_F32, true, s)) return rc;
+    MKD_TRY(router_topk_launch(w.logits, B, m->E, m->K, MKD_ROUTER_QWEN, nullptr, w.moe.idx,
+                               nullptr, w.moe.slot_w, s), "router topk");
+    if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], w.moe.idx, w.moe.slot_w, nullptr,
+                          nullptr, w.r, x, nullptr, B, m->H, m->E, m->I, m->K, MKD_ACT_SILU, 1.f,
+                          INFINITY, -INFINITY, INFINITY, -INFINITY, 1, w.moe, s))
+      return rc;
+  }
+  return MKD_OK;
+}
+
+int mkd_embed(const int* token_ids, const void* table, void* out, int B, int H, int V,
+              void* stream) {
+  MKD_REQUIRE(token_ids && table && out, MKD_ERR_NULL, "embed: null pointer");
+  MKD_REQUIRE(B > 0 && H % 8 == 0 && V > 0, MKD_ERR_INVALID, "embed: bad shape");
+  MKD_TRY(embed_launch(token_ids, static_cast<const uint16_t*>(table), static_cast<uint16_t*>(out),
+                       B, H, V, static_cast<hipStream_t>(stream)), "embed");
+  return MKD_OK;
+}
+
+size_t mkd_lm_head_workspace_bytes(int B, int H, int V) {
+  (void)V;
+  Carver c{nullptr, 0};
+  c.take<uint16_t>((size_t)B * H);
+  c.take<float>((size_t)B * 64);
+  c.take<int>((size_t)B * 64);
+  return c.used;
+}
+
+int mkd_lm_head_greedy(const void* hidden, const void* ln_f, float eps, const void* lm_head_packed,
+                       int B, int H, int V, float* logits, int* next_tokens, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  MKD_REQUIRE(hidden && ln_f && lm_head_packed && logits && next_tokens && workspace, MKD_ERR_NULL,
+              "lm_head: null pointer");
+  MKD_REQUIRE(B > 0 && B <= 128, MKD_ERR_INVALID, "lm_head: B %d must be in [1, 128]", B);
+  if (int rc = check_gemm_dims(V, H, 1)) return rc;
+  Carver c{static_cast<char*>(workspace), workspace_bytes};
+  uint16_t* n = c.take<uint16_t>((size_t)B * H);
+  float* sv = c.take<float>((size_t)B * 64);
+  int* si = c.take<int>((size_t)B * 64);
+  MKD_REQUIRE(c.ok, MKD_ERR_WORKSPACE, "lm_head: workspace %zu < %zu bytes", workspace_bytes, c.used);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  MKD_TRY(rmsnorm_launch(hidden, 0, nullptr, nullptr, static_cast<const uint16_t*>(ln_f), n, nullptr,
+                         B, H, H, H, eps, 2, s), "final norm");
+  GemmArgs a = dense_args(lm_head_packed, n, H, V, H, B, logits, V);
+  if (int rc = dense_gemm(a, EPI_F32, false, s)) return rc;
+  MKD_TRY(argmax_launch(logits, B, V, next_tokens, sv, si, s), "argmax");
+  return MKD_OK;
+}
+
+}  // extern "C"

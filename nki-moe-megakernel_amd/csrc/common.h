@@ -1,0 +1,70 @@
+// Shared device helpers for the gfx950 decode kernels.
+//
+// bf16 is handled as raw uint16 bit patterns: conversion to fp32 is a shift,
+// conversion from fp32 is round-to-nearest-even (NaN -> quiet NaN), which is
+// the rounding torch's bfloat16 cast uses, so every place the reference rounds
+// through bf16 gives the identical bit pattern here.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define MKD_DEV __device__ __forceinline__
+
+typedef uint16_t bf16_t;
+typedef __attribute__((__vector_size__(8 * sizeof(__bf16)))) __bf16 bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(__bf16)))) __bf16 bf16x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(uint32_t)))) uint32_t u32x4_t;
+typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8_t;
+
+constexpr int kWave = 64;
+
+MKD_DEV float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+MKD_DEV float bf_lo(uint32_t packed) { return __uint_as_float(packed << 16); }
+MKD_DEV float bf_hi(uint32_t packed) { return __uint_as_float(packed & 0xffff0000u); }
+
+MKD_DEV uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;  // NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return u >> 16;
+}
+// Round fp32 through bf16 and back.
+MKD_DEV float rbf(float f) { return bf2f(f2bf(f)); }
+MKD_DEV uint32_t pack2bf(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
+
+MKD_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+MKD_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Block-wide sum for blockDim.x a multiple of 64 (<= 1024).  `red` needs 16 floats.
+MKD_DEV float block_sum(float v, float* red) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, nw = blockDim.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();
+  if (lane == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+  for (int i = 0; i < nw; ++i) s += red[i];  // fixed order -> deterministic
+  return s;
+}
+
+MKD_DEV u32x4_t ld16(const void* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+MKD_DEV void st16(void* p, u32x4_t v) { *reinterpret_cast<u32x4_t*>(p) = v; }
+
+MKD_DEV bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+// 16x16x32 bf16 MFMA: A lane l holds row l%16, 8 k-values; B lane l holds
+// column l%16, the same 8 k-values; D lane l holds rows 4*(l/16)+i, column l%16.
+MKD_DEV f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+MKD_DEV float silu_f(float g) { return g / (1.0f + __expf(-g)); }

@@ -1,0 +1,307 @@
+// Weight-streaming skinny GEMM for decode:  Y[t, n] = sum_k X[t, k] * W[n, k]
+//
+// Decode GEMMs have a handful of tokens (1..128) against large weight matrices,
+// so they are HBM-bound on the weight stream.  Weights are repacked once into
+// MFMA fragment order ("frag layout"):
+//
+//   packed[nb][kb][lane][j] = W[nb*16 + lane%16][kb*32 + (lane/16)*8 + j]
+//
+// i.e. one v_mfma_f32_16x16x32_bf16 A-operand (16 rows x 32 k) is a contiguous
+// 1 KiB block and every wave-wide 16-byte load is one fully coalesced 1 KiB
+// transaction.  A row block of 16 output features is a contiguous 16*K*2-byte
+// run, so a wave streams straight through HBM.
+//
+// Work split: block = nsplit waves, all on the same 16-row block (RB = 2 row
+// blocks for the fused gate/up case), each wave owning K/nsplit of the
+// contraction; partial 16x16 tiles are reduced through LDS in a fixed order
+// (deterministic), then one epilogue is applied.  Tokens sit in the MFMA N
+// dimension (16 per tile, TN tiles per block).
+//
+// Grouped mode (MoE): blockIdx.y selects a routed expert group; the group's
+// token rows come from the routing tables and the expert's weights from
+// w + expert * w_group_stride.
+#include "common.h"
+#include "mkd_internal.h"
+
+namespace mkd {
+
+// ---------------------------------------------------------------------------
+// Packing: any [G][N][K] (k-contiguous) or [G][K][N] (n-contiguous) bf16 source
+// into frag layout.  `interleave_half` > 0 reorders row blocks as
+// [rows 0..15 | rows h..h+15 | rows 16..31 | rows h+16..h+31 | ...] with
+// h = interleave_half, which puts a gate block next to its up block.
+// ---------------------------------------------------------------------------
+__global__ void pack_frag_kernel(const uint16_t* __restrict__ src, uint16_t* __restrict__ dst,
+                                 int G, int N, int K, long long src_g_stride,
+                                 long long src_row_stride, long long src_col_stride,
+                                 int interleave_half) {
+  const int KB = K / 32, NB = N / 16;
+  const long long total = (long long)G * NB * KB * 64;
+  for (long long idx = blockIdx.x * (long long)blockDim.x + threadIdx.x; idx < total;
+       idx += (long long)gridDim.x * blockDim.x) {
+    const int lane = (int)(idx & 63);
+    long long r = idx >> 6;
+    const int kb = (int)(r % KB); r /= KB;
+    const int nb = (int)(r % NB);
+    const int g = (int)(r / NB);
+    int row_block = nb;
+    if (interleave_half > 0) {
+      const int pair = nb >> 1;
+      row_block = (nb & 1) ? (interleave_half / 16 + pair) : pair;
+    }
+    const int n = row_block * 16 + (lane & 15);
+    const int k0 = kb * 32 + (lane >> 4) * 8;
+    const uint16_t* s = src + g * src_g_stride + n * src_row_stride + k0 * src_col_stride;
+    uint16_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = s[j * src_col_stride];
+    uint16_t* d = dst + idx * 8;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) d[j] = v[j];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The GEMM.
+// ---------------------------------------------------------------------------
+template <int RB, int TN, bool XF32, int EPI>
+__global__ void __launch_bounds__(1024)
+gemm_frag_kernel(GemmArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rbase = blockIdx.x;          // index of the RB-row-block tile
+  const int group = blockIdx.y;
+  const int ttile = blockIdx.z;
+
+  // ---- token columns of this block ----
+  int count, base;                       // tokens in this group / first pair
+  const uint16_t* w = a.w;
+  if (a.grp_expert) {
+    if (group >= *a.n_groups) return;
+    count = a.grp_count[group];
+    base = a.grp_offset[group];
+    w += (long long)a.grp_expert[group] * a.w_group_stride;
+  } else {
+    count = a.T;
+    base = 0;
+  }
+  const int t0 = ttile * 16 * TN;
+  if (t0 >= count) return;
+
+  // x row of each token column owned by this lane (one column per TN tile)
+  int xrow[TN];
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    const int c = t0 + tn * 16 + (lane & 15);
+    if (c < count)
+      xrow[tn] = a.pair_row ? a.pair_row[base + c] : (base + c);
+    else
+      xrow[tn] = -1;
+  }
+
+  const int KB = a.K / 32;
+  const int NF = a.KW / 32;              // fragments per wave
+  const int kb0 = wave * NF;
+  const int koff = (lane >> 4) * 8;
+
+  f32x4_t acc[RB][TN];
+#pragma unroll
+  for (int r = 0; r < RB; ++r)
+#pragma unroll
+    for (int tn = 0; tn < TN; ++tn) acc[r][tn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const uint16_t* wrow[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r)
+    wrow[r] = w + ((long long)(rbase * RB + r) * KB + kb0) * 512 + lane * 8;
+
+  // Stream the fragments: weights are issued UNROLL ahead of their use.
+  constexpr int UNROLL = 8;
+  for (int f0 = 0; f0 < NF; f0 += UNROLL) {
+    u32x4_t wf[RB][UNROLL];
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+        if (f0 + u < NF) wf[r][u] = __builtin_nontemporal_load(
+            reinterpret_cast<const u32x4_t*>(wrow[r] + (f0 + u) * 512));
+#pragma unroll
+    for (int u = 0; u < UNROLL; ++u) {
+      if (f0 + u >= NF) break;
+      const int k = (kb0 + f0 + u) * 32 + koff;
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        if (XF32) {
+          u32x4_t hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
+          if (xrow[tn] >= 0) {
+            const float* xp = reinterpret_cast<const float*>(a.x) + (long long)xrow[tn] * a.ldx + k;
+            f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(xp);
+            f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(xp + 4);
+            float xs[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+            uint32_t h[8], l[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              h[j] = f2bf(xs[j]);
+              l[j] = f2bf(xs[j] - bf2f(h[j]));
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              hi[j] = h[2 * j] | (h[2 * j + 1] << 16);
+              lo[j] = l[2 * j] | (l[2 * j + 1] << 16);
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < RB; ++r) {
+            acc[r][tn] = mfma16x16x32(wf[r][u], hi, acc[r][tn]);
+            acc[r][tn] = mfma16x16x32(wf[r][u], lo, acc[r][tn]);
+          }
+        } else {
+          u32x4_t xv = {0, 0, 0, 0};
+          if (xrow[tn] >= 0)
+            xv = ld16(reinterpret_cast<const uint16_t*>(a.x) + (long long)xrow[tn] * a.ldx + k);
+#pragma unroll
+          for (int r = 0; r < RB; ++r) acc[r][tn] = mfma16x16x32(wf[r][u], xv, acc[r][tn]);
+        }
+      }
+    }
+  }
+
+  // ---- cross-wave reduction (fixed order) ----
+  extern __shared__ float red[];        // [nsplit][RB*TN*4][64]
+  constexpr int NR = RB * TN * 4;
+  const int nsplit = blockDim.x >> 6;
+  if (nsplit > 1) {
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          red[(wave * NR + (r * TN + tn) * 4 + i) * 64 + lane] = acc[r][tn][i];
+    __syncthreads();
+  }
+
+  // Each wave finalises the (tn) tiles with tn % nsplit == wave.
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    if (tn % nsplit != wave) continue;
+    float v[RB][4];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (nsplit > 1) {
+          float s = 0.f;
+          for (int q = 0; q < nsplit; ++q) s += red[(q * NR + (r * TN + tn) * 4 + i) * 64 + lane];
+          v[r][i] = s;
+        } else {
+          v[r][i] = acc[r][tn][i];
+        }
+      }
+    if (xrow[tn] < 0) continue;
+    const int c = t0 + tn * 16 + (lane & 15);
+    const int orow = a.grp_expert ? (a.pair_out_row ? a.pair_out_row[base + c] : base + c)
+                                  : c;
+    const int n0 = rbase * 16 + (lane >> 4) * 4;   // logical output column of v[.][0]
+    if (a.bias) {
+      const uint16_t* bp = a.bias + (a.grp_expert ? (long long)a.grp_expert[group] * a.bias_group_stride : 0);
+      const int half = a.N / 2;                      // up-row offset for the fused gate/up
+#pragma unroll
+      for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[r][i] += bf2f(bp[(r ? half : 0) + n0 + i]);
+    }
+    if (EPI == EPI_F32) {
+      float* y = reinterpret_cast<float*>(a.y) + (long long)orow * a.ldy + n0;
+      *reinterpret_cast<f32x4_t*>(y) = f32x4_t{v[0][0], v[0][1], v[0][2], v[0][3]};
+    } else if (EPI == EPI_BF16) {
+      uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n0;
+      uint2 o = {pack2bf(v[0][0], v[0][1]), pack2bf(v[0][2], v[0][3])};
+      *reinterpret_cast<uint2*>(y) = o;
+    } else if (EPI == EPI_RESID_BF16) {
+      // o = bf16(acc); out = bf16(res + o)   (projection then bf16 residual add)
+      const uint16_t* rp = a.residual + (long long)orow * a.ldy + n0;
+      uint2 rr = *reinterpret_cast<const uint2*>(rp);
+      float o0 = bf_lo(rr.x) + rbf(v[0][0]), o1 = bf_hi(rr.x) + rbf(v[0][1]);
+      float o2 = bf_lo(rr.y) + rbf(v[0][2]), o3 = bf_hi(rr.y) + rbf(v[0][3]);
+      uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n0;
+      *reinterpret_cast<uint2*>(y) = uint2{pack2bf(o0, o1), pack2bf(o2, o3)};
+    } else if (EPI == EPI_SWIGLU_BF16) {
+      // gate rows in v[0], up rows in v[1]; Qwen rounding: g,u -> bf16,
+      // silu(g) -> bf16, product -> bf16.
+      float h[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        if (a.round_qwen) {
+          const float g = rbf(v[0][i]), u = rbf(v[RB - 1][i]);
+          h[i] = rbf(g / (1.0f + expf(-g))) * u;
+        } else {
+          float g = fmaxf(fminf(v[0][i], a.gate_hi), a.gate_lo);
+          float u = fmaxf(fminf(v[RB - 1][i], a.up_hi), a.up_lo);
+          const float z = a.act ? a.alpha * g : g;
+          h[i] = (g / (1.0f + expf(-z))) * u;
+        }
+      }
+      uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n0;
+      *reinterpret_cast<uint2*>(y) = uint2{pack2bf(h[0], h[1]), pack2bf(h[2], h[3])};
+    } else if (EPI == EPI_SCALE_F32) {
+      const float s = a.pair_scale ? a.pair_scale[orow] : 1.0f;
+      float* y = reinterpret_cast<float*>(a.y) + (long long)orow * a.ldy + n0;
+      *reinterpret_cast<f32x4_t*>(y) =
+          f32x4_t{v[0][0] * s, v[0][1] * s, v[0][2] * s, v[0][3] * s};
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+template <int RB, int TN, bool XF32, int EPI>
+static hipError_t launch_t(const GemmArgs& a, int n_tiles, int groups, int ttiles, hipStream_t s) {
+  const int nsplit = a.K / a.KW;
+  dim3 grid(n_tiles, groups, ttiles);
+  dim3 block(64 * nsplit);
+  const size_t lds = nsplit > 1 ? (size_t)nsplit * RB * TN * 4 * 64 * sizeof(float) : 0;
+  hipLaunchKernelGGL((gemm_frag_kernel<RB, TN, XF32, EPI>), grid, block, lds, s, a);
+  return hipGetLastError();
+}
+
+int choose_kw(int K) {
+  // Largest per-wave K slice <= 512 that divides K into <= 16 waves.
+  for (int kw : {512, 384, 256, 128, 64, 32}) {
+    if (K % kw == 0 && K / kw <= 16) return kw;
+  }
+  return -1;
+}
+
+hipError_t gemm_launch(GemmArgs a, int epi, bool xf32, int tn, int groups_max,
+                       int max_tokens_per_group, hipStream_t s) {
+  const int RB = (epi == EPI_SWIGLU_BF16) ? 2 : 1;
+  const int n_tiles = a.N / (16 * RB);
+  const int ttiles = (max_tokens_per_group + 16 * tn - 1) / (16 * tn);
+  const int groups = a.grp_expert ? groups_max : 1;
+#define MKD_G(RB_, TN_, XF_, EPI_) \
+  if (RB == RB_ && tn == TN_ && xf32 == XF_ && epi == EPI_) return launch_t<RB_, TN_, XF_, EPI_>(a, n_tiles, groups, ttiles, s);
+  MKD_G(1, 1, false, EPI_F32) MKD_G(1, 2, false, EPI_F32) MKD_G(1, 4, false, EPI_F32)
+  MKD_G(1, 1, true, EPI_F32) MKD_G(1, 2, true, EPI_F32) MKD_G(1, 4, true, EPI_F32)
+  MKD_G(1, 1, false, EPI_BF16) MKD_G(1, 2, false, EPI_BF16) MKD_G(1, 4, false, EPI_BF16)
+  MKD_G(1, 1, false, EPI_RESID_BF16) MKD_G(1, 2, false, EPI_RESID_BF16) MKD_G(1, 4, false, EPI_RESID_BF16)
+  MKD_G(2, 1, false, EPI_SWIGLU_BF16) MKD_G(2, 2, false, EPI_SWIGLU_BF16)
+  MKD_G(1, 1, false, EPI_SCALE_F32) MKD_G(1, 2, false, EPI_SCALE_F32) MKD_G(1, 4, false, EPI_SCALE_F32)
+#undef MKD_G
+  return hipErrorInvalidValue;
+}
+
+hipError_t pack_frag_launch(const uint16_t* src, uint16_t* dst, int G, int N, int K,
+                            long long g_stride, long long row_stride, long long col_stride,
+                            int interleave_half, hipStream_t s) {
+  const long long total = (long long)G * (N / 16) * (K / 32) * 64;
+  const int threads = 256;
+  long long blocks = (total + threads - 1) / threads;
+  if (blocks > 65535LL * 16) blocks = 65535LL * 16;
+  hipLaunchKernelGGL(pack_frag_kernel, dim3((unsigned)blocks), dim3(threads), 0, s, src, dst, G,
+                     N, K, g_stride, row_stride, col_stride, interleave_half);
+  return hipGetLastError();
+}
+
+}  // namespace mkd

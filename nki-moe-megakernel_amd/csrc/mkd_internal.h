@@ -1,0 +1,105 @@
+// Internal launch interfaces shared by the kernel files and the C-ABI layer.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mkd {
+
+enum Epi { EPI_F32 = 0, EPI_BF16 = 1, EPI_RESID_BF16 = 2, EPI_SWIGLU_BF16 = 3, EPI_SCALE_F32 = 4 };
+
+struct GemmArgs {
+  const uint16_t* w;          // frag-packed weights (group 0)
+  long long w_group_stride;   // elements between experts
+  const void* x;              // activations, bf16 or fp32 rows
+  int ldx;                    // row stride of x (elements)
+  int N, K, KW;               // output features, contraction, k per wave
+  int T;                      // dense mode: number of token rows
+  // grouped (MoE) mode; all null in dense mode
+  const int* grp_expert;      // expert id of group g
+  const int* grp_count;       // tokens in group g
+  const int* grp_offset;      // first pair of group g
+  const int* n_groups;        // device scalar: number of live groups
+  const int* pair_row;        // x row of pair p
+  const int* pair_out_row;    // output row of pair p
+  // epilogue
+  void* y;                    // output rows
+  int ldy;                    // row stride of y (elements)
+  const uint16_t* residual;   // EPI_RESID_BF16: residual rows (row stride ldy)
+  const float* pair_scale;    // EPI_SCALE_F32: scale per output row (null = 1)
+  const uint16_t* bias;       // bf16 bias per logical output column (null = none)
+  long long bias_group_stride;  // elements between experts' biases
+  // EPI_SWIGLU_BF16 options
+  int act;                    // 0 silu, 1 swish(alpha)
+  float alpha;
+  float gate_hi, gate_lo, up_hi, up_lo;
+  int round_qwen;             // Qwen rounding points (else one rounding of the product)
+};
+
+int choose_kw(int K);
+hipError_t gemm_launch(GemmArgs a, int epi, bool xf32, int tn, int groups_max,
+                       int max_tokens_per_group, hipStream_t s);
+hipError_t pack_frag_launch(const uint16_t* src, uint16_t* dst, int G, int N, int K,
+                            long long g_stride, long long row_stride, long long col_stride,
+                            int interleave_half, hipStream_t s);
+
+// norm.hip
+hipError_t rmsnorm_launch(const void* x, int x_f32, const uint16_t* delta, uint16_t* resid_out,
+                          const uint16_t* gamma, uint16_t* out_bf16, float* out_f32, int rows,
+                          int H, int ld_in, int hidden_actual, float eps, int order_x_rinv_first,
+                          hipStream_t s);
+
+// attention.hip
+struct AttnArgs {
+  const float* qkv;           // [B, (nq + 2 nkv) * d] fp32 projections (or null)
+  const uint16_t* qkv_bf16;   // same, bf16 (operator path) (or null)
+  int ld_qkv;
+  const uint16_t* q_norm;     // [d] or null
+  const uint16_t* k_norm;     // [d] or null
+  float qk_eps;
+  const float* cos;           // [B, d] full-width table (contiguous halves duplicated)
+  const float* sin;
+  const float* inv_freq;      // [d/2] when cos/sin are generated from positions
+  const int* pos;             // [B] cache write position == number of prior tokens
+  uint16_t* q_out;            // [B, nq, d] bf16
+  uint16_t* kv_new;           // [B, 2, nkv, d] bf16 (k then v)
+  uint16_t* k_cache;          // [B, nkv, S_max, d]
+  uint16_t* v_cache;
+  long long cache_b_stride, cache_h_stride;  // elements
+  const int* n_prior;         // [B] prior positions attended (default pos)
+  const uint8_t* mask;        // optional [S_ctx, B, nq] (1 = attend), prior part only
+  int mask_s_ctx;
+  const float* sink;          // optional [nq]
+  float scale;
+  int round_qwen;             // 1: emulate the reference's bf16 score rounding
+  int B, nq, nkv, d, S_max;
+  int chunk;                  // positions per split-K block
+  int n_chunks;               // grid z
+  float* part_o;              // [B, nq, n_chunks, d]
+  float* part_ml;             // [B, nq, n_chunks, 2]
+  uint16_t* attn_out;         // [B, nq * d] bf16
+  int update_cache;
+  const int* write_pos;       // [B] row written (default pos); < 0 -> skip
+};
+hipError_t qk_prep_launch(const AttnArgs& a, int rope_mode, int round_qwen, hipStream_t s);
+hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t s);
+hipError_t attn_combine_launch(const AttnArgs& a, hipStream_t s);
+
+// moe.hip
+hipError_t router_topk_launch(const float* logits, int T, int E, int K, int mode,
+                              float* aff_full, int* idx_out, float* topk_out,
+                              float* slot_w, hipStream_t s);
+hipError_t moe_route_launch(const int* idx, int T, int K, int E, int* n_groups, int* grp_expert,
+                            int* grp_count, int* grp_offset, int* pair_token, int* pair_slot,
+                            hipStream_t s);
+hipError_t moe_finalize_launch(const float* ybuf, int T, int K, int H, const uint16_t* resid,
+                               uint16_t* out, float* out_f32, hipStream_t s);
+
+// misc.hip
+hipError_t embed_launch(const int* ids, const uint16_t* table, uint16_t* out, int B, int H, int V,
+                        hipStream_t s);
+hipError_t argmax_launch(const float* logits, int B, int V, int* out, float* scratch_val,
+                         int* scratch_idx, hipStream_t s);
+hipError_t rope_table_launch(const int* pos, const float* inv_freq, int B, int d, float* cos,
+                             float* sin, hipStream_t s);
+
+}  // namespace mkd

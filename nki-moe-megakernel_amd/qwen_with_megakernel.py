@@ -1,0 +1,312 @@
+"""Qwen3-MoE decode through the MI355X megakernel library.
+
+Mirrors megakernels/qwen3_moe/qwen_with_megakernel.py:
+  * ``convert_qwen3_moe_hf_to_mkd`` <- convert_qwen3_moe_hf_to_neuron_state_dict
+    (:171-271): HF state dict -> the library's packed layouts.
+  * ``Qwen3MoeDecoderLayerMK.forward`` <- NeuronQwen3MoeDecoderLayerV3.forward
+    (:422-526): on token generation layer 0 runs the whole L-layer stack in one
+    library call (mkd_qwen3_decode_layers, the counterpart of
+    transformer_qwen3_moe_tkg_multilayer) and the other layers pass through;
+    returns (Y, (K0, V0), cos, sin, None).
+  * ``Qwen3MoeMegakernelModel`` <- NeuronQwen3MoeModelV3 (:560-594) plus the
+    NxDI decode-step pieces the reference delegates (embedding, final norm,
+    lm_head :533-553, greedy sampling main.py:390-398), with an optional
+    HIP-graph capture of the whole step.
+
+KV caches are [B, kv_heads, S_max, d] bf16 per layer and are updated in place
+at position_ids (the reference's [B, 1, S_prior, d] per TP rank).
+"""
+from __future__ import annotations
+
+import hashlib
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional
+
+import torch
+from torch import nn
+
+from . import _lib as L
+from . import packing
+
+
+@dataclass
+class Qwen3MoeMKConfig:
+    hidden_size: int = 2048
+    num_attention_heads: int = 32
+    num_key_value_heads: int = 4
+    head_dim: int = 128
+    num_experts: int = 128
+    num_experts_per_tok: int = 8
+    moe_intermediate_size: int = 768
+    num_hidden_layers: int = 48
+    vocab_size: int = 151936
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1e6
+    max_batch: int = 1
+    max_seq: int = 2304           # KV capacity per sequence
+
+    @property
+    def qkv_out(self) -> int:
+        return (self.num_attention_heads + 2 * self.num_key_value_heads) * self.head_dim
+
+
+def tensor_seed(base: int, layer: int, name: str) -> int:
+    """Deterministic per-tensor seed from (base seed, layer, tensor name)."""
+    h = hashlib.sha256(f"{base}/{layer}/{name}".encode()).digest()
+    return int.from_bytes(h[:8], "little") & ((1 << 63) - 1)
+
+
+def randn_bf16(shape, seed: int, device, std: float = 0.02, mean: float = 0.0) -> torch.Tensor:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    t = torch.randn(*shape, generator=g, device=device, dtype=torch.float32)
+    return (t * std + mean).to(torch.bfloat16)
+
+
+def random_layer_hf(cfg: Qwen3MoeMKConfig, layer: int, seed: int, device) -> Dict[str, torch.Tensor]:
+    """HF-layout weights of one layer: linears N(0, 0.02), norm gammas 1 + N(0, 0.02)
+    (HF initialises gammas to 1; the perturbation keeps the gamma multiply non-trivial)."""
+    H, nq, nkv, d = cfg.hidden_size, cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim
+    E, I = cfg.num_experts, cfg.moe_intermediate_size
+    r = lambda name, shape, **kw: randn_bf16(shape, tensor_seed(seed, layer, name), device, **kw)
+    return {
+        "q_proj": r("q_proj", (nq * d, H)),
+        "k_proj": r("k_proj", (nkv * d, H)),
+        "v_proj": r("v_proj", (nkv * d, H)),
+        "o_proj": r("o_proj", (H, nq * d)),
+        "q_norm": r("q_norm", (d,), mean=1.0),
+        "k_norm": r("k_norm", (d,), mean=1.0),
+        "input_layernorm": r("input_layernorm", (H,), mean=1.0),
+        "post_attention_layernorm": r("post_attention_layernorm", (H,), mean=1.0),
+        "gate": r("gate", (E, H)),
+        "gate_up_proj": r("gate_up_proj", (E, 2 * I, H)),
+        "down_proj": r("down_proj", (E, H, I)),
+    }
+
+
+@dataclass
+class PackedLayer:
+    w_qkv: torch.Tensor
+    w_o: torch.Tensor
+    q_norm: torch.Tensor
+    k_norm: torch.Tensor
+    ln_in: torch.Tensor
+    ln_post: torch.Tensor
+    router: torch.Tensor
+    gate_up: torch.Tensor
+    down: torch.Tensor
+
+
+def pack_layer(hf: Dict[str, torch.Tensor]) -> PackedLayer:
+    """One layer of HF weights -> packed (convert_qwen3_moe_hf_to_neuron_state_dict's role)."""
+    wqkv = torch.cat([hf["q_proj"], hf["k_proj"], hf["v_proj"]], 0).contiguous()
+    return PackedLayer(
+        w_qkv=packing.pack_out_in(wqkv),
+        w_o=packing.pack_out_in(hf["o_proj"].contiguous()),
+        q_norm=hf["q_norm"].contiguous(), k_norm=hf["k_norm"].contiguous(),
+        ln_in=hf["input_layernorm"].contiguous(),
+        ln_post=hf["post_attention_layernorm"].contiguous(),
+        router=packing.pack_out_in(hf["gate"].contiguous()),
+        gate_up=packing.pack_experts_gate_up_hf(hf["gate_up_proj"].contiguous()),
+        down=packing.pack_experts_down_hf(hf["down_proj"].contiguous()),
+    )
+
+
+def convert_qwen3_moe_hf_to_mkd(state_dict: Dict[str, torch.Tensor], cfg: Qwen3MoeMKConfig,
+                                device) -> List[PackedLayer]:
+    """HF Qwen3-MoE state dict (``model.layers.{l}...`` or ``layers.{l}...`` keys;
+    experts either fused [E, 2I, H] / [E, H, I] or per-expert gate/up/down) ->
+    packed layers on `device`."""
+    def get(l, *names):
+        for pre in (f"model.layers.{l}.", f"layers.{l}."):
+            for n in names:
+                if pre + n in state_dict:
+                    return state_dict[pre + n].to(device=device, dtype=torch.bfloat16)
+        return None
+
+    layers = []
+    for l in range(cfg.num_hidden_layers):
+        gu = get(l, "mlp.experts.gate_up_proj")
+        dn = get(l, "mlp.experts.down_proj")
+        if gu is None:
+            gates = [get(l, f"mlp.experts.{e}.gate_proj.weight") for e in range(cfg.num_experts)]
+            ups = [get(l, f"mlp.experts.{e}.up_proj.weight") for e in range(cfg.num_experts)]
+            downs = [get(l, f"mlp.experts.{e}.down_proj.weight") for e in range(cfg.num_experts)]
+            gu = torch.stack([torch.cat([g, u], 0) for g, u in zip(gates, ups)])
+            dn = torch.stack(downs)
+        hf = {
+            "q_proj": get(l, "self_attn.q_proj.weight"),
+            "k_proj": get(l, "self_attn.k_proj.weight"),
+            "v_proj": get(l, "self_attn.v_proj.weight"),
+            "o_proj": get(l, "self_attn.o_proj.weight"),
+            "q_norm": get(l, "self_attn.q_norm.weight"),
+            "k_norm": get(l, "self_attn.k_norm.weight"),
+            "input_layernorm": get(l, "input_layernorm.weight"),
+            "post_attention_layernorm": get(l, "post_attention_layernorm.weight"),
+            "gate": get(l, "mlp.gate.weight"),
+            "gate_up_proj": gu, "down_proj": dn,
+        }
+        missing = [k for k, v in hf.items() if v is None]
+        if missing:
+            raise KeyError(f"layer {l}: missing {missing}")
+        layers.append(pack_layer(hf))
+    return layers
+
+
+class KVCacheManager:
+    """Holds per-layer K/V caches; ``past_key_values`` is flat [K0, V0, K1, V1, ...]
+    like the NxDI kv_mgr the reference reads (qwen_with_megakernel.py:410-420)."""
+
+    def __init__(self, cfg: Qwen3MoeMKConfig, batch: int, device):
+        shape = (batch, cfg.num_key_value_heads, cfg.max_seq, cfg.head_dim)
+        self.past_key_values = []
+        for _ in range(cfg.num_hidden_layers):
+            self.past_key_values.append(torch.zeros(shape, dtype=torch.bfloat16, device=device))
+            self.past_key_values.append(torch.zeros(shape, dtype=torch.bfloat16, device=device))
+
+    def k(self, l):
+        return self.past_key_values[2 * l]
+
+    def v(self, l):
+        return self.past_key_values[2 * l + 1]
+
+
+class Qwen3MoeMegakernelModel(nn.Module):
+    """Decoder stack + decode-step epilogue on the MI355X library."""
+
+    def __init__(self, cfg: Qwen3MoeMKConfig, layers: List[PackedLayer], batch: int, device,
+                 embed: Optional[torch.Tensor] = None, ln_f: Optional[torch.Tensor] = None,
+                 lm_head: Optional[torch.Tensor] = None):
+        super().__init__()
+        self.cfg = cfg
+        self.batch = batch
+        self.device = torch.device(device)
+        self.packed = layers
+        self.kv_mgr = KVCacheManager(cfg, batch, device)
+        self.embed_tokens = embed                    # [V, H] bf16 or None
+        self.ln_f = ln_f                             # [H] bf16 or None
+        self.lm_head_packed = packing.pack_out_in(lm_head) if lm_head is not None else None
+        d = cfg.head_dim
+        self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float) / d))).to(device)
+        self._build_struct()
+        lib = L.load()
+        self.ws = torch.empty(max(lib.mkd_qwen3_workspace_bytes(self._model, batch), 256),
+                              dtype=torch.uint8, device=device)
+        self.lm_ws = torch.empty(max(lib.mkd_lm_head_workspace_bytes(batch, cfg.hidden_size, cfg.vocab_size), 256),
+                                 dtype=torch.uint8, device=device)
+        self.layers = nn.ModuleList(
+            [Qwen3MoeDecoderLayerMK(cfg, i, self) for i in range(cfg.num_hidden_layers)])
+        self._graph = None
+
+    # -- ctypes model struct (host arrays of device pointers) --
+    def _build_struct(self):
+        cfg, Ln = self.cfg, self.cfg.num_hidden_layers
+        arr = lambda ts: (L.vp * Ln)(*[t.data_ptr() for t in ts])
+        p = self.packed
+        self._arrays = {
+            "w_qkv": arr([x.w_qkv for x in p]), "w_o": arr([x.w_o for x in p]),
+            "q_norm": arr([x.q_norm for x in p]), "k_norm": arr([x.k_norm for x in p]),
+            "ln_in": arr([x.ln_in for x in p]), "ln_post": arr([x.ln_post for x in p]),
+            "router": arr([x.router for x in p]), "gate_up": arr([x.gate_up for x in p]),
+            "down": arr([x.down for x in p]),
+            "k_cache": arr([self.kv_mgr.k(l) for l in range(Ln)]),
+            "v_cache": arr([self.kv_mgr.v(l) for l in range(Ln)]),
+        }
+        self._model = L.Qwen3Model(
+            num_layers=Ln, H=cfg.hidden_size, nq=cfg.num_attention_heads,
+            nkv=cfg.num_key_value_heads, d=cfg.head_dim, E=cfg.num_experts,
+            K=cfg.num_experts_per_tok, I=cfg.moe_intermediate_size, S_max=cfg.max_seq,
+            eps=cfg.rms_norm_eps, inv_freq=self.inv_freq.data_ptr(), **self._arrays)
+
+    def rope_cos_sin(self, position_ids: torch.Tensor):
+        """cos/sin [B, d] at position_ids (HF rotary: fp32 angles, halves duplicated)."""
+        freqs = position_ids.reshape(-1, 1).float() * self.inv_freq[None, :]
+        emb = torch.cat([freqs, freqs], -1)
+        return emb.cos(), emb.sin()
+
+    def decode_layers(self, hidden: torch.Tensor, position_ids: torch.Tensor,
+                      cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None):
+        """Run all layers in place on hidden [B, H] bf16 (the multilayer kernel call)."""
+        B = hidden.shape[0]
+        if B > self.batch:
+            raise ValueError(f"batch {B} exceeds the configured max batch {self.batch}")
+        if hidden.dtype != torch.bfloat16 or not hidden.is_contiguous():
+            raise ValueError("hidden must be a contiguous bf16 [B, H] tensor")
+        pos = position_ids.reshape(-1)
+        if pos.dtype != torch.int32:
+            raise ValueError("position_ids must be int32")
+        rc = L.load().mkd_qwen3_decode_layers(
+            self._model, B, hidden.data_ptr(), pos.data_ptr(), L.ptr(cos), L.ptr(sin),
+            self.ws.data_ptr(), self.ws.numel(), L.stream_ptr(self.device))
+        L.check(rc, "qwen3_decode_layers")
+        return hidden
+
+    def step(self, token_ids: torch.Tensor, position_ids: torch.Tensor, hidden: torch.Tensor,
+             logits: torch.Tensor, next_tokens: torch.Tensor):
+        """Full greedy decode step into caller buffers (no allocation; graph-capturable)."""
+        lib = L.load()
+        B, H = hidden.shape
+        s = L.stream_ptr(self.device)
+        L.check(lib.mkd_embed(token_ids.data_ptr(), self.embed_tokens.data_ptr(), hidden.data_ptr(),
+                              B, H, self.embed_tokens.shape[0], s), "embed")
+        self.decode_layers(hidden, position_ids)
+        L.check(lib.mkd_lm_head_greedy(hidden.data_ptr(), self.ln_f.data_ptr(), self.cfg.rms_norm_eps,
+                                       self.lm_head_packed.data_ptr(), B, H, self.cfg.vocab_size,
+                                       logits.data_ptr(), next_tokens.data_ptr(),
+                                       self.lm_ws.data_ptr(), self.lm_ws.numel(), s), "lm_head")
+        return next_tokens
+
+    def forward(self, input_ids: torch.Tensor, position_ids: torch.Tensor):
+        """Greedy decode step: input_ids [B] -> (logits [B, V] fp32, next ids [B] int32)."""
+        B = input_ids.shape[0]
+        hidden = torch.empty(B, self.cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
+        logits = torch.empty(B, self.cfg.vocab_size, dtype=torch.float32, device=self.device)
+        nxt = torch.empty(B, dtype=torch.int32, device=self.device)
+        self.step(input_ids.to(torch.int32).contiguous(), position_ids.to(torch.int32).contiguous(),
+                  hidden, logits, nxt)
+        return logits, nxt
+
+
+class Qwen3MoeDecoderLayerMK(nn.Module):
+    """Decoder-layer boundary of NeuronQwen3MoeDecoderLayerV3 (qwen_with_megakernel.py:422-526)."""
+
+    def __init__(self, cfg: Qwen3MoeMKConfig, layer_idx: int, parent: Qwen3MoeMegakernelModel):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self._num_hidden_layers = cfg.num_hidden_layers
+        import weakref
+        self._parent_model_ref = weakref.ref(parent)
+
+    @property
+    def _parent_model(self):
+        return self._parent_model_ref()
+
+    def forward(self, hidden_states: torch.Tensor, attention_mask=None, position_ids=None,
+                past_key_value=None, padding_mask=None, kv_mgr=None, idx: int = 0,
+                is_for_context_encoding: bool = True, **kwargs):
+        if is_for_context_encoding:
+            raise NotImplementedError("context encoding (prefill) is outside the decode path")
+        parent = self._parent_model
+        kv_mgr = kv_mgr if kv_mgr is not None else parent.kv_mgr
+        if kv_mgr is not parent.kv_mgr:
+            raise ValueError("kv_mgr must be the model's KVCacheManager (its caches are bound to the step)")
+        Ln = self._num_hidden_layers
+        if self.layer_idx == 0:
+            B, S, H = hidden_states.shape
+            if S != 1:
+                raise NotImplementedError("token generation takes one token per sequence")
+            pos = position_ids.reshape(-1).to(torch.int32).contiguous()
+            cos, sin = parent.rope_cos_sin(pos)
+            y = hidden_states.reshape(B, H).to(torch.bfloat16).contiguous().clone()
+            parent.decode_layers(y, pos)
+            K_out = [kv_mgr.k(l) for l in range(Ln)]
+            V_out = [kv_mgr.v(l) for l in range(Ln)]
+            parent._tkg_kv_out = (K_out, V_out)
+            return (y.reshape(B, S, H), (K_out[0], V_out[0]), cos[:, None, :], sin[:, None, :], None)
+        K_out, V_out = parent._tkg_kv_out
+        return (hidden_states, (K_out[self.layer_idx], V_out[self.layer_idx]), None, None, None)
+
+
+# Alias mirroring the reference module's export (qwen_with_megakernel.py:728).
+NeuronQwen3MoeForCausalLM = Qwen3MoeMegakernelModel

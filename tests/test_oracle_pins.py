@@ -1,0 +1,338 @@
+"""Pins of the CPU oracle (oracle/ref.py) against independent sources.
+
+Each check is chosen so that a plausible mistake in the oracle (a dropped term,
+a wrong sign or index, a transposed operand) fails it:
+  * HF transformers modules (fp32) for RMSNorm, RoPE, router, experts, and the
+    whole decoder layer (committed golden fixture, tests/golden/);
+  * closed forms and special cases (zero rows, padding law, S=1 attention,
+    uniform scores, one-hot routing == dense MLP, position 0 RoPE);
+  * brute force on tiny inputs (top-k).
+"""
+import math
+import os
+
+import pytest
+import torch
+
+from oracle import ref
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "qwen3moe_layer_fp32.safetensors")
+
+
+def _hf():
+    from transformers.models.qwen3_moe import modeling_qwen3_moe as M
+    from transformers.models.qwen3_moe.configuration_qwen3_moe import Qwen3MoeConfig
+    return M, Qwen3MoeConfig
+
+
+# ------------------------------------------------------------------ rmsnorm
+def test_rmsnorm_matches_hf_fp32():
+    M, _ = _hf()
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(5, 256, generator=g)
+    w = 1 + 0.1 * torch.randn(256, generator=g)
+    m = M.Qwen3MoeRMSNorm(256, eps=1e-6)
+    with torch.no_grad():
+        m.weight.copy_(w)
+        y_hf = m(x)
+    y = ref.rmsnorm_tkg(x, w, 1e-6)
+    assert torch.allclose(y, y_hf, rtol=1e-6, atol=1e-6)
+
+
+def test_rmsnorm_closed_forms():
+    # constant row c: y = gamma * c / sqrt(c^2 + eps)
+    x = torch.full((1, 128), 3.0)
+    w = torch.linspace(0.5, 1.5, 128)
+    y = ref.rmsnorm_tkg(x, w, 1e-6)
+    assert torch.allclose(y, w * 3.0 / math.sqrt(9.0 + 1e-6), rtol=1e-6)
+    # zero row -> zero
+    assert torch.all(ref.rmsnorm_tkg(torch.zeros(2, 128), w, 1e-6) == 0)
+
+
+def test_rmsnorm_padding_law():
+    # zero-padding H with hidden_actual = true width leaves the real part unchanged
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(3, 2880, generator=g)
+    w = torch.randn(2880, generator=g)
+    xp = torch.cat([x, torch.zeros(3, 192)], 1)
+    wp = torch.cat([w, torch.ones(192)])
+    y = ref.rmsnorm_tkg(x, w, 1e-5)
+    yp = ref.rmsnorm_tkg(xp, wp, 1e-5, hidden_actual=2880)
+    assert torch.allclose(yp[:, :2880], y, rtol=1e-6, atol=1e-7)
+    assert torch.all(yp[:, 2880:] == 0)
+
+
+# ------------------------------------------------------------------ top-k / router
+def test_stable_topk_brute_force():
+    g = torch.Generator().manual_seed(2)
+    for _ in range(50):
+        x = torch.randint(0, 5, (6,), generator=g).float()   # many exact ties
+        v, i = ref.stable_topk(x, 3)
+        order = sorted(range(6), key=lambda j: (-x[j].item(), j))[:3]
+        assert i.tolist() == order
+        assert v.tolist() == [x[j].item() for j in order]
+
+
+def test_router_matches_hf_qwen_fp32():
+    M, C = _hf()
+    cfg = C(hidden_size=128, num_experts=16, num_experts_per_tok=4, norm_topk_prob=True)
+    r = M.Qwen3MoeTopKRouter(cfg)
+    g = torch.Generator().manual_seed(3)
+    with torch.no_grad():
+        r.weight.copy_(0.1 * torch.randn(16, 128, generator=g))
+    x = torch.randn(7, 128, generator=g)
+    with torch.no_grad():
+        logits_hf, w_hf, idx_hf = r(x)
+    logits, idx, aff, vals = ref.router_topk(x, r.weight.detach().t(), None, "softmax", 4,
+                                             router_pre_norm=True, norm_topk_prob=True)
+    assert torch.allclose(logits, logits_hf, rtol=1e-6, atol=1e-6)
+    assert torch.equal(idx, idx_hf)
+    assert torch.allclose(vals, w_hf, rtol=1e-6, atol=1e-7)
+    # scattered affinities: K non-zeros per row summing to 1
+    assert torch.all((aff > 0).sum(1) == 4)
+    assert torch.allclose(aff.sum(1), torch.ones(7), atol=1e-6)
+    # Qwen fused flow without bf16 emulation is the same math
+    lq, iq, wq = ref.qwen_router(x, r.weight.detach().t(), 4, emulate_bf16=False)
+    assert torch.equal(iq, idx_hf)
+    assert torch.allclose(wq, w_hf, rtol=1e-6, atol=1e-7)
+
+
+def test_router_act2_is_softmax_of_topk():
+    # ACT2 pipeline (GPT-OSS): softmax over the top-k logits only (HF modeling_gpt_oss.py:126-130)
+    g = torch.Generator().manual_seed(4)
+    x = torch.randn(5, 64, generator=g)
+    w = torch.randn(64, 32, generator=g) * 0.2
+    b = torch.randn(32, generator=g) * 0.1
+    logits, idx, aff, vals = ref.router_topk(x, w, b, "softmax", 4, router_pre_norm=False)
+    full = x @ w + b
+    tv, ti = torch.topk(full, 4, dim=-1)
+    assert torch.equal(idx, ti)
+    assert torch.allclose(vals, torch.softmax(tv, -1), atol=1e-6)
+    assert torch.allclose(aff.sum(1), torch.ones(5), atol=1e-6)
+
+
+def test_router_act1_without_norm_keeps_full_activation():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 64, generator=g)
+    w = torch.randn(64, 16, generator=g) * 0.2
+    logits, idx, aff, vals = ref.router_topk(x, w, None, "softmax", 2, router_pre_norm=True)
+    assert torch.allclose(aff, torch.softmax(x @ w, -1), atol=1e-6)
+
+
+# ------------------------------------------------------------------ experts
+def _hf_experts(E=8, H=64, I=32, seed=6):
+    M, C = _hf()
+    cfg = C(hidden_size=H, num_experts=E, num_experts_per_tok=2, moe_intermediate_size=I)
+    cfg._experts_implementation = "eager"
+    ex = M.Qwen3MoeExperts(cfg)
+    g = torch.Generator().manual_seed(seed)
+    with torch.no_grad():
+        ex.gate_up_proj.copy_(0.1 * torch.randn(E, 2 * I, H, generator=g))
+        ex.down_proj.copy_(0.1 * torch.randn(E, H, I, generator=g))
+    return ex, g
+
+
+def test_experts_match_hf_fp32():
+    ex, g = _hf_experts()
+    x = torch.randn(5, 64, generator=g)
+    idx = torch.stack([torch.randperm(8, generator=g)[:2] for _ in range(5)])
+    wts = torch.rand(5, 2, generator=g)
+    with torch.no_grad():
+        y_hf = ex(x, idx, wts)
+    gu = ex.gate_up_proj.detach()
+    dn = ex.down_proj.detach()
+    y_q = ref.qwen_experts(x, gu, dn, idx, wts, emulate_bf16=False)
+    assert torch.allclose(y_q, y_hf, rtol=1e-5, atol=1e-6)
+    # the generic moe_tkg over the reference layouts [E,H,2,I] / [E,I,H], POST_SCALE
+    I = 32
+    gu_ref = torch.stack([gu[:, :I, :], gu[:, I:, :]], 2).permute(0, 3, 2, 1).contiguous()  # [E,H,2,I]
+    dn_ref = dn.transpose(1, 2).contiguous()                                                # [E,I,H]
+    aff = torch.zeros(5, 8).scatter_(1, idx, wts)
+    y_g = ref.moe_tkg(x, gu_ref, dn_ref, aff, idx, scaling_mode="post", emulate_bf16=False)
+    assert torch.allclose(y_g, y_hf, rtol=1e-5, atol=1e-6)
+
+
+def test_one_hot_routing_is_dense_swiglu():
+    ex, g = _hf_experts(seed=7)
+    x = torch.randn(4, 64, generator=g)
+    e = 3
+    idx = torch.full((4, 1), e)
+    y = ref.qwen_experts(x, ex.gate_up_proj.detach(), ex.down_proj.detach(), idx,
+                         torch.ones(4, 1), emulate_bf16=False)
+    W = ex.gate_up_proj.detach()[e]
+    gte, up = (x @ W.t()).chunk(2, -1)
+    dense = (torch.nn.functional.silu(gte) * up) @ ex.down_proj.detach()[e].t()
+    assert torch.allclose(y, dense, rtol=1e-5, atol=1e-6)
+
+
+def test_moe_clamps_and_swish():
+    # GPT-OSS semantics: gate <= 7, up in [-7, 7], g * sigmoid(1.702 g) (HF modeling_gpt_oss.py:82-88)
+    g = torch.Generator().manual_seed(8)
+    E, H, I = 4, 32, 32
+    x = 3 * torch.randn(2, H, generator=g)
+    gu = torch.randn(E, H, 2, I, generator=g)
+    dn = 0.1 * torch.randn(E, I, H, generator=g)
+    idx = torch.tensor([[0, 2], [1, 3]])
+    aff = torch.zeros(2, E).scatter_(1, idx, torch.tensor([[0.7, 0.3], [0.4, 0.6]]))
+    y = ref.moe_tkg(x, gu, dn, aff, idx, scaling_mode="post", act="swish",
+                    gate_clamp_upper=7.0, up_clamp_upper=7.0, up_clamp_lower=-7.0,
+                    emulate_bf16=False)
+    exp = torch.zeros(2, H)
+    for t in range(2):
+        for j in range(2):
+            e = int(idx[t, j])
+            gt = (x[t] @ gu[e, :, 0, :]).clamp(max=7.0)
+            up = (x[t] @ gu[e, :, 1, :]).clamp(min=-7.0, max=7.0)
+            exp[t] += aff[t, e] * ((gt * torch.sigmoid(1.702 * gt) * up) @ dn[e])
+    assert torch.allclose(y, exp, rtol=1e-5, atol=1e-5)
+
+
+# ------------------------------------------------------------------ rope / attention
+def test_rope_matches_hf_and_identity_at_zero():
+    M, _ = _hf()
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(2, 4, 1, 64, generator=g)
+    k = torch.randn(2, 2, 1, 64, generator=g)
+    pos = torch.tensor([5, 1000])
+    cos, sin = ref.rope_cos_sin(pos, 64, 1e6)
+    qh, kh = M.apply_rotary_pos_emb(q, k, cos[:, None, :], sin[:, None, :], unsqueeze_dim=1)
+    qo = ref.rope_apply(q[:, :, 0], cos[:, None], sin[:, None], emulate_bf16=False)
+    assert torch.allclose(qo, qh[:, :, 0], atol=1e-6)
+    c0, s0 = ref.rope_cos_sin(torch.tensor([0]), 64, 1e6)
+    assert torch.equal(ref.rope_apply(q[0, :, 0], c0, s0, emulate_bf16=False), q[0, :, 0])
+
+
+def _generic_attn_inputs(B=2, H=128, nq=4, d=32, S_ctx=20, S_max=24, seed=10):
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn(B, 1, H, generator=g)
+    W = 0.1 * torch.randn(H, d * (nq + 2), generator=g)
+    Kc = torch.randn(B, S_max, d, generator=g)
+    Vc = torch.randn(B, S_max, d, generator=g)
+    mask = torch.ones(S_ctx, B, nq, 1)
+    return X, W, Kc, Vc, mask, g
+
+
+def test_generic_attention_matches_sdpa():
+    X, W, Kc, Vc, mask, g = _generic_attn_inputs()
+    B, nq, d, S_ctx = 2, 4, 32, 20
+    mask[5:9, 1] = 0      # knock out a span for sequence 1
+    out, Kn, Vn = ref.attention_block_tkg(X, W, None, None, None, None, None, 1e-6, None, None,
+                                          Kc.clone(), Vc.clone(), mask, None, False, None,
+                                          None, None)
+    qkv = X.reshape(B, -1) @ W
+    q = qkv[:, :nq * d].reshape(B, nq, d)
+    k = qkv[:, nq * d:(nq + 1) * d]
+    v = qkv[:, (nq + 1) * d:]
+    for b in range(B):
+        keys = torch.cat([Kc[b, :S_ctx - 1], k[b:b + 1]], 0)
+        vals = torch.cat([Vc[b, :S_ctx - 1], v[b:b + 1]], 0)
+        am = mask[:, b, :, 0].t().bool()                         # [nq, S_ctx]
+        o = torch.nn.functional.scaled_dot_product_attention(
+            q[b][:, None, :], keys[None].expand(nq, -1, -1), vals[None].expand(nq, -1, -1),
+            attn_mask=am[:, None, :])
+        assert torch.allclose(out[b].reshape(nq, d), o[:, 0], atol=1e-5)
+
+
+def test_generic_attention_special_cases():
+    X, W, Kc, Vc, mask, g = _generic_attn_inputs(S_ctx=1)
+    # S_ctx = 1: only the active token -> output = its V
+    out, _, _ = ref.attention_block_tkg(X, W, None, None, None, None, None, 1e-6, None, None,
+                                        Kc, Vc, mask, None, False, None, None, None)
+    v = (X.reshape(2, -1) @ W)[:, 5 * 32:]
+    assert torch.allclose(out.reshape(2, 4, 32), v[:, None, :].expand(2, 4, 32), atol=1e-6)
+    # uniform scores (zero queries) -> mean of V over the window
+    W0 = W.clone()
+    W0[:, :4 * 32] = 0
+    X, _, Kc, Vc, mask, _ = _generic_attn_inputs(S_ctx=9)
+    out, _, _ = ref.attention_block_tkg(X, W0, None, None, None, None, None, 1e-6, None, None,
+                                        Kc, Vc, mask, None, False, None, None, None)
+    v = (X.reshape(2, -1) @ W0)[:, 5 * 32:]
+    for b in range(2):
+        mean = torch.cat([Vc[b, :8], v[b:b + 1]], 0).mean(0)
+        assert torch.allclose(out[b].reshape(4, 32), mean.expand(4, 32), atol=1e-5)
+
+
+def test_attention_sink_matches_hf_gpt_oss_formula():
+    # sink: extra logit per head in the softmax denominator, dropped afterwards
+    # (HF modeling_gpt_oss.py eager_attention_forward: cat sinks, softmax, drop last column)
+    X, W, Kc, Vc, mask, g = _generic_attn_inputs(S_ctx=12)
+    sink = torch.randn(4, generator=g)
+    out, _, _ = ref.attention_block_tkg(X, W, None, None, None, None, None, 1e-6, None, None,
+                                        Kc, Vc, mask, sink, False, None, None, None)
+    qkv = X.reshape(2, -1) @ W
+    for b in range(2):
+        q = qkv[b, :128].reshape(4, 32)
+        keys = torch.cat([Kc[b, :11], qkv[b, 128:160][None]], 0)
+        vals = torch.cat([Vc[b, :11], qkv[b, 160:][None]], 0)
+        sc = q @ keys.t() / math.sqrt(32)
+        comb = torch.cat([sc, sink[:, None]], 1)
+        p = torch.softmax(comb, -1)[:, :-1]
+        assert torch.allclose(out[b].reshape(4, 32), p @ vals, atol=1e-5)
+
+
+def test_kv_scatter_only_target_rows_change():
+    X, W, Kc, Vc, mask, g = _generic_attn_inputs(S_ctx=10)
+    K0, V0 = Kc.clone(), Vc.clone()
+    idx = torch.tensor([[9], [0xFFFFFFFF]], dtype=torch.int64)   # seq 1: uint32 max = skip
+    ref.attention_block_tkg(X, W, None, None, None, None, None, 1e-6, None, None, Kc, Vc, mask,
+                            None, True, idx, None, None)
+    qkv = X.reshape(2, -1) @ W
+    changed = (Kc != K0).any(-1)
+    assert changed[0].nonzero().flatten().tolist() == [9]
+    assert not changed[1].any()
+    assert torch.equal(Kc[0, 9], qkv[0, 128:160])
+    assert torch.equal(Vc[0, 9], qkv[0, 160:])
+
+
+# ------------------------------------------------------------------ whole layer vs HF
+def _load_golden():
+    from safetensors.torch import load_file
+    from safetensors import safe_open
+    t = load_file(GOLDEN)
+    with safe_open(GOLDEN, "pt") as f:
+        meta = f.metadata()
+    return t, meta
+
+
+def golden_layer(t, meta):
+    H, nq, nkv, d = int(meta["H"]), int(meta["nq"]), int(meta["nkv"]), int(meta["d"])
+    E, K, I = int(meta["E"]), int(meta["K"]), int(meta["I"])
+    lw = ref.QwenLayer(
+        wq=t["w.self_attn.q_proj.weight"], wk=t["w.self_attn.k_proj.weight"],
+        wv=t["w.self_attn.v_proj.weight"], wo=t["w.self_attn.o_proj.weight"],
+        q_norm=t["w.self_attn.q_norm.weight"], k_norm=t["w.self_attn.k_norm.weight"],
+        ln_in=t["w.input_layernorm.weight"], ln_post=t["w.post_attention_layernorm.weight"],
+        router=t["w.mlp.gate.weight"], gate_up=t["w.mlp.experts.gate_up_proj"],
+        down=t["w.mlp.experts.down_proj"])
+    shape = ref.QwenShape(H=H, q_heads=nq, kv_heads=nkv, d=d, E=E, K=K, I=I, eps=1e-6, theta=1e6)
+    return lw, shape
+
+
+def test_qwen_layer_fp32_matches_hf_golden():
+    t, meta = _load_golden()
+    lw, shape = golden_layer(t, meta)
+    kc, vc = t["k_cache"].float().clone(), t["v_cache"].float().clone()
+    cos, sin = ref.rope_cos_sin(t["pos"], shape.d, shape.theta)
+    assert torch.allclose(cos, t["cos"], atol=1e-6) and torch.allclose(sin, t["sin"], atol=1e-6)
+    y, aux = ref.qwen_decoder_layer(t["x"].float(), lw, kc, vc, cos, sin, t["pos"], shape,
+                                    emulate_bf16=False)
+    assert torch.allclose(y, t["y"], rtol=1e-4, atol=1e-5), (y - t["y"]).abs().max()
+    for b, p in enumerate(t["pos"].tolist()):
+        assert torch.allclose(kc[b, :, p], t["k_new"][b], atol=1e-5)
+        assert torch.allclose(vc[b, :, p], t["v_new"][b], atol=1e-5)
+        # rows other than pos[b] untouched
+        mask = torch.ones(kc.shape[2], dtype=torch.bool)
+        mask[p] = False
+        assert torch.equal(kc[b, :, mask], t["k_cache"].float()[b, :, mask])
+
+
+def test_qwen_layer_bf16_flow_within_tolerance_of_fp32():
+    # the reference's bf16 rounding points move the result by O(bf16 eps), well inside 2e-2
+    t, meta = _load_golden()
+    lw, shape = golden_layer(t, meta)
+    cos, sin = ref.rope_cos_sin(t["pos"], shape.d, shape.theta)
+    y, _ = ref.qwen_decoder_layer(t["x"].float(), lw, t["k_cache"].float().clone(),
+                                  t["v_cache"].float().clone(), cos, sin, t["pos"], shape,
+                                  emulate_bf16=True)
+    err = (y - t["y"]).abs().max() / t["y"].abs().max()
+    assert err < 2e-2, err
