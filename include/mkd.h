@@ -227,6 +227,29 @@ int mkd_lm_head_greedy(const void* hidden, const void* ln_f, float eps, const vo
                        int B, int H, int V, float* logits, int* next_tokens, void* workspace,
                        size_t workspace_bytes, void* stream);
 
+/* Greedy-loop glue for a graph-captured decode step: token_ids[b] = next_tokens[b],
+ * position_ids[b] += 1.  (The reference's host loop does this in NxDI.) */
+int mkd_decode_advance(int* token_ids, int* position_ids, const int* next_tokens, int B,
+                       void* stream);
+
+/* ---------------------------------------------------------------------------
+ * Measurement hook (no counterpart in the reference; used by bench.py).
+ * After this call the library records start_events[i] / stop_events[i]
+ * (hipEvent_t handles, host array) on the launch stream around the i-th
+ * subsequent launch (i < n) of the kernel class below (eager launches only: a
+ * launch on a capturing stream, or a failed record, turns the hook off).
+ * kernel_class < 0 turns the hook off.  Process-global, not thread-safe.
+ * ------------------------------------------------------------------------- */
+#define MKD_KCLASS_MOE_GATE_UP 1
+#define MKD_KCLASS_MOE_DOWN 2
+#define MKD_KCLASS_QKV 3
+#define MKD_KCLASS_OPROJ 4
+#define MKD_KCLASS_ATTN 5
+#define MKD_KCLASS_LM_HEAD 6
+int mkd_profile_events(int kernel_class, void* const* start_events, void* const* stop_events,
+                       int n);
+int mkd_profile_count(void); /* launches recorded since the last mkd_profile_events */
+
 #ifdef __cplusplus
 }
 #endif

@@ -98,7 +98,11 @@ _SIGS = {
     "mkd_embed": (i32, [vp, vp, vp, i32, i32, i32, vp]),
     "mkd_lm_head_workspace_bytes": (sz, [i32, i32, i32]),
     "mkd_lm_head_greedy": (i32, [vp, vp, f32, vp, i32, i32, i32, vp, vp, vp, sz, vp]),
+    "mkd_decode_advance": (i32, [vp, vp, vp, i32, vp]),
+    "mkd_profile_events": (i32, [i32, C.POINTER(vp), C.POINTER(vp), i32]),
+    "mkd_profile_count": (i32, []),
 }
+KCLASS = {"moe_gate_up": 1, "moe_down": 2, "qkv": 3, "oproj": 4, "attn": 5, "lm_head": 6}
 
 EXPORTED = tuple(_SIGS)
 

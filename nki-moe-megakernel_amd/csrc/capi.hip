@@ -6,6 +6,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 
 #include "common.h"
@@ -26,9 +27,68 @@ int fail(int code, const char* fmt, ...) {
   return code;
 }
 
+// MKD_SYNC_CHECK=1 in the environment: synchronise after every launch so a
+// failing kernel is named at its own call site (debugging aid; never on by default).
+bool sync_check() {
+  static const int on = [] {
+    const char* e = getenv("MKD_SYNC_CHECK");
+    return (e && e[0] == '1') ? 1 : 0;
+  }();
+  return on;
+}
+
 int hip_check(hipError_t e, const char* what) {
   if (e != hipSuccess) return fail(MKD_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  if (sync_check()) {
+    e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipGetLastError();
+    if (e != hipSuccess) return fail(MKD_ERR_HIP, "%s (synchronised): %s", what, hipGetErrorString(e));
+  }
   return MKD_OK;
+}
+
+// A HIP error left pending by an earlier, unrelated call would otherwise be
+// reported by the first launch check of the next entry point; clear it at entry
+// and name it if debugging.
+int stale_check(const char* fn) {
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess && sync_check())
+    return fail(MKD_ERR_HIP, "%s: HIP error pending before entry: %s", fn, hipGetErrorString(e));
+  return MKD_OK;
+}
+
+// ---- measurement hook state (mkd_profile_events) ----
+struct ProfState {
+  int cls = -1;
+  int n = 0;
+  int next = 0;
+  hipEvent_t start[512];
+  hipEvent_t stop[512];
+} g_prof;
+
+// Records are skipped while the stream is being captured (timing event nodes are
+// not available in captured graphs on this runtime); a failed record turns the
+// hook off and clears the error so it is not reported by the next launch.
+void record(hipEvent_t ev, hipStream_t s) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &st);
+  if (e == hipSuccess && st == hipStreamCaptureStatusNone) e = hipEventRecord(ev, s);
+  else if (e == hipSuccess) e = hipErrorStreamCaptureUnsupported;
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    g_prof.cls = -1;
+  }
+}
+
+// Bracket one launch of class `cls`: prof_begin returns the slot (or -1).
+int prof_begin(int cls, hipStream_t s) {
+  if (g_prof.cls != cls || g_prof.next >= g_prof.n) return -1;
+  const int i = g_prof.next++;
+  record(g_prof.start[i], s);
+  return i;
+}
+void prof_end(int slot, hipStream_t s) {
+  if (slot >= 0) record(g_prof.stop[slot], s);
 }
 
 #define MKD_REQUIRE(cond, code, ...) \
@@ -75,8 +135,13 @@ GemmArgs dense_args(const void* w, const void* x, int ldx, int N, int K, int T, 
   return a;
 }
 
+// Rows of a packed matrix: the logical count rounded up to a 16-row block.
+long long padded_rows(int N) { return ((long long)N + 15) / 16 * 16; }
+
+// rb == 2 (fused gate/up) needs each half to be whole 16-row blocks.
 int check_gemm_dims(int N, int K, int rb) {
-  MKD_REQUIRE(N > 0 && N % (16 * rb) == 0, MKD_ERR_INVALID, "output features %d must be a multiple of %d", N, 16 * rb);
+  MKD_REQUIRE(N > 0 && (rb == 1 || N % (16 * rb) == 0), MKD_ERR_INVALID,
+              "fused gate/up width %d must be a multiple of %d", N, 16 * rb);
   MKD_REQUIRE(K > 0 && K % 32 == 0, MKD_ERR_INVALID, "contraction %d must be a multiple of 32", K);
   MKD_REQUIRE(choose_kw(K) > 0, MKD_ERR_UNSUPPORTED, "contraction %d too large (max 8192)", K);
   return MKD_OK;
@@ -152,16 +217,20 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
     a.bias = gu_bias; a.bias_group_stride = 2LL * I;
     a.act = act; a.alpha = alpha; a.gate_hi = ghi; a.gate_lo = glo; a.up_hi = uhi; a.up_lo = ulo;
     a.round_qwen = round_qwen;
+    const int ps = prof_begin(MKD_KCLASS_MOE_GATE_UP, s);
     MKD_TRY(gemm_launch(a, EPI_SWIGLU_BF16, false, tn, gmax, T, s), "moe gate_up");
+    prof_end(ps, s);
   }
   {  // down, scaled by the slot affinity
     GemmArgs a = dense_args(down, w.hbuf, I, H, I, T, w.ybuf, H);
-    a.w_group_stride = (long long)H * I;
+    a.w_group_stride = padded_rows(H) * I;
     a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
     a.n_groups = w.n_groups; a.pair_row = w.pair_slot; a.pair_out_row = w.pair_slot;
     a.pair_scale = slot_w;
     a.bias = dn_bias; a.bias_group_stride = H;
+    const int ps = prof_begin(MKD_KCLASS_MOE_DOWN, s);
     MKD_TRY(gemm_launch(a, EPI_SCALE_F32, false, tn, gmax, T, s), "moe down");
+    prof_end(ps, s);
   }
   MKD_TRY(moe_finalize_launch(w.ybuf, T, K, H, resid, out, out_f32, s), "moe finalize");
   return MKD_OK;
@@ -177,6 +246,7 @@ const char* mkd_last_error(void) { return g_err; }
 int mkd_rmsnorm_tkg(const void* input, int input_dtype, const void* gamma, void* output,
                     int output_dtype, int rows, int hidden, int hidden_actual, float eps,
                     void* stream) {
+  if (int rc = stale_check("mkd_rmsnorm_tkg")) return rc;
   MKD_REQUIRE(input && gamma && output, MKD_ERR_NULL, "rmsnorm_tkg: null pointer");
   MKD_REQUIRE(rows > 0, MKD_ERR_INVALID, "rmsnorm_tkg: rows must be > 0, got %d", rows);
   MKD_REQUIRE(hidden > 0 && hidden % 8 == 0 && hidden <= 8192, MKD_ERR_INVALID,
@@ -195,12 +265,13 @@ int mkd_rmsnorm_tkg(const void* input, int input_dtype, const void* gamma, void*
 }
 
 size_t mkd_packed_bytes(int groups, int n, int k) {
-  return (size_t)groups * (size_t)n * (size_t)k * 2;
+  return (size_t)groups * (size_t)padded_rows(n) * (size_t)k * 2;
 }
 
 int mkd_pack_weights(const void* src, void* dst, int groups, int n, int k, long long g_stride,
                      long long row_stride, long long col_stride, int interleave_half,
                      void* stream) {
+  if (int rc = stale_check("mkd_pack_weights")) return rc;
   MKD_REQUIRE(src && dst, MKD_ERR_NULL, "pack_weights: null pointer");
   MKD_REQUIRE(groups > 0 && n > 0 && k > 0, MKD_ERR_INVALID, "pack_weights: empty shape");
   if (int rc = check_gemm_dims(n, k, interleave_half > 0 ? 2 : 1)) return rc;
@@ -215,6 +286,7 @@ int mkd_pack_weights(const void* src, void* dst, int groups, int n, int k, long 
 int mkd_linear(const void* x, int x_dtype, int ldx, int rows, const void* w_packed, int n, int k,
                const void* bias, void* y, int y_dtype, int ldy, const void* residual,
                void* stream) {
+  if (int rc = stale_check("mkd_linear")) return rc;
   MKD_REQUIRE(x && w_packed && y, MKD_ERR_NULL, "linear: null pointer");
   MKD_REQUIRE(rows > 0 && rows <= 128, MKD_ERR_INVALID, "linear: rows %d must be in [1, 128]", rows);
   if (int rc = check_gemm_dims(n, k, 1)) return rc;
@@ -231,6 +303,7 @@ int mkd_linear(const void* x, int x_dtype, int ldx, int rows, const void* w_pack
 int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_packed, int E,
                     const void* w_bias, float* router_logits, float* expert_affinities,
                     int* expert_index, float* topk_affinities, int k, int mode, void* stream) {
+  if (int rc = stale_check("mkd_router_topk")) return rc;
   MKD_REQUIRE(x && w_packed && router_logits && expert_index, MKD_ERR_NULL, "router_topk: null pointer");
   MKD_REQUIRE(T > 0 && T <= 128, MKD_ERR_INVALID, "router_topk: T %d must be in [1, 128]", T);
   MKD_REQUIRE(E > 0 && E <= 512, MKD_ERR_INVALID, "router_topk: E %d must be in [1, 512]", E);
@@ -254,6 +327,7 @@ size_t mkd_moe_workspace_bytes(int T, int H, int E, int I, int K) {
 }
 
 int mkd_moe_tkg(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = stale_check("mkd_moe_tkg")) return rc;
   MKD_REQUIRE(p, MKD_ERR_NULL, "moe_tkg: null args");
   MKD_REQUIRE(p->hidden && p->gate_up_packed && p->down_packed && p->expert_index && p->output,
               MKD_ERR_NULL, "moe_tkg: null pointer");
@@ -337,7 +411,11 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   // 2. QKV projection (fp32 out)
   GemmArgs g = dense_args(p->w_qkv_packed, xin, p->H, qkv_n, p->H, p->B, w.qkv, qkv_n);
   g.bias = static_cast<const uint16_t*>(p->bias_qkv);
-  if (int rc = dense_gemm(g, EPI_F32, false, s)) return rc;
+  {
+    const int ps = prof_begin(MKD_KCLASS_QKV, s);
+    if (int rc = dense_gemm(g, EPI_F32, false, s)) return rc;
+    prof_end(ps, s);
+  }
   // 3. q/k norm + RoPE + staging
   AttnArgs a;
   memset(&a, 0, sizeof(a));
@@ -364,7 +442,11 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   a.write_pos = p->kv_cache_update_idx;
   const int rope_mode = p->cos ? 1 : (inv_freq ? 2 : 0);
   MKD_TRY(qk_prep_launch(a, rope_mode, p->round_qwen, s), "qk_prep");
-  MKD_TRY(attn_decode_launch(a, s), "attn_decode");
+  {
+    const int ps = prof_begin(MKD_KCLASS_ATTN, s);
+    MKD_TRY(attn_decode_launch(a, s), "attn_decode");
+    prof_end(ps, s);
+  }
   MKD_TRY(attn_combine_launch(a, s), "attn_combine");
   // 5. output projection
   if (p->w_out_packed) {
@@ -372,7 +454,9 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
                             p->out, p->H_out);
     o.bias = static_cast<const uint16_t*>(p->bias_out);
     o.residual = static_cast<const uint16_t*>(p->residual);
+    const int ps = prof_begin(MKD_KCLASS_OPROJ, s);
     if (int rc = dense_gemm(o, p->residual ? EPI_RESID_BF16 : EPI_BF16, false, s)) return rc;
+    prof_end(ps, s);
   } else {
     MKD_TRY(hipMemcpyAsync(p->out, w.attn, (size_t)p->B * p->nq * p->d * 2, hipMemcpyDeviceToDevice, s),
             "attn copy");
@@ -404,6 +488,7 @@ static int validate_attn(const mkd_attention_args* p) {
 
 int mkd_attention_block_tkg(const mkd_attention_args* p, void* workspace, size_t workspace_bytes,
                             void* stream) {
+  if (int rc = stale_check("mkd_attention_block_tkg")) return rc;
   if (int rc = validate_attn(p)) return rc;
   MKD_REQUIRE(workspace, MKD_ERR_NULL, "attention: null workspace");
   Carver c{static_cast<char*>(workspace), workspace_bytes};
@@ -445,6 +530,7 @@ size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B) {
 int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
                             const int* position_ids, const float* cos, const float* sin,
                             void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = stale_check("mkd_qwen3_decode_layers")) return rc;
   MKD_REQUIRE(m && hidden && position_ids && workspace, MKD_ERR_NULL, "decode_layers: null pointer");
   MKD_REQUIRE(m->num_layers > 0, MKD_ERR_INVALID, "decode_layers: num_layers must be > 0");
   MKD_REQUIRE(B > 0 && B <= 128, MKD_ERR_INVALID, "decode_layers: B %d must be in [1, 128]", B);
@@ -501,6 +587,7 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
 
 int mkd_embed(const int* token_ids, const void* table, void* out, int B, int H, int V,
               void* stream) {
+  if (int rc = stale_check("mkd_embed")) return rc;
   MKD_REQUIRE(token_ids && table && out, MKD_ERR_NULL, "embed: null pointer");
   MKD_REQUIRE(B > 0 && H % 8 == 0 && V > 0, MKD_ERR_INVALID, "embed: bad shape");
   MKD_TRY(embed_launch(token_ids, static_cast<const uint16_t*>(table), static_cast<uint16_t*>(out),
@@ -520,6 +607,7 @@ size_t mkd_lm_head_workspace_bytes(int B, int H, int V) {
 int mkd_lm_head_greedy(const void* hidden, const void* ln_f, float eps, const void* lm_head_packed,
                        int B, int H, int V, float* logits, int* next_tokens, void* workspace,
                        size_t workspace_bytes, void* stream) {
+  if (int rc = stale_check("mkd_lm_head_greedy")) return rc;
   MKD_REQUIRE(hidden && ln_f && lm_head_packed && logits && next_tokens && workspace, MKD_ERR_NULL,
               "lm_head: null pointer");
   MKD_REQUIRE(B > 0 && B <= 128, MKD_ERR_INVALID, "lm_head: B %d must be in [1, 128]", B);
@@ -533,9 +621,52 @@ int mkd_lm_head_greedy(const void* hidden, const void* ln_f, float eps, const vo
   MKD_TRY(rmsnorm_launch(hidden, 0, nullptr, nullptr, static_cast<const uint16_t*>(ln_f), n, nullptr,
                          B, H, H, H, eps, 2, s), "final norm");
   GemmArgs a = dense_args(lm_head_packed, n, H, V, H, B, logits, V);
-  if (int rc = dense_gemm(a, EPI_F32, false, s)) return rc;
+  {
+    const int ps = prof_begin(MKD_KCLASS_LM_HEAD, s);
+    if (int rc = dense_gemm(a, EPI_F32, false, s)) return rc;
+    prof_end(ps, s);
+  }
   MKD_TRY(argmax_launch(logits, B, V, next_tokens, sv, si, s), "argmax");
   return MKD_OK;
 }
+
+__global__ void decode_advance_kernel(int* ids, int* pos, const int* nxt, int B) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b < B) {
+    ids[b] = nxt[b];
+    pos[b] += 1;
+  }
+}
+
+int mkd_decode_advance(int* token_ids, int* position_ids, const int* next_tokens, int B,
+                       void* stream) {
+  if (int rc = stale_check("mkd_decode_advance")) return rc;
+  MKD_REQUIRE(token_ids && position_ids && next_tokens, MKD_ERR_NULL, "decode_advance: null pointer");
+  MKD_REQUIRE(B > 0, MKD_ERR_INVALID, "decode_advance: B must be > 0");
+  hipLaunchKernelGGL(decode_advance_kernel, dim3((B + 255) / 256), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), token_ids, position_ids, next_tokens, B);
+  MKD_TRY(hipGetLastError(), "decode_advance");
+  return MKD_OK;
+}
+
+int mkd_profile_events(int kernel_class, void* const* start_events, void* const* stop_events,
+                       int n) {
+  if (kernel_class < 0) {
+    g_prof.cls = -1;
+    return MKD_OK;
+  }
+  MKD_REQUIRE(start_events && stop_events, MKD_ERR_NULL, "profile_events: null event array");
+  MKD_REQUIRE(n > 0 && n <= 512, MKD_ERR_INVALID, "profile_events: n %d must be in [1, 512]", n);
+  for (int i = 0; i < n; ++i) {
+    g_prof.start[i] = static_cast<hipEvent_t>(start_events[i]);
+    g_prof.stop[i] = static_cast<hipEvent_t>(stop_events[i]);
+  }
+  g_prof.n = n;
+  g_prof.next = 0;
+  g_prof.cls = kernel_class;
+  return MKD_OK;
+}
+
+int mkd_profile_count(void) { return g_prof.next; }
 
 }  // extern "C"

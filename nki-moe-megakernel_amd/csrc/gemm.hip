@@ -35,7 +35,9 @@ __global__ void pack_frag_kernel(const uint16_t* __restrict__ src, uint16_t* __r
                                  int G, int N, int K, long long src_g_stride,
                                  long long src_row_stride, long long src_col_stride,
                                  int interleave_half) {
-  const int KB = K / 32, NB = N / 16;
+  // N is the logical row count; the packed matrix has ceil(N/16)*16 rows, the
+  // padding rows are zero.
+  const int KB = K / 32, NB = (N + 15) / 16;
   const long long total = (long long)G * NB * KB * 64;
   for (long long idx = blockIdx.x * (long long)blockDim.x + threadIdx.x; idx < total;
        idx += (long long)gridDim.x * blockDim.x) {
@@ -51,10 +53,12 @@ __global__ void pack_frag_kernel(const uint16_t* __restrict__ src, uint16_t* __r
     }
     const int n = row_block * 16 + (lane & 15);
     const int k0 = kb * 32 + (lane >> 4) * 8;
-    const uint16_t* s = src + g * src_g_stride + n * src_row_stride + k0 * src_col_stride;
-    uint16_t v[8];
+    uint16_t v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    if (n < N) {
+      const uint16_t* s = src + g * src_g_stride + n * src_row_stride + k0 * src_col_stride;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = s[j * src_col_stride];
+      for (int j = 0; j < 8; ++j) v[j] = s[j * src_col_stride];
+    }
     uint16_t* d = dst + idx * 8;
 #pragma unroll
     for (int j = 0; j < 8; ++j) d[j] = v[j];
@@ -203,52 +207,66 @@ gemm_frag_kernel(GemmArgs a) {
     const int orow = a.grp_expert ? (a.pair_out_row ? a.pair_out_row[base + c] : base + c)
                                   : c;
     const int n0 = rbase * 16 + (lane >> 4) * 4;   // logical output column of v[.][0]
+    const int ncol = RB == 2 ? a.N / 2 : a.N;       // logical output width
+    const int nv = min(4, ncol - n0);               // valid columns of this lane
+    if (nv <= 0) continue;
+    const bool vec = (nv == 4) && ((a.ldy & 3) == 0);
     if (a.bias) {
       const uint16_t* bp = a.bias + (a.grp_expert ? (long long)a.grp_expert[group] * a.bias_group_stride : 0);
-      const int half = a.N / 2;                      // up-row offset for the fused gate/up
 #pragma unroll
       for (int r = 0; r < RB; ++r)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) v[r][i] += bf2f(bp[(r ? half : 0) + n0 + i]);
+        for (int i = 0; i < 4; ++i)
+          if (i < nv) v[r][i] += bf2f(bp[(r ? ncol : 0) + n0 + i]);
     }
+    float o[4];
     if (EPI == EPI_F32) {
-      float* y = reinterpret_cast<float*>(a.y) + (long long)orow * a.ldy + n0;
-      *reinterpret_cast<f32x4_t*>(y) = f32x4_t{v[0][0], v[0][1], v[0][2], v[0][3]};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = v[0][i];
     } else if (EPI == EPI_BF16) {
-      uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n0;
-      uint2 o = {pack2bf(v[0][0], v[0][1]), pack2bf(v[0][2], v[0][3])};
-      *reinterpret_cast<uint2*>(y) = o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = v[0][i];
     } else if (EPI == EPI_RESID_BF16) {
       // o = bf16(acc); out = bf16(res + o)   (projection then bf16 residual add)
       const uint16_t* rp = a.residual + (long long)orow * a.ldy + n0;
-      uint2 rr = *reinterpret_cast<const uint2*>(rp);
-      float o0 = bf_lo(rr.x) + rbf(v[0][0]), o1 = bf_hi(rr.x) + rbf(v[0][1]);
-      float o2 = bf_lo(rr.y) + rbf(v[0][2]), o3 = bf_hi(rr.y) + rbf(v[0][3]);
-      uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n0;
-      *reinterpret_cast<uint2*>(y) = uint2{pack2bf(o0, o1), pack2bf(o2, o3)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = (i < nv) ? bf2f(rp[i]) + rbf(v[0][i]) : 0.f;
     } else if (EPI == EPI_SWIGLU_BF16) {
       // gate rows in v[0], up rows in v[1]; Qwen rounding: g,u -> bf16,
       // silu(g) -> bf16, product -> bf16.
-      float h[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         if (a.round_qwen) {
           const float g = rbf(v[0][i]), u = rbf(v[RB - 1][i]);
-          h[i] = rbf(g / (1.0f + expf(-g))) * u;
+          o[i] = rbf(g / (1.0f + expf(-g))) * u;
         } else {
           float g = fmaxf(fminf(v[0][i], a.gate_hi), a.gate_lo);
           float u = fmaxf(fminf(v[RB - 1][i], a.up_hi), a.up_lo);
           const float z = a.act ? a.alpha * g : g;
-          h[i] = (g / (1.0f + expf(-z))) * u;
+          o[i] = (g / (1.0f + expf(-z))) * u;
         }
       }
-      uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n0;
-      *reinterpret_cast<uint2*>(y) = uint2{pack2bf(h[0], h[1]), pack2bf(h[2], h[3])};
     } else if (EPI == EPI_SCALE_F32) {
-      const float s = a.pair_scale ? a.pair_scale[orow] : 1.0f;
+      const float sc = a.pair_scale ? a.pair_scale[orow] : 1.0f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[i] = v[0][i] * sc;
+    }
+    if (EPI == EPI_F32 || EPI == EPI_SCALE_F32) {
       float* y = reinterpret_cast<float*>(a.y) + (long long)orow * a.ldy + n0;
-      *reinterpret_cast<f32x4_t*>(y) =
-          f32x4_t{v[0][0] * s, v[0][1] * s, v[0][2] * s, v[0][3] * s};
+      if (vec) {
+        *reinterpret_cast<f32x4_t*>(y) = f32x4_t{o[0], o[1], o[2], o[3]};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) if (i < nv) y[i] = o[i];
+      }
+    } else {
+      uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n0;
+      if (vec) {
+        *reinterpret_cast<uint2*>(y) = uint2{pack2bf(o[0], o[1]), pack2bf(o[2], o[3])};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) if (i < nv) y[i] = (uint16_t)f2bf(o[i]);
+      }
     }
   }
 }
@@ -277,7 +295,7 @@ int choose_kw(int K) {
 hipError_t gemm_launch(GemmArgs a, int epi, bool xf32, int tn, int groups_max,
                        int max_tokens_per_group, hipStream_t s) {
   const int RB = (epi == EPI_SWIGLU_BF16) ? 2 : 1;
-  const int n_tiles = a.N / (16 * RB);
+  const int n_tiles = (a.N + 16 * RB - 1) / (16 * RB);
   const int ttiles = (max_tokens_per_group + 16 * tn - 1) / (16 * tn);
   const int groups = a.grp_expert ? groups_max : 1;
 #define MKD_G(RB_, TN_, XF_, EPI_) \
@@ -295,7 +313,8 @@ hipError_t gemm_launch(GemmArgs a, int epi, bool xf32, int tn, int groups_max,
 hipError_t pack_frag_launch(const uint16_t* src, uint16_t* dst, int G, int N, int K,
                             long long g_stride, long long row_stride, long long col_stride,
                             int interleave_half, hipStream_t s) {
-  const long long total = (long long)G * (N / 16) * (K / 32) * 64;
+  const long long total = (long long)G * ((N + 15) / 16) * (K / 32) * 64;
+  if (total <= 0) return hipErrorInvalidValue;
   const int threads = 256;
   long long blocks = (total + threads - 1) / threads;
   if (blocks > 65535LL * 16) blocks = 65535LL * 16;

@@ -30,7 +30,7 @@ def pack(src: torch.Tensor, groups: int, n: int, k: int, g_stride: int, row_stri
     if src.dtype != torch.bfloat16:
         raise ValueError(f"weights must be bfloat16, got {src.dtype}")
     lib = L.load()
-    out = torch.empty(groups * n * k, dtype=torch.bfloat16, device=src.device)
+    out = torch.empty(lib.mkd_packed_bytes(groups, n, k) // 2, dtype=torch.bfloat16, device=src.device)
     rc = lib.mkd_pack_weights(src.data_ptr(), out.data_ptr(), groups, n, k, g_stride, row_stride,
                               col_stride, interleave_half, L.stream_ptr(src.device))
     L.check(rc, "pack_weights")
