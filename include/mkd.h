@@ -101,10 +101,13 @@ int mkd_linear(const void* x, int x_dtype, int ldx, int rows, const void* w_pack
  * expert_affinities [T, E] fp32 (scattered top-k, or full activation for the
  * (ACT1, topK) pipeline), topk_affinities [T, k] fp32 (may be NULL).
  * E <= 512, k <= 8, T <= 128.  Ties resolve to the lowest expert index.
+ * workspace: mkd_router_workspace_bytes(T, H, E) bytes (split-K partial logits).
  * ------------------------------------------------------------------------- */
+size_t mkd_router_workspace_bytes(int T, int H, int E);
 int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_packed, int E,
                     const void* w_bias, float* router_logits, float* expert_affinities,
-                    int* expert_index, float* topk_affinities, int k, int mode, void* stream);
+                    int* expert_index, float* topk_affinities, int k, int mode, void* workspace,
+                    size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * moe_tkg (selective experts, bf16) -- replaces nki_kernels/moe/moe_tkg.py:56
@@ -246,6 +249,7 @@ int mkd_decode_advance(int* token_ids, int* position_ids, const int* next_tokens
 #define MKD_KCLASS_OPROJ 4
 #define MKD_KCLASS_ATTN 5
 #define MKD_KCLASS_LM_HEAD 6
+#define MKD_KCLASS_ROUTER 7 /* router GEMM + select (two launches, one bracket) */
 int mkd_profile_events(int kernel_class, void* const* start_events, void* const* stop_events,
                        int n);
 int mkd_profile_count(void); /* launches recorded since the last mkd_profile_events */

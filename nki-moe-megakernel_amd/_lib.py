@@ -88,7 +88,8 @@ _SIGS = {
     "mkd_packed_bytes": (sz, [i32, i32, i32]),
     "mkd_pack_weights": (i32, [vp, vp, i32, i32, i32, i64, i64, i64, i32, vp]),
     "mkd_linear": (i32, [vp, i32, i32, i32, vp, i32, i32, vp, vp, i32, i32, vp, vp]),
-    "mkd_router_topk": (i32, [vp, i32, i32, i32, vp, i32, vp, vp, vp, vp, vp, i32, i32, vp]),
+    "mkd_router_workspace_bytes": (sz, [i32, i32, i32]),
+    "mkd_router_topk": (i32, [vp, i32, i32, i32, vp, i32, vp, vp, vp, vp, vp, i32, i32, vp, sz, vp]),
     "mkd_moe_workspace_bytes": (sz, [i32, i32, i32, i32, i32]),
     "mkd_moe_tkg": (i32, [C.POINTER(MoeArgs), vp, sz, vp]),
     "mkd_attention_workspace_bytes": (sz, [i32, i32, i32, i32, i32, i32]),
@@ -102,7 +103,8 @@ _SIGS = {
     "mkd_profile_events": (i32, [i32, C.POINTER(vp), C.POINTER(vp), i32]),
     "mkd_profile_count": (i32, []),
 }
-KCLASS = {"moe_gate_up": 1, "moe_down": 2, "qkv": 3, "oproj": 4, "attn": 5, "lm_head": 6}
+KCLASS = {"moe_gate_up": 1, "moe_down": 2, "qkv": 3, "oproj": 4, "attn": 5, "lm_head": 6,
+          "router": 7}
 
 EXPORTED = tuple(_SIGS)
 

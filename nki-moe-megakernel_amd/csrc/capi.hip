@@ -163,6 +163,33 @@ int dense_gemm(GemmArgs a, int epi, bool xf32, hipStream_t s) {
   return MKD_OK;
 }
 
+// Router GEMM split over K across blocks so that even E = 128 (8 row blocks)
+// occupies ~128 blocks; the select kernel sums the partials in order.
+int router_kgrid(int E, int H) {
+  const int tiles = (E + 15) / 16;
+  int kg = 1;
+  while (kg < 16 && tiles * kg < 128) kg *= 2;
+  while (kg > 1 && choose_kw_split(H, kg) <= 0) kg /= 2;
+  return kg;
+}
+
+// logits (split-K partials into `parts`) -> select (+ groups when r.n_groups).
+int router_stage(const void* x, bool xf32, int H, const void* w_packed, float* parts, RouterArgs r,
+                 hipStream_t s) {
+  const int kg = router_kgrid(r.E, H);
+  GemmArgs a = dense_args(w_packed, x, H, r.E, H, r.T, parts, r.E);
+  a.kgrid = kg;
+  a.KW = kg > 1 ? choose_kw_split(H, kg) : choose_kw(H);
+  a.part_stride = (long long)r.T * r.E;
+  MKD_REQUIRE(a.KW > 0, MKD_ERR_UNSUPPORTED, "router: no K split for H=%d", H);
+  if (int rc = dense_gemm(a, EPI_F32, xf32, s)) return rc;
+  r.parts = parts;
+  r.nparts = kg;
+  r.part_stride = a.part_stride;
+  MKD_TRY(router_select_launch(r, s), "router select");
+  return MKD_OK;
+}
+
 struct MoeWs {
   int *n_groups, *grp_expert, *grp_count, *grp_offset, *pair_token, *pair_slot, *idx;
   float *slot_w, *ybuf;
@@ -203,8 +230,9 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
              const uint16_t* resid, uint16_t* out, float* out_f32, int T, int H, int E, int I,
              int K, int act, float alpha, float ghi, float glo, float uhi, float ulo, int round_qwen,
              MoeWs& w, hipStream_t s) {
-  MKD_TRY(moe_route_launch(idx, T, K, E, w.n_groups, w.grp_expert, w.grp_count, w.grp_offset,
-                           w.pair_token, w.pair_slot, s), "moe_route");
+  if (idx)  // otherwise the router stage already built the expert groups
+    MKD_TRY(moe_route_launch(idx, T, K, E, w.n_groups, w.grp_expert, w.grp_count, w.grp_offset,
+                             w.pair_token, w.pair_slot, s), "moe_route");
   const int gmax = E < T * K ? E : T * K;
   // Routed experts see few tokens each (T*K/E on average), so one 16-token
   // MFMA column tile per block; groups with more tokens use extra z-tiles.
@@ -300,24 +328,33 @@ int mkd_linear(const void* x, int x_dtype, int ldx, int rows, const void* w_pack
   return dense_gemm(a, epi, x_dtype == MKD_DT_F32, static_cast<hipStream_t>(stream));
 }
 
+size_t mkd_router_workspace_bytes(int T, int H, int E) {
+  return (size_t)router_kgrid(E, H) * T * E * sizeof(float) + 256;
+}
+
 int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_packed, int E,
                     const void* w_bias, float* router_logits, float* expert_affinities,
-                    int* expert_index, float* topk_affinities, int k, int mode, void* stream) {
+                    int* expert_index, float* topk_affinities, int k, int mode, void* workspace,
+                    size_t workspace_bytes, void* stream) {
   if (int rc = stale_check("mkd_router_topk")) return rc;
-  MKD_REQUIRE(x && w_packed && router_logits && expert_index, MKD_ERR_NULL, "router_topk: null pointer");
+  MKD_REQUIRE(x && w_packed && router_logits && expert_index && workspace, MKD_ERR_NULL,
+              "router_topk: null pointer");
   MKD_REQUIRE(T > 0 && T <= 128, MKD_ERR_INVALID, "router_topk: T %d must be in [1, 128]", T);
   MKD_REQUIRE(E > 0 && E <= 512, MKD_ERR_INVALID, "router_topk: E %d must be in [1, 512]", E);
   MKD_REQUIRE(k >= 1 && k <= 8 && k <= E, MKD_ERR_INVALID, "router_topk: k %d must be in [1, 8]", k);
   if (int rc = check_gemm_dims(E, H, 1)) return rc;
   const bool pre = mode & MKD_ROUTER_PRE_NORM, norm = mode & MKD_ROUTER_NORM_TOPK;
   MKD_REQUIRE(!(norm && !pre), MKD_ERR_INVALID, "router_topk: norm_topk_prob requires router_pre_norm");
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  GemmArgs a = dense_args(w_packed, x, H, E, H, T, router_logits, E);
-  a.bias = static_cast<const uint16_t*>(w_bias);
-  if (int rc = dense_gemm(a, EPI_F32, x_dtype == MKD_DT_F32, s)) return rc;
-  MKD_TRY(router_topk_launch(router_logits, T, E, k, mode, expert_affinities, expert_index,
-                             topk_affinities, nullptr, s), "router_topk launch");
-  return MKD_OK;
+  MKD_REQUIRE(workspace_bytes >= mkd_router_workspace_bytes(T, H, E), MKD_ERR_WORKSPACE,
+              "router_topk: workspace %zu < %zu bytes", workspace_bytes, mkd_router_workspace_bytes(T, H, E));
+  RouterArgs r;
+  memset(&r, 0, sizeof(r));
+  r.bias = static_cast<const uint16_t*>(w_bias);
+  r.T = T; r.E = E; r.K = k; r.mode = mode;
+  r.logits_out = router_logits; r.aff_full = expert_affinities; r.idx_out = expert_index;
+  r.topk_out = topk_affinities;
+  return router_stage(x, x_dtype == MKD_DT_F32, H, w_packed, static_cast<float*>(workspace), r,
+                      static_cast<hipStream_t>(stream));
 }
 
 size_t mkd_moe_workspace_bytes(int T, int H, int E, int I, int K) {
@@ -368,19 +405,18 @@ int mkd_moe_tkg(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, 
 // ---------------------------------------------------------------------------
 // attention block
 // ---------------------------------------------------------------------------
-static const int kChunk = 256;
-
 struct AttnWs {
   uint16_t* hnorm;
   float* qkv;
   uint16_t *q, *kvn, *attn;
   float *po, *pml;
-  int n_chunks;
+  int chunk, n_chunks;
 };
 
 static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_max) {
   AttnWs w;
-  w.n_chunks = (S_max + 1 + kChunk - 1) / kChunk;
+  w.chunk = attn_chunk_for(B, nkv, S_max);
+  w.n_chunks = (S_max + 1 + w.chunk - 1) / w.chunk;
   w.hnorm = c.take<uint16_t>((size_t)B * H);
   w.qkv = c.take<float>((size_t)B * (nq + 2 * nkv) * d);
   w.q = c.take<uint16_t>((size_t)B * nq * d);
@@ -435,7 +471,7 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   a.scale = p->softmax_scale > 0.f ? p->softmax_scale : 1.0f / sqrtf((float)p->d);
   a.round_qwen = p->round_qwen;
   a.B = p->B; a.nq = p->nq; a.nkv = p->nkv; a.d = p->d; a.S_max = p->S_max;
-  a.chunk = kChunk; a.n_chunks = w.n_chunks;
+  a.chunk = w.chunk; a.n_chunks = w.n_chunks;
   a.part_o = w.po; a.part_ml = w.pml;
   a.attn_out = w.attn;
   a.update_cache = p->update_cache;
@@ -513,7 +549,7 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.r = c.take<uint16_t>((size_t)B * m->H);
   w.nbf = c.take<uint16_t>((size_t)B * m->H);
   w.nf32 = c.take<float>((size_t)B * m->H);
-  w.logits = c.take<float>((size_t)B * m->E);
+  w.logits = c.take<float>((size_t)router_kgrid(m->E, m->H) * B * m->E);  // split-K partials
   w.cos = c.take<float>((size_t)B * m->d);
   w.sin = c.take<float>((size_t)B * m->d);
   w.moe = carve_moe(c, B, m->H, m->E, m->I, m->K);
@@ -573,11 +609,20 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     // post-attention RMSNorm: bf16 copy for the experts, fp32 copy for the router
     MKD_TRY(rmsnorm_launch(w.r, 0, nullptr, nullptr, static_cast<const uint16_t*>(m->ln_post[l]),
                            w.nbf, w.nf32, B, m->H, m->H, m->H, m->eps, 0, s), "post norm");
-    GemmArgs ra = dense_args(m->router[l], w.nf32, m->H, m->E, m->H, B, w.logits, m->E);
-    if (int rc = dense_gemm(ra, EPI_F32, true, s)) return rc;
-    MKD_TRY(router_topk_launch(w.logits, B, m->E, m->K, MKD_ROUTER_QWEN, nullptr, w.moe.idx,
-                               nullptr, w.moe.slot_w, s), "router topk");
-    if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], w.moe.idx, w.moe.slot_w, nullptr,
+    // router (fp32 normed input, split-K) + Qwen top-k + expert groups in one select launch
+    RouterArgs ra;
+    memset(&ra, 0, sizeof(ra));
+    ra.T = B; ra.E = m->E; ra.K = m->K; ra.mode = MKD_ROUTER_QWEN;
+    ra.idx_out = w.moe.idx; ra.slot_w = w.moe.slot_w;
+    ra.n_groups = w.moe.n_groups; ra.grp_expert = w.moe.grp_expert;
+    ra.grp_count = w.moe.grp_count; ra.grp_offset = w.moe.grp_offset;
+    ra.pair_token = w.moe.pair_token; ra.pair_slot = w.moe.pair_slot;
+    {
+      const int ps = prof_begin(MKD_KCLASS_ROUTER, s);
+      if (int rc = router_stage(w.nf32, true, m->H, m->router[l], w.logits, ra, s)) return rc;
+      prof_end(ps, s);
+    }
+    if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], nullptr, w.moe.slot_w, nullptr,
                           nullptr, w.r, x, nullptr, B, m->H, m->E, m->I, m->K, MKD_ACT_SILU, 1.f,
                           INFINITY, -INFINITY, INFINITY, -INFINITY, 1, w.moe, s))
       return rc;

@@ -75,7 +75,9 @@ gemm_frag_kernel(GemmArgs a) {
   const int wave = threadIdx.x >> 6;
   const int rbase = blockIdx.x;          // index of the RB-row-block tile
   const int group = blockIdx.y;
-  const int ttile = blockIdx.z;
+  const int kg = a.kgrid > 1 ? a.kgrid : 1;
+  const int ttile = blockIdx.z / kg;
+  const int kblk = blockIdx.z % kg;
 
   // ---- token columns of this block ----
   int count, base;                       // tokens in this group / first pair
@@ -105,7 +107,7 @@ gemm_frag_kernel(GemmArgs a) {
 
   const int KB = a.K / 32;
   const int NF = a.KW / 32;              // fragments per wave
-  const int kb0 = wave * NF;
+  const int kb0 = (kblk * (int)(blockDim.x >> 6) + wave) * NF;
   const int koff = (lane >> 4) * 8;
 
   f32x4_t acc[RB][TN];
@@ -252,7 +254,7 @@ gemm_frag_kernel(GemmArgs a) {
       for (int i = 0; i < 4; ++i) o[i] = v[0][i] * sc;
     }
     if (EPI == EPI_F32 || EPI == EPI_SCALE_F32) {
-      float* y = reinterpret_cast<float*>(a.y) + (long long)orow * a.ldy + n0;
+      float* y = reinterpret_cast<float*>(a.y) + kblk * a.part_stride + (long long)orow * a.ldy + n0;
       if (vec) {
         *reinterpret_cast<f32x4_t*>(y) = f32x4_t{o[0], o[1], o[2], o[3]};
       } else {
@@ -276,8 +278,11 @@ gemm_frag_kernel(GemmArgs a) {
 // ---------------------------------------------------------------------------
 template <int RB, int TN, bool XF32, int EPI>
 static hipError_t launch_t(const GemmArgs& a, int n_tiles, int groups, int ttiles, hipStream_t s) {
-  const int nsplit = a.K / a.KW;
-  dim3 grid(n_tiles, groups, ttiles);
+  const int kg = a.kgrid > 1 ? a.kgrid : 1;
+  const int nsplit = a.K / (a.KW * kg);
+  if (nsplit < 1 || nsplit > 16 || nsplit * a.KW * kg != a.K) return hipErrorInvalidValue;
+  if (kg > 1 && EPI != EPI_F32) return hipErrorInvalidValue;
+  dim3 grid(n_tiles, groups, ttiles * kg);
   dim3 block(64 * nsplit);
   const size_t lds = nsplit > 1 ? (size_t)nsplit * RB * TN * 4 * 64 * sizeof(float) : 0;
   hipLaunchKernelGGL((gemm_frag_kernel<RB, TN, XF32, EPI>), grid, block, lds, s, a);
@@ -288,6 +293,16 @@ int choose_kw(int K) {
   // Largest per-wave K slice <= 512 that divides K into <= 16 waves.
   for (int kw : {512, 384, 256, 128, 64, 32}) {
     if (K % kw == 0 && K / kw <= 16) return kw;
+  }
+  return -1;
+}
+
+int choose_kw_split(int K, int kgrid) {
+  // per-wave slice for a K split over kgrid blocks of <= 4 waves each
+  if (K % kgrid) return -1;
+  const int kb = K / kgrid;
+  for (int kw : {512, 256, 128, 64, 32}) {
+    if (kb % kw == 0 && kb / kw <= 4) return kw;
   }
   return -1;
 }

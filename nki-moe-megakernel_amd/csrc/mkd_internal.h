@@ -33,9 +33,14 @@ struct GemmArgs {
   float alpha;
   float gate_hi, gate_lo, up_hi, up_lo;
   int round_qwen;             // Qwen rounding points (else one rounding of the product)
+  // split of K across blocks (EPI_F32 only): block kb writes its partial sum to
+  // y + kb * part_stride; the consumer adds the kgrid partials in order.
+  int kgrid;                  // 0 or 1: no split
+  long long part_stride;      // elements between partial outputs
 };
 
 int choose_kw(int K);
+int choose_kw_split(int K, int kgrid);
 hipError_t gemm_launch(GemmArgs a, int epi, bool xf32, int tn, int groups_max,
                        int max_tokens_per_group, hipStream_t s);
 hipError_t pack_frag_launch(const uint16_t* src, uint16_t* dst, int G, int N, int K,
@@ -82,12 +87,25 @@ struct AttnArgs {
 };
 hipError_t qk_prep_launch(const AttnArgs& a, int rope_mode, int round_qwen, hipStream_t s);
 hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t s);
+int attn_chunk_for(int B, int nkv, int S_max);   // positions per attention block (64/128/256)
 hipError_t attn_combine_launch(const AttnArgs& a, hipStream_t s);
 
 // moe.hip
-hipError_t router_topk_launch(const float* logits, int T, int E, int K, int mode,
-                              float* aff_full, int* idx_out, float* topk_out,
-                              float* slot_w, hipStream_t s);
+struct RouterArgs {
+  const float* parts;         // [nparts][T][E] fp32 partial logits (summed in order)
+  int nparts;
+  long long part_stride;      // elements between partials
+  const uint16_t* bias;       // [E] bf16 or null
+  int T, E, K, mode;          // mode: MKD_ROUTER_* bits
+  float* logits_out;          // [T, E] or null
+  float* aff_full;            // [T, E] or null
+  int* idx_out;               // [T, K] or null
+  float* topk_out;            // [T, K] or null
+  float* slot_w;              // [T*K] or null
+  // expert grouping (all null = skip)
+  int *n_groups, *grp_expert, *grp_count, *grp_offset, *pair_token, *pair_slot;
+};
+hipError_t router_select_launch(const RouterArgs& a, hipStream_t s);
 hipError_t moe_route_launch(const int* idx, int T, int K, int E, int* n_groups, int* grp_expert,
                             int* grp_count, int* grp_offset, int* pair_token, int* pair_slot,
                             hipStream_t s);

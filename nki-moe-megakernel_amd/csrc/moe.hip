@@ -1,8 +1,8 @@
 // Router top-k, token->expert grouping and the MoE epilogue.
 //
-// router_topk: one wave per token over fp32 logits [T, E] (E <= 512, K <= 8).
-//   Selection: K rounds of a wave arg-max on (value desc, index asc), i.e. the
-//   lowest index wins an exact tie.  Modes (bit field):
+// router_select: one block over fp32 logits [T, E] (E <= 512, K <= 8, T <= 128),
+//   rank-based top-k (value desc, index asc: the lowest index wins an exact
+//   tie), optionally followed by the expert grouping.  Modes (bit field):
 //     bit0 act      0 softmax, 1 sigmoid
 //     bit1 pre_norm activation on all E before top-k (ACT1) else on the top-k (ACT2)
 //     bit2 norm     L1-renormalise the top-k (ACT1 path)
@@ -23,111 +23,193 @@ namespace mkd {
 constexpr int kMaxE = 512;
 constexpr int kMaxPerLane = kMaxE / 64;
 
-struct VI { float v; int i; };
-MKD_DEV bool better(VI a, VI b) { return a.v > b.v || (a.v == b.v && a.i < b.i); }
-
-MKD_DEV VI wave_argmax(VI x) {
+// ---------------------------------------------------------------------------
+// Router select: one block (16 waves) for all T <= 128 tokens; wave w takes
+// tokens w, w+16, ...  Logits are the in-order sum of the split-K partials
+// (+ bias), all partial loads of a lane issued together.  Selection is
+// rank-based: element e gets slot r = #{e' : key[e'] > key[e] or (key[e'] ==
+// key[e] and e' < e)} and is chosen when r < K -- descending order, lowest
+// index first among equal keys, no serial shuffle chains.  Optionally the
+// same block then builds the expert groups: per-expert counts in LDS, one
+// wave scans them, the slots are scattered by expert.
+MKD_DEV int wave_excl_scan(int v, int lane) {
+  int x = v;
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    VI y{__shfl_xor(x.v, o, 64), __shfl_xor(x.i, o, 64)};
-    if (better(y, x)) x = y;
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
   }
-  return x;
+  return x - v;
 }
 
-__global__ void __launch_bounds__(256)
-router_topk_kernel(const float* __restrict__ logits, int T, int E, int K, int mode,
-                   float* __restrict__ aff_full, int* __restrict__ idx_out,
-                   float* __restrict__ topk_out, float* __restrict__ slot_w) {
-  const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= T) return;
-  const bool sigm = mode & 1, pre = mode & 2, norm = mode & 4, qwen = mode & 8;
-  const int per = (E + 63) / 64;
-  float l[kMaxPerLane], a[kMaxPerLane];
-  float mx = -INFINITY;
-  for (int j = 0; j < per; ++j) {
-    const int e = lane + 64 * j;
-    l[j] = (e < E) ? logits[(long long)t * E + e] : -INFINITY;
-    mx = fmaxf(mx, l[j]);
-  }
-  mx = wave_max(mx);
-  float sum = 0.f;
-  for (int j = 0; j < per; ++j) {
-    const int e = lane + 64 * j;
-    a[j] = (e < E) ? expf(l[j] - mx) : 0.f;
-    sum += a[j];
-  }
-  sum = wave_sum(sum);
-  const float inv = 1.0f / sum;
-  // selection key
-  float key[kMaxPerLane];
-  for (int j = 0; j < per; ++j) {
-    const int e = lane + 64 * j;
-    if (e >= E) { key[j] = -INFINITY; continue; }
-    if (qwen || !pre) key[j] = l[j];
-    else key[j] = sigm ? 1.0f / (1.0f + expf(-l[j])) : a[j] * inv;
-  }
-  int sel_i[8];
-  float sel_v[8];
-  for (int k = 0; k < K; ++k) {
-    VI best{-INFINITY, 0x7fffffff};
-    for (int j = 0; j < per; ++j) {
-      VI c{key[j], lane + 64 * j};
-      if (c.i < E && better(c, best)) best = c;
-    }
-    best = wave_argmax(best);
-    sel_i[k] = best.i;
-    sel_v[k] = best.v;
-    for (int j = 0; j < per; ++j)
-      if (lane + 64 * j == best.i) key[j] = -INFINITY;
-  }
-  // affinities of the selected experts
-  float w[8];
-  if (qwen) {
-    float s = 0.f;
-    for (int k = 0; k < K; ++k) { w[k] = rbf(expf(sel_v[k] - mx) * inv); s += w[k]; }
-    const float r = 1.0f / s;
-    for (int k = 0; k < K; ++k) w[k] = rbf(w[k] * r);
-  } else if (pre) {
-    for (int k = 0; k < K; ++k) w[k] = sel_v[k];
-    if (norm) {
-      float s = 0.f;
-      for (int k = 0; k < K; ++k) s += w[k];
-      const float r = 1.0f / s;
-      for (int k = 0; k < K; ++k) w[k] *= r;
-    }
-  } else {  // ACT2 on the top-k logits
-    if (sigm) {
-      for (int k = 0; k < K; ++k) w[k] = 1.0f / (1.0f + expf(-sel_v[k]));
-    } else {
-      const float m2 = sel_v[0];
-      float s = 0.f;
-      for (int k = 0; k < K; ++k) { w[k] = expf(sel_v[k] - m2); s += w[k]; }
-      const float r = 1.0f / s;
-      for (int k = 0; k < K; ++k) w[k] *= r;
-    }
-  }
-  if (lane < K) {
-    float wl = 0.f; int il = 0;
-    for (int k = 0; k < K; ++k) if (k == lane) { wl = w[k]; il = sel_i[k]; }
-    if (idx_out) idx_out[t * K + lane] = il;
-    if (topk_out) topk_out[t * K + lane] = wl;
-    if (slot_w) slot_w[t * K + lane] = wl;
-  }
-  if (aff_full) {
-    const bool full = pre && !norm && !qwen;
-    for (int j = 0; j < per; ++j) {
-      const int e = lane + 64 * j;
-      if (e >= E) continue;
-      float v = 0.f;
-      if (full) {
-        v = sigm ? 1.0f / (1.0f + expf(-l[j])) : a[j] * inv;
-      } else {
-        for (int k = 0; k < K; ++k) if (sel_i[k] == e) v = w[k];
+template <int PER>
+__global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
+  __shared__ __attribute__((aligned(16))) float key_s[16][kMaxE + 4];
+  __shared__ float sel_s[16][8];
+  __shared__ float wsel_s[16][8];
+  __shared__ int idx_s[128 * 8];
+  __shared__ int cnt[kMaxE], off[kMaxE], cursor[kMaxE];
+  __shared__ int n_live;
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int E = a.E, K = a.K, T = a.T;
+  const bool sigm = a.mode & 1, pre = a.mode & 2, norm = a.mode & 4, qwen = a.mode & 8;
+  const int E4 = (E + 3) & ~3;
+  // every slot starts invalid so that NaN logits (no consistent ranks) can never
+  // route a slot to an out-of-range expert below
+  for (int p = tid; p < T * K; p += blockDim.x) idx_s[p] = -1;
+  for (int e = tid; e < E; e += blockDim.x) { cnt[e] = 0; cursor[e] = 0; }
+  __syncthreads();
+  for (int t = wv; t < T; t += 16) {
+    float l[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) l[j] = 0.f;
+#pragma unroll
+    for (int p = 0; p < 16; ++p) {
+      if (p < a.nparts) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int e = lane + 64 * j;
+          if (e < E) l[j] += a.parts[p * a.part_stride + (long long)t * E + e];
+        }
       }
-      aff_full[(long long)t * E + e] = v;
     }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E) {
+        if (a.bias) l[j] += bf2f(a.bias[e]);
+        if (a.logits_out) a.logits_out[(long long)t * E + e] = l[j];
+      } else {
+        l[j] = -INFINITY;
+      }
+      mx = fmaxf(mx, l[j]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.f, ex[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      ex[j] = (lane + 64 * j < E) ? expf(l[j] - mx) : 0.f;
+      sum += ex[j];
+    }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sum;
+    float key[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      key[j] = -INFINITY;
+      if (e < E) key[j] = (qwen || !pre) ? l[j] : (sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv);
+      if (e < E4) key_s[wv][e] = key[j];      // pad [E, E4) with -inf
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    int rank[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) rank[j] = 0;
+    for (int e4 = 0; e4 < E4; e4 += 4) {
+      const f32x4_t kv = *reinterpret_cast<const f32x4_t*>(&key_s[wv][e4]);
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int e = lane + 64 * j;
+          rank[j] += (kv[q] > key[j] || (kv[q] == key[j] && e4 + q < e)) ? 1 : 0;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E && rank[j] < K) {
+        idx_s[t * K + rank[j]] = e;
+        sel_s[wv][rank[j]] = key[j];
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    if (lane < K) {
+      float w;
+      if (qwen) {
+        // softmax value at the selected logits -> bf16 -> bf16 L1 renormalisation
+        float s = 0.f;
+        for (int k = 0; k < K; ++k) s += rbf(expf(sel_s[wv][k] - mx) * inv);
+        w = rbf(rbf(expf(sel_s[wv][lane] - mx) * inv) * (1.0f / s));
+      } else if (pre) {
+        w = sel_s[wv][lane];
+        if (norm) {
+          float s = 0.f;
+          for (int k = 0; k < K; ++k) s += sel_s[wv][k];
+          w *= 1.0f / s;
+        }
+      } else if (sigm) {
+        w = 1.0f / (1.0f + expf(-sel_s[wv][lane]));
+      } else {
+        const float m2 = sel_s[wv][0];
+        float s = 0.f;
+        for (int k = 0; k < K; ++k) s += expf(sel_s[wv][k] - m2);
+        w = expf(sel_s[wv][lane] - m2) * (1.0f / s);
+      }
+      wsel_s[wv][lane] = w;
+      const int e = idx_s[t * K + lane];
+      if (a.idx_out) a.idx_out[t * K + lane] = e;
+      if (a.topk_out) a.topk_out[t * K + lane] = w;
+      if (a.slot_w) a.slot_w[t * K + lane] = w;
+      if (a.n_groups && e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __builtin_amdgcn_s_waitcnt(0);
+    __builtin_amdgcn_wave_barrier();
+    if (a.aff_full) {
+      const bool full = pre && !norm && !qwen;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int e = lane + 64 * j;
+        if (e >= E) continue;
+        float v;
+        if (full) v = sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv;
+        else v = rank[j] < K ? wsel_s[wv][rank[j]] : 0.f;
+        a.aff_full[(long long)t * E + e] = v;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (!a.n_groups) return;
+  __syncthreads();
+  // ---- expert groups: one wave scans the per-expert counts ----
+  if (wv == 0) {
+    constexpr int PE = kMaxE / 64;
+    int c[PE], lsum = 0, llive = 0;
+#pragma unroll
+    for (int j = 0; j < PE; ++j) {
+      const int e = lane * PE + j;
+      c[j] = (e < E) ? cnt[e] : 0;
+      lsum += c[j];
+      llive += c[j] > 0;
+    }
+    int base = wave_excl_scan(lsum, lane);
+    int gbase = wave_excl_scan(llive, lane);
+#pragma unroll
+    for (int j = 0; j < PE; ++j) {
+      const int e = lane * PE + j;
+      if (e < E) {
+        off[e] = base;
+        if (c[j] > 0) {
+          a.grp_expert[gbase] = e;
+          a.grp_count[gbase] = c[j];
+          a.grp_offset[gbase] = base;
+          ++gbase;
+        }
+      }
+      base += c[j];
+    }
+    if (lane == 63) { *a.n_groups = gbase; n_live = gbase; }
+  }
+  __syncthreads();
+  for (int p = tid; p < T * K; p += blockDim.x) {
+    const int e = idx_s[p];
+    if (e < 0 || e >= E) continue;
+    const int q = off[e] + atomicAdd(&cursor[e], 1);
+    a.pair_token[q] = p / K;
+    a.pair_slot[q] = p;
   }
 }
 
@@ -207,11 +289,14 @@ moe_finalize_kernel(const float* __restrict__ ybuf, int K, int H, const uint16_t
 }
 
 // ---------------------------------------------------------------------------
-hipError_t router_topk_launch(const float* logits, int T, int E, int K, int mode, float* aff_full,
-                              int* idx_out, float* topk_out, float* slot_w, hipStream_t s) {
-  if (E > kMaxE || K > 8 || K < 1 || K > E) return hipErrorInvalidValue;
-  hipLaunchKernelGGL(router_topk_kernel, dim3((T + 3) / 4), dim3(256), 0, s, logits, T, E, K, mode,
-                     aff_full, idx_out, topk_out, slot_w);
+hipError_t router_select_launch(const RouterArgs& a, hipStream_t s) {
+  if (a.E > kMaxE || a.K > 8 || a.K < 1 || a.K > a.E || a.T > 128 || a.T < 1 || a.nparts > 16)
+    return hipErrorInvalidValue;
+  const int per = (a.E + 63) / 64;
+  if (per <= 1) hipLaunchKernelGGL(router_select_kernel<1>, dim3(1), dim3(1024), 0, s, a);
+  else if (per <= 2) hipLaunchKernelGGL(router_select_kernel<2>, dim3(1), dim3(1024), 0, s, a);
+  else if (per <= 4) hipLaunchKernelGGL(router_select_kernel<4>, dim3(1), dim3(1024), 0, s, a);
+  else hipLaunchKernelGGL(router_select_kernel<8>, dim3(1), dim3(1024), 0, s, a);
   return hipGetLastError();
 }
 
