@@ -125,8 +125,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnArgs a) {
       const u32x4_t v = (t <= n) ? ld16(vr + dq + j * 8) : u32x4_t{0, 0, 0, 0};
       *reinterpret_cast<u32x4_t*>(vt + (lane & 15) * VS + dq + j * 8) = v;
     }
-    __builtin_amdgcn_s_waitcnt(0);            // LDS writes of this wave complete
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_sync();                          // V tile visible to the whole wave
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       const int col = dt * 16 + (lane & 15);

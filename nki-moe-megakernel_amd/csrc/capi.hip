@@ -229,7 +229,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
              const float* slot_w, const uint16_t* gu_bias, const uint16_t* dn_bias,
              const uint16_t* resid, uint16_t* out, float* out_f32, int T, int H, int E, int I,
              int K, int act, float alpha, float ghi, float glo, float uhi, float ulo, int round_qwen,
-             MoeWs& w, hipStream_t s) {
+             MoeWs& w, hipStream_t s, bool do_finalize = true) {
   if (idx)  // otherwise the router stage already built the expert groups
     MKD_TRY(moe_route_launch(idx, T, K, E, w.n_groups, w.grp_expert, w.grp_count, w.grp_offset,
                              w.pair_token, w.pair_slot, s), "moe_route");
@@ -239,6 +239,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
   const int tn = 1;
   {  // gate/up + activation
     GemmArgs a = dense_args(gate_up, hidden, H, 2 * I, H, T, w.hbuf, I);
+    a.KW = choose_kw(H, 256);   // two row blocks per wave: 2 x 8 fragments in one batch
     a.w_group_stride = (long long)2 * I * H;
     a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
     a.n_groups = w.n_groups; a.pair_row = w.pair_token; a.pair_out_row = w.pair_slot;
@@ -260,7 +261,8 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
     MKD_TRY(gemm_launch(a, EPI_SCALE_F32, false, tn, gmax, T, s), "moe down");
     prof_end(ps, s);
   }
-  MKD_TRY(moe_finalize_launch(w.ybuf, T, K, H, resid, out, out_f32, s), "moe finalize");
+  if (do_finalize)
+    MKD_TRY(moe_finalize_launch(w.ybuf, T, K, H, resid, out, out_f32, s), "moe finalize");
   return MKD_OK;
 }
 
@@ -284,8 +286,7 @@ int mkd_rmsnorm_tkg(const void* input, int input_dtype, const void* gamma, void*
   const int ha = hidden_actual > 0 ? hidden_actual : hidden;
   MKD_REQUIRE(ha <= hidden, MKD_ERR_INVALID, "rmsnorm_tkg: hidden_actual %d > hidden %d", ha, hidden);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  MKD_TRY(rmsnorm_launch(input, input_dtype == MKD_DT_F32, nullptr, nullptr,
-                         static_cast<const uint16_t*>(gamma),
+  MKD_TRY(rmsnorm_launch(input, input_dtype == MKD_DT_F32, static_cast<const uint16_t*>(gamma),
                          output_dtype == MKD_DT_BF16 ? static_cast<uint16_t*>(output) : nullptr,
                          output_dtype == MKD_DT_F32 ? static_cast<float*>(output) : nullptr, rows,
                          hidden, hidden, ha, eps, 0, s), "rmsnorm launch");
@@ -433,13 +434,17 @@ size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S
   return c.used;
 }
 
+// o_parts != null: the output projection writes fp32 split-K partials
+// [kgrid][B][H_out] there (the caller's next norm folds them into the residual)
+// instead of applying the bf16 / residual epilogue.
 static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos_for_rope,
-                          const float* inv_freq, hipStream_t s) {
+                          const float* inv_freq, hipStream_t s, float* o_parts = nullptr,
+                          int o_kgrid = 1) {
   const int qkv_n = (p->nq + 2 * p->nkv) * p->d;
   // 1. optional RMSNorm
   const void* xin = p->X;
   if (p->rmsnorm_gamma) {
-    MKD_TRY(rmsnorm_launch(p->X, 0, nullptr, nullptr, static_cast<const uint16_t*>(p->rmsnorm_gamma),
+    MKD_TRY(rmsnorm_launch(p->X, 0, static_cast<const uint16_t*>(p->rmsnorm_gamma),
                            w.hnorm, nullptr, p->B, p->H, p->H, p->H, p->rmsnorm_eps,
                            p->rmsnorm_order, s), "attn rmsnorm");
     xin = w.hnorm;
@@ -491,7 +496,16 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     o.bias = static_cast<const uint16_t*>(p->bias_out);
     o.residual = static_cast<const uint16_t*>(p->residual);
     const int ps = prof_begin(MKD_KCLASS_OPROJ, s);
-    if (int rc = dense_gemm(o, p->residual ? EPI_RESID_BF16 : EPI_BF16, false, s)) return rc;
+    if (o_parts) {
+      o.y = o_parts;
+      o.residual = nullptr;
+      o.kgrid = o_kgrid;
+      o.KW = o_kgrid > 1 ? choose_kw_split(p->nq * p->d, o_kgrid) : choose_kw(p->nq * p->d);
+      o.part_stride = (long long)p->B * p->H_out;
+      if (int rc = dense_gemm(o, EPI_F32, false, s)) return rc;
+    } else if (int rc = dense_gemm(o, p->residual ? EPI_RESID_BF16 : EPI_BF16, false, s)) {
+      return rc;
+    }
     prof_end(ps, s);
   } else {
     MKD_TRY(hipMemcpyAsync(p->out, w.attn, (size_t)p->B * p->nq * p->d * 2, hipMemcpyDeviceToDevice, s),
@@ -539,7 +553,7 @@ int mkd_attention_block_tkg(const mkd_attention_args* p, void* workspace, size_t
 struct StepWs {
   AttnWs attn;
   uint16_t *r, *nbf;
-  float *nf32, *logits, *cos, *sin;
+  float *nf32, *logits, *cos, *sin, *oparts;
   MoeWs moe;
 };
 
@@ -552,6 +566,7 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.logits = c.take<float>((size_t)router_kgrid(m->E, m->H) * B * m->E);  // split-K partials
   w.cos = c.take<float>((size_t)B * m->d);
   w.sin = c.take<float>((size_t)B * m->d);
+  w.oparts = c.take<float>((size_t)2 * B * m->H);      // o_proj split-K partials
   w.moe = carve_moe(c, B, m->H, m->E, m->I, m->K);
   return w;
 }
@@ -586,14 +601,19 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     sin = w.sin;
   }
   uint16_t* x = static_cast<uint16_t*>(hidden);
-  for (int l = 0; l < m->num_layers; ++l) {
+  for (int l = 0; l < m->num_layers; ++l)
     MKD_REQUIRE(m->w_qkv[l] && m->w_o[l] && m->router[l] && m->gate_up[l] && m->down[l] &&
                 m->k_cache[l] && m->v_cache[l] && m->ln_in[l] && m->ln_post[l],
                 MKD_ERR_NULL, "decode_layers: null weight in layer %d", l);
+  // Layer l's pre-attention norm is produced by the previous layer's MoE
+  // finalize (one fused kernel); layer 0 normalises the input here.
+  MKD_TRY(rmsnorm_launch(x, 0, static_cast<const uint16_t*>(m->ln_in[0]), w.attn.hnorm, nullptr, B,
+                         m->H, m->H, m->H, m->eps, 1, s), "pre norm");
+  const int o_kgrid = ((m->H + 15) / 16 < 256 && choose_kw_split(m->nq * m->d, 2) > 0) ? 2 : 1;
+  for (int l = 0; l < m->num_layers; ++l) {
     mkd_attention_args ap;
     memset(&ap, 0, sizeof(ap));
-    ap.X = x;
-    ap.rmsnorm_gamma = m->ln_in[l]; ap.rmsnorm_eps = m->eps; ap.rmsnorm_order = 1;
+    ap.X = w.attn.hnorm;                       // already normalised
     ap.w_qkv_packed = m->w_qkv[l];
     ap.q_norm = m->q_norm[l]; ap.k_norm = m->k_norm[l]; ap.qk_eps = m->eps;
     ap.cos = cos; ap.sin = sin;
@@ -601,14 +621,23 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     ap.n_prior = position_ids;
     ap.update_cache = 1; ap.kv_cache_update_idx = position_ids;
     ap.w_out_packed = m->w_o[l];
-    ap.residual = x;
     ap.out = w.r;
     ap.B = B; ap.H = m->H; ap.H_out = m->H; ap.nq = m->nq; ap.nkv = m->nkv; ap.d = m->d;
     ap.S_max = m->S_max; ap.round_qwen = 1;
-    if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s)) return rc;
-    // post-attention RMSNorm: bf16 copy for the experts, fp32 copy for the router
-    MKD_TRY(rmsnorm_launch(w.r, 0, nullptr, nullptr, static_cast<const uint16_t*>(m->ln_post[l]),
-                           w.nbf, w.nf32, B, m->H, m->H, m->H, m->eps, 0, s), "post norm");
+    if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s, w.oparts, o_kgrid))
+      return rc;
+    // r = bf16(x + bf16(o_proj)) from the split-K partials, then the post-attention
+    // RMSNorm: bf16 copy for the experts, fp32 copy for the router
+    {
+      NormArgs na = {};
+      na.x = x; na.ld_in = m->H;
+      na.dsum = w.oparts; na.dK = o_kgrid; na.ds_row = m->H; na.ds_k = (long long)B * m->H;
+      na.resid_out = w.r;
+      na.gamma = static_cast<const uint16_t*>(m->ln_post[l]);
+      na.out_bf16 = w.nbf; na.out_f32 = w.nf32;
+      na.rows = B; na.H = m->H; na.hidden_actual = m->H; na.eps = m->eps; na.order = 0;
+      MKD_TRY(norm_launch(na, s), "residual + post norm");
+    }
     // router (fp32 normed input, split-K) + Qwen top-k + expert groups in one select launch
     RouterArgs ra;
     memset(&ra, 0, sizeof(ra));
@@ -624,8 +653,19 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     }
     if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], nullptr, w.moe.slot_w, nullptr,
                           nullptr, w.r, x, nullptr, B, m->H, m->E, m->I, m->K, MKD_ACT_SILU, 1.f,
-                          INFINITY, -INFINITY, INFINITY, -INFINITY, 1, w.moe, s))
+                          INFINITY, -INFINITY, INFINITY, -INFINITY, 1, w.moe, s, false))
       return rc;
+    // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention norm
+    {
+      NormArgs na = {};
+      na.x = w.r; na.ld_in = m->H;
+      na.dsum = w.moe.ybuf; na.dK = m->K; na.ds_row = (long long)m->K * m->H; na.ds_k = m->H;
+      na.resid_out = x;
+      na.gamma = (l + 1 < m->num_layers) ? static_cast<const uint16_t*>(m->ln_in[l + 1]) : nullptr;
+      na.out_bf16 = w.attn.hnorm;
+      na.rows = B; na.H = m->H; na.hidden_actual = m->H; na.eps = m->eps; na.order = 1;
+      MKD_TRY(norm_launch(na, s), "moe finalize + next norm");
+    }
   }
   return MKD_OK;
 }
@@ -663,8 +703,8 @@ int mkd_lm_head_greedy(const void* hidden, const void* ln_f, float eps, const vo
   int* si = c.take<int>((size_t)B * 64);
   MKD_REQUIRE(c.ok, MKD_ERR_WORKSPACE, "lm_head: workspace %zu < %zu bytes", workspace_bytes, c.used);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  MKD_TRY(rmsnorm_launch(hidden, 0, nullptr, nullptr, static_cast<const uint16_t*>(ln_f), n, nullptr,
-                         B, H, H, H, eps, 2, s), "final norm");
+  MKD_TRY(rmsnorm_launch(hidden, 0, static_cast<const uint16_t*>(ln_f), n, nullptr, B, H, H, H, eps,
+                         2, s), "final norm");
   GemmArgs a = dense_args(lm_head_packed, n, H, V, H, B, logits, V);
   {
     const int ps = prof_begin(MKD_KCLASS_LM_HEAD, s);

@@ -68,3 +68,12 @@ MKD_DEV f32x4_t mfma16x16x32(u32x4_t a, u32x4_t b, f32x4_t c) {
 }
 
 MKD_DEV float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+
+// Make this wave's LDS writes visible to its own later LDS reads by other lanes.
+// A wave's LDS operations complete in issue order, so no hardware wait is needed
+// (an s_waitcnt 0 here would also drain every outstanding global access); the
+// wavefront-scope fence only keeps the compiler from moving accesses across.
+MKD_DEV void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+}

@@ -65,6 +65,61 @@ __global__ void pack_frag_kernel(const uint16_t* __restrict__ src, uint16_t* __r
   }
 }
 
+// One fragment step: MFMA of weight fragment column u against the x fragments of
+// the TN token tiles (bf16 rows, or fp32 rows carried as a bf16 hi + lo pair).
+template <int RB, int TN, bool XF32, int U>
+MKD_DEV void frag_mma(const u32x4_t (&wf)[RB][U], int u, int k, const int (&xrow)[TN],
+                      const GemmArgs& a, f32x4_t (&acc)[RB][TN]) {
+#pragma unroll
+  for (int tn = 0; tn < TN; ++tn) {
+    if (XF32) {
+      u32x4_t hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
+      if (xrow[tn] >= 0) {
+        const float* xp = reinterpret_cast<const float*>(a.x) + (long long)xrow[tn] * a.ldx + k;
+        const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(xp);
+        const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(xp + 4);
+        const float xs[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+        uint32_t h[8], l[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          h[j] = f2bf(xs[j]);
+          l[j] = f2bf(xs[j] - bf2f(h[j]));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          hi[j] = h[2 * j] | (h[2 * j + 1] << 16);
+          lo[j] = l[2 * j] | (l[2 * j + 1] << 16);
+        }
+      }
+#pragma unroll
+      for (int r = 0; r < RB; ++r) {
+        acc[r][tn] = mfma16x16x32(wf[r][u], hi, acc[r][tn]);
+        acc[r][tn] = mfma16x16x32(wf[r][u], lo, acc[r][tn]);
+      }
+    } else {
+      u32x4_t xv = {0, 0, 0, 0};
+      if (xrow[tn] >= 0)
+        xv = ld16(reinterpret_cast<const uint16_t*>(a.x) + (long long)xrow[tn] * a.ldx + k);
+#pragma unroll
+      for (int r = 0; r < RB; ++r) acc[r][tn] = mfma16x16x32(wf[r][u], xv, acc[r][tn]);
+    }
+  }
+}
+
+// B consecutive fragments of every row block: all loads first, then the MFMAs.
+template <int RB, int TN, bool XF32, int B>
+MKD_DEV void stream_batch(const uint16_t* const (&wrow)[RB], int f, int kb0, int koff,
+                          const int (&xrow)[TN], const GemmArgs& a, f32x4_t (&acc)[RB][TN]) {
+  u32x4_t wf[RB][B];
+#pragma unroll
+  for (int u = 0; u < B; ++u)
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      wf[r][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow[r] + (f + u) * 512));
+#pragma unroll
+  for (int u = 0; u < B; ++u) frag_mma<RB, TN, XF32>(wf, u, (kb0 + f + u) * 32 + koff, xrow, a, acc);
+}
+
 // ---------------------------------------------------------------------------
 // The GEMM.
 // ---------------------------------------------------------------------------
@@ -121,56 +176,22 @@ gemm_frag_kernel(GemmArgs a) {
   for (int r = 0; r < RB; ++r)
     wrow[r] = w + ((long long)(rbase * RB + r) * KB + kb0) * 512 + lane * 8;
 
-  // Stream the fragments: weights are issued UNROLL ahead of their use.
-  constexpr int UNROLL = 8;
-  for (int f0 = 0; f0 < NF; f0 += UNROLL) {
-    u32x4_t wf[RB][UNROLL];
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u)
-#pragma unroll
-      for (int r = 0; r < RB; ++r)
-        if (f0 + u < NF) wf[r][u] = __builtin_nontemporal_load(
-            reinterpret_cast<const u32x4_t*>(wrow[r] + (f0 + u) * 512));
-#pragma unroll
-    for (int u = 0; u < UNROLL; ++u) {
-      if (f0 + u >= NF) break;
-      const int k = (kb0 + f0 + u) * 32 + koff;
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        if (XF32) {
-          u32x4_t hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
-          if (xrow[tn] >= 0) {
-            const float* xp = reinterpret_cast<const float*>(a.x) + (long long)xrow[tn] * a.ldx + k;
-            f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(xp);
-            f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(xp + 4);
-            float xs[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-            uint32_t h[8], l[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              h[j] = f2bf(xs[j]);
-              l[j] = f2bf(xs[j] - bf2f(h[j]));
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              hi[j] = h[2 * j] | (h[2 * j + 1] << 16);
-              lo[j] = l[2 * j] | (l[2 * j + 1] << 16);
-            }
-          }
-#pragma unroll
-          for (int r = 0; r < RB; ++r) {
-            acc[r][tn] = mfma16x16x32(wf[r][u], hi, acc[r][tn]);
-            acc[r][tn] = mfma16x16x32(wf[r][u], lo, acc[r][tn]);
-          }
-        } else {
-          u32x4_t xv = {0, 0, 0, 0};
-          if (xrow[tn] >= 0)
-            xv = ld16(reinterpret_cast<const uint16_t*>(a.x) + (long long)xrow[tn] * a.ldx + k);
-#pragma unroll
-          for (int r = 0; r < RB; ++r) acc[r][tn] = mfma16x16x32(wf[r][u], xv, acc[r][tn]);
-        }
-      }
-    }
-  }
+  // Stream the fragments: a wave issues a batch of UNROLL*RB fragment loads
+  // (<= 16 KiB) before the MFMAs that consume them; batches carry no guards so
+  // they stay in registers, and the remainder (< UNROLL) is taken as batches of
+  // 8/4/2/1 so short slices still keep several loads in flight.
+  constexpr int UNROLL = (TN <= 2) ? 16 / RB : 8 / RB;
+  int f = 0;
+  for (; f + UNROLL <= NF; f += UNROLL)
+    stream_batch<RB, TN, XF32, UNROLL>(wrow, f, kb0, koff, xrow, a, acc);
+  if constexpr (UNROLL > 8)
+    if (f + 8 <= NF) { stream_batch<RB, TN, XF32, 8>(wrow, f, kb0, koff, xrow, a, acc); f += 8; }
+  if constexpr (UNROLL > 4)
+    if (f + 4 <= NF) { stream_batch<RB, TN, XF32, 4>(wrow, f, kb0, koff, xrow, a, acc); f += 4; }
+  if constexpr (UNROLL > 2)
+    if (f + 2 <= NF) { stream_batch<RB, TN, XF32, 2>(wrow, f, kb0, koff, xrow, a, acc); f += 2; }
+  if constexpr (UNROLL > 1)
+    if (f < NF) stream_batch<RB, TN, XF32, 1>(wrow, f, kb0, koff, xrow, a, acc);
 
   // ---- cross-wave reduction (fixed order) ----
   extern __shared__ float red[];        // [nsplit][RB*TN*4][64]
@@ -289,10 +310,10 @@ static hipError_t launch_t(const GemmArgs& a, int n_tiles, int groups, int ttile
   return hipGetLastError();
 }
 
-int choose_kw(int K) {
-  // Largest per-wave K slice <= 512 that divides K into <= 16 waves.
+int choose_kw(int K, int max_kw) {
+  // Largest per-wave K slice <= max_kw that divides K into <= 16 waves.
   for (int kw : {512, 384, 256, 128, 64, 32}) {
-    if (K % kw == 0 && K / kw <= 16) return kw;
+    if (kw <= max_kw && K % kw == 0 && K / kw <= 16) return kw;
   }
   return -1;
 }

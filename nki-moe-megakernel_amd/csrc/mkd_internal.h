@@ -39,7 +39,7 @@ struct GemmArgs {
   long long part_stride;      // elements between partial outputs
 };
 
-int choose_kw(int K);
+int choose_kw(int K, int max_kw = 512);
 int choose_kw_split(int K, int kgrid);
 hipError_t gemm_launch(GemmArgs a, int epi, bool xf32, int tn, int groups_max,
                        int max_tokens_per_group, hipStream_t s);
@@ -48,10 +48,24 @@ hipError_t pack_frag_launch(const uint16_t* src, uint16_t* dst, int G, int N, in
                             int interleave_half, hipStream_t s);
 
 // norm.hip
-hipError_t rmsnorm_launch(const void* x, int x_f32, const uint16_t* delta, uint16_t* resid_out,
-                          const uint16_t* gamma, uint16_t* out_bf16, float* out_f32, int rows,
-                          int H, int ld_in, int hidden_actual, float eps, int order_x_rinv_first,
-                          hipStream_t s);
+struct NormArgs {
+  const void* x;              // [rows, ld_in] bf16 or fp32
+  int x_f32, ld_in;
+  const float* dsum;          // optional fp32 partial rows added to x (see norm.hip)
+  int dK;                     // number of partial rows per row
+  long long ds_row, ds_k;     // element strides of dsum (row, partial)
+  uint16_t* resid_out;        // bf16(x + bf16(sum)) when dsum
+  const uint16_t* gamma;      // null: no normalisation outputs
+  uint16_t* out_bf16;
+  float* out_f32;
+  int rows, H, hidden_actual;
+  float eps, inv_h;
+  int order;                  // 0 (x*g)*rinv, 1 (x*rinv)*g, 2 g*bf16(x*rinv)
+};
+hipError_t norm_launch(NormArgs a, hipStream_t s);
+hipError_t rmsnorm_launch(const void* x, int x_f32, const uint16_t* gamma, uint16_t* out_bf16,
+                          float* out_f32, int rows, int H, int ld_in, int hidden_actual,
+                          float eps, int order, hipStream_t s);
 
 // attention.hip
 struct AttnArgs {

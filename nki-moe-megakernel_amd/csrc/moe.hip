@@ -63,15 +63,26 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
     float l[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) l[j] = 0.f;
+    // split-K partial logits: issue a whole batch of loads (slots past nparts
+    // re-read the last partial and are masked out) before summing in fixed order
+    constexpr int PB = (PER <= 2) ? 16 : 4;
 #pragma unroll
-    for (int p = 0; p < 16; ++p) {
-      if (p < a.nparts) {
+    for (int p0 = 0; p0 < 16; p0 += PB) {
+      float v[PB][PER];
+#pragma unroll
+      for (int q = 0; q < PB; ++q) {
+        const int pp = min(p0 + q, a.nparts - 1);
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
-          const int e = lane + 64 * j;
-          if (e < E) l[j] += a.parts[p * a.part_stride + (long long)t * E + e];
+          const int e = min(lane + 64 * j, E - 1);
+          v[q][j] = a.parts[pp * a.part_stride + (long long)t * E + e];
         }
       }
+#pragma unroll
+      for (int q = 0; q < PB; ++q)
+#pragma unroll
+        for (int j = 0; j < PER; ++j)
+          if (p0 + q < a.nparts) l[j] += v[q][j];
     }
     float mx = -INFINITY;
 #pragma unroll
@@ -102,8 +113,7 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
       if (e < E) key[j] = (qwen || !pre) ? l[j] : (sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv);
       if (e < E4) key_s[wv][e] = key[j];      // pad [E, E4) with -inf
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_sync();
     int rank[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) rank[j] = 0;
@@ -125,8 +135,7 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
         sel_s[wv][rank[j]] = key[j];
       }
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_sync();
     if (lane < K) {
       float w;
       if (qwen) {
@@ -156,8 +165,7 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
       if (a.slot_w) a.slot_w[t * K + lane] = w;
       if (a.n_groups && e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __builtin_amdgcn_wave_barrier();
+    wave_lds_sync();
     if (a.aff_full) {
       const bool full = pre && !norm && !qwen;
 #pragma unroll

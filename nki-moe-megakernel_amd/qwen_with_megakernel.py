@@ -191,7 +191,7 @@ class Qwen3MoeMegakernelModel(nn.Module):
         self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float) / d))).to(device)
         self._build_struct()
         lib = L.load()
-        self.ws = torch.empty(max(lib.mkd_qwen3_workspace_bytes(self._model, batch), 256),
+        self.ws = torch.zeros(max(lib.mkd_qwen3_workspace_bytes(self._model, batch), 256),
                               dtype=torch.uint8, device=device)
         self.lm_ws = torch.empty(max(lib.mkd_lm_head_workspace_bytes(batch, cfg.hidden_size, cfg.vocab_size), 256),
                                  dtype=torch.uint8, device=device)
