@@ -10,10 +10,14 @@ back.  The whole step is captured once as a HIP graph and replayed.
 
 Also reported:
   roofline      -- the dominant kernel (MoE gate/up grouped GEMM) timed live
-                   with HIP events recorded by the library around each of its
-                   launches inside the captured step; algorithmic bytes per
-                   launch = distinct experts * 2*I*H*2 (weights; activations
-                   are < 0.1%).
+                   with HIP events carried by each of its dispatch packets, in
+                   one eager step of the same workload right after the timed
+                   region; algorithmic bytes per launch = distinct experts *
+                   2*I*H*2 (weights; activations are < 0.1%).  `traffic` is
+                   the HBM bytes per launch measured by rocprofv3 counter runs
+                   (FETCH_SIZE + WRITE_SIZE, calibrated against a copy kernel of
+                   known size, `--calib-copy`) and read from
+                   profiles/gate_up_traffic.json when its workload matches.
   cpu_baseline  -- the CPU oracle (oracle/ref.py, fp32 torch on the host) on a
                    bounded sample: decode steps over 2 distinct layers' weights
                    (each used for 24 of the 48 layer slots), scaled to tok/s.
@@ -122,6 +126,8 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="after the JSON line, run a copy kernel of known size (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -193,9 +199,10 @@ def main():
     ms_step = ms_total / args.steps
     tok_s = B * args.steps / (ms_total / 1e3)
 
-    # Dominant kernel (MoE gate/up): HIP events recorded by the library on the
-    # launch stream around each launch, in one eager step right after the timed
-    # region (events are not recorded inside captured graphs).
+    # Dominant kernel (MoE gate/up): HIP events recorded by each gate/up
+    # kernel's own dispatch packet on the launch stream (hipExtLaunchKernel), so
+    # a pair times the kernel alone, in one eager step right after the timed
+    # region (a captured graph keeps no timing events).
     L.check(lib.mkd_profile_events(L.KCLASS["moe_gate_up"], arr(ev_s), arr(ev_e), n_ev),
             "profile_events")
     step()
@@ -242,11 +249,40 @@ def main():
                    "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4)},
         "roofline": {"bound": "hbm", "kernel": "moe gate_up grouped GEMM (gemm_frag_kernel<2,1,0,3>)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers),
                      "avg_us": round(avg_ms * 1e3, 2), "bytes_per_launch": int(alg_bytes)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
+    if args.calib_copy:
+        calib_copy(dev)
+
+
+def measured_traffic(B, ctx, layers):
+    """HBM bytes per gate/up launch from the committed counter summary, or None."""
+    path = os.path.join(ROOT, "profiles", "gate_up_traffic.json")
+    try:
+        with open(path) as f:
+            t = json.load(f)
+    except (OSError, ValueError):
+        return None
+    w = t.get("workload", {})
+    if (w.get("batch"), w.get("kv_context"), w.get("layers")) != (B, ctx, layers):
+        return None
+    return t.get("bytes_per_launch")
+
+
+def calib_copy(dev, nbytes=256 << 20, reps=3):
+    """A plain copy kernel of known size (reads and writes `nbytes` each) for
+    scaling the FETCH_SIZE / WRITE_SIZE counters of a rocprofv3 --pmc run."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log(f"calib copy: {reps} x neg over {nbytes} bytes")
 
 
 if __name__ == "__main__":

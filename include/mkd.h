@@ -237,11 +237,13 @@ int mkd_decode_advance(int* token_ids, int* position_ids, const int* next_tokens
 
 /* ---------------------------------------------------------------------------
  * Measurement hook (no counterpart in the reference; used by bench.py).
- * After this call the library records start_events[i] / stop_events[i]
- * (hipEvent_t handles, host array) on the launch stream around the i-th
- * subsequent launch (i < n) of the kernel class below (eager launches only: a
- * launch on a capturing stream, or a failed record, turns the hook off).
- * kernel_class < 0 turns the hook off.  Process-global, not thread-safe.
+ * After this call the i-th subsequent launch (i < n) of the kernel class below
+ * records start_events[i] / stop_events[i] (hipEvent_t handles, host array) as
+ * part of the GEMM / attention kernel's own dispatch (hipExtLaunchKernel), so
+ * each pair times that kernel's execution alone.  Eager launches only: on a
+ * capturing stream nothing is recorded.  A class whose launch has no timed
+ * kernel turns the hook off.  kernel_class < 0 turns the hook off.
+ * Process-global, not thread-safe.
  * ------------------------------------------------------------------------- */
 #define MKD_KCLASS_MOE_GATE_UP 1
 #define MKD_KCLASS_MOE_DOWN 2

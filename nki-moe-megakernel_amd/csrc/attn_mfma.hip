@@ -171,9 +171,8 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnArgs a) {
 
 template <int D, int GQA, int TPW>
 static hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((attn_mfma_kernel<D, GQA, TPW>), dim3(a.n_chunks, a.nkv, a.B), dim3(256), 0,
-                     s, a);
-  return hipGetLastError();
+  return timed_launch(attn_mfma_kernel<D, GQA, TPW>, dim3(a.n_chunks, a.nkv, a.B), dim3(256), 0, s,
+                      a);
 }
 
 template <int D, int GQA>

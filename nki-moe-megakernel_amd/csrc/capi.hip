@@ -15,6 +15,8 @@
 
 using namespace mkd;
 
+LaunchTiming mkd::g_launch_timing;
+
 namespace {
 
 thread_local char g_err[512] = "";
@@ -66,29 +68,30 @@ struct ProfState {
   hipEvent_t stop[512];
 } g_prof;
 
-// Records are skipped while the stream is being captured (timing event nodes are
-// not available in captured graphs on this runtime); a failed record turns the
-// hook off and clears the error so it is not reported by the next launch.
-void record(hipEvent_t ev, hipStream_t s) {
-  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
-  hipError_t e = hipStreamIsCapturing(s, &st);
-  if (e == hipSuccess && st == hipStreamCaptureStatusNone) e = hipEventRecord(ev, s);
-  else if (e == hipSuccess) e = hipErrorStreamCaptureUnsupported;
-  if (e != hipSuccess) {
-    (void)hipGetLastError();
-    g_prof.cls = -1;
-  }
-}
-
-// Bracket one launch of class `cls`: prof_begin returns the slot (or -1).
+// The events of a slot are recorded by the bracketed kernel's own dispatch
+// (g_launch_timing), so they time the kernel alone.  Nothing is armed while the
+// stream is being captured (a graph keeps no timing events).  A bracket whose
+// launches never consumed the pair gives its slot back and turns the hook off,
+// so mkd_profile_count() reports fewer launches than the caller expected.
 int prof_begin(int cls, hipStream_t s) {
   if (g_prof.cls != cls || g_prof.next >= g_prof.n) return -1;
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &st) != hipSuccess || st != hipStreamCaptureStatusNone) {
+    (void)hipGetLastError();
+    return -1;
+  }
   const int i = g_prof.next++;
-  record(g_prof.start[i], s);
+  g_launch_timing.start = g_prof.start[i];
+  g_launch_timing.stop = g_prof.stop[i];
   return i;
 }
-void prof_end(int slot, hipStream_t s) {
-  if (slot >= 0) record(g_prof.stop[slot], s);
+void prof_end(int slot, hipStream_t) {
+  if (slot < 0) return;
+  if (g_launch_timing.start) {                // not consumed by any launch
+    g_launch_timing = LaunchTiming{};
+    --g_prof.next;
+    g_prof.cls = -1;
+  }
 }
 
 #define MKD_REQUIRE(cond, code, ...) \

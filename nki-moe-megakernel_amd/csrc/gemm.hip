@@ -306,8 +306,7 @@ static hipError_t launch_t(const GemmArgs& a, int n_tiles, int groups, int ttile
   dim3 grid(n_tiles, groups, ttiles * kg);
   dim3 block(64 * nsplit);
   const size_t lds = nsplit > 1 ? (size_t)nsplit * RB * TN * 4 * 64 * sizeof(float) : 0;
-  hipLaunchKernelGGL((gemm_frag_kernel<RB, TN, XF32, EPI>), grid, block, lds, s, a);
-  return hipGetLastError();
+  return timed_launch(gemm_frag_kernel<RB, TN, XF32, EPI>, grid, block, lds, s, a);
 }
 
 int choose_kw(int K, int max_kw) {

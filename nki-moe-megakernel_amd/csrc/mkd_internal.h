@@ -1,6 +1,7 @@
 // Internal launch interfaces shared by the kernel files and the C-ABI layer.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 #include <stdint.h>
 
 namespace mkd {
@@ -38,6 +39,28 @@ struct GemmArgs {
   int kgrid;                  // 0 or 1: no split
   long long part_stride;      // elements between partial outputs
 };
+
+// Kernel-dispatch timing.  When `start` is set, the next GEMM or attention
+// launch records the two events as part of its own dispatch packet
+// (hipExtLaunchKernel), so their elapsed time is that kernel's execution alone,
+// and clears the pair.  Host-side state of the library, single-threaded use.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+extern LaunchTiming g_launch_timing;
+
+// Launch `kernel` on `s`, consuming g_launch_timing when it is set.
+template <typename K, typename... Args>
+hipError_t timed_launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+  if (g_launch_timing.start) {
+    const LaunchTiming t = g_launch_timing;
+    g_launch_timing = LaunchTiming{};
+    hipExtLaunchKernelGGL(kernel, grid, block, (uint32_t)lds, s, t.start, t.stop, 0u, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds, s, args...);
+  }
+  return hipGetLastError();
+}
 
 int choose_kw(int K, int max_kw = 512);
 int choose_kw_split(int K, int kgrid);

@@ -20,7 +20,10 @@ import torch
 
 from . import _lib as L
 
-_cache: "weakref.WeakKeyDictionary[torch.Tensor, tuple]" = weakref.WeakKeyDictionary()
+# id(source tensor) -> (weakref to it, key, packed); an entry is dropped when its
+# source tensor is collected.  (A WeakKeyDictionary would compare tensor keys
+# with ==, which is elementwise for tensors.)
+_cache: "dict[int, tuple]" = {}
 
 
 def pack(src: torch.Tensor, groups: int, n: int, k: int, g_stride: int, row_stride: int,
@@ -92,10 +95,14 @@ def pack_experts_down_hf(w: torch.Tensor) -> torch.Tensor:
 
 def packed_cached(src: torch.Tensor, fn) -> torch.Tensor:
     """Memoise fn(src) per tensor object and version."""
-    ent = _cache.get(src)
+    ident = id(src)
     key = (fn.__name__, src._version, src.data_ptr(), tuple(src.shape), tuple(src.stride()))
-    if ent is not None and ent[0] == key:
-        return ent[1]
+    ent = _cache.get(ident)
+    same = ent is not None and ent[0]() is src
+    if same and ent[1] == key:
+        return ent[2]
     out = fn(src)
-    _cache[src] = (key, out)
+    if not same:
+        weakref.finalize(src, _cache.pop, ident, None)
+    _cache[ident] = (weakref.ref(src), key, out)
     return out

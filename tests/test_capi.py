@@ -51,3 +51,29 @@ def test_operators_fail_loudly_without_gpu_tensors():
     x = torch.zeros(1, 1, 128, dtype=torch.bfloat16)
     with pytest.raises(ValueError):
         mk.rmsnorm_tkg(x, torch.ones(128, dtype=torch.bfloat16), torch.empty_like(x))
+
+
+def test_packed_cache_is_per_tensor_and_version(mk):
+    """The repack memo hits for the same tensor object, misses after an in-place
+    change or for another tensor, and drops the entry when the tensor dies."""
+    import gc
+    import torch
+    from nki_moe_megakernel_amd import packing
+    calls = []
+
+    def fake_pack(t):
+        calls.append(1)
+        return t.clone()
+
+    a = torch.randn(4, 8)
+    b = torch.randn(4, 8)
+    pa = packing.packed_cached(a, fake_pack)
+    assert packing.packed_cached(a, fake_pack) is pa and len(calls) == 1
+    packing.packed_cached(b, fake_pack)
+    assert len(calls) == 2
+    a.add_(1.0)                      # bumps the version counter
+    assert packing.packed_cached(a, fake_pack) is not pa and len(calls) == 3
+    ident = id(b)
+    del b
+    gc.collect()
+    assert ident not in packing._cache

@@ -209,6 +209,38 @@ def test_moe_tkg(mk, dev, T, E, K, H, I, act, clamp, bias):
     assert max_abs_rel(out, y_ref) < TOL
 
 
+def test_profile_events_time_gate_up_dispatch(mk, dev):
+    """The measurement hook: each armed launch of the class records its event pair
+    through its own dispatch and the count matches the launches made."""
+    from nki_moe_megakernel_amd import _lib as L
+    lib = L.load()
+    g = torch.Generator().manual_seed(3)
+    T, E, K, H, I = 2, 8, 2, 512, 256
+    x = bf(torch.randn(T, H, generator=g)).to(dev)
+    gu = bf(0.03 * torch.randn(E, H, 2, I, generator=g)).to(dev)
+    dn = bf(0.03 * torch.randn(E, I, H, generator=g)).to(dev)
+    idx = torch.tensor([[0, 3], [3, 5]], dtype=torch.int32)
+    aff = torch.zeros(T, E).scatter_(1, idx.long(), 0.5).to(dev)
+    idx = idx.to(dev)
+    n = 3
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(2 * n)]
+    for e in ev:
+        e.record()
+    torch.cuda.synchronize()
+    arr = lambda es: (L.vp * n)(*[e.cuda_event for e in es])
+    L.check(lib.mkd_profile_events(L.KCLASS["moe_gate_up"], arr(ev[:n]), arr(ev[n:]), n), "arm")
+    try:
+        ys = [mk.moe_tkg(x, gu, dn, aff, idx, False) for _ in range(2)]
+        torch.cuda.synchronize()
+        assert lib.mkd_profile_count() == 2
+    finally:
+        L.check(lib.mkd_profile_events(-1, None, None, 0), "off")
+    for i in range(2):
+        ms = ev[i].elapsed_time(ev[n + i])
+        assert 0.0 < ms < 50.0, ms
+    torch.testing.assert_close(ys[0], ys[1], rtol=0, atol=0)
+
+
 def test_moe_tkg_rejects_large_T(mk, dev):
     x = torch.zeros(129, 128, dtype=torch.bfloat16, device=dev)
     gu = torch.zeros(4, 128, 2, 32, dtype=torch.bfloat16, device=dev)
