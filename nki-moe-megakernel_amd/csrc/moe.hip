@@ -29,9 +29,23 @@ constexpr int kMaxPerLane = kMaxE / 64;
 // (+ bias), all partial loads of a lane issued together.  Selection is
 // rank-based: element e gets slot r = #{e' : key[e'] > key[e] or (key[e'] ==
 // key[e] and e' < e)} and is chosen when r < K -- descending order, lowest
-// index first among equal keys, no serial shuffle chains.  Optionally the
+// index first among equal keys.  The K chosen are found by a radix select over
+// the keys' order-preserving codes (32 ballot steps per token, no data-
+// dependent branches); only those K are then ranked against each other.  Optionally the
 // same block then builds the expert groups: per-expert counts in LDS, one
 // wave scans them, the slots are scattered by expert.
+// Unsigned code with the order of the float (+0 and -0 share one code, NaN sorts
+// above +inf as in torch.topk).
+MKD_DEV uint32_t order_code(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b << 1) == 0) b = 0;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+// Number of set bits of `m` at lanes below this one.
+MKD_DEV int lanes_below(unsigned long long m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 MKD_DEV int wave_excl_scan(int v, int lane) {
   int x = v;
 #pragma unroll
@@ -44,7 +58,9 @@ MKD_DEV int wave_excl_scan(int v, int lane) {
 
 template <int PER>
 __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
-  __shared__ __attribute__((aligned(16))) float key_s[16][kMaxE + 4];
+  __shared__ uint32_t cu_s[16][8];
+  __shared__ int ce_s[16][8], slot_s[16][8];
+  __shared__ float ck_s[16][8];
   __shared__ float sel_s[16][8];
   __shared__ float wsel_s[16][8];
   __shared__ int idx_s[128 * 8];
@@ -53,7 +69,6 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int E = a.E, K = a.K, T = a.T;
   const bool sigm = a.mode & 1, pre = a.mode & 2, norm = a.mode & 4, qwen = a.mode & 8;
-  const int E4 = (E + 3) & ~3;
   // every slot starts invalid so that NaN logits (no consistent ranks) can never
   // route a slot to an out-of-range expert below
   for (int p = tid; p < T * K; p += blockDim.x) idx_s[p] = -1;
@@ -105,35 +120,60 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
     }
     sum = wave_sum(sum);
     const float inv = 1.0f / sum;
+    // ---- top-K: radix select on order-preserving key codes ----
+    // The threshold is the code of the K-th largest key, found bit by bit from
+    // the top with wave ballots; keys above it are taken, keys equal to it are
+    // taken lowest index first until K.  Slots e >= E get code 0, below every
+    // real key.
     float key[PER];
+    uint32_t u[PER];
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int e = lane + 64 * j;
-      key[j] = -INFINITY;
-      if (e < E) key[j] = (qwen || !pre) ? l[j] : (sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv);
-      if (e < E4) key_s[wv][e] = key[j];      // pad [E, E4) with -inf
+      key[j] = (qwen || !pre) ? l[j] : (sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv);
+      u[j] = (e < E) ? order_code(key[j]) : 0u;
+    }
+    uint32_t thr = 0, hmask = 0;
+    int kt = K;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t m = hmask | (1u << bit), want = thr | (1u << bit);
+      int c = 0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) c += __popcll(__ballot((u[j] & m) == want));
+      if (c >= kt) thr = want;
+      else kt -= c;
+      hmask = m;
+    }
+    // compact the K chosen elements (index order) into the wave's candidate slots
+    int cpos[PER];
+    int nsel = 0, ties = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const unsigned long long eq = __ballot(u[j] == thr);
+      const bool take = u[j] > thr || (u[j] == thr && ties + lanes_below(eq) < kt);
+      const unsigned long long tm = __ballot(take);
+      cpos[j] = take ? nsel + lanes_below(tm) : -1;
+      if (take) {
+        cu_s[wv][cpos[j]] = u[j];
+        ce_s[wv][cpos[j]] = lane + 64 * j;
+        ck_s[wv][cpos[j]] = key[j];
+      }
+      nsel += __popcll(tm);
+      ties += __popcll(eq);
     }
     wave_lds_sync();
-    int rank[PER];
-#pragma unroll
-    for (int j = 0; j < PER; ++j) rank[j] = 0;
-    for (int e4 = 0; e4 < E4; e4 += 4) {
-      const f32x4_t kv = *reinterpret_cast<const f32x4_t*>(&key_s[wv][e4]);
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-          const int e = lane + 64 * j;
-          rank[j] += (kv[q] > key[j] || (kv[q] == key[j] && e4 + q < e)) ? 1 : 0;
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const int e = lane + 64 * j;
-      if (e < E && rank[j] < K) {
-        idx_s[t * K + rank[j]] = e;
-        sel_s[wv][rank[j]] = key[j];
+    // output slot = rank among the K chosen (key descending, index ascending)
+    if (lane < K) {
+      const uint32_t ui = cu_s[wv][lane];
+      const int ei = ce_s[wv][lane];
+      int r = 0;
+      for (int m = 0; m < K; ++m) {
+        const uint32_t um = cu_s[wv][m];
+        r += (um > ui) | ((um == ui) & (ce_s[wv][m] < ei));
       }
+      idx_s[t * K + r] = ei;
+      sel_s[wv][r] = ck_s[wv][lane];
+      slot_s[wv][lane] = r;
     }
     wave_lds_sync();
     if (lane < K) {
@@ -174,7 +214,7 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
         if (e >= E) continue;
         float v;
         if (full) v = sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv;
-        else v = rank[j] < K ? wsel_s[wv][rank[j]] : 0.f;
+        else v = cpos[j] >= 0 ? wsel_s[wv][slot_s[wv][cpos[j]]] : 0.f;
         a.aff_full[(long long)t * E + e] = v;
       }
     }

@@ -164,6 +164,29 @@ def test_router_topk(mk, dev, T, E, k, pre, norm, act, xdt):
         assert (aff.cpu() - a_ref).abs().max().item() < 1e-5
 
 
+@pytest.mark.parametrize("T,E,k", [(1, 128, 8), (16, 128, 8), (3, 512, 8), (40, 64, 6)])
+def test_router_topk_exact_ties(mk, dev, T, E, k):
+    """Duplicated router columns give bit-identical logits: the chosen experts and
+    their order must be the stable order (value descending, lowest index first)."""
+    from nki_moe_megakernel_amd.common_types import RouterActFnType
+    g = torch.Generator().manual_seed(E + k)
+    H = 2048
+    x = bf(torch.randn(T, H, generator=g))
+    w = bf(0.02 * torch.randn(H, E, generator=g))
+    for a, b in [(1, 5), (2, 9), (9, 40), (3, E - 1), (0, E // 2)]:
+        w[:, b] = w[:, a]                        # exact duplicates
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    aff = torch.empty(T, E, dtype=torch.float32, device=dev)
+    idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+    mk.router_topk(x.to(dev), w.to(dev), None, logits, aff, idx, RouterActFnType.SOFTMAX, k, 1, 0,
+                   router_pre_norm=False, norm_topk_prob=False)
+    lg = logits.cpu()
+    for a, b in [(1, 5), (2, 9), (9, 40), (3, E - 1), (0, E // 2)]:
+        assert torch.equal(lg[:, a], lg[:, b])
+    order = torch.sort(-lg, dim=-1, stable=True)[1][:, :k]
+    assert torch.equal(idx.cpu().long(), order)
+
+
 def test_router_rejects_bad_pipeline(mk, dev):
     from nki_moe_megakernel_amd.common_types import RouterActFnType
     x = torch.zeros(2, 128, dtype=torch.bfloat16, device=dev)
