@@ -110,8 +110,37 @@ int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_pack
                     size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
- * moe_tkg (selective experts, bf16) -- replaces nki_kernels/moe/moe_tkg.py:56
- * with is_all_expert=False (selective_expert_impl.py:84-519).
+ * MX (OCP Microscaling v1.0) formats -- the reference's MXFP8 / MXFP4 expert
+ * path (selective_expert_mx_impl.py:60-531, down_projection_mx_shard_H.py:
+ * 138-211; activations quantised by nisa.quantize_mx, :143-149).
+ * Blocks of 32 consecutive elements along the contraction share one E8M0
+ * scale byte (2^(byte-127)); elements are E4M3 (1 byte) or E2M1 (4 bits, two
+ * per byte, low nibble first).
+ *
+ * mkd_quantize_mx: rows of x (bf16 or fp32, row stride ldx elements, 16-byte
+ * aligned rows, k % 32 == 0) -> codes [rows][k_pad] (e4m3) or [rows][k_pad/2]
+ * (e2m1) and scales [rows][k_pad/32]; k_pad % 128 == 0, k_pad >= k, blocks
+ * past k are zero (scale byte 0).  Scale X = 2^(floor(log2 amax) - emax),
+ * element = RNE(v / X) saturated (448 / 6).
+ * mkd_pack_mx_weights: row-major codes [groups][n][k] (e4m3) or
+ * [groups][n][k/2] (e2m1) + scales [groups][n][k/32] (byte strides) into the
+ * scaled-MFMA fragment order; interleave_half as in mkd_pack_weights.
+ * ------------------------------------------------------------------------- */
+#define MKD_MX_E4M3 1
+#define MKD_MX_E2M1 2
+int mkd_quantize_mx(const void* x, int x_dtype, int rows, int k, int ldx, int fmt, void* codes,
+                    void* scales, int k_pad, void* stream);
+size_t mkd_packed_mx_bytes(int groups, int n, int k, int fmt);
+size_t mkd_packed_mx_scale_bytes(int groups, int n, int k);
+int mkd_pack_mx_weights(const void* codes, const void* scales, void* dst, void* dst_scales,
+                        int groups, int n, int k, long long g_stride, long long row_stride,
+                        long long s_g_stride, long long s_row_stride, int fmt,
+                        int interleave_half, void* stream);
+
+/* ---------------------------------------------------------------------------
+ * moe_tkg (selective experts) -- replaces nki_kernels/moe/moe_tkg.py:56
+ * with is_all_expert=False (selective_expert_impl.py:84-519; MX weights:
+ * selective_expert_mx_impl.py:60-531).
  * hidden [T, H] bf16; gate_up packed per expert from [E, H, 2, I]
  * (n = 2I interleaved, k = H); down packed per expert from [E, I, H] (n = H,
  * k = I); expert_index [T, K] int32; slot scales: expert_affinities [T, E]
@@ -121,6 +150,11 @@ int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_pack
  * round_qwen = 1 emulates the Qwen fused kernel's bf16 rounding points
  * (moe_fused_nki.py:506-527).  output [T, H] bf16; with residual (bf16 [T,H])
  * output = bf16(residual + bf16(moe)).  T <= 128.
+ * weight_format MKD_MX_E4M3 / MKD_MX_E2M1: the packed weights are MX
+ * (mkd_pack_mx_weights, gate/up k = H, down k = I) with their packed scales;
+ * the hidden rows and the bf16 SwiGLU output are quantised to MXFP8 (E4M3)
+ * before each projection (selective_expert_mx_impl.py:143-149,
+ * down_projection_mx_shard_H.py:74-79); round_qwen must be 0.
  * ------------------------------------------------------------------------- */
 typedef struct {
   const void* hidden;          /* [T, H] bf16                    */
@@ -140,6 +174,9 @@ typedef struct {
   float alpha;                 /* swish alpha                    */
   float gate_hi, gate_lo, up_hi, up_lo; /* +-INFINITY = no clamp */
   int round_qwen;
+  int weight_format;           /* 0 bf16, MKD_MX_E4M3, MKD_MX_E2M1 */
+  const void* gate_up_scales;  /* MX: packed scales of gate_up   */
+  const void* down_scales;     /* MX: packed scales of down      */
 } mkd_moe_args;
 size_t mkd_moe_workspace_bytes(int T, int H, int E, int I, int K);
 int mkd_moe_tkg(const mkd_moe_args* args, void* workspace, size_t workspace_bytes, void* stream);

@@ -53,6 +53,7 @@ class MoeArgs(C.Structure):
         ("scaling_mode", i32), ("activation", i32), ("alpha", f32),
         ("gate_hi", f32), ("gate_lo", f32), ("up_hi", f32), ("up_lo", f32),
         ("round_qwen", i32),
+        ("weight_format", i32), ("gate_up_scales", vp), ("down_scales", vp),
     ]
 
 
@@ -90,6 +91,10 @@ _SIGS = {
     "mkd_linear": (i32, [vp, i32, i32, i32, vp, i32, i32, vp, vp, i32, i32, vp, vp]),
     "mkd_router_workspace_bytes": (sz, [i32, i32, i32]),
     "mkd_router_topk": (i32, [vp, i32, i32, i32, vp, i32, vp, vp, vp, vp, vp, i32, i32, vp, sz, vp]),
+    "mkd_quantize_mx": (i32, [vp, i32, i32, i32, i32, i32, vp, vp, i32, vp]),
+    "mkd_packed_mx_bytes": (sz, [i32, i32, i32, i32]),
+    "mkd_packed_mx_scale_bytes": (sz, [i32, i32, i32]),
+    "mkd_pack_mx_weights": (i32, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i64, i64, i32, i32, vp]),
     "mkd_moe_workspace_bytes": (sz, [i32, i32, i32, i32, i32]),
     "mkd_moe_tkg": (i32, [C.POINTER(MoeArgs), vp, sz, vp]),
     "mkd_attention_workspace_bytes": (sz, [i32, i32, i32, i32, i32, i32]),

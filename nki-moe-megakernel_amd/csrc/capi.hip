@@ -146,7 +146,18 @@ int check_gemm_dims(int N, int K, int rb) {
   MKD_REQUIRE(N > 0 && (rb == 1 || N % (16 * rb) == 0), MKD_ERR_INVALID,
               "fused gate/up width %d must be a multiple of %d", N, 16 * rb);
   MKD_REQUIRE(K > 0 && K % 32 == 0, MKD_ERR_INVALID, "contraction %d must be a multiple of 32", K);
-  MKD_REQUIRE(choose_kw(K) > 0, MKD_ERR_UNSUPPORTED, "contraction %d too large (max 8192)", K);
+  MKD_REQUIRE(choose_kw(K) > 0, MKD_ERR_UNSUPPORTED,
+              "contraction %d has no split into <= 16 waves of a multiple of 32 (max 8192)", K);
+  return MKD_OK;
+}
+
+// MX weights: whole 16-row blocks (32 for fused gate/up), K % 32 == 0, and a
+// padded contraction that splits over <= 8 waves.
+int check_mx_dims(int N, int K, int rb) {
+  MKD_REQUIRE(N > 0 && N % (16 * rb) == 0, MKD_ERR_INVALID,
+              "MX weight rows %d must be a multiple of %d", N, 16 * rb);
+  MKD_REQUIRE(K > 0 && K % 32 == 0, MKD_ERR_INVALID, "MX contraction %d must be a multiple of 32", K);
+  MKD_REQUIRE(choose_kw_mx(mx_kpad(K)) > 0, MKD_ERR_UNSUPPORTED, "MX contraction %d is too large", K);
   return MKD_OK;
 }
 
@@ -197,7 +208,10 @@ struct MoeWs {
   int *n_groups, *grp_expert, *grp_count, *grp_offset, *pair_token, *pair_slot, *idx;
   float *slot_w, *ybuf;
   uint16_t* hbuf;
+  uint8_t *xq, *xs, *hq, *hs;   // MXFP8 codes / scales of the hidden rows and of hbuf
 };
+
+int mx_pad(int k) { return mx_kpad(k); }
 
 MoeWs carve_moe(Carver& c, int T, int H, int E, int I, int K) {
   MoeWs w;
@@ -211,6 +225,10 @@ MoeWs carve_moe(Carver& c, int T, int H, int E, int I, int K) {
   w.slot_w = c.take<float>((size_t)T * K);
   w.hbuf = c.take<uint16_t>((size_t)T * K * I);
   w.ybuf = c.take<float>((size_t)T * K * H);
+  w.xq = c.take<uint8_t>((size_t)T * mx_pad(H));
+  w.xs = c.take<uint8_t>((size_t)T * mx_pad(H) / 32);
+  w.hq = c.take<uint8_t>((size_t)T * K * mx_pad(I));
+  w.hs = c.take<uint8_t>((size_t)T * K * mx_pad(I) / 32);
   return w;
 }
 
@@ -232,11 +250,54 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
              const float* slot_w, const uint16_t* gu_bias, const uint16_t* dn_bias,
              const uint16_t* resid, uint16_t* out, float* out_f32, int T, int H, int E, int I,
              int K, int act, float alpha, float ghi, float glo, float uhi, float ulo, int round_qwen,
-             MoeWs& w, hipStream_t s, bool do_finalize = true) {
+             MoeWs& w, hipStream_t s, bool do_finalize = true, int wfmt = 0,
+             const void* gu_scales = nullptr, const void* dn_scales = nullptr) {
   if (idx)  // otherwise the router stage already built the expert groups
     MKD_TRY(moe_route_launch(idx, T, K, E, w.n_groups, w.grp_expert, w.grp_count, w.grp_offset,
                              w.pair_token, w.pair_slot, s), "moe_route");
   const int gmax = E < T * K ? E : T * K;
+  if (wfmt) {
+    // MX experts: hidden -> MXFP8, gate/up (scaled MFMA) + SwiGLU -> bf16 h,
+    // h -> MXFP8, down (scaled MFMA) * slot affinity.
+    const int Hp = mx_pad(H), Ip = mx_pad(I);
+    MKD_TRY(mx_quantize_launch(hidden, false, T, H, H, MX_E4M3, w.xq, w.xs, Hp, s), "moe quantize hidden");
+    {
+      GemmArgs a = dense_args(gate_up, w.xq, Hp, 2 * I, Hp, T, w.hbuf, I);
+      a.KW = choose_kw_mx(Hp);
+      a.w_group_stride = mx_packed_code_bytes(1, 2 * I, H, wfmt);
+      a.w_scale = static_cast<const uint8_t*>(gu_scales);
+      a.w_scale_group_stride = mx_packed_scale_bytes(1, 2 * I, H);
+      a.x_scale = w.xs; a.ldxs = Hp / 32;
+      a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
+      a.n_groups = w.n_groups; a.pair_row = w.pair_token; a.pair_out_row = w.pair_slot;
+      a.bias = gu_bias; a.bias_group_stride = 2LL * I;
+      a.act = act; a.alpha = alpha; a.gate_hi = ghi; a.gate_lo = glo; a.up_hi = uhi; a.up_lo = ulo;
+      a.round_qwen = 0;
+      const int ps = prof_begin(MKD_KCLASS_MOE_GATE_UP, s);
+      MKD_TRY(gemm_mx_launch(a, wfmt, EPI_SWIGLU_BF16, gmax, T, s), "moe gate_up (mx)");
+      prof_end(ps, s);
+    }
+    MKD_TRY(mx_quantize_launch(w.hbuf, false, T * K, I, I, MX_E4M3, w.hq, w.hs, Ip, s),
+            "moe quantize intermediate");
+    {
+      GemmArgs a = dense_args(down, w.hq, Ip, H, Ip, T, w.ybuf, H);
+      a.KW = choose_kw_mx(Ip);
+      a.w_group_stride = mx_packed_code_bytes(1, H, I, wfmt);
+      a.w_scale = static_cast<const uint8_t*>(dn_scales);
+      a.w_scale_group_stride = mx_packed_scale_bytes(1, H, I);
+      a.x_scale = w.hs; a.ldxs = Ip / 32;
+      a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
+      a.n_groups = w.n_groups; a.pair_row = w.pair_slot; a.pair_out_row = w.pair_slot;
+      a.pair_scale = slot_w;
+      a.bias = dn_bias; a.bias_group_stride = H;
+      const int ps = prof_begin(MKD_KCLASS_MOE_DOWN, s);
+      MKD_TRY(gemm_mx_launch(a, wfmt, EPI_SCALE_F32, gmax, T, s), "moe down (mx)");
+      prof_end(ps, s);
+    }
+    if (do_finalize)
+      MKD_TRY(moe_finalize_launch(w.ybuf, T, K, H, resid, out, out_f32, s), "moe finalize");
+    return MKD_OK;
+  }
   // Routed experts see few tokens each (T*K/E on average), so one 16-token
   // MFMA column tile per block; groups with more tokens use extra z-tiles.
   const int tn = 1;
@@ -376,14 +437,26 @@ int mkd_moe_tkg(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, 
               "moe_tkg: only T <= 128 tokens are supported in selective mode, got %d", p->T);
   MKD_REQUIRE(p->E > 0 && p->E <= 512 && p->K >= 1 && p->K <= 8 && p->K <= p->E, MKD_ERR_INVALID,
               "moe_tkg: bad E=%d / K=%d", p->E, p->K);
-  if (int rc = check_gemm_dims(2 * p->I, p->H, 2)) return rc;
-  if (int rc = check_gemm_dims(p->H, p->I, 1)) return rc;
+  if (p->weight_format) {
+    if (int rc = check_mx_dims(2 * p->I, p->H, 2)) return rc;
+    if (int rc = check_mx_dims(p->H, p->I, 1)) return rc;
+  } else {
+    if (int rc = check_gemm_dims(2 * p->I, p->H, 2)) return rc;
+    if (int rc = check_gemm_dims(p->H, p->I, 1)) return rc;
+  }
   MKD_REQUIRE(p->scaling_mode == MKD_SCALE_NONE || p->scaling_mode == MKD_SCALE_POST,
               MKD_ERR_UNSUPPORTED, "moe_tkg: only NO_SCALE and POST_SCALE affinity scaling are supported");
   MKD_REQUIRE(!(p->scaling_mode == MKD_SCALE_POST && !p->expert_affinities && !p->slot_weights),
               MKD_ERR_NULL, "moe_tkg: POST_SCALE needs expert_affinities");
   MKD_REQUIRE(p->activation == MKD_ACT_SILU || p->activation == MKD_ACT_SWISH, MKD_ERR_UNSUPPORTED,
               "moe_tkg: unsupported activation %d", p->activation);
+  MKD_REQUIRE(p->weight_format == 0 || p->weight_format == MKD_MX_E4M3 ||
+                  p->weight_format == MKD_MX_E2M1, MKD_ERR_INVALID,
+              "moe_tkg: unknown weight_format %d", p->weight_format);
+  if (p->weight_format) {
+    MKD_REQUIRE(p->gate_up_scales && p->down_scales, MKD_ERR_NULL, "moe_tkg: MX weights need their scales");
+    MKD_REQUIRE(!p->round_qwen, MKD_ERR_UNSUPPORTED, "moe_tkg: round_qwen applies to bf16 weights only");
+  }
   MKD_REQUIRE(workspace, MKD_ERR_NULL, "moe_tkg: null workspace");
   Carver c{static_cast<char*>(workspace), workspace_bytes};
   MoeWs w = carve_moe(c, p->T, p->H, p->E, p->I, p->K);
@@ -403,7 +476,57 @@ int mkd_moe_tkg(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, 
                   static_cast<const uint16_t*>(p->down_bias),
                   static_cast<const uint16_t*>(p->residual), static_cast<uint16_t*>(p->output),
                   p->output_f32, p->T, p->H, p->E, p->I, p->K, p->activation, p->alpha,
-                  p->gate_hi, p->gate_lo, p->up_hi, p->up_lo, p->round_qwen, w, s);
+                  p->gate_hi, p->gate_lo, p->up_hi, p->up_lo, p->round_qwen, w, s, true,
+                  p->weight_format, p->gate_up_scales, p->down_scales);
+}
+
+int mkd_quantize_mx(const void* x, int x_dtype, int rows, int k, int ldx, int fmt, void* codes,
+                    void* scales, int k_pad, void* stream) {
+  if (int rc = stale_check("mkd_quantize_mx")) return rc;
+  MKD_REQUIRE(x && codes && scales, MKD_ERR_NULL, "quantize_mx: null pointer");
+  MKD_REQUIRE(x_dtype == MKD_DT_BF16 || x_dtype == MKD_DT_F32, MKD_ERR_INVALID, "quantize_mx: bad dtype");
+  MKD_REQUIRE(fmt == MKD_MX_E4M3 || fmt == MKD_MX_E2M1, MKD_ERR_INVALID, "quantize_mx: bad format %d", fmt);
+  MKD_REQUIRE(rows > 0 && k > 0 && k % 32 == 0 && k_pad >= k && k_pad % 128 == 0, MKD_ERR_INVALID,
+              "quantize_mx: need rows > 0, k %% 32 == 0, k_pad >= k, k_pad %% 128 == 0 (rows=%d k=%d k_pad=%d)",
+              rows, k, k_pad);
+  const int vec = x_dtype == MKD_DT_F32 ? 4 : 8;   // elements per 16 bytes
+  MKD_REQUIRE(ldx >= k && ldx % vec == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+                  (reinterpret_cast<uintptr_t>(codes) & 15) == 0, MKD_ERR_INVALID,
+              "quantize_mx: rows must be 16-byte aligned (ldx=%d)", ldx);
+  MKD_TRY(mx_quantize_launch(x, x_dtype == MKD_DT_F32, rows, k, ldx, fmt, static_cast<uint8_t*>(codes),
+                             static_cast<uint8_t*>(scales), k_pad, static_cast<hipStream_t>(stream)),
+          "quantize_mx launch");
+  return MKD_OK;
+}
+
+size_t mkd_packed_mx_bytes(int groups, int n, int k, int fmt) {
+  if (groups <= 0 || n <= 0 || k <= 0 || (fmt != MKD_MX_E4M3 && fmt != MKD_MX_E2M1)) return 0;
+  return (size_t)mx_packed_code_bytes(groups, n, k, fmt);
+}
+
+size_t mkd_packed_mx_scale_bytes(int groups, int n, int k) {
+  if (groups <= 0 || n <= 0 || k <= 0) return 0;
+  return (size_t)mx_packed_scale_bytes(groups, n, k);
+}
+
+int mkd_pack_mx_weights(const void* codes, const void* scales, void* dst, void* dst_scales,
+                        int groups, int n, int k, long long g_stride, long long row_stride,
+                        long long s_g_stride, long long s_row_stride, int fmt,
+                        int interleave_half, void* stream) {
+  if (int rc = stale_check("mkd_pack_mx_weights")) return rc;
+  MKD_REQUIRE(codes && scales && dst && dst_scales, MKD_ERR_NULL, "pack_mx_weights: null pointer");
+  MKD_REQUIRE(fmt == MKD_MX_E4M3 || fmt == MKD_MX_E2M1, MKD_ERR_INVALID, "pack_mx_weights: bad format %d", fmt);
+  MKD_REQUIRE(groups > 0 && n > 0 && k > 0 && k % 32 == 0, MKD_ERR_INVALID,
+              "pack_mx_weights: need k %% 32 == 0 (groups=%d n=%d k=%d)", groups, n, k);
+  MKD_REQUIRE(interleave_half == 0 || (interleave_half % 16 == 0 && 2 * interleave_half == n),
+              MKD_ERR_INVALID, "pack_mx_weights: interleave_half %d must be n/2 and a multiple of 16",
+              interleave_half);
+  MKD_TRY(mx_pack_launch(static_cast<const uint8_t*>(codes), static_cast<const uint8_t*>(scales),
+                         static_cast<uint8_t*>(dst), static_cast<uint8_t*>(dst_scales), groups, n, k,
+                         g_stride, row_stride, s_g_stride, s_row_stride, fmt, interleave_half,
+                         static_cast<hipStream_t>(stream)),
+          "pack_mx_weights launch");
+  return MKD_OK;
 }
 
 // ---------------------------------------------------------------------------

@@ -21,6 +21,7 @@
 // token rows come from the routing tables and the expert's weights from
 // w + expert * w_group_stride.
 #include "common.h"
+#include "gemm_epi.h"
 #include "mkd_internal.h"
 
 namespace mkd {
@@ -193,105 +194,7 @@ gemm_frag_kernel(GemmArgs a) {
   if constexpr (UNROLL > 1)
     if (f < NF) stream_batch<RB, TN, XF32, 1>(wrow, f, kb0, koff, xrow, a, acc);
 
-  // ---- cross-wave reduction (fixed order) ----
-  extern __shared__ float red[];        // [nsplit][RB*TN*4][64]
-  constexpr int NR = RB * TN * 4;
-  const int nsplit = blockDim.x >> 6;
-  if (nsplit > 1) {
-#pragma unroll
-    for (int r = 0; r < RB; ++r)
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          red[(wave * NR + (r * TN + tn) * 4 + i) * 64 + lane] = acc[r][tn][i];
-    __syncthreads();
-  }
-
-  // Each wave finalises the (tn) tiles with tn % nsplit == wave.
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) {
-    if (tn % nsplit != wave) continue;
-    float v[RB][4];
-#pragma unroll
-    for (int r = 0; r < RB; ++r)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (nsplit > 1) {
-          float s = 0.f;
-          for (int q = 0; q < nsplit; ++q) s += red[(q * NR + (r * TN + tn) * 4 + i) * 64 + lane];
-          v[r][i] = s;
-        } else {
-          v[r][i] = acc[r][tn][i];
-        }
-      }
-    if (xrow[tn] < 0) continue;
-    const int c = t0 + tn * 16 + (lane & 15);
-    const int orow = a.grp_expert ? (a.pair_out_row ? a.pair_out_row[base + c] : base + c)
-                                  : c;
-    const int n0 = rbase * 16 + (lane >> 4) * 4;   // logical output column of v[.][0]
-    const int ncol = RB == 2 ? a.N / 2 : a.N;       // logical output width
-    const int nv = min(4, ncol - n0);               // valid columns of this lane
-    if (nv <= 0) continue;
-    const bool vec = (nv == 4) && ((a.ldy & 3) == 0);
-    if (a.bias) {
-      const uint16_t* bp = a.bias + (a.grp_expert ? (long long)a.grp_expert[group] * a.bias_group_stride : 0);
-#pragma unroll
-      for (int r = 0; r < RB; ++r)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (i < nv) v[r][i] += bf2f(bp[(r ? ncol : 0) + n0 + i]);
-    }
-    float o[4];
-    if (EPI == EPI_F32) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = v[0][i];
-    } else if (EPI == EPI_BF16) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = v[0][i];
-    } else if (EPI == EPI_RESID_BF16) {
-      // o = bf16(acc); out = bf16(res + o)   (projection then bf16 residual add)
-      const uint16_t* rp = a.residual + (long long)orow * a.ldy + n0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = (i < nv) ? bf2f(rp[i]) + rbf(v[0][i]) : 0.f;
-    } else if (EPI == EPI_SWIGLU_BF16) {
-      // gate rows in v[0], up rows in v[1]; Qwen rounding: g,u -> bf16,
-      // silu(g) -> bf16, product -> bf16.
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (a.round_qwen) {
-          const float g = rbf(v[0][i]), u = rbf(v[RB - 1][i]);
-          o[i] = rbf(g / (1.0f + expf(-g))) * u;
-        } else {
-          float g = fmaxf(fminf(v[0][i], a.gate_hi), a.gate_lo);
-          float u = fmaxf(fminf(v[RB - 1][i], a.up_hi), a.up_lo);
-          const float z = a.act ? a.alpha * g : g;
-          o[i] = (g / (1.0f + expf(-z))) * u;
-        }
-      }
-    } else if (EPI == EPI_SCALE_F32) {
-      const float sc = a.pair_scale ? a.pair_scale[orow] : 1.0f;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) o[i] = v[0][i] * sc;
-    }
-    if (EPI == EPI_F32 || EPI == EPI_SCALE_F32) {
-      float* y = reinterpret_cast<float*>(a.y) + kblk * a.part_stride + (long long)orow * a.ldy + n0;
-      if (vec) {
-        *reinterpret_cast<f32x4_t*>(y) = f32x4_t{o[0], o[1], o[2], o[3]};
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) if (i < nv) y[i] = o[i];
-      }
-    } else {
-      uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n0;
-      if (vec) {
-        *reinterpret_cast<uint2*>(y) = uint2{pack2bf(o[0], o[1]), pack2bf(o[2], o[3])};
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) if (i < nv) y[i] = (uint16_t)f2bf(o[i]);
-      }
-    }
-  }
+  gemm_finish<RB, TN, EPI>(a, acc, lane, wave, rbase, group, t0, base, xrow, kblk);
 }
 
 // ---------------------------------------------------------------------------
@@ -310,9 +213,10 @@ static hipError_t launch_t(const GemmArgs& a, int n_tiles, int groups, int ttile
 }
 
 int choose_kw(int K, int max_kw) {
-  // Largest per-wave K slice <= max_kw that divides K into <= 16 waves.
-  for (int kw : {512, 384, 256, 128, 64, 32}) {
-    if (kw <= max_kw && K % kw == 0 && K / kw <= 16) return kw;
+  // Largest per-wave K slice (a multiple of 32, <= max_kw) that divides K into
+  // <= 16 waves.
+  for (int kw = (max_kw < K ? max_kw : K) / 32 * 32; kw >= 32; kw -= 32) {
+    if (K % kw == 0 && K / kw <= 16) return kw;
   }
   return -1;
 }

@@ -38,7 +38,17 @@ struct GemmArgs {
   // y + kb * part_stride; the consumer adds the kgrid partials in order.
   int kgrid;                  // 0 or 1: no split
   long long part_stride;      // elements between partial outputs
+  // MX weights (mx.hip): `w` holds element codes in MX frag order and
+  // w_group_stride counts bytes; x holds MXFP8 activation codes (ldx bytes per
+  // row) with E8M0 scales x_scale (ldxs bytes per row, one per 32 along K).
+  const uint8_t* w_scale;     // packed weight scales (group 0)
+  long long w_scale_group_stride;  // bytes between experts' scales
+  const uint8_t* x_scale;
+  int ldxs;
 };
+
+// MX element formats (OCP MX v1.0): codes as in the C ABI (MKD_MX_*).
+enum MxFmt { MX_E4M3 = 1, MX_E2M1 = 2 };
 
 // Kernel-dispatch timing.  When `start` is set, the next GEMM or attention
 // launch records the two events as part of its own dispatch packet
@@ -66,6 +76,20 @@ int choose_kw(int K, int max_kw = 512);
 int choose_kw_split(int K, int kgrid);
 hipError_t gemm_launch(GemmArgs a, int epi, bool xf32, int tn, int groups_max,
                        int max_tokens_per_group, hipStream_t s);
+// mx.hip
+hipError_t mx_quantize_launch(const void* x, bool x_f32, int rows, int K, int ldx, int fmt,
+                              uint8_t* codes, uint8_t* scales, int K_pad, hipStream_t s);
+long long mx_packed_code_bytes(int G, int N, int K, int fmt);
+long long mx_packed_scale_bytes(int G, int N, int K);
+hipError_t mx_pack_launch(const uint8_t* codes, const uint8_t* scales, uint8_t* dst,
+                          uint8_t* dst_scales, int G, int N, int K, long long g_stride,
+                          long long row_stride, long long s_g_stride, long long s_row_stride,
+                          int fmt, int interleave_half, hipStream_t s);
+hipError_t gemm_mx_launch(GemmArgs a, int fmt, int epi, int groups_max, int max_tokens_per_group,
+                          hipStream_t s);
+int choose_kw_mx(int K_pad);
+int mx_kpad(int K);   // contraction padding of the packed MX layout
+
 hipError_t pack_frag_launch(const uint16_t* src, uint16_t* dst, int G, int N, int K,
                             long long g_stride, long long row_stride, long long col_stride,
                             int interleave_half, hipStream_t s);

@@ -1,0 +1,435 @@
+// MX (OCP Microscaling v1.0) expert path for gfx950: MXFP8 / MXFP4 weights,
+// MXFP8 activations, v_mfma_scale_f32_16x16x128_f8f6f4.
+//
+// Quantisation (mx_quantize_kernel): blocks of 32 consecutive elements along K
+// share one E8M0 scale X = 2^(floor(log2 amax) - emax_elem) (byte = exponent
+// + 127, clamped to [0, 254]; an all-zero block gets byte 0); each element is
+// v / X rounded to nearest-even in the element format and saturated to its
+// largest finite magnitude (E4M3 448, E2M1 6).  This is the OCP rule; the
+// reference's nisa.quantize_mx (selective_expert_mx_impl.py:143-149,
+// down_projection_mx_shard_H.py:74-79) is a Neuron instruction whose rounding
+// is not in its sources.
+//
+// MX frag layout.  One scaled MFMA takes a 16 x 128 A tile; lane l = 16*q + r
+// supplies row r and, for 8-bit elements, k in [16q, 16q+16) and
+// [64+16q, 64+16q+16) (two 16-byte halves), for 4-bit elements k in
+// [32q, 32q+32) (one 16-byte run, low nibble first); the scale byte a lane
+// supplies is the E8M0 of row r, k-block q (k in [32q, 32q+32)).  The B
+// operand (16 token columns x 128 k) uses the same per-lane layout.  Packed:
+//   codes [G][NB][KB][64 lanes][32 B (e4m3) | 16 B (e2m1)]   KB = K_pad/128
+//   scales[G][NB][ceil(KB/4)][64 lanes][4 B]  byte i = fragment 4*kb4 + i
+// Rows past N and k past K are zero codes with scale byte 0.  K_pad (mx_kpad)
+// is K rounded up to 128, or to 512 when that leaves no even split of the
+// fragments over <= 8 waves.
+//
+// The GEMM is the weight-streaming scheme of gemm.hip with 128-k fragments:
+// waves split K, partial tiles meet in LDS (fixed order), shared epilogues
+// (gemm_epi.h).  Activations arrive pre-quantised (MXFP8, row-major codes,
+// one scale byte per 32).
+#include "common.h"
+#include "gemm_epi.h"
+#include "mkd_internal.h"
+
+namespace mkd {
+
+typedef __attribute__((__vector_size__(8 * sizeof(int)))) int i32x8_t;
+
+template <int FMT>
+struct MxSpec;
+template <>
+struct MxSpec<MX_E4M3> {
+  static constexpr int MB = 3, EB = 4, BIAS = 7, EMIN = -6, EMAX = 8, BPL = 32, HW = 0;
+  static constexpr float VMAX = 448.0f;
+};
+template <>
+struct MxSpec<MX_E2M1> {
+  static constexpr int MB = 1, EB = 2, BIAS = 1, EMIN = 0, EMAX = 2, BPL = 16, HW = 4;
+  static constexpr float VMAX = 6.0f;
+};
+
+// floor(log2(a)) for finite a > 0, fp32 subnormals included.
+MKD_DEV int floor_log2_pos(float a) {
+  const uint32_t b = __float_as_uint(a);
+  const int e = (int)((b >> 23) & 0xffu);
+  if (e) return e - 127;
+  return (31 - __clz(b & 0x7fffffu)) - 149;
+}
+
+// Element code of v (already divided by the block scale): RNE, saturating.
+template <int FMT>
+MKD_DEV uint32_t mx_encode(float v) {
+  using S = MxSpec<FMT>;
+  const uint32_t sign = __float_as_uint(v) >> 31;
+  const float a = fabsf(v);
+  const int e = a > 0.f ? max(floor_log2_pos(a), S::EMIN) : S::EMIN;
+  float q = ldexpf(rintf(ldexpf(a, S::MB - e)), e - S::MB);  // exact scalings, RNE
+  q = fminf(q, S::VMAX);
+  uint32_t mag = 0;
+  if (q > 0.f) {
+    const int qe = floor_log2_pos(q);
+    if (qe >= S::EMIN)
+      mag = ((uint32_t)(qe + S::BIAS) << S::MB) |
+            ((__float_as_uint(q) >> (23 - S::MB)) & ((1u << S::MB) - 1u));
+    else
+      mag = (uint32_t)ldexpf(q, S::MB - S::EMIN);            // subnormal: q / 2^(EMIN-MB)
+  }
+  return (sign << (S::EB + S::MB)) | mag;
+}
+
+template <int FMT>
+MKD_DEV uint32_t mx_scale_byte(float amax) {
+  if (!(amax > 0.f)) return 0u;
+  const int e = floor_log2_pos(amax) - MxSpec<FMT>::EMAX + 127;
+  return (uint32_t)min(max(e, 0), 254);
+}
+
+// ---------------------------------------------------------------------------
+// Quantisation: one thread per 32-element block.  codes row stride: K_pad bytes
+// (e4m3) or K_pad/2 bytes (e2m1, two per byte, low nibble first); scales row
+// stride K_pad/32.  Blocks at k >= K are written as zeros.
+// ---------------------------------------------------------------------------
+template <int FMT, bool XF32>
+__global__ void mx_quantize_kernel(const void* __restrict__ x, int rows, int K, int ldx,
+                                   uint8_t* __restrict__ codes, uint8_t* __restrict__ scales,
+                                   int K_pad) {
+  const int nblk = K_pad / 32;
+  const long long idx = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  if (idx >= (long long)rows * nblk) return;
+  const int r = (int)(idx / nblk), b = (int)(idx % nblk);
+  float v[32];
+  if (b * 32 < K) {
+    if (XF32) {
+      const float* p = static_cast<const float*>(x) + (long long)r * ldx + b * 32;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const f32x4_t t = *reinterpret_cast<const f32x4_t*>(p + 4 * j);
+        v[4 * j] = t[0]; v[4 * j + 1] = t[1]; v[4 * j + 2] = t[2]; v[4 * j + 3] = t[3];
+      }
+    } else {
+      const uint16_t* p = static_cast<const uint16_t*>(x) + (long long)r * ldx + b * 32;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const u32x4_t t = ld16(p + 8 * j);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          v[8 * j + 2 * h] = bf_lo(t[h]);
+          v[8 * j + 2 * h + 1] = bf_hi(t[h]);
+        }
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 32; ++j) v[j] = 0.f;
+  }
+  float amax = 0.f;
+#pragma unroll
+  for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  const uint32_t sb = mx_scale_byte<FMT>(amax);
+  const int sh = 127 - (int)sb;
+  if (FMT == MX_E4M3) {
+    u32x4_t o[2];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint32_t d = 0;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) d |= mx_encode<FMT>(ldexpf(v[4 * j + h], sh)) << (8 * h);
+      o[j >> 2][j & 3] = d;
+    }
+    uint8_t* c = codes + (long long)r * K_pad + b * 32;
+    st16(c, o[0]);
+    st16(c + 16, o[1]);
+  } else {
+    u32x4_t o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t d = 0;
+#pragma unroll
+      for (int h = 0; h < 8; ++h) d |= mx_encode<FMT>(ldexpf(v[8 * j + h], sh)) << (4 * h);
+      o[j] = d;
+    }
+    st16(codes + (long long)r * (K_pad / 2) + b * 16, o);
+  }
+  scales[(long long)r * nblk + b] = (uint8_t)sb;
+}
+
+// ---------------------------------------------------------------------------
+// Packing into MX frag layout.  Source codes [G][N][K] (e4m3, one byte each) or
+// [G][N][K/2] (e2m1 pairs), k contiguous, strides in bytes; source scales
+// [G][N][K/32].  interleave_half as in pack_frag_kernel (gate/up row blocks).
+// ---------------------------------------------------------------------------
+template <int FMT>
+__global__ void mx_pack_kernel(const uint8_t* __restrict__ codes, const uint8_t* __restrict__ scales,
+                               uint8_t* __restrict__ dst, uint8_t* __restrict__ dst_s, int G, int N,
+                               int K, int KB, long long gs, long long rs, long long sgs,
+                               long long srs, int interleave_half) {
+  constexpr int BPL = MxSpec<FMT>::BPL;
+  const int KB4 = (KB + 3) / 4, NB = (N + 15) / 16;
+  const long long total = (long long)G * NB * KB * 64;
+  for (long long idx = blockIdx.x * (long long)blockDim.x + threadIdx.x; idx < total;
+       idx += (long long)gridDim.x * blockDim.x) {
+    const int lane = (int)(idx & 63);
+    long long t = idx >> 6;
+    const int kb = (int)(t % KB); t /= KB;
+    const int nb = (int)(t % NB);
+    const int g = (int)(t / NB);
+    int row_block = nb;
+    if (interleave_half > 0) {
+      const int pair = nb >> 1;
+      row_block = (nb & 1) ? (interleave_half / 16 + pair) : pair;
+    }
+    const int n = row_block * 16 + (lane & 15), q = lane >> 4;
+    uint8_t out[BPL];
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) out[j] = 0;
+    if (n < N) {
+      const uint8_t* src = codes + g * gs + n * rs;
+      if (FMT == MX_E4M3) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const int k0 = kb * 128 + h * 64 + 16 * q;   // 16-aligned, K % 32 == 0
+          if (k0 < K)
+#pragma unroll
+            for (int j = 0; j < 16; ++j) out[16 * h + j] = src[k0 + j];
+        }
+      } else {
+        const int k0 = kb * 128 + 32 * q;
+        if (k0 < K)
+#pragma unroll
+          for (int j = 0; j < 16; ++j) out[j] = src[k0 / 2 + j];
+      }
+    }
+    uint8_t* d = dst + ((((long long)g * NB + nb) * KB + kb) * 64 + lane) * BPL;
+#pragma unroll
+    for (int j = 0; j < BPL; ++j) d[j] = out[j];
+    if ((kb & 3) == 0) {
+      uint32_t sv = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int blk = (kb + i) * 4 + q;                // 32-wide block index along K
+        if (n < N && kb + i < KB && blk * 32 < K)
+          sv |= (uint32_t)scales[g * sgs + n * srs + blk] << (8 * i);
+      }
+      *reinterpret_cast<uint32_t*>(dst_s + ((((long long)g * NB + nb) * KB4 + (kb >> 2)) * 64 + lane) * 4) = sv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// The MX GEMM (16 token columns per block, TN = 1).
+// ---------------------------------------------------------------------------
+// A fragment registers: 8 dwords for 8-bit elements, 4 for 4-bit ones (the
+// MFMA reads only the low 4 dwords of a 4-bit operand).
+template <int FMT>
+struct WFrag {
+  u32x4_t lo, hi;
+  MKD_DEV void load(const uint8_t* p) {
+    lo = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+    hi = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p + 16));
+  }
+  MKD_DEV i32x8_t op() const {
+    return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                   (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+  }
+};
+template <>
+struct WFrag<MX_E2M1> {
+  u32x4_t lo;
+  MKD_DEV void load(const uint8_t* p) {
+    lo = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  }
+  MKD_DEV i32x8_t op() const {
+    return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3], 0, 0, 0, 0};
+  }
+};
+
+// B fragment: token row codes (e4m3) for fragment kb, this lane's two halves.
+MKD_DEV i32x8_t load_xfrag(const uint8_t* xr, int kb, int q) {
+  const u32x4_t lo = ld16(xr + kb * 128 + 16 * q);
+  const u32x4_t hi = ld16(xr + kb * 128 + 64 + 16 * q);
+  return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
+                 (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+}
+
+template <int RB, int FMT, int B>
+MKD_DEV void mx_batch(const uint8_t* const (&wrow)[RB], const uint8_t* const (&srow)[RB],
+                      const uint8_t* xr, const uint8_t* xs, int kb0, int f, int q,
+                      f32x4_t (&acc)[RB][1]) {
+  constexpr int BPL = MxSpec<FMT>::BPL;
+  WFrag<FMT> wf[RB][B];
+  uint32_t ws[RB][B];
+#pragma unroll
+  for (int u = 0; u < B; ++u)
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int kb = kb0 + f + u;
+      wf[r][u].load(wrow[r] + (long long)(f + u) * 64 * BPL);
+      ws[r][u] = *reinterpret_cast<const uint32_t*>(srow[r] + (kb >> 2) * 256) >> (8 * (kb & 3));
+    }
+#pragma unroll
+  for (int u = 0; u < B; ++u) {
+    const int kb = kb0 + f + u;
+    i32x8_t xf = {0, 0, 0, 0, 0, 0, 0, 0};
+    uint32_t xsc = 0;
+    if (xr) {
+      xf = load_xfrag(xr, kb, q);
+      xsc = *reinterpret_cast<const uint32_t*>(xs + kb * 4) >> (8 * q);
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+      acc[r][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
+          wf[r][u].op(), xf, acc[r][0], MxSpec<FMT>::HW, MxSpec<MX_E4M3>::HW, 0, (int)(ws[r][u] & 0xffu), 0,
+          (int)(xsc & 0xffu));
+  }
+}
+
+template <int RB, int FMT, int EPI>
+__global__ void __launch_bounds__(512) gemm_mx_kernel(GemmArgs a) {
+  constexpr int BPL = MxSpec<FMT>::BPL;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int rbase = blockIdx.x;
+  const int group = blockIdx.y;
+  const int kg = a.kgrid > 1 ? a.kgrid : 1;
+  const int ttile = blockIdx.z / kg;
+  const int kblk = blockIdx.z % kg;
+
+  int count, base;
+  const uint8_t* w = reinterpret_cast<const uint8_t*>(a.w);
+  const uint8_t* wsc = a.w_scale;
+  if (a.grp_expert) {
+    if (group >= *a.n_groups) return;
+    count = a.grp_count[group];
+    base = a.grp_offset[group];
+    w += (long long)a.grp_expert[group] * a.w_group_stride;
+    wsc += (long long)a.grp_expert[group] * a.w_scale_group_stride;
+  } else {
+    count = a.T;
+    base = 0;
+  }
+  const int t0 = ttile * 16;
+  if (t0 >= count) return;
+  int xrow[1];
+  {
+    const int c = t0 + (lane & 15);
+    xrow[0] = c < count ? (a.pair_row ? a.pair_row[base + c] : base + c) : -1;
+  }
+  const uint8_t* xr = xrow[0] >= 0 ? reinterpret_cast<const uint8_t*>(a.x) + (long long)xrow[0] * a.ldx : nullptr;
+  const uint8_t* xs = xrow[0] >= 0 ? a.x_scale + (long long)xrow[0] * a.ldxs : nullptr;
+
+  const int KB = a.K / 128, KB4 = (KB + 3) / 4;
+  const int NF = a.KW / 128;
+  const int kb0 = (kblk * (int)(blockDim.x >> 6) + wave) * NF;
+  const int q = lane >> 4;
+
+  f32x4_t acc[RB][1];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) acc[r][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint8_t* wrow[RB];
+  const uint8_t* srow[RB];
+#pragma unroll
+  for (int r = 0; r < RB; ++r) {
+    const long long rb = rbase * RB + r;
+    wrow[r] = w + ((rb * KB + kb0) * 64 + lane) * BPL;
+    srow[r] = wsc + (rb * KB4 * 64 + lane) * 4;
+  }
+  // batches of U fragments per row block (<= 16 KiB of weight loads in flight
+  // per wave), remainder in batches of 4/2/1
+  constexpr int U = (FMT == MX_E4M3 ? 8 : 16) / RB;
+  int f = 0;
+  for (; f + U <= NF; f += U) mx_batch<RB, FMT, U>(wrow, srow, xr, xs, kb0, f, q, acc);
+  if constexpr (U > 4)
+    if (f + 4 <= NF) { mx_batch<RB, FMT, 4>(wrow, srow, xr, xs, kb0, f, q, acc); f += 4; }
+  if constexpr (U > 2)
+    if (f + 2 <= NF) { mx_batch<RB, FMT, 2>(wrow, srow, xr, xs, kb0, f, q, acc); f += 2; }
+  if constexpr (U > 1)
+    if (f < NF) mx_batch<RB, FMT, 1>(wrow, srow, xr, xs, kb0, f, q, acc);
+
+  gemm_finish<RB, 1, EPI>(a, acc, lane, wave, rbase, group, t0, base, xrow, kblk);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+hipError_t mx_quantize_launch(const void* x, bool x_f32, int rows, int K, int ldx, int fmt,
+                              uint8_t* codes, uint8_t* scales, int K_pad, hipStream_t s) {
+  if (rows <= 0 || K <= 0 || K % 32 || K_pad < K || K_pad % 128) return hipErrorInvalidValue;
+  const long long n = (long long)rows * (K_pad / 32);
+  const int threads = 256;
+  const unsigned blocks = (unsigned)((n + threads - 1) / threads);
+#define MKD_Q(F, X) hipLaunchKernelGGL((mx_quantize_kernel<F, X>), dim3(blocks), dim3(threads), 0, s, x, rows, K, ldx, codes, scales, K_pad)
+  if (fmt == MX_E4M3) { if (x_f32) MKD_Q(MX_E4M3, true); else MKD_Q(MX_E4M3, false); }
+  else if (fmt == MX_E2M1) { if (x_f32) MKD_Q(MX_E2M1, true); else MKD_Q(MX_E2M1, false); }
+  else return hipErrorInvalidValue;
+#undef MKD_Q
+  return hipGetLastError();
+}
+
+long long mx_packed_code_bytes(int G, int N, int K, int fmt) {
+  const long long KB = mx_kpad(K) / 128, NB = (N + 15) / 16;
+  return (long long)G * NB * KB * 64 * (fmt == MX_E4M3 ? 32 : 16);
+}
+
+long long mx_packed_scale_bytes(int G, int N, int K) {
+  const long long KB = mx_kpad(K) / 128, NB = (N + 15) / 16;
+  return (long long)G * NB * ((KB + 3) / 4) * 64 * 4;
+}
+
+hipError_t mx_pack_launch(const uint8_t* codes, const uint8_t* scales, uint8_t* dst,
+                          uint8_t* dst_scales, int G, int N, int K, long long g_stride,
+                          long long row_stride, long long s_g_stride, long long s_row_stride,
+                          int fmt, int interleave_half, hipStream_t s) {
+  if (G <= 0 || N <= 0 || K <= 0 || K % 32) return hipErrorInvalidValue;
+  // every scale dword is written by the first fragment of its 4-fragment group
+  const int KB = mx_kpad(K) / 128;
+  const long long total = (long long)G * ((N + 15) / 16) * KB * 64;
+  const int threads = 256;
+  long long blocks = (total + threads - 1) / threads;
+  if (blocks > 65535LL * 16) blocks = 65535LL * 16;
+#define MKD_P(F) hipLaunchKernelGGL(mx_pack_kernel<F>, dim3((unsigned)blocks), dim3(threads), 0, s, codes, scales, dst, dst_scales, G, N, K, KB, g_stride, row_stride, s_g_stride, s_row_stride, interleave_half)
+  if (fmt == MX_E4M3) MKD_P(MX_E4M3);
+  else if (fmt == MX_E2M1) MKD_P(MX_E2M1);
+  else return hipErrorInvalidValue;
+#undef MKD_P
+  return hipGetLastError();
+}
+
+int choose_kw_mx(int K_pad) {
+  // per-wave K slice (multiple of 128) splitting K_pad over <= 8 waves
+  for (int kw : {512, 384, 256, 128, 1024, 768, 1536, 2048})
+    if (K_pad % kw == 0 && K_pad / kw <= 8) return kw;
+  return -1;
+}
+
+int mx_kpad(int K) {
+  const int p = (K + 127) / 128 * 128;
+  return choose_kw_mx(p) > 0 ? p : (K + 511) / 512 * 512;
+}
+
+template <int RB, int FMT, int EPI>
+static hipError_t launch_mx(const GemmArgs& a, int n_tiles, int groups, int ttiles, hipStream_t s) {
+  const int nsplit = a.K / a.KW;
+  if (a.KW <= 0 || a.KW % 128 || nsplit < 1 || nsplit > 8 || nsplit * a.KW != a.K)
+    return hipErrorInvalidValue;
+  dim3 grid(n_tiles, groups, ttiles);
+  dim3 block(64 * nsplit);
+  const size_t lds = nsplit > 1 ? (size_t)nsplit * RB * 4 * 64 * sizeof(float) : 0;
+  return timed_launch(gemm_mx_kernel<RB, FMT, EPI>, grid, block, lds, s, a);
+}
+
+hipError_t gemm_mx_launch(GemmArgs a, int fmt, int epi, int groups_max, int max_tokens_per_group,
+                          hipStream_t s) {
+  if (a.kgrid > 1) return hipErrorInvalidValue;
+  const int RB = (epi == EPI_SWIGLU_BF16) ? 2 : 1;
+  const int n_tiles = (a.N + 16 * RB - 1) / (16 * RB);
+  const int ttiles = (max_tokens_per_group + 15) / 16;
+  const int groups = a.grp_expert ? groups_max : 1;
+#define MKD_M(RB_, F_, E_) \
+  if (RB == RB_ && fmt == F_ && epi == E_) return launch_mx<RB_, F_, E_>(a, n_tiles, groups, ttiles, s);
+  MKD_M(2, MX_E4M3, EPI_SWIGLU_BF16) MKD_M(2, MX_E2M1, EPI_SWIGLU_BF16)
+  MKD_M(1, MX_E4M3, EPI_SCALE_F32) MKD_M(1, MX_E2M1, EPI_SCALE_F32)
+  MKD_M(1, MX_E4M3, EPI_F32) MKD_M(1, MX_E2M1, EPI_F32)
+#undef MKD_M
+  return hipErrorInvalidValue;
+}
+
+}  // namespace mkd

@@ -23,5 +23,10 @@ Parity pinning (what checks each function; see tests/test_oracle_*.py):
   rope                 HF apply_rotary_pos_emb, position 0 identity
   qwen layer / step    HF Qwen3MoeDecoderLayer (fp32) via golden fixtures
   mx                   OCP MX v1.0 spec: exact KATs (powers of two, every
-                       representable E4M3 / E2M1 value round-trips)
+                       representable E4M3 / E2M1 value round-trips), every
+                       E4M3 code and RNE+saturation against torch's
+                       float8_e4m3fn, E2M1 rounding by brute force
+  moe_tkg_mx           = moe_tkg on the dequantised weights up to the
+                       activation quantisation (bounded), exact when the
+                       activations are MX-representable
 """

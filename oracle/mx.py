@@ -72,7 +72,10 @@ def decode_elements(code: np.ndarray, fmt: str) -> np.ndarray:
     val = np.where(normal,
                    np.ldexp(1.0 + mf / (1 << mb), (ef - bias)),
                    np.ldexp(mf.astype(np.float64), (1 - bias - mb)))
-    return np.where(sign == 1, -val, val)
+    val = np.where(sign == 1, -val, val)
+    if fmt == "e4m3":                                   # E4M3 "fn": s 1111 111 is NaN, no inf
+        val = np.where((ef == 15) & (mf == 7), np.nan, val)
+    return val
 
 
 def quantize_mx(x: np.ndarray, fmt: str = "e4m3"):

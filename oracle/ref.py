@@ -196,6 +196,64 @@ def moe_tkg(hidden: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor,
     return out
 
 
+def mx_qdq(x: torch.Tensor, fmt: str = "e4m3") -> torch.Tensor:
+    """Quantise the rows of x to MX (blocks of 32 along the last dim) and back to fp32."""
+    from . import mx
+    c, s = mx.quantize_mx(x.float().numpy(), fmt)
+    return torch.from_numpy(mx.dequantize_mx(c, s, fmt))
+
+
+def moe_tkg_mx(hidden: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor,
+               affinities: torch.Tensor, index: torch.Tensor,
+               gate_up_bias: Optional[torch.Tensor] = None,
+               down_bias: Optional[torch.Tensor] = None,
+               scaling_mode: str = "post", act: str = "silu",
+               gate_clamp_upper: Optional[float] = None, gate_clamp_lower: Optional[float] = None,
+               up_clamp_upper: Optional[float] = None,
+               up_clamp_lower: Optional[float] = None) -> torch.Tensor:
+    """MX selective-expert MoE (selective_expert_mx_impl.py:60-531); returns fp32 [T, H].
+
+    gate_up [E, 2I, H] and down [E, H, I] are the DEQUANTISED MX weights (fp32,
+    gate rows then up rows).  Activations go through MXFP8 (E4M3) before each
+    projection: the hidden rows (selective_expert_mx_impl.py:143-149) and the
+    bf16 intermediate act(g)*u (down_projection_mx_shard_H.py:74-79).  Products
+    and sums in fp32; down bias added before the affinity scale, which equals
+    the reference's aff[T,E] @ b[E,H] term (selective_expert_mx_impl.py:457-497);
+    fp32 accumulation over k (the reference accumulates in the io dtype,
+    :421-440 -- a difference well inside the MX tolerance).
+    """
+    T, H = hidden.shape
+    K = index.shape[1]
+    I = gate_up.shape[1] // 2
+    x = mx_qdq(_bf(hidden.float(), True))
+    out = torch.zeros(T, H)
+    for t in range(T):
+        for j in range(K):
+            e = int(index[t, j])
+            g = gate_up[e, :I].float() @ x[t]
+            u = gate_up[e, I:].float() @ x[t]
+            if gate_up_bias is not None:
+                g = g + gate_up_bias[e, 0].float()
+                u = u + gate_up_bias[e, 1].float()
+            if gate_clamp_upper is not None:
+                g = torch.clamp(g, max=gate_clamp_upper)
+            if gate_clamp_lower is not None:
+                g = torch.clamp(g, min=gate_clamp_lower)
+            g = act_fn_apply(g, act)
+            if up_clamp_upper is not None:
+                u = torch.clamp(u, max=up_clamp_upper)
+            if up_clamp_lower is not None:
+                u = torch.clamp(u, min=up_clamp_lower)
+            h = mx_qdq(_bf(g * u, True)[None])[0]
+            y = down[e].float() @ h
+            if down_bias is not None:
+                y = y + down_bias[e].float()
+            if scaling_mode == "post":
+                y = y * affinities[t, e].float()
+            out[t] += y
+    return out
+
+
 def qwen_experts(x_bf: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor,
                  idx: torch.Tensor, weights: torch.Tensor, emulate_bf16: bool = True) -> torch.Tensor:
     """Qwen fused experts (moe_fused_nki.py:282-762), HF layouts.
