@@ -49,7 +49,7 @@ def build_model(Q, cfg, B, dev, seed):
     layers = []
     for l in range(cfg.num_hidden_layers):
         hf = Q.random_layer_hf(cfg, l, seed, dev)
-        layers.append(Q.pack_layer(hf))
+        layers.append(Q.pack_layer(hf, cfg.expert_format))
         del hf
     g = torch.Generator(device=dev)
     g.manual_seed(seed + 1)
@@ -70,14 +70,22 @@ def prefill_kv(model, cfg, ctx, seed, dev):
             t[:, :, :ctx].copy_(torch.randn(t[:, :, :ctx].shape, generator=g, device=dev))
 
 
-def cpu_baseline(cfg, ctx, seconds_budget=20.0):
-    """Time the CPU oracle's decode step on host cores (bounded sample)."""
+def cpu_baseline(cfg, lens, seconds_budget=20.0):
+    """Time the CPU oracle's decode step on host cores (bounded sample).
+
+    The batch and per-sequence KV lengths are the GPU workload's.  Weights of 2
+    distinct layers are reused for all layer slots.  When a full 48-layer step
+    does not fit the budget, a pass over fewer layers is timed and scaled to 48
+    layers (said in `sample`).  Expert math is the bf16-weight oracle in every
+    mode (an MX run's CPU leg does not dequantise).
+    """
     import torch
     from oracle import ref
     from importlib import import_module
     Q = import_module("nki_moe_megakernel_amd.qwen_with_megakernel")
     torch.set_num_threads(os.cpu_count() or 1)
     cores = torch.get_num_threads()
+    B = int(lens.numel())
     n_distinct = 2
     hfs = [Q.random_layer_hf(cfg, l, 77, "cpu") for l in range(n_distinct)]
     lws = [ref.QwenLayer(wq=h["q_proj"], wk=h["k_proj"], wv=h["v_proj"], wo=h["o_proj"],
@@ -85,33 +93,54 @@ def cpu_baseline(cfg, ctx, seconds_budget=20.0):
                          ln_post=h["post_attention_layernorm"], router=h["gate"],
                          gate_up=h["gate_up_proj"], down=h["down_proj"]) for h in hfs]
     g = torch.Generator().manual_seed(5)
-    S = ctx + 64
-    kcs = [torch.randn(1, cfg.num_key_value_heads, S, cfg.head_dim, generator=g).to(torch.bfloat16)
+    S = int(lens.max()) + 64
+    kcs = [torch.randn(B, cfg.num_key_value_heads, S, cfg.head_dim, generator=g).to(torch.bfloat16)
            for _ in range(n_distinct)]
-    vcs = [torch.randn(1, cfg.num_key_value_heads, S, cfg.head_dim, generator=g).to(torch.bfloat16)
+    vcs = [torch.randn(B, cfg.num_key_value_heads, S, cfg.head_dim, generator=g).to(torch.bfloat16)
            for _ in range(n_distinct)]
     lm = (0.02 * torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g)).to(torch.bfloat16)
     lnf = torch.ones(cfg.hidden_size, dtype=torch.bfloat16)
     shape = ref.QwenShape()
-    x0 = torch.randn(1, cfg.hidden_size, generator=g).to(torch.bfloat16).float()
-    steps, t_total = 0, 0.0
-    pos = ctx
-    while t_total < seconds_budget and steps < 8:
-        t0 = time.perf_counter()
-        x = x0
-        p = torch.tensor([pos], dtype=torch.int32)
+    x0 = torch.randn(B, cfg.hidden_size, generator=g).to(torch.bfloat16).float()
+    pos = lens.clone()
+    L = cfg.num_hidden_layers
+
+    def layers(x, n, p):
         cos, sin = ref.rope_cos_sin(p, cfg.head_dim, cfg.rope_theta)
-        for l in range(cfg.num_hidden_layers):
+        for l in range(n):
             j = l % n_distinct
             x, _ = ref.qwen_decoder_layer(x, lws[j], kcs[j], vcs[j], cos, sin, p, shape)
+        return x
+
+    t0 = time.perf_counter()
+    layers(x0, 1, pos)
+    t1 = time.perf_counter() - t0
+    if t1 * L <= seconds_budget:
+        steps, t_total = 0, 0.0
+        while t_total < seconds_budget and steps < 8:
+            t0 = time.perf_counter()
+            x = layers(x0, L, pos)
+            ref.final_norm_lm_head(x, lnf, lm, cfg.rms_norm_eps)
+            t_total += time.perf_counter() - t0
+            steps += 1
+            pos = pos + 1
+        step_s = t_total / steps
+        sample = (f"{steps} full {L}-layer bs={B} decode steps of the fp32 torch oracle")
+    else:
+        n = max(2, min(L, int(seconds_budget / t1)))
+        t0 = time.perf_counter()
+        x = layers(x0, n, pos)
+        t_layers = time.perf_counter() - t0
+        t0 = time.perf_counter()
         ref.final_norm_lm_head(x, lnf, lm, cfg.rms_norm_eps)
-        t_total += time.perf_counter() - t0
-        steps += 1
-        pos += 1
-    return {"value": steps / t_total, "unit": "tok/s", "cores": cores, "kind": "port",
-            "sample": f"{steps} full 48-layer bs=1 decode steps of the fp32 torch oracle at "
-                      f"ctx {ctx} ({n_distinct} distinct layers' weights, each reused for "
-                      f"{cfg.num_hidden_layers // n_distinct} layer slots) + lm_head, "
+        t_lm = time.perf_counter() - t0
+        t_total = t_layers + t_lm
+        step_s = t_layers * L / n + t_lm
+        sample = (f"one pass of {n} of {L} layers at bs={B} of the fp32 torch oracle, scaled by "
+                  f"{L}/{n}, + lm_head")
+    return {"value": B / step_s, "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{sample}, KV lengths mean {float(lens.float().mean()):.0f} "
+                      f"({n_distinct} distinct layers' weights reused for all layer slots), "
                       f"{t_total:.1f} s on {cores} host threads"}
 
 
@@ -128,6 +157,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=20.0)
     ap.add_argument("--calib-copy", action="store_true",
                     help="after the JSON line, run a copy kernel of known size (counter calibration)")
+    ap.add_argument("--ragged", action="store_true",
+                    help="per-sequence KV lengths drawn uniformly from [512, 8192] (configs[2])")
+    ap.add_argument("--experts", choices=["bf16", "mxfp8", "mxfp4"], default="bf16",
+                    help="expert weight format (mxfp8 at --batch 32 is configs[3])")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -142,11 +175,17 @@ def main():
 
     dev = torch.device("cuda:0")
     B, ctx = args.batch, args.ctx
-    S_max = ((ctx + args.warmup + args.steps + 8 + 127) // 128) * 128
-    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=args.layers, max_batch=B, max_seq=S_max)
+    if args.ragged:
+        gl = torch.Generator().manual_seed(4321)
+        lens = torch.randint(512, 8193, (B,), generator=gl, dtype=torch.int32)
+    else:
+        lens = torch.full((B,), ctx, dtype=torch.int32)
+    S_max = ((int(lens.max()) + args.warmup + args.steps + 8 + 127) // 128) * 128
+    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=args.layers, max_batch=B, max_seq=S_max,
+                             expert_format=args.experts)
     t0 = time.time()
     model = build_model(Q, cfg, B, dev, seed=1234)
-    prefill_kv(model, cfg, ctx, 1234, dev)
+    prefill_kv(model, cfg, int(lens.max()), 1234, dev)
     torch.cuda.synchronize()
     log(f"model built in {time.time() - t0:.1f}s "
         f"({torch.cuda.memory_allocated() / 2**30:.1f} GiB allocated)")
@@ -154,7 +193,7 @@ def main():
     g = torch.Generator(device=dev)
     g.manual_seed(99)
     ids = torch.randint(0, cfg.vocab_size, (B,), generator=g, device=dev, dtype=torch.int32)
-    pos = torch.full((B,), ctx, dtype=torch.int32, device=dev)
+    pos = lens.to(dev)
     hidden = torch.empty(B, cfg.hidden_size, dtype=torch.bfloat16, device=dev)
     logits = torch.empty(B, cfg.vocab_size, dtype=torch.float32, device=dev)
     nxt = torch.empty(B, dtype=torch.int32, device=dev)
@@ -214,21 +253,27 @@ def main():
     durs = [a.elapsed_time(b) for a, b in zip(ev_s, ev_e)]
     avg_ms = sum(durs) / len(durs)
     H, I, E, K = cfg.hidden_size, cfg.moe_intermediate_size, cfg.num_experts, cfg.num_experts_per_tok
+    # expected number of distinct experts a layer touches (near-uniform routing)
     distinct = E * (1 - (1 - K / E) ** B) if B > 1 else K
-    alg_bytes = distinct * 2 * I * H * 2
+    # bytes per expert weight element: bf16 2; MX codes + one scale byte per 32
+    wbytes = {"bf16": 2.0, "mxfp8": 1.0 + 1 / 32, "mxfp4": 0.5 + 1 / 32}[args.experts]
+    alg_bytes = distinct * 2 * I * H * wbytes
     achieved = alg_bytes / (avg_ms / 1e3) / 1e9
+    gu_flops = 2.0 * B * K * 2 * I * H                 # one gate/up launch
+    gu_tflops = gu_flops / (avg_ms / 1e3) / 1e12
+    mfma_peak = MFMA_BF16_PEAK_TFLOPS if args.experts == "bf16" else 2 * MFMA_BF16_PEAK_TFLOPS
     # whole-step algorithmic bytes (weights + KV read + lm_head) for reference
     attn_b = 2 * H * (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim + \
         2 * cfg.num_attention_heads * cfg.head_dim * H
-    kv_b = 2 * cfg.num_key_value_heads * cfg.head_dim * 2 * (ctx + args.steps / 2) * B
-    layer_b = attn_b + 2 * E * H + distinct * 3 * H * I * 2 + kv_b
+    kv_b = 2 * cfg.num_key_value_heads * cfg.head_dim * 2 * float((lens.float() + args.steps / 2).sum())
+    layer_b = attn_b + 2 * E * H + distinct * 3 * H * I * wbytes + kv_b
     step_b = cfg.num_hidden_layers * layer_b + 2 * H * cfg.vocab_size
     step_gbs = step_b / (ms_step / 1e3) / 1e9
 
     cpu = None
     if not args.no_cpu:
         try:
-            cpu = cpu_baseline(cfg, ctx, args.cpu_seconds)
+            cpu = cpu_baseline(cfg, lens, args.cpu_seconds)
         except Exception as e:  # report, never fail the GPU number on it
             log(f"cpu baseline failed: {e!r}")
     log(f"step {ms_step:.3f} ms ({tok_s:.1f} tok/s), wall {wall:.2f}s; whole-step algorithmic "
@@ -239,24 +284,45 @@ def main():
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic (seeded random bf16 weights N(0,0.02), KV N(0,1), uniform token ids)",
-        "config": {"workload": f"Qwen3-30B-A3B-shaped {cfg.num_hidden_layers}-layer greedy decode, "
-                               f"bs={B}, KV context {ctx} (BASELINE configs[1])",
-                   "batch": B, "kv_context": ctx, "layers": cfg.num_hidden_layers,
+        "data": "synthetic (seeded random bf16 weights N(0,0.02)" +
+                (f", experts quantised to {args.experts}" if args.experts != "bf16" else "") +
+                ", KV N(0,1), uniform token ids)",
+        "config": {"workload": workload_name(cfg, B, ctx, lens, args),
+                   "batch": B, "kv_context": ctx if not args.ragged else "U[512,8192]",
+                   "kv_lengths_mean": round(float(lens.float().mean()), 1),
+                   "layers": cfg.num_hidden_layers, "experts": args.experts,
                    "graph": graph is not None,
                    "step_algorithmic_GB": round(step_b / 1e9, 4),
                    "step_GBps": round(step_gbs, 1),
-                   "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4)},
-        "roofline": {"bound": "hbm", "kernel": "moe gate_up grouped GEMM (gemm_frag_kernel<2,1,0,3>)",
+                   "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
+                   "gate_up_TFLOPs": round(gu_tflops, 2),
+                   "gate_up_mfma_frac": round(gu_tflops / mfma_peak, 5)},
+        "roofline": {"bound": "hbm",
+                     "kernel": "moe gate_up grouped GEMM (" + ("gemm_frag_kernel<2,1,0,3>" if args.experts == "bf16"
+                                                               else "gemm_mx_kernel<2,fmt,3>") + ")",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers),
+                     "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers)
+                     if (args.experts == "bf16" and not args.ragged) else None,
                      "avg_us": round(avg_ms * 1e3, 2), "bytes_per_launch": int(alg_bytes)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
     if args.calib_copy:
         calib_copy(dev)
+
+
+def workload_name(cfg, B, ctx, lens, args):
+    kv = "KV lengths U[512,8192] (ragged)" if args.ragged else f"KV context {ctx}"
+    tag = ""
+    if args.experts == "bf16" and not args.ragged and B == 1 and ctx == 2048 and cfg.num_hidden_layers == 48:
+        tag = " (BASELINE configs[1])"
+    elif args.experts == "bf16" and args.ragged and B in (16, 64):
+        tag = " (BASELINE configs[2])"
+    elif args.experts == "mxfp8" and B == 32:
+        tag = " (BASELINE configs[3] expert format)"
+    return (f"Qwen3-30B-A3B-shaped {cfg.num_hidden_layers}-layer greedy decode, bs={B}, {kv}, "
+            f"{args.experts} experts{tag}")
 
 
 def measured_traffic(B, ctx, layers):

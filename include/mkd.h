@@ -246,6 +246,11 @@ typedef struct {
   void* const* k_cache;        /* [B, nkv, S_max, d] bf16                */
   void* const* v_cache;
   const float* inv_freq;       /* [d/2] fp32 device, RoPE inverse freqs  */
+  int expert_format;           /* 0 bf16 experts, MKD_MX_E4M3 / MKD_MX_E2M1: MX
+                                  experts (mkd_pack_mx_weights), activations
+                                  quantised to MXFP8 before each projection */
+  const void* const* gate_up_scales;  /* MX: packed scales per layer     */
+  const void* const* down_scales;
 } mkd_qwen3_model;
 size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B);
 /* hidden [B, H] bf16 in/out; position_ids [B] int32 (device); cos/sin [B, d]

@@ -78,6 +78,7 @@ class Qwen3Model(C.Structure):
         ("k_norm", C.POINTER(vp)), ("ln_in", C.POINTER(vp)), ("ln_post", C.POINTER(vp)),
         ("router", C.POINTER(vp)), ("gate_up", C.POINTER(vp)), ("down", C.POINTER(vp)),
         ("k_cache", C.POINTER(vp)), ("v_cache", C.POINTER(vp)), ("inv_freq", vp),
+        ("expert_format", i32), ("gate_up_scales", C.POINTER(vp)), ("down_scales", C.POINTER(vp)),
     ]
 
 

@@ -714,8 +714,17 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
   MKD_REQUIRE(cos || m->inv_freq, MKD_ERR_NULL, "decode_layers: need cos/sin or inv_freq");
   MKD_REQUIRE(m->E <= 512 && m->K >= 1 && m->K <= 8, MKD_ERR_INVALID, "decode_layers: bad E/K");
   MKD_REQUIRE(m->H % 8 == 0 && m->H <= 8192, MKD_ERR_INVALID, "decode_layers: bad H");
-  if (int rc = check_gemm_dims(2 * m->I, m->H, 2)) return rc;
-  if (int rc = check_gemm_dims(m->H, m->I, 1)) return rc;
+  MKD_REQUIRE(m->expert_format == 0 || m->expert_format == MKD_MX_E4M3 ||
+                  m->expert_format == MKD_MX_E2M1, MKD_ERR_INVALID,
+              "decode_layers: unknown expert_format %d", m->expert_format);
+  if (m->expert_format) {
+    MKD_REQUIRE(m->gate_up_scales && m->down_scales, MKD_ERR_NULL, "decode_layers: MX experts need scales");
+    if (int rc = check_mx_dims(2 * m->I, m->H, 2)) return rc;
+    if (int rc = check_mx_dims(m->H, m->I, 1)) return rc;
+  } else {
+    if (int rc = check_gemm_dims(2 * m->I, m->H, 2)) return rc;
+    if (int rc = check_gemm_dims(m->H, m->I, 1)) return rc;
+  }
   if (int rc = check_gemm_dims(m->E, m->H, 1)) return rc;
   Carver c{static_cast<char*>(workspace), workspace_bytes};
   StepWs w = carve_step(c, m, B);
@@ -729,7 +738,8 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
   uint16_t* x = static_cast<uint16_t*>(hidden);
   for (int l = 0; l < m->num_layers; ++l)
     MKD_REQUIRE(m->w_qkv[l] && m->w_o[l] && m->router[l] && m->gate_up[l] && m->down[l] &&
-                m->k_cache[l] && m->v_cache[l] && m->ln_in[l] && m->ln_post[l],
+                m->k_cache[l] && m->v_cache[l] && m->ln_in[l] && m->ln_post[l] &&
+                (!m->expert_format || (m->gate_up_scales[l] && m->down_scales[l])),
                 MKD_ERR_NULL, "decode_layers: null weight in layer %d", l);
   // Layer l's pre-attention norm is produced by the previous layer's MoE
   // finalize (one fused kernel); layer 0 normalises the input here.
@@ -779,7 +789,10 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     }
     if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], nullptr, w.moe.slot_w, nullptr,
                           nullptr, w.r, x, nullptr, B, m->H, m->E, m->I, m->K, MKD_ACT_SILU, 1.f,
-                          INFINITY, -INFINITY, INFINITY, -INFINITY, 1, w.moe, s, false))
+                          INFINITY, -INFINITY, INFINITY, -INFINITY, m->expert_format ? 0 : 1,
+                          w.moe, s, false, m->expert_format,
+                          m->expert_format ? m->gate_up_scales[l] : nullptr,
+                          m->expert_format ? m->down_scales[l] : nullptr))
       return rc;
     // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention norm
     {

@@ -45,6 +45,7 @@ class Qwen3MoeMKConfig:
     rope_theta: float = 1e6
     max_batch: int = 1
     max_seq: int = 2304           # KV capacity per sequence
+    expert_format: str = "bf16"   # "bf16", "mxfp8" (E4M3) or "mxfp4" (E2M1) expert weights
 
     @property
     def qkv_out(self) -> int:
@@ -96,11 +97,38 @@ class PackedLayer:
     router: torch.Tensor
     gate_up: torch.Tensor
     down: torch.Tensor
+    gate_up_scales: Optional[torch.Tensor] = None   # MX experts only
+    down_scales: Optional[torch.Tensor] = None
 
 
-def pack_layer(hf: Dict[str, torch.Tensor]) -> PackedLayer:
-    """One layer of HF weights -> packed (convert_qwen3_moe_hf_to_neuron_state_dict's role)."""
+EXPERT_FORMATS = {"bf16": 0, "mxfp8": 1, "mxfp4": 2}
+
+
+def pack_experts_mx(gate_up: torch.Tensor, down: torch.Tensor, fmt: int):
+    """HF expert weights gate_up [E, 2I, H], down [E, H, I] (bf16) -> MX quantised
+    (OCP rule, one E8M0 per 32 along the contraction) and packed:
+    (gate_up, gate_up_scales, down, down_scales)."""
+    from . import mx
+    E, N2, H = gate_up.shape
+    I = N2 // 2
+    gc, gs = mx.quantize_mx(gate_up.reshape(E * N2, H), fmt, H)
+    gu, gus = mx.pack_mx(gc.reshape(E, N2, -1), gs.reshape(E, N2, -1), fmt, H, I)
+    dc, ds = mx.quantize_mx(down.reshape(E * H, I), fmt, (I + 127) // 128 * 128)
+    dn, dns = mx.pack_mx(dc.reshape(E, H, -1), ds.reshape(E, H, -1), fmt, I)
+    return gu, gus, dn, dns
+
+
+def pack_layer(hf: Dict[str, torch.Tensor], expert_format: str = "bf16") -> PackedLayer:
+    """One layer of HF weights -> packed (convert_qwen3_moe_hf_to_neuron_state_dict's role).
+    expert_format "mxfp8" / "mxfp4" quantises the experts to MX first."""
     wqkv = torch.cat([hf["q_proj"], hf["k_proj"], hf["v_proj"]], 0).contiguous()
+    fmt = EXPERT_FORMATS[expert_format]
+    if fmt:
+        gu, gus, dn, dns = pack_experts_mx(hf["gate_up_proj"].contiguous(), hf["down_proj"].contiguous(), fmt)
+    else:
+        gu = packing.pack_experts_gate_up_hf(hf["gate_up_proj"].contiguous())
+        dn = packing.pack_experts_down_hf(hf["down_proj"].contiguous())
+        gus = dns = None
     return PackedLayer(
         w_qkv=packing.pack_out_in(wqkv),
         w_o=packing.pack_out_in(hf["o_proj"].contiguous()),
@@ -108,8 +136,7 @@ def pack_layer(hf: Dict[str, torch.Tensor]) -> PackedLayer:
         ln_in=hf["input_layernorm"].contiguous(),
         ln_post=hf["post_attention_layernorm"].contiguous(),
         router=packing.pack_out_in(hf["gate"].contiguous()),
-        gate_up=packing.pack_experts_gate_up_hf(hf["gate_up_proj"].contiguous()),
-        down=packing.pack_experts_down_hf(hf["down_proj"].contiguous()),
+        gate_up=gu, down=dn, gate_up_scales=gus, down_scales=dns,
     )
 
 
@@ -150,7 +177,7 @@ def convert_qwen3_moe_hf_to_mkd(state_dict: Dict[str, torch.Tensor], cfg: Qwen3M
         missing = [k for k, v in hf.items() if v is None]
         if missing:
             raise KeyError(f"layer {l}: missing {missing}")
-        layers.append(pack_layer(hf))
+        layers.append(pack_layer(hf, cfg.expert_format))
     return layers
 
 
@@ -213,11 +240,18 @@ class Qwen3MoeMegakernelModel(nn.Module):
             "k_cache": arr([self.kv_mgr.k(l) for l in range(Ln)]),
             "v_cache": arr([self.kv_mgr.v(l) for l in range(Ln)]),
         }
+        fmt = EXPERT_FORMATS[cfg.expert_format]
+        if fmt:
+            if any(x.gate_up_scales is None or x.down_scales is None for x in p):
+                raise ValueError(f"expert_format {cfg.expert_format!r} needs layers packed with MX experts")
+            self._arrays["gate_up_scales"] = arr([x.gate_up_scales for x in p])
+            self._arrays["down_scales"] = arr([x.down_scales for x in p])
         self._model = L.Qwen3Model(
             num_layers=Ln, H=cfg.hidden_size, nq=cfg.num_attention_heads,
             nkv=cfg.num_key_value_heads, d=cfg.head_dim, E=cfg.num_experts,
             K=cfg.num_experts_per_tok, I=cfg.moe_intermediate_size, S_max=cfg.max_seq,
-            eps=cfg.rms_norm_eps, inv_freq=self.inv_freq.data_ptr(), **self._arrays)
+            eps=cfg.rms_norm_eps, inv_freq=self.inv_freq.data_ptr(), expert_format=fmt,
+            **self._arrays)
 
     def rope_cos_sin(self, position_ids: torch.Tensor):
         """cos/sin [B, d] at position_ids (HF rotary: fp32 angles, halves duplicated)."""

@@ -420,13 +420,17 @@ class QwenLayer:
 
 def qwen_decoder_layer(x_bf: torch.Tensor, lw: QwenLayer, k_cache: torch.Tensor,
                        v_cache: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
-                       pos: torch.Tensor, shape: QwenShape, emulate_bf16: bool = True):
+                       pos: torch.Tensor, shape: QwenShape, emulate_bf16: bool = True,
+                       mx_experts: bool = False):
     """Residual stream in bf16 (transformer_qwen.py:117-127, adds :332, :371).
 
     Pre-attn RMSNorm is fused in attention as (x*rinv)*gamma -> bf16
     (attn_fused_nki.py:263-316); the post-attn RMSNorm is (x*gamma)*rinv with an
     fp32 copy for the router and a bf16 copy for the experts
-    (moe_fused_nki.py:70-153).  Returns (x_out, aux dict).
+    (moe_fused_nki.py:70-153).  mx_experts: lw.gate_up / lw.down hold the
+    dequantised MX expert weights and the experts follow moe_tkg_mx (MXFP8
+    activations) with the router's top-k weights as POST scales.
+    Returns (x_out, aux dict).
     """
     bf = lambda t: _bf(t, emulate_bf16)
     x = x_bf.float()
@@ -439,7 +443,11 @@ def qwen_decoder_layer(x_bf: torch.Tensor, lw: QwenLayer, k_cache: torch.Tensor,
     n32 = rmsnorm_tkg(r, lw.ln_post, shape.eps)
     n_bf = bf(n32)
     logits, idx, w = qwen_router(n32, lw.router.float().t(), shape.K, emulate_bf16)
-    moe = bf(qwen_experts(n_bf, lw.gate_up, lw.down, idx, w, emulate_bf16))
+    if mx_experts:
+        aff = torch.zeros(logits.shape).scatter_(1, idx, w)
+        moe = bf(moe_tkg_mx(n_bf, lw.gate_up, lw.down, aff, idx, scaling_mode="post"))
+    else:
+        moe = bf(qwen_experts(n_bf, lw.gate_up, lw.down, idx, w, emulate_bf16))
     out = bf(r + moe)
     return out, {"h": h, "attn": attn, "r": r, "n32": n32, "logits": logits, "idx": idx,
                  "w": w, "moe": moe}

@@ -351,7 +351,7 @@ def test_attention_block_tkg(mk, dev, B, H, nq, nkv, d, S_ctx, S_max, qknorm, si
 # ---------------------------------------------------------------- Qwen layer / step
 def _model_from_hf(mk, hf, cfg, B, dev):
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
-    layers = [Q.pack_layer({k: v.to(dev) for k, v in h.items()}) for h in hf]
+    layers = [Q.pack_layer({k: v.to(dev) for k, v in h.items()}, cfg.expert_format) for h in hf]
     return Q.Qwen3MoeMegakernelModel(cfg, layers, B, dev)
 
 
@@ -440,6 +440,36 @@ def test_qwen_full_shape_layer_teacher_forced(mk, dev, B, positions):
         assert changed in ([p], [])
 
 
+@pytest.mark.parametrize("B,fmt", [(4, "mxfp8"), (2, "mxfp4")])
+def test_qwen_full_shape_layer_mx_experts(mk, dev, B, fmt):
+    """Full-shape layer with MX experts (BASELINE config 4 flow): attention and norms
+    bf16, experts MX, activations MXFP8; vs the oracle on the dequantised weights
+    at 5e-2 (teacher-forced, same input)."""
+    import numpy as np
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    from oracle import mx as omx
+    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=1, max_batch=B, max_seq=1024, expert_format=fmt)
+    hf = Q.random_layer_hf(cfg, 0, 7, "cpu")
+    g = torch.Generator().manual_seed(B + 100)
+    pos = torch.randint(1, 1023, (B,), generator=g, dtype=torch.int32)
+    x = bf(torch.randn(B, cfg.hidden_size, generator=g))
+    kc = bf(torch.randn(B, 4, cfg.max_seq, 128, generator=g))
+    vc = bf(torch.randn(B, 4, cfg.max_seq, 128, generator=g))
+    model = _model_from_hf(mk, [hf], cfg, B, dev)
+    model.kv_mgr.k(0).copy_(kc.to(dev))
+    model.kv_mgr.v(0).copy_(vc.to(dev))
+    y = x.to(dev).contiguous()
+    model.decode_layers(y, pos.to(dev))
+    ofmt = "e4m3" if fmt == "mxfp8" else "e2m1"
+    lw = _ref_layer(hf)
+    lw.gate_up = torch.from_numpy(omx.dequantize_mx(*omx.quantize_mx(hf["gate_up_proj"].float().numpy(), ofmt), ofmt))
+    lw.down = torch.from_numpy(omx.dequantize_mx(*omx.quantize_mx(hf["down_proj"].float().numpy(), ofmt), ofmt))
+    cos, sin = ref.rope_cos_sin(pos, 128, cfg.rope_theta)
+    y_ref, _ = ref.qwen_decoder_layer(x, lw, kc.clone(), vc.clone(), cos, sin, pos, ref.QwenShape(),
+                                      mx_experts=True)
+    assert max_abs_rel(y, y_ref) < 5e-2
+
+
 def test_decode_step_two_layers_greedy(mk, dev):
     """Embedding -> 2 layers -> final norm -> lm_head -> argmax vs the oracle."""
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
@@ -453,7 +483,7 @@ def test_decode_step_two_layers_greedy(mk, dev):
     emb = bf(torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g))
     lnf = bf(1 + 0.1 * torch.randn(cfg.hidden_size, generator=g))
     lm = bf(0.05 * torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g))
-    layers = [Q.pack_layer({k: v.to(dev) for k, v in h.items()}) for h in hf]
+    layers = [Q.pack_layer({k: v.to(dev) for k, v in h.items()}, cfg.expert_format) for h in hf]
     model = Q.Qwen3MoeMegakernelModel(cfg, layers, B, dev, embed=emb.to(dev), ln_f=lnf.to(dev),
                                       lm_head=lm.to(dev))
     kc = [bf(torch.randn(B, 2, 128, 128, generator=g)) for _ in range(2)]
