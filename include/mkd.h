@@ -11,7 +11,8 @@
  *  - Every pointer argument is a DEVICE pointer unless stated otherwise; the
  *    caller owns all buffers.  The library never allocates device memory: any
  *    temporary storage comes from a caller-provided workspace whose size is
- *    reported by the matching *_workspace_bytes() query.
+ *    reported by the matching *_workspace_bytes() query.  Calls that share
+ *    one workspace must not overlap in time.
  *  - `stream` is a hipStream_t passed as void* (NULL = default stream).  All
  *    calls are asynchronous and stream-ordered; none synchronise the host.
  *  - Return value: 0 on success, a negative MKD_ERR_* code otherwise; the

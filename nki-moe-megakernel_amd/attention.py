@@ -146,7 +146,7 @@ def attention_block_tkg(
         w_out_packed=L.ptr(wout), bias_out=L.ptr(bout), residual=None, out=out.data_ptr(),
         B=B, H=H, H_out=H_out, nq=nq, nkv=nkv, d=d, S_max=S_max, round_qwen=0)
     lib = L.load()
-    ws = torch.empty(max(lib.mkd_attention_workspace_bytes(B, H, nq, nkv, d, S_max), 256),
+    ws = torch.zeros(max(lib.mkd_attention_workspace_bytes(B, H, nq, nkv, d, S_max), 256),
                      dtype=torch.uint8, device=dev)
     rc = lib.mkd_attention_block_tkg(args, ws.data_ptr(), ws.numel(), L.stream_ptr(dev))
     L.check(rc, "attention_block_tkg")

@@ -16,7 +16,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libmkd.so")
-SOURCES = ["capi.hip", "gemm.hip", "norm.hip", "attention.hip", "attn_mfma.hip", "moe.hip",
+SOURCES = ["capi.hip", "gemm.hip", "norm.hip", "attn_mfma.hip", "moe.hip",
            "misc.hip", "mx.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"

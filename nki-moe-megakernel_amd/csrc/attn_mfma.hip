@@ -1,22 +1,38 @@
-// Split-K GQA decode attention on MFMA (gfx950).
+// Decode attention for one new token per sequence (GQA, split-K over the KV
+// length) on gfx950 MFMA: two kernels.
 //
-// Grid (chunk, kv_head, sequence); block = 4 waves; wave w owns TPW tiles of 16
-// consecutive KV positions.  Per 16-position tile:
-//   S = K_tile . q^T   v_mfma_f32_16x16x32_bf16, A = 16 K rows read straight
-//                      from HBM (each lane 4 x 16 B of one row), B = the gqa
-//                      query heads of this kv head (16 columns, >= gqa zero).
-//                      D lane l holds S[pos 4*(l/16)+i][head l%16].
-//   softmax numerator  p = exp(s - m_head) with the wave's per-head max.
-//   O += P . V        v_mfma_f32_16x16x16_bf16: the S layout above IS the
-//                      A layout of this MFMA (row = head l%16, k = positions
-//                      4*(l/16)+i), so P never leaves registers.  B = V tile
-//                      [16 pos][16 d], staged through LDS (rows padded to
-//                      D+8 elements: conflict-free 2-byte transposed reads).
-// The 4 wave partials are merged in LDS; the block writes (max, sum,
-// unnormalised O) per (sequence, head, chunk) for attn_combine_kernel.
-// Positions: t < n_prior[b] read the cache, t == n_prior[b] is the new token
-// (staged by qk_prep), t > n_prior[b] are masked.  With round_qwen the score
-// is bf16(bf16(q.k) * scale) as in the reference's fused kernel.
+// attn_fused_kernel, grid (chunk, kv_head g, sequence b), block = 4 waves:
+//  1. prep: the GQA query heads of kv head g and the new k / v rows of g are
+//     taken from the fp32 projections, rounded (Qwen flow), per-head RMSNorm'd,
+//     RoPE'd (rotate-half, contiguous halves) into LDS.  Every block of (b, g)
+//     recomputes this (a few hundred elements; all of a wave's loads are issued
+//     before any use) instead of a separate launch.
+//  2. split-K attention over its 64*TPW positions; wave w owns TPW tiles of 16
+//     positions.  Per tile:
+//       S = K_tile . q^T   v_mfma_f32_16x16x32_bf16, A = 16 K rows (HBM, each
+//                          lane 4 x 16 B of one row), B = the gqa query heads
+//                          (16 columns, >= gqa zero).  D lane l holds
+//                          S[pos 4*(l/16)+i][head l%16].
+//       p = exp(s - m_head) with the wave's per-head max.
+//       O += P . V        v_mfma_f32_16x16x16_bf16: the S layout above IS the A
+//                          layout of this MFMA (row = head l%16, k = positions
+//                          4*(l/16)+i), so P never leaves registers.  B = V tile
+//                          [16 pos][16 d] staged through LDS (rows padded to
+//                          D+8 elements: conflict-free 2-byte transposed reads).
+//     Positions t < n_prior[b] read the cache, t == n_prior[b] is the new token
+//     (from LDS), t > n_prior[b] are masked.  With round_qwen the score is
+//     bf16(bf16(q.k) * scale) as in the reference's fused kernel.  The 4 wave
+//     partials merge in LDS into (max, sum, unnormalised O) per head, written
+//     to the chunk's slot of part_ml / part_o; the chunk holding position
+//     n_prior[b] also stages the new k / v rows for the scatter.
+// attn_combine_kernel, grid (q head, sequence), block = 4 waves: log-sum-exp
+//  merge of the chunks (waves take every 4th chunk, LDS reduce), optional sink
+//  logit, bf16 output; the blocks of the first head of each kv group then
+//  scatter the new k / v rows into the caches at write_pos[b] -- after every
+//  chunk has read the cache, because the kernels run in stream order.
+//  (A single kernel with a last-arriving-block combine was measured slower:
+//  the device-scope fence and the counter atomic cost ~9 us per block on
+//  this part, more than a kernel boundary.)
 #include "common.h"
 #include "mkd_internal.h"
 
@@ -29,50 +45,136 @@ MKD_DEV f32x4_t mfma16x16x16(uint2 a, uint2 b, f32x4_t c) {
                                                    __builtin_bit_cast(bf16x4v, b), c, 0, 0, 0);
 }
 
+// One wave: head `head` of sequence b (kind 0 query, 1 key, 2 value) from the
+// fp32 / bf16 projections to bf16 bits (attention_block_tkg.py:915-1138; Qwen
+// rounding attn_fused_nki.py:393-398, 426-446, 494-498, 543-582).  Split into
+// load and finish so a wave can issue the loads of all its heads first.
+template <int D>
+struct HeadPrep {
+  static constexpr int EL = D / 64;        // elements per lane
+  float x[EL], nw[EL], cs[EL], sn[EL];
+  MKD_DEV void load(const AttnArgs& a, int rope_mode, int b, int head, int kind, int lane) {
+    const uint16_t* nwp = kind == 0 ? a.q_norm : (kind == 1 ? a.k_norm : nullptr);
+#pragma unroll
+    for (int e = 0; e < EL; ++e) {
+      const int i = lane * EL + e;
+      const long long off = (long long)b * a.ld_qkv + head * D + i;
+      x[e] = a.qkv ? a.qkv[off] : bf2f(a.qkv_bf16[off]);
+      nw[e] = nwp ? bf2f(nwp[i]) : 1.f;
+      cs[e] = 1.f;
+      sn[e] = 0.f;
+      if (kind < 2 && rope_mode == 1) {
+        cs[e] = a.cos[(long long)b * D + i];
+        sn[e] = a.sin[(long long)b * D + i];
+      } else if (kind < 2 && rope_mode == 2) {   // from the position: pos * inv_freq[i mod D/2]
+        const float ang = (float)a.pos[b] * a.inv_freq[i % (D / 2)];
+        cs[e] = cosf(ang);
+        sn[e] = sinf(ang);
+      }
+    }
+  }
+  MKD_DEV void finish(const AttnArgs& a, int rope_mode, int kind, uint16_t* dst, int lane) {
+#pragma unroll
+    for (int e = 0; e < EL; ++e)
+      if (a.round_qwen) x[e] = rbf(x[e]);
+    if (kind < 2) {
+      if (kind == 0 ? a.q_norm != nullptr : a.k_norm != nullptr) {
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < EL; ++e) ss += x[e] * x[e];
+        ss = wave_sum(ss);
+        const float rinv = 1.0f / sqrtf(ss * (1.0f / D) + a.qk_eps);
+#pragma unroll
+        for (int e = 0; e < EL; ++e) {
+          x[e] = (x[e] * rinv) * nw[e];
+          if (a.round_qwen) x[e] = rbf(x[e]);
+        }
+      }
+      if (rope_mode) {
+        float p[EL];
+#pragma unroll
+        for (int e = 0; e < EL; ++e) p[e] = __shfl_xor(x[e], 32, 64);   // element i +- D/2
+#pragma unroll
+        for (int e = 0; e < EL; ++e) {
+          const int i = lane * EL + e;
+          const float rot = (i < D / 2) ? -p[e] : p[e];
+          x[e] = a.round_qwen ? rbf(rbf(x[e] * rbf(cs[e])) + rbf(rot * rbf(sn[e])))
+                              : x[e] * cs[e] + rot * sn[e];
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < EL; ++e) dst[lane * EL + e] = (uint16_t)f2bf(x[e]);
+  }
+};
+
 template <int D, int GQA, int TPW>
-__global__ void __launch_bounds__(256) attn_mfma_kernel(AttnArgs a) {
+__global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mode) {
   constexpr int VS = D + 8;                   // padded LDS row stride (elements)
   constexpr int NK = D / 32;                  // QK MFMAs per tile (k = 32)
   constexpr int NDT = D / 16;                 // PV d-tiles
+  constexpr int CP = 4 * TPW * 16;            // positions per block
   __shared__ uint16_t v_s[4][16 * VS];        // one V tile per wave
   __shared__ float m_s[4][16], l_s[4][16];
   __shared__ float o_s[4][GQA][D];
+  __shared__ __attribute__((aligned(16))) uint16_t q_s[GQA][D];
+  __shared__ __attribute__((aligned(16))) uint16_t kn_s[D];
+  __shared__ __attribute__((aligned(16))) uint16_t vn_s[D];
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int n = min(max(a.n_prior[b], 0), a.S_max);
   const int total = n + 1;
-  const int chunk0 = c * (4 * TPW * 16);
+  const int chunk0 = c * CP;
   if (chunk0 >= total) return;                // whole block: uniform exit
+
+  // ---- 1. prep of this kv group's heads: wave w takes heads w, w+4, ... of
+  // [q heads of g | k of g | v of g]; all loads first, then the math ----
+  constexpr int NR = (GQA + 2 + 3) / 4;
+  HeadPrep<D> hp[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int h = w + 4 * r;
+    if (h < GQA + 2) {
+      const int kind = h < GQA ? 0 : h - GQA + 1;
+      const int head = h < GQA ? g * GQA + h : (kind == 1 ? a.nq + g : a.nq + a.nkv + g);
+      hp[r].load(a, rope_mode, b, head, kind, lane);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int h = w + 4 * r;
+    if (h < GQA + 2) {
+      const int kind = h < GQA ? 0 : h - GQA + 1;
+      hp[r].finish(a, rope_mode, kind, h < GQA ? q_s[h] : (kind == 1 ? kn_s : vn_s), lane);
+    }
+  }
+  __syncthreads();
 
   const uint16_t* kbase = a.k_cache + b * a.cache_b_stride + g * a.cache_h_stride;
   const uint16_t* vbase = a.v_cache + b * a.cache_b_stride + g * a.cache_h_stride;
-  const uint16_t* knew = a.kv_new + (((long long)b * 2 + 0) * a.nkv + g) * D;
-  const uint16_t* vnew = a.kv_new + (((long long)b * 2 + 1) * a.nkv + g) * D;
 
   // q fragments (B operand): lane l -> head l%16, d = (l/16)*(D/4) + kk*8 .. +8
   const int hcol = lane & 15;
   const int dq = (lane >> 4) * (D / 4);
   u32x4_t qf[NK];
 #pragma unroll
-  for (int kk = 0; kk < NK; ++kk) {
-    if (hcol < GQA)
-      qf[kk] = ld16(a.q_out + ((long long)b * a.nq + g * GQA + hcol) * D + dq + kk * 8);
-    else
-      qf[kk] = u32x4_t{0, 0, 0, 0};
-  }
+  for (int kk = 0; kk < NK; ++kk)
+    qf[kk] = hcol < GQA ? *reinterpret_cast<const u32x4_t*>(&q_s[hcol][dq + kk * 8])
+                        : u32x4_t{0, 0, 0, 0};
 
-  // ---- scores for the wave's tiles ----
+  // ---- 2. scores for the wave's tiles ----
   float s[TPW][4];
   const int wbase = chunk0 + w * TPW * 16;
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
     const int t = wbase + tt * 16 + (lane & 15);  // A row owned by this lane
-    const uint16_t* kr = (t < n) ? kbase + (long long)t * D : knew;
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
-      u32x4_t kf = (t <= n) ? ld16(kr + dq + kk * 8) : u32x4_t{0, 0, 0, 0};
+      u32x4_t kf = {0, 0, 0, 0};
+      if (t < n) kf = ld16(kbase + (long long)t * D + dq + kk * 8);
+      else if (t == n) kf = *reinterpret_cast<const u32x4_t*>(&kn_s[dq + kk * 8]);
       acc = mfma16x16x32(kf, qf[kk], acc);
     }
 #pragma unroll
@@ -119,10 +221,11 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnArgs a) {
   for (int tt = 0; tt < TPW; ++tt) {
     // stage V rows of the tile: lane -> row l%16, D/4 elements at (l/16)*(D/4)
     const int t = wbase + tt * 16 + (lane & 15);
-    const uint16_t* vr = (t < n) ? vbase + (long long)t * D : vnew;
 #pragma unroll
     for (int j = 0; j < D / 32; ++j) {
-      const u32x4_t v = (t <= n) ? ld16(vr + dq + j * 8) : u32x4_t{0, 0, 0, 0};
+      u32x4_t v = {0, 0, 0, 0};
+      if (t < n) v = ld16(vbase + (long long)t * D + dq + j * 8);
+      else if (t == n) v = *reinterpret_cast<const u32x4_t*>(&vn_s[dq + j * 8]);
       *reinterpret_cast<u32x4_t*>(vt + (lane & 15) * VS + dq + j * 8) = v;
     }
     wave_lds_sync();                          // V tile visible to the whole wave
@@ -137,7 +240,7 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnArgs a) {
     __builtin_amdgcn_wave_barrier();
   }
 
-  // ---- merge the 4 waves ----
+  // ---- merge the 4 waves into this chunk's partial ----
   if (lane < 16) { m_s[w][lane] = m; l_s[w][lane] = lsum; }
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt)
@@ -167,20 +270,102 @@ __global__ void __launch_bounds__(256) attn_mfma_kernel(AttnArgs a) {
       ml[1] = L;
     }
   }
+
+  // the chunk holding the new token stages its k / v rows for the scatter
+  if (n >= chunk0 && n < chunk0 + CP)
+    for (int i = threadIdx.x; i < D; i += 256) {
+      a.kv_new[(((long long)b * 2 + 0) * a.nkv + g) * D + i] = kn_s[i];
+      a.kv_new[(((long long)b * 2 + 1) * a.nkv + g) * D + i] = vn_s[i];
+    }
+}
+
+// Combine: block (head h, sequence b), 4 waves; wave w takes chunks w, w+4, ...
+template <int D>
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
+  constexpr int EL = D / 64;
+  __shared__ float red[4];
+  __shared__ float acc_s[4][D];
+  __shared__ float l_s[4];
+  const int h = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int CP = a.chunk;
+  const int n = min(max(a.n_prior[b], 0), a.S_max);
+  const int nch = (n + 1 + CP - 1) / CP;
+  const float* ml = a.part_ml + ((long long)b * a.nq + h) * a.n_chunks * 2;
+  const float* po = a.part_o + ((long long)b * a.nq + h) * a.n_chunks * D;
+  // global max over the chunk maxima (and the sink)
+  float M = -INFINITY;
+  for (int k = threadIdx.x; k < nch; k += 256) M = fmaxf(M, ml[2 * k]);
+  M = wave_max(M);
+  if (lane == 0) red[w] = M;
+  __syncthreads();
+  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  if (a.sink) M = fmaxf(M, a.sink[h]);
+  float acc[EL], L = 0.f;
+#pragma unroll
+  for (int e = 0; e < EL; ++e) acc[e] = 0.f;
+  int k = w;
+  for (; k + 12 < nch; k += 16) {            // 4 chunks of this wave per batch
+    float mk[4], lk[4], pv[4][EL];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      mk[u] = ml[2 * (k + 4 * u)];
+      lk[u] = ml[2 * (k + 4 * u) + 1];
+#pragma unroll
+      for (int e = 0; e < EL; ++e) pv[u][e] = po[(long long)(k + 4 * u) * D + lane * EL + e];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const float wk = mk[u] == -INFINITY ? 0.f : expf(mk[u] - M);
+      L += lk[u] * wk;
+#pragma unroll
+      for (int e = 0; e < EL; ++e) acc[e] += pv[u][e] * wk;
+    }
+  }
+  for (; k < nch; k += 4) {
+    const float mk = ml[2 * k];
+    const float wk = mk == -INFINITY ? 0.f : expf(mk - M);
+    L += ml[2 * k + 1] * wk;
+#pragma unroll
+    for (int e = 0; e < EL; ++e) acc[e] += po[(long long)k * D + lane * EL + e] * wk;
+  }
+#pragma unroll
+  for (int e = 0; e < EL; ++e) acc_s[w][lane * EL + e] = acc[e];
+  if (lane == 0) l_s[w] = L;
+  __syncthreads();
+  if (threadIdx.x < D) {
+    const int d = threadIdx.x;
+    float Lt = (l_s[0] + l_s[1]) + (l_s[2] + l_s[3]);
+    if (a.sink) Lt += expf(a.sink[h] - M);
+    const float o = (acc_s[0][d] + acc_s[1][d]) + (acc_s[2][d] + acc_s[3][d]);
+    a.attn_out[((long long)b * a.nq + h) * D + d] = (uint16_t)f2bf(Lt > 0.f ? o / Lt : 0.f);
+    // in-place KV scatter of the new rows (attention_block_tkg.py:1144-1470):
+    // the first query head of each kv group writes that group's rows
+    const int gqa = a.nq / a.nkv;
+    if (a.update_cache && h % gqa == 0) {
+      const int g = h / gqa;
+      const int wp = a.write_pos ? a.write_pos[b] : a.pos[b];
+      if (wp >= 0 && wp < a.S_max) {
+        const long long off = b * a.cache_b_stride + g * a.cache_h_stride + (long long)wp * D + d;
+        a.k_cache[off] = a.kv_new[(((long long)b * 2 + 0) * a.nkv + g) * D + d];
+        a.v_cache[off] = a.kv_new[(((long long)b * 2 + 1) * a.nkv + g) * D + d];
+      }
+    }
+  }
 }
 
 template <int D, int GQA, int TPW>
-static hipError_t launch_attn(const AttnArgs& a, hipStream_t s) {
-  return timed_launch(attn_mfma_kernel<D, GQA, TPW>, dim3(a.n_chunks, a.nkv, a.B), dim3(256), 0, s,
-                      a);
+static hipError_t launch_attn(const AttnArgs& a, int rope_mode, hipStream_t s) {
+  return timed_launch(attn_fused_kernel<D, GQA, TPW>, dim3(a.n_chunks, a.nkv, a.B), dim3(256), 0, s,
+                      a, rope_mode);
 }
 
 template <int D, int GQA>
-static hipError_t launch_tpw(const AttnArgs& a, hipStream_t s) {
+static hipError_t launch_tpw(const AttnArgs& a, int rope_mode, hipStream_t s) {
   const int chunk = a.chunk;
-  if (chunk == 64) return launch_attn<D, GQA, 1>(a, s);
-  if (chunk == 128) return launch_attn<D, GQA, 2>(a, s);
-  if (chunk == 256) return launch_attn<D, GQA, 4>(a, s);
+  if (chunk == 64) return launch_attn<D, GQA, 1>(a, rope_mode, s);
+  if (chunk == 128) return launch_attn<D, GQA, 2>(a, rope_mode, s);
+  if (chunk == 256) return launch_attn<D, GQA, 4>(a, rope_mode, s);
   return hipErrorInvalidValue;
 }
 
@@ -193,23 +378,30 @@ int attn_chunk_for(int B, int nkv, int S_max) {
   return 64;
 }
 
-hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t s) {
+hipError_t attn_combine_launch(const AttnArgs& a, hipStream_t s) {
+  if (a.d == 128) hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(a.nq, a.B), dim3(256), 0, s, a);
+  else if (a.d == 64) hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(a.nq, a.B), dim3(256), 0, s, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s) {
   const int gqa = a.nq / a.nkv;
   if (a.d == 128) {
     switch (gqa) {
-      case 1: return launch_tpw<128, 1>(a, s);
-      case 2: return launch_tpw<128, 2>(a, s);
-      case 4: return launch_tpw<128, 4>(a, s);
-      case 8: return launch_tpw<128, 8>(a, s);
-      case 16: return launch_tpw<128, 16>(a, s);
+      case 1: return launch_tpw<128, 1>(a, rope_mode, s);
+      case 2: return launch_tpw<128, 2>(a, rope_mode, s);
+      case 4: return launch_tpw<128, 4>(a, rope_mode, s);
+      case 8: return launch_tpw<128, 8>(a, rope_mode, s);
+      case 16: return launch_tpw<128, 16>(a, rope_mode, s);
     }
   } else if (a.d == 64) {
     switch (gqa) {
-      case 1: return launch_tpw<64, 1>(a, s);
-      case 2: return launch_tpw<64, 2>(a, s);
-      case 4: return launch_tpw<64, 4>(a, s);
-      case 8: return launch_tpw<64, 8>(a, s);
-      case 16: return launch_tpw<64, 16>(a, s);
+      case 1: return launch_tpw<64, 1>(a, rope_mode, s);
+      case 2: return launch_tpw<64, 2>(a, rope_mode, s);
+      case 4: return launch_tpw<64, 4>(a, rope_mode, s);
+      case 8: return launch_tpw<64, 8>(a, rope_mode, s);
+      case 16: return launch_tpw<64, 16>(a, rope_mode, s);
     }
   }
   return hipErrorInvalidValue;

@@ -535,7 +535,7 @@ int mkd_pack_mx_weights(const void* codes, const void* scales, void* dst, void* 
 struct AttnWs {
   uint16_t* hnorm;
   float* qkv;
-  uint16_t *q, *kvn, *attn;
+  uint16_t *attn, *kvn;
   float *po, *pml;
   int chunk, n_chunks;
 };
@@ -546,9 +546,8 @@ static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_
   w.n_chunks = (S_max + 1 + w.chunk - 1) / w.chunk;
   w.hnorm = c.take<uint16_t>((size_t)B * H);
   w.qkv = c.take<float>((size_t)B * (nq + 2 * nkv) * d);
-  w.q = c.take<uint16_t>((size_t)B * nq * d);
-  w.kvn = c.take<uint16_t>((size_t)B * 2 * nkv * d);
   w.attn = c.take<uint16_t>((size_t)B * nq * d);
+  w.kvn = c.take<uint16_t>((size_t)B * 2 * nkv * d);
   w.po = c.take<float>((size_t)B * nq * w.n_chunks * d);
   w.pml = c.take<float>((size_t)B * nq * w.n_chunks * 2);
   return w;
@@ -591,7 +590,7 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   a.k_norm = static_cast<const uint16_t*>(p->k_norm);
   a.qk_eps = p->qk_eps;
   a.cos = p->cos; a.sin = p->sin; a.inv_freq = inv_freq; a.pos = pos_for_rope;
-  a.q_out = w.q; a.kv_new = w.kvn;
+  a.kv_new = w.kvn;
   a.k_cache = static_cast<uint16_t*>(p->k_cache);
   a.v_cache = static_cast<uint16_t*>(p->v_cache);
   a.cache_h_stride = (long long)p->S_max * p->d;
@@ -608,13 +607,12 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   a.update_cache = p->update_cache;
   a.write_pos = p->kv_cache_update_idx;
   const int rope_mode = p->cos ? 1 : (inv_freq ? 2 : 0);
-  MKD_TRY(qk_prep_launch(a, rope_mode, p->round_qwen, s), "qk_prep");
-  {
+  {  // q/k norm + RoPE and split-K attention in one launch
     const int ps = prof_begin(MKD_KCLASS_ATTN, s);
-    MKD_TRY(attn_decode_launch(a, s), "attn_decode");
+    MKD_TRY(attn_decode_launch(a, rope_mode, s), "attention");
     prof_end(ps, s);
   }
-  MKD_TRY(attn_combine_launch(a, s), "attn_combine");
+  MKD_TRY(attn_combine_launch(a, s), "attention combine + kv scatter");
   // 5. output projection
   if (p->w_out_packed) {
     GemmArgs o = dense_args(p->w_out_packed, w.attn, p->nq * p->d, p->H_out, p->nq * p->d, p->B,

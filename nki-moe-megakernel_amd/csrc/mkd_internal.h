@@ -126,8 +126,6 @@ struct AttnArgs {
   const float* sin;
   const float* inv_freq;      // [d/2] when cos/sin are generated from positions
   const int* pos;             // [B] cache write position == number of prior tokens
-  uint16_t* q_out;            // [B, nq, d] bf16
-  uint16_t* kv_new;           // [B, 2, nkv, d] bf16 (k then v)
   uint16_t* k_cache;          // [B, nkv, S_max, d]
   uint16_t* v_cache;
   long long cache_b_stride, cache_h_stride;  // elements
@@ -145,11 +143,12 @@ struct AttnArgs {
   uint16_t* attn_out;         // [B, nq * d] bf16
   int update_cache;
   const int* write_pos;       // [B] row written (default pos); < 0 -> skip
+  uint16_t* kv_new;           // [B, 2, nkv, d] staged new k / v rows
 };
-hipError_t qk_prep_launch(const AttnArgs& a, int rope_mode, int round_qwen, hipStream_t s);
-hipError_t attn_decode_launch(const AttnArgs& a, hipStream_t s);
-int attn_chunk_for(int B, int nkv, int S_max);   // positions per attention block (64/128/256)
+// rope_mode: 0 none, 1 cos/sin tables, 2 from pos and inv_freq
+hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s);
 hipError_t attn_combine_launch(const AttnArgs& a, hipStream_t s);
+int attn_chunk_for(int B, int nkv, int S_max);   // positions per attention block (64/128/256)
 
 // moe.hip
 struct RouterArgs {
