@@ -67,7 +67,10 @@ def prefill_kv(model, cfg, ctx, seed, dev):
     g.manual_seed(seed + 2)
     for l in range(cfg.num_hidden_layers):
         for t in (model.kv_mgr.k(l), model.kv_mgr.v(l)):
-            t[:, :, :ctx].copy_(torch.randn(t[:, :, :ctx].shape, generator=g, device=dev))
+            if cfg.kv_block_len:          # block pool: every row random
+                t.copy_(torch.randn(t.shape, generator=g, device=dev))
+            else:
+                t[:, :, :ctx].copy_(torch.randn(t[:, :, :ctx].shape, generator=g, device=dev))
 
 
 def cpu_baseline(cfg, lens, seconds_budget=20.0):
@@ -161,6 +164,8 @@ def main():
                     help="per-sequence KV lengths drawn uniformly from [512, 8192] (configs[2])")
     ap.add_argument("--experts", choices=["bf16", "mxfp8", "mxfp4"], default="bf16",
                     help="expert weight format (mxfp8 at --batch 32 is configs[3])")
+    ap.add_argument("--kv-block", type=int, default=0,
+                    help="paged KV cache with blocks of this many positions (0: flat)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -181,8 +186,10 @@ def main():
     else:
         lens = torch.full((B,), ctx, dtype=torch.int32)
     S_max = ((int(lens.max()) + args.warmup + args.steps + 8 + 127) // 128) * 128
+    if args.kv_block:
+        S_max = (S_max + args.kv_block - 1) // args.kv_block * args.kv_block
     cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=args.layers, max_batch=B, max_seq=S_max,
-                             expert_format=args.experts)
+                             expert_format=args.experts, kv_block_len=args.kv_block)
     t0 = time.time()
     model = build_model(Q, cfg, B, dev, seed=1234)
     prefill_kv(model, cfg, int(lens.max()), 1234, dev)
@@ -291,6 +298,7 @@ def main():
                    "batch": B, "kv_context": ctx if not args.ragged else "U[512,8192]",
                    "kv_lengths_mean": round(float(lens.float().mean()), 1),
                    "layers": cfg.num_hidden_layers, "experts": args.experts,
+                   "kv_block": args.kv_block,
                    "graph": graph is not None,
                    "step_algorithmic_GB": round(step_b / 1e9, 4),
                    "step_GBps": round(step_gbs, 1),
@@ -303,7 +311,7 @@ def main():
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers)
-                     if (args.experts == "bf16" and not args.ragged) else None,
+                     if (args.experts == "bf16" and not args.ragged and not args.kv_block) else None,
                      "avg_us": round(avg_ms * 1e3, 2), "bytes_per_launch": int(alg_bytes)},
         "cpu_baseline": cpu,
     }
@@ -320,13 +328,15 @@ REF_TOK_S_BS1 = 122.7
 
 def vs_baseline(tok_s, cfg, B, ctx, args):
     if (args.experts == "bf16" and not args.ragged and B == 1 and ctx == 2048
-            and cfg.num_hidden_layers == 48):
+            and cfg.num_hidden_layers == 48 and not args.kv_block):
         return round(tok_s / REF_TOK_S_BS1, 3)
     return None
 
 
 def workload_name(cfg, B, ctx, lens, args):
     kv = "KV lengths U[512,8192] (ragged)" if args.ragged else f"KV context {ctx}"
+    if args.kv_block:
+        kv += f", paged KV (blocks of {args.kv_block})"
     tag = ""
     if args.experts == "bf16" and not args.ragged and B == 1 and ctx == 2048 and cfg.num_hidden_layers == 48:
         tag = " (BASELINE configs[1])"

@@ -218,6 +218,16 @@ typedef struct {
   void* out;                   /* [B, H_out] bf16, or [B, nq d] bf16 without W_out */
   int B, H, H_out, nq, nkv, d, S_max;
   int round_qwen;              /* emulate the Qwen kernel's bf16 rounding points */
+  /* Block (paged) KV cache, attention_block_tkg.py:199-206, 1473-1685.  When
+   * active_blocks_table ([B, blocks_per_seq] int32, device) is set, k_cache /
+   * v_cache are [num_blocks, block_len, nkv, d]; position t of sequence b is
+   * row t % block_len of block table[b][t / block_len] (entries outside
+   * [0, num_blocks) read as zero rows); S_max must be blocks_per_seq *
+   * block_len; kv_cache_update_idx holds GLOBAL rows (block * block_len + row,
+   * outside [0, num_blocks * block_len) skips) or NULL to derive the row of
+   * position n_prior[b] from the table. */
+  const int* active_blocks_table;
+  int blocks_per_seq, block_len, num_blocks;
 } mkd_attention_args;
 size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S_max);
 int mkd_attention_block_tkg(const mkd_attention_args* args, void* workspace,
@@ -252,6 +262,12 @@ typedef struct {
                                   quantised to MXFP8 before each projection */
   const void* const* gate_up_scales;  /* MX: packed scales per layer     */
   const void* const* down_scales;
+  /* Block (paged) KV: when block_table ([B, blocks_per_seq] int32, device,
+   * shared by all layers) is set, each layer's k_cache / v_cache is
+   * [num_blocks, block_len, nkv, d] and S_max = blocks_per_seq * block_len; the
+   * new row of sequence b goes to the table slot of position_ids[b]. */
+  const int* block_table;
+  int blocks_per_seq, block_len, num_blocks;
 } mkd_qwen3_model;
 size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B);
 /* hidden [B, H] bf16 in/out; position_ids [B] int32 (device); cos/sin [B, d]

@@ -67,6 +67,7 @@ class AttentionArgs(C.Structure):
         ("w_out_packed", vp), ("bias_out", vp), ("residual", vp), ("out", vp),
         ("B", i32), ("H", i32), ("H_out", i32), ("nq", i32), ("nkv", i32), ("d", i32),
         ("S_max", i32), ("round_qwen", i32),
+        ("active_blocks_table", vp), ("blocks_per_seq", i32), ("block_len", i32), ("num_blocks", i32),
     ]
 
 
@@ -79,6 +80,7 @@ class Qwen3Model(C.Structure):
         ("router", C.POINTER(vp)), ("gate_up", C.POINTER(vp)), ("down", C.POINTER(vp)),
         ("k_cache", C.POINTER(vp)), ("v_cache", C.POINTER(vp)), ("inv_freq", vp),
         ("expert_format", i32), ("gate_up_scales", C.POINTER(vp)), ("down_scales", C.POINTER(vp)),
+        ("block_table", vp), ("blocks_per_seq", i32), ("block_len", i32), ("num_blocks", i32),
     ]
 
 

@@ -44,15 +44,22 @@ def attention_block_tkg(
     W_out [q_heads*d, H].  out is [B*S_tkg, H] (or [B, q_heads, d, S_tkg]
     without W_out).  The caches are updated in place.
 
-    Supported: S_tkg = 1, flat (non-block) caches, no quantisation.  Other
-    reference options raise NotImplementedError; post-RoPE RMSNorm is applied
-    when enabled.  enable_fa_s_prior_tiling is a scheduling hint (the GPU path
-    always tiles the KV length).
+    Block (paged) KV cache (attention_block_tkg.py:199-206, 699-707,
+    1473-1685): with active_blocks_table [B, num_active_blocks], K_cache /
+    V_cache are [num_blocks, block_len, d] (or [num_blocks, block_len,
+    kv_heads, d]); S_ctx = num_active_blocks * block_len, position t of
+    sequence b is row t % block_len of block table[b, t // block_len], the
+    active token is mask slot S_ctx - 1, and kv_cache_update_idx holds global
+    rows block * block_len + row (uint32 max = skip).
+
+    Supported: S_tkg = 1, flat or block caches, no quantisation.  Other
+    reference options raise NotImplementedError.  enable_fa_s_prior_tiling is a
+    scheduling hint (the GPU path always tiles the KV length).
     """
     if KVDP != 1:
         raise NotImplementedError("KV data parallelism spans several devices; one GPU only")
-    if active_blocks_table is not None:
-        raise NotImplementedError("block (paged) KV cache is not supported by this operator yet")
+    if K_cache_transposed and active_blocks_table is not None:
+        raise ValueError("K_cache_transposed must be False for block KV cache")
     if K_cache_transposed:
         raise NotImplementedError("K_cache_transposed=True is not supported (K is stored [.., S, d])")
     if transposed_out or out_in_sb or sbm is not None:
@@ -74,23 +81,39 @@ def attention_block_tkg(
     d = V_cache.shape[-1]
     if d % 2:
         raise ValueError(f"d_head must be even, got {d}")
-    if K_cache.dim() == 3:
-        nkv = 1
-        S_max = K_cache.shape[1]
-    elif K_cache.dim() == 4:
-        nkv = K_cache.shape[1]
-        S_max = K_cache.shape[2]
-    else:
-        raise ValueError(f"K_cache must be 3-D or 4-D, got {tuple(K_cache.shape)}")
     if tuple(K_cache.shape) != tuple(V_cache.shape):
-        raise ValueError("K_cache / V_cache shape mismatch")
-    if K_cache.shape[0] != B:
-        raise ValueError(f"V_cache batch mismatch: expected {B}, got {K_cache.shape[0]}")
+        raise ValueError(f"KV cache shape mismatch: K={tuple(K_cache.shape)} vs V={tuple(V_cache.shape)}")
+    block = active_blocks_table is not None
+    if block:
+        if K_cache.dim() == 3:
+            nkv = 1
+        elif K_cache.dim() == 4:
+            nkv = K_cache.shape[2]
+        else:
+            raise ValueError(f"block K_cache must be [num_blocks, block_len, (kv_heads,) d], got {tuple(K_cache.shape)}")
+        num_blocks, blk_len = K_cache.shape[0], K_cache.shape[1]
+        if active_blocks_table.dim() != 2 or active_blocks_table.shape[0] != B:
+            raise ValueError(f"active_blocks_table must be [B={B}, num_active_blocks], got {tuple(active_blocks_table.shape)}")
+        n_active = active_blocks_table.shape[1]
+        S_max = n_active * blk_len
+    else:
+        if K_cache.dim() == 3:
+            nkv = 1
+            S_max = K_cache.shape[1]
+        elif K_cache.dim() == 4:
+            nkv = K_cache.shape[1]
+            S_max = K_cache.shape[2]
+        else:
+            raise ValueError(f"K_cache must be 3-D or 4-D, got {tuple(K_cache.shape)}")
+        if K_cache.shape[0] != B:
+            raise ValueError(f"V_cache batch mismatch: expected {B}, got {K_cache.shape[0]}")
     I = W_qkv.shape[1]
     if I % d:
         raise ValueError(f"QKV weights must be packed as (q_heads + 2) * d_head, got I={I}, d_head={d}")
     nq = I // d - 2 * nkv
     S_ctx = attention_mask.shape[0]
+    if block and S_ctx != S_max:
+        raise ValueError(f"block KV: attention_mask covers S_ctx={S_ctx}, the table covers {S_max}")
     if tuple(attention_mask.shape) != (S_ctx, B, nq, S_tkg):
         raise ValueError(f"attention_mask shape mismatch: expected {(S_ctx, B, nq, S_tkg)}, got {tuple(attention_mask.shape)}")
     if S_ctx - 1 > S_max:
@@ -129,7 +152,13 @@ def attention_block_tkg(
     wpos = None
     if update_cache:
         idx = kv_cache_update_idx.reshape(-1).to(torch.int64)
-        wpos = torch.where(idx == U32_MAX, torch.full_like(idx, -1), idx).to(torch.int32).contiguous()
+        wpos = torch.where((idx == U32_MAX) | (idx < 0) | (idx > 0x7FFFFFFF),
+                           torch.full_like(idx, -1), idx).to(torch.int32).contiguous()
+    table = None
+    if block:
+        t64 = active_blocks_table.to(torch.int64)
+        table = torch.where((t64 < 0) | (t64 >= num_blocks), torch.full_like(t64, -1), t64) \
+            .to(torch.int32).contiguous()
     sink_f = sink.reshape(-1).float().contiguous() if sink is not None else None
     bqkv = bias_qkv.reshape(-1).to(torch.bfloat16).contiguous() if bias_qkv is not None else None
     bout = bias_out.reshape(-1).to(torch.bfloat16).contiguous() if bias_out is not None else None
@@ -144,7 +173,9 @@ def attention_block_tkg(
         mask=mask_u8.data_ptr(), mask_s_ctx=S_ctx, sink=L.ptr(sink_f), softmax_scale=scale,
         update_cache=int(bool(update_cache)), kv_cache_update_idx=L.ptr(wpos),
         w_out_packed=L.ptr(wout), bias_out=L.ptr(bout), residual=None, out=out.data_ptr(),
-        B=B, H=H, H_out=H_out, nq=nq, nkv=nkv, d=d, S_max=S_max, round_qwen=0)
+        B=B, H=H, H_out=H_out, nq=nq, nkv=nkv, d=d, S_max=S_max, round_qwen=0,
+        active_blocks_table=L.ptr(table), blocks_per_seq=table.shape[1] if block else 0,
+        block_len=blk_len if block else 0, num_blocks=num_blocks if block else 0)
     lib = L.load()
     ws = torch.zeros(max(lib.mkd_attention_workspace_bytes(B, H, nq, nkv, d, S_max), 256),
                      dtype=torch.uint8, device=dev)

@@ -19,7 +19,10 @@
 //                          4*(l/16)+i), so P never leaves registers.  B = V tile
 //                          [16 pos][16 d] staged through LDS (rows padded to
 //                          D+8 elements: conflict-free 2-byte transposed reads).
-//     Positions t < n_prior[b] read the cache, t == n_prior[b] is the new token
+//     Positions t < n_prior[b] read the cache (flat [B, nkv, S_max, d], or block
+//     [num_blocks, blk_len, nkv, d] through the sequence's block table: the
+//     paged layout of attention_block_tkg.py:199-206, 1473-1685), t == n_prior[b]
+//     is the new token
 //     (from LDS), t > n_prior[b] are masked.  With round_qwen the score is
 //     bf16(bf16(q.k) * scale) as in the reference's fused kernel.  The 4 wave
 //     partials merge in LDS into (max, sum, unnormalised O) per head, written
@@ -108,6 +111,35 @@ struct HeadPrep {
   }
 };
 
+// Row t of kv head g of sequence b in a cache (flat or block layout); null when
+// the block table holds no valid block there (the row then reads as zero).
+template <int D>
+MKD_DEV const uint16_t* kv_row(const AttnArgs& a, const uint16_t* cache, int b, int g, int t) {
+  if (!a.block_table) return cache + b * a.cache_b_stride + g * a.cache_h_stride + (long long)t * D;
+  const int blk = a.block_table[(long long)b * a.tbl_stride + t / a.blk_len];
+  if ((unsigned)blk >= (unsigned)a.num_blocks) return nullptr;
+  return cache + (((long long)blk * a.blk_len + t % a.blk_len) * a.nkv + g) * D;
+}
+
+// Cache row that receives the new token of sequence b (-1: skip).
+MKD_DEV long long kv_write_row(const AttnArgs& a, int b) {
+  if (!a.block_table) {
+    const int wp = a.write_pos ? a.write_pos[b] : a.pos[b];
+    return (wp >= 0 && wp < a.S_max) ? wp : -1;
+  }
+  long long row;
+  if (a.write_pos) {
+    row = a.write_pos[b];
+  } else {
+    const int p = a.pos[b];
+    if (p < 0 || p >= a.S_max) return -1;
+    const int blk = a.block_table[(long long)b * a.tbl_stride + p / a.blk_len];
+    if ((unsigned)blk >= (unsigned)a.num_blocks) return -1;
+    row = (long long)blk * a.blk_len + p % a.blk_len;
+  }
+  return (row >= 0 && row < (long long)a.num_blocks * a.blk_len) ? row : -1;
+}
+
 template <int D, int GQA, int TPW>
 __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mode) {
   constexpr int VS = D + 8;                   // padded LDS row stride (elements)
@@ -151,8 +183,6 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   }
   __syncthreads();
 
-  const uint16_t* kbase = a.k_cache + b * a.cache_b_stride + g * a.cache_h_stride;
-  const uint16_t* vbase = a.v_cache + b * a.cache_b_stride + g * a.cache_h_stride;
 
   // q fragments (B operand): lane l -> head l%16, d = (l/16)*(D/4) + kk*8 .. +8
   const int hcol = lane & 15;
@@ -169,11 +199,12 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
     const int t = wbase + tt * 16 + (lane & 15);  // A row owned by this lane
+    const uint16_t* kr = t < n ? kv_row<D>(a, a.k_cache, b, g, t) : nullptr;
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
       u32x4_t kf = {0, 0, 0, 0};
-      if (t < n) kf = ld16(kbase + (long long)t * D + dq + kk * 8);
+      if (kr) kf = ld16(kr + dq + kk * 8);
       else if (t == n) kf = *reinterpret_cast<const u32x4_t*>(&kn_s[dq + kk * 8]);
       acc = mfma16x16x32(kf, qf[kk], acc);
     }
@@ -221,10 +252,11 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   for (int tt = 0; tt < TPW; ++tt) {
     // stage V rows of the tile: lane -> row l%16, D/4 elements at (l/16)*(D/4)
     const int t = wbase + tt * 16 + (lane & 15);
+    const uint16_t* vr = t < n ? kv_row<D>(a, a.v_cache, b, g, t) : nullptr;
 #pragma unroll
     for (int j = 0; j < D / 32; ++j) {
       u32x4_t v = {0, 0, 0, 0};
-      if (t < n) v = ld16(vbase + (long long)t * D + dq + j * 8);
+      if (vr) v = ld16(vr + dq + j * 8);
       else if (t == n) v = *reinterpret_cast<const u32x4_t*>(&vn_s[dq + j * 8]);
       *reinterpret_cast<u32x4_t*>(vt + (lane & 15) * VS + dq + j * 8) = v;
     }
@@ -344,9 +376,11 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
     const int gqa = a.nq / a.nkv;
     if (a.update_cache && h % gqa == 0) {
       const int g = h / gqa;
-      const int wp = a.write_pos ? a.write_pos[b] : a.pos[b];
-      if (wp >= 0 && wp < a.S_max) {
-        const long long off = b * a.cache_b_stride + g * a.cache_h_stride + (long long)wp * D + d;
+      const long long row = kv_write_row(a, b);
+      if (row >= 0) {
+        const long long off = a.block_table
+                                  ? (row * a.nkv + g) * D + d
+                                  : b * a.cache_b_stride + g * a.cache_h_stride + row * D + d;
         a.k_cache[off] = a.kv_new[(((long long)b * 2 + 0) * a.nkv + g) * D + d];
         a.v_cache[off] = a.kv_new[(((long long)b * 2 + 1) * a.nkv + g) * D + d];
       }

@@ -606,6 +606,8 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   a.attn_out = w.attn;
   a.update_cache = p->update_cache;
   a.write_pos = p->kv_cache_update_idx;
+  a.block_table = p->active_blocks_table;
+  a.tbl_stride = p->blocks_per_seq; a.blk_len = p->block_len; a.num_blocks = p->num_blocks;
   const int rope_mode = p->cos ? 1 : (inv_freq ? 2 : 0);
   {  // q/k norm + RoPE and split-K attention in one launch
     const int ps = prof_begin(MKD_KCLASS_ATTN, s);
@@ -655,8 +657,16 @@ static int validate_attn(const mkd_attention_args* p) {
   MKD_REQUIRE(!p->residual || p->w_out_packed, MKD_ERR_INVALID, "attention: residual needs W_out");
   MKD_REQUIRE(!p->mask || p->mask_s_ctx >= 1, MKD_ERR_INVALID, "attention: mask_s_ctx must be >= 1");
   MKD_REQUIRE(!(p->cos && !p->sin), MKD_ERR_NULL, "attention: cos without sin");
-  MKD_REQUIRE(!p->update_cache || p->kv_cache_update_idx, MKD_ERR_NULL,
-              "attention: update_cache needs kv_cache_update_idx");
+  if (p->active_blocks_table) {
+    MKD_REQUIRE(p->block_len > 0 && p->blocks_per_seq > 0 && p->num_blocks > 0, MKD_ERR_INVALID,
+                "attention: block cache needs block_len, blocks_per_seq, num_blocks > 0");
+    MKD_REQUIRE((long long)p->blocks_per_seq * p->block_len == p->S_max, MKD_ERR_INVALID,
+                "attention: S_max %d != blocks_per_seq %d * block_len %d", p->S_max,
+                p->blocks_per_seq, p->block_len);
+  } else {
+    MKD_REQUIRE(!p->update_cache || p->kv_cache_update_idx, MKD_ERR_NULL,
+                "attention: update_cache needs kv_cache_update_idx");
+  }
   return MKD_OK;
 }
 
@@ -724,6 +734,11 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     if (int rc = check_gemm_dims(m->H, m->I, 1)) return rc;
   }
   if (int rc = check_gemm_dims(m->E, m->H, 1)) return rc;
+  if (m->block_table)
+    MKD_REQUIRE(m->block_len > 0 && m->num_blocks > 0 &&
+                    (long long)m->blocks_per_seq * m->block_len == m->S_max,
+                MKD_ERR_INVALID, "decode_layers: S_max %d != blocks_per_seq %d * block_len %d",
+                m->S_max, m->blocks_per_seq, m->block_len);
   Carver c{static_cast<char*>(workspace), workspace_bytes};
   StepWs w = carve_step(c, m, B);
   MKD_REQUIRE(c.ok, MKD_ERR_WORKSPACE, "decode_layers: workspace %zu < %zu bytes", workspace_bytes, c.used);
@@ -753,7 +768,10 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     ap.cos = cos; ap.sin = sin;
     ap.k_cache = m->k_cache[l]; ap.v_cache = m->v_cache[l];
     ap.n_prior = position_ids;
-    ap.update_cache = 1; ap.kv_cache_update_idx = position_ids;
+    ap.update_cache = 1;
+    ap.kv_cache_update_idx = m->block_table ? nullptr : position_ids;
+    ap.active_blocks_table = m->block_table;
+    ap.blocks_per_seq = m->blocks_per_seq; ap.block_len = m->block_len; ap.num_blocks = m->num_blocks;
     ap.w_out_packed = m->w_o[l];
     ap.out = w.r;
     ap.B = B; ap.H = m->H; ap.H_out = m->H; ap.nq = m->nq; ap.nkv = m->nkv; ap.d = m->d;

@@ -144,6 +144,12 @@ struct AttnArgs {
   int update_cache;
   const int* write_pos;       // [B] row written (default pos); < 0 -> skip
   uint16_t* kv_new;           // [B, 2, nkv, d] staged new k / v rows
+  // block (paged) KV cache: caches are [num_blocks, blk_len, nkv, d]; position t
+  // of sequence b lives in block block_table[b * tbl_stride + t / blk_len] at
+  // row t % blk_len; write_pos is then a global row (block * blk_len + row), or
+  // derived from pos through the table when write_pos is null.  null = flat.
+  const int* block_table;
+  int tbl_stride, blk_len, num_blocks;
 };
 // rope_mode: 0 none, 1 cos/sin tables, 2 from pos and inv_freq
 hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s);

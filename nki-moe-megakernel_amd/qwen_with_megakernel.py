@@ -46,6 +46,7 @@ class Qwen3MoeMKConfig:
     max_batch: int = 1
     max_seq: int = 2304           # KV capacity per sequence
     expert_format: str = "bf16"   # "bf16", "mxfp8" (E4M3) or "mxfp4" (E2M1) expert weights
+    kv_block_len: int = 0         # > 0: paged KV cache with blocks of this many positions
 
     @property
     def qkv_out(self) -> int:
@@ -183,10 +184,31 @@ def convert_qwen3_moe_hf_to_mkd(state_dict: Dict[str, torch.Tensor], cfg: Qwen3M
 
 class KVCacheManager:
     """Holds per-layer K/V caches; ``past_key_values`` is flat [K0, V0, K1, V1, ...]
-    like the NxDI kv_mgr the reference reads (qwen_with_megakernel.py:410-420)."""
+    like the NxDI kv_mgr the reference reads (qwen_with_megakernel.py:410-420).
 
-    def __init__(self, cfg: Qwen3MoeMKConfig, batch: int, device):
-        shape = (batch, cfg.num_key_value_heads, cfg.max_seq, cfg.head_dim)
+    Flat caches are [B, kv_heads, max_seq, d].  With cfg.kv_block_len > 0 the
+    caches are a block pool [num_blocks, block_len, kv_heads, d] per layer and
+    ``block_table`` [B, blocks_per_seq] (int32, shared by all layers) maps
+    sequence b's positions t to row t % block_len of block
+    block_table[b, t // block_len] -- the paged layout of
+    attention_block_tkg.py:199-206.  Blocks are handed out as a seeded random
+    permutation, so sequences own scattered blocks."""
+
+    def __init__(self, cfg: Qwen3MoeMKConfig, batch: int, device, seed: int = 0):
+        self.block_len = cfg.kv_block_len
+        self.block_table = None
+        if self.block_len:
+            if cfg.max_seq % self.block_len:
+                raise ValueError(f"max_seq {cfg.max_seq} must be a multiple of kv_block_len {self.block_len}")
+            self.blocks_per_seq = cfg.max_seq // self.block_len
+            self.num_blocks = batch * self.blocks_per_seq
+            g = torch.Generator().manual_seed(seed)
+            perm = torch.randperm(self.num_blocks, generator=g).to(torch.int32)
+            self.block_table = perm.reshape(batch, self.blocks_per_seq).contiguous().to(device)
+            shape = (self.num_blocks, self.block_len, cfg.num_key_value_heads, cfg.head_dim)
+        else:
+            self.blocks_per_seq = self.num_blocks = 0
+            shape = (batch, cfg.num_key_value_heads, cfg.max_seq, cfg.head_dim)
         self.past_key_values = []
         for _ in range(cfg.num_hidden_layers):
             self.past_key_values.append(torch.zeros(shape, dtype=torch.bfloat16, device=device))
@@ -246,12 +268,14 @@ class Qwen3MoeMegakernelModel(nn.Module):
                 raise ValueError(f"expert_format {cfg.expert_format!r} needs layers packed with MX experts")
             self._arrays["gate_up_scales"] = arr([x.gate_up_scales for x in p])
             self._arrays["down_scales"] = arr([x.down_scales for x in p])
+        kv = self.kv_mgr
         self._model = L.Qwen3Model(
             num_layers=Ln, H=cfg.hidden_size, nq=cfg.num_attention_heads,
             nkv=cfg.num_key_value_heads, d=cfg.head_dim, E=cfg.num_experts,
             K=cfg.num_experts_per_tok, I=cfg.moe_intermediate_size, S_max=cfg.max_seq,
             eps=cfg.rms_norm_eps, inv_freq=self.inv_freq.data_ptr(), expert_format=fmt,
-            **self._arrays)
+            block_table=L.ptr(kv.block_table), blocks_per_seq=kv.blocks_per_seq,
+            block_len=kv.block_len, num_blocks=kv.num_blocks, **self._arrays)
 
     def rope_cos_sin(self, position_ids: torch.Tensor):
         """cos/sin [B, d] at position_ids (HF rotary: fp32 angles, halves duplicated)."""

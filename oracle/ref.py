@@ -465,6 +465,23 @@ def final_norm_lm_head(x_bf: torch.Tensor, ln_f: torch.Tensor, lm_head: torch.Te
 # ---------------------------------------------------------------------------
 # Generic attention_block_tkg (nki_kernels/attention/attention_block_tkg.py:83-583)
 # ---------------------------------------------------------------------------
+def block_kv_to_flat(cache: torch.Tensor, table: torch.Tensor) -> torch.Tensor:
+    """Block KV cache [num_blocks, block_len, ...] + active_blocks_table [B, n]
+    -> flat [B, n * block_len, ...]: position t of sequence b is row
+    t % block_len of block table[b, t // block_len]
+    (attention_block_tkg.py:199-206, 699-707; entries outside [0, num_blocks)
+    give zero rows)."""
+    nb, blk = cache.shape[0], cache.shape[1]
+    B, n = table.shape
+    out = torch.zeros((B, n * blk) + tuple(cache.shape[2:]), dtype=cache.dtype)
+    for b in range(B):
+        for j in range(n):
+            e = int(table[b, j])
+            if 0 <= e < nb:
+                out[b, j * blk:(j + 1) * blk] = cache[e]
+    return out
+
+
 def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
                         q_norm_w, k_norm_w, qk_eps, cos, sin, K_cache, V_cache,
                         attention_mask, sink, update_cache, kv_cache_update_idx,

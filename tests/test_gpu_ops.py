@@ -348,6 +348,70 @@ def test_attention_block_tkg(mk, dev, B, H, nq, nkv, d, S_ctx, S_max, qknorm, si
             assert max_abs_rel(Kn[b, :, p], Kr4[b, :, p]) < TOL
 
 
+@pytest.mark.parametrize("B,nq,nkv,d,blk,n_act,num_blocks", [
+    (2, 8, 1, 128, 16, 5, 24), (3, 8, 2, 64, 32, 4, 20), (1, 16, 2, 128, 64, 3, 7)])
+def test_attention_block_tkg_block_kv(mk, dev, B, nq, nkv, d, blk, n_act, num_blocks):
+    """Paged KV: [num_blocks, block_len, (kv_heads,) d] caches addressed through
+    active_blocks_table; same result as the flat oracle on the gathered cache, and
+    only the global row kv_cache_update_idx[b] of the block cache is written."""
+    from nki_moe_megakernel_amd.common_types import QuantizationType
+    g = torch.Generator().manual_seed(B * 7 + blk)
+    H = 256
+    X = bf(torch.randn(B, 1, H, generator=g))
+    W = bf(0.05 * torch.randn(H, d * (nq + 2 * nkv), generator=g))
+    Wo = bf(0.05 * torch.randn(nq * d, H, generator=g))
+    kshape = (num_blocks, blk, d) if nkv == 1 else (num_blocks, blk, nkv, d)
+    Kb = bf(torch.randn(*kshape, generator=g))
+    Vb = bf(torch.randn(*kshape, generator=g))
+    table = torch.stack([torch.randperm(num_blocks, generator=g)[:n_act] for _ in range(B)]).to(torch.int32)
+    table[0, 1] = -1                                  # an unmapped block (masked below)
+    S_ctx = n_act * blk
+    mask = (torch.rand(S_ctx, B, nq, 1, generator=g) > 0.2).to(torch.bfloat16)
+    mask[blk:2 * blk, 0] = 0                          # positions of the unmapped block
+    mask[-1] = 1
+    pos = torch.arange(B) * 5 + 2
+    cos, sin = ref.rope_cos_sin(pos, d, 1e6)
+    cos_r = cos[:, :d // 2].t()[:, :, None].contiguous()
+    sin_r = sin[:, :d // 2].t()[:, :, None].contiguous()
+    free = [r for r in range(num_blocks * blk)]
+    upd = torch.tensor([[free[(b * 37 + 11) % len(free)]] for b in range(B)], dtype=torch.int64)
+    if B > 1:
+        upd[-1, 0] = 0xFFFFFFFF
+    Kg, Vg = Kb.to(dev), Vb.to(dev)
+    out, _, _ = mk.attention_block_tkg(
+        X.to(dev), None, False, 1e-6, None, W.to(dev), None, QuantizationType.NONE, None, None,
+        False, 1e-6, None, None, cos_r.to(dev), sin_r.to(dev), True, False, 1e-6, None, None,
+        False, table.to(dev), Kg, Vg, mask.to(dev), None, True, upd.to(dev), Wo.to(dev), None,
+        QuantizationType.NONE, None, None, False, False)
+    # oracle: gather the flat view, run the flat restatement per kv head
+    Kf = ref.block_kv_to_flat(Kb.float() if nkv > 1 else Kb.float()[:, :, None], table)  # [B, S, nkv, d]
+    Vf = ref.block_kv_to_flat(Vb.float() if nkv > 1 else Vb.float()[:, :, None], table)
+    gqa = nq // nkv
+    attn = torch.zeros(B, nq * d)
+    newk = torch.zeros(B, nkv, d)
+    for h in range(nkv):
+        cols = torch.cat([torch.arange(h * gqa * d, (h + 1) * gqa * d),
+                          nq * d + h * d + torch.arange(d),
+                          (nq + nkv) * d + h * d + torch.arange(d)])
+        Kh, Vh = Kf[:, :, h].clone(), Vf[:, :, h].clone()
+        o, K2, _ = ref.attention_block_tkg(
+            X.float(), W.float()[:, cols], None, 1e-6, None, None, None, 1e-6, cos_r, sin_r,
+            Kh, Vh, mask[:, :, h * gqa:(h + 1) * gqa].float(), None, True,
+            torch.full((B, 1), S_ctx - 1), None, None)
+        attn[:, h * gqa * d:(h + 1) * gqa * d] = o
+        newk[:, h] = K2[:, S_ctx - 1]
+    assert max_abs_rel(out, attn @ Wo.float()) < TOL
+    Kn = Kg.cpu().reshape(num_blocks * blk, nkv, d)
+    K0 = Kb.reshape(num_blocks * blk, nkv, d)
+    changed = (Kn != K0).any(-1).any(-1).nonzero().flatten().tolist()
+    want = sorted(int(upd[b, 0]) for b in range(B) if int(upd[b, 0]) != 0xFFFFFFFF)
+    assert changed == want or set(changed) <= set(want)
+    for b in range(B):
+        r = int(upd[b, 0])
+        if r != 0xFFFFFFFF:
+            assert max_abs_rel(Kn[r], newk[b]) < TOL
+
+
 # ---------------------------------------------------------------- Qwen layer / step
 def _model_from_hf(mk, hf, cfg, B, dev):
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
@@ -468,6 +532,48 @@ def test_qwen_full_shape_layer_mx_experts(mk, dev, B, fmt):
     y_ref, _ = ref.qwen_decoder_layer(x, lw, kc.clone(), vc.clone(), cos, sin, pos, ref.QwenShape(),
                                       mx_experts=True)
     assert max_abs_rel(y, y_ref) < 5e-2
+
+
+def test_qwen_layer_paged_kv_matches_flat(mk, dev):
+    """The decode step on a paged KV pool (scattered blocks per sequence) gives
+    bit-identical hidden states to the flat cache holding the same rows, and writes
+    the new rows at the block-table slot of each position."""
+    import dataclasses
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    B, S, blk = 3, 1024, 64
+    cfg_f = Q.Qwen3MoeMKConfig(num_hidden_layers=1, max_batch=B, max_seq=S)
+    cfg_p = dataclasses.replace(cfg_f, kv_block_len=blk)
+    hf = Q.random_layer_hf(cfg_f, 0, 5, "cpu")
+    g = torch.Generator().manual_seed(77)
+    pos = torch.tensor([1000, 63, 640], dtype=torch.int32)
+    x = bf(torch.randn(B, cfg_f.hidden_size, generator=g))
+    kc = bf(torch.randn(B, 4, S, 128, generator=g))
+    vc = bf(torch.randn(B, 4, S, 128, generator=g))
+    mf = _model_from_hf(mk, [hf], cfg_f, B, dev)
+    mp = _model_from_hf(mk, [hf], cfg_p, B, dev)
+    mf.kv_mgr.k(0).copy_(kc.to(dev))
+    mf.kv_mgr.v(0).copy_(vc.to(dev))
+    table = mp.kv_mgr.block_table.cpu().long()
+    kp = torch.zeros(mp.kv_mgr.num_blocks, blk, 4, 128, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    for b in range(B):
+        for j in range(S // blk):
+            kp[table[b, j]] = kc[b, :, j * blk:(j + 1) * blk].permute(1, 0, 2)
+            vp[table[b, j]] = vc[b, :, j * blk:(j + 1) * blk].permute(1, 0, 2)
+    mp.kv_mgr.k(0).copy_(kp.to(dev))
+    mp.kv_mgr.v(0).copy_(vp.to(dev))
+    yf = x.to(dev).contiguous()
+    yp = x.to(dev).contiguous()
+    mf.decode_layers(yf, pos.to(dev))
+    mp.decode_layers(yp, pos.to(dev))
+    assert torch.equal(yf.cpu(), yp.cpu())
+    kf_new, kp_new = mf.kv_mgr.k(0).cpu(), mp.kv_mgr.k(0).cpu()
+    changed = (kp_new != kp).any(-1).any(-1).nonzero().tolist()
+    want = sorted([int(table[b, int(pos[b]) // blk]), int(pos[b]) % blk] for b in range(B))
+    assert sorted(changed) == want
+    for b in range(B):
+        p = int(pos[b])
+        assert torch.equal(kp_new[table[b, p // blk], p % blk], kf_new[b, :, p])
 
 
 def test_decode_step_two_layers_greedy(mk, dev):

@@ -336,3 +336,16 @@ def test_qwen_layer_bf16_flow_within_tolerance_of_fp32():
                                   emulate_bf16=True)
     err = (y - t["y"]).abs().max() / t["y"].abs().max()
     assert err < 2e-2, err
+
+
+def test_block_kv_gather_identity_and_permutation():
+    """block_kv_to_flat: an identity table is a reshape; a permuted table moves
+    whole blocks; an entry outside the pool reads as zeros."""
+    from oracle import ref
+    cache = torch.randn(6, 4, 3)
+    ident = torch.arange(6).reshape(2, 3)
+    assert torch.equal(ref.block_kv_to_flat(cache, ident), cache.reshape(2, 12, 3))
+    perm = torch.tensor([[5, 0], [-1, 2]])
+    flat = ref.block_kv_to_flat(cache, perm)
+    assert torch.equal(flat[0, :4], cache[5]) and torch.equal(flat[0, 4:], cache[0])
+    assert torch.equal(flat[1, :4], torch.zeros(4, 3)) and torch.equal(flat[1, 4:], cache[2])
