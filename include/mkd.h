@@ -228,6 +228,12 @@ typedef struct {
    * position n_prior[b] from the table. */
   const int* active_blocks_table;
   int blocks_per_seq, block_len, num_blocks;
+  int hidden_actual;           /* pre-attention RMSNorm divisor (X_hidden_dim_actual);
+                                  <= 0: H                                         */
+  int window;                  /* > 0: the cache is a ring of `window` rows (sliding
+                                  window): min(n_prior, window-1) prior rows are
+                                  attended and, with kv_cache_update_idx NULL, the
+                                  new row goes to n_prior % (window-1)            */
 } mkd_attention_args;
 size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S_max);
 int mkd_attention_block_tkg(const mkd_attention_args* args, void* workspace,
@@ -268,7 +274,31 @@ typedef struct {
    * new row of sequence b goes to the table slot of position_ids[b]. */
   const int* block_table;
   int blocks_per_seq, block_len, num_blocks;
+  /* Model variant.  MKD_VARIANT_QWEN3 (0): the Qwen3 fused-kernel flow above.
+   * MKD_VARIANT_GPT_OSS: the stock-kernel flow of transformer_gpt_oss.py:
+   * 239-522 -- RMSNorm (x*g)*rsqrt(sum/H_actual + eps) in both places, QKV and
+   * o_proj biases, no q/k norm, RoPE from the cos/sin tables, attention sinks,
+   * per-layer sliding windows, router top-k on biased bf16-input logits then
+   * softmax over the top-k (router_pre_norm=False), experts Swish(alpha) with
+   * clamps and biases, no Qwen rounding points.  The per-layer arrays below are
+   * HOST arrays of device pointers (NULL array or NULL entry = none). */
+  int variant;
+  int H_actual;                /* RMSNorm divisor; <= 0: H                      */
+  const void* const* b_qkv;    /* [(nq + 2 nkv) d] bf16                          */
+  const void* const* b_o;      /* [H] bf16                                       */
+  const void* const* sinks;    /* [nq] fp32                                      */
+  const void* const* router_bias;  /* [E] bf16                                   */
+  const void* const* gate_up_bias; /* [E, 2, I] bf16                             */
+  const void* const* down_bias;    /* [E, H] bf16                                */
+  const int* window;           /* host [num_layers]: sliding window W (0 = full);
+                                  a windowed layer's caches hold W rows          */
+  const int* layer_s_max;      /* host [num_layers] cache rows per layer, or NULL
+                                  (all S_max)                                    */
+  float act_alpha;             /* Swish alpha (GPT-OSS 1.702)                    */
+  float gate_hi, gate_lo, up_hi, up_lo;   /* expert clamps (+-INFINITY = none)   */
 } mkd_qwen3_model;
+#define MKD_VARIANT_QWEN3 0
+#define MKD_VARIANT_GPT_OSS 1
 size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B);
 /* hidden [B, H] bf16 in/out; position_ids [B] int32 (device); cos/sin [B, d]
  * fp32 or NULL (then generated from position_ids and inv_freq). */
@@ -284,10 +314,13 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
 /* token_ids [B] int32 (ids outside [0, V) give zero rows), table [V, H] bf16, out [B, H]. */
 int mkd_embed(const int* token_ids, const void* table, void* out, int B, int H, int V,
               void* stream);
+/* hidden_actual: RMSNorm divisor (<= 0: H, for a zero-padded H); norm_order: 2 =
+ * weight * bf16(x * rinv) (HF Qwen3 RMSNorm), 1 = bf16((x * rinv) * weight)
+ * (HF GPT-OSS RMSNorm). */
 size_t mkd_lm_head_workspace_bytes(int B, int H, int V);
 int mkd_lm_head_greedy(const void* hidden, const void* ln_f, float eps, const void* lm_head_packed,
-                       int B, int H, int V, float* logits, int* next_tokens, void* workspace,
-                       size_t workspace_bytes, void* stream);
+                       int B, int H, int V, int hidden_actual, int norm_order, float* logits,
+                       int* next_tokens, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Greedy-loop glue for a graph-captured decode step: token_ids[b] = next_tokens[b],
  * position_ids[b] += 1.  (The reference's host loop does this in NxDI.) */

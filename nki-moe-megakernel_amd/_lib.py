@@ -68,6 +68,7 @@ class AttentionArgs(C.Structure):
         ("B", i32), ("H", i32), ("H_out", i32), ("nq", i32), ("nkv", i32), ("d", i32),
         ("S_max", i32), ("round_qwen", i32),
         ("active_blocks_table", vp), ("blocks_per_seq", i32), ("block_len", i32), ("num_blocks", i32),
+        ("hidden_actual", i32), ("window", i32),
     ]
 
 
@@ -81,6 +82,10 @@ class Qwen3Model(C.Structure):
         ("k_cache", C.POINTER(vp)), ("v_cache", C.POINTER(vp)), ("inv_freq", vp),
         ("expert_format", i32), ("gate_up_scales", C.POINTER(vp)), ("down_scales", C.POINTER(vp)),
         ("block_table", vp), ("blocks_per_seq", i32), ("block_len", i32), ("num_blocks", i32),
+        ("variant", i32), ("H_actual", i32), ("b_qkv", C.POINTER(vp)), ("b_o", C.POINTER(vp)),
+        ("sinks", C.POINTER(vp)), ("router_bias", C.POINTER(vp)), ("gate_up_bias", C.POINTER(vp)),
+        ("down_bias", C.POINTER(vp)), ("window", C.POINTER(i32)), ("layer_s_max", C.POINTER(i32)),
+        ("act_alpha", f32), ("gate_hi", f32), ("gate_lo", f32), ("up_hi", f32), ("up_lo", f32),
     ]
 
 
@@ -106,7 +111,7 @@ _SIGS = {
     "mkd_qwen3_decode_layers": (i32, [C.POINTER(Qwen3Model), i32, vp, vp, vp, vp, vp, sz, vp]),
     "mkd_embed": (i32, [vp, vp, vp, i32, i32, i32, vp]),
     "mkd_lm_head_workspace_bytes": (sz, [i32, i32, i32]),
-    "mkd_lm_head_greedy": (i32, [vp, vp, f32, vp, i32, i32, i32, vp, vp, vp, sz, vp]),
+    "mkd_lm_head_greedy": (i32, [vp, vp, f32, vp, i32, i32, i32, i32, i32, vp, vp, vp, sz, vp]),
     "mkd_decode_advance": (i32, [vp, vp, vp, i32, vp]),
     "mkd_profile_events": (i32, [i32, C.POINTER(vp), C.POINTER(vp), i32]),
     "mkd_profile_count": (i32, []),

@@ -121,10 +121,18 @@ MKD_DEV const uint16_t* kv_row(const AttnArgs& a, const uint16_t* cache, int b, 
   return cache + (((long long)blk * a.blk_len + t % a.blk_len) * a.nkv + g) * D;
 }
 
+// Prior positions attended by sequence b (the new token sits at index n).
+MKD_DEV int prior_len(const AttnArgs& a, int b) {
+  int n = max(a.n_prior[b], 0);
+  if (a.window > 0) n = min(n, a.window - 1);
+  return min(n, a.S_max);
+}
+
 // Cache row that receives the new token of sequence b (-1: skip).
 MKD_DEV long long kv_write_row(const AttnArgs& a, int b) {
   if (!a.block_table) {
-    const int wp = a.write_pos ? a.write_pos[b] : a.pos[b];
+    int wp = a.write_pos ? a.write_pos[b] : a.pos[b];
+    if (a.window > 1 && !a.write_pos) wp = wp >= 0 ? wp % (a.window - 1) : -1;
     return (wp >= 0 && wp < a.S_max) ? wp : -1;
   }
   long long row;
@@ -155,7 +163,7 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int n = min(max(a.n_prior[b], 0), a.S_max);
+  const int n = prior_len(a, b);
   const int total = n + 1;
   const int chunk0 = c * CP;
   if (chunk0 >= total) return;                // whole block: uniform exit
@@ -321,7 +329,7 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
   const int h = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int CP = a.chunk;
-  const int n = min(max(a.n_prior[b], 0), a.S_max);
+  const int n = prior_len(a, b);
   const int nch = (n + 1 + CP - 1) / CP;
   const float* ml = a.part_ml + ((long long)b * a.nq + h) * a.n_chunks * 2;
   const float* po = a.part_o + ((long long)b * a.nq + h) * a.n_chunks * D;

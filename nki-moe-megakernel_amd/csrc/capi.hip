@@ -570,7 +570,8 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   const void* xin = p->X;
   if (p->rmsnorm_gamma) {
     MKD_TRY(rmsnorm_launch(p->X, 0, static_cast<const uint16_t*>(p->rmsnorm_gamma),
-                           w.hnorm, nullptr, p->B, p->H, p->H, p->H, p->rmsnorm_eps,
+                           w.hnorm, nullptr, p->B, p->H, p->H,
+                           p->hidden_actual > 0 ? p->hidden_actual : p->H, p->rmsnorm_eps,
                            p->rmsnorm_order, s), "attn rmsnorm");
     xin = w.hnorm;
   }
@@ -606,6 +607,7 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   a.attn_out = w.attn;
   a.update_cache = p->update_cache;
   a.write_pos = p->kv_cache_update_idx;
+  a.window = p->window;
   a.block_table = p->active_blocks_table;
   a.tbl_stride = p->blocks_per_seq; a.blk_len = p->block_len; a.num_blocks = p->num_blocks;
   const int rope_mode = p->cos ? 1 : (inv_freq ? 2 : 0);
@@ -754,28 +756,48 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
                 m->k_cache[l] && m->v_cache[l] && m->ln_in[l] && m->ln_post[l] &&
                 (!m->expert_format || (m->gate_up_scales[l] && m->down_scales[l])),
                 MKD_ERR_NULL, "decode_layers: null weight in layer %d", l);
+  // Qwen3 flow: pre-attention norm (x*rinv)*g, Qwen rounding points, fp32 router
+  // input.  GPT-OSS flow: rmsnorm_tkg's (x*g)*rinv with H_actual everywhere,
+  // biases, sinks, sliding windows, bf16 router input with logit top-k.
+  const bool oss = m->variant == MKD_VARIANT_GPT_OSS;
+  const int ha = m->H_actual > 0 ? m->H_actual : m->H;
+  const int pre_order = oss ? 0 : 1;
+  auto at = [](const void* const* arr, int l) -> const void* { return arr ? arr[l] : nullptr; };
+  for (int l = 0; l < m->num_layers; ++l) {
+    const int wl = m->window ? m->window[l] : 0;
+    const int sl = m->layer_s_max ? m->layer_s_max[l] : m->S_max;
+    MKD_REQUIRE(sl > 0 && sl <= m->S_max && wl >= 0 && wl <= sl && (wl == 0 || wl >= 2) &&
+                    !(wl && m->block_table),
+                MKD_ERR_INVALID, "decode_layers: layer %d window %d / cache rows %d invalid", l, wl, sl);
+  }
   // Layer l's pre-attention norm is produced by the previous layer's MoE
   // finalize (one fused kernel); layer 0 normalises the input here.
   MKD_TRY(rmsnorm_launch(x, 0, static_cast<const uint16_t*>(m->ln_in[0]), w.attn.hnorm, nullptr, B,
-                         m->H, m->H, m->H, m->eps, 1, s), "pre norm");
+                         m->H, m->H, ha, m->eps, pre_order, s), "pre norm");
   const int o_kgrid = ((m->H + 15) / 16 < 256 && choose_kw_split(m->nq * m->d, 2) > 0) ? 2 : 1;
   for (int l = 0; l < m->num_layers; ++l) {
+    const int wl = m->window ? m->window[l] : 0;
     mkd_attention_args ap;
     memset(&ap, 0, sizeof(ap));
     ap.X = w.attn.hnorm;                       // already normalised
     ap.w_qkv_packed = m->w_qkv[l];
-    ap.q_norm = m->q_norm[l]; ap.k_norm = m->k_norm[l]; ap.qk_eps = m->eps;
+    ap.bias_qkv = at(m->b_qkv, l);
+    ap.q_norm = at(m->q_norm, l); ap.k_norm = at(m->k_norm, l); ap.qk_eps = m->eps;
     ap.cos = cos; ap.sin = sin;
     ap.k_cache = m->k_cache[l]; ap.v_cache = m->v_cache[l];
     ap.n_prior = position_ids;
+    ap.sink = static_cast<const float*>(at(m->sinks, l));
+    ap.window = wl;
     ap.update_cache = 1;
-    ap.kv_cache_update_idx = m->block_table ? nullptr : position_ids;
-    ap.active_blocks_table = m->block_table;
+    ap.kv_cache_update_idx = (m->block_table || wl) ? nullptr : position_ids;
+    ap.active_blocks_table = wl ? nullptr : m->block_table;
     ap.blocks_per_seq = m->blocks_per_seq; ap.block_len = m->block_len; ap.num_blocks = m->num_blocks;
     ap.w_out_packed = m->w_o[l];
+    ap.bias_out = at(m->b_o, l);
     ap.out = w.r;
     ap.B = B; ap.H = m->H; ap.H_out = m->H; ap.nq = m->nq; ap.nkv = m->nkv; ap.d = m->d;
-    ap.S_max = m->S_max; ap.round_qwen = 1;
+    ap.S_max = m->layer_s_max ? m->layer_s_max[l] : m->S_max;
+    ap.round_qwen = oss ? 0 : 1;
     if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s, w.oparts, o_kgrid))
       return rc;
     // r = bf16(x + bf16(o_proj)) from the split-K partials, then the post-attention
@@ -786,26 +808,35 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
       na.dsum = w.oparts; na.dK = o_kgrid; na.ds_row = m->H; na.ds_k = (long long)B * m->H;
       na.resid_out = w.r;
       na.gamma = static_cast<const uint16_t*>(m->ln_post[l]);
-      na.out_bf16 = w.nbf; na.out_f32 = w.nf32;
-      na.rows = B; na.H = m->H; na.hidden_actual = m->H; na.eps = m->eps; na.order = 0;
+      na.out_bf16 = w.nbf; na.out_f32 = oss ? nullptr : w.nf32;
+      na.rows = B; na.H = m->H; na.hidden_actual = ha; na.eps = m->eps; na.order = 0;
       MKD_TRY(norm_launch(na, s), "residual + post norm");
     }
-    // router (fp32 normed input, split-K) + Qwen top-k + expert groups in one select launch
+    // router (split-K GEMM) + top-k + expert groups in one select launch: Qwen
+    // fp32 input and fused flow; GPT-OSS bf16 input, biased logits, top-k then
+    // softmax over the top-k (router_topk.py:868-887)
     RouterArgs ra;
     memset(&ra, 0, sizeof(ra));
-    ra.T = B; ra.E = m->E; ra.K = m->K; ra.mode = MKD_ROUTER_QWEN;
+    ra.T = B; ra.E = m->E; ra.K = m->K; ra.mode = oss ? 0 : MKD_ROUTER_QWEN;
+    ra.bias = static_cast<const uint16_t*>(at(m->router_bias, l));
     ra.idx_out = w.moe.idx; ra.slot_w = w.moe.slot_w;
     ra.n_groups = w.moe.n_groups; ra.grp_expert = w.moe.grp_expert;
     ra.grp_count = w.moe.grp_count; ra.grp_offset = w.moe.grp_offset;
     ra.pair_token = w.moe.pair_token; ra.pair_slot = w.moe.pair_slot;
     {
       const int ps = prof_begin(MKD_KCLASS_ROUTER, s);
-      if (int rc = router_stage(w.nf32, true, m->H, m->router[l], w.logits, ra, s)) return rc;
+      if (int rc = router_stage(oss ? static_cast<const void*>(w.nbf) : w.nf32, !oss, m->H,
+                                m->router[l], w.logits, ra, s))
+        return rc;
       prof_end(ps, s);
     }
-    if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], nullptr, w.moe.slot_w, nullptr,
-                          nullptr, w.r, x, nullptr, B, m->H, m->E, m->I, m->K, MKD_ACT_SILU, 1.f,
-                          INFINITY, -INFINITY, INFINITY, -INFINITY, m->expert_format ? 0 : 1,
+    if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], nullptr, w.moe.slot_w,
+                          static_cast<const uint16_t*>(at(m->gate_up_bias, l)),
+                          static_cast<const uint16_t*>(at(m->down_bias, l)), w.r, x, nullptr, B,
+                          m->H, m->E, m->I, m->K, oss ? MKD_ACT_SWISH : MKD_ACT_SILU,
+                          oss ? m->act_alpha : 1.f, oss ? m->gate_hi : INFINITY,
+                          oss ? m->gate_lo : -INFINITY, oss ? m->up_hi : INFINITY,
+                          oss ? m->up_lo : -INFINITY, (oss || m->expert_format) ? 0 : 1,
                           w.moe, s, false, m->expert_format,
                           m->expert_format ? m->gate_up_scales[l] : nullptr,
                           m->expert_format ? m->down_scales[l] : nullptr))
@@ -818,7 +849,7 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
       na.resid_out = x;
       na.gamma = (l + 1 < m->num_layers) ? static_cast<const uint16_t*>(m->ln_in[l + 1]) : nullptr;
       na.out_bf16 = w.attn.hnorm;
-      na.rows = B; na.H = m->H; na.hidden_actual = m->H; na.eps = m->eps; na.order = 1;
+      na.rows = B; na.H = m->H; na.hidden_actual = ha; na.eps = m->eps; na.order = pre_order;
       MKD_TRY(norm_launch(na, s), "moe finalize + next norm");
     }
   }
@@ -845,8 +876,8 @@ size_t mkd_lm_head_workspace_bytes(int B, int H, int V) {
 }
 
 int mkd_lm_head_greedy(const void* hidden, const void* ln_f, float eps, const void* lm_head_packed,
-                       int B, int H, int V, float* logits, int* next_tokens, void* workspace,
-                       size_t workspace_bytes, void* stream) {
+                       int B, int H, int V, int hidden_actual, int norm_order, float* logits,
+                       int* next_tokens, void* workspace, size_t workspace_bytes, void* stream) {
   if (int rc = stale_check("mkd_lm_head_greedy")) return rc;
   MKD_REQUIRE(hidden && ln_f && lm_head_packed && logits && next_tokens && workspace, MKD_ERR_NULL,
               "lm_head: null pointer");
@@ -858,8 +889,10 @@ int mkd_lm_head_greedy(const void* hidden, const void* ln_f, float eps, const vo
   int* si = c.take<int>((size_t)B * 64);
   MKD_REQUIRE(c.ok, MKD_ERR_WORKSPACE, "lm_head: workspace %zu < %zu bytes", workspace_bytes, c.used);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  MKD_TRY(rmsnorm_launch(hidden, 0, static_cast<const uint16_t*>(ln_f), n, nullptr, B, H, H, H, eps,
-                         2, s), "final norm");
+  MKD_REQUIRE(norm_order == 1 || norm_order == 2, MKD_ERR_INVALID, "lm_head: norm_order %d", norm_order);
+  MKD_REQUIRE(hidden_actual <= H, MKD_ERR_INVALID, "lm_head: hidden_actual %d > H %d", hidden_actual, H);
+  MKD_TRY(rmsnorm_launch(hidden, 0, static_cast<const uint16_t*>(ln_f), n, nullptr, B, H, H,
+                         hidden_actual > 0 ? hidden_actual : H, eps, norm_order, s), "final norm");
   GemmArgs a = dense_args(lm_head_packed, n, H, V, H, B, logits, V);
   {
     const int ps = prof_begin(MKD_KCLASS_LM_HEAD, s);

@@ -60,7 +60,7 @@ MKD_DEV void gemm_finish(const GemmArgs& a, f32x4_t (&acc)[RB][TN], int lane, in
     const int nv = min(4, ncol - n0);               // valid columns of this lane
     if (nv <= 0) continue;
     const bool vec = (nv == 4) && ((a.ldy & 3) == 0);
-    if (a.bias) {
+    if (a.bias && kblk == 0) {   // split-K: the bias goes into partial 0 only
       const uint16_t* bp = a.bias + (a.grp_expert ? (long long)a.grp_expert[group] * a.bias_group_stride : 0);
 #pragma unroll
       for (int r = 0; r < RB; ++r)

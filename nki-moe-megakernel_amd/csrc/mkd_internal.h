@@ -150,6 +150,11 @@ struct AttnArgs {
   // derived from pos through the table when write_pos is null.  null = flat.
   const int* block_table;
   int tbl_stride, blk_len, num_blocks;
+  // sliding window W > 0 (flat cache of W rows used as a ring): the prior
+  // positions attended are the min(pos, W-1) filled rows and the new row goes
+  // to row pos % (W-1) -- the GPT-OSS SWA layers (gpt_oss_with_megakernel.py:
+  // 669-671, transformer_gpt_oss.py:139-205).  0 = full attention.
+  int window;
 };
 // rope_mode: 0 none, 1 cos/sin tables, 2 from pos and inv_freq
 hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s);

@@ -310,7 +310,7 @@ class Qwen3MoeMegakernelModel(nn.Module):
                               B, H, self.embed_tokens.shape[0], s), "embed")
         self.decode_layers(hidden, position_ids)
         L.check(lib.mkd_lm_head_greedy(hidden.data_ptr(), self.ln_f.data_ptr(), self.cfg.rms_norm_eps,
-                                       self.lm_head_packed.data_ptr(), B, H, self.cfg.vocab_size,
+                                       self.lm_head_packed.data_ptr(), B, H, self.cfg.vocab_size, H, 2,
                                        logits.data_ptr(), next_tokens.data_ptr(),
                                        self.lm_ws.data_ptr(), self.lm_ws.numel(), s), "lm_head")
         return next_tokens

@@ -556,3 +556,130 @@ def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
     if bias_out is not None:
         o = o + bias_out.float().reshape(1, -1)
     return o, K_cache, V_cache
+
+
+# ---------------------------------------------------------------------------
+# GPT-OSS decoder layer, stock-kernel flow (megakernels/gpt_oss/
+# transformer_gpt_oss.py:239-522; HF semantics modeling_gpt_oss.py)
+# ---------------------------------------------------------------------------
+@dataclass
+class GptOssShape:
+    H: int = 2880            # actual hidden size (the kernel pads to 3072)
+    nq: int = 64
+    nkv: int = 8
+    d: int = 64
+    E: int = 32
+    K: int = 4
+    I: int = 2880
+    eps: float = 1e-5
+    alpha: float = 1.702
+    limit: float = 7.0
+
+
+@dataclass
+class GptOssLayer:
+    """HF-layout weights: q/k/v/o [out, in] with biases, sinks [nq], router [E, H] +
+    bias, experts gate_up [E, H, 2I] with gate / up columns INTERLEAVED (HF
+    modeling_gpt_oss.py:83), gate_up_b [E, 2I] interleaved, down [E, I, H], down_b [E, H]."""
+    wq: torch.Tensor
+    bq: torch.Tensor
+    wk: torch.Tensor
+    bk: torch.Tensor
+    wv: torch.Tensor
+    bv: torch.Tensor
+    wo: torch.Tensor
+    bo: torch.Tensor
+    sinks: torch.Tensor
+    ln_in: torch.Tensor
+    ln_post: torch.Tensor
+    router_w: torch.Tensor
+    router_b: torch.Tensor
+    gate_up: torch.Tensor
+    gate_up_b: torch.Tensor
+    down: torch.Tensor
+    down_b: torch.Tensor
+
+
+def gpt_oss_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Contiguous-halves rotation (HF _apply_rotary_emb): cos/sin [B, d/2] (already
+    carrying YaRN's attention scaling) broadcast over heads; x [B, heads, d]."""
+    h = x.shape[-1] // 2
+    c, s = cos[:, None, :], sin[:, None, :]
+    x1, x2 = x[..., :h], x[..., h:]
+    return torch.cat([x1 * c - x2 * s, x2 * c + x1 * s], -1)
+
+
+def gpt_oss_decoder_layer(x_bf: torch.Tensor, lw: GptOssLayer, k_cache: torch.Tensor,
+                          v_cache: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+                          pos: torch.Tensor, window: int, shape: GptOssShape,
+                          mx_experts: bool = False, emulate_bf16: bool = True):
+    """One decode token per sequence; residual in bf16 (transformer_gpt_oss.py:358-519).
+
+    x [B, H] (bf16 values, unpadded H); caches [B, nkv, S, d] bf16, updated in
+    place; cos/sin [B, d/2] fp32.  Full layers attend positions [0, pos) plus the
+    new token; sliding layers (window W) hold a ring of W rows and attend its
+    min(pos, W-1) filled rows plus the new token, the new row going to
+    pos % (W-1) (gpt_oss_with_megakernel.py:669-671; masks :67-205).
+    RMSNorm is rmsnorm_tkg's (x*g)*rsqrt(mean + eps) (rmsnorm_tkg.py:318-454),
+    output bf16; q/k/v rounded to bf16 after RoPE (they are stored as bf16);
+    softmax with the sink logit in the denominator (HF eager_attention_forward);
+    router: biased logits, top-k, softmax over the top-k (router_topk.py:868-887;
+    HF GptOssTopKRouter); experts: gate <= 7, up in [-7, 7], (up + 1) *
+    gate * sigmoid(1.702 gate) -> bf16, down + bias, * routing weight, fp32 sum
+    over k (HF GptOssExperts).  mx_experts: the expert weights given are
+    dequantised MX and the activations go through MXFP8 before each projection
+    (as moe_tkg_mx).  emulate_bf16=False drops every bf16 rounding point (the
+    plain fp32 math the HF pin checks).  Returns (x_out [B, H], aux).
+    """
+    bf = lambda t: _bf(t, emulate_bf16)
+    B, H = x_bf.shape
+    x = x_bf.float()
+    h = bf(rmsnorm_tkg(x, lw.ln_in, shape.eps))
+    q = (h @ lw.wq.float().t() + lw.bq.float()).reshape(B, shape.nq, shape.d)
+    k = (h @ lw.wk.float().t() + lw.bk.float()).reshape(B, shape.nkv, shape.d)
+    v = (h @ lw.wv.float().t() + lw.bv.float()).reshape(B, shape.nkv, shape.d)
+    q = bf(gpt_oss_rope(q, cos, sin))
+    k = bf(gpt_oss_rope(k, cos, sin))
+    v = bf(v)
+    gq = shape.nq // shape.nkv
+    scale = shape.d ** -0.5
+    attn = torch.zeros(B, shape.nq, shape.d)
+    for b in range(B):
+        p = int(pos[b])
+        prior = min(p, window - 1) if window else p
+        for g in range(shape.nkv):
+            keys = torch.cat([k_cache[b, g, :prior].float(), k[b, g][None]], 0)
+            vals = torch.cat([v_cache[b, g, :prior].float(), v[b, g][None]], 0)
+            for j in range(gq):
+                hq = g * gq + j
+                sc = (keys @ q[b, hq]) * scale
+                sink = lw.sinks[hq].float()
+                m = torch.maximum(sc.max(), sink)
+                e = torch.exp(sc - m)
+                attn[b, hq] = (e / (e.sum() + torch.exp(sink - m))) @ vals
+    for b in range(B):                                   # KV scatter after attention
+        p = int(pos[b])
+        row = p % (window - 1) if window else p
+        k_cache[b, :, row] = k[b].to(k_cache.dtype)
+        v_cache[b, :, row] = v[b].to(v_cache.dtype)
+    o = bf(bf(attn.reshape(B, -1)) @ lw.wo.float().t() + lw.bo.float())
+    r = bf(x + o)
+    n = bf(rmsnorm_tkg(r, lw.ln_post, shape.eps))
+    logits = n @ lw.router_w.float().t() + lw.router_b.float()
+    top, idx = stable_topk(logits, shape.K)
+    w = torch.softmax(top, -1)
+    xin = mx_qdq(n) if mx_experts else n
+    moe = torch.zeros(B, H)
+    for b in range(B):
+        for j in range(shape.K):
+            e = int(idx[b, j])
+            gu = xin[b] @ lw.gate_up[e].float() + lw.gate_up_b[e].float()
+            gate = torch.clamp(gu[0::2], max=shape.limit)
+            up = torch.clamp(gu[1::2], -shape.limit, shape.limit)
+            hh = bf((up + 1) * (gate * torch.sigmoid(gate * shape.alpha)))
+            if mx_experts:
+                hh = mx_qdq(hh[None])[0]
+            y = hh @ lw.down[e].float() + lw.down_b[e].float()
+            moe[b] += w[b, j] * y
+    out = bf(r + bf(moe))
+    return out, {"h": h, "r": r, "n": n, "logits": logits, "idx": idx, "w": w, "moe": moe}

@@ -612,3 +612,82 @@ def test_decode_step_two_layers_greedy(mk, dev):
     for b in range(B):
         if (top2[b, 0] - top2[b, 1]).item() > 1e-2 * lg_ref[b].abs().max().item():
             assert int(nxt[b]) == int(nxt_ref[b])
+
+
+# ---------------------------------------------------------------- GPT-OSS layer
+def _dequant_mx_torch(codes, scales, fmt, k):
+    """Independent dequantiser for the test: element value table x 2^(scale-127)."""
+    import numpy as np
+    from oracle import mx as omx
+    if fmt == "e2m1":
+        tab = torch.from_numpy(omx.decode_elements(np.arange(16, dtype=np.uint8), "e2m1")).float()
+        c = codes.long()
+        vals = torch.stack([tab[c & 15], tab[c >> 4]], -1).reshape(*codes.shape[:-1], -1)
+    else:
+        tab = torch.from_numpy(np.nan_to_num(omx.decode_elements(np.arange(256, dtype=np.uint8), "e4m3"))).float()
+        vals = tab[codes.long()]
+    vals = vals[..., :k]
+    sc = torch.exp2(scales[..., : k // 32].float() - 127).repeat_interleave(32, -1)
+    return vals * sc
+
+
+@pytest.mark.parametrize("sliding,fmt,B", [(True, "bf16", 3), (False, "mxfp4", 2), (True, "mxfp4", 2)])
+def test_gpt_oss_layer_teacher_forced(mk, dev, sliding, fmt, B):
+    """GPT-OSS-20B layer shape (H 2880 padded to 3072, 64/8 heads, d 64, sinks,
+    sliding window 128 ring or full cache, biases, router top-4 on logits, clamped
+    Swish experts; E reduced to 8 to keep the oracle quick) vs the HF-pinned oracle."""
+    from nki_moe_megakernel_amd import gpt_oss_with_megakernel as G
+    from nki_moe_megakernel_amd import mx
+    cfg = G.GptOssMKConfig(num_hidden_layers=1, num_experts=8, max_batch=B, max_seq=1024,
+                           expert_format=fmt, first_sliding=sliding)
+    hf = G.random_layer_hf(cfg, 0, 3, "cpu")
+    g = torch.Generator().manual_seed(B * 11 + int(sliding))
+    pos = torch.tensor([50, 300, 127][:B] if sliding else [700, 5, 1023][:B], dtype=torch.int32)
+    rows = 128 if sliding else 1024
+    x = bf(torch.randn(B, cfg.hidden_size, generator=g))
+    kc = bf(torch.randn(B, 8, rows, 64, generator=g))
+    vc = bf(torch.randn(B, 8, rows, 64, generator=g))
+    layers = [G.pack_layer({k: v.to(dev) for k, v in hf.items()}, cfg)]
+    model = G.GptOssMegakernelModel(cfg, layers, B, dev)
+    model.kv_mgr.k(0).copy_(kc.to(dev))
+    model.kv_mgr.v(0).copy_(vc.to(dev))
+    xp = torch.zeros(B, cfg.hidden_pad, dtype=torch.bfloat16)
+    xp[:, : cfg.hidden_size] = x
+    y = xp.to(dev).contiguous()
+    model.decode_layers(y, pos.to(dev))
+    yc = y.cpu()
+    assert torch.equal(yc[:, cfg.hidden_size:], torch.zeros(B, cfg.hidden_pad - cfg.hidden_size, dtype=torch.bfloat16))
+    # oracle
+    from oracle import ref
+    lw = ref.GptOssLayer(
+        wq=hf["q_proj.weight"], bq=hf["q_proj.bias"], wk=hf["k_proj.weight"], bk=hf["k_proj.bias"],
+        wv=hf["v_proj.weight"], bv=hf["v_proj.bias"], wo=hf["o_proj.weight"], bo=hf["o_proj.bias"],
+        sinks=hf["sinks"], ln_in=hf["input_layernorm"], ln_post=hf["post_attention_layernorm"],
+        router_w=hf["router.weight"], router_b=hf["router.bias"], gate_up=hf["experts.gate_up_proj"],
+        gate_up_b=hf["experts.gate_up_proj_bias"], down=hf["experts.down_proj"],
+        down_b=hf["experts.down_proj_bias"])
+    if fmt != "bf16":
+        c = G.convert_layer({k: v.to(dev) for k, v in hf.items()}, cfg)
+        E, N2, Hp = c["gate_up"].shape
+        I = N2 // 2
+        gc, gs = mx.quantize_mx(c["gate_up"].reshape(E * N2, Hp), 2, Hp)
+        rows_deq = _dequant_mx_torch(gc.cpu(), gs.cpu(), "e2m1", Hp).reshape(E, N2, Hp)[:, :, : cfg.hidden_size]
+        gu = torch.empty(E, cfg.hidden_size, N2)
+        gu[:, :, 0::2] = rows_deq[:, :I].transpose(1, 2)
+        gu[:, :, 1::2] = rows_deq[:, I:].transpose(1, 2)
+        lw.gate_up = gu
+        dc, ds = mx.quantize_mx(c["down"].reshape(E * Hp, I), 2, (I + 127) // 128 * 128)
+        dn = _dequant_mx_torch(dc.cpu(), ds.cpu(), "e2m1", I).reshape(E, Hp, I)[:, : cfg.hidden_size]
+        lw.down = dn.transpose(1, 2).contiguous()
+    cos, sin = model.rope_cos_sin(pos.to(dev))
+    y_ref, aux = ref.gpt_oss_decoder_layer(
+        x, lw, kc.clone(), vc.clone(), cos[:, :32].cpu(), sin[:, :32].cpu(), pos,
+        128 if sliding else 0, ref.GptOssShape(E=8), mx_experts=(fmt != "bf16"))
+    err = max_abs_rel(yc[:, : cfg.hidden_size], y_ref)
+    assert err < (5e-2 if fmt != "bf16" else TOL), err
+    # the new rows: sliding layers write the ring row pos % 127
+    kn = model.kv_mgr.k(0).cpu()
+    for b in range(B):
+        row = int(pos[b]) % 127 if sliding else int(pos[b])
+        changed = (kn[b] != kc[b]).any(-1).any(0).nonzero().flatten().tolist()
+        assert changed in ([row], [])

@@ -349,3 +349,68 @@ def test_block_kv_gather_identity_and_permutation():
     flat = ref.block_kv_to_flat(cache, perm)
     assert torch.equal(flat[0, :4], cache[5]) and torch.equal(flat[0, 4:], cache[0])
     assert torch.equal(flat[1, :4], torch.zeros(4, 3)) and torch.equal(flat[1, 4:], cache[2])
+
+
+@pytest.mark.parametrize("pos,window", [(5, 0), (11, 8), (3, 8)])
+def test_gpt_oss_layer_oracle_matches_hf(pos, window):
+    """oracle.ref.gpt_oss_decoder_layer (fp32, no bf16 rounding) == HF
+    GptOssDecoderLayer on the last token of a causal (optionally sliding-window)
+    prefill, with the decode oracle's KV cache built from the earlier tokens
+    (ring rows t % (W-1) for a sliding layer)."""
+    from transformers import GptOssConfig
+    from transformers.models.gpt_oss import modeling_gpt_oss as M
+    from oracle import ref
+    torch.manual_seed(pos * 10 + window)
+    H, nq, nkv, d, E, K, I = 128, 4, 2, 32, 4, 2, 64
+    cfg = GptOssConfig(hidden_size=H, num_attention_heads=nq, num_key_value_heads=nkv, head_dim=d,
+                       num_local_experts=E, num_experts_per_tok=K, intermediate_size=I,
+                       num_hidden_layers=2, sliding_window=window or 8,
+                       layer_types=["sliding_attention" if window else "full_attention"] * 2,
+                       rms_norm_eps=1e-5, attn_implementation="eager")
+    layer = M.GptOssDecoderLayer(cfg, 0).float().eval()
+    with torch.no_grad():
+        for p_ in layer.parameters():
+            p_.copy_(0.1 * torch.randn_like(p_))
+        layer.input_layernorm.weight.add_(1.0)
+        layer.post_attention_layernorm.weight.add_(1.0)
+    rot = M.GptOssRotaryEmbedding(cfg)
+    S = pos + 1
+    X = torch.randn(1, S, H)
+    ids = torch.arange(S)[None]
+    cos, sin = rot(X, ids)
+    # HF causal (+ sliding) mask for the prefill, additive
+    mask = torch.full((S, S), float("-inf"))
+    for i in range(S):
+        for j in range(S):
+            if j <= i and (not window or i - j < window):
+                mask[i, j] = 0.0
+    with torch.no_grad():
+        y_hf = layer(X, attention_mask=mask[None, None], position_ids=ids,
+                     position_embeddings=(cos, sin))
+        y_hf = y_hf[0] if isinstance(y_hf, tuple) else y_hf
+    a = layer.self_attn
+    lw = ref.GptOssLayer(
+        wq=a.q_proj.weight.data, bq=a.q_proj.bias.data, wk=a.k_proj.weight.data, bk=a.k_proj.bias.data,
+        wv=a.v_proj.weight.data, bv=a.v_proj.bias.data, wo=a.o_proj.weight.data, bo=a.o_proj.bias.data,
+        sinks=a.sinks.data, ln_in=layer.input_layernorm.weight.data,
+        ln_post=layer.post_attention_layernorm.weight.data,
+        router_w=layer.mlp.router.weight.data, router_b=layer.mlp.router.bias.data,
+        gate_up=layer.mlp.experts.gate_up_proj.data, gate_up_b=layer.mlp.experts.gate_up_proj_bias.data,
+        down=layer.mlp.experts.down_proj.data, down_b=layer.mlp.experts.down_proj_bias.data)
+    shape = ref.GptOssShape(H=H, nq=nq, nkv=nkv, d=d, E=E, K=K, I=I)
+    # decode cache from tokens 0..pos-1: rmsnorm -> k/v proj (+bias) -> RoPE
+    rows = window if window else S
+    kc = torch.zeros(1, nkv, rows, d)
+    vc = torch.zeros(1, nkv, rows, d)
+    for t in range(pos):
+        h = ref.rmsnorm_tkg(X[0, t][None], lw.ln_in, shape.eps)
+        k = (h @ lw.wk.t() + lw.bk).reshape(1, nkv, d)
+        v = (h @ lw.wv.t() + lw.bv).reshape(1, nkv, d)
+        k = ref.gpt_oss_rope(k, cos[0, t][None, : d // 2], sin[0, t][None, : d // 2])
+        r = t % (window - 1) if window else t
+        kc[0, :, r] = k[0]
+        vc[0, :, r] = v[0]
+    y, _ = ref.gpt_oss_decoder_layer(X[0, pos][None], lw, kc, vc, cos[0, pos][None, : d // 2],
+                                     sin[0, pos][None, : d // 2], torch.tensor([pos]), window, shape,
+                                     emulate_bf16=False)
+    torch.testing.assert_close(y[0], y_hf[0, pos], rtol=2e-5, atol=2e-5)
