@@ -61,13 +61,30 @@ def build_model(Q, cfg, B, dev, seed):
     return model
 
 
+def build_gpt_oss(G, cfg, B, dev, seed):
+    import torch
+    layers = []
+    for l in range(cfg.num_hidden_layers):
+        hf = G.random_layer_hf(cfg, l, seed, dev)
+        layers.append(G.pack_layer(hf, cfg))
+        del hf
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 1)
+    emb = (0.02 * torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g, device=dev)).to(torch.bfloat16)
+    lm = (0.02 * torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g, device=dev)).to(torch.bfloat16)
+    lnf = (1 + 0.02 * torch.randn(cfg.hidden_size, generator=g, device=dev)).to(torch.bfloat16)
+    model = G.GptOssMegakernelModel(cfg, layers, B, dev, embed=emb, ln_f=lnf, lm_head=lm)
+    del lm, emb
+    return model
+
+
 def prefill_kv(model, cfg, ctx, seed, dev):
     import torch
     g = torch.Generator(device=dev)
     g.manual_seed(seed + 2)
     for l in range(cfg.num_hidden_layers):
         for t in (model.kv_mgr.k(l), model.kv_mgr.v(l)):
-            if cfg.kv_block_len:          # block pool: every row random
+            if getattr(cfg, "kv_block_len", 0) or t.shape[2] < ctx:   # block pool / ring: every row
                 t.copy_(torch.randn(t.shape, generator=g, device=dev))
             else:
                 t[:, :, :ctx].copy_(torch.randn(t[:, :, :ctx].shape, generator=g, device=dev))
@@ -147,6 +164,59 @@ def cpu_baseline(cfg, lens, seconds_budget=20.0):
                       f"{t_total:.1f} s on {cores} host threads"}
 
 
+def cpu_baseline_gpt_oss(cfg, lens, seconds_budget=20.0):
+    """Time the CPU oracle's GPT-OSS decode layers (bf16 experts, same batch and KV
+    lengths, 2 distinct layers' weights reused); a pass over a bounded number of
+    layers is scaled to all layers (said in `sample`)."""
+    import torch
+    from oracle import ref
+    from importlib import import_module
+    G = import_module("nki_moe_megakernel_amd.gpt_oss_with_megakernel")
+    torch.set_num_threads(os.cpu_count() or 1)
+    cores = torch.get_num_threads()
+    B = int(lens.numel())
+    hfs = [G.random_layer_hf(cfg, l, 77, "cpu") for l in range(2)]
+    lws = [ref.GptOssLayer(
+        wq=h["q_proj.weight"], bq=h["q_proj.bias"], wk=h["k_proj.weight"], bk=h["k_proj.bias"],
+        wv=h["v_proj.weight"], bv=h["v_proj.bias"], wo=h["o_proj.weight"], bo=h["o_proj.bias"],
+        sinks=h["sinks"], ln_in=h["input_layernorm"], ln_post=h["post_attention_layernorm"],
+        router_w=h["router.weight"], router_b=h["router.bias"], gate_up=h["experts.gate_up_proj"],
+        gate_up_b=h["experts.gate_up_proj_bias"], down=h["experts.down_proj"],
+        down_b=h["experts.down_proj_bias"]) for h in hfs]
+    g = torch.Generator().manual_seed(5)
+    S = int(lens.max()) + 64
+    caches = []
+    for l in range(2):
+        rows = cfg.sliding_window if cfg.is_sliding(l) else S
+        caches.append((torch.randn(B, cfg.num_key_value_heads, rows, cfg.head_dim, generator=g).to(torch.bfloat16),
+                       torch.randn(B, cfg.num_key_value_heads, rows, cfg.head_dim, generator=g).to(torch.bfloat16)))
+    inv, scl = G.yarn_inv_freq(cfg)
+    freqs = lens.reshape(-1, 1).float() * inv[None, :]
+    cos, sin = freqs.cos() * scl, freqs.sin() * scl
+    shape = ref.GptOssShape(H=cfg.hidden_size, nq=cfg.num_attention_heads, nkv=cfg.num_key_value_heads,
+                            d=cfg.head_dim, E=cfg.num_experts, K=cfg.num_experts_per_tok,
+                            I=cfg.intermediate_size, eps=cfg.rms_norm_eps)
+    x = torch.randn(B, cfg.hidden_size, generator=g).to(torch.bfloat16).float()
+    L = cfg.num_hidden_layers
+    n, t_layers = 0, 0.0
+    while n < L and (n < 2 or t_layers < seconds_budget):
+        j = n % 2
+        t0 = time.perf_counter()
+        x, _ = ref.gpt_oss_decoder_layer(x, lws[j], caches[j][0], caches[j][1], cos, sin, lens,
+                                         cfg.sliding_window if cfg.is_sliding(j) else 0, shape)
+        t_layers += time.perf_counter() - t0
+        n += 1
+    lm = (0.02 * torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g)).to(torch.bfloat16)
+    t0 = time.perf_counter()
+    ref.final_norm_lm_head(x, torch.ones(cfg.hidden_size, dtype=torch.bfloat16), lm, cfg.rms_norm_eps)
+    t_lm = time.perf_counter() - t0
+    step_s = t_layers * L / n + t_lm
+    return {"value": B / step_s, "unit": "tok/s", "cores": cores, "kind": "port",
+            "sample": f"{n} of {L} GPT-OSS layers at bs={B} of the fp32 torch oracle (bf16 experts), "
+                      f"scaled by {L}/{n}, + lm_head; KV lengths mean {float(lens.float().mean()):.0f}; "
+                      f"{t_layers + t_lm:.1f} s on {cores} host threads"}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -166,6 +236,9 @@ def main():
                     help="expert weight format (mxfp8 at --batch 32 is configs[3])")
     ap.add_argument("--kv-block", type=int, default=0,
                     help="paged KV cache with blocks of this many positions (0: flat)")
+    ap.add_argument("--model", choices=["qwen3", "gpt-oss"], default="qwen3",
+                    help="gpt-oss: GPT-OSS-20B shape, 24 layers, MXFP4 experts (configs[4]; "
+                         "use --batch 32 --ragged --experts mxfp4)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
@@ -180,18 +253,30 @@ def main():
 
     dev = torch.device("cuda:0")
     B, ctx = args.batch, args.ctx
+    oss = args.model == "gpt-oss"
+    lo, hi = (1024, 4096) if oss else (512, 8192)
     if args.ragged:
         gl = torch.Generator().manual_seed(4321)
-        lens = torch.randint(512, 8193, (B,), generator=gl, dtype=torch.int32)
+        lens = torch.randint(lo, hi + 1, (B,), generator=gl, dtype=torch.int32)
     else:
         lens = torch.full((B,), ctx, dtype=torch.int32)
     S_max = ((int(lens.max()) + args.warmup + args.steps + 8 + 127) // 128) * 128
     if args.kv_block:
         S_max = (S_max + args.kv_block - 1) // args.kv_block * args.kv_block
-    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=args.layers, max_batch=B, max_seq=S_max,
-                             expert_format=args.experts, kv_block_len=args.kv_block)
     t0 = time.time()
-    model = build_model(Q, cfg, B, dev, seed=1234)
+    if oss:
+        from nki_moe_megakernel_amd import gpt_oss_with_megakernel as G
+        if args.kv_block:
+            raise SystemExit("--kv-block applies to the qwen3 model only")
+        cfg = G.GptOssMKConfig(num_hidden_layers=24 if args.layers == 48 else args.layers,
+                               max_batch=B, max_seq=S_max, expert_format=args.experts)
+        model = build_gpt_oss(G, cfg, B, dev, seed=1234)
+        width = cfg.hidden_pad
+    else:
+        cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=args.layers, max_batch=B, max_seq=S_max,
+                                 expert_format=args.experts, kv_block_len=args.kv_block)
+        model = build_model(Q, cfg, B, dev, seed=1234)
+        width = cfg.hidden_size
     prefill_kv(model, cfg, int(lens.max()), 1234, dev)
     torch.cuda.synchronize()
     log(f"model built in {time.time() - t0:.1f}s "
@@ -201,7 +286,7 @@ def main():
     g.manual_seed(99)
     ids = torch.randint(0, cfg.vocab_size, (B,), generator=g, device=dev, dtype=torch.int32)
     pos = lens.to(dev)
-    hidden = torch.empty(B, cfg.hidden_size, dtype=torch.bfloat16, device=dev)
+    hidden = torch.empty(B, width, dtype=torch.bfloat16, device=dev)
     logits = torch.empty(B, cfg.vocab_size, dtype=torch.float32, device=dev)
     nxt = torch.empty(B, dtype=torch.int32, device=dev)
     lib = L.load()
@@ -259,7 +344,8 @@ def main():
         raise RuntimeError(f"expected {n_ev} profiled gate_up launches, got {n_rec}")
     durs = [a.elapsed_time(b) for a, b in zip(ev_s, ev_e)]
     avg_ms = sum(durs) / len(durs)
-    H, I, E, K = cfg.hidden_size, cfg.moe_intermediate_size, cfg.num_experts, cfg.num_experts_per_tok
+    H, E, K = cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok
+    I = cfg.intermediate_size if oss else cfg.moe_intermediate_size
     # expected number of distinct experts a layer touches (near-uniform routing)
     distinct = E * (1 - (1 - K / E) ** B) if B > 1 else K
     # bytes per expert weight element: bf16 2; MX codes + one scale byte per 32
@@ -268,11 +354,19 @@ def main():
     achieved = alg_bytes / (avg_ms / 1e3) / 1e9
     gu_flops = 2.0 * B * K * 2 * I * H                 # one gate/up launch
     gu_tflops = gu_flops / (avg_ms / 1e3) / 1e12
-    mfma_peak = MFMA_BF16_PEAK_TFLOPS if args.experts == "bf16" else 2 * MFMA_BF16_PEAK_TFLOPS
+    # dense MFMA peaks: bf16 2.5, MXFP8 5.0, MXFP4 10.1 PFLOP/s
+    mfma_peak = {"bf16": MFMA_BF16_PEAK_TFLOPS, "mxfp8": 5000.0, "mxfp4": 10100.0}[args.experts]
     # whole-step algorithmic bytes (weights + KV read + lm_head) for reference
     attn_b = 2 * H * (cfg.num_attention_heads + 2 * cfg.num_key_value_heads) * cfg.head_dim + \
         2 * cfg.num_attention_heads * cfg.head_dim * H
-    kv_b = 2 * cfg.num_key_value_heads * cfg.head_dim * 2 * float((lens.float() + args.steps / 2).sum())
+    kv_row = 2 * cfg.num_key_value_heads * cfg.head_dim * 2       # K + V bytes per position
+    kv_full = kv_row * float((lens.float() + args.steps / 2).sum())
+    if oss:   # sliding layers read at most window - 1 prior rows
+        kv_win = kv_row * float((lens.float() + args.steps / 2).clamp(max=cfg.sliding_window - 1).sum())
+        n_win = sum(cfg.is_sliding(l) for l in range(cfg.num_hidden_layers))
+        kv_b = (n_win * kv_win + (cfg.num_hidden_layers - n_win) * kv_full) / cfg.num_hidden_layers
+    else:
+        kv_b = kv_full
     layer_b = attn_b + 2 * E * H + distinct * 3 * H * I * wbytes + kv_b
     step_b = cfg.num_hidden_layers * layer_b + 2 * H * cfg.vocab_size
     step_gbs = step_b / (ms_step / 1e3) / 1e9
@@ -280,7 +374,8 @@ def main():
     cpu = None
     if not args.no_cpu:
         try:
-            cpu = cpu_baseline(cfg, lens, args.cpu_seconds)
+            cpu = cpu_baseline_gpt_oss(cfg, lens, args.cpu_seconds) if oss else \
+                cpu_baseline(cfg, lens, args.cpu_seconds)
         except Exception as e:  # report, never fail the GPU number on it
             log(f"cpu baseline failed: {e!r}")
     log(f"step {ms_step:.3f} ms ({tok_s:.1f} tok/s), wall {wall:.2f}s; whole-step algorithmic "
@@ -295,7 +390,7 @@ def main():
                 (f", experts quantised to {args.experts}" if args.experts != "bf16" else "") +
                 ", KV N(0,1), uniform token ids)",
         "config": {"workload": workload_name(cfg, B, ctx, lens, args),
-                   "batch": B, "kv_context": ctx if not args.ragged else "U[512,8192]",
+                   "batch": B, "kv_context": ctx if not args.ragged else f"U[{lo},{hi}]",
                    "kv_lengths_mean": round(float(lens.float().mean()), 1),
                    "layers": cfg.num_hidden_layers, "experts": args.experts,
                    "kv_block": args.kv_block,
@@ -311,7 +406,8 @@ def main():
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers)
-                     if (args.experts == "bf16" and not args.ragged and not args.kv_block) else None,
+                     if (args.model == "qwen3" and args.experts == "bf16" and not args.ragged
+                         and not args.kv_block) else None,
                      "avg_us": round(avg_ms * 1e3, 2), "bytes_per_launch": int(alg_bytes)},
         "cpu_baseline": cpu,
     }
@@ -327,8 +423,8 @@ REF_TOK_S_BS1 = 122.7
 
 
 def vs_baseline(tok_s, cfg, B, ctx, args):
-    if (args.experts == "bf16" and not args.ragged and B == 1 and ctx == 2048
-            and cfg.num_hidden_layers == 48 and not args.kv_block):
+    if (args.model == "qwen3" and args.experts == "bf16" and not args.ragged and B == 1
+            and ctx == 2048 and cfg.num_hidden_layers == 48 and not args.kv_block):
         return round(tok_s / REF_TOK_S_BS1, 3)
     return None
 
@@ -344,6 +440,11 @@ def workload_name(cfg, B, ctx, lens, args):
         tag = " (BASELINE configs[2])"
     elif args.experts == "mxfp8" and B == 32:
         tag = " (BASELINE configs[3] expert format)"
+    if args.model == "gpt-oss":
+        kv = kv.replace("U[512,8192]", "U[1024,4096]")
+        tag = " (BASELINE configs[4])" if (B == 32 and args.experts == "mxfp4" and args.ragged) else ""
+        return (f"GPT-OSS-20B-shaped {cfg.num_hidden_layers}-layer greedy decode (sliding-window 128 / "
+                f"full alternating, sinks), bs={B}, {kv}, {args.experts} experts{tag}")
     return (f"Qwen3-30B-A3B-shaped {cfg.num_hidden_layers}-layer greedy decode, bs={B}, {kv}, "
             f"{args.experts} experts{tag}")
 
