@@ -29,13 +29,16 @@
 //     to the chunk's slot of part_ml / part_o; the chunk holding position
 //     n_prior[b] also stages the new k / v rows for the scatter.
 // attn_combine_kernel, grid (q head, sequence), block = 4 waves: log-sum-exp
-//  merge of the chunks (waves take every 4th chunk, LDS reduce), optional sink
-//  logit, bf16 output; the blocks of the first head of each kv group then
-//  scatter the new k / v rows into the caches at write_pos[b] -- after every
-//  chunk has read the cache, because the kernels run in stream order.
+//  merge of the chunks (waves take every 4th chunk, online rescaling, LDS
+//  reduce), optional sink logit, bf16 output; the blocks of the first head of
+//  each kv group then scatter the new k / v rows into the caches at
+//  write_pos[b] -- after every chunk has read the cache, because the kernels
+//  run in stream order.
 //  (A single kernel with a last-arriving-block combine was measured slower:
 //  the device-scope fence and the counter atomic cost ~9 us per block on
 //  this part, more than a kernel boundary.)
+// Both kernels issue their independent global loads (cache rows, partials)
+// before the dependent math so that one memory latency covers them.
 #include "common.h"
 #include "mkd_internal.h"
 
@@ -50,64 +53,95 @@ MKD_DEV f32x4_t mfma16x16x16(uint2 a, uint2 b, f32x4_t c) {
 
 // One wave: head `head` of sequence b (kind 0 query, 1 key, 2 value) from the
 // fp32 / bf16 projections to bf16 bits (attention_block_tkg.py:915-1138; Qwen
-// rounding attn_fused_nki.py:393-398, 426-446, 494-498, 543-582).  Split into
-// load and finish so a wave can issue the loads of all its heads first.
+// rounding attn_fused_nki.py:393-398, 426-446, 494-498, 543-582).  Lane l < D/2
+// holds elements l and l + D/2 -- the pair that rotate-half RoPE mixes -- so
+// the rotation stays inside the lane; lanes >= D/2 (D = 64) hold zeros.  Split
+// into load and finish so a wave can issue the loads of all its heads first.
 template <int D>
 struct HeadPrep {
-  static constexpr int EL = D / 64;        // elements per lane
-  float x[EL], nw[EL], cs[EL], sn[EL];
+  static constexpr int HD = D / 2;
+  // raw loads (converted in finish, so that a wave's loads for all its heads
+  // are in flight together: a conversion inside a conditional would make the
+  // compiler wait for each load where it is issued)
+  uint32_t xr[2], nr[2];
+  float cs[2], sn[2], invf[2];
+  int posr;
+  bool f32, has_nw, rope_tab;
+  long long off0;
   MKD_DEV void load(const AttnArgs& a, int rope_mode, int b, int head, int kind, int lane) {
+    f32 = a.qkv != nullptr;
+    const char* src = f32 ? reinterpret_cast<const char*>(a.qkv)
+                          : reinterpret_cast<const char*>(a.qkv_bf16);
+    // pointers that may be absent fall back to the start of the projection
+    // buffer (>= 3 * D elements), whose values are then discarded
     const uint16_t* nwp = kind == 0 ? a.q_norm : (kind == 1 ? a.k_norm : nullptr);
+    has_nw = nwp != nullptr;
+    if (!has_nw) nwp = reinterpret_cast<const uint16_t*>(src);
+    rope_tab = kind < 2 && rope_mode == 1;
+    const float* cp = rope_tab ? a.cos + (long long)b * D : reinterpret_cast<const float*>(src);
+    const float* sp = rope_tab ? a.sin + (long long)b * D : reinterpret_cast<const float*>(src);
+    const int l = lane < HD ? lane : 0;
+    off0 = (long long)b * a.ld_qkv + head * D + l;
 #pragma unroll
-    for (int e = 0; e < EL; ++e) {
-      const int i = lane * EL + e;
-      const long long off = (long long)b * a.ld_qkv + head * D + i;
-      x[e] = a.qkv ? a.qkv[off] : bf2f(a.qkv_bf16[off]);
-      nw[e] = nwp ? bf2f(nwp[i]) : 1.f;
-      cs[e] = 1.f;
-      sn[e] = 0.f;
-      if (kind < 2 && rope_mode == 1) {
-        cs[e] = a.cos[(long long)b * D + i];
-        sn[e] = a.sin[(long long)b * D + i];
-      } else if (kind < 2 && rope_mode == 2) {   // from the position: pos * inv_freq[i mod D/2]
-        const float ang = (float)a.pos[b] * a.inv_freq[i % (D / 2)];
+    for (int e = 0; e < 2; ++e) {
+      const int i = l + e * HD;
+      const long long off = off0 + e * HD;
+      // one aligned dword: the fp32 element, or the pair holding the bf16 one
+      xr[e] = *reinterpret_cast<const uint32_t*>(src + ((off << (f32 ? 2 : 1)) & ~3LL));
+      nr[e] = nwp[i];
+      cs[e] = cp[i];
+      sn[e] = sp[i];
+    }
+    if (kind < 2 && rope_mode == 2) {   // from the position: pos * inv_freq[i mod D/2]
+      posr = a.pos[b];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) invf[e] = a.inv_freq[l];
+    }
+  }
+  float x[2], nw[2];
+  MKD_DEV void convert(int rope_mode, int kind, int lane) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const long long off = off0 + e * HD;
+      const uint32_t h16 = (off & 1) ? (xr[e] >> 16) : (xr[e] & 0xffffu);
+      x[e] = lane < HD ? (f32 ? __uint_as_float(xr[e]) : bf2f(h16)) : 0.f;
+      nw[e] = has_nw ? bf2f(nr[e]) : 1.f;
+      if (!rope_tab) { cs[e] = 1.f; sn[e] = 0.f; }
+      if (kind < 2 && rope_mode == 2) {
+        const float ang = (float)posr * invf[e];
         cs[e] = cosf(ang);
         sn[e] = sinf(ang);
       }
     }
   }
   MKD_DEV void finish(const AttnArgs& a, int rope_mode, int kind, uint16_t* dst, int lane) {
+    convert(rope_mode, kind, lane);
 #pragma unroll
-    for (int e = 0; e < EL; ++e)
+    for (int e = 0; e < 2; ++e)
       if (a.round_qwen) x[e] = rbf(x[e]);
     if (kind < 2) {
       if (kind == 0 ? a.q_norm != nullptr : a.k_norm != nullptr) {
-        float ss = 0.f;
-#pragma unroll
-        for (int e = 0; e < EL; ++e) ss += x[e] * x[e];
-        ss = wave_sum(ss);
+        const float ss = wave_sum(x[0] * x[0] + x[1] * x[1]);
         const float rinv = 1.0f / sqrtf(ss * (1.0f / D) + a.qk_eps);
 #pragma unroll
-        for (int e = 0; e < EL; ++e) {
+        for (int e = 0; e < 2; ++e) {
           x[e] = (x[e] * rinv) * nw[e];
           if (a.round_qwen) x[e] = rbf(x[e]);
         }
       }
       if (rope_mode) {
-        float p[EL];
+        // element i < D/2 pairs with -x[i + D/2], element i + D/2 with x[i]
+        const float rot[2] = {-x[1], x[0]};
 #pragma unroll
-        for (int e = 0; e < EL; ++e) p[e] = __shfl_xor(x[e], 32, 64);   // element i +- D/2
-#pragma unroll
-        for (int e = 0; e < EL; ++e) {
-          const int i = lane * EL + e;
-          const float rot = (i < D / 2) ? -p[e] : p[e];
-          x[e] = a.round_qwen ? rbf(rbf(x[e] * rbf(cs[e])) + rbf(rot * rbf(sn[e])))
-                              : x[e] * cs[e] + rot * sn[e];
-        }
+        for (int e = 0; e < 2; ++e)
+          x[e] = a.round_qwen ? rbf(rbf(x[e] * rbf(cs[e])) + rbf(rot[e] * rbf(sn[e])))
+                              : x[e] * cs[e] + rot[e] * sn[e];
       }
     }
-#pragma unroll
-    for (int e = 0; e < EL; ++e) dst[lane * EL + e] = (uint16_t)f2bf(x[e]);
+    if (lane < HD) {
+      dst[lane] = (uint16_t)f2bf(x[0]);
+      dst[lane + HD] = (uint16_t)f2bf(x[1]);
+    }
   }
 };
 
@@ -168,6 +202,22 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   const int chunk0 = c * CP;
   if (chunk0 >= total) return;                // whole block: uniform exit
 
+  // ---- 0. the wave's K and V rows from the cache: they depend on nothing
+  // computed here, so their loads are issued first and overlap the prep ----
+  const int dq = (lane >> 4) * (D / 4);       // lane's d range in a 16-row tile
+  const int wbase = chunk0 + w * TPW * 16;
+  u32x4_t kpre[TPW][NK], vpre[TPW][D / 32];
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int t = wbase + tt * 16 + (lane & 15);
+    const uint16_t* kr = t < n ? kv_row<D>(a, a.k_cache, b, g, t) : nullptr;
+    const uint16_t* vr = t < n ? kv_row<D>(a, a.v_cache, b, g, t) : nullptr;
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) kpre[tt][kk] = kr ? ld16(kr + dq + kk * 8) : u32x4_t{0, 0, 0, 0};
+#pragma unroll
+    for (int j = 0; j < D / 32; ++j) vpre[tt][j] = vr ? ld16(vr + dq + j * 8) : u32x4_t{0, 0, 0, 0};
+  }
+
   // ---- 1. prep of this kv group's heads: wave w takes heads w, w+4, ... of
   // [q heads of g | k of g | v of g]; all loads first, then the math ----
   constexpr int NR = (GQA + 2 + 3) / 4;
@@ -194,7 +244,6 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
 
   // q fragments (B operand): lane l -> head l%16, d = (l/16)*(D/4) + kk*8 .. +8
   const int hcol = lane & 15;
-  const int dq = (lane >> 4) * (D / 4);
   u32x4_t qf[NK];
 #pragma unroll
   for (int kk = 0; kk < NK; ++kk)
@@ -203,17 +252,14 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
 
   // ---- 2. scores for the wave's tiles ----
   float s[TPW][4];
-  const int wbase = chunk0 + w * TPW * 16;
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
     const int t = wbase + tt * 16 + (lane & 15);  // A row owned by this lane
-    const uint16_t* kr = t < n ? kv_row<D>(a, a.k_cache, b, g, t) : nullptr;
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
-      u32x4_t kf = {0, 0, 0, 0};
-      if (kr) kf = ld16(kr + dq + kk * 8);
-      else if (t == n) kf = *reinterpret_cast<const u32x4_t*>(&kn_s[dq + kk * 8]);
+      u32x4_t kf = kpre[tt][kk];
+      if (t == n) kf = *reinterpret_cast<const u32x4_t*>(&kn_s[dq + kk * 8]);
       acc = mfma16x16x32(kf, qf[kk], acc);
     }
 #pragma unroll
@@ -260,12 +306,10 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   for (int tt = 0; tt < TPW; ++tt) {
     // stage V rows of the tile: lane -> row l%16, D/4 elements at (l/16)*(D/4)
     const int t = wbase + tt * 16 + (lane & 15);
-    const uint16_t* vr = t < n ? kv_row<D>(a, a.v_cache, b, g, t) : nullptr;
 #pragma unroll
     for (int j = 0; j < D / 32; ++j) {
-      u32x4_t v = {0, 0, 0, 0};
-      if (vr) v = ld16(vr + dq + j * 8);
-      else if (t == n) v = *reinterpret_cast<const u32x4_t*>(&vn_s[dq + j * 8]);
+      u32x4_t v = vpre[tt][j];
+      if (t == n) v = *reinterpret_cast<const u32x4_t*>(&vn_s[dq + j * 8]);
       *reinterpret_cast<u32x4_t*>(vt + (lane & 15) * VS + dq + j * 8) = v;
     }
     wave_lds_sync();                          // V tile visible to the whole wave
@@ -320,12 +364,16 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
 }
 
 // Combine: block (head h, sequence b), 4 waves; wave w takes chunks w, w+4, ...
+// in batches of up to 16 whose loads are all issued before any use, with a
+// running (max, sum, O) per wave rescaled when a batch raises the max; the 4
+// wave results then merge in LDS in wave order, with the sink logit if any.
+// The new k / v rows of the scatter are loaded at the start as well.
 template <int D>
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
   constexpr int EL = D / 64;
-  __shared__ float red[4];
+  constexpr int U = 16;
+  __shared__ float m_s[4], l_s[4];
   __shared__ float acc_s[4][D];
-  __shared__ float l_s[4];
   const int h = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int CP = a.chunk;
@@ -333,64 +381,77 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
   const int nch = (n + 1 + CP - 1) / CP;
   const float* ml = a.part_ml + ((long long)b * a.nq + h) * a.n_chunks * 2;
   const float* po = a.part_o + ((long long)b * a.nq + h) * a.n_chunks * D;
-  // global max over the chunk maxima (and the sink)
-  float M = -INFINITY;
-  for (int k = threadIdx.x; k < nch; k += 256) M = fmaxf(M, ml[2 * k]);
-  M = wave_max(M);
-  if (lane == 0) red[w] = M;
-  __syncthreads();
-  M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  if (a.sink) M = fmaxf(M, a.sink[h]);
-  float acc[EL], L = 0.f;
+
+  // scatter operands: the first query head of each kv group writes that group's rows
+  const int gqa = a.nq / a.nkv;
+  const bool scatter = a.update_cache && h % gqa == 0 && threadIdx.x < D;
+  uint16_t knew = 0, vnew = 0;
+  if (scatter) {
+    const int g = h / gqa;
+    knew = a.kv_new[(((long long)b * 2 + 0) * a.nkv + g) * D + threadIdx.x];
+    vnew = a.kv_new[(((long long)b * 2 + 1) * a.nkv + g) * D + threadIdx.x];
+  }
+
+  float m = -INFINITY, L = 0.f, acc[EL];
 #pragma unroll
   for (int e = 0; e < EL; ++e) acc[e] = 0.f;
-  int k = w;
-  for (; k + 12 < nch; k += 16) {            // 4 chunks of this wave per batch
-    float mk[4], lk[4], pv[4][EL];
+  for (int k0 = w; k0 < nch; k0 += 4 * U) {
+    float mk[U], lk[U], pv[U][EL];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      mk[u] = ml[2 * (k + 4 * u)];
-      lk[u] = ml[2 * (k + 4 * u) + 1];
+    for (int u = 0; u < U; ++u) {
+      const int k = k0 + 4 * u;
+      const int kc = k < nch ? k : k0;       // in-range address; masked below
+      mk[u] = ml[2 * kc];
+      lk[u] = ml[2 * kc + 1];
 #pragma unroll
-      for (int e = 0; e < EL; ++e) pv[u][e] = po[(long long)(k + 4 * u) * D + lane * EL + e];
+      for (int e = 0; e < EL; ++e) pv[u][e] = po[(long long)kc * D + lane * EL + e];
+      if (k >= nch) mk[u] = -INFINITY;
     }
+    float bm = m;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const float wk = mk[u] == -INFINITY ? 0.f : expf(mk[u] - M);
+    for (int u = 0; u < U; ++u) bm = fmaxf(bm, mk[u]);
+    if (bm == -INFINITY) continue;           // nothing live yet (uniform)
+    const float r = (m == -INFINITY) ? 0.f : expf(m - bm);
+    L *= r;
+#pragma unroll
+    for (int e = 0; e < EL; ++e) acc[e] *= r;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float wk = mk[u] == -INFINITY ? 0.f : expf(mk[u] - bm);
       L += lk[u] * wk;
 #pragma unroll
       for (int e = 0; e < EL; ++e) acc[e] += pv[u][e] * wk;
     }
-  }
-  for (; k < nch; k += 4) {
-    const float mk = ml[2 * k];
-    const float wk = mk == -INFINITY ? 0.f : expf(mk - M);
-    L += ml[2 * k + 1] * wk;
-#pragma unroll
-    for (int e = 0; e < EL; ++e) acc[e] += po[(long long)k * D + lane * EL + e] * wk;
+    m = bm;
   }
 #pragma unroll
   for (int e = 0; e < EL; ++e) acc_s[w][lane * EL + e] = acc[e];
-  if (lane == 0) l_s[w] = L;
+  if (lane == 0) { m_s[w] = m; l_s[w] = L; }
   __syncthreads();
   if (threadIdx.x < D) {
     const int d = threadIdx.x;
-    float Lt = (l_s[0] + l_s[1]) + (l_s[2] + l_s[3]);
+    float M = fmaxf(fmaxf(m_s[0], m_s[1]), fmaxf(m_s[2], m_s[3]));
+    if (a.sink) M = fmaxf(M, a.sink[h]);
+    float Lt = 0.f, o = 0.f;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const float f = (m_s[q] == -INFINITY) ? 0.f : expf(m_s[q] - M);
+      Lt += l_s[q] * f;
+      o += acc_s[q][d] * f;
+    }
     if (a.sink) Lt += expf(a.sink[h] - M);
-    const float o = (acc_s[0][d] + acc_s[1][d]) + (acc_s[2][d] + acc_s[3][d]);
     a.attn_out[((long long)b * a.nq + h) * D + d] = (uint16_t)f2bf(Lt > 0.f ? o / Lt : 0.f);
-    // in-place KV scatter of the new rows (attention_block_tkg.py:1144-1470):
-    // the first query head of each kv group writes that group's rows
-    const int gqa = a.nq / a.nkv;
-    if (a.update_cache && h % gqa == 0) {
+    // in-place KV scatter of the new rows (attention_block_tkg.py:1144-1470),
+    // after every chunk has read the cache (kernels run in stream order)
+    if (scatter) {
       const int g = h / gqa;
       const long long row = kv_write_row(a, b);
       if (row >= 0) {
         const long long off = a.block_table
                                   ? (row * a.nkv + g) * D + d
                                   : b * a.cache_b_stride + g * a.cache_h_stride + row * D + d;
-        a.k_cache[off] = a.kv_new[(((long long)b * 2 + 0) * a.nkv + g) * D + d];
-        a.v_cache[off] = a.kv_new[(((long long)b * 2 + 1) * a.nkv + g) * D + d];
+        a.k_cache[off] = knew;
+        a.v_cache[off] = vnew;
       }
     }
   }

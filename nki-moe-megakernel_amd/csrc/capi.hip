@@ -130,7 +130,7 @@ GemmArgs dense_args(const void* w, const void* x, int ldx, int N, int K, int T, 
   a.ldx = ldx;
   a.N = N;
   a.K = K;
-  a.KW = choose_kw(K);
+  a.KW = choose_kw(K, 512, (N + 15) / 16);
   a.T = T;
   a.y = y;
   a.ldy = ldy;
@@ -303,7 +303,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
   const int tn = 1;
   {  // gate/up + activation
     GemmArgs a = dense_args(gate_up, hidden, H, 2 * I, H, T, w.hbuf, I);
-    a.KW = choose_kw(H, 256);   // two row blocks per wave: 2 x 8 fragments in one batch
+    a.KW = choose_kw(H, 256, (long long)(I / 16) * gmax);   // two row blocks per wave
     a.w_group_stride = (long long)2 * I * H;
     a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
     a.n_groups = w.n_groups; a.pair_row = w.pair_token; a.pair_out_row = w.pair_slot;
@@ -316,6 +316,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
   }
   {  // down, scaled by the slot affinity
     GemmArgs a = dense_args(down, w.hbuf, I, H, I, T, w.ybuf, H);
+    a.KW = choose_kw(I, 512, (long long)((H + 15) / 16) * gmax);
     a.w_group_stride = padded_rows(H) * I;
     a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
     a.n_groups = w.n_groups; a.pair_row = w.pair_slot; a.pair_out_row = w.pair_slot;
@@ -628,7 +629,8 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
       o.y = o_parts;
       o.residual = nullptr;
       o.kgrid = o_kgrid;
-      o.KW = o_kgrid > 1 ? choose_kw_split(p->nq * p->d, o_kgrid) : choose_kw(p->nq * p->d);
+      o.KW = o_kgrid > 1 ? choose_kw_split(p->nq * p->d, o_kgrid)
+                         : choose_kw(p->nq * p->d, 512, (p->H_out + 15) / 16);
       o.part_stride = (long long)p->B * p->H_out;
       if (int rc = dense_gemm(o, EPI_F32, false, s)) return rc;
     } else if (int rc = dense_gemm(o, p->residual ? EPI_RESID_BF16 : EPI_BF16, false, s)) {
@@ -774,7 +776,7 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
   // finalize (one fused kernel); layer 0 normalises the input here.
   MKD_TRY(rmsnorm_launch(x, 0, static_cast<const uint16_t*>(m->ln_in[0]), w.attn.hnorm, nullptr, B,
                          m->H, m->H, ha, m->eps, pre_order, s), "pre norm");
-  const int o_kgrid = ((m->H + 15) / 16 < 256 && choose_kw_split(m->nq * m->d, 2) > 0) ? 2 : 1;
+  const int o_kgrid = 1;   // one block per 16 output rows, up to 16 waves over K
   for (int l = 0; l < m->num_layers; ++l) {
     const int wl = m->window ? m->window[l] : 0;
     mkd_attention_args ap;

@@ -33,15 +33,42 @@ MKD_DEV uint32_t f2bf(float f) {
 MKD_DEV float rbf(float f) { return bf2f(f2bf(f)); }
 MKD_DEV uint32_t pack2bf(float lo, float hi) { return f2bf(lo) | (f2bf(hi) << 16); }
 
-MKD_DEV float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+// Wave reductions without LDS traffic: DPP moves inside each row of 16 lanes
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror, row_mirror: the
+// gfx9 encodings 0xB1, 0x4E, 0x141, 0x140), after which every lane of a row
+// holds the row's value, then the four row values are read out with readlane
+// and combined in a fixed order.  The wave must be fully active.  Every lane
+// gets the bit-identical result (each step combines a pair of identical
+// partial results in both lanes, and the final combine is uniform).
+template <int CTRL>
+MKD_DEV float dpp_f(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+MKD_DEV float lane_f(float v, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), l));
+}
+MKD_DEV float row_sum(float v) {
+  v += dpp_f<0xB1>(v);
+  v += dpp_f<0x4E>(v);
+  v += dpp_f<0x141>(v);
+  v += dpp_f<0x140>(v);
   return v;
 }
-MKD_DEV float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+MKD_DEV float row_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));
+  v = fmaxf(v, dpp_f<0x140>(v));
   return v;
+}
+MKD_DEV float wave_sum(float v) {
+  v = row_sum(v);
+  return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
+}
+MKD_DEV float wave_max(float v) {
+  v = row_max(v);
+  return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 // Block-wide sum for blockDim.x a multiple of 64 (<= 1024).  `red` needs 16 floats.

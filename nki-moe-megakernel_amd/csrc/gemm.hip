@@ -66,48 +66,11 @@ __global__ void pack_frag_kernel(const uint16_t* __restrict__ src, uint16_t* __r
   }
 }
 
-// One fragment step: MFMA of weight fragment column u against the x fragments of
-// the TN token tiles (bf16 rows, or fp32 rows carried as a bf16 hi + lo pair).
-template <int RB, int TN, bool XF32, int U>
-MKD_DEV void frag_mma(const u32x4_t (&wf)[RB][U], int u, int k, const int (&xrow)[TN],
-                      const GemmArgs& a, f32x4_t (&acc)[RB][TN]) {
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) {
-    if (XF32) {
-      u32x4_t hi = {0, 0, 0, 0}, lo = {0, 0, 0, 0};
-      if (xrow[tn] >= 0) {
-        const float* xp = reinterpret_cast<const float*>(a.x) + (long long)xrow[tn] * a.ldx + k;
-        const f32x4_t v0 = *reinterpret_cast<const f32x4_t*>(xp);
-        const f32x4_t v1 = *reinterpret_cast<const f32x4_t*>(xp + 4);
-        const float xs[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-        uint32_t h[8], l[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          h[j] = f2bf(xs[j]);
-          l[j] = f2bf(xs[j] - bf2f(h[j]));
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          hi[j] = h[2 * j] | (h[2 * j + 1] << 16);
-          lo[j] = l[2 * j] | (l[2 * j + 1] << 16);
-        }
-      }
-#pragma unroll
-      for (int r = 0; r < RB; ++r) {
-        acc[r][tn] = mfma16x16x32(wf[r][u], hi, acc[r][tn]);
-        acc[r][tn] = mfma16x16x32(wf[r][u], lo, acc[r][tn]);
-      }
-    } else {
-      u32x4_t xv = {0, 0, 0, 0};
-      if (xrow[tn] >= 0)
-        xv = ld16(reinterpret_cast<const uint16_t*>(a.x) + (long long)xrow[tn] * a.ldx + k);
-#pragma unroll
-      for (int r = 0; r < RB; ++r) acc[r][tn] = mfma16x16x32(wf[r][u], xv, acc[r][tn]);
-    }
-  }
-}
-
-// B consecutive fragments of every row block: all loads first, then the MFMAs.
+// B consecutive fragments of every row block: every weight and x load of the
+// batch is issued before the first MFMA.  Lanes of absent tokens (xrow < 0)
+// read x row 0 instead -- their output column is never written, and MFMA
+// columns are independent.  fp32 x rows are
+// carried as a bf16 hi + lo pair (two MFMAs).
 template <int RB, int TN, bool XF32, int B>
 MKD_DEV void stream_batch(const uint16_t* const (&wrow)[RB], int f, int kb0, int koff,
                           const int (&xrow)[TN], const GemmArgs& a, f32x4_t (&acc)[RB][TN]) {
@@ -117,8 +80,63 @@ MKD_DEV void stream_batch(const uint16_t* const (&wrow)[RB], int f, int kb0, int
 #pragma unroll
     for (int r = 0; r < RB; ++r)
       wf[r][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow[r] + (f + u) * 512));
+  // the weight loads go out before the x addresses are formed: in grouped mode
+  // the token rows come from a routing table whose load may still be in flight
+  __builtin_amdgcn_sched_barrier(0);
+  const void* xp[TN];
 #pragma unroll
-  for (int u = 0; u < B; ++u) frag_mma<RB, TN, XF32>(wf, u, (kb0 + f + u) * 32 + koff, xrow, a, acc);
+  for (int tn = 0; tn < TN; ++tn) {
+    int xr = xrow[tn];
+    asm volatile("" : "+v"(xr));         // formed here, not hoisted out of the k loop
+    const long long off = (long long)(xr >= 0 ? xr : 0) * a.ldx + koff;
+    xp[tn] = XF32 ? static_cast<const void*>(static_cast<const float*>(a.x) + off)
+                  : static_cast<const void*>(static_cast<const uint16_t*>(a.x) + off);
+  }
+  if constexpr (XF32) {
+    f32x4_t xa[B][TN], xb[B][TN];
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const float* p = static_cast<const float*>(xp[tn]) + (kb0 + f + u) * 32;
+        xa[u][tn] = *reinterpret_cast<const f32x4_t*>(p);
+        xb[u][tn] = *reinterpret_cast<const f32x4_t*>(p + 4);
+      }
+    __builtin_amdgcn_sched_barrier(0);     // keep every load ahead of the MFMAs
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn) {
+        const float xs[8] = {xa[u][tn][0], xa[u][tn][1], xa[u][tn][2], xa[u][tn][3],
+                             xb[u][tn][0], xb[u][tn][1], xb[u][tn][2], xb[u][tn][3]};
+        u32x4_t hi, lo;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const uint32_t h0 = f2bf(xs[2 * j]), h1 = f2bf(xs[2 * j + 1]);
+          hi[j] = h0 | (h1 << 16);
+          lo[j] = f2bf(xs[2 * j] - bf2f(h0)) | (f2bf(xs[2 * j + 1] - bf2f(h1)) << 16);
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+          acc[r][tn] = mfma16x16x32(wf[r][u], hi, acc[r][tn]);
+          acc[r][tn] = mfma16x16x32(wf[r][u], lo, acc[r][tn]);
+        }
+      }
+  } else {
+    u32x4_t xv[B][TN];
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+        xv[u][tn] = ld16(static_cast<const uint16_t*>(xp[tn]) + (kb0 + f + u) * 32);
+    __builtin_amdgcn_sched_barrier(0);     // keep every load ahead of the MFMAs
+#pragma unroll
+    for (int u = 0; u < B; ++u)
+#pragma unroll
+      for (int tn = 0; tn < TN; ++tn)
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[r][tn] = mfma16x16x32(wf[r][u], xv[u][tn], acc[r][tn]);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -139,10 +157,15 @@ gemm_frag_kernel(GemmArgs a) {
   int count, base;                       // tokens in this group / first pair
   const uint16_t* w = a.w;
   if (a.grp_expert) {
-    if (group >= *a.n_groups) return;
+    // the group's table entries are read together with the group count (one
+    // memory round trip; group < gridDim.y <= the tables' length)
+    const int ng = *a.n_groups;
     count = a.grp_count[group];
     base = a.grp_offset[group];
-    w += (long long)a.grp_expert[group] * a.w_group_stride;
+    const int ex = a.grp_expert[group];
+    asm volatile("" ::"s"(ng), "s"(count), "s"(base), "s"(ex));   // no sinking past the exit
+    if (group >= ng) return;
+    w += (long long)ex * a.w_group_stride;
   } else {
     count = a.T;
     base = 0;
@@ -178,10 +201,12 @@ gemm_frag_kernel(GemmArgs a) {
     wrow[r] = w + ((long long)(rbase * RB + r) * KB + kb0) * 512 + lane * 8;
 
   // Stream the fragments: a wave issues a batch of UNROLL*RB fragment loads
-  // (<= 16 KiB) before the MFMAs that consume them; batches carry no guards so
+  // (8 KiB) before the MFMAs that consume them; batches carry no guards so
   // they stay in registers, and the remainder (< UNROLL) is taken as batches of
-  // 8/4/2/1 so short slices still keep several loads in flight.
-  constexpr int UNROLL = (TN <= 2) ? 16 / RB : 8 / RB;
+  // 4/2/1 so short slices still keep several loads in flight.  (Measured at
+  // decode shapes: 8 fragments per batch with up to 16 waves per block beat
+  // 16- and 32-fragment batches with fewer waves.)
+  constexpr int UNROLL = 8 / RB;
   int f = 0;
   for (; f + UNROLL <= NF; f += UNROLL)
     stream_batch<RB, TN, XF32, UNROLL>(wrow, f, kb0, koff, xrow, a, acc);
@@ -212,13 +237,23 @@ static hipError_t launch_t(const GemmArgs& a, int n_tiles, int groups, int ttile
   return timed_launch(gemm_frag_kernel<RB, TN, XF32, EPI>, grid, block, lds, s, a);
 }
 
-int choose_kw(int K, int max_kw) {
-  // Largest per-wave K slice (a multiple of 32, <= max_kw) that divides K into
-  // <= 16 waves.
+int choose_kw(int K, int max_kw, long long blocks) {
+  // Per-wave K slice (a multiple of 32 dividing K into <= 16 waves, <= max_kw).
+  // The longest slice is cheapest per fragment (fewer partial sums to reduce),
+  // but a launch of few blocks needs more waves per block to keep enough loads
+  // in flight: take the longest slice that gives >= kMinWaves waves in total,
+  // else the most waves whose slices still hold >= 64 elements.  Measured at
+  // decode shapes: o_proj 2048x4096 (128 blocks) 7.2 us at 16 waves vs 8.1 us
+  // at 8; lm_head 151936x2048 (9496 blocks) 94 us at 4 waves vs 99 us at 8.
+  constexpr long long kMinWaves = 2048;
+  int best = -1, most = -1;
   for (int kw = (max_kw < K ? max_kw : K) / 32 * 32; kw >= 32; kw -= 32) {
-    if (K % kw == 0 && K / kw <= 16) return kw;
+    if (K % kw || K / kw > 16) continue;
+    if (blocks * (K / kw) >= kMinWaves) return kw;
+    if (best < 0) best = kw;
+    if (kw >= 64 || most < 0) most = kw;
   }
-  return -1;
+  return most > 0 ? most : best;
 }
 
 int choose_kw_split(int K, int kgrid) {

@@ -72,7 +72,7 @@ hipError_t timed_launch(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t
   return hipGetLastError();
 }
 
-int choose_kw(int K, int max_kw = 512);
+int choose_kw(int K, int max_kw = 512, long long blocks = 1LL << 40);
 int choose_kw_split(int K, int kgrid);
 hipError_t gemm_launch(GemmArgs a, int epi, bool xf32, int tn, int groups_max,
                        int max_tokens_per_group, hipStream_t s);

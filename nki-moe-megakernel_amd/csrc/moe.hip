@@ -46,14 +46,63 @@ MKD_DEV int lanes_below(unsigned long long m) {
   return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
 }
 
+// Exclusive prefix sum over the wave: Hillis-Steele inside each row of 16
+// lanes with DPP row_shr 1/2/4/8 (a source outside the row reads 0), then the
+// row totals (readlane of lanes 15/31/47) are added to the later rows.
+template <int CTRL>
+MKD_DEV int dpp_shr_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
 MKD_DEV int wave_excl_scan(int v, int lane) {
   int x = v;
-#pragma unroll
-  for (int o = 1; o < 64; o <<= 1) {
-    const int y = __shfl_up(x, o, 64);
-    if (lane >= o) x += y;
-  }
+  x += dpp_shr_i<0x111>(x);
+  x += dpp_shr_i<0x112>(x);
+  x += dpp_shr_i<0x114>(x);
+  x += dpp_shr_i<0x118>(x);
+  const int r0 = __builtin_amdgcn_readlane(x, 15);
+  const int r1 = __builtin_amdgcn_readlane(x, 31);
+  const int r2 = __builtin_amdgcn_readlane(x, 47);
+  const int row = lane >> 4;
+  x += (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
   return x - v;
+}
+
+// Sum of the split-K partial logits of token t for the lane's experts (+ the
+// bias): a whole batch of loads is issued (slots past nparts re-read the last
+// partial and are masked out) before summing in fixed order.
+template <int PER>
+MKD_DEV void load_logits(const RouterArgs& a, int t, int lane, float (&l)[PER]) {
+  const int E = a.E;
+  uint32_t braw[PER];                   // bias bits, loaded with the partials
+  if (a.bias) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) braw[j] = a.bias[min(lane + 64 * j, E - 1)];
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) l[j] = 0.f;
+  constexpr int PB = (PER <= 2) ? 16 : 4;
+#pragma unroll
+  for (int p0 = 0; p0 < 16; p0 += PB) {
+    float v[PB][PER];
+#pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const int pp = min(p0 + q, a.nparts - 1);
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int e = min(lane + 64 * j, E - 1);
+        v[q][j] = a.parts[pp * a.part_stride + (long long)t * E + e];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < PB; ++q)
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (p0 + q < a.nparts) l[j] += v[q][j];
+  }
+  if (a.bias) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) l[j] += bf2f(braw[j]);
+  }
 }
 
 template <int PER>
@@ -61,50 +110,35 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
   __shared__ uint32_t cu_s[16][8];
   __shared__ int ce_s[16][8], slot_s[16][8];
   __shared__ float ck_s[16][8];
-  __shared__ float sel_s[16][8];
+  __shared__ float sel_s[16][8], pw_s[16][8];
   __shared__ float wsel_s[16][8];
   __shared__ int idx_s[128 * 8];
   __shared__ int cnt[kMaxE], off[kMaxE], cursor[kMaxE];
-  __shared__ int n_live;
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int E = a.E, K = a.K, T = a.T;
   const bool sigm = a.mode & 1, pre = a.mode & 2, norm = a.mode & 4, qwen = a.mode & 8;
-  // every slot starts invalid so that NaN logits (no consistent ranks) can never
-  // route a slot to an out-of-range expert below
-  for (int p = tid; p < T * K; p += blockDim.x) idx_s[p] = -1;
+  // the first token's logits are loaded before anything else (their latency
+  // covers the LDS set-up; the first block barrier comes after the per-token
+  // phase, which only touches the wave's own LDS rows)
+  float lfirst[PER];
+  if (wv < T) load_logits<PER>(a, wv, lane, lfirst);
   for (int e = tid; e < E; e += blockDim.x) { cnt[e] = 0; cursor[e] = 0; }
-  __syncthreads();
   for (int t = wv; t < T; t += 16) {
     float l[PER];
+    if (t == wv) {
 #pragma unroll
-    for (int j = 0; j < PER; ++j) l[j] = 0.f;
-    // split-K partial logits: issue a whole batch of loads (slots past nparts
-    // re-read the last partial and are masked out) before summing in fixed order
-    constexpr int PB = (PER <= 2) ? 16 : 4;
-#pragma unroll
-    for (int p0 = 0; p0 < 16; p0 += PB) {
-      float v[PB][PER];
-#pragma unroll
-      for (int q = 0; q < PB; ++q) {
-        const int pp = min(p0 + q, a.nparts - 1);
-#pragma unroll
-        for (int j = 0; j < PER; ++j) {
-          const int e = min(lane + 64 * j, E - 1);
-          v[q][j] = a.parts[pp * a.part_stride + (long long)t * E + e];
-        }
-      }
-#pragma unroll
-      for (int q = 0; q < PB; ++q)
-#pragma unroll
-        for (int j = 0; j < PER; ++j)
-          if (p0 + q < a.nparts) l[j] += v[q][j];
+      for (int j = 0; j < PER; ++j) l[j] = lfirst[j];
+    } else {
+      load_logits<PER>(a, t, lane, l);
     }
+    // every slot of the token starts invalid so that NaN logits (no consistent
+    // ranks) can never route a slot to an out-of-range expert below
+    if (lane < K) idx_s[t * K + lane] = -1;
     float mx = -INFINITY;
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const int e = lane + 64 * j;
       if (e < E) {
-        if (a.bias) l[j] += bf2f(a.bias[e]);
         if (a.logits_out) a.logits_out[(long long)t * E + e] = l[j];
       } else {
         l[j] = -INFINITY;
@@ -162,7 +196,8 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
       ties += __popcll(eq);
     }
     wave_lds_sync();
-    // output slot = rank among the K chosen (key descending, index ascending)
+    // output slot = rank among the K chosen (key descending, index ascending);
+    // each lane also forms its slot's term of the weight normalisation
     if (lane < K) {
       const uint32_t ui = cu_s[wv][lane];
       const int ei = ce_s[wv][lane];
@@ -177,33 +212,28 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
     }
     wave_lds_sync();
     if (lane < K) {
-      float w;
-      if (qwen) {
-        // softmax value at the selected logits -> bf16 -> bf16 L1 renormalisation
-        float s = 0.f;
-        for (int k = 0; k < K; ++k) s += rbf(expf(sel_s[wv][k] - mx) * inv);
-        w = rbf(rbf(expf(sel_s[wv][lane] - mx) * inv) * (1.0f / s));
-      } else if (pre) {
-        w = sel_s[wv][lane];
-        if (norm) {
-          float s = 0.f;
-          for (int k = 0; k < K; ++k) s += sel_s[wv][k];
-          w *= 1.0f / s;
-        }
-      } else if (sigm) {
-        w = 1.0f / (1.0f + expf(-sel_s[wv][lane]));
-      } else {
-        const float m2 = sel_s[wv][0];
-        float s = 0.f;
-        for (int k = 0; k < K; ++k) s += expf(sel_s[wv][k] - m2);
-        w = expf(sel_s[wv][lane] - m2) * (1.0f / s);
+      const float sv = sel_s[wv][lane];
+      float pv;
+      if (qwen) pv = rbf(expf(sv - mx) * inv);        // softmax value at the logit, bf16
+      else if (pre) pv = sv;
+      else if (sigm) pv = 1.0f / (1.0f + expf(-sv));
+      else pv = expf(sv - sel_s[wv][0]);             // softmax over the top-k (slot 0 = max)
+      pw_s[wv][lane] = pv;
+    }
+    wave_lds_sync();
+    if (lane < K) {
+      const float pv = pw_s[wv][lane];
+      float w = pv;
+      if (qwen || (pre && norm) || (!pre && !sigm)) {
+        float s = 0.f;                                 // k order
+        for (int k = 0; k < K; ++k) s += pw_s[wv][k];
+        w = qwen ? rbf(pv * (1.0f / s)) : pv * (1.0f / s);
       }
       wsel_s[wv][lane] = w;
       const int e = idx_s[t * K + lane];
       if (a.idx_out) a.idx_out[t * K + lane] = e;
       if (a.topk_out) a.topk_out[t * K + lane] = w;
       if (a.slot_w) a.slot_w[t * K + lane] = w;
-      if (a.n_groups && e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
     wave_lds_sync();
     if (a.aff_full) {
@@ -222,7 +252,12 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
   }
   if (!a.n_groups) return;
   __syncthreads();
-  // ---- expert groups: one wave scans the per-expert counts ----
+  // ---- expert groups: per-expert counts, one wave scans them ----
+  for (int p = tid; p < T * K; p += blockDim.x) {
+    const int e = idx_s[p];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
   if (wv == 0) {
     constexpr int PE = kMaxE / 64;
     int c[PE], lsum = 0, llive = 0;
@@ -249,7 +284,7 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
       }
       base += c[j];
     }
-    if (lane == 63) { *a.n_groups = gbase; n_live = gbase; }
+    if (lane == 63) *a.n_groups = gbase;
   }
   __syncthreads();
   for (int p = tid; p < T * K; p += blockDim.x) {

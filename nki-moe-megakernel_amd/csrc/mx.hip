@@ -250,10 +250,14 @@ MKD_DEV i32x8_t load_xfrag(const uint8_t* xr, int kb, int q) {
                  (int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
 }
 
+// B fragments of every row block: the weight codes and scales go out first,
+// then the x codes and scales of the lane's token row (formed only now: in
+// grouped mode the row comes from a routing table whose load may still be in
+// flight), and only then the MFMAs.  Lanes of absent tokens (xrow < 0) read
+// row 0 -- their output column is never written.
 template <int RB, int FMT, int B>
 MKD_DEV void mx_batch(const uint8_t* const (&wrow)[RB], const uint8_t* const (&srow)[RB],
-                      const uint8_t* xr, const uint8_t* xs, int kb0, int f, int q,
-                      f32x4_t (&acc)[RB][1]) {
+                      int xrow, const GemmArgs& a, int kb0, int f, int q, f32x4_t (&acc)[RB][1]) {
   constexpr int BPL = MxSpec<FMT>::BPL;
   WFrag<FMT> wf[RB][B];
   uint32_t ws[RB][B];
@@ -265,21 +269,28 @@ MKD_DEV void mx_batch(const uint8_t* const (&wrow)[RB], const uint8_t* const (&s
       wf[r][u].load(wrow[r] + (long long)(f + u) * 64 * BPL);
       ws[r][u] = *reinterpret_cast<const uint32_t*>(srow[r] + (kb >> 2) * 256) >> (8 * (kb & 3));
     }
+  __builtin_amdgcn_sched_barrier(0);
+  int xr_i = xrow;
+  asm volatile("" : "+v"(xr_i));         // formed here, not hoisted out of the k loop
+  const long long row = xr_i >= 0 ? xr_i : 0;
+  const uint8_t* xr = reinterpret_cast<const uint8_t*>(a.x) + row * a.ldx;
+  const uint8_t* xs = a.x_scale + row * a.ldxs;
+  i32x8_t xf[B];
+  uint32_t xsc[B];
 #pragma unroll
   for (int u = 0; u < B; ++u) {
     const int kb = kb0 + f + u;
-    i32x8_t xf = {0, 0, 0, 0, 0, 0, 0, 0};
-    uint32_t xsc = 0;
-    if (xr) {
-      xf = load_xfrag(xr, kb, q);
-      xsc = *reinterpret_cast<const uint32_t*>(xs + kb * 4) >> (8 * q);
-    }
+    xf[u] = load_xfrag(xr, kb, q);
+    xsc[u] = *reinterpret_cast<const uint32_t*>(xs + kb * 4) >> (8 * q);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < B; ++u)
 #pragma unroll
     for (int r = 0; r < RB; ++r)
       acc[r][0] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(
-          wf[r][u].op(), xf, acc[r][0], MxSpec<FMT>::HW, MxSpec<MX_E4M3>::HW, 0, (int)(ws[r][u] & 0xffu), 0,
-          (int)(xsc & 0xffu));
-  }
+          wf[r][u].op(), xf[u], acc[r][0], MxSpec<FMT>::HW, MxSpec<MX_E4M3>::HW, 0,
+          (int)(ws[r][u] & 0xffu), 0, (int)(xsc[u] & 0xffu));
 }
 
 template <int RB, int FMT, int EPI>
@@ -297,11 +308,15 @@ __global__ void __launch_bounds__(512) gemm_mx_kernel(GemmArgs a) {
   const uint8_t* w = reinterpret_cast<const uint8_t*>(a.w);
   const uint8_t* wsc = a.w_scale;
   if (a.grp_expert) {
-    if (group >= *a.n_groups) return;
+    // table entries read with the group count: one memory round trip
+    const int ng = *a.n_groups;
     count = a.grp_count[group];
     base = a.grp_offset[group];
-    w += (long long)a.grp_expert[group] * a.w_group_stride;
-    wsc += (long long)a.grp_expert[group] * a.w_scale_group_stride;
+    const int ex = a.grp_expert[group];
+    asm volatile("" ::"s"(ng), "s"(count), "s"(base), "s"(ex));   // no sinking past the exit
+    if (group >= ng) return;
+    w += (long long)ex * a.w_group_stride;
+    wsc += (long long)ex * a.w_scale_group_stride;
   } else {
     count = a.T;
     base = 0;
@@ -313,8 +328,6 @@ __global__ void __launch_bounds__(512) gemm_mx_kernel(GemmArgs a) {
     const int c = t0 + (lane & 15);
     xrow[0] = c < count ? (a.pair_row ? a.pair_row[base + c] : base + c) : -1;
   }
-  const uint8_t* xr = xrow[0] >= 0 ? reinterpret_cast<const uint8_t*>(a.x) + (long long)xrow[0] * a.ldx : nullptr;
-  const uint8_t* xs = xrow[0] >= 0 ? a.x_scale + (long long)xrow[0] * a.ldxs : nullptr;
 
   const int KB = a.K / 128, KB4 = (KB + 3) / 4;
   const int NF = a.KW / 128;
@@ -334,15 +347,15 @@ __global__ void __launch_bounds__(512) gemm_mx_kernel(GemmArgs a) {
   }
   // batches of U fragments per row block (<= 16 KiB of weight loads in flight
   // per wave), remainder in batches of 4/2/1
-  constexpr int U = (FMT == MX_E4M3 ? 8 : 16) / RB;
+  constexpr int U = 8 / RB;
   int f = 0;
-  for (; f + U <= NF; f += U) mx_batch<RB, FMT, U>(wrow, srow, xr, xs, kb0, f, q, acc);
+  for (; f + U <= NF; f += U) mx_batch<RB, FMT, U>(wrow, srow, xrow[0], a, kb0, f, q, acc);
   if constexpr (U > 4)
-    if (f + 4 <= NF) { mx_batch<RB, FMT, 4>(wrow, srow, xr, xs, kb0, f, q, acc); f += 4; }
+    if (f + 4 <= NF) { mx_batch<RB, FMT, 4>(wrow, srow, xrow[0], a, kb0, f, q, acc); f += 4; }
   if constexpr (U > 2)
-    if (f + 2 <= NF) { mx_batch<RB, FMT, 2>(wrow, srow, xr, xs, kb0, f, q, acc); f += 2; }
+    if (f + 2 <= NF) { mx_batch<RB, FMT, 2>(wrow, srow, xrow[0], a, kb0, f, q, acc); f += 2; }
   if constexpr (U > 1)
-    if (f < NF) mx_batch<RB, FMT, 1>(wrow, srow, xr, xs, kb0, f, q, acc);
+    if (f < NF) mx_batch<RB, FMT, 1>(wrow, srow, xrow[0], a, kb0, f, q, acc);
 
   gemm_finish<RB, 1, EPI>(a, acc, lane, wave, rbase, group, t0, base, xrow, kblk);
 }

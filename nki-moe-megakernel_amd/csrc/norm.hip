@@ -21,6 +21,7 @@ namespace mkd {
 
 constexpr int kNormThreads = 256;
 constexpr int kNormMaxVec = 4;  // 4 x 8 elements x 256 threads = 8192
+constexpr int kNormMaxDK = 8;   // partial rows summed per element (experts / split-K)
 
 __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(NormArgs a) {
   __shared__ float red[16];
@@ -28,11 +29,25 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(NormArgs a) {
   const int tid = threadIdx.x;
   const int H = a.H;
   float v[kNormMaxVec][8];
+  u32x4_t gp[kNormMaxVec];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < kNormMaxVec; ++c) {
     const int i = (c * kNormThreads + tid) * 8;
     if (i < H) {
+      if (a.gamma) gp[c] = ld16(a.gamma + i);
+      // every load of this slice first (gamma, the partial rows, x) so their
+      // latencies overlap; the partials are then summed in k order
+      f32x4_t dp[kNormMaxDK][2];
+      if (a.dsum) {
+#pragma unroll
+        for (int k = 0; k < kNormMaxDK; ++k)
+          if (k < a.dK) {
+            const float* p = a.dsum + row * a.ds_row + k * a.ds_k + i;
+            dp[k][0] = *reinterpret_cast<const f32x4_t*>(p);
+            dp[k][1] = *reinterpret_cast<const f32x4_t*>(p + 4);
+          }
+      }
       if (a.x_f32) {
         const float* xp = reinterpret_cast<const float*>(a.x) + (long long)row * a.ld_in + i;
         f32x4_t p = *reinterpret_cast<const f32x4_t*>(xp);
@@ -46,13 +61,13 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(NormArgs a) {
       }
       if (a.dsum) {
         float s[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-        for (int k = 0; k < a.dK; ++k) {
-          const float* dp = a.dsum + row * a.ds_row + k * a.ds_k + i;
-          f32x4_t p = *reinterpret_cast<const f32x4_t*>(dp);
-          f32x4_t q = *reinterpret_cast<const f32x4_t*>(dp + 4);
-          s[0] += p[0]; s[1] += p[1]; s[2] += p[2]; s[3] += p[3];
-          s[4] += q[0]; s[5] += q[1]; s[6] += q[2]; s[7] += q[3];
-        }
+#pragma unroll
+        for (int k = 0; k < kNormMaxDK; ++k)
+          if (k < a.dK) {
+            const f32x4_t p = dp[k][0], q = dp[k][1];
+            s[0] += p[0]; s[1] += p[1]; s[2] += p[2]; s[3] += p[3];
+            s[4] += q[0]; s[5] += q[1]; s[6] += q[2]; s[7] += q[3];
+          }
         u32x4_t o;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -73,11 +88,10 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(NormArgs a) {
   for (int c = 0; c < kNormMaxVec; ++c) {
     const int i = (c * kNormThreads + tid) * 8;
     if (i < H) {
-      u32x4_t gp = ld16(a.gamma + i);
       float y[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float g = (j & 1) ? bf_hi(gp[j >> 1]) : bf_lo(gp[j >> 1]);
+        const float g = (j & 1) ? bf_hi(gp[c][j >> 1]) : bf_lo(gp[c][j >> 1]);
         if (a.order == 0) y[j] = (v[c][j] * g) * rinv;
         else if (a.order == 1) y[j] = (v[c][j] * rinv) * g;
         else y[j] = g * rbf(v[c][j] * rinv);
@@ -98,7 +112,8 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(NormArgs a) {
 }
 
 hipError_t norm_launch(NormArgs a, hipStream_t s) {
-  if (a.H % 8 != 0 || a.H > kNormThreads * 8 * kNormMaxVec || a.rows <= 0 || a.hidden_actual <= 0)
+  if (a.H % 8 != 0 || a.H > kNormThreads * 8 * kNormMaxVec || a.rows <= 0 || a.hidden_actual <= 0 ||
+      (a.dsum && (a.dK < 1 || a.dK > kNormMaxDK)))
     return hipErrorInvalidValue;
   a.inv_h = 1.0f / (float)a.hidden_actual;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(a.rows), dim3(kNormThreads), 0, s, a);
