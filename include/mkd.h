@@ -181,6 +181,15 @@ typedef struct {
 } mkd_moe_args;
 size_t mkd_moe_workspace_bytes(int T, int H, int E, int I, int K);
 int mkd_moe_tkg(const mkd_moe_args* args, void* workspace, size_t workspace_bytes, void* stream);
+/* moe_prefill: the same selective-expert computation for a prefill-shaped
+ * batch (many tokens per expert), on LDS-tiled grouped MFMA GEMMs (256 x 256
+ * tiles, operands copied global -> LDS in MFMA order) instead of the
+ * weight-streaming decode GEMMs.  The reference's
+ * selective mode stops at T <= 128 (moe_tkg.py:388-392) and has no
+ * counterpart for this entry; it measures the MFMA-bound regime with the same
+ * packed weights and arguments.  bf16 weights only; 1 <= T <= 65535,
+ * T*K <= 2^24; H and I multiples of 32.  Workspace: mkd_moe_workspace_bytes. */
+int mkd_moe_prefill(const mkd_moe_args* args, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * attention_block_tkg -- replaces nki_kernels/attention/attention_block_tkg.py:83

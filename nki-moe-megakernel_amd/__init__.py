@@ -5,8 +5,11 @@ Operator surface (same names, argument order and defaults as the reference):
   attention_block_tkg   nki_kernels/attention/attention_block_tkg.py:83
   router_topk           nki_kernels/moe/router_topk.py:69
   moe_tkg               nki_kernels/moe/moe_tkg.py:56
+  moe_prefill           moe_tkg for prefill-shaped batches (T > 128; no
+                        reference counterpart), LDS-tiled MFMA GEMMs
 Model surface:
   qwen_with_megakernel  megakernels/qwen3_moe/qwen_with_megakernel.py
+  gpt_oss_with_megakernel  megakernels/gpt_oss/gpt_oss_with_megakernel.py
 
 All compute runs in libmkd.so (hand-written HIP for gfx950, C ABI in
 include/mkd.h).  The package directory name contains dashes, so it is
@@ -17,8 +20,8 @@ from . import _lib
 from .attention import attention_block_tkg
 from .common_types import (ActFnType, ExpertAffinityScaleMode, QuantizationType,
                            RouterActFnType)
-from .moe import moe_tkg, router_topk
+from .moe import moe_prefill, moe_tkg, router_topk
 from .norm import rmsnorm_tkg
 
-__all__ = ["rmsnorm_tkg", "attention_block_tkg", "router_topk", "moe_tkg", "ActFnType",
+__all__ = ["rmsnorm_tkg", "attention_block_tkg", "router_topk", "moe_tkg", "moe_prefill", "ActFnType",
            "ExpertAffinityScaleMode", "QuantizationType", "RouterActFnType"]

@@ -105,6 +105,7 @@ _SIGS = {
     "mkd_pack_mx_weights": (i32, [vp, vp, vp, vp, i32, i32, i32, i64, i64, i64, i64, i32, i32, vp]),
     "mkd_moe_workspace_bytes": (sz, [i32, i32, i32, i32, i32]),
     "mkd_moe_tkg": (i32, [C.POINTER(MoeArgs), vp, sz, vp]),
+    "mkd_moe_prefill": (i32, [C.POINTER(MoeArgs), vp, sz, vp]),
     "mkd_attention_workspace_bytes": (sz, [i32, i32, i32, i32, i32, i32]),
     "mkd_attention_block_tkg": (i32, [C.POINTER(AttentionArgs), vp, sz, vp]),
     "mkd_qwen3_workspace_bytes": (sz, [C.POINTER(Qwen3Model), i32]),

@@ -241,7 +241,6 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   }
   __syncthreads();
 
-
   // q fragments (B operand): lane l -> head l%16, d = (l/16)*(D/4) + kk*8 .. +8
   const int hcol = lane & 15;
   u32x4_t qf[NK];

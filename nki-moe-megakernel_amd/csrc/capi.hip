@@ -251,7 +251,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
              const uint16_t* resid, uint16_t* out, float* out_f32, int T, int H, int E, int I,
              int K, int act, float alpha, float ghi, float glo, float uhi, float ulo, int round_qwen,
              MoeWs& w, hipStream_t s, bool do_finalize = true, int wfmt = 0,
-             const void* gu_scales = nullptr, const void* dn_scales = nullptr) {
+             const void* gu_scales = nullptr, const void* dn_scales = nullptr, bool tiled = false) {
   if (idx)  // otherwise the router stage already built the expert groups
     MKD_TRY(moe_route_launch(idx, T, K, E, w.n_groups, w.grp_expert, w.grp_count, w.grp_offset,
                              w.pair_token, w.pair_slot, s), "moe_route");
@@ -292,6 +292,36 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
       a.bias = dn_bias; a.bias_group_stride = H;
       const int ps = prof_begin(MKD_KCLASS_MOE_DOWN, s);
       MKD_TRY(gemm_mx_launch(a, wfmt, EPI_SCALE_F32, gmax, T, s), "moe down (mx)");
+      prof_end(ps, s);
+    }
+    if (do_finalize)
+      MKD_TRY(moe_finalize_launch(w.ybuf, T, K, H, resid, out, out_f32, s), "moe finalize");
+    return MKD_OK;
+  }
+  if (tiled) {
+    // Many tokens per expert: LDS-tiled grouped GEMMs (256 x 256 tiles), one
+    // token tile per 256 tokens of the largest possible group (T).
+    {
+      GemmArgs a = dense_args(gate_up, hidden, H, 2 * I, H, T, w.hbuf, I);
+      a.w_group_stride = (long long)2 * I * H;
+      a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
+      a.n_groups = w.n_groups; a.pair_row = w.pair_token; a.pair_out_row = w.pair_slot;
+      a.bias = gu_bias; a.bias_group_stride = 2LL * I;
+      a.act = act; a.alpha = alpha; a.gate_hi = ghi; a.gate_lo = glo; a.up_hi = uhi; a.up_lo = ulo;
+      a.round_qwen = round_qwen;
+      const int ps = prof_begin(MKD_KCLASS_MOE_GATE_UP, s);
+      MKD_TRY(gemm_tile_launch(a, EPI_SWIGLU_BF16, gmax, T, s), "moe gate_up (tiled)");
+      prof_end(ps, s);
+    }
+    {
+      GemmArgs a = dense_args(down, w.hbuf, I, H, I, T, w.ybuf, H);
+      a.w_group_stride = padded_rows(H) * I;
+      a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
+      a.n_groups = w.n_groups; a.pair_row = w.pair_slot; a.pair_out_row = w.pair_slot;
+      a.pair_scale = slot_w;
+      a.bias = dn_bias; a.bias_group_stride = H;
+      const int ps = prof_begin(MKD_KCLASS_MOE_DOWN, s);
+      MKD_TRY(gemm_tile_launch(a, EPI_SCALE_F32, gmax, T, s), "moe down (tiled)");
       prof_end(ps, s);
     }
     if (do_finalize)
@@ -429,13 +459,25 @@ size_t mkd_moe_workspace_bytes(int T, int H, int E, int I, int K) {
   return c.used;
 }
 
-int mkd_moe_tkg(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, void* stream) {
-  if (int rc = stale_check("mkd_moe_tkg")) return rc;
+}  // extern "C"
+
+namespace {
+int moe_entry(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, void* stream,
+              bool tiled) {
   MKD_REQUIRE(p, MKD_ERR_NULL, "moe_tkg: null args");
   MKD_REQUIRE(p->hidden && p->gate_up_packed && p->down_packed && p->expert_index && p->output,
               MKD_ERR_NULL, "moe_tkg: null pointer");
-  MKD_REQUIRE(p->T > 0 && p->T <= 128, MKD_ERR_INVALID,
-              "moe_tkg: only T <= 128 tokens are supported in selective mode, got %d", p->T);
+  if (tiled) {
+    MKD_REQUIRE(p->T > 0 && p->T <= 65535 && (long long)p->T * p->K <= (1 << 24), MKD_ERR_INVALID,
+                "moe_prefill: T %d must be in [1, 65535] with T*K <= 2^24", p->T);
+    MKD_REQUIRE(p->weight_format == 0, MKD_ERR_UNSUPPORTED, "moe_prefill: bf16 expert weights only");
+    MKD_REQUIRE(gemm_tile_supported(2 * p->I, p->H, EPI_SWIGLU_BF16) &&
+                    gemm_tile_supported(p->H, p->I, EPI_SCALE_F32),
+                MKD_ERR_UNSUPPORTED, "moe_prefill: H (%d) and I (%d) must be multiples of 32", p->H, p->I);
+  } else {
+    MKD_REQUIRE(p->T > 0 && p->T <= 128, MKD_ERR_INVALID,
+                "moe_tkg: only T <= 128 tokens are supported in selective mode, got %d", p->T);
+  }
   MKD_REQUIRE(p->E > 0 && p->E <= 512 && p->K >= 1 && p->K <= 8 && p->K <= p->E, MKD_ERR_INVALID,
               "moe_tkg: bad E=%d / K=%d", p->E, p->K);
   if (p->weight_format) {
@@ -478,7 +520,20 @@ int mkd_moe_tkg(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, 
                   static_cast<const uint16_t*>(p->residual), static_cast<uint16_t*>(p->output),
                   p->output_f32, p->T, p->H, p->E, p->I, p->K, p->activation, p->alpha,
                   p->gate_hi, p->gate_lo, p->up_hi, p->up_lo, p->round_qwen, w, s, true,
-                  p->weight_format, p->gate_up_scales, p->down_scales);
+                  p->weight_format, p->gate_up_scales, p->down_scales, tiled);
+}
+}  // namespace
+
+extern "C" {
+
+int mkd_moe_tkg(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = stale_check("mkd_moe_tkg")) return rc;
+  return moe_entry(p, workspace, workspace_bytes, stream, false);
+}
+
+int mkd_moe_prefill(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = stale_check("mkd_moe_prefill")) return rc;
+  return moe_entry(p, workspace, workspace_bytes, stream, true);
 }
 
 int mkd_quantize_mx(const void* x, int x_dtype, int rows, int k, int ldx, int fmt, void* codes,

@@ -16,6 +16,20 @@
 
 namespace mkd {
 
+// One gated activation value from the gate and up projections (fp32, bias
+// already added).  Qwen rounding: g, u -> bf16, silu(g) -> bf16, product;
+// otherwise clamps, then act(g) * u with act = silu or swish(alpha).
+MKD_DEV float swiglu_value(const GemmArgs& a, float gv, float uv) {
+  if (a.round_qwen) {
+    const float g = rbf(gv), u = rbf(uv);
+    return rbf(g / (1.0f + expf(-g))) * u;
+  }
+  const float g = fmaxf(fminf(gv, a.gate_hi), a.gate_lo);
+  const float u = fmaxf(fminf(uv, a.up_hi), a.up_lo);
+  const float z = a.act ? a.alpha * g : g;
+  return (g / (1.0f + expf(-z))) * u;
+}
+
 template <int RB, int TN, int EPI>
 MKD_DEV void gemm_finish(const GemmArgs& a, f32x4_t (&acc)[RB][TN], int lane, int wave, int rbase,
                          int group, int t0, int base, const int (&xrow)[TN], int kblk) {
@@ -81,20 +95,9 @@ MKD_DEV void gemm_finish(const GemmArgs& a, f32x4_t (&acc)[RB][TN], int lane, in
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[i] = (i < nv) ? bf2f(rp[i]) + rbf(v[0][i]) : 0.f;
     } else if (EPI == EPI_SWIGLU_BF16) {
-      // gate rows in v[0], up rows in v[1]; Qwen rounding: g,u -> bf16,
-      // silu(g) -> bf16, product -> bf16.
+      // gate rows in v[0], up rows in v[1]; the product is stored as bf16
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (a.round_qwen) {
-          const float g = rbf(v[0][i]), u = rbf(v[RB - 1][i]);
-          o[i] = rbf(g / (1.0f + expf(-g))) * u;
-        } else {
-          float g = fmaxf(fminf(v[0][i], a.gate_hi), a.gate_lo);
-          float u = fmaxf(fminf(v[RB - 1][i], a.up_hi), a.up_lo);
-          const float z = a.act ? a.alpha * g : g;
-          o[i] = (g / (1.0f + expf(-z))) * u;
-        }
-      }
+      for (int i = 0; i < 4; ++i) o[i] = swiglu_value(a, v[0][i], v[RB - 1][i]);
     } else if (EPI == EPI_SCALE_F32) {
       const float sc = a.pair_scale ? a.pair_scale[orow] : 1.0f;
 #pragma unroll

@@ -88,6 +88,10 @@ hipError_t mx_pack_launch(const uint8_t* codes, const uint8_t* scales, uint8_t* 
 hipError_t gemm_mx_launch(GemmArgs a, int fmt, int epi, int groups_max, int max_tokens_per_group,
                           hipStream_t s);
 int choose_kw_mx(int K_pad);
+// gemm_tile.hip: LDS-tiled grouped GEMM (many tokens per expert)
+bool gemm_tile_supported(int N, int K, int epi);
+hipError_t gemm_tile_launch(const GemmArgs& a, int epi, int groups_max, int max_tokens_per_group,
+                            hipStream_t s);
 int mx_kpad(int K);   // contraction padding of the packed MX layout
 
 hipError_t pack_frag_launch(const uint16_t* src, uint16_t* dst, int G, int N, int K,

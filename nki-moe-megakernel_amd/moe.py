@@ -126,7 +126,7 @@ def moe_tkg(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
             up_clamp_upper_limit: Optional[float] = None,
             up_clamp_lower_limit: Optional[float] = None, output_in_sbuf: bool = False,
             is_all_expert_dynamic: bool = False, block_size: int = None,
-            name_prefix: str = "") -> torch.Tensor:
+            name_prefix: str = "", _prefill: bool = False) -> torch.Tensor:
     """Selective-expert MoE for decode; returns output [T, H].
 
     hidden_input [T, H] bf16; expert_gate_up_weights [E, H, 2, I] bf16 (or
@@ -165,7 +165,7 @@ def moe_tkg(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
         raise ValueError(f"gate_up weights {tuple(expert_gate_up_weights.shape)} do not match [E, {H}, 2, I]")
     if tuple(expert_down_weights.shape) != (E, I, H):
         raise ValueError(f"down weights {tuple(expert_down_weights.shape)} != {(E, I, H)}")
-    if T > 128:
+    if T > 128 and not _prefill:
         raise ValueError("Currently only batch size * seq len <= 128 is supported (except for all-expert mode)")
     K = expert_index.shape[-1]
     act = {ActFnType.SiLU: L.ACT_SILU, ActFnType.Swish: L.ACT_SWISH}.get(activation_fn)
@@ -199,8 +199,42 @@ def moe_tkg(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
         round_qwen=0)
     lib = L.load()
     ws = _ws(lib.mkd_moe_workspace_bytes(T, H, E, I, K), dev)
-    rc = lib.mkd_moe_tkg(args, ws.data_ptr(), ws.numel(), L.stream_ptr(dev))
-    L.check(rc, "moe_tkg")
+    entry = lib.mkd_moe_prefill if _prefill else lib.mkd_moe_tkg
+    rc = entry(args, ws.data_ptr(), ws.numel(), L.stream_ptr(dev))
+    L.check(rc, "moe_prefill" if _prefill else "moe_tkg")
     if out32 is not None:
         return out32
     return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
+
+
+def moe_prefill(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
+                expert_down_weights: torch.Tensor, expert_affinities: torch.Tensor,
+                expert_index: torch.Tensor,
+                expert_gate_up_bias: Optional[torch.Tensor] = None,
+                expert_down_bias: Optional[torch.Tensor] = None,
+                expert_affinities_scaling_mode: ExpertAffinityScaleMode = ExpertAffinityScaleMode.NO_SCALE,
+                activation_fn: ActFnType = ActFnType.SiLU, output_dtype=None,
+                gate_clamp_upper_limit: Optional[float] = None,
+                gate_clamp_lower_limit: Optional[float] = None,
+                up_clamp_upper_limit: Optional[float] = None,
+                up_clamp_lower_limit: Optional[float] = None) -> torch.Tensor:
+    """moe_tkg's selective-expert computation for a prefill-shaped batch.
+
+    Same arguments and result as moe_tkg (bf16 weights), for T up to 65535
+    tokens: many tokens per expert make the expert GEMMs MFMA-bound, so they
+    run on LDS-tiled grouped GEMMs (mkd_moe_prefill) instead of the decode
+    path's weight-streaming kernels.  The reference's selective mode stops at
+    T <= 128 (moe_tkg.py:388-392); this entry has no reference counterpart.
+    """
+    from . import mx as _mx
+    if _mx.is_mx_weight(expert_gate_up_weights):
+        raise NotImplementedError("moe_prefill: bf16 expert weights only")
+    return moe_tkg(hidden_input, expert_gate_up_weights, expert_down_weights, expert_affinities,
+                   expert_index, False, expert_gate_up_bias=expert_gate_up_bias,
+                   expert_down_bias=expert_down_bias,
+                   expert_affinities_scaling_mode=expert_affinities_scaling_mode,
+                   activation_fn=activation_fn, output_dtype=output_dtype,
+                   gate_clamp_upper_limit=gate_clamp_upper_limit,
+                   gate_clamp_lower_limit=gate_clamp_lower_limit,
+                   up_clamp_upper_limit=up_clamp_upper_limit,
+                   up_clamp_lower_limit=up_clamp_lower_limit, _prefill=True)
