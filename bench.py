@@ -23,6 +23,7 @@ Also reported:
                    (each used for 24 of the 48 layer slots), scaled to tok/s.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
+       python bench.py --moe-prefill T   (MFMA regime of the expert GEMMs)
 """
 from __future__ import annotations
 
@@ -239,7 +240,12 @@ def main():
     ap.add_argument("--model", choices=["qwen3", "gpt-oss"], default="qwen3",
                     help="gpt-oss: GPT-OSS-20B shape, 24 layers, MXFP4 experts (configs[4]; "
                          "use --batch 32 --ragged --experts mxfp4)")
+    ap.add_argument("--moe-prefill", type=int, default=0, metavar="T",
+                    help="measure the MFMA regime instead: moe_prefill (LDS-tiled grouped GEMMs) "
+                         "on T tokens of the Qwen3 expert shape (E=128, K=8), T*K/E tokens/expert")
     args = ap.parse_args()
+    if args.moe_prefill and args.gpus == 1:
+        return bench_moe_prefill(args)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
@@ -420,6 +426,91 @@ def main():
 # bs = 1, 48 fused layers, 122.7 tok/s on one Trainium 3 chip
 # (megakernels/qwen3_moe/README.md:12).
 REF_TOK_S_BS1 = 122.7
+
+
+def bench_moe_prefill(args):
+    """MFMA-regime measurement of the expert GEMMs: moe_prefill on a
+    prefill-shaped batch (T tokens, Qwen3-30B-A3B expert shape, uniform
+    seeded routing), timed with events around K calls and per kernel through
+    the dispatch-packet profile events.  FLOPs: gate/up 2*T*K*H*2I, down
+    2*T*K*I*H."""
+    import torch
+    import __graft_entry__ as ge
+    mk = ge.load_package()
+    from nki_moe_megakernel_amd import _lib as L
+    from nki_moe_megakernel_amd.common_types import ExpertAffinityScaleMode
+    dev = torch.device("cuda:0")
+    lib = L.load()
+    T, E, K, H, I = args.moe_prefill, 128, 8, 2048, 768
+    g = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn(T, H, device=dev, generator=g).to(torch.bfloat16)
+    gu = (0.02 * torch.randn(E, H, 2, I, device=dev, generator=g)).to(torch.bfloat16)
+    dn = (0.02 * torch.randn(E, I, H, device=dev, generator=g)).to(torch.bfloat16)
+    idx = torch.argsort(torch.rand(T, E, device=dev, generator=g), dim=1)[:, :K].to(torch.int32)
+    aff = torch.zeros(T, E, device=dev).scatter_(1, idx.long(), 1.0 / K)
+    post = ExpertAffinityScaleMode.POST_SCALE
+    run = lambda: mk.moe_prefill(x, gu, dn, aff, idx, expert_affinities_scaling_mode=post)
+    for _ in range(max(args.warmup, 2)):
+        run()
+    torch.cuda.synchronize()
+    n = max(args.steps, 4)
+    kern = {}
+    for cls in ("moe_gate_up", "moe_down"):
+        st = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        sp = [torch.cuda.Event(enable_timing=True) for _ in range(n)]
+        for e in st + sp:
+            e.record()                         # creates the events
+        torch.cuda.synchronize()
+        arr = lambda es: (L.vp * n)(*[e.cuda_event for e in es])
+        L.check(lib.mkd_profile_events(L.KCLASS[cls], arr(st), arr(sp), n), "arm")
+        try:
+            for _ in range(n):
+                run()
+            torch.cuda.synchronize()
+        finally:
+            L.check(lib.mkd_profile_events(-1, None, None, 0), "off")
+        kern[cls] = sum(a.elapsed_time(b) for a, b in zip(st, sp)) / n * 1e3   # us
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(n):
+        run()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    fl_gu, fl_dn = 2.0 * T * K * H * 2 * I, 2.0 * T * K * I * H
+    gu_tf = fl_gu / kern["moe_gate_up"] / 1e6
+    dn_tf = fl_dn / kern["moe_down"] / 1e6
+    # the same per-expert gate/up shape through torch.matmul (hipBLASLt), one call per expert
+    xs = torch.randn(T * K // E, H, device=dev).to(torch.bfloat16)
+    wt = torch.randn(2 * I, H, device=dev).to(torch.bfloat16).t().contiguous()
+    for _ in range(3):
+        torch.matmul(xs, wt)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(E):
+        torch.matmul(xs, wt)
+    e1.record()
+    torch.cuda.synchronize()
+    bl_tf = fl_gu / (e0.elapsed_time(e1) * 1e3) / 1e6
+    line = {
+        "metric": "MoE expert GEMM throughput in the MFMA regime (moe_prefill, grouped bf16 GEMMs)",
+        "value": round((fl_gu + fl_dn) / (ms * 1e3) / 1e6, 1), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": n, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded random bf16 weights N(0,0.02), hidden N(0,1), uniform top-8 routing)",
+        "config": {"workload": f"Qwen3-30B-A3B expert shape (E=128, K=8, H=2048, I=768), "
+                               f"{T} tokens = ~{T * K // E} tokens/expert, whole moe_prefill",
+                   "tokens": T, "tokens_per_expert": T * K // E,
+                   "gate_up_us": round(kern["moe_gate_up"], 1), "down_us": round(kern["moe_down"], 1),
+                   "down_TFLOPs": round(dn_tf, 1), "down_mfma_frac": round(dn_tf / MFMA_BF16_PEAK_TFLOPS, 4),
+                   "hipblaslt_per_expert_gate_up_TFLOPs": round(bl_tf, 1)},
+        "roofline": {"bound": "mfma", "kernel": "gate/up grouped GEMM (gemm_tile_kernel<3>)",
+                     "achieved": round(gu_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(gu_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
+                     "flops_per_launch": fl_gu, "avg_us": round(kern["moe_gate_up"], 1)},
+    }
+    print(json.dumps(line), flush=True)
 
 
 def vs_baseline(tok_s, cfg, B, ctx, args):

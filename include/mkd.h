@@ -188,7 +188,7 @@ int mkd_moe_tkg(const mkd_moe_args* args, void* workspace, size_t workspace_byte
  * selective mode stops at T <= 128 (moe_tkg.py:388-392) and has no
  * counterpart for this entry; it measures the MFMA-bound regime with the same
  * packed weights and arguments.  bf16 weights only; 1 <= T <= 65535,
- * T*K <= 2^24; H and I multiples of 32.  Workspace: mkd_moe_workspace_bytes. */
+ * T*K <= 2^23; H and I multiples of 32.  Workspace: mkd_moe_workspace_bytes. */
 int mkd_moe_prefill(const mkd_moe_args* args, void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------

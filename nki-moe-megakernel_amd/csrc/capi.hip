@@ -310,7 +310,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
       a.act = act; a.alpha = alpha; a.gate_hi = ghi; a.gate_lo = glo; a.up_hi = uhi; a.up_lo = ulo;
       a.round_qwen = round_qwen;
       const int ps = prof_begin(MKD_KCLASS_MOE_GATE_UP, s);
-      MKD_TRY(gemm_tile_launch(a, EPI_SWIGLU_BF16, gmax, T, s), "moe gate_up (tiled)");
+      MKD_TRY(gemm_tile_launch(a, EPI_SWIGLU_BF16, gmax, (long long)T * K, s), "moe gate_up (tiled)");
       prof_end(ps, s);
     }
     {
@@ -321,7 +321,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
       a.pair_scale = slot_w;
       a.bias = dn_bias; a.bias_group_stride = H;
       const int ps = prof_begin(MKD_KCLASS_MOE_DOWN, s);
-      MKD_TRY(gemm_tile_launch(a, EPI_SCALE_F32, gmax, T, s), "moe down (tiled)");
+      MKD_TRY(gemm_tile_launch(a, EPI_SCALE_F32, gmax, (long long)T * K, s), "moe down (tiled)");
       prof_end(ps, s);
     }
     if (do_finalize)
@@ -468,8 +468,8 @@ int moe_entry(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, vo
   MKD_REQUIRE(p->hidden && p->gate_up_packed && p->down_packed && p->expert_index && p->output,
               MKD_ERR_NULL, "moe_tkg: null pointer");
   if (tiled) {
-    MKD_REQUIRE(p->T > 0 && p->T <= 65535 && (long long)p->T * p->K <= (1 << 24), MKD_ERR_INVALID,
-                "moe_prefill: T %d must be in [1, 65535] with T*K <= 2^24", p->T);
+    MKD_REQUIRE(p->T > 0 && p->T <= 65535 && (long long)p->T * p->K <= (1 << 23), MKD_ERR_INVALID,
+                "moe_prefill: T %d must be in [1, 65535] with T*K <= 2^23", p->T);
     MKD_REQUIRE(p->weight_format == 0, MKD_ERR_UNSUPPORTED, "moe_prefill: bf16 expert weights only");
     MKD_REQUIRE(gemm_tile_supported(2 * p->I, p->H, EPI_SWIGLU_BF16) &&
                     gemm_tile_supported(p->H, p->I, EPI_SCALE_F32),

@@ -11,7 +11,7 @@
 // and barrier waits).  A stage is 16 A fragments (each a contiguous 1 KiB
 // run of the packed weights) and 16 B fragments (16 tokens x 32 k, gathered
 // through the routing table), copied global -> LDS directly in MFMA operand
-// order (global_load_lds_dwordx4), three stages ahead in a ring of four LDS
+// order (buffer_load_dwordx4 ... lds), three stages ahead in a ring of four LDS
 // buffers (128 KiB); one barrier per stage.  Per stage a wave issues 32 MFMAs
 // against 12 contiguous 1 KiB LDS reads.
 //
@@ -37,114 +37,174 @@ constexpr int kLdsBytes = kStages * kStageFrags * 1024;
 
 // s_waitcnt with only vmcnt = n (expcnt / lgkmcnt left at their maxima); gfx9
 // encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14.
+// One 1 KiB fragment into LDS: lane l's 16 bytes from byte offset voff of the
+// buffer land at dst + 16 l (buffer_load_dwordx4 ... lds; dst is wave-uniform).
+// A plain function so that the builtin stays out of template instantiation.
+MKD_DEV void copy_frag_lds(__amdgpu_buffer_rsrc_t src, u32x4_t* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, voff,
+                                           0, 0, 0);
+}
+
 template <int N>
 MKD_DEV void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+
+}  // namespace
+
 template <int EPI>
 __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
+  constexpr int NW = 8;                  // waves: 2 (rows) x 4 (tokens)
+  constexpr int WT = 4;                  // token tiles per wave
+  constexpr int FPW = kStageFrags / NW;  // fragments copied per wave per stage
   extern __shared__ u32x4_t lds[];       // [kStages][kStageFrags][64 lanes]: A tiles 0..15, B 16..31
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int wm = w & 1, wn = w >> 1;     // wave: 128 rows (wm) x 64 tokens (wn)
-  // XCD-aware tile order: blocks are dealt round-robin to the 8 XCDs by linear
-  // id, so linear id L runs logical tile (L % 8) * per + L / 8 -- each XCD
-  // walks a contiguous run of (n tile, token tile, group), and the blocks that
-  // share an expert's weight and token tiles run together on one XCD's L2.
-  const int gx = gridDim.x, gy = gridDim.y;
-  const int total = gx * gy * gridDim.z;
-  const int per = (total + 7) / 8;
-  const int L = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
-  const int lt = (L % 8) * per + L / 8;
-  if (lt >= total) return;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform in an SGPR
+  const int wm = w & 1, wn = w >> 1;     // wave: 128 rows (wm) x 16*WT tokens (wn)
+  // Grid (n tile, work item).  Work items are the token tiles of all groups in
+  // group order (group g owns ceil(count_g / 256) consecutive items); the grid
+  // holds an upper bound (ceil(T*K / 256) + groups) and the block finds its
+  // group by a scan of the device-side group counts.  XCD-aware order: blocks
+  // are dealt round-robin to the 8 XCDs by linear id, so each XCD is given a
+  // contiguous run of logical tiles (n tile fastest, then item): the blocks
+  // that share an expert's weight tiles and token rows run together on one
+  // XCD's L2.
+  __shared__ int scan_s[8], item_s[3];
+  const int gx = gridDim.x;
+  const int total = gx * gridDim.y;
+  const int L = blockIdx.x + gx * blockIdx.y;
+  // XCD x (= L % 8) owns the contiguous logical range starting at x*q + min(x, r)
+  // of q or q + 1 tiles (total = 8q + r): a bijection of [0, total)
+  const int q8 = total / 8, r8 = total % 8, xcd = L % 8;
+  const int lt = xcd * q8 + min(xcd, r8) + L / 8;
   const int nb0 = (lt % gx) * kRB;
-  const int t0 = ((lt / gx) % gy) * kTileTok;
-  const int group = lt / (gx * gy);
+  const int item = lt / gx;
 
-  int count, base;
+  int count, base, t0, expert = 0;
   const uint16_t* wp = a.w;
   if (a.grp_expert) {
+    // thread g holds group g's token-tile count (<= 512 groups); block-wide
+    // inclusive scan in group order; the owner of `item` publishes it
     const int ng = *a.n_groups;
-    count = a.grp_count[group];
-    base = a.grp_offset[group];
-    const int ex = a.grp_expert[group];
-    asm volatile("" ::"s"(ng), "s"(count), "s"(base), "s"(ex));
-    if (group >= ng) return;
-    wp += (long long)ex * a.w_group_stride;
+    const int c = tid < ng ? a.grp_count[tid] : 0;
+    const int tiles = (c + kTileTok - 1) / kTileTok;
+    int x = tiles;                       // wave inclusive scan (64 lanes)
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int y = __shfl_up(x, o, 64);
+      if (lane >= o) x += y;
+    }
+    if (lane == 63) scan_s[w] = x;
+    if (tid == 0) item_s[0] = -1;
+    __syncthreads();
+    int before = 0;
+    for (int q = 0; q < w; ++q) before += scan_s[q];
+    const int incl = before + x, excl = incl - tiles;
+    if (tid < ng && item >= excl && item < incl) {
+      item_s[0] = tid;
+      item_s[1] = (item - excl) * kTileTok;
+    }
+    __syncthreads();
+    const int g = item_s[0];
+    if (g < 0) return;                   // past the last live token tile (uniform)
+    t0 = item_s[1];
+    count = a.grp_count[g];
+    base = a.grp_offset[g];
+    expert = a.grp_expert[g];
+    wp += (long long)expert * a.w_group_stride;
   } else {
     count = a.T;
     base = 0;
+    t0 = item * kTileTok;
+    if (t0 >= count) return;
   }
-  if (t0 >= count) return;
 
   const int KB = a.K / 32;
   const int NB = (a.N + 15) / 16;
   const int S = KB;                      // one 32-wide fragment per stage
 
   // ---- loads: wave w moves fragments f = w + 8j (j < 4) of each stage, one
-  // 1 KiB fragment per global_load_lds_dwordx4 (lane l's 16 bytes land at
-  // l * 16 of the fragment's LDS slot).  f < 16: A row block f (the packed
-  // weights are already in operand order).  f >= 16: B token tile f - 16, lane
-  // l = token l%16, k (l/16)*8 .. +8 of its routed row.
-  const uint16_t* src[4];
+  // 1 KiB fragment per buffer_load_dwordx4 ... lds (lane l's 16 bytes land at
+  // l * 16 of the fragment's LDS slot; the MUBUF form is tracked by vmcnt
+  // alone, so LDS reads issued around it keep their own lgkmcnt waits).
+  // f < 16: A row block f (the packed weights are already in operand order).
+  // f >= 16: B token tile f - 16, lane l = token l%16, k (l/16)*8 .. +8 of its
+  // routed row.  Offsets are bytes from the expert's weights / from x.
+  const __amdgpu_buffer_rsrc_t wsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(wp), 0, 0x7fffffff, 0x00020000);
+  const __amdgpu_buffer_rsrc_t xsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(a.x), 0, 0x7fffffff, 0x00020000);
+  int voff[FPW];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int f = w + 8 * j;
-    if (f < kRB) {
-      const int nb = min(nb0 + f, NB - 1);         // rows past N: any valid block
-      src[j] = wp + (long long)nb * KB * 512 + lane * 8;
-    } else {
-      const int c = min(t0 + (f - kRB) * 16 + (lane & 15), count - 1);   // absent: any valid row
-      const int row = a.pair_row ? a.pair_row[base + c] : base + c;
-      src[j] = static_cast<const uint16_t*>(a.x) + (long long)row * a.ldx + (lane >> 4) * 8;
-    }
+  for (int j = 0; j < FPW; ++j) {
+    const int f = w + NW * j;
+    const int nb = min(nb0 + f, NB - 1);           // rows past N: any valid block
+    voff[j] = f < kRB ? ((nb * KB) * 512 + lane * 8) * 2 : 0;
   }
-  auto issue = [&](int s) {
-    u32x4_t* dst = lds + (s % kStages) * kStageFrags * 64;
+  auto issue = [&](int s, int buf) {
+    u32x4_t* dst = lds + buf * kStageFrags * 64;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int f = w + 8 * j;
-      const long long step = f < kRB ? (long long)s * 512 : (long long)s * 32;
-      __builtin_amdgcn_global_load_lds(src[j] + step, dst + f * 64, 16, 0, 0);
+    for (int j = 0; j < FPW; ++j) {
+      const int f = w + NW * j;
+      if (f < kRB)   // wave-uniform: j and w fix f
+        copy_frag_lds(wsrc, dst + f * 64, voff[j] + s * 1024);
+      else
+        copy_frag_lds(xsrc, dst + f * 64, voff[j] + s * 64);
     }
   };
 
-  f32x4_t acc[8][4];
+#pragma unroll
+  for (int j = 0; j < FPW; ++j) {
+    const int f = w + NW * j;
+    if (f >= kRB) {
+      const int c = min(t0 + (f - kRB) * 16 + (lane & 15), count - 1);   // absent: any valid row
+      const int row = a.pair_row ? a.pair_row[base + c] : base + c;
+      voff[j] = (row * a.ldx + (lane >> 4) * 8) * 2;
+    }
+  }
+  f32x4_t acc[8][WT];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int j = 0; j < WT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int s = 0; s < kStages - 1 && s < S; ++s) issue(s);
+  for (int s = 0; s < kStages - 1; ++s) issue(min(s, S - 1), s);
   for (int s = 0; s < S; ++s) {
-    // this thread's loads of stage s have landed once at most the later issued
-    // stages (4 loads each) are outstanding; the barrier then makes every
-    // wave's stage s visible and frees the buffer of stage s - 1
-    const int later = min(kStages - 2, S - 1 - s);
-    if (later >= 2) wait_vmcnt<8>();
-    else if (later == 1) wait_vmcnt<4>();
-    else wait_vmcnt<0>();
+    // this thread's loads of stage s have landed once at most the two later
+    // issued stages (4 loads each) are outstanding -- every iteration issues
+    // one stage, so the count is the same throughout; the barrier then makes
+    // every wave's stage s visible and frees the buffer of stage s - 1
+    wait_vmcnt<2 * FPW>();
     asm volatile("s_barrier" ::: "memory");
-    if (s + kStages - 1 < S) issue(s + kStages - 1);
     const u32x4_t* st = lds + (s % kStages) * kStageFrags * 64;
-    u32x4_t af[8], bf[4];
+    // B first, then A in MFMA order: the MFMAs of row block i wait only for
+    // the reads up to af[i] (LDS returns in order), so they start early
+    u32x4_t af[8], bf[WT];
+#pragma unroll
+    for (int j = 0; j < WT; ++j) bf[j] = st[(kRB + wn * WT + j) * 64 + lane];
 #pragma unroll
     for (int i = 0; i < 8; ++i) af[i] = st[(wm * 8 + i) * 64 + lane];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bf[j] = st[(kRB + wn * 4 + j) * 64 + lane];
     __builtin_amdgcn_sched_barrier(0);     // all 12 operand reads in flight together
+    // the copies of stage s + 3 go out behind the reads (into the buffer that
+    // stage s - 1 used, which every wave has left: barrier above); past the
+    // last stage the last stage is copied again into that dead buffer, which
+    // keeps the loop free of branches and the wait count fixed
+    issue(min(s + kStages - 1, S - 1), (s + kStages - 1) % kStages);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int i = 0; i < 8; ++i)
+    for (int i = 0; i < 8; ++i) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+      for (int j = 0; j < WT; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);   // row-block order: group i waits for af[i] only
+    }
   }
 
   // ---- epilogue: lane holds rows 4*(lane/16)+e of each row block, token lane%16 ----
   const int q4 = (lane >> 4) * 4;
   if (EPI == EPI_SWIGLU_BF16) {
     const int I = a.N / 2;
-    const uint16_t* bp = a.bias ? a.bias + (a.grp_expert ? (long long)a.grp_expert[group] * a.bias_group_stride : 0)
-                                : nullptr;
+    const uint16_t* bp = a.bias ? a.bias + (long long)expert * a.bias_group_stride : nullptr;
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int nbg = nb0 + wm * 8 + 2 * p;           // gate row block (even), up = nbg + 1
@@ -156,8 +216,8 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
         for (int e = 0; e < 4; ++e) { gb[e] = bf2f(bp[n + e]); ub[e] = bf2f(bp[I + n + e]); }
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tc = t0 + (wn * 4 + j) * 16 + (lane & 15);
+      for (int j = 0; j < WT; ++j) {
+        const int tc = t0 + (wn * WT + j) * 16 + (lane & 15);
         if (tc >= count) continue;
         const int orow = a.pair_out_row ? a.pair_out_row[base + tc] : base + tc;
         float o[4];
@@ -169,8 +229,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
       }
     }
   } else {   // EPI_SCALE_F32
-    const uint16_t* bp = a.bias ? a.bias + (a.grp_expert ? (long long)a.grp_expert[group] * a.bias_group_stride : 0)
-                                : nullptr;
+    const uint16_t* bp = a.bias ? a.bias + (long long)expert * a.bias_group_stride : nullptr;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int nb = nb0 + wm * 8 + i;
@@ -182,8 +241,8 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
         for (int e = 0; e < 4; ++e) bb[e] = (n + e < a.N) ? bf2f(bp[n + e]) : 0.f;
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int tc = t0 + (wn * 4 + j) * 16 + (lane & 15);
+      for (int j = 0; j < WT; ++j) {
+        const int tc = t0 + (wn * WT + j) * 16 + (lane & 15);
         if (tc >= count) continue;
         const int orow = a.pair_out_row ? a.pair_out_row[base + tc] : base + tc;
         const float sc = a.pair_scale ? a.pair_scale[orow] : 1.0f;
@@ -199,9 +258,9 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
       }
     }
   }
+  wait_vmcnt<0>();                       // no copy into LDS outlives the block
 }
 
-}  // namespace
 
 int gemm_tile_lds_bytes() { return kLdsBytes; }
 
@@ -211,18 +270,25 @@ bool gemm_tile_supported(int N, int K, int epi) {
   return epi == EPI_SCALE_F32;
 }
 
-hipError_t gemm_tile_launch(const GemmArgs& a, int epi, int groups_max, int max_tokens_per_group,
+hipError_t gemm_tile_launch(const GemmArgs& a, int epi, int groups_max, long long total_rows,
                             hipStream_t s) {
-  if (!gemm_tile_supported(a.N, a.K, epi) || groups_max <= 0 || max_tokens_per_group <= 0)
+  if (!gemm_tile_supported(a.N, a.K, epi) || groups_max <= 0 || total_rows <= 0)
     return hipErrorInvalidValue;
-  const dim3 grid((a.N + kTileRows - 1) / kTileRows, (max_tokens_per_group + kTileTok - 1) / kTileTok,
-                  a.grp_expert ? groups_max : 1);
-  const void* fn = epi == EPI_SWIGLU_BF16 ? reinterpret_cast<const void*>(gemm_tile_kernel<EPI_SWIGLU_BF16>)
-                                          : reinterpret_cast<const void*>(gemm_tile_kernel<EPI_SCALE_F32>);
+  // work items: every group's token tiles; with total_rows = sum of the group
+  // sizes, sum_g ceil(c_g / 256) <= ceil(total_rows / 256) + groups
+  const long long items = (total_rows + kTileTok - 1) / kTileTok + (a.grp_expert ? groups_max : 0);
+  if (items > 65535) return hipErrorInvalidValue;
+  const dim3 grid((a.N + kTileRows - 1) / kTileRows, (unsigned)items);
   // 128 KiB of dynamic LDS is above the default launch limit (set per kernel)
-  if (hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes)) return e;
-  if (epi == EPI_SWIGLU_BF16)
+  if (epi == EPI_SWIGLU_BF16) {
+    if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tile_kernel<EPI_SWIGLU_BF16>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes))
+      return e;
     return timed_launch(gemm_tile_kernel<EPI_SWIGLU_BF16>, grid, dim3(512), kLdsBytes, s, a);
+  }
+  if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tile_kernel<EPI_SCALE_F32>),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes))
+    return e;
   return timed_launch(gemm_tile_kernel<EPI_SCALE_F32>, grid, dim3(512), kLdsBytes, s, a);
 }
 

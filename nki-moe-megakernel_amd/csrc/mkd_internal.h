@@ -90,7 +90,8 @@ hipError_t gemm_mx_launch(GemmArgs a, int fmt, int epi, int groups_max, int max_
 int choose_kw_mx(int K_pad);
 // gemm_tile.hip: LDS-tiled grouped GEMM (many tokens per expert)
 bool gemm_tile_supported(int N, int K, int epi);
-hipError_t gemm_tile_launch(const GemmArgs& a, int epi, int groups_max, int max_tokens_per_group,
+// total_rows: the sum of the group sizes (grouped mode: T*K pairs), else the rows.
+hipError_t gemm_tile_launch(const GemmArgs& a, int epi, int groups_max, long long total_rows,
                             hipStream_t s);
 int mx_kpad(int K);   // contraction padding of the packed MX layout
 
