@@ -756,7 +756,7 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.r = c.take<uint16_t>((size_t)B * m->H);
   w.nbf = c.take<uint16_t>((size_t)B * m->H);
   w.nf32 = c.take<float>((size_t)B * m->H);
-  w.logits = c.take<float>((size_t)router_kgrid(m->E, m->H) * B * m->E);  // split-K partials
+  w.logits = c.take<float>((size_t)16 * B * m->E);  // split-K partials (<= 16)
   w.cos = c.take<float>((size_t)B * m->d);
   w.sin = c.take<float>((size_t)B * m->d);
   w.oparts = c.take<float>((size_t)2 * B * m->H);      // o_proj split-K partials
@@ -857,18 +857,6 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     ap.round_qwen = oss ? 0 : 1;
     if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s, w.oparts, o_kgrid))
       return rc;
-    // r = bf16(x + bf16(o_proj)) from the split-K partials, then the post-attention
-    // RMSNorm: bf16 copy for the experts, fp32 copy for the router
-    {
-      NormArgs na = {};
-      na.x = x; na.ld_in = m->H;
-      na.dsum = w.oparts; na.dK = o_kgrid; na.ds_row = m->H; na.ds_k = (long long)B * m->H;
-      na.resid_out = w.r;
-      na.gamma = static_cast<const uint16_t*>(m->ln_post[l]);
-      na.out_bf16 = w.nbf; na.out_f32 = oss ? nullptr : w.nf32;
-      na.rows = B; na.H = m->H; na.hidden_actual = ha; na.eps = m->eps; na.order = 0;
-      MKD_TRY(norm_launch(na, s), "residual + post norm");
-    }
     // router (split-K GEMM) + top-k + expert groups in one select launch: Qwen
     // fp32 input and fused flow; GPT-OSS bf16 input, biased logits, top-k then
     // softmax over the top-k (router_topk.py:868-887)
@@ -880,12 +868,41 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     ra.n_groups = w.moe.n_groups; ra.grp_expert = w.moe.grp_expert;
     ra.grp_count = w.moe.grp_count; ra.grp_offset = w.moe.grp_offset;
     ra.pair_token = w.moe.pair_token; ra.pair_slot = w.moe.pair_slot;
-    {
+    if (router_fused_supported(B, m->E, m->H)) {
+      // a few tokens: the residual add and post norm are folded into the router
+      // GEMM (each block forms the row norms itself), then the select launch
+      RouterFusedArgs fa = {};
+      fa.r = ra;
+      fa.r.parts = w.logits;
+      fa.x = x; fa.o = w.oparts;
+      fa.gamma = static_cast<const uint16_t*>(m->ln_post[l]);
+      fa.eps = m->eps; fa.inv_h = 1.0f / (float)ha; fa.H = m->H;
+      fa.resid_out = w.r; fa.hnorm = w.nbf;
+      fa.w = static_cast<const uint16_t*>(m->router[l]);
+      fa.x_f32 = oss ? 0 : 1;
       const int ps = prof_begin(MKD_KCLASS_ROUTER, s);
-      if (int rc = router_stage(oss ? static_cast<const void*>(w.nbf) : w.nf32, !oss, m->H,
-                                m->router[l], w.logits, ra, s))
-        return rc;
+      MKD_TRY(router_fused_launch(fa, s), "residual + post norm + router");
       prof_end(ps, s);
+    } else {
+      // r = bf16(x + bf16(o_proj)) from the split-K partials, then the post-attention
+      // RMSNorm: bf16 copy for the experts, fp32 copy for the router
+      {
+        NormArgs na = {};
+        na.x = x; na.ld_in = m->H;
+        na.dsum = w.oparts; na.dK = o_kgrid; na.ds_row = m->H; na.ds_k = (long long)B * m->H;
+        na.resid_out = w.r;
+        na.gamma = static_cast<const uint16_t*>(m->ln_post[l]);
+        na.out_bf16 = w.nbf; na.out_f32 = oss ? nullptr : w.nf32;
+        na.rows = B; na.H = m->H; na.hidden_actual = ha; na.eps = m->eps; na.order = 0;
+        MKD_TRY(norm_launch(na, s), "residual + post norm");
+      }
+      {
+        const int ps = prof_begin(MKD_KCLASS_ROUTER, s);
+        if (int rc = router_stage(oss ? static_cast<const void*>(w.nbf) : w.nf32, !oss, m->H,
+                                  m->router[l], w.logits, ra, s))
+          return rc;
+        prof_end(ps, s);
+      }
     }
     if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], nullptr, w.moe.slot_w,
                           static_cast<const uint16_t*>(at(m->gate_up_bias, l)),

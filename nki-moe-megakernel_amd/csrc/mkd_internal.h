@@ -182,6 +182,23 @@ struct RouterArgs {
   int *n_groups, *grp_expert, *grp_count, *grp_offset, *pair_token, *pair_slot;
 };
 hipError_t router_select_launch(const RouterArgs& a, hipStream_t s);
+// Residual add + post-attention RMSNorm folded into the split-K router GEMM, then
+// the select launch, for a handful of tokens (router_fused_supported).  r.parts
+// must hold 16 * T * E floats.
+struct RouterFusedArgs {
+  RouterArgs r;               // T, E, K, mode, bias, outputs and grouping (parts unused)
+  const uint16_t* x;          // [T, H] bf16 residual stream
+  const float* o;             // [T, H] fp32 attention output projection
+  const uint16_t* gamma;      // [H] post-attention norm weight
+  float eps, inv_h;
+  int H;
+  uint16_t* resid_out;        // [T, H] bf16(x + bf16(o))
+  uint16_t* hnorm;            // [T, H] bf16 normalised rows (expert input)
+  const uint16_t* w;          // router weights [E, H], frag-packed
+  int x_f32;                  // router input: 1 fp32 normalised rows (bf16 hi + lo), 0 bf16
+};
+bool router_fused_supported(int T, int E, int H);
+hipError_t router_fused_launch(RouterFusedArgs a, hipStream_t s);
 hipError_t moe_route_launch(const int* idx, int T, int K, int E, int* n_groups, int* grp_expert,
                             int* grp_count, int* grp_offset, int* pair_token, int* pair_slot,
                             hipStream_t s);

@@ -105,8 +105,11 @@ MKD_DEV void load_logits(const RouterArgs& a, int t, int lane, float (&l)[PER]) 
   }
 }
 
-template <int PER>
-__global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
+// Top-k, weights and expert grouping for the T tokens of one block (16 waves;
+// wave w takes tokens w, w+16, ...).  load(t, l) fills the lane's logits l[j] of
+// experts lane + 64 j (bias included).
+template <int PER, class Load>
+MKD_DEV void select_body(const RouterArgs& a, Load&& load) {
   __shared__ uint32_t cu_s[16][8];
   __shared__ int ce_s[16][8], slot_s[16][8];
   __shared__ float ck_s[16][8];
@@ -117,20 +120,10 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
   const int E = a.E, K = a.K, T = a.T;
   const bool sigm = a.mode & 1, pre = a.mode & 2, norm = a.mode & 4, qwen = a.mode & 8;
-  // the first token's logits are loaded before anything else (their latency
-  // covers the LDS set-up; the first block barrier comes after the per-token
-  // phase, which only touches the wave's own LDS rows)
-  float lfirst[PER];
-  if (wv < T) load_logits<PER>(a, wv, lane, lfirst);
   for (int e = tid; e < E; e += blockDim.x) { cnt[e] = 0; cursor[e] = 0; }
   for (int t = wv; t < T; t += 16) {
     float l[PER];
-    if (t == wv) {
-#pragma unroll
-      for (int j = 0; j < PER; ++j) l[j] = lfirst[j];
-    } else {
-      load_logits<PER>(a, t, lane, l);
-    }
+    load(t, l);
     // every slot of the token starts invalid so that NaN logits (no consistent
     // ranks) can never route a slot to an out-of-range expert below
     if (lane < K) idx_s[t * K + lane] = -1;
@@ -296,6 +289,24 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
   }
 }
 
+template <int PER>
+__global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+  // the first token's logits are loaded before anything else (their latency
+  // covers the LDS set-up; the first block barrier comes after the per-token
+  // phase, which only touches the wave's own LDS rows)
+  float lfirst[PER];
+  if (wv < a.T) load_logits<PER>(a, wv, lane, lfirst);
+  select_body<PER>(a, [&](int t, float (&l)[PER]) {
+    if (t == wv) {
+#pragma unroll
+      for (int j = 0; j < PER; ++j) l[j] = lfirst[j];
+    } else {
+      load_logits<PER>(a, t, lane, l);
+    }
+  });
+}
+
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(1024)
 moe_route_kernel(const int* __restrict__ idx, int T, int K, int E, int* __restrict__ n_groups,
@@ -372,6 +383,142 @@ moe_finalize_kernel(const float* __restrict__ ybuf, int K, int H, const uint16_t
 }
 
 // ---------------------------------------------------------------------------
+// ---------------------------------------------------------------------------
+// Router logits with the residual add and post-attention RMSNorm folded in, for
+// T <= 4 tokens.  Grid (E/16 row blocks, KG contraction slices), one wave per
+// block; the block writes the split-K partial logits that router_select sums:
+//   r = bf16(x + bf16(o))            residual stream (slice written by row block 0)
+//   y = (r * gamma) * rsqrt(mean_actual(r^2) + eps)   (bf16 copy of the slice written)
+//   part[kg][t][e] = sum over the slice of y * W_router   (fp32 y as bf16 hi + lo)
+// Every block reads the T full rows to form the sum of squares itself (a few KB
+// from L2), which removes the separate norm launch (moe_fused_nki.py:70-153,
+// router_topk.py:337-410).
+constexpr int kFusedMaxT = 4;
+
+// Contraction slices: enough blocks (>= ~128) with whole fragments per slice.
+static int fused_kg(int E, int H) {
+  const int KB = H / 32;
+  int kg = 1;
+  while (kg < 16 && (E / 16) * kg < 128 && KB % (kg * 2) == 0) kg *= 2;
+  return kg;
+}
+
+bool router_fused_supported(int T, int E, int H) {
+  return T >= 1 && T <= kFusedMaxT && E % 16 == 0 && E <= kMaxE && H % 32 == 0 && H > 0 &&
+         (H / 32) % fused_kg(E, H) == 0 && (H / 32) / fused_kg(E, H) <= 8;
+}
+
+__global__ void __launch_bounds__(64) router_norm_gemm_kernel(RouterFusedArgs a, int kg) {
+  const int lane = threadIdx.x;
+  const int rb = blockIdx.x, kblk = blockIdx.y;
+  const int T = a.r.T, E = a.r.E, H = a.H, KB = H / 32;
+  const int nf = KB / kg;                // fragments of this slice
+  const int kb0 = kblk * nf;
+  const int tcol = lane & 15, koff = (lane >> 4) * 8;
+  const bool live = tcol < T;
+  constexpr int MAXF = 8;                // fragments per slice (router_fused_supported)
+
+  // ---- loads, all independent: weight fragments, the lane's operand values,
+  // gamma, and a 1/64 share of every row for the sum of squares ----
+  u32x4_t wf[MAXF];
+  const uint16_t* wrow = a.w + ((long long)rb * KB + kb0) * 512 + lane * 8;
+#pragma unroll
+  for (int u = 0; u < MAXF; ++u)
+    if (u < nf) wf[u] = ld16(wrow + u * 512);
+  u32x4_t xb[MAXF], gb[MAXF];
+  f32x4_t o0[MAXF], o1[MAXF];
+  const int tr = live ? tcol : 0;
+#pragma unroll
+  for (int u = 0; u < MAXF; ++u)
+    if (u < nf) {
+      const int k = (kb0 + u) * 32 + koff;
+      xb[u] = ld16(a.x + (long long)tr * H + k);
+      gb[u] = ld16(a.gamma + k);
+      o0[u] = *reinterpret_cast<const f32x4_t*>(a.o + (long long)tr * H + k);
+      o1[u] = *reinterpret_cast<const f32x4_t*>(a.o + (long long)tr * H + k + 4);
+    }
+  // sum of squares of r over the whole row, lane share: H / 64 elements
+  float ss[kFusedMaxT];
+#pragma unroll
+  for (int t = 0; t < kFusedMaxT; ++t) {
+    ss[t] = 0.f;
+    if (t >= T) continue;
+    for (int c = lane * 8; c < H; c += 512) {
+      const u32x4_t xv = ld16(a.x + (long long)t * H + c);
+      const f32x4_t p = *reinterpret_cast<const f32x4_t*>(a.o + (long long)t * H + c);
+      const f32x4_t q = *reinterpret_cast<const f32x4_t*>(a.o + (long long)t * H + c + 4);
+      const float ov[8] = {p[0], p[1], p[2], p[3], q[0], q[1], q[2], q[3]};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xv_j = (j & 1) ? bf_hi(xv[j >> 1]) : bf_lo(xv[j >> 1]);
+        const float r = rbf(xv_j + rbf(ov[j]));
+        ss[t] += r * r;
+      }
+    }
+  }
+  float rinv_t[kFusedMaxT];
+#pragma unroll
+  for (int t = 0; t < kFusedMaxT; ++t) rinv_t[t] = 1.0f / sqrtf(wave_sum(ss[t]) * a.inv_h + a.eps);
+  float rinv = rinv_t[0];
+#pragma unroll
+  for (int t = 1; t < kFusedMaxT; ++t)
+    if (tcol == t) rinv = rinv_t[t];
+
+  // ---- operands: y for the lane's token and k range, MFMAs ----
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < MAXF; ++u) {
+    if (u >= nf) break;
+    const int k = (kb0 + u) * 32 + koff;
+    const float ov[8] = {o0[u][0], o0[u][1], o0[u][2], o0[u][3], o1[u][0], o1[u][1], o1[u][2], o1[u][3]};
+    float r[8], y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float xv_j = (j & 1) ? bf_hi(xb[u][j >> 1]) : bf_lo(xb[u][j >> 1]);
+      const float g = (j & 1) ? bf_hi(gb[u][j >> 1]) : bf_lo(gb[u][j >> 1]);
+      r[j] = rbf(xv_j + rbf(ov[j]));
+      y[j] = live ? (r[j] * g) * rinv : 0.f;
+    }
+    if (rb == 0 && live) {   // the slice's residual and bf16 normalised rows
+      u32x4_t ro, yo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        ro[j] = pack2bf(r[2 * j], r[2 * j + 1]);
+        yo[j] = pack2bf(y[2 * j], y[2 * j + 1]);
+      }
+      st16(a.resid_out + (long long)tcol * H + k, ro);
+      st16(a.hnorm + (long long)tcol * H + k, yo);
+    }
+    u32x4_t hi, lo;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float y0 = a.x_f32 ? y[2 * j] : rbf(y[2 * j]);
+      const float y1 = a.x_f32 ? y[2 * j + 1] : rbf(y[2 * j + 1]);
+      const uint32_t h0 = f2bf(y0), h1 = f2bf(y1);
+      hi[j] = h0 | (h1 << 16);
+      lo[j] = f2bf(y0 - bf2f(h0)) | (f2bf(y1 - bf2f(h1)) << 16);
+    }
+    acc = mfma16x16x32(wf[u], hi, acc);
+    if (a.x_f32) acc = mfma16x16x32(wf[u], lo, acc);
+  }
+  // D lane l: experts rb*16 + 4*(l/16) + i, token l%16 -> part[kblk][t][e]
+  if (live) {
+    float* pp = const_cast<float*>(a.r.parts) + kblk * a.r.part_stride + (long long)tcol * E + rb * 16 + (lane >> 4) * 4;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pp[i] = acc[i];
+  }
+}
+
+hipError_t router_fused_launch(RouterFusedArgs a, hipStream_t s) {
+  if (!router_fused_supported(a.r.T, a.r.E, a.H) || !a.r.parts) return hipErrorInvalidValue;
+  const int kg = fused_kg(a.r.E, a.H);
+  a.r.nparts = kg;
+  a.r.part_stride = (long long)a.r.T * a.r.E;
+  if (hipError_t e = timed_launch(router_norm_gemm_kernel, dim3(a.r.E / 16, kg), dim3(64), 0, s, a, kg))
+    return e;
+  return router_select_launch(a.r, s);
+}
+
 hipError_t router_select_launch(const RouterArgs& a, hipStream_t s) {
   if (a.E > kMaxE || a.K > 8 || a.K < 1 || a.K > a.E || a.T > 128 || a.T < 1 || a.nparts > 16)
     return hipErrorInvalidValue;
