@@ -182,6 +182,44 @@ MKD_DEV long long kv_write_row(const AttnArgs& a, int b) {
   return (row >= 0 && row < (long long)a.num_blocks * a.blk_len) ? row : -1;
 }
 
+// The GQA + 2 heads of kv group g of sequence b, prepared (attention_block_tkg.py:
+// 915-1138) by the 4 waves of a block: wave w takes heads w, w+4, ... of
+// [q heads of g | k of g | v of g]; all loads first, then the math.
+template <int D, int GQA>
+MKD_DEV void prep_heads(const AttnArgs& a, int rope_mode, int b, int g, int w, int lane,
+                        uint16_t (*q_dst)[D], uint16_t* k_dst, uint16_t* v_dst) {
+  constexpr int NR = (GQA + 2 + 3) / 4;
+  HeadPrep<D> hp[NR];
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int h = w + 4 * r;
+    if (h < GQA + 2) {
+      const int kind = h < GQA ? 0 : h - GQA + 1;
+      const int head = h < GQA ? g * GQA + h : (kind == 1 ? a.nq + g : a.nq + a.nkv + g);
+      hp[r].load(a, rope_mode, b, head, kind, lane);
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < NR; ++r) {
+    const int h = w + 4 * r;
+    if (h < GQA + 2) {
+      const int kind = h < GQA ? 0 : h - GQA + 1;
+      hp[r].finish(a, rope_mode, kind, h < GQA ? q_dst[h] : (kind == 1 ? k_dst : v_dst), lane);
+    }
+  }
+}
+
+// Large grids: the heads of (b, g) are prepared once here, block (g, b), into
+// a.prep [B, nkv, gqa + 2, d], instead of in every one of its chunk blocks.
+template <int D, int GQA>
+__global__ void __launch_bounds__(256) attn_prep_kernel(AttnArgs a, int rope_mode) {
+  const int g = blockIdx.x, b = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  uint16_t* dst = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
+  prep_heads<D, GQA>(a, rope_mode, b, g, w, lane, reinterpret_cast<uint16_t(*)[D]>(dst),
+                     dst + GQA * D, dst + (GQA + 1) * D);
+}
+
 template <int D, int GQA, int TPW>
 __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mode) {
   constexpr int VS = D + 8;                   // padded LDS row stride (elements)
@@ -203,10 +241,14 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   if (chunk0 >= total) return;                // whole block: uniform exit
 
   // ---- 0. the wave's K and V rows from the cache: they depend on nothing
-  // computed here, so their loads are issued first and overlap the prep ----
+  // computed here, so their loads are issued first and overlap the prep.  With
+  // 4 tiles per wave (large grids) the registers cost more occupancy than the
+  // overlap gains, and the rows are loaded where they are used. ----
+  constexpr bool PRE = TPW <= 2;
   const int dq = (lane >> 4) * (D / 4);       // lane's d range in a 16-row tile
   const int wbase = chunk0 + w * TPW * 16;
-  u32x4_t kpre[TPW][NK], vpre[TPW][D / 32];
+  u32x4_t kpre[PRE ? TPW : 1][NK], vpre[PRE ? TPW : 1][D / 32];
+  if constexpr (PRE)
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
     const int t = wbase + tt * 16 + (lane & 15);
@@ -218,26 +260,18 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
     for (int j = 0; j < D / 32; ++j) vpre[tt][j] = vr ? ld16(vr + dq + j * 8) : u32x4_t{0, 0, 0, 0};
   }
 
-  // ---- 1. prep of this kv group's heads: wave w takes heads w, w+4, ... of
-  // [q heads of g | k of g | v of g]; all loads first, then the math ----
-  constexpr int NR = (GQA + 2 + 3) / 4;
-  HeadPrep<D> hp[NR];
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const int h = w + 4 * r;
-    if (h < GQA + 2) {
-      const int kind = h < GQA ? 0 : h - GQA + 1;
-      const int head = h < GQA ? g * GQA + h : (kind == 1 ? a.nq + g : a.nq + a.nkv + g);
-      hp[r].load(a, rope_mode, b, head, kind, lane);
+  // ---- 1. the kv group's prepared heads [q heads of g | k of g | v of g]:
+  // copied from attn_prep_kernel's output (large grids), or prepared here --
+  // wave w takes heads w, w+4, ...; all loads first, then the math ----
+  if (a.prep) {
+    const uint16_t* src = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
+    for (int i = threadIdx.x * 8; i < (GQA + 2) * D; i += 256 * 8) {
+      const int h = i / D, d = i % D;
+      uint16_t* dst = h < GQA ? &q_s[h][d] : (h == GQA ? &kn_s[d] : &vn_s[d]);
+      *reinterpret_cast<u32x4_t*>(dst) = ld16(src + i);
     }
-  }
-#pragma unroll
-  for (int r = 0; r < NR; ++r) {
-    const int h = w + 4 * r;
-    if (h < GQA + 2) {
-      const int kind = h < GQA ? 0 : h - GQA + 1;
-      hp[r].finish(a, rope_mode, kind, h < GQA ? q_s[h] : (kind == 1 ? kn_s : vn_s), lane);
-    }
+  } else {
+    prep_heads<D, GQA>(a, rope_mode, b, g, w, lane, q_s, kn_s, vn_s);
   }
   __syncthreads();
 
@@ -255,9 +289,12 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   for (int tt = 0; tt < TPW; ++tt) {
     const int t = wbase + tt * 16 + (lane & 15);  // A row owned by this lane
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    const uint16_t* kr = (!PRE && t < n) ? kv_row<D>(a, a.k_cache, b, g, t) : nullptr;
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
-      u32x4_t kf = kpre[tt][kk];
+      u32x4_t kf;
+      if constexpr (PRE) kf = kpre[tt][kk];
+      else kf = kr ? ld16(kr + dq + kk * 8) : u32x4_t{0, 0, 0, 0};
       if (t == n) kf = *reinterpret_cast<const u32x4_t*>(&kn_s[dq + kk * 8]);
       acc = mfma16x16x32(kf, qf[kk], acc);
     }
@@ -305,9 +342,12 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   for (int tt = 0; tt < TPW; ++tt) {
     // stage V rows of the tile: lane -> row l%16, D/4 elements at (l/16)*(D/4)
     const int t = wbase + tt * 16 + (lane & 15);
+    const uint16_t* vr = (!PRE && t < n) ? kv_row<D>(a, a.v_cache, b, g, t) : nullptr;
 #pragma unroll
     for (int j = 0; j < D / 32; ++j) {
-      u32x4_t v = vpre[tt][j];
+      u32x4_t v;
+      if constexpr (PRE) v = vpre[tt][j];
+      else v = vr ? ld16(vr + dq + j * 8) : u32x4_t{0, 0, 0, 0};
       if (t == n) v = *reinterpret_cast<const u32x4_t*>(&vn_s[dq + j * 8]);
       *reinterpret_cast<u32x4_t*>(vt + (lane & 15) * VS + dq + j * 8) = v;
     }
@@ -363,14 +403,13 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
 }
 
 // Combine: block (head h, sequence b), 4 waves; wave w takes chunks w, w+4, ...
-// in batches of up to 16 whose loads are all issued before any use, with a
+// in batches of U whose loads are all issued before any use, with a
 // running (max, sum, O) per wave rescaled when a batch raises the max; the 4
 // wave results then merge in LDS in wave order, with the sink logit if any.
 // The new k / v rows of the scatter are loaded at the start as well.
-template <int D>
+template <int D, int U>
 __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
   constexpr int EL = D / 64;
-  constexpr int U = 16;
   __shared__ float m_s[4], l_s[4];
   __shared__ float acc_s[4][D];
   const int h = blockIdx.x, b = blockIdx.y;
@@ -464,6 +503,10 @@ static hipError_t launch_attn(const AttnArgs& a, int rope_mode, hipStream_t s) {
 
 template <int D, int GQA>
 static hipError_t launch_tpw(const AttnArgs& a, int rope_mode, hipStream_t s) {
+  if (a.prep) {
+    hipLaunchKernelGGL((attn_prep_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode);
+    if (hipError_t e = hipGetLastError()) return e;
+  }
   const int chunk = a.chunk;
   if (chunk == 64) return launch_attn<D, GQA, 1>(a, rope_mode, s);
   if (chunk == 128) return launch_attn<D, GQA, 2>(a, rope_mode, s);
@@ -481,9 +524,17 @@ int attn_chunk_for(int B, int nkv, int S_max) {
 }
 
 hipError_t attn_combine_launch(const AttnArgs& a, hipStream_t s) {
-  if (a.d == 128) hipLaunchKernelGGL(attn_combine_kernel<128>, dim3(a.nq, a.B), dim3(256), 0, s, a);
-  else if (a.d == 64) hipLaunchKernelGGL(attn_combine_kernel<64>, dim3(a.nq, a.B), dim3(256), 0, s, a);
-  else return hipErrorInvalidValue;
+  // chunks per wave in one batch of loads: 8 covers up to 32 chunks
+  const bool small = a.n_chunks <= 32;
+  if (a.d == 128) {
+    if (small) hipLaunchKernelGGL((attn_combine_kernel<128, 8>), dim3(a.nq, a.B), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((attn_combine_kernel<128, 16>), dim3(a.nq, a.B), dim3(256), 0, s, a);
+  } else if (a.d == 64) {
+    if (small) hipLaunchKernelGGL((attn_combine_kernel<64, 8>), dim3(a.nq, a.B), dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((attn_combine_kernel<64, 16>), dim3(a.nq, a.B), dim3(256), 0, s, a);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

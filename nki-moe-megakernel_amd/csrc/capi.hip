@@ -591,7 +591,7 @@ int mkd_pack_mx_weights(const void* codes, const void* scales, void* dst, void* 
 struct AttnWs {
   uint16_t* hnorm;
   float* qkv;
-  uint16_t *attn, *kvn;
+  uint16_t *attn, *kvn, *prep;
   float *po, *pml;
   int chunk, n_chunks;
 };
@@ -604,6 +604,7 @@ static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_
   w.qkv = c.take<float>((size_t)B * (nq + 2 * nkv) * d);
   w.attn = c.take<uint16_t>((size_t)B * nq * d);
   w.kvn = c.take<uint16_t>((size_t)B * 2 * nkv * d);
+  w.prep = c.take<uint16_t>((size_t)B * (nq + 2 * nkv) * d);
   w.po = c.take<float>((size_t)B * nq * w.n_chunks * d);
   w.pml = c.take<float>((size_t)B * nq * w.n_chunks * 2);
   return w;
@@ -660,6 +661,9 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   a.B = p->B; a.nq = p->nq; a.nkv = p->nkv; a.d = p->d; a.S_max = p->S_max;
   a.chunk = w.chunk; a.n_chunks = w.n_chunks;
   a.part_o = w.po; a.part_ml = w.pml;
+  // large grids prepare the q / k / v heads once per (sequence, kv head) in a
+  // launch of their own; small ones inside every attention block
+  a.prep = (long long)w.n_chunks * p->nkv * p->B > 1024 ? w.prep : nullptr;
   a.attn_out = w.attn;
   a.update_cache = p->update_cache;
   a.write_pos = p->kv_cache_update_idx;

@@ -149,6 +149,8 @@ struct AttnArgs {
   int update_cache;
   const int* write_pos;       // [B] row written (default pos); < 0 -> skip
   uint16_t* kv_new;           // [B, 2, nkv, d] staged new k / v rows
+  uint16_t* prep;             // [B, nkv, gqa + 2, d] prepared q / k / v rows (large grids;
+                              // null: every attention block prepares them itself)
   // block (paged) KV cache: caches are [num_blocks, blk_len, nkv, d]; position t
   // of sequence b lives in block block_table[b * tbl_stride + t / blk_len] at
   // row t % blk_len; write_pos is then a global row (block * blk_len + row), or
