@@ -283,18 +283,32 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
     qf[kk] = hcol < GQA ? *reinterpret_cast<const u32x4_t*>(&q_s[hcol][dq + kk * 8])
                         : u32x4_t{0, 0, 0, 0};
 
-  // ---- 2. scores for the wave's tiles ----
+  // ---- 2. scores for the wave's tiles (without the up-front copies: the K
+  // rows of LB tiles are loaded together, then their MFMAs run) ----
+#ifndef MKD_ATTN_LB
+#define MKD_ATTN_LB 2
+#endif
+  constexpr int LB = PRE ? 1 : MKD_ATTN_LB;
   float s[TPW][4];
+  u32x4_t kl[LB][NK];
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
     const int t = wbase + tt * 16 + (lane & 15);  // A row owned by this lane
+    if (!PRE && tt % LB == 0) {
+#pragma unroll
+      for (int u = 0; u < LB; ++u) {
+        const int tu = t + u * 16;
+        const uint16_t* kr = (tt + u < TPW && tu < n) ? kv_row<D>(a, a.k_cache, b, g, tu) : nullptr;
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) kl[u][kk] = kr ? ld16(kr + dq + kk * 8) : u32x4_t{0, 0, 0, 0};
+      }
+    }
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    const uint16_t* kr = (!PRE && t < n) ? kv_row<D>(a, a.k_cache, b, g, t) : nullptr;
 #pragma unroll
     for (int kk = 0; kk < NK; ++kk) {
       u32x4_t kf;
       if constexpr (PRE) kf = kpre[tt][kk];
-      else kf = kr ? ld16(kr + dq + kk * 8) : u32x4_t{0, 0, 0, 0};
+      else kf = kl[tt % LB][kk];
       if (t == n) kf = *reinterpret_cast<const u32x4_t*>(&kn_s[dq + kk * 8]);
       acc = mfma16x16x32(kf, qf[kk], acc);
     }
@@ -338,16 +352,25 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   uint16_t* vt = v_s[w];
+  u32x4_t vl[LB][D / 32];
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
     // stage V rows of the tile: lane -> row l%16, D/4 elements at (l/16)*(D/4)
     const int t = wbase + tt * 16 + (lane & 15);
-    const uint16_t* vr = (!PRE && t < n) ? kv_row<D>(a, a.v_cache, b, g, t) : nullptr;
+    if (!PRE && tt % LB == 0) {
+#pragma unroll
+      for (int u = 0; u < LB; ++u) {
+        const int tu = t + u * 16;
+        const uint16_t* vr = (tt + u < TPW && tu < n) ? kv_row<D>(a, a.v_cache, b, g, tu) : nullptr;
+#pragma unroll
+        for (int j = 0; j < D / 32; ++j) vl[u][j] = vr ? ld16(vr + dq + j * 8) : u32x4_t{0, 0, 0, 0};
+      }
+    }
 #pragma unroll
     for (int j = 0; j < D / 32; ++j) {
       u32x4_t v;
       if constexpr (PRE) v = vpre[tt][j];
-      else v = vr ? ld16(vr + dq + j * 8) : u32x4_t{0, 0, 0, 0};
+      else v = vl[tt % LB][j];
       if (t == n) v = *reinterpret_cast<const u32x4_t*>(&vn_s[dq + j * 8]);
       *reinterpret_cast<u32x4_t*>(vt + (lane & 15) * VS + dq + j * 8) = v;
     }
