@@ -16,9 +16,13 @@
 //       p = exp(s - m_head) with the wave's per-head max.
 //       O += P . V        v_mfma_f32_16x16x16_bf16: the S layout above IS the A
 //                          layout of this MFMA (row = head l%16, k = positions
-//                          4*(l/16)+i), so P never leaves registers.  B = V tile
-//                          [16 pos][16 d] staged through LDS (rows padded to
-//                          D+8 elements: conflict-free 2-byte transposed reads).
+//                          4*(l/16)+i), so P never leaves registers.  B = V
+//                          [pos 4*(l/16)+j][d label l%16]: the d labels are
+//                          permuted so that lane column c = l%16 owns the D/16
+//                          contiguous elements c*D/16.. of its four position
+//                          rows (one 16 B / 8 B load per row straight from
+//                          HBM); d-tile dt's operand is element dt of those
+//                          rows, two byte-permutes -- no transpose through LDS.
 //     Positions t < n_prior[b] read the cache (flat [B, nkv, S_max, d], or block
 //     [num_blocks, blk_len, nkv, d] through the sequence's block table: the
 //     paged layout of attention_block_tkg.py:199-206, 1473-1685), t == n_prior[b]
@@ -222,13 +226,12 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnArgs a, int rope_mod
 
 template <int D, int GQA, int TPW>
 __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mode) {
-  constexpr int VS = D + 8;                   // padded LDS row stride (elements)
   constexpr int NK = D / 32;                  // QK MFMAs per tile (k = 32)
   constexpr int NDT = D / 16;                 // PV d-tiles
   constexpr int CP = 4 * TPW * 16;            // positions per block
-  __shared__ uint16_t v_s[4][16 * VS];        // one V tile per wave
+  constexpr int VW = D / 32;                  // dwords of a lane's V row segment
   __shared__ float m_s[4][16], l_s[4][16];
-  __shared__ float o_s[4][GQA][D];
+  __shared__ __attribute__((aligned(16))) float o_s[4][GQA][D];
   __shared__ __attribute__((aligned(16))) uint16_t q_s[GQA][D];
   __shared__ __attribute__((aligned(16))) uint16_t kn_s[D];
   __shared__ __attribute__((aligned(16))) uint16_t vn_s[D];
@@ -247,17 +250,55 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   constexpr bool PRE = TPW <= 2;
   const int dq = (lane >> 4) * (D / 4);       // lane's d range in a 16-row tile
   const int wbase = chunk0 + w * TPW * 16;
-  u32x4_t kpre[PRE ? TPW : 1][NK], vpre[PRE ? TPW : 1][D / 32];
-  if constexpr (PRE)
+  const int vc = (lane & 15) * (D / 16);      // lane's V row segment (d labels)
+  // Row pointers first, then the loads: with a block table every pointer is
+  // itself a load, and interleaving them would make each data load wait.
+  // V rows of tile `tile0` for the PV operand: position tile0 + 4*(l/16) + j.
+  auto v_ptrs = [&](int tile0, bool live, const uint16_t* (&p)[4]) {
 #pragma unroll
-  for (int tt = 0; tt < TPW; ++tt) {
-    const int t = wbase + tt * 16 + (lane & 15);
-    const uint16_t* kr = t < n ? kv_row<D>(a, a.k_cache, b, g, t) : nullptr;
-    const uint16_t* vr = t < n ? kv_row<D>(a, a.v_cache, b, g, t) : nullptr;
+    for (int j = 0; j < 4; ++j) {
+      const int t = tile0 + (lane >> 4) * 4 + j;
+      p[j] = (live && t < n) ? kv_row<D>(a, a.v_cache, b, g, t) : nullptr;
+    }
+  };
+  auto v_load = [&](const uint16_t* const (&p)[4], uint32_t (&dst)[4][VW]) {
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) kpre[tt][kk] = kr ? ld16(kr + dq + kk * 8) : u32x4_t{0, 0, 0, 0};
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (VW == 4) {
+        const u32x4_t v = p[j] ? ld16(p[j] + vc) : u32x4_t{0, 0, 0, 0};
 #pragma unroll
-    for (int j = 0; j < D / 32; ++j) vpre[tt][j] = vr ? ld16(vr + dq + j * 8) : u32x4_t{0, 0, 0, 0};
+        for (int e = 0; e < 4; ++e) dst[j][e] = v[e];
+      } else {
+        const uint2 v = p[j] ? *reinterpret_cast<const uint2*>(p[j] + vc) : uint2{0, 0};
+        dst[j][0] = v.x;
+        dst[j][1] = v.y;
+      }
+    }
+  };
+  // K row of tile `tile0` for the score operand: position tile0 + l%16
+  auto k_ptr = [&](int tile0, bool live) {
+    const int t = tile0 + (lane & 15);
+    return (live && t < n) ? kv_row<D>(a, a.k_cache, b, g, t) : nullptr;
+  };
+  auto k_load = [&](const uint16_t* kr, u32x4_t (&dst)[NK]) {
+#pragma unroll
+    for (int kk = 0; kk < NK; ++kk) dst[kk] = kr ? ld16(kr + dq + kk * 8) : u32x4_t{0, 0, 0, 0};
+  };
+  u32x4_t kpre[PRE ? TPW : 1][NK];
+  uint32_t vpre[PRE ? TPW : 1][4][VW];
+  if constexpr (PRE) {
+    const uint16_t* kp[TPW];
+    const uint16_t* vp[TPW][4];
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+      kp[tt] = k_ptr(wbase + tt * 16, true);
+      v_ptrs(wbase + tt * 16, true, vp[tt]);
+    }
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) {
+      k_load(kp[tt], kpre[tt]);
+      v_load(vp[tt], vpre[tt]);
+    }
   }
 
   // ---- 1. the kv group's prepared heads [q heads of g | k of g | v of g]:
@@ -295,13 +336,11 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   for (int tt = 0; tt < TPW; ++tt) {
     const int t = wbase + tt * 16 + (lane & 15);  // A row owned by this lane
     if (!PRE && tt % LB == 0) {
+      const uint16_t* kp[LB];
 #pragma unroll
-      for (int u = 0; u < LB; ++u) {
-        const int tu = t + u * 16;
-        const uint16_t* kr = (tt + u < TPW && tu < n) ? kv_row<D>(a, a.k_cache, b, g, tu) : nullptr;
+      for (int u = 0; u < LB; ++u) kp[u] = k_ptr(wbase + (tt + u) * 16, tt + u < TPW);
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) kl[u][kk] = kr ? ld16(kr + dq + kk * 8) : u32x4_t{0, 0, 0, 0};
-      }
+      for (int u = 0; u < LB; ++u) k_load(kp[u], kl[u]);
     }
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -351,50 +390,53 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   f32x4_t o[NDT];
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  uint16_t* vt = v_s[w];
-  u32x4_t vl[LB][D / 32];
+  uint32_t vl[LB][4][VW];
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
-    // stage V rows of the tile: lane -> row l%16, D/4 elements at (l/16)*(D/4)
-    const int t = wbase + tt * 16 + (lane & 15);
+    const int tile0 = wbase + tt * 16;
     if (!PRE && tt % LB == 0) {
+      const uint16_t* vp[LB][4];
 #pragma unroll
-      for (int u = 0; u < LB; ++u) {
-        const int tu = t + u * 16;
-        const uint16_t* vr = (tt + u < TPW && tu < n) ? kv_row<D>(a, a.v_cache, b, g, tu) : nullptr;
+      for (int u = 0; u < LB; ++u) v_ptrs(tile0 + u * 16, tt + u < TPW, vp[u]);
 #pragma unroll
-        for (int j = 0; j < D / 32; ++j) vl[u][j] = vr ? ld16(vr + dq + j * 8) : u32x4_t{0, 0, 0, 0};
+      for (int u = 0; u < LB; ++u) v_load(vp[u], vl[u]);
+    }
+    uint32_t v[4][VW];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < VW; ++e) {
+        if constexpr (PRE) v[j][e] = vpre[tt][j][e];
+        else v[j][e] = vl[tt % LB][j][e];
       }
-    }
+    // the new token's row comes from LDS (at most one j per lane)
 #pragma unroll
-    for (int j = 0; j < D / 32; ++j) {
-      u32x4_t v;
-      if constexpr (PRE) v = vpre[tt][j];
-      else v = vl[tt % LB][j];
-      if (t == n) v = *reinterpret_cast<const u32x4_t*>(&vn_s[dq + j * 8]);
-      *reinterpret_cast<u32x4_t*>(vt + (lane & 15) * VS + dq + j * 8) = v;
-    }
-    wave_lds_sync();                          // V tile visible to the whole wave
+    for (int j = 0; j < 4; ++j)
+      if (tile0 + (lane >> 4) * 4 + j == n)
+#pragma unroll
+        for (int e = 0; e < VW; ++e) v[j][e] = *reinterpret_cast<const uint32_t*>(&vn_s[vc + 2 * e]);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      const int col = dt * 16 + (lane & 15);
-      const int r0 = (lane >> 4) * 4;
-      const uint32_t e0 = vt[(r0 + 0) * VS + col], e1 = vt[(r0 + 1) * VS + col];
-      const uint32_t e2 = vt[(r0 + 2) * VS + col], e3 = vt[(r0 + 3) * VS + col];
-      o[dt] = mfma16x16x16(pa[tt], uint2{e0 | (e1 << 16), e2 | (e3 << 16)}, o[dt]);
+      const int e = dt >> 1;
+      const uint2 bop = (dt & 1)
+          ? uint2{(v[0][e] >> 16) | (v[1][e] & 0xffff0000u), (v[2][e] >> 16) | (v[3][e] & 0xffff0000u)}
+          : uint2{(v[0][e] & 0xffffu) | (v[1][e] << 16), (v[2][e] & 0xffffu) | (v[3][e] << 16)};
+      o[dt] = mfma16x16x16(pa[tt], bop, o[dt]);
     }
-    __builtin_amdgcn_wave_barrier();
   }
 
   // ---- merge the 4 waves into this chunk's partial ----
   if (lane < 16) { m_s[w][lane] = m; l_s[w][lane] = lsum; }
+  // o[dt][i] = O[head 4*(l/16)+i][d = vc + dt]: NDT contiguous floats per head
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+  for (int i = 0; i < 4; ++i) {
+    const int h = (lane >> 4) * 4 + i;
+    if (h < GQA)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int h = (lane >> 4) * 4 + i;
-      if (h < GQA) o_s[w][h][dt * 16 + (lane & 15)] = o[dt][i];
-    }
+      for (int q = 0; q < NDT / 4; ++q)
+        *reinterpret_cast<f32x4_t*>(&o_s[w][h][vc + 4 * q]) =
+            f32x4_t{o[4 * q][i], o[4 * q + 1][i], o[4 * q + 2][i], o[4 * q + 3][i]};
+  }
   __syncthreads();
   for (int idx = threadIdx.x; idx < GQA * D; idx += 256) {
     const int h = idx / D, d = idx % D;
