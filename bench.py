@@ -240,6 +240,8 @@ def main():
     ap.add_argument("--model", choices=["qwen3", "gpt-oss"], default="qwen3",
                     help="gpt-oss: GPT-OSS-20B shape, 24 layers, MXFP4 experts (configs[4]; "
                          "use --batch 32 --ragged --experts mxfp4)")
+    ap.add_argument("--persistent", action="store_true",
+                    help="run each decoder layer as one persistent kernel launch (batches <= 4)")
     ap.add_argument("--moe-prefill", type=int, default=0, metavar="T",
                     help="measure the MFMA regime instead: moe_prefill (LDS-tiled grouped GEMMs) "
                          "on T tokens of the Qwen3 expert shape (E=128, K=8), T*K/E tokens/expert")
@@ -258,6 +260,7 @@ def main():
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
 
     dev = torch.device("cuda:0")
+    Q.set_decode_path("persistent" if args.persistent else "multi_kernel")
     B, ctx = args.batch, args.ctx
     oss = args.model == "gpt-oss"
     lo, hi = (1024, 4096) if oss else (512, 8192)
@@ -336,18 +339,22 @@ def main():
     ms_step = ms_total / args.steps
     tok_s = B * args.steps / (ms_total / 1e3)
 
-    # Dominant kernel (MoE gate/up): HIP events recorded by each gate/up
-    # kernel's own dispatch packet on the launch stream (hipExtLaunchKernel), so
-    # a pair times the kernel alone, in one eager step right after the timed
-    # region (a captured graph keeps no timing events).
-    L.check(lib.mkd_profile_events(L.KCLASS["moe_gate_up"], arr(ev_s), arr(ev_e), n_ev),
-            "profile_events")
+    # Dominant kernel: the persistent layer kernel when the step runs one launch
+    # per layer, else the MoE gate/up GEMM.  HIP events recorded by each of its
+    # dispatch packets on the launch stream (hipExtLaunchKernel), so a pair
+    # times the kernel alone, in one eager step right after the timed region (a
+    # captured graph keeps no timing events).
+    layer_kernel = (not oss) and model.layer_kernel_status(B)[0]
+    if layer_kernel and model.layer_kernel_status(B)[1]:
+        raise RuntimeError("a grid barrier of the persistent layer kernel timed out")
+    kcls = "layer" if layer_kernel else "moe_gate_up"
+    L.check(lib.mkd_profile_events(L.KCLASS[kcls], arr(ev_s), arr(ev_e), n_ev), "profile_events")
     step()
     torch.cuda.synchronize()
     n_rec = lib.mkd_profile_count()
     L.check(lib.mkd_profile_events(-1, None, None, 0), "profile off")
     if n_rec != n_ev:
-        raise RuntimeError(f"expected {n_ev} profiled gate_up launches, got {n_rec}")
+        raise RuntimeError(f"expected {n_ev} profiled {kcls} launches, got {n_rec}")
     durs = [a.elapsed_time(b) for a, b in zip(ev_s, ev_e)]
     avg_ms = sum(durs) / len(durs)
     H, E, K = cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok
@@ -376,6 +383,9 @@ def main():
     layer_b = attn_b + 2 * E * H + distinct * 3 * H * I * wbytes + kv_b
     step_b = cfg.num_hidden_layers * layer_b + 2 * H * cfg.vocab_size
     step_gbs = step_b / (ms_step / 1e3) / 1e9
+    if layer_kernel:   # the launch streams the whole layer: its algorithmic bytes
+        alg_bytes = layer_b
+        achieved = alg_bytes / (avg_ms / 1e3) / 1e9
 
     cpu = None
     if not args.no_cpu:
@@ -386,7 +396,7 @@ def main():
             log(f"cpu baseline failed: {e!r}")
     log(f"step {ms_step:.3f} ms ({tok_s:.1f} tok/s), wall {wall:.2f}s; whole-step algorithmic "
         f"{step_b / 1e9:.3f} GB -> {step_gbs:.0f} GB/s ({step_gbs / HBM_PEAK_GBS:.1%} of HBM); "
-        f"gate_up avg {avg_ms * 1e3:.1f} us over {len(durs)} launches -> {achieved:.0f} GB/s")
+        f"{kcls} avg {avg_ms * 1e3:.1f} us over {len(durs)} launches -> {achieved:.0f} GB/s")
     out = {
         "metric": "decode tok/s/GPU, Qwen3-30B-A3B shape bs=1/16/64; % of HBM & MFMA roofline",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
@@ -407,11 +417,13 @@ def main():
                    "gate_up_TFLOPs": round(gu_tflops, 2),
                    "gate_up_mfma_frac": round(gu_tflops / mfma_peak, 5)},
         "roofline": {"bound": "hbm",
-                     "kernel": "moe gate_up grouped GEMM (" + ("gemm_frag_kernel<2,1,0,3>" if args.experts == "bf16"
+                     "kernel": ("persistent decoder layer (layer_kernel<%d,%d>), one launch per layer"
+                                % (cfg.head_dim, 2 if cfg.num_experts <= 128 else 8)) if layer_kernel else
+                               "moe gate_up grouped GEMM (" + ("gemm_frag_kernel<2,1,0,3>" if args.experts == "bf16"
                                                                else "gemm_mx_kernel<2,fmt,3>") + ")",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers)
+                     "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers, kcls)
                      if (args.model == "qwen3" and args.experts == "bf16" and not args.ragged
                          and not args.kv_block) else None,
                      "avg_us": round(avg_ms * 1e3, 2), "bytes_per_launch": int(alg_bytes)},
@@ -540,9 +552,11 @@ def workload_name(cfg, B, ctx, lens, args):
             f"{args.experts} experts{tag}")
 
 
-def measured_traffic(B, ctx, layers):
-    """HBM bytes per gate/up launch from the committed counter summary, or None."""
-    path = os.path.join(ROOT, "profiles", "gate_up_traffic.json")
+def measured_traffic(B, ctx, layers, kcls="moe_gate_up"):
+    """HBM bytes per launch of the dominant kernel from the committed counter
+    summary for that kernel and workload, or None."""
+    name = "layer_kernel_traffic.json" if kcls == "layer" else "gate_up_traffic.json"
+    path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:
             t = json.load(f)

@@ -353,9 +353,28 @@ int mkd_decode_advance(int* token_ids, int* position_ids, const int* next_tokens
 #define MKD_KCLASS_ATTN 5
 #define MKD_KCLASS_LM_HEAD 6
 #define MKD_KCLASS_ROUTER 7 /* router GEMM + select (two launches, one bracket) */
+#define MKD_KCLASS_LAYER 8  /* persistent decoder-layer kernel (one launch per layer) */
 int mkd_profile_events(int kernel_class, void* const* start_events, void* const* stop_events,
                        int n);
 int mkd_profile_count(void); /* launches recorded since the last mkd_profile_events */
+
+/* ---------------------------------------------------------------------------
+ * Decode-layer execution path (no counterpart in the reference, whose step is
+ * one compiled NEFF).  mode 0 (default): each layer of
+ * mkd_qwen3_decode_layers is the multi-kernel sequence.  mode 1: each layer is
+ * ONE persistent kernel launch (all stages on one block per CU, separated by
+ * grid barriers) when the model is the Qwen3 flow with bf16 experts, B <= 4,
+ * d in {64, 128}, gqa <= 16, no biases / sinks / windows, and the stage
+ * buffers fit the LDS budget; other configurations keep the multi-kernel
+ * sequence.  The workspace size does not depend on the mode.  Process-global.
+ * mkd_qwen3_layer_kernel_status reports (after a stream sync) whether the
+ * workspace's plan uses the persistent kernel and whether any of its grid
+ * barriers timed out (results of such a step are invalid; the barrier spins
+ * are bounded so the kernel always completes).
+ * ------------------------------------------------------------------------- */
+int mkd_set_decode_path(int mode);
+int mkd_qwen3_layer_kernel_status(const mkd_qwen3_model* m, int B, const void* workspace,
+                                  size_t workspace_bytes, int* used, int* barrier_timeout);
 
 #ifdef __cplusplus
 }

@@ -116,9 +116,12 @@ _SIGS = {
     "mkd_decode_advance": (i32, [vp, vp, vp, i32, vp]),
     "mkd_profile_events": (i32, [i32, C.POINTER(vp), C.POINTER(vp), i32]),
     "mkd_profile_count": (i32, []),
+    "mkd_set_decode_path": (i32, [i32]),
+    "mkd_qwen3_layer_kernel_status": (i32, [C.POINTER(Qwen3Model), i32, vp, sz, C.POINTER(i32),
+                                            C.POINTER(i32)]),
 }
 KCLASS = {"moe_gate_up": 1, "moe_down": 2, "qkv": 3, "oproj": 4, "attn": 5, "lm_head": 6,
-          "router": 7}
+          "router": 7, "layer": 8}
 
 EXPORTED = tuple(_SIGS)
 

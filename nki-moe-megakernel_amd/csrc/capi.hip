@@ -3,6 +3,7 @@
 // This layer validates shapes and pointers on the host, carves the caller's
 // workspace, and enqueues the kernels on the caller's stream.  It never
 // allocates device memory and never synchronises.
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -747,11 +748,130 @@ int mkd_attention_block_tkg(const mkd_attention_args* p, void* workspace, size_t
 // ---------------------------------------------------------------------------
 // multi-layer Qwen3 decode step
 // ---------------------------------------------------------------------------
+// Persistent layer kernel (layer_mk.hip) plan: possible for the Qwen3 flow with
+// bf16 experts and up to kLkMaxB tokens when the shapes and the LDS budget
+// allow (its buffers are then always part of the workspace); used when the
+// decode path is set to it, otherwise every layer runs the multi-kernel sequence.
+static int g_decode_path = 0;   // 0 multi-kernel layers, 1 persistent layer kernel where eligible
+
+static int lk_device_cus() {
+  static int cus = -1;
+  if (cus < 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    cus = n;
+  }
+  return cus;
+}
+
+struct LkPlan {
+  bool on = false;
+  int NB = 0, LW = 0, nch_max = 0;
+  int LBq = 0, LBo = 0, LBr = 0, LBgu = 0, LBdn = 0;
+  int lds_a = 0, lds_b = 0, lds_c = 0, lds_s = 0, lds_total = 0;
+};
+
+// Units per block (LB) and per wave (LW) of a split-K stage, over every group count.
+static void lk_bounds(int NRB, int KB, int ngmax, int NB, int& LB, int& LW) {
+  LB = LW = 0;
+  for (int ng = 1; ng <= ngmax; ++ng) {
+    const int F = ng * NRB * KB;
+    const long long fpb = lk_fpb(F, KB, NB);
+    const long long fpw = (fpb + 7) / 8;
+    LB = std::max(LB, (int)((fpb + KB - 1) / KB + 1));
+    LW = std::max(LW, (int)((fpw + KB - 1) / KB + 1));
+  }
+}
+
+static size_t a16(size_t n) { return (n + 15) & ~size_t(15); }
+
+static LkPlan lk_plan(const mkd_qwen3_model* m, int B) {
+  LkPlan p;
+  const bool biasless = !m->b_qkv && !m->b_o && !m->sinks && !m->router_bias && !m->gate_up_bias &&
+                        !m->down_bias && !m->window && !m->layer_s_max;
+  if (m->variant != MKD_VARIANT_QWEN3 || m->expert_format != 0 || !biasless) return p;
+  if (B < 1 || B > kLkMaxB || (m->d != 64 && m->d != 128) || m->nkv < 1 || m->nq % m->nkv != 0 ||
+      m->nq / m->nkv > 16 || m->H % 32 != 0 || m->I % 32 != 0 || m->E % 16 != 0 || m->E > 512 ||
+      m->K < 1 || m->K > 8 || m->K > m->E || (m->nq * m->d) % 32 != 0 || !m->q_norm || !m->k_norm ||
+      B * m->H > kLkMaxRowElems)
+    return p;
+  const int NB = std::min(lk_device_cus(), kLkMaxNB);
+  if (NB < 8) return p;
+  const int ngmax = std::min(m->E, B * m->K);
+  const int qkv_n = (m->nq + 2 * m->nkv) * m->d;
+  {  // every stage's fragment count fits the kernel's 32-bit partition arithmetic
+    const long long frags[] = {(long long)qkv_n / 16 * (m->H / 32), (long long)m->H / 16 * (m->nq * m->d / 32),
+                               (long long)m->E / 16 * (m->H / 32), (long long)ngmax * (2 * m->I / 16) * (m->H / 32),
+                               (long long)ngmax * (m->H / 16) * (m->I / 32)};
+    for (long long f : frags)     // also bounds every divisor of the partition (< 2^20)
+      if (f >= (1LL << 20)) return p;
+  }
+  int lw, LW = 0;
+  lk_bounds(qkv_n / 16, m->H / 32, 1, NB, p.LBq, lw); LW = std::max(LW, lw);
+  lk_bounds(m->H / 16, m->nq * m->d / 32, 1, NB, p.LBo, lw); LW = std::max(LW, lw);
+  lk_bounds(m->E / 16, m->H / 32, 1, NB, p.LBr, lw); LW = std::max(LW, lw);
+  lk_bounds(2 * m->I / 16, m->H / 32, ngmax, NB, p.LBgu, lw); LW = std::max(LW, lw);
+  lk_bounds(m->H / 16, m->I / 32, ngmax, NB, p.LBdn, lw); LW = std::max(LW, lw);
+  // a down-stage block range must span at most kLkActG expert groups
+  for (int ng = 1; ng <= ngmax; ++ng) {
+    const int FGd = (m->H / 16) * (m->I / 32), F = ng * FGd;
+    if (lk_fpb(F, m->I / 32, NB) > (kLkActG - 1) * FGd + 1) return p;
+  }
+  p.LW = LW;
+  p.NB = NB;
+  p.nch_max = (m->S_max + 1 + 127) / 128;
+  const int gqa = m->nq / m->nkv, d = m->d;
+  const size_t A = a16((size_t)2 * B * m->H);
+  const size_t Bs = a16(std::max({(size_t)2 * B * std::max(m->H, m->nq * d), (size_t)6 * B * m->H,
+                                  (size_t)2 * kLkActG * kLkMaxB * m->I}));
+  const size_t Cs = a16(std::max((size_t)8 * LW * 1024,
+                                 (size_t)16 * d * 2 + 2 * d * 2 + 2 * 8 * 16 * 4 + (size_t)8 * gqa * d * 4));
+  const size_t S = kLkSelBytes;
+  const size_t total = A + Bs + Cs + S;
+  if (total + kLkStaticLds > 160 * 1024) return p;
+  p.lds_a = 0;
+  p.lds_b = (int)A;
+  p.lds_c = (int)(A + Bs);
+  p.lds_s = (int)(A + Bs + Cs);
+  p.lds_total = (int)total;
+  p.on = true;
+  return p;
+}
+
+struct LkWs {
+  LkPlan plan;
+  float *pq = nullptr, *po = nullptr, *pr = nullptr, *pgu = nullptr, *pdn = nullptr;
+  float *apo = nullptr, *aml = nullptr;
+  unsigned* bar = nullptr;
+};
+
+static LkWs carve_lk(Carver& c, const mkd_qwen3_model* m, int B) {
+  LkWs w;
+  w.plan = lk_plan(m, B);
+  if (!w.plan.on) return w;
+  const LkPlan& p = w.plan;
+  const size_t ent = (size_t)p.NB * kLkMaxB * 16;
+  w.pq = c.take<float>(ent * p.LBq);
+  w.po = c.take<float>(ent * p.LBo);
+  w.pr = c.take<float>(ent * p.LBr);
+  w.pgu = c.take<float>(ent * p.LBgu);
+  w.pdn = c.take<float>(ent * p.LBdn);
+  w.apo = c.take<float>((size_t)B * m->nq * p.nch_max * m->d);
+  w.aml = c.take<float>((size_t)B * m->nq * p.nch_max * 2);
+  w.bar = c.take<unsigned>(kLkBarWords);
+  return w;
+}
+
 struct StepWs {
   AttnWs attn;
   uint16_t *r, *nbf;
   float *nf32, *logits, *cos, *sin, *oparts;
   MoeWs moe;
+  LkWs lk;
 };
 
 static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
@@ -765,14 +885,68 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.sin = c.take<float>((size_t)B * m->d);
   w.oparts = c.take<float>((size_t)2 * B * m->H);      // o_proj split-K partials
   w.moe = carve_moe(c, B, m->H, m->E, m->I, m->K);
+  w.lk = carve_lk(c, m, B);
   return w;
 }
 
+// The decode layers as persistent layer-kernel launches (one per layer).
+static int decode_layers_lk(const mkd_qwen3_model* m, int B, uint16_t* x, const int* position_ids,
+                            const float* cos, const float* sin, StepWs& w, hipStream_t s) {
+  const LkPlan& p = w.lk.plan;
+  const int ha = m->H_actual > 0 ? m->H_actual : m->H;
+  const int qkv_n = (m->nq + 2 * m->nkv) * m->d;
+  MKD_TRY(layer_reset_launch(w.lk.bar, s), "layer kernel barrier reset");
+  for (int l = 0; l < m->num_layers; ++l) {
+    LayerArgs L;
+    memset(&L, 0, sizeof(L));
+    L.B = B; L.H = m->H; L.nq = m->nq; L.nkv = m->nkv; L.gqa = m->nq / m->nkv; L.d = m->d;
+    L.E = m->E; L.K = m->K; L.I = m->I; L.S_max = m->S_max; L.NB = p.NB;
+    L.eps = m->eps; L.inv_h = 1.0f / (float)ha; L.qk_eps = m->eps;
+    L.scale = 1.0f / sqrtf((float)m->d);
+    L.ln_in = static_cast<const uint16_t*>(m->ln_in[l]);
+    L.ln_post = static_cast<const uint16_t*>(m->ln_post[l]);
+    L.q_norm = static_cast<const uint16_t*>(m->q_norm[l]);
+    L.k_norm = static_cast<const uint16_t*>(m->k_norm[l]);
+    L.q = LkGemv{static_cast<const uint16_t*>(m->w_qkv[l]), 0, qkv_n / 16, m->H / 32, w.lk.pq, p.LBq, p.LW};
+    L.o = LkGemv{static_cast<const uint16_t*>(m->w_o[l]), 0, m->H / 16, m->nq * m->d / 32, w.lk.po,
+                 p.LBo, p.LW};
+    L.r = LkGemv{static_cast<const uint16_t*>(m->router[l]), 0, m->E / 16, m->H / 32, w.lk.pr, p.LBr, p.LW};
+    L.gu = LkGemv{static_cast<const uint16_t*>(m->gate_up[l]), (long long)2 * m->I * m->H,
+                  2 * m->I / 16, m->H / 32, w.lk.pgu, p.LBgu, p.LW};
+    L.dn = LkGemv{static_cast<const uint16_t*>(m->down[l]), padded_rows(m->H) * m->I, m->H / 16,
+                  m->I / 32, w.lk.pdn, p.LBdn, p.LW};
+    L.k_cache = static_cast<uint16_t*>(m->k_cache[l]);
+    L.v_cache = static_cast<uint16_t*>(m->v_cache[l]);
+    L.cache_h_stride = (long long)m->S_max * m->d;
+    L.cache_b_stride = L.cache_h_stride * m->nkv;
+    L.block_table = m->block_table;
+    L.tbl_stride = m->blocks_per_seq; L.blk_len = m->block_len; L.num_blocks = m->num_blocks;
+    L.cos = cos; L.sin = sin; L.pos = position_ids;
+    L.x = x;
+    L.attn_po = w.lk.apo; L.attn_ml = w.lk.aml; L.nch_max = p.nch_max;
+    L.attn_out = w.attn.attn;
+    L.bar = w.lk.bar; L.bar_base = l * kLkBarriers;
+    L.router_mode = MKD_ROUTER_QWEN;
+    L.lds_a = p.lds_a; L.lds_b = p.lds_b; L.lds_c = p.lds_c; L.lds_s = p.lds_s;
+    L.lds_total = p.lds_total;
+    const int ps = prof_begin(MKD_KCLASS_LAYER, s);
+    MKD_TRY(layer_kernel_launch(L, s), "persistent layer kernel");
+    prof_end(ps, s);
+  }
+  return MKD_OK;
+}
+
+// The largest carve over every batch up to B: a workspace sized for the maximum
+// batch serves every smaller batch (whose plan may use the persistent kernel).
 size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B) {
   if (!m) return 0;
-  Carver c{nullptr, 0};
-  carve_step(c, m, B);
-  return c.used;
+  size_t most = 0;
+  for (int b = 1; b <= std::max(B, 1); ++b) {
+    Carver c{nullptr, 0};
+    carve_step(c, m, b);
+    most = std::max(most, c.used);
+  }
+  return most;
 }
 
 int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
@@ -817,6 +991,7 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
                 m->k_cache[l] && m->v_cache[l] && m->ln_in[l] && m->ln_post[l] &&
                 (!m->expert_format || (m->gate_up_scales[l] && m->down_scales[l])),
                 MKD_ERR_NULL, "decode_layers: null weight in layer %d", l);
+  if (w.lk.plan.on && g_decode_path == 1) return decode_layers_lk(m, B, x, position_ids, cos, sin, w, s);
   // Qwen3 flow: pre-attention norm (x*rinv)*g, Qwen rounding points, fp32 router
   // input.  GPT-OSS flow: rmsnorm_tkg's (x*g)*rinv with H_actual everywhere,
   // biases, sinks, sliding windows, bf16 router input with logit top-k.
@@ -1019,5 +1194,27 @@ int mkd_profile_events(int kernel_class, void* const* start_events, void* const*
 }
 
 int mkd_profile_count(void) { return g_prof.next; }
+
+int mkd_set_decode_path(int mode) {
+  MKD_REQUIRE(mode == 0 || mode == 1, MKD_ERR_INVALID, "set_decode_path: mode %d must be 0 or 1", mode);
+  g_decode_path = mode;
+  return MKD_OK;
+}
+
+int mkd_qwen3_layer_kernel_status(const mkd_qwen3_model* m, int B, const void* workspace,
+                                  size_t workspace_bytes, int* used, int* barrier_timeout) {
+  MKD_REQUIRE(m && workspace && used && barrier_timeout, MKD_ERR_NULL, "layer_kernel_status: null pointer");
+  Carver c{static_cast<char*>(const_cast<void*>(workspace)), workspace_bytes};
+  StepWs w = carve_step(c, m, B);
+  MKD_REQUIRE(c.ok, MKD_ERR_WORKSPACE, "layer_kernel_status: workspace %zu < %zu bytes", workspace_bytes, c.used);
+  *used = (w.lk.plan.on && g_decode_path == 1) ? 1 : 0;
+  *barrier_timeout = 0;
+  if (w.lk.plan.on) {
+    unsigned e = 0;
+    MKD_TRY(hipMemcpy(&e, w.lk.bar + kLkMaxNB, sizeof(e), hipMemcpyDeviceToHost), "read error word");
+    *barrier_timeout = e ? 1 : 0;
+  }
+  return MKD_OK;
+}
 
 }  // extern "C"

@@ -99,6 +99,51 @@ hipError_t pack_frag_launch(const uint16_t* src, uint16_t* dst, int G, int N, in
                             long long g_stride, long long row_stride, long long col_stride,
                             int interleave_half, hipStream_t s);
 
+// layer_mk.hip: persistent decoder layer (small batches, Qwen3 flow, bf16 experts)
+constexpr int kLkMaxB = 4;          // tokens per launch
+constexpr int kLkMaxNB = 1024;      // blocks (CUs) per launch
+constexpr int kLkBarWords = kLkMaxNB + 64;   // per-block flags + error word (zeroed once per step)
+struct LkGemv {                     // one split-K GEMV stage
+  const uint16_t* w;                // frag-packed weights (expert 0 / dense)
+  long long gstride;                // elements between experts
+  int NRB, KB;                      // 16-row blocks per group, 32-wide k blocks
+  float* part;                      // [#CUs][LB][kLkMaxB][16] block partials
+  int LB, LW;                       // partials per block, reduction slots per wave
+};
+// Fragments per block of a stage of F fragments over NB blocks: at least
+// ceil(KB / 3), so that a unit of KB fragments spans at most 4 blocks.
+__host__ __device__ inline int lk_fpb(int F, int KB, int NB) {
+  const int a = (F + NB - 1) / NB, b = (KB + 2) / 3;
+  return a > b ? a : b;
+}
+constexpr int kLkMaxRowElems = 16384;   // B * H bound (whole rows held per block)
+struct LayerArgs {
+  int B, H, nq, nkv, gqa, d, E, K, I, S_max, NB;
+  float eps, inv_h, qk_eps, scale;
+  const uint16_t *ln_in, *ln_post, *q_norm, *k_norm;
+  LkGemv q, o, r, gu, dn;
+  uint16_t *k_cache, *v_cache;
+  long long cache_b_stride, cache_h_stride;
+  const int* block_table;
+  int tbl_stride, blk_len, num_blocks;
+  const float *cos, *sin;           // [B, d] RoPE tables
+  const int* pos;                   // [B] positions (prior length and cache row)
+  uint16_t* x;                      // [B, H] residual stream, in and out
+  float *attn_po, *attn_ml;         // [B, nq, nch_max, d], [B, nq, nch_max, 2]
+  int nch_max;
+  uint16_t* attn_out;               // [B, nq * d]
+  unsigned* bar;                    // kLkBarWords barrier words
+  int bar_base;                     // barrier index of this launch's first barrier
+  int router_mode;                  // MKD_ROUTER_* bits
+  int lds_a, lds_b, lds_c, lds_s, lds_total;   // dynamic LDS carve (bytes)
+};
+constexpr int kLkBarriers = 7;      // grid barriers per layer launch
+constexpr int kLkActG = 2;          // expert groups per block in the down stage
+constexpr int kLkSelBytes = 2048;   // LDS of the selection results
+constexpr int kLkStaticLds = 14336; // static LDS of the kernel (router select body), bound
+hipError_t layer_kernel_launch(const LayerArgs& a, hipStream_t s);
+hipError_t layer_reset_launch(unsigned* bar, hipStream_t s);
+
 // norm.hip
 struct NormArgs {
   const void* x;              // [rows, ld_in] bf16 or fp32

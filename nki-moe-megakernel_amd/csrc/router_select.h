@@ -1,0 +1,278 @@
+// Router top-k selection body shared by the router select kernel (moe.hip) and
+// the persistent layer kernel (layer_mk.hip).
+#pragma once
+#include "common.h"
+#include "mkd_internal.h"
+
+namespace mkd {
+
+constexpr int kMaxE = 512;
+constexpr int kMaxPerLane = kMaxE / 64;
+
+// ---------------------------------------------------------------------------
+// Router select: one block (16 waves) for all T <= 128 tokens; wave w takes
+// tokens w, w+16, ...  Logits are the in-order sum of the split-K partials
+// (+ bias), all partial loads of a lane issued together.  Selection is
+// rank-based: element e gets slot r = #{e' : key[e'] > key[e] or (key[e'] ==
+// key[e] and e' < e)} and is chosen when r < K -- descending order, lowest
+// index first among equal keys.  The K chosen are found by a radix select over
+// the keys' order-preserving codes (32 ballot steps per token, no data-
+// dependent branches); only those K are then ranked against each other.  Optionally the
+// same block then builds the expert groups: per-expert counts in LDS, one
+// wave scans them, the slots are scattered by expert.
+// Unsigned code with the order of the float (+0 and -0 share one code, NaN sorts
+// above +inf as in torch.topk).
+MKD_DEV uint32_t order_code(float f) {
+  uint32_t b = __float_as_uint(f);
+  if ((b << 1) == 0) b = 0;
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+// Number of set bits of `m` at lanes below this one.
+MKD_DEV int lanes_below(unsigned long long m) {
+  return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
+// Exclusive prefix sum over the wave: Hillis-Steele inside each row of 16
+// lanes with DPP row_shr 1/2/4/8 (a source outside the row reads 0), then the
+// row totals (readlane of lanes 15/31/47) are added to the later rows.
+template <int CTRL>
+MKD_DEV int dpp_shr_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xF, 0xF, true);
+}
+MKD_DEV int wave_excl_scan(int v, int lane) {
+  int x = v;
+  x += dpp_shr_i<0x111>(x);
+  x += dpp_shr_i<0x112>(x);
+  x += dpp_shr_i<0x114>(x);
+  x += dpp_shr_i<0x118>(x);
+  const int r0 = __builtin_amdgcn_readlane(x, 15);
+  const int r1 = __builtin_amdgcn_readlane(x, 31);
+  const int r2 = __builtin_amdgcn_readlane(x, 47);
+  const int row = lane >> 4;
+  x += (row > 0 ? r0 : 0) + (row > 1 ? r1 : 0) + (row > 2 ? r2 : 0);
+  return x - v;
+}
+
+// Sum of the split-K partial logits of token t for the lane's experts (+ the
+// bias): a whole batch of loads is issued (slots past nparts re-read the last
+// partial and are masked out) before summing in fixed order.
+template <int PER>
+MKD_DEV void load_logits(const RouterArgs& a, int t, int lane, float (&l)[PER]) {
+  const int E = a.E;
+  uint32_t braw[PER];                   // bias bits, loaded with the partials
+  if (a.bias) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) braw[j] = a.bias[min(lane + 64 * j, E - 1)];
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) l[j] = 0.f;
+  constexpr int PB = (PER <= 2) ? 16 : 4;
+#pragma unroll
+  for (int p0 = 0; p0 < 16; p0 += PB) {
+    float v[PB][PER];
+#pragma unroll
+    for (int q = 0; q < PB; ++q) {
+      const int pp = min(p0 + q, a.nparts - 1);
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int e = min(lane + 64 * j, E - 1);
+        v[q][j] = a.parts[pp * a.part_stride + (long long)t * E + e];
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < PB; ++q)
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (p0 + q < a.nparts) l[j] += v[q][j];
+  }
+  if (a.bias) {
+#pragma unroll
+    for (int j = 0; j < PER; ++j) l[j] += bf2f(braw[j]);
+  }
+}
+
+// Top-k, weights and expert grouping for the T tokens of one block (16 waves;
+// wave w takes tokens w, w+16, ...).  load(t, l) fills the lane's logits l[j] of
+// experts lane + 64 j (bias included).
+template <int PER, class Load>
+MKD_DEV void select_body(const RouterArgs& a, Load&& load) {
+  __shared__ uint32_t cu_s[16][8];
+  __shared__ int ce_s[16][8], slot_s[16][8];
+  __shared__ float ck_s[16][8];
+  __shared__ float sel_s[16][8], pw_s[16][8];
+  __shared__ float wsel_s[16][8];
+  __shared__ int idx_s[128 * 8];
+  __shared__ int cnt[kMaxE], off[kMaxE], cursor[kMaxE];
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int E = a.E, K = a.K, T = a.T;
+  const bool sigm = a.mode & 1, pre = a.mode & 2, norm = a.mode & 4, qwen = a.mode & 8;
+  for (int e = tid; e < E; e += blockDim.x) { cnt[e] = 0; cursor[e] = 0; }
+  for (int t = wv; t < T; t += 16) {
+    float l[PER];
+    load(t, l);
+    // every slot of the token starts invalid so that NaN logits (no consistent
+    // ranks) can never route a slot to an out-of-range expert below
+    if (lane < K) idx_s[t * K + lane] = -1;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E) {
+        if (a.logits_out) a.logits_out[(long long)t * E + e] = l[j];
+      } else {
+        l[j] = -INFINITY;
+      }
+      mx = fmaxf(mx, l[j]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.f, ex[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      ex[j] = (lane + 64 * j < E) ? expf(l[j] - mx) : 0.f;
+      sum += ex[j];
+    }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sum;
+    // ---- top-K: radix select on order-preserving key codes ----
+    // The threshold is the code of the K-th largest key, found bit by bit from
+    // the top with wave ballots; keys above it are taken, keys equal to it are
+    // taken lowest index first until K.  Slots e >= E get code 0, below every
+    // real key.
+    float key[PER];
+    uint32_t u[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      key[j] = (qwen || !pre) ? l[j] : (sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv);
+      u[j] = (e < E) ? order_code(key[j]) : 0u;
+    }
+    uint32_t thr = 0, hmask = 0;
+    int kt = K;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t m = hmask | (1u << bit), want = thr | (1u << bit);
+      int c = 0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) c += __popcll(__ballot((u[j] & m) == want));
+      if (c >= kt) thr = want;
+      else kt -= c;
+      hmask = m;
+    }
+    // compact the K chosen elements (index order) into the wave's candidate slots
+    int cpos[PER];
+    int nsel = 0, ties = 0;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const unsigned long long eq = __ballot(u[j] == thr);
+      const bool take = u[j] > thr || (u[j] == thr && ties + lanes_below(eq) < kt);
+      const unsigned long long tm = __ballot(take);
+      cpos[j] = take ? nsel + lanes_below(tm) : -1;
+      if (take) {
+        cu_s[wv][cpos[j]] = u[j];
+        ce_s[wv][cpos[j]] = lane + 64 * j;
+        ck_s[wv][cpos[j]] = key[j];
+      }
+      nsel += __popcll(tm);
+      ties += __popcll(eq);
+    }
+    wave_lds_sync();
+    // output slot = rank among the K chosen (key descending, index ascending);
+    // each lane also forms its slot's term of the weight normalisation
+    if (lane < K) {
+      const uint32_t ui = cu_s[wv][lane];
+      const int ei = ce_s[wv][lane];
+      int r = 0;
+      for (int m = 0; m < K; ++m) {
+        const uint32_t um = cu_s[wv][m];
+        r += (um > ui) | ((um == ui) & (ce_s[wv][m] < ei));
+      }
+      idx_s[t * K + r] = ei;
+      sel_s[wv][r] = ck_s[wv][lane];
+      slot_s[wv][lane] = r;
+    }
+    wave_lds_sync();
+    if (lane < K) {
+      const float sv = sel_s[wv][lane];
+      float pv;
+      if (qwen) pv = rbf(expf(sv - mx) * inv);        // softmax value at the logit, bf16
+      else if (pre) pv = sv;
+      else if (sigm) pv = 1.0f / (1.0f + expf(-sv));
+      else pv = expf(sv - sel_s[wv][0]);             // softmax over the top-k (slot 0 = max)
+      pw_s[wv][lane] = pv;
+    }
+    wave_lds_sync();
+    if (lane < K) {
+      const float pv = pw_s[wv][lane];
+      float w = pv;
+      if (qwen || (pre && norm) || (!pre && !sigm)) {
+        float s = 0.f;                                 // k order
+        for (int k = 0; k < K; ++k) s += pw_s[wv][k];
+        w = qwen ? rbf(pv * (1.0f / s)) : pv * (1.0f / s);
+      }
+      wsel_s[wv][lane] = w;
+      const int e = idx_s[t * K + lane];
+      if (a.idx_out) a.idx_out[t * K + lane] = e;
+      if (a.topk_out) a.topk_out[t * K + lane] = w;
+      if (a.slot_w) a.slot_w[t * K + lane] = w;
+    }
+    wave_lds_sync();
+    if (a.aff_full) {
+      const bool full = pre && !norm && !qwen;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const int e = lane + 64 * j;
+        if (e >= E) continue;
+        float v;
+        if (full) v = sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv;
+        else v = cpos[j] >= 0 ? wsel_s[wv][slot_s[wv][cpos[j]]] : 0.f;
+        a.aff_full[(long long)t * E + e] = v;
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  if (!a.n_groups) return;
+  __syncthreads();
+  // ---- expert groups: per-expert counts, one wave scans them ----
+  for (int p = tid; p < T * K; p += blockDim.x) {
+    const int e = idx_s[p];
+    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  }
+  __syncthreads();
+  if (wv == 0) {
+    constexpr int PE = kMaxE / 64;
+    int c[PE], lsum = 0, llive = 0;
+#pragma unroll
+    for (int j = 0; j < PE; ++j) {
+      const int e = lane * PE + j;
+      c[j] = (e < E) ? cnt[e] : 0;
+      lsum += c[j];
+      llive += c[j] > 0;
+    }
+    int base = wave_excl_scan(lsum, lane);
+    int gbase = wave_excl_scan(llive, lane);
+#pragma unroll
+    for (int j = 0; j < PE; ++j) {
+      const int e = lane * PE + j;
+      if (e < E) {
+        off[e] = base;
+        if (c[j] > 0) {
+          a.grp_expert[gbase] = e;
+          a.grp_count[gbase] = c[j];
+          a.grp_offset[gbase] = base;
+          ++gbase;
+        }
+      }
+      base += c[j];
+    }
+    if (lane == 63) *a.n_groups = gbase;
+  }
+  __syncthreads();
+  for (int p = tid; p < T * K; p += blockDim.x) {
+    const int e = idx_s[p];
+    if (e < 0 || e >= E) continue;
+    const int q = off[e] + atomicAdd(&cursor[e], 1);
+    a.pair_token[q] = p / K;
+    a.pair_slot[q] = p;
+  }
+}
+
+}  // namespace mkd

@@ -18,6 +18,7 @@ at position_ids (the reference's [B, 1, S_prior, d] per TP rank).
 """
 from __future__ import annotations
 
+import ctypes as C
 import hashlib
 import math
 from dataclasses import dataclass, field
@@ -28,6 +29,16 @@ from torch import nn
 
 from . import _lib as L
 from . import packing
+
+
+def set_decode_path(mode: str = "multi_kernel") -> None:
+    """Decode-layer execution (process-global): "multi_kernel" (default) runs
+    each layer as the per-stage kernel sequence; "persistent" runs each layer
+    as one persistent kernel launch where the model and batch allow it."""
+    modes = {"multi_kernel": 0, "persistent": 1}
+    if mode not in modes:
+        raise ValueError(f"decode path {mode!r} not in {sorted(modes)}")
+    L.check(L.load().mkd_set_decode_path(modes[mode]), "set_decode_path")
 
 
 @dataclass
@@ -299,6 +310,15 @@ class Qwen3MoeMegakernelModel(nn.Module):
             self.ws.data_ptr(), self.ws.numel(), L.stream_ptr(self.device))
         L.check(rc, "qwen3_decode_layers")
         return hidden
+
+    def layer_kernel_status(self, batch: Optional[int] = None):
+        """(persistent layer kernel planned for this batch, a grid barrier timed out).
+        Synchronises the device."""
+        used, timeout = C.c_int32(0), C.c_int32(0)
+        rc = L.load().mkd_qwen3_layer_kernel_status(self._model, batch or self.batch, self.ws.data_ptr(),
+                                                   self.ws.numel(), C.byref(used), C.byref(timeout))
+        L.check(rc, "qwen3_layer_kernel_status")
+        return bool(used.value), bool(timeout.value)
 
     def step(self, token_ids: torch.Tensor, position_ids: torch.Tensor, hidden: torch.Tensor,
              logits: torch.Tensor, next_tokens: torch.Tensor):

@@ -1,0 +1,128 @@
+"""The persistent decoder-layer kernel (one launch per layer, stages separated by
+grid barriers) against the fp32 oracle (qwen_decoder_layer, the reference
+layer flow qwen_with_megakernel.py:414-531) and against the multi-kernel layer
+path on the same inputs.  Hidden states within 2e-2 (max-abs error relative to
+the reference's max-abs), bit-identical from run to run, KV rows written only at
+each sequence's position, no grid-barrier timeout."""
+import pytest
+import torch
+
+from conftest import max_abs_rel
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def bf(t):
+    return t.to(torch.bfloat16)
+
+
+def _ref_layer(hf):
+    return ref.QwenLayer(wq=hf["q_proj"], wk=hf["k_proj"], wv=hf["v_proj"], wo=hf["o_proj"],
+                         q_norm=hf["q_norm"], k_norm=hf["k_norm"], ln_in=hf["input_layernorm"],
+                         ln_post=hf["post_attention_layernorm"], router=hf["gate"],
+                         gate_up=hf["gate_up_proj"], down=hf["down_proj"])
+
+
+@pytest.fixture
+def persistent():
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    Q.set_decode_path("persistent")
+    yield
+    Q.set_decode_path("multi_kernel")
+
+
+def _setup(dev, B, S, seed, kv_block=0):
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=1, max_batch=B, max_seq=S, kv_block_len=kv_block)
+    hf = Q.random_layer_hf(cfg, 0, seed, "cpu")
+    g = torch.Generator().manual_seed(seed)
+    pos = torch.randint(S // 2, S - 1, (B,), generator=g, dtype=torch.int32)
+    x = bf(torch.randn(B, cfg.hidden_size, generator=g))
+    kc = bf(torch.randn(B, 4, S, 128, generator=g))
+    vc = bf(torch.randn(B, 4, S, 128, generator=g))
+    layers = [Q.pack_layer({k: v.to(dev) for k, v in hf.items()}, cfg.expert_format)]
+    model = Q.Qwen3MoeMegakernelModel(cfg, layers, B, dev)
+    return Q, cfg, hf, pos, x, kc, vc, model
+
+
+def _run(model, x, kc, vc, pos, dev):
+    model.kv_mgr.k(0).copy_(kc.to(dev))
+    model.kv_mgr.v(0).copy_(vc.to(dev))
+    y = x.to(dev).contiguous()
+    model.decode_layers(y, pos.to(dev))
+    torch.cuda.synchronize()
+    return y.cpu(), model.kv_mgr.k(0).cpu(), model.kv_mgr.v(0).cpu()
+
+
+@pytest.mark.parametrize("B,S", [(1, 1024), (2, 1024), (4, 1024), (2, 4096)])
+def test_layer_kernel_vs_oracle_and_multi_kernel(mk, dev, persistent, B, S):
+    print(f"layer kernel B={B} S={S}", flush=True)
+    Q, cfg, hf, pos, x, kc, vc, model = _setup(dev, B, S, seed=31 + B + S)
+    assert model.layer_kernel_status(B)[0], "persistent kernel not planned for this shape"
+    y1, k1, v1 = _run(model, x, kc, vc, pos, dev)
+    used, timeout = model.layer_kernel_status(B)
+    assert used and not timeout
+    y1b, _, _ = _run(model, x, kc, vc, pos, dev)
+    assert torch.equal(y1, y1b)
+    Q.set_decode_path("multi_kernel")
+    try:
+        assert not model.layer_kernel_status(B)[0]
+        y2, k2, v2 = _run(model, x, kc, vc, pos, dev)
+    finally:
+        Q.set_decode_path("persistent")
+    cos, sin = ref.rope_cos_sin(pos, 128, cfg.rope_theta)
+    y_ref, _ = ref.qwen_decoder_layer(x, _ref_layer(hf), kc.clone(), vc.clone(), cos, sin, pos,
+                                      ref.QwenShape())
+    assert max_abs_rel(y1, y_ref) < TOL
+    assert max_abs_rel(y1, y2) < TOL
+    for b in range(B):
+        p = int(pos[b])
+        for new, old, other in ((k1, kc, k2), (v1, vc, v2)):
+            changed = (new[b] != old[b]).any(-1).any(0).nonzero().flatten().tolist()
+            assert changed in ([p], [])
+            assert max_abs_rel(new[b, :, p], other[b, :, p]) < TOL
+
+
+def test_layer_kernel_paged_kv_matches_flat(mk, dev, persistent):
+    """Block (paged) KV pool through the persistent kernel: bit-identical hidden
+    states to the flat cache holding the same rows; new rows at the table slot."""
+    B, S, blk = 3, 1024, 64
+    Q, cfg, hf, pos, x, kc, vc, mf = _setup(dev, B, S, seed=5)
+    _, _, _, _, _, _, _, mp = _setup(dev, B, S, seed=5, kv_block=blk)
+    assert mf.layer_kernel_status(B)[0] and mp.layer_kernel_status(B)[0]
+    pos = torch.tensor([1000, 63, 640], dtype=torch.int32)
+    table = mp.kv_mgr.block_table.cpu().long()
+    kp = torch.zeros(mp.kv_mgr.num_blocks, blk, 4, 128, dtype=torch.bfloat16)
+    vp = torch.zeros_like(kp)
+    for b in range(B):
+        for j in range(S // blk):
+            kp[table[b, j]] = kc[b, :, j * blk:(j + 1) * blk].permute(1, 0, 2)
+            vp[table[b, j]] = vc[b, :, j * blk:(j + 1) * blk].permute(1, 0, 2)
+    yf, kf, _ = _run(mf, x, kc, vc, pos, dev)
+    mp.kv_mgr.k(0).copy_(kp.to(dev))
+    mp.kv_mgr.v(0).copy_(vp.to(dev))
+    yp = x.to(dev).contiguous()
+    mp.decode_layers(yp, pos.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(yf, yp.cpu())
+    kp_new = mp.kv_mgr.k(0).cpu()
+    changed = (kp_new != kp).any(-1).any(-1).nonzero().tolist()
+    want = sorted([int(table[b, int(pos[b]) // blk]), int(pos[b]) % blk] for b in range(B))
+    assert sorted(changed) == want
+    for b in range(B):
+        p = int(pos[b])
+        assert torch.equal(kp_new[table[b, p // blk], p % blk], kf[b, :, p])
+    assert not mp.layer_kernel_status(B)[1]
+
+
+def test_layer_kernel_not_planned_for_large_batch(mk, dev, persistent):
+    """Batches above the persistent kernel's limit run the multi-kernel layers."""
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=1, max_batch=8, max_seq=256)
+    hf = Q.random_layer_hf(cfg, 0, 3, "cpu")
+    layers = [Q.pack_layer({k: v.to(dev) for k, v in hf.items()}, cfg.expert_format)]
+    model = Q.Qwen3MoeMegakernelModel(cfg, layers, 8, dev)
+    assert not model.layer_kernel_status(8)[0]
+    assert model.layer_kernel_status(4)[0]
