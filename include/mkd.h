@@ -305,6 +305,9 @@ typedef struct {
                                   (all S_max)                                    */
   float act_alpha;             /* Swish alpha (GPT-OSS 1.702)                    */
   float gate_hi, gate_lo, up_hi, up_lo;   /* expert clamps (+-INFINITY = none)   */
+  /* Device copy of the per-layer pointers (mkd_qwen3_write_layer_table), read by
+   * the persistent decode path; NULL: that path is not used.                   */
+  const void* layer_table;
 } mkd_qwen3_model;
 #define MKD_VARIANT_QWEN3 0
 #define MKD_VARIANT_GPT_OSS 1
@@ -362,8 +365,9 @@ int mkd_profile_count(void); /* launches recorded since the last mkd_profile_eve
  * Decode-layer execution path (no counterpart in the reference, whose step is
  * one compiled NEFF).  mode 0 (default): each layer of
  * mkd_qwen3_decode_layers is the multi-kernel sequence.  mode 1: each layer is
- * ONE persistent kernel launch (all stages on one block per CU, separated by
- * grid barriers) when the model is the Qwen3 flow with bf16 experts, B <= 4,
+ * ONE persistent kernel launch for all layers (all stages on one block per CU,
+ * separated by grid barriers) when m->layer_table is set and the model is the
+ * Qwen3 flow with bf16 experts, B <= 4,
  * d in {64, 128}, gqa <= 16, no biases / sinks / windows, and the stage
  * buffers fit the LDS budget; other configurations keep the multi-kernel
  * sequence.  The workspace size does not depend on the mode.  Process-global.
@@ -373,6 +377,11 @@ int mkd_profile_count(void); /* launches recorded since the last mkd_profile_eve
  * are bounded so the kernel always completes).
  * ------------------------------------------------------------------------- */
 int mkd_set_decode_path(int mode);
+/* The per-layer weight and cache pointers of m as a device table (written once,
+ * synchronously, to `table`, a device buffer of mkd_qwen3_layer_table_bytes(m)
+ * bytes); set m->layer_table to it to enable the persistent decode path. */
+size_t mkd_qwen3_layer_table_bytes(const mkd_qwen3_model* m);
+int mkd_qwen3_write_layer_table(const mkd_qwen3_model* m, void* table, size_t table_bytes);
 int mkd_qwen3_layer_kernel_status(const mkd_qwen3_model* m, int B, const void* workspace,
                                   size_t workspace_bytes, int* used, int* barrier_timeout);
 

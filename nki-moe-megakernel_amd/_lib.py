@@ -86,6 +86,7 @@ class Qwen3Model(C.Structure):
         ("sinks", C.POINTER(vp)), ("router_bias", C.POINTER(vp)), ("gate_up_bias", C.POINTER(vp)),
         ("down_bias", C.POINTER(vp)), ("window", C.POINTER(i32)), ("layer_s_max", C.POINTER(i32)),
         ("act_alpha", f32), ("gate_hi", f32), ("gate_lo", f32), ("up_hi", f32), ("up_lo", f32),
+        ("layer_table", vp),
     ]
 
 
@@ -117,6 +118,8 @@ _SIGS = {
     "mkd_profile_events": (i32, [i32, C.POINTER(vp), C.POINTER(vp), i32]),
     "mkd_profile_count": (i32, []),
     "mkd_set_decode_path": (i32, [i32]),
+    "mkd_qwen3_layer_table_bytes": (sz, [C.POINTER(Qwen3Model)]),
+    "mkd_qwen3_write_layer_table": (i32, [C.POINTER(Qwen3Model), vp, sz]),
     "mkd_qwen3_layer_kernel_status": (i32, [C.POINTER(Qwen3Model), i32, vp, sz, C.POINTER(i32),
                                             C.POINTER(i32)]),
 }

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <vector>
 
 #include "common.h"
 #include "mkd_internal.h"
@@ -776,13 +777,15 @@ struct LkPlan {
 };
 
 // Units per block (LB) and per wave (LW) of a split-K stage, over every group count.
-static void lk_bounds(int NRB, int KB, int ngmax, int NB, int& LB, int& LW) {
+// Units per block (LB; row blocks for the down stage, rbm) and per wave (LW)
+// of a split-K stage, over every group count.
+static void lk_bounds(int NRB, int KB, int ngmax, int NB, int& LB, int& LW, bool rbm = false) {
   LB = LW = 0;
   for (int ng = 1; ng <= ngmax; ++ng) {
-    const int F = ng * NRB * KB;
-    const long long fpb = lk_fpb(F, KB, NB);
+    const int F = ng * NRB * KB, span = rbm ? ng * KB : KB;
+    const long long fpb = lk_fpb(F, span, NB);
     const long long fpw = (fpb + 7) / 8;
-    LB = std::max(LB, (int)((fpb + KB - 1) / KB + 1));
+    LB = std::max(LB, (int)((fpb + span - 1) / span + 1));
     LW = std::max(LW, (int)((fpw + KB - 1) / KB + 1));
   }
 }
@@ -793,7 +796,8 @@ static LkPlan lk_plan(const mkd_qwen3_model* m, int B) {
   LkPlan p;
   const bool biasless = !m->b_qkv && !m->b_o && !m->sinks && !m->router_bias && !m->gate_up_bias &&
                         !m->down_bias && !m->window && !m->layer_s_max;
-  if (m->variant != MKD_VARIANT_QWEN3 || m->expert_format != 0 || !biasless) return p;
+  if (m->variant != MKD_VARIANT_QWEN3 || m->expert_format != 0 || !biasless || !m->layer_table) return p;
+  if ((long long)m->num_layers * kLkBarriers >= (1LL << 30)) return p;
   if (B < 1 || B > kLkMaxB || (m->d != 64 && m->d != 128) || m->nkv < 1 || m->nq % m->nkv != 0 ||
       m->nq / m->nkv > 16 || m->H % 32 != 0 || m->I % 32 != 0 || m->E % 16 != 0 || m->E > 512 ||
       m->K < 1 || m->K > 8 || m->K > m->E || (m->nq * m->d) % 32 != 0 || !m->q_norm || !m->k_norm ||
@@ -815,19 +819,14 @@ static LkPlan lk_plan(const mkd_qwen3_model* m, int B) {
   lk_bounds(m->H / 16, m->nq * m->d / 32, 1, NB, p.LBo, lw); LW = std::max(LW, lw);
   lk_bounds(m->E / 16, m->H / 32, 1, NB, p.LBr, lw); LW = std::max(LW, lw);
   lk_bounds(2 * m->I / 16, m->H / 32, ngmax, NB, p.LBgu, lw); LW = std::max(LW, lw);
-  lk_bounds(m->H / 16, m->I / 32, ngmax, NB, p.LBdn, lw); LW = std::max(LW, lw);
-  // a down-stage block range must span at most kLkActG expert groups
-  for (int ng = 1; ng <= ngmax; ++ng) {
-    const int FGd = (m->H / 16) * (m->I / 32), F = ng * FGd;
-    if (lk_fpb(F, m->I / 32, NB) > (kLkActG - 1) * FGd + 1) return p;
-  }
+  lk_bounds(m->H / 16, m->I / 32, ngmax, NB, p.LBdn, lw, true); LW = std::max(LW, lw);
   p.LW = LW;
   p.NB = NB;
   p.nch_max = (m->S_max + 1 + 127) / 128;
   const int gqa = m->nq / m->nkv, d = m->d;
   const size_t A = a16((size_t)2 * B * m->H);
   const size_t Bs = a16(std::max({(size_t)2 * B * std::max(m->H, m->nq * d), (size_t)6 * B * m->H,
-                                  (size_t)2 * kLkActG * kLkMaxB * m->I}));
+                                  (size_t)2 * B * m->K * m->I}));
   const size_t Cs = a16(std::max((size_t)8 * LW * 1024,
                                  (size_t)16 * d * 2 + 2 * d * 2 + 2 * 8 * 16 * 4 + (size_t)8 * gqa * d * 4));
   const size_t S = kLkSelBytes;
@@ -889,50 +888,41 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   return w;
 }
 
-// The decode layers as persistent layer-kernel launches (one per layer).
+// The decode layers as ONE persistent kernel launch (all layers).
 static int decode_layers_lk(const mkd_qwen3_model* m, int B, uint16_t* x, const int* position_ids,
                             const float* cos, const float* sin, StepWs& w, hipStream_t s) {
   const LkPlan& p = w.lk.plan;
   const int ha = m->H_actual > 0 ? m->H_actual : m->H;
   const int qkv_n = (m->nq + 2 * m->nkv) * m->d;
   MKD_TRY(layer_reset_launch(w.lk.bar, s), "layer kernel barrier reset");
-  for (int l = 0; l < m->num_layers; ++l) {
-    LayerArgs L;
-    memset(&L, 0, sizeof(L));
-    L.B = B; L.H = m->H; L.nq = m->nq; L.nkv = m->nkv; L.gqa = m->nq / m->nkv; L.d = m->d;
-    L.E = m->E; L.K = m->K; L.I = m->I; L.S_max = m->S_max; L.NB = p.NB;
-    L.eps = m->eps; L.inv_h = 1.0f / (float)ha; L.qk_eps = m->eps;
-    L.scale = 1.0f / sqrtf((float)m->d);
-    L.ln_in = static_cast<const uint16_t*>(m->ln_in[l]);
-    L.ln_post = static_cast<const uint16_t*>(m->ln_post[l]);
-    L.q_norm = static_cast<const uint16_t*>(m->q_norm[l]);
-    L.k_norm = static_cast<const uint16_t*>(m->k_norm[l]);
-    L.q = LkGemv{static_cast<const uint16_t*>(m->w_qkv[l]), 0, qkv_n / 16, m->H / 32, w.lk.pq, p.LBq, p.LW};
-    L.o = LkGemv{static_cast<const uint16_t*>(m->w_o[l]), 0, m->H / 16, m->nq * m->d / 32, w.lk.po,
-                 p.LBo, p.LW};
-    L.r = LkGemv{static_cast<const uint16_t*>(m->router[l]), 0, m->E / 16, m->H / 32, w.lk.pr, p.LBr, p.LW};
-    L.gu = LkGemv{static_cast<const uint16_t*>(m->gate_up[l]), (long long)2 * m->I * m->H,
-                  2 * m->I / 16, m->H / 32, w.lk.pgu, p.LBgu, p.LW};
-    L.dn = LkGemv{static_cast<const uint16_t*>(m->down[l]), padded_rows(m->H) * m->I, m->H / 16,
-                  m->I / 32, w.lk.pdn, p.LBdn, p.LW};
-    L.k_cache = static_cast<uint16_t*>(m->k_cache[l]);
-    L.v_cache = static_cast<uint16_t*>(m->v_cache[l]);
-    L.cache_h_stride = (long long)m->S_max * m->d;
-    L.cache_b_stride = L.cache_h_stride * m->nkv;
-    L.block_table = m->block_table;
-    L.tbl_stride = m->blocks_per_seq; L.blk_len = m->block_len; L.num_blocks = m->num_blocks;
-    L.cos = cos; L.sin = sin; L.pos = position_ids;
-    L.x = x;
-    L.attn_po = w.lk.apo; L.attn_ml = w.lk.aml; L.nch_max = p.nch_max;
-    L.attn_out = w.attn.attn;
-    L.bar = w.lk.bar; L.bar_base = l * kLkBarriers;
-    L.router_mode = MKD_ROUTER_QWEN;
-    L.lds_a = p.lds_a; L.lds_b = p.lds_b; L.lds_c = p.lds_c; L.lds_s = p.lds_s;
-    L.lds_total = p.lds_total;
-    const int ps = prof_begin(MKD_KCLASS_LAYER, s);
-    MKD_TRY(layer_kernel_launch(L, s), "persistent layer kernel");
-    prof_end(ps, s);
-  }
+  LayerArgs L;
+  memset(&L, 0, sizeof(L));
+  L.B = B; L.H = m->H; L.nq = m->nq; L.nkv = m->nkv; L.gqa = m->nq / m->nkv; L.d = m->d;
+  L.E = m->E; L.K = m->K; L.I = m->I; L.S_max = m->S_max; L.NB = p.NB;
+  L.num_layers = m->num_layers;
+  L.layers = static_cast<const LkLayer*>(m->layer_table);
+  L.eps = m->eps; L.inv_h = 1.0f / (float)ha; L.qk_eps = m->eps;
+  L.scale = 1.0f / sqrtf((float)m->d);
+  L.q = LkGemv{nullptr, 0, qkv_n / 16, m->H / 32, w.lk.pq, p.LBq, p.LW};
+  L.o = LkGemv{nullptr, 0, m->H / 16, m->nq * m->d / 32, w.lk.po, p.LBo, p.LW};
+  L.r = LkGemv{nullptr, 0, m->E / 16, m->H / 32, w.lk.pr, p.LBr, p.LW};
+  L.gu = LkGemv{nullptr, (long long)2 * m->I * m->H, 2 * m->I / 16, m->H / 32, w.lk.pgu, p.LBgu, p.LW};
+  L.dn = LkGemv{nullptr, padded_rows(m->H) * m->I, m->H / 16, m->I / 32, w.lk.pdn, p.LBdn, p.LW};
+  L.cache_h_stride = (long long)m->S_max * m->d;
+  L.cache_b_stride = L.cache_h_stride * m->nkv;
+  L.block_table = m->block_table;
+  L.tbl_stride = m->blocks_per_seq; L.blk_len = m->block_len; L.num_blocks = m->num_blocks;
+  L.cos = cos; L.sin = sin; L.pos = position_ids;
+  L.x = x;
+  L.attn_po = w.lk.apo; L.attn_ml = w.lk.aml; L.nch_max = p.nch_max;
+  L.attn_out = w.attn.attn;
+  L.bar = w.lk.bar;
+  L.router_mode = MKD_ROUTER_QWEN;
+  L.lds_a = p.lds_a; L.lds_b = p.lds_b; L.lds_c = p.lds_c; L.lds_s = p.lds_s;
+  L.lds_total = p.lds_total;
+  const int ps = prof_begin(MKD_KCLASS_LAYER, s);
+  MKD_TRY(layer_kernel_launch(L, s), "persistent decode kernel");
+  prof_end(ps, s);
   return MKD_OK;
 }
 
@@ -1194,6 +1184,29 @@ int mkd_profile_events(int kernel_class, void* const* start_events, void* const*
 }
 
 int mkd_profile_count(void) { return g_prof.next; }
+
+size_t mkd_qwen3_layer_table_bytes(const mkd_qwen3_model* m) {
+  return m && m->num_layers > 0 ? sizeof(LkLayer) * (size_t)m->num_layers : 0;
+}
+
+int mkd_qwen3_write_layer_table(const mkd_qwen3_model* m, void* table, size_t table_bytes) {
+  MKD_REQUIRE(m && table, MKD_ERR_NULL, "write_layer_table: null pointer");
+  MKD_REQUIRE(m->num_layers > 0, MKD_ERR_INVALID, "write_layer_table: num_layers must be > 0");
+  MKD_REQUIRE(table_bytes >= mkd_qwen3_layer_table_bytes(m), MKD_ERR_WORKSPACE,
+              "write_layer_table: %zu < %zu bytes", table_bytes, mkd_qwen3_layer_table_bytes(m));
+  std::vector<LkLayer> t((size_t)m->num_layers);
+  auto at = [](const void* const* arr, int l) { return arr ? static_cast<const uint16_t*>(arr[l]) : nullptr; };
+  for (int l = 0; l < m->num_layers; ++l) {
+    t[l].w_qkv = at(m->w_qkv, l); t[l].w_o = at(m->w_o, l);
+    t[l].q_norm = at(m->q_norm, l); t[l].k_norm = at(m->k_norm, l);
+    t[l].ln_in = at(m->ln_in, l); t[l].ln_post = at(m->ln_post, l);
+    t[l].router = at(m->router, l); t[l].gate_up = at(m->gate_up, l); t[l].down = at(m->down, l);
+    t[l].k_cache = m->k_cache ? static_cast<uint16_t*>(m->k_cache[l]) : nullptr;
+    t[l].v_cache = m->v_cache ? static_cast<uint16_t*>(m->v_cache[l]) : nullptr;
+  }
+  MKD_TRY(hipMemcpy(table, t.data(), sizeof(LkLayer) * t.size(), hipMemcpyHostToDevice), "layer table");
+  return MKD_OK;
+}
 
 int mkd_set_decode_path(int mode) {
   MKD_REQUIRE(mode == 0 || mode == 1, MKD_ERR_INVALID, "set_decode_path: mode %d must be 0 or 1", mode);

@@ -52,7 +52,7 @@
 namespace mkd {
 
 #ifndef MKD_LK_U
-#define MKD_LK_U 12
+#define MKD_LK_U 8
 #endif
 namespace {
 constexpr int kThreads = 512;
@@ -60,7 +60,6 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kU = MKD_LK_U;            // fragments per load batch
 constexpr int kMaxS = 4;               // partials per unit
 constexpr int kCols = kLkMaxB;         // token columns stored per partial
-constexpr int kActG = kLkActG;          // expert groups per block in the down stage
 constexpr int kChunk = 16 * kWaves;    // attention positions per unit
 constexpr int kRowChunks = kLkMaxRowElems / (8 * kThreads);   // 8-element row chunks per thread
 constexpr int kSc1 = 16;               // buffer cache-policy bit sc1 (device coherent)
@@ -107,6 +106,20 @@ MKD_DEV void dev_st4(__amdgpu_buffer_rsrc_t r, int off, uint32_t v) {
 MKD_DEV void dev_st2(__amdgpu_buffer_rsrc_t r, int off, uint16_t v) {
   __builtin_amdgcn_raw_buffer_store_b16(v, r, off, 0, kSc1);
 }
+// Reads of stage outputs (partials, attention chunks, attn_out): device
+// coherent, like the barrier flags -- every stage buffer is rewritten by the
+// next layer within the same launch, so an L2 copy of one of its lines could be
+// stale.
+constexpr int kXch = kSc1;
+MKD_DEV float xch_ldf(__amdgpu_buffer_rsrc_t r, int off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kXch));
+}
+MKD_DEV f32x4_t xch_ld4f(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(f32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kXch));
+}
+MKD_DEV u32x4_t xch_ld16(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kXch));
+}
 MKD_DEV u32x4_t ld_stream(const uint16_t* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
 }
@@ -129,13 +142,13 @@ MKD_DEV void grid_arrive(const LayerArgs& L, int k) {
   __builtin_amdgcn_s_waitcnt(0xF70);   // vmcnt(0): this wave's stores have completed
   __syncthreads();
   if (k == 3) LK_STAMP(22);
-  if (threadIdx.x == 0) ag_store(L.bar + blockIdx.x, (unsigned)(L.bar_base + k) + 1u);
+  if (threadIdx.x == 0) ag_store(L.bar + blockIdx.x, (unsigned)k + 1u);
   if (k == 3) LK_STAMP(23);
 }
 
 MKD_DEV void grid_wait(const LayerArgs& L, int k) {
   if (threadIdx.x < 64) {
-    const unsigned gen = (unsigned)(L.bar_base + k) + 1u;
+    const unsigned gen = (unsigned)k + 1u;
     const int nb = gridDim.x, lane = threadIdx.x;
     const __amdgpu_buffer_rsrc_t r = dev_rsrc(L.bar);
     unsigned* err = L.bar + kLkMaxNB;
@@ -185,11 +198,12 @@ MKD_DEV uint32_t fdiv(uint32_t n, const FDiv& f) { return (__umulhi(n, f.m) + n)
 // fpb = max(ceil(F / #CUs), ceil(KB / 3)) so that a unit of KB fragments
 // spans at most 4 blocks; waves split the block range evenly.
 struct GemvCtx {
-  int F, fpb, nbp, KB, NRB;
+  int F, fpb, nbp, KB, NRB, ng;
   int lo, hi;      // block range
   int wlo, whi;    // wave range
   int w0;          // first streaming wave (waves below it take no fragments)
-  FDiv dfpb, dKB, dNRB, dFG;
+  int span;        // fragments that must stay within 4 blocks (KB, or ng * KB)
+  FDiv dfpb, dKB, dNRB, dFG, dNG, dspan;
 };
 
 // Range of wave q: the block range split evenly over waves w0 .. 7.
@@ -203,39 +217,69 @@ MKD_DEV void wave_range(const GemvCtx& c, int q, int& wlo, int& whi) {
 // w0 = 1 for a stage whose first batch is issued between a barrier's arrival
 // and its wait: wave 0 (which spins on the barrier) then has no loads in
 // flight, since a wave's vector loads complete in issue order.
-MKD_DEV GemvCtx gemv_ctx(const LkGemv& p, int ngroups, int NB, int blk, int w, int w0) {
+// rbm: the down stage's order -- units (row block, group), groups fastest --
+// with a row block's ng * KB fragments spread over at most 4 blocks.
+MKD_DEV GemvCtx gemv_ctx(const LkGemv& p, int ngroups, int NB, int blk, int w, int w0,
+                         bool rbm = false) {
+  // inputs laundered through an opaque asm: the set-up is recomputed where it
+  // is used rather than hoisted out of the layer loop and held in registers
+  int KB = p.KB, NRB = p.NRB;
+  asm volatile("" : "+s"(KB), "+s"(NRB), "+s"(ngroups), "+s"(NB));
   GemvCtx c;
   c.w0 = w0;
-  c.KB = p.KB;
-  c.NRB = p.NRB;
-  c.F = ngroups * p.NRB * p.KB;
-  c.fpb = lk_fpb(c.F, p.KB, NB);
+  c.KB = KB;
+  c.NRB = NRB;
+  c.ng = ngroups;
+  c.F = ngroups * NRB * KB;
+  c.span = rbm ? ngroups * KB : KB;
+  c.fpb = lk_fpb(c.F, c.span, NB);
   c.nbp = (c.F + c.fpb - 1) / c.fpb;
   c.lo = (int)min((long long)c.F, (long long)blk * c.fpb);
   c.hi = min(c.F, c.lo + c.fpb);
   wave_range(c, w, c.wlo, c.whi);
   c.dfpb = fdiv_make(c.fpb);
-  c.dKB = fdiv_make(p.KB);
-  c.dNRB = fdiv_make(p.NRB);
-  c.dFG = fdiv_make(p.NRB * p.KB);
+  c.dKB = fdiv_make(KB);
+  c.dNRB = fdiv_make(NRB);
+  c.dFG = fdiv_make(NRB * KB);
+  c.dNG = fdiv_make(ngroups);
+  c.dspan = fdiv_make(c.span);
   return c;
 }
 
 // Weight fragments f0 .. f0 + kU - 1 of the wave's range (past its end: the
 // first fragment of the matrix, discarded).  gexp: expert of group (null: dense).
+template <bool RBM>
 MKD_DEV void gemv_load(const LkGemv& p, const int* gexp, const GemvCtx& c, int f0,
                        u32x4_t (&buf)[kU], int lane) {
-  const int FG = p.NRB * p.KB;
-  int g = (int)fdiv((uint32_t)f0, c.dFG), rem = f0 - g * FG;
+  if constexpr (!RBM) {
+    const int FG = p.NRB * p.KB;
+    int g = (int)fdiv((uint32_t)f0, c.dFG), rem = f0 - g * FG;
 #pragma unroll
-  for (int u = 0; u < kU; ++u) {
-    const uint16_t* src = p.w + lane * 8;
-    if (f0 + u < c.whi) {
-      const long long e = gexp ? gexp[g] : 0;
-      src = p.w + e * p.gstride + ((long long)rem * 64 + lane) * 8;
+    for (int u = 0; u < kU; ++u) {
+      const uint16_t* src = p.w + lane * 8;
+      if (f0 + u < c.whi) {
+        const long long e = gexp ? gexp[g] : 0;
+        src = p.w + e * p.gstride + ((long long)rem * 64 + lane) * 8;
+      }
+      buf[u] = ld_stream(src);
+      if (++rem == FG) { rem = 0; ++g; }
     }
-    buf[u] = ld_stream(src);
-    if (++rem == FG) { rem = 0; ++g; }
+  } else {
+    const int uu = (int)fdiv((uint32_t)f0, c.dKB);
+    int kb = f0 - uu * p.KB;
+    int rb = (int)fdiv((uint32_t)uu, c.dNG);
+    int g = uu - rb * c.ng;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const uint16_t* src = p.w + lane * 8;
+      if (f0 + u < c.whi)
+        src = p.w + (long long)gexp[g] * p.gstride + ((long long)(rb * p.KB + kb) * 64 + lane) * 8;
+      buf[u] = ld_stream(src);
+      if (++kb == p.KB) {
+        kb = 0;
+        if (++g == c.ng) { g = 0; ++rb; }
+      }
+    }
   }
 }
 
@@ -249,7 +293,6 @@ struct XSrc {
   const int* gcnt;        // GROUP / ACT: tokens of each group
   const int* goff;        // GROUP: first pair of each group
   const int* ptok;        // GROUP: token of each pair
-  int gbase;              // ACT: first group held in rows
 };
 
 // Row of the lane's column for group g (null: no such column -> zeros).
@@ -262,8 +305,8 @@ MKD_DEV const void* x_row(const XSrc& x, int g, int lane) {
     return col < x.ncol ? x.rows32 + col * x.ld : nullptr;
   } else if constexpr (XM == XM_GROUP) {
     return col < x.gcnt[g] ? x.rows + x.ptok[x.goff[g] + col] * x.ld : nullptr;
-  } else {
-    return col < x.gcnt[g] ? x.rows + ((g - x.gbase) * kCols + col) * x.ld : nullptr;
+  } else {   // ACT: one row per pair position goff[g] + col
+    return col < x.gcnt[g] ? x.rows + (x.goff[g] + col) * x.ld : nullptr;
   }
 }
 
@@ -291,14 +334,21 @@ MKD_DEV void x_frag(const void* row, int k, u32x4_t& hi, u32x4_t& lo) {
 
 // The wave's fragments: MFMA tiles per unit into red[w][slot] (slot = unit -
 // the wave's first unit).  buf holds the first batch (already issued).
-template <int XM>
+template <int XM, bool RBM = false>
 MKD_DEV void gemv_run(const LkGemv& p, const int* gexp, const GemvCtx& c, u32x4_t (&buf)[kU],
                       const XSrc& x, f32x4_t* red, int lane, int w) {
   if (c.whi <= c.wlo) return;
-  const int KB = p.KB, NRB = p.NRB;
+  const int KB = p.KB, NRB = RBM ? c.ng : p.NRB;   // RBM: the group cycles fastest
   const int ufirst = (int)fdiv((uint32_t)c.wlo, c.dKB);
   int uu = ufirst, kb = c.wlo - ufirst * KB;
-  int g = (int)fdiv((uint32_t)uu, c.dNRB), urem = uu - g * NRB;
+  int g, urem;
+  if constexpr (RBM) {
+    urem = (int)fdiv((uint32_t)uu, c.dNG);   // row block
+    g = uu - urem * c.ng;
+  } else {
+    g = (int)fdiv((uint32_t)uu, c.dNRB);
+    urem = uu - g * NRB;
+  }
   const void* row = x_row<XM>(x, g, lane);
   const int koff = (lane >> 4) * 8;
   int cur = uu;
@@ -306,7 +356,7 @@ MKD_DEV void gemv_run(const LkGemv& p, const int* gexp, const GemvCtx& c, u32x4_
   for (int f0 = c.wlo; f0 < c.whi; f0 += kU) {
     u32x4_t nxt[kU];
     const bool more = f0 + kU < c.whi;
-    if (more) gemv_load(p, gexp, c, f0 + kU, nxt, lane);
+    if (more) gemv_load<RBM>(p, gexp, c, f0 + kU, nxt, lane);
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       if (f0 + u >= c.whi) break;
@@ -322,7 +372,10 @@ MKD_DEV void gemv_run(const LkGemv& p, const int* gexp, const GemvCtx& c, u32x4_
       if (++kb == KB) {
         kb = 0;
         ++uu;
-        if (++urem == NRB) {
+        if constexpr (RBM) {
+          if (++g == c.ng) { g = 0; ++urem; }
+          if (f0 + u + 1 < c.whi) row = x_row<XM>(x, g, lane);
+        } else if (++urem == NRB) {
           urem = 0;
           ++g;
           if (f0 + u + 1 < c.whi) row = x_row<XM>(x, g, lane);
@@ -366,6 +419,15 @@ MKD_DEV void gemv_finish(const LkGemv& p, const GemvCtx& c, const f32x4_t* red, 
   __syncthreads();
 }
 
+// Down stage (units (row block rb, group g), groups fastest): per row block of
+// the block range, the waves' tiles of each of its units are summed in wave
+// order, each column scaled by its (token, slot) routing weight and added to
+// that token's rows, units in group order -> one partial per (block, row block,
+// token): rows of the weighted expert sum sum_k w_k y_k (moe_tkg.py:151-170).
+struct LkSel;
+MKD_DEV void gemv_finish_dn(const LkGemv& p, const GemvCtx& c, const f32x4_t* red, LkSel* sel,
+                            int B, int blk, int lane, int w);
+
 // Sum of unit u's block partials at column col, rows r0..r0+3 (or row r0):
 // the unit's first block b0 holds it at its local index u - first unit of b0,
 // every later block (up to 3) as its local unit 0.
@@ -384,7 +446,7 @@ MKD_DEV f32x4_t part_sum4(const LkGemv& p, const GemvCtx& c, int u, int col, int
   for (int s = 0; s < kMaxS; ++s) {
     const int bb = min(b0 + s, b1);
     const int lu = bb == b0 ? lu0 : 0;
-    v[s] = dev_ld4f(r, (((bb * p.LB + lu) * kCols + col) * 16 + r0) * 4);
+    v[s] = xch_ld4f(r, (((bb * p.LB + lu) * kCols + col) * 16 + r0) * 4);
   }
   f32x4_t sum = v[0];
 #pragma unroll
@@ -401,7 +463,7 @@ MKD_DEV float part_sum1(const LkGemv& p, const GemvCtx& c, int u, int col, int r
   for (int s = 0; s < kMaxS; ++s) {
     const int bb = min(b0 + s, b1);
     const int lu = bb == b0 ? lu0 : 0;
-    v[s] = dev_ldf(rs, (((bb * p.LB + lu) * kCols + col) * 16 + r) * 4);
+    v[s] = xch_ldf(rs, (((bb * p.LB + lu) * kCols + col) * 16 + r) * 4);
   }
   float sum = v[0];
 #pragma unroll
@@ -419,9 +481,56 @@ struct LkSel {
   int pg[kLkMaxB * 8], pj[kLkMaxB * 8];
   float slot_w[kLkMaxB * 8];
   float red[kWaves * kLkMaxB];
+  float dacc[kWaves][kLkMaxB * 16];   // down stage: per-wave (token, row) sums
+  int pgrp[kLkMaxB * 8];              // group of each pair position
 };
 
 static_assert(sizeof(LkSel) <= kLkSelBytes, "selection results exceed their LDS carve");
+
+MKD_DEV void gemv_finish_dn(const LkGemv& p, const GemvCtx& c, const f32x4_t* red, LkSel* sel,
+                            int B, int blk, int lane, int w) {
+  __syncthreads();
+  if (c.hi > c.lo) {
+    const int ng = c.ng;
+    const int ub0 = (int)fdiv((uint32_t)c.lo, c.dKB), ub1 = (int)fdiv((uint32_t)(c.hi - 1), c.dKB);
+    const int rb0 = (int)fdiv((uint32_t)ub0, c.dNG), rb1 = (int)fdiv((uint32_t)ub1, c.dNG);
+    const __amdgpu_buffer_rsrc_t r = dev_rsrc(p.part);
+    float* acc = sel->dacc[w];
+    for (int ri = w; ri <= rb1 - rb0; ri += kWaves) {
+      const int rb = rb0 + ri;
+      acc[lane] = 0.f;                       // kLkMaxB * 16 == 64 entries
+      wave_lds_sync();
+      const int u0 = max(ub0, rb * ng), u1 = min(ub1, rb * ng + ng - 1);
+      for (int u = u0; u <= u1; ++u) {
+        f32x4_t s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < kWaves; ++q) {
+          int qlo, qhi;
+          wave_range(c, q, qlo, qhi);
+          if (qhi <= qlo) continue;
+          const int q0 = (int)fdiv((uint32_t)qlo, c.dKB), q1 = (int)fdiv((uint32_t)(qhi - 1), c.dKB);
+          if (q0 <= u && u <= q1) s += red[(q * p.LW + (u - q0)) * 64 + lane];
+        }
+        const int g = u - rb * ng, j = lane & 15;
+        if (j < sel->gcnt[g]) {
+          const int pq = sel->goff[g] + j;
+          const int t = sel->ptok[pq];
+          const float wt = sel->slot_w[sel->pslot[pq]];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[t * 16 + (lane >> 4) * 4 + i] += s[i] * wt;
+        }
+        wave_lds_sync();
+      }
+      if (lane < B * 4) {
+        const int t = lane >> 2, r0 = (lane & 3) * 4;
+        dev_st16(r, (((blk * p.LB + ri) * kCols + t) * 16 + r0) * 4,
+                 f32x4_t{acc[t * 16 + r0], acc[t * 16 + r0 + 1], acc[t * 16 + r0 + 2], acc[t * 16 + r0 + 3]});
+      }
+      wave_lds_sync();
+    }
+  }
+  __syncthreads();
+}
 
 // Per-token sums of squares of the block's 512 threads: ss[t] per thread in,
 // full sums out (fixed order).
@@ -463,18 +572,19 @@ struct AttnRows {
 };
 
 template <int D>
-MKD_DEV void attn_load(const LayerArgs& L, int b, int g, int c, int lane, int w, AttnRows<D>& R) {
+MKD_DEV void attn_load(const LayerArgs& L, const LkLayer& ly, int b, int g, int c, int lane, int w,
+                       AttnRows<D>& R) {
   constexpr int NK = D / 32, VW = D / 32;
   const int n = lk_prior_len(L, b);
   const int tile0 = c * kChunk + w * 16;
   const int dq = (lane >> 4) * (D / 4), vc = (lane & 15) * (D / 16);
   const int tk = tile0 + (lane & 15);
-  const uint16_t* kr = tk < n ? lk_kv_row<D>(L, L.k_cache, b, g, tk) : nullptr;
+  const uint16_t* kr = tk < n ? lk_kv_row<D>(L, ly.k_cache, b, g, tk) : nullptr;
   const uint16_t* vp[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int t = tile0 + (lane >> 4) * 4 + j;
-    vp[j] = t < n ? lk_kv_row<D>(L, L.v_cache, b, g, t) : nullptr;
+    vp[j] = t < n ? lk_kv_row<D>(L, ly.v_cache, b, g, t) : nullptr;
   }
 #pragma unroll
   for (int kk = 0; kk < NK; ++kk) R.k[kk] = kr ? ld16(kr + dq + kk * 8) : u32x4_t{0, 0, 0, 0};
@@ -493,8 +603,8 @@ MKD_DEV void attn_load(const LayerArgs& L, int b, int g, int c, int lane, int w,
 }
 
 template <int D>
-MKD_DEV void attn_unit(const LayerArgs& L, const AttnArgs& aa, const GemvCtx& cq, int b, int g, int c,
-                       AttnRows<D>& R, char* lds, int lane, int w) {
+MKD_DEV void attn_unit(const LayerArgs& L, const LkLayer& ly, const AttnArgs& aa, const GemvCtx& cq,
+                       int b, int g, int c, AttnRows<D>& R, char* lds, int lane, int w) {
   constexpr int NK = D / 32, NDT = D / 16, VW = D / 32, HD = D / 2;
   const int gqa = L.gqa;
   uint16_t* q_s = reinterpret_cast<uint16_t*>(lds);                 // [16][D]
@@ -520,7 +630,7 @@ MKD_DEV void attn_unit(const LayerArgs& L, const AttnArgs& aa, const GemvCtx& cq
       const int kind = h < gqa ? 0 : h - gqa + 1;
       const int head = h < gqa ? g * gqa + h : (kind == 1 ? L.nq + g : L.nq + L.nkv + g);
       kinds[r] = kind;
-      const uint16_t* nw = kind == 0 ? L.q_norm : (kind == 1 ? L.k_norm : nullptr);
+      const uint16_t* nw = kind == 0 ? ly.q_norm : (kind == 1 ? ly.k_norm : nullptr);
       HeadPrep<D>& q = hp[r];
       q.f32 = true;
       q.off0 = 0;
@@ -655,8 +765,8 @@ MKD_DEV void attn_unit(const LayerArgs& L, const AttnArgs& aa, const GemvCtx& cq
       const int d = threadIdx.x;
       const long long off = L.block_table ? (row * L.nkv + g) * D + d
                                           : b * L.cache_b_stride + g * L.cache_h_stride + row * D + d;
-      L.k_cache[off] = kn_s[d];
-      L.v_cache[off] = vn_s[d];
+      ly.k_cache[off] = kn_s[d];
+      ly.v_cache[off] = vn_s[d];
     }
   }
   __syncthreads();
@@ -685,10 +795,10 @@ MKD_DEV void combine_block(const LayerArgs& L, int b, int h, char* lds, int lane
     for (int u = 0; u < U; ++u) {
       const int k = k0 + kWaves * u;
       const int kc = k < nch ? k : k0;
-      mk[u] = dev_ldf(rml, (int)((base + kc) * 8));
-      lk[u] = dev_ldf(rml, (int)((base + kc) * 8 + 4));
+      mk[u] = xch_ldf(rml, (int)((base + kc) * 8));
+      lk[u] = xch_ldf(rml, (int)((base + kc) * 8 + 4));
 #pragma unroll
-      for (int e = 0; e < EL; ++e) pv[u][e] = dev_ldf(rpo, (int)(((base + kc) * D + lane * EL + e) * 4));
+      for (int e = 0; e < EL; ++e) pv[u][e] = xch_ldf(rpo, (int)(((base + kc) * D + lane * EL + e) * 4));
     }
 #pragma unroll
     for (int u = 0; u < U; ++u)
@@ -743,7 +853,7 @@ __global__ void __launch_bounds__(kThreads) layer_kernel(LayerArgs L) {
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int blk = blockIdx.x, NB = gridDim.x;
   const int B = L.B, H = L.H, QD = L.nq * D;
-  uint16_t* xs = reinterpret_cast<uint16_t*>(lds + L.lds_a);       // [B][H] x, then r
+  uint16_t* xs = reinterpret_cast<uint16_t*>(lds + L.lds_a);       // [B][H] x, then r, then next x
   char* rb = lds + L.lds_b;
   f32x4_t* red = reinterpret_cast<f32x4_t*>(lds + L.lds_c);
   LkSel* sel = reinterpret_cast<LkSel*>(lds + L.lds_s);
@@ -754,71 +864,7 @@ __global__ void __launch_bounds__(kThreads) layer_kernel(LayerArgs L) {
   aa.qk_eps = L.qk_eps;
   aa.round_qwen = 1;
 
-  // ---- P: pre-attention norm (every block, whole rows; each thread holds
-  // up to kRowChunks 8-element chunks; the x and gamma loads go out before the
-  // first QKV weight batch so that their use does not wait for it) ----
-  GemvCtx cq = gemv_ctx(L.q, 1, NB, blk, w, 0);
-  u32x4_t buf[kU];
-  uint16_t* hn = reinterpret_cast<uint16_t*>(rb);                     // [B][H]
-  {
-    u32x4_t xv[kRowChunks], gm[kRowChunks];
-#pragma unroll
-    for (int c = 0; c < kRowChunks; ++c) {
-      const int i = (c * kThreads + threadIdx.x) * 8;
-      if (i < B * H) {
-        xv[c] = ld16(L.x + i);
-        gm[c] = ld16(L.ln_in + (i % H));
-      }
-    }
-    gemv_load(L.q, nullptr, cq, cq.wlo, buf, lane);
-    float ss[kLkMaxB] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < kRowChunks; ++c) {
-      const int i = (c * kThreads + threadIdx.x) * 8;
-      if (i < B * H) {
-        *reinterpret_cast<u32x4_t*>(xs + i) = xv[c];
-        const int t = i / H;
-        float a = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) a += bf_lo(xv[c][j]) * bf_lo(xv[c][j]) + bf_hi(xv[c][j]) * bf_hi(xv[c][j]);
-#pragma unroll
-        for (int q = 0; q < kLkMaxB; ++q)
-          if (q == t) ss[q] += a;
-      }
-    }
-    block_sums(ss, B, sel, lane, w);
-#pragma unroll
-    for (int c = 0; c < kRowChunks; ++c) {
-      const int i = (c * kThreads + threadIdx.x) * 8;
-      if (i < B * H) {
-        const int t = i / H;
-        float rinv = 0.f;
-#pragma unroll
-        for (int q = 0; q < kLkMaxB; ++q)
-          if (q == t) rinv = 1.0f / sqrtf(ss[q] * L.inv_h + L.eps);
-        u32x4_t o;
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-          o[j] = pack2bf((bf_lo(xv[c][j]) * rinv) * bf_lo(gm[c][j]), (bf_hi(xv[c][j]) * rinv) * bf_hi(gm[c][j]));
-        *reinterpret_cast<u32x4_t*>(hn + i) = o;
-      }
-    }
-  }
-  __syncthreads();
-
-  LK_STAMP(1);
-  // ---- Q: QKV projection ----
-  {
-    XSrc x = {};
-    x.rows = hn;
-    x.ld = H;
-    x.ncol = B;
-    gemv_run<XM_DENSE>(L.q, nullptr, cq, buf, x, red, lane, w);
-    gemv_finish(L.q, cq, red, nullptr, B, blk, lane, w);
-  }
-
-  // ---- T: attention units (first unit's cache rows issued across the barrier) ----
-  // units (sequence t, kv head, chunk), sequence-major
+  // attention units (sequence t, kv head, chunk), sequence-major
   int ucount[kLkMaxB];
   int nunits = 0;
 #pragma unroll
@@ -838,262 +884,377 @@ __global__ void __launch_bounds__(kThreads) layer_kernel(LayerArgs L) {
     ug = r % L.nkv;
     uc = r / L.nkv;
   };
-  AttnRows<D> rows;
-  LK_STAMP(2);
-  grid_arrive(L, 0);
-  // the first unit's cache rows are loaded across the barrier (not by wave 0,
-  // which polls the barrier flags)
-  if (blk < nunits && w != 0) {
-    int ub, ug, uc;
-    unit_of(blk, ub, ug, uc);
-    attn_load<D>(L, ub, ug, uc, lane, w, rows);
-  }
-  grid_wait(L, 0);
-  LK_STAMP(3);
-  for (int uid = blk; uid < nunits; uid += NB) {
-    int ub, ug, uc;
-    unit_of(uid, ub, ug, uc);
-    if (uid != blk || w == 0) attn_load<D>(L, ub, ug, uc, lane, w, rows);
-    attn_unit<D>(L, aa, cq, ub, ug, uc, rows, reinterpret_cast<char*>(red), lane, w);
-  }
-  LK_STAMP(4);
-  grid_arrive(L, 1);
-  grid_wait(L, 1);
-  LK_STAMP(5);
 
-  // ---- C: combine, one wave per (sequence, q head) ----
-  for (int u = blk; u < B * L.nq; u += NB)
-    combine_block<D>(L, u / L.nq, u - (u / L.nq) * L.nq, reinterpret_cast<char*>(red), lane, w);
-  GemvCtx co = gemv_ctx(L.o, 1, NB, blk, w, 1);
-  LK_STAMP(6);
-  grid_arrive(L, 2);
-  gemv_load(L.o, nullptr, co, co.wlo, buf, lane);
-  grid_wait(L, 2);
-  LK_STAMP(7);
-
-  // ---- O: output projection ----
+  // ---- the input rows into LDS; the first QKV batch of layer 0 ----
+  u32x4_t buf[kU];
   {
-    uint16_t* ao = reinterpret_cast<uint16_t*>(rb);                   // [B][nq * D]
-    const __amdgpu_buffer_rsrc_t ra = dev_rsrc(L.attn_out);
-    for (int i = threadIdx.x * 8; i < B * QD; i += kThreads * 8)
-      *reinterpret_cast<u32x4_t*>(ao + i) = dev_ld16(ra, i * 2);
-    __syncthreads();
-    XSrc x = {};
-    x.rows = ao;
-    x.ld = QD;
-    x.ncol = B;
-    gemv_run<XM_DENSE>(L.o, nullptr, co, buf, x, red, lane, w);
-    gemv_finish(L.o, co, red, nullptr, B, blk, lane, w);
-  }
-  GemvCtx cr = gemv_ctx(L.r, 1, NB, blk, w, 1);
-  LK_STAMP(8);
-  grid_arrive(L, 3);
-  gemv_load(L.r, nullptr, cr, cr.wlo, buf, lane);
-  grid_wait(L, 3);
-  LK_STAMP(9);
-
-  // ---- R: residual + post-attention norm, router logits (the o_proj
-  // partials and gamma of the thread's chunks are loaded together) ----
-  uint16_t* hn2 = reinterpret_cast<uint16_t*>(rb);                    // [B][H] bf16
-  float* y32 = reinterpret_cast<float*>(rb + (size_t)B * H * 2);      // [B][H] fp32
-  {
-    f32x4_t o0[kRowChunks], o1[kRowChunks];
-    u32x4_t gm[kRowChunks];
+    const GemvCtx cq = gemv_ctx(L.q, 1, NB, blk, w, 1);
+    LkGemv q0 = L.q;
+    q0.w = L.layers[0].w_qkv;
 #pragma unroll
     for (int c = 0; c < kRowChunks; ++c) {
       const int i = (c * kThreads + threadIdx.x) * 8;
-      if (i < B * H) {
+      if (i < B * H) *reinterpret_cast<u32x4_t*>(xs + i) = ld16(L.x + i);
+    }
+    gemv_load<false>(q0, nullptr, cq, cq.wlo, buf, lane);
+  }
+  __syncthreads();
+
+  for (int l = 0; l < L.num_layers; ++l) {
+    // opaque copies: keeps the per-stage partition set-up inside the loop
+    // instead of hoisted (and held in registers across every stage)
+    int lw = w, lb = blk, tid = threadIdx.x, ln = lane;
+    asm volatile("" : "+s"(lw), "+s"(lb), "+v"(tid), "+v"(ln));
+    const LkLayer ly = L.layers[l];
+    const int kb = l * kLkBarriers;          // this layer's first barrier
+    LkGemv gq = L.q, go = L.o, gr = L.r, ggu = L.gu, gdn = L.dn;
+    gq.w = ly.w_qkv;
+    go.w = ly.w_o;
+    gr.w = ly.router;
+    ggu.w = ly.gate_up;
+    gdn.w = ly.down;
+
+    // ---- P: pre-attention norm from the rows in LDS ----
+    uint16_t* hn = reinterpret_cast<uint16_t*>(rb);                   // [B][H]
+    {
+      u32x4_t gm[kRowChunks];
+#pragma unroll
+      for (int c = 0; c < kRowChunks; ++c) {
+        const int i = (c * kThreads + tid) * 8;
+        if (i < B * H) gm[c] = ld16(ly.ln_in + (i % H));
+      }
+      float ss[kLkMaxB] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < kRowChunks; ++c) {
+        const int i = (c * kThreads + tid) * 8;
+        if (i < B * H) {
+          const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xs + i);
+          const int t = i / H;
+          float a = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) a += bf_lo(xv[j]) * bf_lo(xv[j]) + bf_hi(xv[j]) * bf_hi(xv[j]);
+#pragma unroll
+          for (int q = 0; q < kLkMaxB; ++q)
+            if (q == t) ss[q] += a;
+        }
+      }
+      block_sums(ss, B, sel, ln, w);
+#pragma unroll
+      for (int c = 0; c < kRowChunks; ++c) {
+        const int i = (c * kThreads + tid) * 8;
+        if (i < B * H) {
+          const int t = i / H;
+          float rinv = 0.f;
+#pragma unroll
+          for (int q = 0; q < kLkMaxB; ++q)
+            if (q == t) rinv = 1.0f / sqrtf(ss[q] * L.inv_h + L.eps);
+          const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xs + i);
+          u32x4_t o;
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            o[j] = pack2bf((bf_lo(xv[j]) * rinv) * bf_lo(gm[c][j]), (bf_hi(xv[j]) * rinv) * bf_hi(gm[c][j]));
+          *reinterpret_cast<u32x4_t*>(hn + i) = o;
+        }
+      }
+    }
+    __syncthreads();
+    LK_STAMP(1);
+
+    // ---- Q: QKV projection ----
+    const GemvCtx cq = gemv_ctx(L.q, 1, NB, lb, lw, 1);
+    {
+      XSrc x = {};
+      x.rows = hn;
+      x.ld = H;
+      x.ncol = B;
+      gemv_run<XM_DENSE>(gq, nullptr, cq, buf, x, red, ln, w);
+      gemv_finish(gq, cq, red, nullptr, B, blk, ln, w);
+    }
+
+    // ---- T: attention units (the first unit's cache rows across the barrier,
+    // not by wave 0, which polls the barrier flags) ----
+    AttnRows<D> rows;
+    LK_STAMP(2);
+    grid_arrive(L, kb + 0);
+    if (blk < nunits && w != 0) {
+      int ub, ug, uc;
+      unit_of(blk, ub, ug, uc);
+      attn_load<D>(L, ly, ub, ug, uc, ln, w, rows);
+    }
+    grid_wait(L, kb + 0);
+    LK_STAMP(3);
+    for (int uid = blk; uid < nunits; uid += NB) {
+      int ub, ug, uc;
+      unit_of(uid, ub, ug, uc);
+      if (uid != blk || w == 0) attn_load<D>(L, ly, ub, ug, uc, ln, w, rows);
+      attn_unit<D>(L, ly, aa, cq, ub, ug, uc, rows, reinterpret_cast<char*>(red), ln, w);
+    }
+    LK_STAMP(4);
+    grid_arrive(L, kb + 1);
+    grid_wait(L, kb + 1);
+    LK_STAMP(5);
+
+    // ---- C: combine, one block per (sequence, q head) ----
+    for (int u = blk; u < B * L.nq; u += NB)
+      combine_block<D>(L, u / L.nq, u - (u / L.nq) * L.nq, reinterpret_cast<char*>(red), ln, w);
+    LK_STAMP(6);
+    const GemvCtx co = gemv_ctx(L.o, 1, NB, lb, lw, 1);
+    grid_arrive(L, kb + 2);
+    gemv_load<false>(go, nullptr, co, co.wlo, buf, ln);
+    grid_wait(L, kb + 2);
+    LK_STAMP(7);
+
+    // ---- O: output projection ----
+    {
+      uint16_t* ao = reinterpret_cast<uint16_t*>(rb);                 // [B][nq * D]
+      const __amdgpu_buffer_rsrc_t ra = dev_rsrc(L.attn_out);
+      for (int i = tid * 8; i < B * QD; i += kThreads * 8)
+        *reinterpret_cast<u32x4_t*>(ao + i) = xch_ld16(ra, i * 2);
+      __syncthreads();
+      XSrc x = {};
+      x.rows = ao;
+      x.ld = QD;
+      x.ncol = B;
+      gemv_run<XM_DENSE>(go, nullptr, co, buf, x, red, ln, w);
+      gemv_finish(go, co, red, nullptr, B, blk, ln, w);
+    }
+    LK_STAMP(8);
+    const GemvCtx cr = gemv_ctx(L.r, 1, NB, lb, lw, 1);
+    grid_arrive(L, kb + 3);
+    gemv_load<false>(gr, nullptr, cr, cr.wlo, buf, ln);
+    grid_wait(L, kb + 3);
+    LK_STAMP(9);
+
+    // ---- R: residual + post-attention norm (r kept in LDS), router logits ----
+    uint16_t* hn2 = reinterpret_cast<uint16_t*>(rb);                  // [B][H] bf16
+    float* y32 = reinterpret_cast<float*>(rb + (size_t)B * H * 2);    // [B][H] fp32
+    {
+      f32x4_t o0[kRowChunks], o1[kRowChunks];
+      u32x4_t gm[kRowChunks];
+#pragma unroll
+      for (int c = 0; c < kRowChunks; ++c) {
+        const int i = (c * kThreads + tid) * 8;
+        if (i < B * H) {
+          const int t = i / H, h = i - t * H;
+          gm[c] = ld16(ly.ln_post + h);
+          o0[c] = part_sum4(go, co, h >> 4, t, h & 15);
+          o1[c] = part_sum4(go, co, h >> 4, t, (h & 15) + 4);
+        }
+      }
+      float ss[kLkMaxB] = {0.f, 0.f, 0.f, 0.f};
+      u32x4_t rvs[kRowChunks];
+#pragma unroll
+      for (int c = 0; c < kRowChunks; ++c) {
+        const int i = (c * kThreads + tid) * 8;
+        if (i < B * H) {
+          const int t = i / H;
+          const float ov[8] = {o0[c][0], o0[c][1], o0[c][2], o0[c][3], o1[c][0], o1[c][1], o1[c][2], o1[c][3]};
+          const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xs + i);
+          float a = 0.f;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const float r0 = rbf(bf_lo(xv[j]) + rbf(ov[2 * j]));
+            const float r1 = rbf(bf_hi(xv[j]) + rbf(ov[2 * j + 1]));
+            a += r0 * r0 + r1 * r1;
+            rvs[c][j] = pack2bf(r0, r1);
+          }
+          *reinterpret_cast<u32x4_t*>(xs + i) = rvs[c];
+#pragma unroll
+          for (int q = 0; q < kLkMaxB; ++q)
+            if (q == t) ss[q] += a;
+        }
+      }
+      block_sums(ss, B, sel, ln, w);
+#pragma unroll
+      for (int c = 0; c < kRowChunks; ++c) {
+        const int i = (c * kThreads + tid) * 8;
+        if (i < B * H) {
+          const int t = i / H;
+          float rinv = 0.f;
+#pragma unroll
+          for (int q = 0; q < kLkMaxB; ++q)
+            if (q == t) rinv = 1.0f / sqrtf(ss[q] * L.inv_h + L.eps);
+          float y[8];
+          u32x4_t yb;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            y[2 * j] = (bf_lo(rvs[c][j]) * bf_lo(gm[c][j])) * rinv;
+            y[2 * j + 1] = (bf_hi(rvs[c][j]) * bf_hi(gm[c][j])) * rinv;
+            yb[j] = pack2bf(y[2 * j], y[2 * j + 1]);
+          }
+          *reinterpret_cast<u32x4_t*>(hn2 + i) = yb;
+          *reinterpret_cast<f32x4_t*>(y32 + i) = f32x4_t{y[0], y[1], y[2], y[3]};
+          *reinterpret_cast<f32x4_t*>(y32 + i + 4) = f32x4_t{y[4], y[5], y[6], y[7]};
+        }
+      }
+    }
+    __syncthreads();
+    LK_STAMP(19);
+    {
+      XSrc x = {};
+      x.rows32 = y32;
+      x.ld = H;
+      x.ncol = B;
+      gemv_run<XM_F32>(gr, nullptr, cr, buf, x, red, ln, w);
+      gemv_finish(gr, cr, red, nullptr, B, blk, ln, w);
+    }
+    LK_STAMP(10);
+    grid_arrive(L, kb + 4);
+    grid_wait(L, kb + 4);
+    LK_STAMP(11);
+
+    // ---- S: top-k and expert groups in every block ----
+    {
+      RouterArgs ra;
+      memset(&ra, 0, sizeof(ra));
+      ra.T = B;
+      ra.E = L.E;
+      ra.K = L.K;
+      ra.mode = L.router_mode;
+      ra.slot_w = sel->slot_w;
+      ra.n_groups = &sel->ng;
+      ra.grp_expert = sel->gexp;
+      ra.grp_count = sel->gcnt;
+      ra.grp_offset = sel->goff;
+      ra.pair_token = sel->ptok;
+      ra.pair_slot = sel->pslot;
+      select_body<PER>(ra, [&](int t, float (&lg)[PER]) {
+#pragma unroll
+        for (int j = 0; j < PER; ++j) {
+          const int e = min(ln + 64 * j, L.E - 1);
+          lg[j] = part_sum1(gr, cr, e >> 4, t, e & 15);
+        }
+      });
+    }
+    __syncthreads();
+    LK_STAMP(20);
+    const int ng = sel->ng;
+    if (threadIdx.x < ng)
+      for (int j = 0; j < sel->gcnt[threadIdx.x]; ++j) sel->pgrp[sel->goff[threadIdx.x] + j] = threadIdx.x;
+    __syncthreads();
+    const int npairs = ng > 0 ? sel->goff[ng - 1] + sel->gcnt[ng - 1] : 0;
+    LK_STAMP(12);
+
+    // ---- G: expert gate / up projections ----
+    const GemvCtx cg = gemv_ctx(ggu, ng, NB, lb, lw, 0);
+    gemv_load<false>(ggu, sel->gexp, cg, cg.wlo, buf, ln);
+    {
+      XSrc x = {};
+      x.rows = hn2;
+      x.ld = H;
+      x.gcnt = sel->gcnt;
+      x.goff = sel->goff;
+      x.ptok = sel->ptok;
+      gemv_run<XM_GROUP>(ggu, sel->gexp, cg, buf, x, red, ln, w);
+      gemv_finish(ggu, cg, red, sel->gcnt, 0, blk, ln, w);
+    }
+    const GemvCtx cd = gemv_ctx(gdn, ng, NB, lb, lw, 1, true);
+    LK_STAMP(13);
+    grid_arrive(L, kb + 5);
+    gemv_load<true>(gdn, sel->gexp, cd, cd.wlo, buf, ln);
+    grid_wait(L, kb + 5);
+    LK_STAMP(14);
+
+    // ---- D: activations of the groups in the block's range, then the down
+    // projections (row-block-major) with the routing-weighted sum over experts ----
+    {
+      uint16_t* act = reinterpret_cast<uint16_t*>(rb);               // [pair position][I]
+      const int I = L.I;
+      // the groups of the block's units: all of them, or nu consecutive ones
+      // (cyclically) from the first unit's group
+      int g0 = 0, nu = 0;
+      if (cd.hi > cd.lo) {
+        const int ub0 = (int)fdiv((uint32_t)cd.lo, cd.dKB), ub1 = (int)fdiv((uint32_t)(cd.hi - 1), cd.dKB);
+        nu = ub1 - ub0 + 1;
+        g0 = ub0 - (int)fdiv((uint32_t)ub0, cd.dNG) * ng;
+      }
+      GemmArgs ga;
+      memset(&ga, 0, sizeof(ga));
+      ga.round_qwen = 1;
+      const int per_p = I / 4;
+      for (int it = tid; it < npairs * per_p; it += kThreads) {
+        const int q = it / per_p, i = (it - q * per_p) * 4;
+        const int gg = sel->pgrp[q];
+        if (nu < ng && (gg - g0 + ng) % ng >= nu) continue;
+        const int j = q - sel->goff[gg];
+        const int ub = gg * ggu.NRB + 2 * (i >> 4);
+        const f32x4_t gv = part_sum4(ggu, cg, ub, j, i & 15);
+        const f32x4_t uv = part_sum4(ggu, cg, ub + 1, j, i & 15);
+        uint2 o;
+        o.x = pack2bf(swiglu_value(ga, gv[0], uv[0]), swiglu_value(ga, gv[1], uv[1]));
+        o.y = pack2bf(swiglu_value(ga, gv[2], uv[2]), swiglu_value(ga, gv[3], uv[3]));
+        *reinterpret_cast<uint2*>(act + q * I + i) = o;
+      }
+      __syncthreads();
+      LK_STAMP(21);
+      XSrc x = {};
+      x.rows = act;
+      x.ld = I;
+      x.gcnt = sel->gcnt;
+      x.goff = sel->goff;
+      gemv_run<XM_ACT, true>(gdn, sel->gexp, cd, buf, x, red, ln, w);
+      gemv_finish_dn(gdn, cd, red, sel, B, blk, ln, w);
+    }
+    LK_STAMP(15);
+    grid_arrive(L, kb + 6);
+    if (l + 1 < L.num_layers) {              // the next layer's first QKV batch
+      LkGemv q1 = L.q;
+      q1.w = L.layers[l + 1].w_qkv;
+      gemv_load<false>(q1, nullptr, cq, cq.wlo, buf, ln);
+    }
+    grid_wait(L, kb + 6);
+    LK_STAMP(16);
+
+    // ---- F: every block, all rows: x = bf16(r + bf16(sum of the row block's
+    // partials)), the next layer's input, kept in LDS ----
+    {
+      const int span = cd.span;
+#pragma unroll 1
+      for (int c = 0; c < kRowChunks; ++c) {
+        const int i = (c * kThreads + tid) * 8;
+        if (i >= B * H) break;
         const int t = i / H, h = i - t * H;
-        gm[c] = ld16(L.ln_post + h);
-        o0[c] = part_sum4(L.o, co, h >> 4, t, h & 15);
-        o1[c] = part_sum4(L.o, co, h >> 4, t, (h & 15) + 4);
-      }
-    }
-    float ss[kLkMaxB] = {0.f, 0.f, 0.f, 0.f};
-    u32x4_t rvs[kRowChunks];
+        const int rbk = h >> 4, r0 = h & 15;
+        const uint32_t f0 = (uint32_t)(rbk * span);
+        const int b0 = (int)fdiv(f0, cd.dfpb), b1 = (int)fdiv(f0 + span - 1, cd.dfpb);
+        const int lr0 = rbk - (int)fdiv((uint32_t)(b0 * cd.fpb), cd.dspan);
+        const __amdgpu_buffer_rsrc_t rp = dev_rsrc(gdn.part);
+        f32x4_t v0[kMaxS], v1[kMaxS];
 #pragma unroll
-    for (int c = 0; c < kRowChunks; ++c) {
-      const int i = (c * kThreads + threadIdx.x) * 8;
-      if (i < B * H) {
-        const int t = i / H;
-        const float ov[8] = {o0[c][0], o0[c][1], o0[c][2], o0[c][3], o1[c][0], o1[c][1], o1[c][2], o1[c][3]};
-        const u32x4_t xv = *reinterpret_cast<const u32x4_t*>(xs + i);
-        float a = 0.f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float r0 = rbf(bf_lo(xv[j]) + rbf(ov[2 * j]));
-          const float r1 = rbf(bf_hi(xv[j]) + rbf(ov[2 * j + 1]));
-          a += r0 * r0 + r1 * r1;
-          rvs[c][j] = pack2bf(r0, r1);
+        for (int sidx = 0; sidx < kMaxS; ++sidx) {
+          const int bb = min(b0 + sidx, b1);
+          const int lr = bb == b0 ? lr0 : 0;
+          const int off = (((bb * gdn.LB + lr) * kCols + t) * 16 + r0) * 4;
+          v0[sidx] = xch_ld4f(rp, off);
+          v1[sidx] = xch_ld4f(rp, off + 16);
         }
-        *reinterpret_cast<u32x4_t*>(xs + i) = rvs[c];
+        f32x4_t s0 = v0[0], s1 = v1[0];
 #pragma unroll
-        for (int q = 0; q < kLkMaxB; ++q)
-          if (q == t) ss[q] += a;
+        for (int sidx = 1; sidx < kMaxS; ++sidx)
+          if (b0 + sidx <= b1) {
+            s0 += v0[sidx];
+            s1 += v1[sidx];
+          }
+        const float sv[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+        const u32x4_t rv = *reinterpret_cast<const u32x4_t*>(xs + i);
+        u32x4_t o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          o[j] = pack2bf(rbf(bf_lo(rv[j]) + rbf(sv[2 * j])), rbf(bf_hi(rv[j]) + rbf(sv[2 * j + 1])));
+        *reinterpret_cast<u32x4_t*>(xs + i) = o;
       }
-    }
-    block_sums(ss, B, sel, lane, w);
-#pragma unroll
-    for (int c = 0; c < kRowChunks; ++c) {
-      const int i = (c * kThreads + threadIdx.x) * 8;
-      if (i < B * H) {
-        const int t = i / H;
-        float rinv = 0.f;
-#pragma unroll
-        for (int q = 0; q < kLkMaxB; ++q)
-          if (q == t) rinv = 1.0f / sqrtf(ss[q] * L.inv_h + L.eps);
-        float y[8];
-        u32x4_t yb;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          y[2 * j] = (bf_lo(rvs[c][j]) * bf_lo(gm[c][j])) * rinv;
-          y[2 * j + 1] = (bf_hi(rvs[c][j]) * bf_hi(gm[c][j])) * rinv;
-          yb[j] = pack2bf(y[2 * j], y[2 * j + 1]);
-        }
-        *reinterpret_cast<u32x4_t*>(hn2 + i) = yb;
-        *reinterpret_cast<f32x4_t*>(y32 + i) = f32x4_t{y[0], y[1], y[2], y[3]};
-        *reinterpret_cast<f32x4_t*>(y32 + i + 4) = f32x4_t{y[4], y[5], y[6], y[7]};
-      }
-    }
-  }
-  __syncthreads();
-  LK_STAMP(19);
-  {
-    XSrc x = {};
-    x.rows32 = y32;
-    x.ld = H;
-    x.ncol = B;
-    gemv_run<XM_F32>(L.r, nullptr, cr, buf, x, red, lane, w);
-    LK_STAMP(25);
-    gemv_finish(L.r, cr, red, nullptr, B, blk, lane, w);
-  }
-  LK_STAMP(10);
-  grid_arrive(L, 4);
-  grid_wait(L, 4);
-  LK_STAMP(11);
-
-  // ---- S: top-k and expert groups in every block ----
-  {
-    RouterArgs ra;
-    memset(&ra, 0, sizeof(ra));
-    ra.T = B;
-    ra.E = L.E;
-    ra.K = L.K;
-    ra.mode = L.router_mode;
-    ra.slot_w = sel->slot_w;
-    ra.n_groups = &sel->ng;
-    ra.grp_expert = sel->gexp;
-    ra.grp_count = sel->gcnt;
-    ra.grp_offset = sel->goff;
-    ra.pair_token = sel->ptok;
-    ra.pair_slot = sel->pslot;
-    select_body<PER>(ra, [&](int t, float (&l)[PER]) {
-#pragma unroll
-      for (int j = 0; j < PER; ++j) {
-        const int e = min(lane + 64 * j, L.E - 1);
-        l[j] = part_sum1(L.r, cr, e >> 4, t, e & 15);
-      }
-    });
-  }
-  __syncthreads();
-  LK_STAMP(20);
-  const int ng = sel->ng;
-  // pair p = t * K + k -> (group, column); pairs with no valid expert stay at -1
-  if (threadIdx.x < B * L.K) sel->pg[threadIdx.x] = -1;
-  __syncthreads();
-  if (threadIdx.x < ng) {
-    const int gg = threadIdx.x, o = sel->goff[gg], cnt = sel->gcnt[gg];
-    for (int j = 0; j < cnt; ++j) {
-      const int p = sel->pslot[o + j];
-      sel->pg[p] = gg;
-      sel->pj[p] = j;
-    }
-  }
-  __syncthreads();
-
-  LK_STAMP(12);
-  // ---- G: expert gate / up projections ----
-  GemvCtx cg = gemv_ctx(L.gu, ng, NB, blk, w, 0);
-  gemv_load(L.gu, sel->gexp, cg, cg.wlo, buf, lane);
-  {
-    XSrc x = {};
-    x.rows = hn2;
-    x.ld = H;
-    x.gcnt = sel->gcnt;
-    x.goff = sel->goff;
-    x.ptok = sel->ptok;
-    gemv_run<XM_GROUP>(L.gu, sel->gexp, cg, buf, x, red, lane, w);
-    gemv_finish(L.gu, cg, red, sel->gcnt, 0, blk, lane, w);
-  }
-  GemvCtx cd = gemv_ctx(L.dn, ng, NB, blk, w, 1);
-  LK_STAMP(13);
-  grid_arrive(L, 5);
-  gemv_load(L.dn, sel->gexp, cd, cd.wlo, buf, lane);
-  grid_wait(L, 5);
-  LK_STAMP(14);
-
-  // ---- D: activations of the block's groups, then the down projections ----
-  {
-    uint16_t* act = reinterpret_cast<uint16_t*>(rb);                 // [kActG][kCols][I]
-    const int I = L.I, FGd = L.dn.NRB * L.dn.KB;
-    const int g0 = cd.hi > cd.lo ? cd.lo / FGd : 0;
-    const int g1 = cd.hi > cd.lo ? min((cd.hi - 1) / FGd, g0 + kActG - 1) : -1;
-    GemmArgs ga;
-    memset(&ga, 0, sizeof(ga));
-    ga.round_qwen = 1;
-    const int per_g = kCols * I / 4;
-    for (int it = threadIdx.x; it < (g1 - g0 + 1) * per_g; it += kThreads) {
-      const int gi = it / per_g, r = it - gi * per_g;
-      const int j = r / (I / 4), i = (r - j * (I / 4)) * 4;
-      const int gg = g0 + gi;
-      if (j >= sel->gcnt[gg]) continue;
-      const int ub = gg * L.gu.NRB + 2 * (i >> 4);
-      const f32x4_t gv = part_sum4(L.gu, cg, ub, j, i & 15);
-      const f32x4_t uv = part_sum4(L.gu, cg, ub + 1, j, i & 15);
-      uint2 o;
-      o.x = pack2bf(swiglu_value(ga, gv[0], uv[0]), swiglu_value(ga, gv[1], uv[1]));
-      o.y = pack2bf(swiglu_value(ga, gv[2], uv[2]), swiglu_value(ga, gv[3], uv[3]));
-      *reinterpret_cast<uint2*>(act + (gi * kCols + j) * I + i) = o;
     }
     __syncthreads();
-    LK_STAMP(21);
-    XSrc x = {};
-    x.rows = act;
-    x.ld = I;
-    x.gcnt = sel->gcnt;
-    x.gbase = g0;
-    gemv_run<XM_ACT>(L.dn, sel->gexp, cd, buf, x, red, lane, w);
-    gemv_finish(L.dn, cd, red, sel->gcnt, 0, blk, lane, w);
+    LK_STAMP(17);
   }
-  LK_STAMP(15);
-  grid_arrive(L, 6);
-  grid_wait(L, 6);
-  LK_STAMP(16);
 
-  // ---- F: block slice of the rows, x = bf16(r + bf16(sum_k w_k y_k)) ----
+  // ---- the block's slice of the final rows ----
   {
-    const int h0 = (int)((long long)H * blk / NB), h1 = (int)((long long)H * (blk + 1) / NB);
-    const int nh = h1 - h0;
-    for (int it = threadIdx.x; it < B * nh; it += kThreads) {
-      const int t = it / nh, h = h0 + (it - t * nh);
-      float yk[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        yk[k] = 0.f;
-        if (k < L.K) {
-          const int p = t * L.K + k;
-          const int gg = max(sel->pg[p], 0);
-          yk[k] = part_sum1(L.dn, cd, gg * L.dn.NRB + (h >> 4), sel->pj[p], h & 15);
-        }
-      }
-      float s = 0.f;
-#pragma unroll
-      for (int k = 0; k < 8; ++k)
-        if (k < L.K && sel->pg[t * L.K + k] >= 0) s += yk[k] * sel->slot_w[t * L.K + k];
-      L.x[(long long)t * H + h] = (uint16_t)f2bf(rbf(bf2f(xs[t * H + h]) + rbf(s)));
-    }
+    const int n8 = B * H / 8;
+    for (int c = (int)((long long)n8 * blk / NB) + threadIdx.x; c < (int)((long long)n8 * (blk + 1) / NB);
+         c += kThreads)
+      *reinterpret_cast<u32x4_t*>(L.x + c * 8) = *reinterpret_cast<const u32x4_t*>(xs + c * 8);
   }
-  LK_STAMP(17);
 }
 
 // ---------------------------------------------------------------------------

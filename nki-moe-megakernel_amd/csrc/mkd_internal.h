@@ -117,12 +117,16 @@ __host__ __device__ inline int lk_fpb(int F, int KB, int NB) {
   return a > b ? a : b;
 }
 constexpr int kLkMaxRowElems = 16384;   // B * H bound (whole rows held per block)
+struct LkLayer {                    // one layer's pointers (device table)
+  const uint16_t *w_qkv, *w_o, *q_norm, *k_norm, *ln_in, *ln_post, *router, *gate_up, *down;
+  uint16_t *k_cache, *v_cache;
+};
 struct LayerArgs {
   int B, H, nq, nkv, gqa, d, E, K, I, S_max, NB;
+  int num_layers;
+  const LkLayer* layers;            // [num_layers] device table
   float eps, inv_h, qk_eps, scale;
-  const uint16_t *ln_in, *ln_post, *q_norm, *k_norm;
-  LkGemv q, o, r, gu, dn;
-  uint16_t *k_cache, *v_cache;
+  LkGemv q, o, r, gu, dn;           // stage shapes and partial buffers (w set per layer)
   long long cache_b_stride, cache_h_stride;
   const int* block_table;
   int tbl_stride, blk_len, num_blocks;
@@ -133,13 +137,11 @@ struct LayerArgs {
   int nch_max;
   uint16_t* attn_out;               // [B, nq * d]
   unsigned* bar;                    // kLkBarWords barrier words
-  int bar_base;                     // barrier index of this launch's first barrier
   int router_mode;                  // MKD_ROUTER_* bits
   int lds_a, lds_b, lds_c, lds_s, lds_total;   // dynamic LDS carve (bytes)
 };
-constexpr int kLkBarriers = 7;      // grid barriers per layer launch
-constexpr int kLkActG = 2;          // expert groups per block in the down stage
-constexpr int kLkSelBytes = 2048;   // LDS of the selection results
+constexpr int kLkBarriers = 7;      // grid barriers per layer
+constexpr int kLkSelBytes = 4096;   // LDS of the selection results and small per-wave scratch
 constexpr int kLkStaticLds = 14336; // static LDS of the kernel (router select body), bound
 hipError_t layer_kernel_launch(const LayerArgs& a, hipStream_t s);
 hipError_t layer_reset_launch(unsigned* bar, hipStream_t s);

@@ -251,6 +251,12 @@ class Qwen3MoeMegakernelModel(nn.Module):
         self.inv_freq = (1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float) / d))).to(device)
         self._build_struct()
         lib = L.load()
+        # device table of the per-layer pointers (persistent decode path)
+        self.layer_table = torch.empty(max(lib.mkd_qwen3_layer_table_bytes(self._model), 8),
+                                       dtype=torch.uint8, device=device)
+        L.check(lib.mkd_qwen3_write_layer_table(self._model, self.layer_table.data_ptr(),
+                                                self.layer_table.numel()), "qwen3_write_layer_table")
+        self._model.layer_table = self.layer_table.data_ptr()
         self.ws = torch.zeros(max(lib.mkd_qwen3_workspace_bytes(self._model, batch), 256),
                               dtype=torch.uint8, device=device)
         self.lm_ws = torch.empty(max(lib.mkd_lm_head_workspace_bytes(batch, cfg.hidden_size, cfg.vocab_size), 256),
