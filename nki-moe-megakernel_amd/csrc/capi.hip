@@ -623,7 +623,7 @@ size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S
 // instead of applying the bf16 / residual epilogue.
 static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos_for_rope,
                           const float* inv_freq, hipStream_t s, float* o_parts = nullptr,
-                          int o_kgrid = 1) {
+                          int o_kgrid = 1, const QkvNormArgs* qn = nullptr) {
   const int qkv_n = (p->nq + 2 * p->nkv) * p->d;
   // 1. optional RMSNorm
   const void* xin = p->X;
@@ -634,10 +634,19 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
                            p->rmsnorm_order, s), "attn rmsnorm");
     xin = w.hnorm;
   }
-  // 2. QKV projection (fp32 out)
-  GemmArgs g = dense_args(p->w_qkv_packed, xin, p->H, qkv_n, p->H, p->B, w.qkv, qkv_n);
-  g.bias = static_cast<const uint16_t*>(p->bias_qkv);
-  {
+  // 2. QKV projection (fp32 out); with qn, the residual update and the norm
+  // are formed inside the projection kernel itself
+  if (qn) {
+    QkvNormArgs q = *qn;
+    q.w = static_cast<const uint16_t*>(p->w_qkv_packed);
+    q.N = qkv_n; q.K = p->H; q.T = p->B;
+    q.y = w.qkv; q.ldy = qkv_n;
+    const int ps = prof_begin(MKD_KCLASS_QKV, s);
+    MKD_TRY(qkv_norm_launch(q, s), "qkv + norm");
+    prof_end(ps, s);
+  } else {
+    GemmArgs g = dense_args(p->w_qkv_packed, xin, p->H, qkv_n, p->H, p->B, w.qkv, qkv_n);
+    g.bias = static_cast<const uint16_t*>(p->bias_qkv);
     const int ps = prof_begin(MKD_KCLASS_QKV, s);
     if (int rc = dense_gemm(g, EPI_F32, false, s)) return rc;
     prof_end(ps, s);
@@ -996,10 +1005,15 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
                     !(wl && m->block_table),
                 MKD_ERR_INVALID, "decode_layers: layer %d window %d / cache rows %d invalid", l, wl, sl);
   }
-  // Layer l's pre-attention norm is produced by the previous layer's MoE
-  // finalize (one fused kernel); layer 0 normalises the input here.
-  MKD_TRY(rmsnorm_launch(x, 0, static_cast<const uint16_t*>(m->ln_in[0]), w.attn.hnorm, nullptr, B,
-                         m->H, m->H, ha, m->eps, pre_order, s), "pre norm");
+  // Small batches (Qwen flow): the MoE finalize and each layer's pre-attention
+  // norm are formed inside that layer's QKV projection kernel.  Otherwise layer
+  // l's pre-attention norm is produced by the previous layer's MoE finalize (one
+  // fused kernel) and layer 0 normalises the input here.
+  const int qkv_n = (m->nq + 2 * m->nkv) * m->d;
+  const bool fuse_qn = !oss && !m->b_qkv && qkv_norm_supported(B, qkv_n, m->H);
+  if (!fuse_qn)
+    MKD_TRY(rmsnorm_launch(x, 0, static_cast<const uint16_t*>(m->ln_in[0]), w.attn.hnorm, nullptr, B,
+                           m->H, m->H, ha, m->eps, pre_order, s), "pre norm");
   const int o_kgrid = 1;   // one block per 16 output rows, up to 16 waves over K
   for (int l = 0; l < m->num_layers; ++l) {
     const int wl = m->window ? m->window[l] : 0;
@@ -1024,7 +1038,18 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     ap.B = B; ap.H = m->H; ap.H_out = m->H; ap.nq = m->nq; ap.nkv = m->nkv; ap.d = m->d;
     ap.S_max = m->layer_s_max ? m->layer_s_max[l] : m->S_max;
     ap.round_qwen = oss ? 0 : 1;
-    if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s, w.oparts, o_kgrid))
+    QkvNormArgs qn = {};
+    if (fuse_qn) {
+      qn.r = l == 0 ? x : w.r;                 // previous layer's post-attention residual
+      qn.ld_r = m->H;
+      qn.dsum = l == 0 ? nullptr : w.moe.ybuf; // its expert outputs (already weighted)
+      qn.dK = m->K; qn.ds_row = (long long)m->K * m->H; qn.ds_k = m->H;
+      qn.gamma = static_cast<const uint16_t*>(m->ln_in[l]);
+      qn.eps = m->eps; qn.inv_h = 1.0f / (float)ha;
+      qn.resid_out = l == 0 ? nullptr : x;
+    }
+    if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s, w.oparts, o_kgrid,
+                                fuse_qn ? &qn : nullptr))
       return rc;
     // router (split-K GEMM) + top-k + expert groups in one select launch: Qwen
     // fp32 input and fused flow; GPT-OSS bf16 input, biased logits, top-k then
@@ -1084,8 +1109,10 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
                           m->expert_format ? m->gate_up_scales[l] : nullptr,
                           m->expert_format ? m->down_scales[l] : nullptr))
       return rc;
-    // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention norm
-    {
+    // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention
+    // norm (with fuse_qn: the next QKV kernel does both; after the last layer the
+    // finalize alone)
+    if (!fuse_qn || l + 1 == m->num_layers) {
       NormArgs na = {};
       na.x = w.r; na.ld_in = m->H;
       na.dsum = w.moe.ybuf; na.dK = m->K; na.ds_row = (long long)m->K * m->H; na.ds_k = m->H;

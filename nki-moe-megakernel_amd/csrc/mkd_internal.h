@@ -146,6 +146,25 @@ constexpr int kLkStaticLds = 14336; // static LDS of the kernel (router select b
 hipError_t layer_kernel_launch(const LayerArgs& a, hipStream_t s);
 hipError_t layer_reset_launch(unsigned* bar, hipStream_t s);
 
+// qkv_norm.hip: QKV projection with the MoE finalize and pre-attention norm folded in
+constexpr int kQkvNormMaxT = 4;
+struct QkvNormArgs {
+  const uint16_t* w;          // packed [N, K] QKV weights
+  int N, K, T;
+  const uint16_t* r;          // [T, ld_r] bf16 residual before the expert sum
+  int ld_r;
+  const float* dsum;          // partial rows added to r (null: x = r)
+  int dK;
+  long long ds_row, ds_k;     // element strides of dsum (token, partial)
+  const uint16_t* gamma;      // [K] pre-attention norm weight
+  float eps, inv_h;
+  uint16_t* resid_out;        // [T, ld_r] x, the new residual stream (or null)
+  float* y;                   // [T, ldy] fp32 projections
+  int ldy;
+};
+bool qkv_norm_supported(int T, int N, int K);
+hipError_t qkv_norm_launch(const QkvNormArgs& a, hipStream_t s);
+
 // norm.hip
 struct NormArgs {
   const void* x;              // [rows, ld_in] bf16 or fp32

@@ -150,32 +150,58 @@ __global__ void __launch_bounds__(64) router_norm_gemm_kernel(RouterFusedArgs a,
   const bool live = tcol < T;
   constexpr int MAXF = 8;                // fragments per slice (router_fused_supported)
 
-  // ---- loads, all independent: weight fragments, the lane's operand values,
-  // gamma, and a 1/64 share of every row for the sum of squares ----
-  u32x4_t wf[MAXF];
-  const uint16_t* wrow = a.w + ((long long)rb * KB + kb0) * 512 + lane * 8;
+  // ---- loads, all independent: a 1/64 share of every row for the sum of
+  // squares and the lane's operand values and gamma first, the weight
+  // fragments last -- a wave's loads complete in issue order, so the norm runs
+  // while the weights are in flight.  Addresses are clamped in range so every
+  // load is unconditional; the values are masked where they are used. ----
+  constexpr int MAXC = 4;                // row shares preloaded per token (H <= 2048)
+  u32x4_t sx[kFusedMaxT][MAXC];
+  f32x4_t sp[kFusedMaxT][MAXC], sq[kFusedMaxT][MAXC];
 #pragma unroll
-  for (int u = 0; u < MAXF; ++u)
-    if (u < nf) wf[u] = ld16(wrow + u * 512);
+  for (int t = 0; t < kFusedMaxT; ++t)
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      const long long row = (long long)min(t, T - 1) * H;
+      const int cc = min(lane * 8 + c * 512, H - 8);
+      sx[t][c] = ld16(a.x + row + cc);
+      sp[t][c] = *reinterpret_cast<const f32x4_t*>(a.o + row + cc);
+      sq[t][c] = *reinterpret_cast<const f32x4_t*>(a.o + row + cc + 4);
+    }
   u32x4_t xb[MAXF], gb[MAXF];
   f32x4_t o0[MAXF], o1[MAXF];
   const int tr = live ? tcol : 0;
 #pragma unroll
-  for (int u = 0; u < MAXF; ++u)
-    if (u < nf) {
-      const int k = (kb0 + u) * 32 + koff;
-      xb[u] = ld16(a.x + (long long)tr * H + k);
-      gb[u] = ld16(a.gamma + k);
-      o0[u] = *reinterpret_cast<const f32x4_t*>(a.o + (long long)tr * H + k);
-      o1[u] = *reinterpret_cast<const f32x4_t*>(a.o + (long long)tr * H + k + 4);
-    }
+  for (int u = 0; u < MAXF; ++u) {
+    const int k = (kb0 + min(u, nf - 1)) * 32 + koff;
+    xb[u] = ld16(a.x + (long long)tr * H + k);
+    gb[u] = ld16(a.gamma + k);
+    o0[u] = *reinterpret_cast<const f32x4_t*>(a.o + (long long)tr * H + k);
+    o1[u] = *reinterpret_cast<const f32x4_t*>(a.o + (long long)tr * H + k + 4);
+  }
+  u32x4_t wf[MAXF];
+  const uint16_t* wrow = a.w + ((long long)rb * KB + kb0) * 512 + lane * 8;
+#pragma unroll
+  for (int u = 0; u < MAXF; ++u) wf[u] = ld16(wrow + min(u, nf - 1) * 512);
   // sum of squares of r over the whole row, lane share: H / 64 elements
   float ss[kFusedMaxT];
 #pragma unroll
   for (int t = 0; t < kFusedMaxT; ++t) {
     ss[t] = 0.f;
     if (t >= T) continue;
-    for (int c = lane * 8; c < H; c += 512) {
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+      if (lane * 8 + c * 512 >= H) continue;
+      const float ov[8] = {sp[t][c][0], sp[t][c][1], sp[t][c][2], sp[t][c][3],
+                           sq[t][c][0], sq[t][c][1], sq[t][c][2], sq[t][c][3]};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float xv_j = (j & 1) ? bf_hi(sx[t][c][j >> 1]) : bf_lo(sx[t][c][j >> 1]);
+        const float r = rbf(xv_j + rbf(ov[j]));
+        ss[t] += r * r;
+      }
+    }
+    for (int c = lane * 8 + MAXC * 512; c < H; c += 512) {   // rows longer than MAXC shares
       const u32x4_t xv = ld16(a.x + (long long)t * H + c);
       const f32x4_t p = *reinterpret_cast<const f32x4_t*>(a.o + (long long)t * H + c);
       const f32x4_t q = *reinterpret_cast<const f32x4_t*>(a.o + (long long)t * H + c + 4);
@@ -200,7 +226,7 @@ __global__ void __launch_bounds__(64) router_norm_gemm_kernel(RouterFusedArgs a,
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int u = 0; u < MAXF; ++u) {
-    if (u >= nf) break;
+    if (u < nf) {
     const int k = (kb0 + u) * 32 + koff;
     const float ov[8] = {o0[u][0], o0[u][1], o0[u][2], o0[u][3], o1[u][0], o1[u][1], o1[u][2], o1[u][3]};
     float r[8], y[8];
@@ -232,6 +258,7 @@ __global__ void __launch_bounds__(64) router_norm_gemm_kernel(RouterFusedArgs a,
     }
     acc = mfma16x16x32(wf[u], hi, acc);
     if (a.x_f32) acc = mfma16x16x32(wf[u], lo, acc);
+    }
   }
   // D lane l: experts rb*16 + 4*(l/16) + i, token l%16 -> part[kblk][t][e]
   if (live) {
