@@ -247,13 +247,20 @@ __global__ void copy_slot_weights(const float* src, int n, float* dst) {
   if (p < n) dst[p] = src[p];
 }
 
+// Per-wave K slice of the frag gate/up GEMM (two row blocks per wave).
+int gate_up_kw(int H, int I, int gmax) { return choose_kw(H, 256, (long long)(I / 16) * gmax); }
+
 // The expert FFN on an already-routed batch: routing tables -> gate/up -> down -> finalize.
+// With `sel` (a few tokens, bf16 frag experts) the routing is formed inside the
+// gate/up launch from the router's partial logits instead.
 int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, const int* idx,
              const float* slot_w, const uint16_t* gu_bias, const uint16_t* dn_bias,
              const uint16_t* resid, uint16_t* out, float* out_f32, int T, int H, int E, int I,
              int K, int act, float alpha, float ghi, float glo, float uhi, float ulo, int round_qwen,
              MoeWs& w, hipStream_t s, bool do_finalize = true, int wfmt = 0,
-             const void* gu_scales = nullptr, const void* dn_scales = nullptr, bool tiled = false) {
+             const void* gu_scales = nullptr, const void* dn_scales = nullptr, bool tiled = false,
+             const RouterArgs* sel = nullptr) {
+  if (sel && (idx || wfmt || tiled)) return MKD_ERR_INVALID;
   if (idx)  // otherwise the router stage already built the expert groups
     MKD_TRY(moe_route_launch(idx, T, K, E, w.n_groups, w.grp_expert, w.grp_count, w.grp_offset,
                              w.pair_token, w.pair_slot, s), "moe_route");
@@ -335,7 +342,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
   const int tn = 1;
   {  // gate/up + activation
     GemmArgs a = dense_args(gate_up, hidden, H, 2 * I, H, T, w.hbuf, I);
-    a.KW = choose_kw(H, 256, (long long)(I / 16) * gmax);   // two row blocks per wave
+    a.KW = gate_up_kw(H, I, gmax);
     a.w_group_stride = (long long)2 * I * H;
     a.grp_expert = w.grp_expert; a.grp_count = w.grp_count; a.grp_offset = w.grp_offset;
     a.n_groups = w.n_groups; a.pair_row = w.pair_token; a.pair_out_row = w.pair_slot;
@@ -343,7 +350,10 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
     a.act = act; a.alpha = alpha; a.gate_hi = ghi; a.gate_lo = glo; a.up_hi = uhi; a.up_lo = ulo;
     a.round_qwen = round_qwen;
     const int ps = prof_begin(MKD_KCLASS_MOE_GATE_UP, s);
-    MKD_TRY(gemm_launch(a, EPI_SWIGLU_BF16, false, tn, gmax, T, s), "moe gate_up");
+    if (sel)   // the router top-k and the expert groups are formed in the gate/up blocks
+      MKD_TRY(gemm_sel_launch(a, *sel, gmax, s), "moe router select + gate_up");
+    else
+      MKD_TRY(gemm_launch(a, EPI_SWIGLU_BF16, false, tn, gmax, T, s), "moe gate_up");
     prof_end(ps, s);
   }
   {  // down, scaled by the slot affinity
@@ -1062,7 +1072,18 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     ra.n_groups = w.moe.n_groups; ra.grp_expert = w.moe.grp_expert;
     ra.grp_count = w.moe.grp_count; ra.grp_offset = w.moe.grp_offset;
     ra.pair_token = w.moe.pair_token; ra.pair_slot = w.moe.pair_slot;
+    const int gmax_l = m->E < B * m->K ? m->E : B * m->K;
+    const int gu_kw = gate_up_kw(m->H, m->I, gmax_l);
+    RouterArgs sel;
+    bool defer_sel = false;
     if (router_fused_supported(B, m->E, m->H)) {
+      // the router top-k inside the gate/up blocks: each block pays the selection
+      // before its weight loads, so only when the whole grid is resident at once
+      // (two blocks per CU); measured at 4 tokens (1536 blocks) the select launch
+      // is cheaper than three rounds of in-block selection
+      const long long gu_blocks = (long long)((2 * m->I + 31) / 32) * gmax_l;
+      defer_sel = !m->expert_format && gu_kw > 0 && gemm_sel_supported(B, m->K, m->E, m->H / gu_kw) &&
+                  gu_blocks <= 2LL * lk_device_cus();
       // a few tokens: the residual add and post norm are folded into the router
       // GEMM (each block forms the row norms itself), then the select launch
       RouterFusedArgs fa = {};
@@ -1075,7 +1096,7 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
       fa.w = static_cast<const uint16_t*>(m->router[l]);
       fa.x_f32 = oss ? 0 : 1;
       const int ps = prof_begin(MKD_KCLASS_ROUTER, s);
-      MKD_TRY(router_fused_launch(fa, s), "residual + post norm + router");
+      MKD_TRY(router_fused_launch(fa, s, defer_sel ? &sel : nullptr), "residual + post norm + router");
       prof_end(ps, s);
     } else {
       // r = bf16(x + bf16(o_proj)) from the split-K partials, then the post-attention
@@ -1107,7 +1128,8 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
                           oss ? m->up_lo : -INFINITY, (oss || m->expert_format) ? 0 : 1,
                           w.moe, s, false, m->expert_format,
                           m->expert_format ? m->gate_up_scales[l] : nullptr,
-                          m->expert_format ? m->down_scales[l] : nullptr))
+                          m->expert_format ? m->down_scales[l] : nullptr, false,
+                          defer_sel ? &sel : nullptr))
       return rc;
     // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention
     // norm (with fuse_qn: the next QKV kernel does both; after the last layer the

@@ -23,6 +23,7 @@
 #include "common.h"
 #include "gemm_epi.h"
 #include "mkd_internal.h"
+#include "router_select.h"
 
 namespace mkd {
 
@@ -146,8 +147,7 @@ MKD_DEV void stream_batch(const uint16_t* const (&wrow)[RB], int f, int kb0, int
 // The GEMM.
 // ---------------------------------------------------------------------------
 template <int RB, int TN, bool XF32, int EPI>
-__global__ void __launch_bounds__(1024)
-gemm_frag_kernel(GemmArgs a) {
+MKD_DEV void frag_body(const GemmArgs& a) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int rbase = blockIdx.x;          // index of the RB-row-block tile
@@ -225,6 +225,55 @@ gemm_frag_kernel(GemmArgs a) {
   gemm_finish<RB, TN, EPI>(a, acc, lane, wave, rbase, group, t0, base, xrow, kblk);
 }
 
+template <int RB, int TN, bool XF32, int EPI>
+__global__ void __launch_bounds__(1024) gemm_frag_kernel(GemmArgs a) {
+  frag_body<RB, TN, XF32, EPI>(a);
+}
+
+// Grouped gate/up + SwiGLU with the router top-k folded in, for a few tokens
+// (router_topk.py:868-887 selection, moe_tkg gate/up): every block forms the
+// top-k, the routing weights and the expert groups of all T tokens from the
+// router's split-K partial logits itself (select_small: the values of
+// router_select_kernel), keeps the tables in LDS for its own columns, and block
+// (0,0,0) also writes them out for the down projection.  The partials are
+// T * E * nparts floats read from L2 by every block; the select launch and its
+// dependent round trip leave the decode step.
+template <int PER>
+__global__ void __launch_bounds__(1024) gemm_frag_sel_kernel(GemmArgs a, RouterArgs r) {
+  __shared__ int s_ng;
+  __shared__ int s_gexp[kSelMaxPairs], s_gcnt[kSelMaxPairs], s_goff[kSelMaxPairs];
+  __shared__ int s_ptok[kSelMaxPairs], s_pslot[kSelMaxPairs];
+  __shared__ float s_w[kSelMaxPairs];
+  const bool lead = (blockIdx.x | blockIdx.y | blockIdx.z) == 0;
+  const int lane = threadIdx.x & 63;
+  RouterArgs q = r;
+  q.n_groups = &s_ng;
+  q.grp_expert = s_gexp; q.grp_count = s_gcnt; q.grp_offset = s_goff;
+  q.pair_token = s_ptok; q.pair_slot = s_pslot; q.slot_w = s_w;
+  if (!lead) q.logits_out = nullptr, q.aff_full = nullptr, q.idx_out = nullptr, q.topk_out = nullptr;
+  select_small<PER>(q, [&](int t, float (&l)[PER]) { load_logits<PER>(q, t, lane, l); });
+  __syncthreads();
+  if (lead) {
+    const int ng = s_ng, np = r.T * r.K;
+    if (threadIdx.x == 0) *r.n_groups = ng;
+    for (int i = threadIdx.x; i < ng; i += blockDim.x) {
+      r.grp_expert[i] = s_gexp[i];
+      r.grp_count[i] = s_gcnt[i];
+      r.grp_offset[i] = s_goff[i];
+    }
+    for (int i = threadIdx.x; i < np; i += blockDim.x) {
+      r.pair_token[i] = s_ptok[i];
+      r.pair_slot[i] = s_pslot[i];
+      if (r.slot_w) r.slot_w[i] = s_w[i];
+    }
+  }
+  GemmArgs b = a;
+  b.n_groups = &s_ng;
+  b.grp_expert = s_gexp; b.grp_count = s_gcnt; b.grp_offset = s_goff;
+  b.pair_row = s_ptok; b.pair_out_row = s_pslot;
+  frag_body<2, 1, false, EPI_SWIGLU_BF16>(b);
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -238,6 +287,25 @@ static hipError_t launch_t(const GemmArgs& a, int n_tiles, int groups, int ttile
   dim3 block(64 * nsplit);
   const size_t lds = nsplit > 1 ? (size_t)nsplit * RB * TN * 4 * 64 * sizeof(float) : 0;
   return timed_launch(gemm_frag_kernel<RB, TN, XF32, EPI>, grid, block, lds, s, a);
+}
+
+bool gemm_sel_supported(int T, int K, int E, int nsplit) {
+  return T >= 1 && T <= nsplit && T * K <= kSelMaxPairs && K >= 1 && K <= 8 && K <= E && E <= 256;
+}
+
+hipError_t gemm_sel_launch(const GemmArgs& a, const RouterArgs& r, int groups_max, hipStream_t s) {
+  const int nsplit = a.KW > 0 ? a.K / a.KW : 0;
+  if (nsplit < 1 || nsplit > 16 || nsplit * a.KW != a.K || (a.kgrid > 1) ||
+      !gemm_sel_supported(r.T, r.K, r.E, nsplit) || a.T != r.T || !r.parts || r.nparts < 1 ||
+      r.nparts > 16 || !r.n_groups || !r.grp_expert || !r.grp_count || !r.grp_offset ||
+      !r.pair_token || !r.pair_slot || !a.grp_expert || groups_max < 1 || groups_max > kSelMaxPairs)
+    return hipErrorInvalidValue;
+  const dim3 grid((a.N + 31) / 32, groups_max, (a.T + 15) / 16), block(64 * nsplit);
+  const size_t lds = nsplit > 1 ? (size_t)nsplit * 2 * 4 * 64 * sizeof(float) : 0;
+  const int per = (r.E + 63) / 64;
+  if (per <= 1) return timed_launch(gemm_frag_sel_kernel<1>, grid, block, lds, s, a, r);
+  if (per <= 2) return timed_launch(gemm_frag_sel_kernel<2>, grid, block, lds, s, a, r);
+  return timed_launch(gemm_frag_sel_kernel<4>, grid, block, lds, s, a, r);
 }
 
 int choose_kw(int K, int max_kw, long long blocks) {

@@ -1118,7 +1118,7 @@ __global__ void __launch_bounds__(kThreads) layer_kernel(LayerArgs L) {
       ra.grp_offset = sel->goff;
       ra.pair_token = sel->ptok;
       ra.pair_slot = sel->pslot;
-      select_body<PER>(ra, [&](int t, float (&lg)[PER]) {
+      select_small<PER>(ra, [&](int t, float (&lg)[PER]) {
 #pragma unroll
         for (int j = 0; j < PER; ++j) {
           const int e = min(ln + 64 * j, L.E - 1);

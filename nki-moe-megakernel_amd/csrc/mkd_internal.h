@@ -142,7 +142,7 @@ struct LayerArgs {
 };
 constexpr int kLkBarriers = 7;      // grid barriers per layer
 constexpr int kLkSelBytes = 4096;   // LDS of the selection results and small per-wave scratch
-constexpr int kLkStaticLds = 14336; // static LDS of the kernel (router select body), bound
+constexpr int kLkStaticLds = 1024;  // static LDS of the kernel (router select_small), bound
 hipError_t layer_kernel_launch(const LayerArgs& a, hipStream_t s);
 hipError_t layer_reset_launch(unsigned* bar, hipStream_t s);
 
@@ -266,7 +266,15 @@ struct RouterFusedArgs {
   int x_f32;                  // router input: 1 fp32 normalised rows (bf16 hi + lo), 0 bf16
 };
 bool router_fused_supported(int T, int E, int H);
-hipError_t router_fused_launch(RouterFusedArgs a, hipStream_t s);
+// With `deferred` set the select launch is left out and the completed
+// RouterArgs (partials, count, stride) are returned there for gemm_sel_launch.
+hipError_t router_fused_launch(RouterFusedArgs a, hipStream_t s, RouterArgs* deferred = nullptr);
+// Grouped gate/up + SwiGLU (frag GEMM, one token tile) whose blocks form the
+// router top-k and expert groups themselves from r's partial logits; r's group
+// tables and slot weights are written for the down projection.
+constexpr int kSelMaxPairs = 64;
+bool gemm_sel_supported(int T, int K, int E, int nsplit);
+hipError_t gemm_sel_launch(const GemmArgs& a, const RouterArgs& r, int groups_max, hipStream_t s);
 hipError_t moe_route_launch(const int* idx, int T, int K, int E, int* n_groups, int* grp_expert,
                             int* grp_count, int* grp_offset, int* pair_token, int* pair_slot,
                             hipStream_t s);

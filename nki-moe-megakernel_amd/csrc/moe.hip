@@ -268,13 +268,17 @@ __global__ void __launch_bounds__(64) router_norm_gemm_kernel(RouterFusedArgs a,
   }
 }
 
-hipError_t router_fused_launch(RouterFusedArgs a, hipStream_t s) {
+hipError_t router_fused_launch(RouterFusedArgs a, hipStream_t s, RouterArgs* deferred) {
   if (!router_fused_supported(a.r.T, a.r.E, a.H) || !a.r.parts) return hipErrorInvalidValue;
   const int kg = fused_kg(a.r.E, a.H);
   a.r.nparts = kg;
   a.r.part_stride = (long long)a.r.T * a.r.E;
   if (hipError_t e = timed_launch(router_norm_gemm_kernel, dim3(a.r.E / 16, kg), dim3(64), 0, s, a, kg))
     return e;
+  if (deferred) {
+    *deferred = a.r;
+    return hipSuccess;
+  }
   return router_select_launch(a.r, s);
 }
 

@@ -275,4 +275,148 @@ MKD_DEV void select_body(const RouterArgs& a, Load&& load) {
   }
 }
 
+// Unsigned wave max (every lane gets the result); the wave must be fully active.
+template <int CTRL>
+MKD_DEV uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xF, 0xF, false);
+}
+MKD_DEV uint32_t wave_max_u(uint32_t v) {
+  v = max(v, dpp_u<0xB1>(v));
+  v = max(v, dpp_u<0x4E>(v));
+  v = max(v, dpp_u<0x141>(v));
+  v = max(v, dpp_u<0x140>(v));
+  const uint32_t a = (uint32_t)__builtin_amdgcn_readlane((int)v, 0), b = (uint32_t)__builtin_amdgcn_readlane((int)v, 16);
+  const uint32_t c = (uint32_t)__builtin_amdgcn_readlane((int)v, 32), d = (uint32_t)__builtin_amdgcn_readlane((int)v, 48);
+  return max(max(a, b), max(c, d));
+}
+
+// Top-k, weights and expert groups for a few tokens: T <= the block's waves and
+// T * K <= 64 (the decode step at small batch), with the values of select_body
+// in every mode (aff_full is not produced).  Wave t takes token t; the K chosen
+// come out already in rank order from K rounds of a wave-wide max over the
+// order codes (largest code, lowest index among equal codes: select_body's
+// order), lane r holding rank r.  After one block barrier wave 0 forms the
+// groups from the T * K pairs directly (experts ascending, pairs of an expert in
+// token order): pair p's position is #{valid q : e_q < e_p} + #{q < p : e_q ==
+// e_p}.  The caller synchronises the block before reading the group tables.
+template <int PER, class Load>
+MKD_DEV void select_small(const RouterArgs& a, Load&& load) {
+  __shared__ int pe_s[64];                 // expert of pair t * K + rank
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int E = a.E, K = a.K, T = a.T;
+  const bool sigm = a.mode & 1, pre = a.mode & 2, norm = a.mode & 4, qwen = a.mode & 8;
+  if (wv < T) {
+    const int t = wv;
+    float l[PER];
+    load(t, l);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E) {
+        if (a.logits_out) a.logits_out[(long long)t * E + e] = l[j];
+      } else {
+        l[j] = -INFINITY;
+      }
+      mx = fmaxf(mx, l[j]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.f, ex[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      ex[j] = (lane + 64 * j < E) ? expf(l[j] - mx) : 0.f;
+      sum += ex[j];
+    }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sum;
+    float key[PER];
+    uint32_t u[PER];
+    bool av[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      key[j] = (qwen || !pre) ? l[j] : (sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv);
+      u[j] = order_code(key[j]);
+      av[j] = lane + 64 * j < E;
+    }
+    int my_e = -1;
+    float my_key = 0.f;
+    for (int r = 0; r < K; ++r) {
+      uint32_t m = 0;
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (av[j]) m = max(m, u[j]);
+      m = wave_max_u(m);
+      int pick = -1;
+#pragma unroll
+      for (int j = 0; j < PER; ++j) {
+        const unsigned long long hit = __ballot(av[j] && u[j] == m);
+        if (pick < 0 && hit) pick = 64 * j + (int)__builtin_ctzll(hit);
+      }
+      const int pl = pick & 63, pj = pick >> 6;
+      float kv = key[0];
+#pragma unroll
+      for (int j = 1; j < PER; ++j)
+        if (j == pj) kv = key[j];
+      kv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, kv), pl));
+#pragma unroll
+      for (int j = 0; j < PER; ++j)
+        if (j == pj && lane == pl) av[j] = false;
+      if (lane == r) {
+        my_e = pick;
+        my_key = kv;
+      }
+    }
+    // weights: lane r < K holds rank r
+    const float k0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_key), 0));
+    float pv;
+    if (qwen) pv = rbf(expf(my_key - mx) * inv);   // softmax value at the logit, bf16
+    else if (pre) pv = my_key;
+    else if (sigm) pv = 1.0f / (1.0f + expf(-my_key));
+    else pv = expf(my_key - k0);                    // softmax over the top-k (rank 0 = max)
+    float w = pv;
+    if (qwen || (pre && norm) || (!pre && !sigm)) {
+      float s = 0.f;                                 // k order
+      for (int k = 0; k < K; ++k)
+        s += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), k));
+      w = qwen ? rbf(pv * (1.0f / s)) : pv * (1.0f / s);
+    }
+    if (lane < K) {
+      pe_s[t * K + lane] = my_e;
+      if (a.idx_out) a.idx_out[t * K + lane] = my_e;
+      if (a.topk_out) a.topk_out[t * K + lane] = w;
+      if (a.slot_w) a.slot_w[t * K + lane] = w;
+    }
+  }
+  if (!a.n_groups) return;
+  __syncthreads();
+  if (wv == 0) {
+    const int P = T * K;
+    const int e = lane < P ? pe_s[lane] : -1;
+    const bool valid = e >= 0 && e < E;
+    int less = 0, before = 0, cnt = 0;
+    for (int q = 0; q < P; ++q) {
+      const int eq = __builtin_amdgcn_readlane(e, q);
+      const bool vq = eq >= 0 && eq < E;
+      less += vq && eq < e;
+      before += q < lane && eq == e;
+      cnt += eq == e;
+    }
+    const bool first = valid && before == 0;
+    const unsigned long long fm = __ballot(first);
+    int g = 0;
+    for (int q = 0; q < P; ++q)
+      if ((fm >> q) & 1) g += __builtin_amdgcn_readlane(e, q) < e;
+    if (valid) {
+      a.pair_token[less + before] = lane / K;
+      a.pair_slot[less + before] = lane;
+    }
+    if (first) {
+      a.grp_expert[g] = e;
+      a.grp_count[g] = cnt;
+      a.grp_offset[g] = less;
+    }
+    if (lane == 0) *a.n_groups = __popcll(fm);
+  }
+}
+
 }  // namespace mkd
