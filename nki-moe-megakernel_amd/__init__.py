@@ -10,6 +10,9 @@ Operator surface (same names, argument order and defaults as the reference):
 Model surface:
   qwen_with_megakernel  megakernels/qwen3_moe/qwen_with_megakernel.py
   gpt_oss_with_megakernel  megakernels/gpt_oss/gpt_oss_with_megakernel.py
+  checkpoint            HF safetensors directories -> packed decode models
+                        (the converters at qwen_with_megakernel.py:171-271,
+                        gpt_oss_with_megakernel.py:290-327)
 
 All compute runs in libmkd.so (hand-written HIP for gfx950, C ABI in
 include/mkd.h).  The package directory name contains dashes, so it is
