@@ -317,6 +317,20 @@ size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B);
 int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
                             const int* position_ids, const float* cos, const float* sin,
                             void* workspace, size_t workspace_bytes, void* stream);
+/* Context encoding (prefill) of one sequence through all layers:
+ * hidden [T, H] bf16 in/out holds T consecutive tokens of sequence `seq` at
+ * position_ids [T] (int32, device; normally p0 .. p0 + T - 1), 1 <= T <= 128.
+ * Every token's k / v rows are written to sequence seq's cache (flat: batch
+ * index seq; paged: block_table row seq) before the attention reads it, so
+ * token t attends the cache rows below its position, including those of the
+ * earlier tokens of the same call.  The reference's counterpart is the CTE
+ * (context-encoding) layer path, qwen_with_megakernel.py:496-526.  The caller
+ * keeps seq within the caches; workspace from mkd_qwen3_workspace_bytes(m, T).
+ * Models with sliding-window layers take T = 1 (MKD_ERR_UNSUPPORTED otherwise).
+ * Always the multi-kernel layers (the decode-path setting is ignored). */
+int mkd_qwen3_prefill_layers(const mkd_qwen3_model* m, int seq, int T, void* hidden,
+                             const int* position_ids, const float* cos, const float* sin,
+                             void* workspace, size_t workspace_bytes, void* stream);
 
 /* ---------------------------------------------------------------------------
  * Decode-step epilogue (the NxDI side of the reference step:

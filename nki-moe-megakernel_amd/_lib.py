@@ -111,6 +111,7 @@ _SIGS = {
     "mkd_attention_block_tkg": (i32, [C.POINTER(AttentionArgs), vp, sz, vp]),
     "mkd_qwen3_workspace_bytes": (sz, [C.POINTER(Qwen3Model), i32]),
     "mkd_qwen3_decode_layers": (i32, [C.POINTER(Qwen3Model), i32, vp, vp, vp, vp, vp, sz, vp]),
+    "mkd_qwen3_prefill_layers": (i32, [C.POINTER(Qwen3Model), i32, i32, vp, vp, vp, vp, vp, sz, vp]),
     "mkd_embed": (i32, [vp, vp, vp, i32, i32, i32, vp]),
     "mkd_lm_head_workspace_bytes": (sz, [i32, i32, i32]),
     "mkd_lm_head_greedy": (i32, [vp, vp, f32, vp, i32, i32, i32, i32, i32, vp, vp, vp, sz, vp]),

@@ -94,6 +94,21 @@ __global__ void __launch_bounds__(256) attn_prep_kernel(AttnArgs a, int rope_mod
                      dst + GQA * D, dst + (GQA + 1) * D);
 }
 
+// Prefill (tokens of one sequence in one step): block (g, b) writes token b's
+// prepared k / v rows of kv head g to the cache before any attention block
+// reads it; the combine kernel later stores the same values again.
+template <int D, int GQA>
+__global__ void __launch_bounds__(D) attn_kv_write_kernel(AttnArgs a) {
+  const int g = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const long long row = kv_write_row(a, b);
+  if (row < 0) return;
+  const uint16_t* src = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
+  const long long off = a.block_table ? (row * a.nkv + g) * D + d
+                                      : b * a.cache_b_stride + g * a.cache_h_stride + row * D + d;
+  a.k_cache[off] = src[GQA * D + d];
+  a.v_cache[off] = src[(GQA + 1) * D + d];
+}
+
 template <int D, int GQA, int TPW>
 __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mode) {
   constexpr int NK = D / 32;                  // QK MFMAs per tile (k = 32)
@@ -438,8 +453,13 @@ static hipError_t launch_attn(const AttnArgs& a, int rope_mode, hipStream_t s) {
 
 template <int D, int GQA>
 static hipError_t launch_tpw(const AttnArgs& a, int rope_mode, hipStream_t s) {
+  if (a.prefill && (!a.prep || !a.update_cache)) return hipErrorInvalidValue;
   if (a.prep) {
     hipLaunchKernelGGL((attn_prep_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode);
+    if (hipError_t e = hipGetLastError()) return e;
+  }
+  if (a.prefill) {
+    hipLaunchKernelGGL((attn_kv_write_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(D), 0, s, a);
     if (hipError_t e = hipGetLastError()) return e;
   }
   const int chunk = a.chunk;

@@ -633,7 +633,7 @@ size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S
 // instead of applying the bf16 / residual epilogue.
 static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos_for_rope,
                           const float* inv_freq, hipStream_t s, float* o_parts = nullptr,
-                          int o_kgrid = 1, const QkvNormArgs* qn = nullptr) {
+                          int o_kgrid = 1, const QkvNormArgs* qn = nullptr, bool prefill = false) {
   const int qkv_n = (p->nq + 2 * p->nkv) * p->d;
   // 1. optional RMSNorm
   const void* xin = p->X;
@@ -691,6 +691,14 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   a.window = p->window;
   a.block_table = p->active_blocks_table;
   a.tbl_stride = p->blocks_per_seq; a.blk_len = p->block_len; a.num_blocks = p->num_blocks;
+  if (prefill) {
+    // the B tokens belong to one sequence whose cache (or block-table row) the
+    // caller's pointers already select
+    a.cache_b_stride = 0;
+    a.tbl_stride = 0;
+    a.prep = w.prep;
+    a.prefill = 1;
+  }
   const int rope_mode = p->cos ? 1 : (inv_freq ? 2 : 0);
   {  // q/k norm + RoPE and split-K attention in one launch
     const int ps = prof_begin(MKD_KCLASS_ATTN, s);
@@ -958,10 +966,12 @@ size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B) {
   return most;
 }
 
-int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
-                            const int* position_ids, const float* cos, const float* sin,
-                            void* workspace, size_t workspace_bytes, void* stream) {
-  if (int rc = stale_check("mkd_qwen3_decode_layers")) return rc;
+// prefill_seq >= 0: the B tokens are consecutive tokens of sequence prefill_seq
+// (context encoding); < 0: one token of each of B sequences (decode).
+static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const int* position_ids,
+                         const float* cos, const float* sin, void* workspace,
+                         size_t workspace_bytes, void* stream, int prefill_seq) {
+  const bool prefill = prefill_seq >= 0;
   MKD_REQUIRE(m && hidden && position_ids && workspace, MKD_ERR_NULL, "decode_layers: null pointer");
   MKD_REQUIRE(m->num_layers > 0, MKD_ERR_INVALID, "decode_layers: num_layers must be > 0");
   MKD_REQUIRE(B > 0 && B <= 128, MKD_ERR_INVALID, "decode_layers: B %d must be in [1, 128]", B);
@@ -1000,7 +1010,8 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
                 m->k_cache[l] && m->v_cache[l] && m->ln_in[l] && m->ln_post[l] &&
                 (!m->expert_format || (m->gate_up_scales[l] && m->down_scales[l])),
                 MKD_ERR_NULL, "decode_layers: null weight in layer %d", l);
-  if (w.lk.plan.on && g_decode_path == 1) return decode_layers_lk(m, B, x, position_ids, cos, sin, w, s);
+  if (w.lk.plan.on && g_decode_path == 1 && !prefill)
+    return decode_layers_lk(m, B, x, position_ids, cos, sin, w, s);
   // Qwen3 flow: pre-attention norm (x*rinv)*g, Qwen rounding points, fp32 router
   // input.  GPT-OSS flow: rmsnorm_tkg's (x*g)*rinv with H_actual everywhere,
   // biases, sinks, sliding windows, bf16 router input with logit top-k.
@@ -1014,6 +1025,10 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     MKD_REQUIRE(sl > 0 && sl <= m->S_max && wl >= 0 && wl <= sl && (wl == 0 || wl >= 2) &&
                     !(wl && m->block_table),
                 MKD_ERR_INVALID, "decode_layers: layer %d window %d / cache rows %d invalid", l, wl, sl);
+    // a ring cache of W - 1 prior rows cannot take several tokens' rows before
+    // their attention: the later tokens would overwrite rows the earlier ones read
+    MKD_REQUIRE(!(prefill && wl && B > 1), MKD_ERR_UNSUPPORTED,
+                "prefill_layers: layer %d has a sliding window; prefill it one token per call", l);
   }
   // Small batches (Qwen flow): the MoE finalize and each layer's pre-attention
   // norm are formed inside that layer's QKV projection kernel.  Otherwise layer
@@ -1035,12 +1050,22 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     ap.q_norm = at(m->q_norm, l); ap.k_norm = at(m->k_norm, l); ap.qk_eps = m->eps;
     ap.cos = cos; ap.sin = sin;
     ap.k_cache = m->k_cache[l]; ap.v_cache = m->v_cache[l];
+    // prefill: the caches (or block-table row) of sequence prefill_seq; a windowed
+    // layer (one token per call) keeps the decode order -- its ring row still
+    // holds the oldest attended position until the attention has read it
+    if (prefill && !m->block_table) {
+      const size_t seq_off = (size_t)prefill_seq * m->nkv *
+                             (size_t)(m->layer_s_max ? m->layer_s_max[l] : m->S_max) * m->d;
+      ap.k_cache = static_cast<uint16_t*>(m->k_cache[l]) + seq_off;
+      ap.v_cache = static_cast<uint16_t*>(m->v_cache[l]) + seq_off;
+    }
     ap.n_prior = position_ids;
     ap.sink = static_cast<const float*>(at(m->sinks, l));
     ap.window = wl;
     ap.update_cache = 1;
     ap.kv_cache_update_idx = (m->block_table || wl) ? nullptr : position_ids;
     ap.active_blocks_table = wl ? nullptr : m->block_table;
+    if (prefill && ap.active_blocks_table) ap.active_blocks_table += (size_t)prefill_seq * m->blocks_per_seq;
     ap.blocks_per_seq = m->blocks_per_seq; ap.block_len = m->block_len; ap.num_blocks = m->num_blocks;
     ap.w_out_packed = m->w_o[l];
     ap.bias_out = at(m->b_o, l);
@@ -1059,7 +1084,7 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
       qn.resid_out = l == 0 ? nullptr : x;
     }
     if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s, w.oparts, o_kgrid,
-                                fuse_qn ? &qn : nullptr))
+                                fuse_qn ? &qn : nullptr, prefill && !wl))
       return rc;
     // router (split-K GEMM) + top-k + expert groups in one select launch: Qwen
     // fp32 input and fused flow; GPT-OSS bf16 input, biased logits, top-k then
@@ -1146,6 +1171,21 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
     }
   }
   return MKD_OK;
+}
+
+int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
+                            const int* position_ids, const float* cos, const float* sin,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = stale_check("mkd_qwen3_decode_layers")) return rc;
+  return decode_layers(m, B, hidden, position_ids, cos, sin, workspace, workspace_bytes, stream, -1);
+}
+
+int mkd_qwen3_prefill_layers(const mkd_qwen3_model* m, int seq, int T, void* hidden,
+                             const int* position_ids, const float* cos, const float* sin,
+                             void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = stale_check("mkd_qwen3_prefill_layers")) return rc;
+  MKD_REQUIRE(seq >= 0, MKD_ERR_INVALID, "prefill_layers: sequence %d must be >= 0", seq);
+  return decode_layers(m, T, hidden, position_ids, cos, sin, workspace, workspace_bytes, stream, seq);
 }
 
 int mkd_embed(const int* token_ids, const void* table, void* out, int B, int H, int V,

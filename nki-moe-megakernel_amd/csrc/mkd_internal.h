@@ -228,6 +228,10 @@ struct AttnArgs {
   // to row pos % (W-1) -- the GPT-OSS SWA layers (gpt_oss_with_megakernel.py:
   // 669-671, transformer_gpt_oss.py:139-205).  0 = full attention.
   int window;
+  // prefill of one sequence's tokens in one step (prep required): the prepared
+  // k / v rows are written to the cache before the attention reads it, so each
+  // token attends the rows of the earlier tokens of the same step
+  int prefill;
 };
 // rope_mode: 0 none, 1 cos/sin tables, 2 from pos and inv_freq
 hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s);

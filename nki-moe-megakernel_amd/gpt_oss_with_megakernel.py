@@ -32,7 +32,7 @@ from torch import nn
 
 from . import _lib as L
 from . import packing
-from .qwen_with_megakernel import EXPERT_FORMATS, pack_experts_mx, randn_bf16, tensor_seed
+from .qwen_with_megakernel import EXPERT_FORMATS, _prefill, pack_experts_mx, randn_bf16, tensor_seed
 
 VARIANT_GPT_OSS = 1
 
@@ -327,6 +327,16 @@ class GptOssMegakernelModel(nn.Module):
                                        next_tokens.data_ptr(), self.lm_ws.data_ptr(),
                                        self.lm_ws.numel(), s), "lm_head")
         return next_tokens
+
+    def prefill(self, input_ids: torch.Tensor, start_pos: int = 0, seq: int = 0, chunk: int = 128):
+        """Context encoding of one sequence: input_ids [T] fill the caches of sequence
+        `seq` from start_pos, then the step epilogue on the last token: (logits [V]
+        fp32, next id [1] int32).  The sliding-window layers' ring caches take one
+        token per pass, so a model with them prefills token by token."""
+        if any(self.cfg.is_sliding(l) for l in range(self.cfg.num_hidden_layers)):
+            chunk = 1
+        return _prefill(self, input_ids, start_pos, seq, chunk, self.cfg.hidden_pad, self.cfg.hidden_size,
+                        1, lambda pos: self.rope_cos_sin(pos))
 
     def get_model_output(self, input_ids: torch.Tensor, position_ids: torch.Tensor):
         """(norm(Y) [B, 1, H], [K0, V0, K1, V1, ...]) -- NeuronGptOssModelV1's return

@@ -341,6 +341,15 @@ class Qwen3MoeMegakernelModel(nn.Module):
                                        self.lm_ws.data_ptr(), self.lm_ws.numel(), s), "lm_head")
         return next_tokens
 
+    def prefill(self, input_ids: torch.Tensor, start_pos: int = 0, seq: int = 0, chunk: int = 128):
+        """Context encoding of one sequence (the reference's CTE layer path,
+        qwen_with_megakernel.py:496-526): input_ids [T] fill cache rows start_pos ..
+        start_pos + T - 1 of sequence `seq`, in passes of up to `chunk` tokens through
+        all layers (mkd_qwen3_prefill_layers), then the step epilogue on the last
+        token: (logits [V] fp32, next id [1] int32)."""
+        return _prefill(self, input_ids, start_pos, seq, chunk, self.cfg.hidden_size,
+                        self.cfg.hidden_size, 2, lambda pos: (None, None))
+
     def forward(self, input_ids: torch.Tensor, position_ids: torch.Tensor):
         """Greedy decode step: input_ids [B] -> (logits [B, V] fp32, next ids [B] int32)."""
         B = input_ids.shape[0]
@@ -350,6 +359,45 @@ class Qwen3MoeMegakernelModel(nn.Module):
         self.step(input_ids.to(torch.int32).contiguous(), position_ids.to(torch.int32).contiguous(),
                   hidden, logits, nxt)
         return logits, nxt
+
+
+def _prefill(model, input_ids, start_pos, seq, chunk, H, h_actual, norm_order, rope):
+    """Shared prefill loop of the Qwen3 and GPT-OSS models (same C entry point)."""
+    if model.embed_tokens is None or model.lm_head_packed is None:
+        raise ValueError("prefill needs the embedding table and lm_head")
+    if not 0 <= seq < model.batch:
+        raise ValueError(f"sequence {seq} outside the model's {model.batch} cache slots")
+    ids = input_ids.reshape(-1).to(device=model.device, dtype=torch.int32).contiguous()
+    T = ids.numel()
+    if T < 1 or start_pos < 0 or start_pos + T > model.cfg.max_seq:
+        raise ValueError(f"prompt of {T} tokens at {start_pos} does not fit max_seq {model.cfg.max_seq}")
+    chunk = max(1, min(int(chunk), 128, T))
+    lib = L.load()
+    ws = getattr(model, "_prefill_ws", None)
+    need = max(lib.mkd_qwen3_workspace_bytes(model._model, chunk), 256)
+    if ws is None or ws.numel() < need:
+        ws = model._prefill_ws = torch.zeros(need, dtype=torch.uint8, device=model.device)
+    V = model.cfg.vocab_size
+    hidden = torch.empty(chunk, H, dtype=torch.bfloat16, device=model.device)
+    s = L.stream_ptr(model.device)
+    n = 0
+    for c0 in range(0, T, chunk):
+        n = min(chunk, T - c0)
+        pos = torch.arange(start_pos + c0, start_pos + c0 + n, dtype=torch.int32, device=model.device)
+        h = hidden[:n]
+        L.check(lib.mkd_embed(ids[c0:].data_ptr(), model.embed_tokens.data_ptr(), h.data_ptr(), n, H,
+                              model.embed_tokens.shape[0], s), "embed")
+        cos, sin = rope(pos)
+        L.check(lib.mkd_qwen3_prefill_layers(model._model, seq, n, h.data_ptr(), pos.data_ptr(),
+                                             L.ptr(cos), L.ptr(sin), ws.data_ptr(), ws.numel(), s),
+                "qwen3_prefill_layers")
+    logits = torch.empty(1, V, dtype=torch.float32, device=model.device)
+    nxt = torch.empty(1, dtype=torch.int32, device=model.device)
+    L.check(lib.mkd_lm_head_greedy(hidden[n - 1:n].data_ptr(), model.ln_f.data_ptr(), model.cfg.rms_norm_eps,
+                                   model.lm_head_packed.data_ptr(), 1, H, V, h_actual, norm_order,
+                                   logits.data_ptr(), nxt.data_ptr(), model.lm_ws.data_ptr(),
+                                   model.lm_ws.numel(), s), "lm_head")
+    return logits[0], nxt
 
 
 class Qwen3MoeDecoderLayerMK(nn.Module):

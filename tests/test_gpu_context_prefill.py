@@ -1,0 +1,113 @@
+"""Context encoding (mkd_qwen3_prefill_layers through model.prefill): a prompt
+of one sequence in multi-token passes fills that sequence's KV cache and gives
+the last token's logits as the token-by-token decode step does (the reference's
+CTE layer path, qwen_with_megakernel.py:496-526, produces the same context the
+TKG path then reads).  Tolerance 2e-2 (max-abs error relative to the max-abs of
+the decode result): the two paths run the GEMMs at different token counts, so
+bf16 roundings differ; other sequences' caches are left bit-identical."""
+import pytest
+import torch
+
+from conftest import max_abs_rel
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-2
+
+
+def _qwen(dev, batch, kv_block=0, layers=2, seed=23):
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=layers, max_batch=batch, max_seq=256, vocab_size=1024,
+                             kv_block_len=kv_block)
+    packed = [Q.pack_layer({k: v.to(dev) for k, v in Q.random_layer_hf(cfg, l, seed, "cpu").items()})
+              for l in range(layers)]
+    g = torch.Generator().manual_seed(seed)
+    embed = (torch.randn(1024, cfg.hidden_size, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+    ln_f = (1 + 0.02 * torch.randn(cfg.hidden_size, generator=g)).to(torch.bfloat16).to(dev)
+    lm = (0.02 * torch.randn(1024, cfg.hidden_size, generator=g)).to(torch.bfloat16).to(dev)
+    return Q.Qwen3MoeMegakernelModel(cfg, packed, batch, dev, embed=embed, ln_f=ln_f, lm_head=lm)
+
+
+def _decode_seq1(m, ids, dev):
+    """Token-by-token decode of sequence 1 (sequence 0 decodes token 0 alongside)."""
+    logits = None
+    for t in range(ids.numel()):
+        tok = torch.tensor([0, int(ids[t])], dtype=torch.int32, device=dev)
+        pos = torch.tensor([t, t], dtype=torch.int32, device=dev)
+        logits, _ = m(tok, pos)
+    torch.cuda.synchronize()
+    return logits[1].cpu()
+
+
+@pytest.mark.parametrize("chunk", [16, 37])
+def test_qwen3_prefill_matches_token_by_token_decode(mk, dev, chunk):
+    print(f"qwen3 prefill T=37 chunk={chunk}", flush=True)
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, 1024, (37,), generator=g, dtype=torch.int32)
+    ma = _qwen(dev, 2)
+    la, na = ma.prefill(ids.to(dev), start_pos=0, seq=1, chunk=chunk)
+    torch.cuda.synchronize()
+    mb = _qwen(dev, 2)
+    lb = _decode_seq1(mb, ids, dev)
+    la = la.cpu()
+    assert torch.isfinite(la).all()
+    assert max_abs_rel(la, lb) < TOL
+    assert int(na.cpu()[0]) == int(la.argmax())
+    for l in range(2):
+        ka, kb = ma.kv_mgr.k(l).cpu(), mb.kv_mgr.k(l).cpu()
+        va, vb = ma.kv_mgr.v(l).cpu(), mb.kv_mgr.v(l).cpu()
+        assert max_abs_rel(ka[1, :, :37], kb[1, :, :37]) < TOL
+        assert max_abs_rel(va[1, :, :37], vb[1, :, :37]) < TOL
+        assert not ka[1, :, 37:].any() and not va[1, :, 37:].any()   # nothing past the prompt
+        assert not ka[0].any() and not va[0].any()                   # other sequence untouched
+
+
+def test_qwen3_prefill_continues_into_decode_and_paged_matches_flat(mk, dev):
+    """Prefill 20 tokens at position 0 then 9 more at position 20 == one 29-token
+    prefill (to tolerance); the paged cache gives bit-identical logits to the flat
+    one for the same calls; decoding after the prefill reads the prefilled rows."""
+    print("qwen3 prefill paged vs flat, two calls", flush=True)
+    g = torch.Generator().manual_seed(8)
+    ids = torch.randint(0, 1024, (29,), generator=g, dtype=torch.int32).to(dev)
+    mf, mp = _qwen(dev, 1), _qwen(dev, 1, kv_block=64)
+    outs = []
+    for m in (mf, mp):
+        m.prefill(ids[:20], start_pos=0, seq=0, chunk=128)
+        l2, n2 = m.prefill(ids[20:], start_pos=20, seq=0, chunk=128)
+        l3, _ = m(n2.to(torch.int32), torch.tensor([29], dtype=torch.int32, device=dev))
+        torch.cuda.synchronize()
+        outs.append((l2.cpu(), l3[0].cpu()))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    m1 = _qwen(dev, 1)
+    l1, _ = m1.prefill(ids, start_pos=0, seq=0, chunk=128)
+    torch.cuda.synchronize()
+    assert max_abs_rel(outs[0][0], l1.cpu()) < TOL
+
+
+def test_gpt_oss_prefill_token_by_token(mk, dev):
+    """GPT-OSS (sliding-window layers: one token per pass) prefill == decode steps."""
+    from nki_moe_megakernel_amd import gpt_oss_with_megakernel as G
+    print("gpt-oss prefill T=6", flush=True)
+    cfg = G.GptOssMKConfig(num_hidden_layers=2, max_batch=1, max_seq=256, vocab_size=1024,
+                           num_experts=8, intermediate_size=1024, expert_format="bf16")
+
+    def build():
+        packed = [G.pack_layer({k: v.to(dev) for k, v in G.random_layer_hf(cfg, l, 3, "cpu").items()}, cfg)
+                  for l in range(2)]
+        g = torch.Generator().manual_seed(3)
+        embed = (torch.randn(1024, cfg.hidden_size, generator=g) * 0.5).to(torch.bfloat16).to(dev)
+        ln_f = (1 + 0.02 * torch.randn(cfg.hidden_size, generator=g)).to(torch.bfloat16).to(dev)
+        lm = (0.02 * torch.randn(1024, cfg.hidden_size, generator=g)).to(torch.bfloat16).to(dev)
+        return G.GptOssMegakernelModel(cfg, packed, 1, dev, embed=embed, ln_f=ln_f, lm_head=lm)
+
+    ids = torch.tensor([5, 17, 900, 3, 44, 1000], dtype=torch.int32, device=dev)
+    ma, mb = build(), build()
+    la, _ = ma.prefill(ids, start_pos=0)
+    hidden = torch.empty(1, cfg.hidden_pad, dtype=torch.bfloat16, device=dev)
+    logits = torch.empty(1, cfg.vocab_size, dtype=torch.float32, device=dev)
+    nxt = torch.empty(1, dtype=torch.int32, device=dev)
+    for t in range(6):
+        mb.step(ids[t:t + 1], torch.tensor([t], dtype=torch.int32, device=dev), hidden, logits, nxt)
+    torch.cuda.synchronize()
+    assert max_abs_rel(la.cpu(), logits[0].cpu()) < TOL
+    for l in range(2):
+        assert max_abs_rel(ma.kv_mgr.k(l).cpu(), mb.kv_mgr.k(l).cpu()) < TOL
