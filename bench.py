@@ -24,6 +24,7 @@ Also reported:
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--batch B]
        python bench.py --moe-prefill T   (MFMA regime of the expert GEMMs)
+       python bench.py --prefill T       (context encoding of a T-token prompt)
 """
 from __future__ import annotations
 
@@ -242,12 +243,17 @@ def main():
                          "use --batch 32 --ragged --experts mxfp4)")
     ap.add_argument("--persistent", action="store_true",
                     help="run each decoder layer as one persistent kernel launch (batches <= 4)")
+    ap.add_argument("--prefill", type=int, default=0, metavar="T",
+                    help="measure context encoding instead: model.prefill of a T-token prompt "
+                         "(passes of 128 tokens through all layers)")
     ap.add_argument("--moe-prefill", type=int, default=0, metavar="T",
                     help="measure the MFMA regime instead: moe_prefill (LDS-tiled grouped GEMMs) "
                          "on T tokens of the Qwen3 expert shape (E=128, K=8), T*K/E tokens/expert")
     args = ap.parse_args()
     if args.moe_prefill and args.gpus == 1:
         return bench_moe_prefill(args)
+    if args.prefill and args.gpus == 1:
+        return bench_context_prefill(args)
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only (--gpus {args.gpus} requested); "
               "multi-GPU sharding is a design note, not a measured path", file=sys.stderr)
@@ -522,6 +528,65 @@ def bench_moe_prefill(args):
                      "achieved": round(gu_tf, 1), "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(gu_tf / MFMA_BF16_PEAK_TFLOPS, 4), "traffic": None,
                      "flops_per_launch": fl_gu, "avg_us": round(kern["moe_gate_up"], 1)},
+    }
+    print(json.dumps(line), flush=True)
+
+
+def bench_context_prefill(args):
+    """Context encoding: model.prefill of a T-token prompt (one sequence, passes of
+    128 tokens through all 48 layers), each step re-encoding the same prompt into
+    cache rows 0..T-1.  Algorithmic HBM bytes per pass: the attention / router
+    weights once, each expert's weights once if any token of the pass routes to
+    it (counted from the routing of a seeded uniform draw), and the K/V prefix each
+    token attends; reported against HBM peak for the whole pass (several kernels)."""
+    import torch
+    import __graft_entry__ as ge
+    ge.load_package()
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    dev = torch.device("cuda:0")
+    T = args.prefill
+    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=args.layers, max_batch=1,
+                             max_seq=(T + 127) // 128 * 128 + 128)
+    t0 = time.time()
+    model = build_model(Q, cfg, 1, dev, seed=1234)
+    torch.cuda.synchronize()
+    log(f"model built in {time.time() - t0:.1f}s")
+    g = torch.Generator(device=dev).manual_seed(7)
+    ids = torch.randint(0, cfg.vocab_size, (T,), generator=g, device=dev, dtype=torch.int32)
+    for _ in range(max(args.warmup, 1)):
+        model.prefill(ids, start_pos=0, chunk=128)
+    torch.cuda.synchronize()
+    n = max(1, min(args.steps, 16))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        model.prefill(ids, start_pos=0, chunk=128)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    H, E, K, I, d, nq, nkv = (cfg.hidden_size, cfg.num_experts, cfg.num_experts_per_tok,
+                              cfg.moe_intermediate_size, cfg.head_dim, cfg.num_attention_heads,
+                              cfg.num_key_value_heads)
+    dense_b = 2 * ((nq + 2 * nkv) * d * H + H * nq * d + E * H)
+    expert_b = 2 * 3 * I * H
+    passes = [(c0, min(128, T - c0)) for c0 in range(0, T, 128)]
+    alg = 0.0
+    for c0, nt in passes:
+        distinct = E * (1 - (1 - K / E) ** nt)
+        kv = sum(2 * nkv * (c0 + t + 1) * d * 2 for t in range(nt))
+        alg += cfg.num_hidden_layers * (dense_b + distinct * expert_b + kv)
+    gbs = alg / (ms * 1e-3) / 1e9
+    line = {
+        "metric": "context-encoding throughput (prefill of one sequence)", "value": round(T / (ms * 1e-3), 1),
+        "unit": "tokens/s", "n_gpus": 1, "steps": n, "warmup": args.warmup, "ms_per_step": round(ms, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded random bf16 weights, random prompt ids)",
+        "config": {"workload": f"Qwen3-30B-A3B shape, {cfg.num_hidden_layers} layers, {T}-token prompt "
+                               f"in {len(passes)} passes of <= 128 tokens", "tokens": T},
+        "roofline": {"bound": "hbm", "kernel": "whole prefill pass (all kernels)",
+                     "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes_per_step": round(alg)},
     }
     print(json.dumps(line), flush=True)
 
