@@ -426,8 +426,10 @@ def main():
         "roofline": {"bound": "hbm",
                      "kernel": ("persistent decoder (layer_kernel<%d,%d>), one launch for all layers"
                                 % (cfg.head_dim, 2 if cfg.num_experts <= 128 else 8)) if layer_kernel else
-                               "moe gate_up grouped GEMM (" + ("gemm_frag_kernel<2,1,0,3>" if args.experts == "bf16"
-                                                               else "gemm_mx_kernel<2,fmt,3>") + ")",
+                               "moe gate_up grouped GEMM (" + (
+                                   "gemm_mx_kernel<2,fmt,3>" if args.experts != "bf16" else
+                                   "gemm_frag_sel_kernel<2>: router top-k formed in every block"
+                                   if B == 1 and not oss else "gemm_frag_kernel<2,1,0,3>") + ")",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers, kcls)
