@@ -245,7 +245,9 @@ def main():
                     help="run each decoder layer as one persistent kernel launch (batches <= 4)")
     ap.add_argument("--prefill", type=int, default=0, metavar="T",
                     help="measure context encoding instead: model.prefill of a T-token prompt "
-                         "(passes of 128 tokens through all layers)")
+                         "(passes of --prefill-chunk tokens through all layers)")
+    ap.add_argument("--prefill-chunk", type=int, default=512,
+                    help="tokens per prefill pass (<= 1024; above 128 the experts run as tiled MFMA GEMMs)")
     ap.add_argument("--moe-prefill", type=int, default=0, metavar="T",
                     help="measure the MFMA regime instead: moe_prefill (LDS-tiled grouped GEMMs) "
                          "on T tokens of the Qwen3 expert shape (E=128, K=8), T*K/E tokens/expert")
@@ -536,7 +538,7 @@ def bench_moe_prefill(args):
 
 def bench_context_prefill(args):
     """Context encoding: model.prefill of a T-token prompt (one sequence, passes of
-    128 tokens through all 48 layers), each step re-encoding the same prompt into
+    --prefill-chunk tokens through all 48 layers), each step re-encoding the same prompt into
     cache rows 0..T-1.  Algorithmic HBM bytes per pass: the attention / router
     weights once, each expert's weights once if any token of the pass routes to
     it (counted from the routing of a seeded uniform draw), and the K/V prefix each
@@ -546,7 +548,7 @@ def bench_context_prefill(args):
     ge.load_package()
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
     dev = torch.device("cuda:0")
-    T = args.prefill
+    T, CH = args.prefill, max(1, min(args.prefill_chunk, 1024))
     cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=args.layers, max_batch=1,
                              max_seq=(T + 127) // 128 * 128 + 128)
     t0 = time.time()
@@ -556,13 +558,13 @@ def bench_context_prefill(args):
     g = torch.Generator(device=dev).manual_seed(7)
     ids = torch.randint(0, cfg.vocab_size, (T,), generator=g, device=dev, dtype=torch.int32)
     for _ in range(max(args.warmup, 1)):
-        model.prefill(ids, start_pos=0, chunk=128)
+        model.prefill(ids, start_pos=0, chunk=CH)
     torch.cuda.synchronize()
     n = max(1, min(args.steps, 16))
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(n):
-        model.prefill(ids, start_pos=0, chunk=128)
+        model.prefill(ids, start_pos=0, chunk=CH)
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / n
@@ -571,7 +573,7 @@ def bench_context_prefill(args):
                               cfg.num_key_value_heads)
     dense_b = 2 * ((nq + 2 * nkv) * d * H + H * nq * d + E * H)
     expert_b = 2 * 3 * I * H
-    passes = [(c0, min(128, T - c0)) for c0 in range(0, T, 128)]
+    passes = [(c0, min(CH, T - c0)) for c0 in range(0, T, CH)]
     alg = 0.0
     for c0, nt in passes:
         distinct = E * (1 - (1 - K / E) ** nt)
@@ -584,7 +586,7 @@ def bench_context_prefill(args):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded random bf16 weights, random prompt ids)",
         "config": {"workload": f"Qwen3-30B-A3B shape, {cfg.num_hidden_layers} layers, {T}-token prompt "
-                               f"in {len(passes)} passes of <= 128 tokens", "tokens": T},
+                               f"in {len(passes)} passes of <= {CH} tokens", "tokens": T, "chunk": CH},
         "roofline": {"bound": "hbm", "kernel": "whole prefill pass (all kernels)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,

@@ -974,7 +974,8 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
   const bool prefill = prefill_seq >= 0;
   MKD_REQUIRE(m && hidden && position_ids && workspace, MKD_ERR_NULL, "decode_layers: null pointer");
   MKD_REQUIRE(m->num_layers > 0, MKD_ERR_INVALID, "decode_layers: num_layers must be > 0");
-  MKD_REQUIRE(B > 0 && B <= 128, MKD_ERR_INVALID, "decode_layers: B %d must be in [1, 128]", B);
+  const int max_b = prefill ? kMaxPrefillT : 128;
+  MKD_REQUIRE(B > 0 && B <= max_b, MKD_ERR_INVALID, "decode_layers: %d tokens must be in [1, %d]", B, max_b);
   MKD_REQUIRE(cos || m->inv_freq, MKD_ERR_NULL, "decode_layers: need cos/sin or inv_freq");
   MKD_REQUIRE(m->E <= 512 && m->K >= 1 && m->K <= 8, MKD_ERR_INVALID, "decode_layers: bad E/K");
   MKD_REQUIRE(m->H % 8 == 0 && m->H <= 8192, MKD_ERR_INVALID, "decode_layers: bad H");
@@ -1136,15 +1137,32 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
         na.rows = B; na.H = m->H; na.hidden_actual = ha; na.eps = m->eps; na.order = 0;
         MKD_TRY(norm_launch(na, s), "residual + post norm");
       }
-      {
-        const int ps = prof_begin(MKD_KCLASS_ROUTER, s);
+      const int ps = prof_begin(MKD_KCLASS_ROUTER, s);
+      if (B <= 128) {
         if (int rc = router_stage(oss ? static_cast<const void*>(w.nbf) : w.nf32, !oss, m->H,
                                   m->router[l], w.logits, ra, s))
           return rc;
-        prof_end(ps, s);
+      } else {
+        // a long prefill pass: top-k per slice of 128 tokens (the select is one
+        // block), the expert groups of all tokens from the indices afterwards
+        for (int t0 = 0; t0 < B; t0 += 128) {
+          RouterArgs rs = ra;
+          rs.T = std::min(128, B - t0);
+          rs.idx_out = ra.idx_out + (size_t)t0 * m->K;
+          rs.slot_w = ra.slot_w + (size_t)t0 * m->K;
+          rs.n_groups = nullptr; rs.grp_expert = rs.grp_count = rs.grp_offset = nullptr;
+          rs.pair_token = rs.pair_slot = nullptr;
+          const void* xr = oss ? static_cast<const void*>(w.nbf + (size_t)t0 * m->H)
+                               : static_cast<const void*>(w.nf32 + (size_t)t0 * m->H);
+          if (int rc = router_stage(xr, !oss, m->H, m->router[l], w.logits, rs, s)) return rc;
+        }
       }
+      prof_end(ps, s);
     }
-    if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], nullptr, w.moe.slot_w,
+    // > 128 tokens (prefill): groups from the indices, and with bf16 experts the
+    // LDS-tiled grouped GEMMs (tens of tokens per expert)
+    const bool long_pass = B > 128;
+    if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], long_pass ? w.moe.idx : nullptr, w.moe.slot_w,
                           static_cast<const uint16_t*>(at(m->gate_up_bias, l)),
                           static_cast<const uint16_t*>(at(m->down_bias, l)), w.r, x, nullptr, B,
                           m->H, m->E, m->I, m->K, oss ? MKD_ACT_SWISH : MKD_ACT_SILU,
@@ -1153,7 +1171,9 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
                           oss ? m->up_lo : -INFINITY, (oss || m->expert_format) ? 0 : 1,
                           w.moe, s, false, m->expert_format,
                           m->expert_format ? m->gate_up_scales[l] : nullptr,
-                          m->expert_format ? m->down_scales[l] : nullptr, false,
+                          m->expert_format ? m->down_scales[l] : nullptr,
+                          long_pass && !m->expert_format && gemm_tile_supported(2 * m->I, m->H, EPI_SWIGLU_BF16) &&
+                              gemm_tile_supported(m->H, m->I, EPI_SCALE_F32),
                           defer_sel ? &sel : nullptr))
       return rc;
     // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention

@@ -83,6 +83,46 @@ def test_qwen3_prefill_continues_into_decode_and_paged_matches_flat(mk, dev):
     assert max_abs_rel(outs[0][0], l1.cpu()) < TOL
 
 
+def test_qwen3_long_prefill_pass_matches_short_passes(mk, dev):
+    """One 300-token pass (router top-k in slices of 128, expert groups from the
+    indices, LDS-tiled MFMA expert GEMMs) == passes of <= 128 tokens (to
+    tolerance), caches included."""
+    print("qwen3 prefill T=300 one pass vs three", flush=True)
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    g = torch.Generator().manual_seed(12)
+    ids = torch.randint(0, 1024, (300,), generator=g, dtype=torch.int32).to(dev)
+
+    outs = []
+    for chunk in (300, 128):
+        cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=2, max_batch=1, max_seq=512, vocab_size=1024)
+        packed = [Q.pack_layer({k: v.to(dev) for k, v in Q.random_layer_hf(cfg, l, 29, "cpu").items()})
+                  for l in range(2)]
+        gg = torch.Generator().manual_seed(29)
+        embed = (torch.randn(1024, cfg.hidden_size, generator=gg) * 0.5).to(torch.bfloat16).to(dev)
+        ln_f = (1 + 0.02 * torch.randn(cfg.hidden_size, generator=gg)).to(torch.bfloat16).to(dev)
+        lm = (0.02 * torch.randn(1024, cfg.hidden_size, generator=gg)).to(torch.bfloat16).to(dev)
+        m = Q.Qwen3MoeMegakernelModel(cfg, packed, 1, dev, embed=embed, ln_f=ln_f, lm_head=lm)
+        lo, _ = m.prefill(ids, start_pos=0, seq=0, chunk=chunk)
+        torch.cuda.synchronize()
+        outs.append((lo.cpu(), [m.kv_mgr.k(l).cpu() for l in range(2)], [m.kv_mgr.v(l).cpu() for l in range(2)]))
+    (la, ka, va), (lb, kb, vb) = outs
+    assert torch.isfinite(la).all()
+    assert max_abs_rel(la, lb) < TOL
+    # per position: the two runs sum the expert GEMMs (tiled vs streaming) and the
+    # router inputs in different fp32 orders, so a token whose 8th / 9th router
+    # logits nearly tie (< 1e-4, the bar for router indices) may take another
+    # expert in layer 0 and carry different layer-1 K / V rows; at most 1 % of
+    # the positions may do so, every other row stays within the tolerance
+    for l in range(2):
+        for new, old in ((ka[l][0], kb[l][0]), (va[l][0], vb[l][0])):
+            scale = old[:, :300].abs().max()
+            err = ((new[:, :300].float() - old[:, :300].float()).abs().amax(dim=(0, 2)) / scale)
+            bad = (err >= TOL).nonzero().flatten().tolist()
+            print(f"layer {l}: positions beyond tolerance {bad}", flush=True)
+            assert len(bad) <= (0 if l == 0 else 3)
+            assert not new[:, 300:].any()
+
+
 def test_gpt_oss_prefill_token_by_token(mk, dev):
     """GPT-OSS (sliding-window layers: one token per pass) prefill == decode steps."""
     from nki_moe_megakernel_amd import gpt_oss_with_megakernel as G
