@@ -166,6 +166,13 @@ int check_mx_dims(int N, int K, int rb) {
 // Dense launch with the token count split into tiles of <= 64 rows.
 int dense_gemm(GemmArgs a, int epi, bool xf32, hipStream_t s) {
   const int T = a.T;
+  // many tokens (prefill passes): the LDS-tiled MFMA GEMM, fp32 out (+ bias)
+  if (T >= 256 && epi == EPI_F32 && !xf32 && a.kgrid <= 1 && !a.residual && !a.grp_expert &&
+      gemm_tile_supported(a.N, a.K, EPI_SCALE_F32)) {
+    a.pair_scale = nullptr;
+    MKD_TRY(gemm_tile_launch(a, EPI_SCALE_F32, 1, T, s), "tiled gemm");
+    return MKD_OK;
+  }
   for (int t0 = 0; t0 < T; t0 += 64) {
     GemmArgs b = a;
     const int tt = T - t0 < 64 ? T - t0 : 64;
@@ -191,7 +198,7 @@ int router_kgrid(int E, int H) {
 
 // logits (split-K partials into `parts`) -> select (+ groups when r.n_groups).
 int router_stage(const void* x, bool xf32, int H, const void* w_packed, float* parts, RouterArgs r,
-                 hipStream_t s) {
+                 hipStream_t s, bool multi = false) {
   const int kg = router_kgrid(r.E, H);
   GemmArgs a = dense_args(w_packed, x, H, r.E, H, r.T, parts, r.E);
   a.kgrid = kg;
@@ -202,7 +209,10 @@ int router_stage(const void* x, bool xf32, int H, const void* w_packed, float* p
   r.parts = parts;
   r.nparts = kg;
   r.part_stride = a.part_stride;
-  MKD_TRY(router_select_launch(r, s), "router select");
+  if (multi)
+    MKD_TRY(router_select_multi_launch(r, s), "router select (multi-block)");
+  else
+    MKD_TRY(router_select_launch(r, s), "router select");
   return MKD_OK;
 }
 
@@ -1143,19 +1153,14 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
                                   m->router[l], w.logits, ra, s))
           return rc;
       } else {
-        // a long prefill pass: top-k per slice of 128 tokens (the select is one
-        // block), the expert groups of all tokens from the indices afterwards
-        for (int t0 = 0; t0 < B; t0 += 128) {
-          RouterArgs rs = ra;
-          rs.T = std::min(128, B - t0);
-          rs.idx_out = ra.idx_out + (size_t)t0 * m->K;
-          rs.slot_w = ra.slot_w + (size_t)t0 * m->K;
-          rs.n_groups = nullptr; rs.grp_expert = rs.grp_count = rs.grp_offset = nullptr;
-          rs.pair_token = rs.pair_slot = nullptr;
-          const void* xr = oss ? static_cast<const void*>(w.nbf + (size_t)t0 * m->H)
-                               : static_cast<const void*>(w.nf32 + (size_t)t0 * m->H);
-          if (int rc = router_stage(xr, !oss, m->H, m->router[l], w.logits, rs, s)) return rc;
-        }
+        // a long prefill pass: one router GEMM, the top-k of 16 tokens per
+        // block, and the expert groups of all tokens from the indices afterwards
+        RouterArgs rs = ra;
+        rs.n_groups = nullptr; rs.grp_expert = rs.grp_count = rs.grp_offset = nullptr;
+        rs.pair_token = rs.pair_slot = nullptr;
+        if (int rc = router_stage(oss ? static_cast<const void*>(w.nbf) : w.nf32, !oss, m->H,
+                                  m->router[l], w.logits, rs, s, true))
+          return rc;
       }
       prof_end(ps, s);
     }

@@ -255,6 +255,9 @@ struct RouterArgs {
   int *n_groups, *grp_expert, *grp_count, *grp_offset, *pair_token, *pair_slot;
 };
 hipError_t router_select_launch(const RouterArgs& a, hipStream_t s);
+// Any number of tokens, no expert grouping (n_groups must be null): 16 tokens
+// per block.
+hipError_t router_select_multi_launch(const RouterArgs& a, hipStream_t s);
 // Residual add + post-attention RMSNorm folded into the split-K router GEMM, then
 // the select launch, for a handful of tokens (router_fused_supported).  r.parts
 // must hold 16 * T * E floats.

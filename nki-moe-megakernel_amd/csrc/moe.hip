@@ -39,6 +39,35 @@ __global__ void __launch_bounds__(1024) router_select_kernel(RouterArgs a) {
   });
 }
 
+// Many tokens without grouping (a long prefill pass): block b selects tokens
+// 16b .. 16b + 15, one per wave, with the arithmetic of router_select_kernel.
+template <int PER>
+__global__ void __launch_bounds__(1024) router_select_multi_kernel(RouterArgs a) {
+  const int t0 = blockIdx.x * 16;
+  RouterArgs q = a;
+  q.T = min(16, a.T - t0);
+  q.parts = a.parts + (long long)t0 * a.E;
+  if (a.logits_out) q.logits_out = a.logits_out + (long long)t0 * a.E;
+  if (a.aff_full) q.aff_full = a.aff_full + (long long)t0 * a.E;
+  if (a.idx_out) q.idx_out = a.idx_out + t0 * a.K;
+  if (a.topk_out) q.topk_out = a.topk_out + t0 * a.K;
+  if (a.slot_w) q.slot_w = a.slot_w + t0 * a.K;
+  const int lane = threadIdx.x & 63;
+  select_body<PER>(q, [&](int t, float (&l)[PER]) { load_logits<PER>(q, t, lane, l); });
+}
+
+hipError_t router_select_multi_launch(const RouterArgs& a, hipStream_t s) {
+  if (a.E > kMaxE || a.K > 8 || a.K < 1 || a.K > a.E || a.T < 1 || a.nparts > 16 || a.n_groups)
+    return hipErrorInvalidValue;
+  const dim3 grid((a.T + 15) / 16);
+  const int per = (a.E + 63) / 64;
+  if (per <= 1) hipLaunchKernelGGL(router_select_multi_kernel<1>, grid, dim3(1024), 0, s, a);
+  else if (per <= 2) hipLaunchKernelGGL(router_select_multi_kernel<2>, grid, dim3(1024), 0, s, a);
+  else if (per <= 4) hipLaunchKernelGGL(router_select_multi_kernel<4>, grid, dim3(1024), 0, s, a);
+  else hipLaunchKernelGGL(router_select_multi_kernel<8>, grid, dim3(1024), 0, s, a);
+  return hipGetLastError();
+}
+
 // ---------------------------------------------------------------------------
 __global__ void __launch_bounds__(1024)
 moe_route_kernel(const int* __restrict__ idx, int T, int K, int E, int* __restrict__ n_groups,
