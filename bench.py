@@ -246,8 +246,8 @@ def main():
     ap.add_argument("--prefill", type=int, default=0, metavar="T",
                     help="measure context encoding instead: model.prefill of a T-token prompt "
                          "(passes of --prefill-chunk tokens through all layers)")
-    ap.add_argument("--prefill-chunk", type=int, default=512,
-                    help="tokens per prefill pass (<= 1024; above 128 the experts run as tiled MFMA GEMMs)")
+    ap.add_argument("--prefill-chunk", type=int, default=4096,
+                    help="tokens per prefill pass (<= 4096; above 128 the experts run as tiled MFMA GEMMs)")
     ap.add_argument("--moe-prefill", type=int, default=0, metavar="T",
                     help="measure the MFMA regime instead: moe_prefill (LDS-tiled grouped GEMMs) "
                          "on T tokens of the Qwen3 expert shape (E=128, K=8), T*K/E tokens/expert")
@@ -548,7 +548,7 @@ def bench_context_prefill(args):
     ge.load_package()
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
     dev = torch.device("cuda:0")
-    T, CH = args.prefill, max(1, min(args.prefill_chunk, 1024))
+    T, CH = args.prefill, max(1, min(args.prefill_chunk, 4096))
     cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=args.layers, max_batch=1,
                              max_seq=(T + 127) // 128 * 128 + 128)
     t0 = time.time()

@@ -319,7 +319,7 @@ int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,
                             void* workspace, size_t workspace_bytes, void* stream);
 /* Context encoding (prefill) of one sequence through all layers:
  * hidden [T, H] bf16 in/out holds T consecutive tokens of sequence `seq` at
- * position_ids [T] (int32, device; normally p0 .. p0 + T - 1), 1 <= T <= 1024
+ * position_ids [T] (int32, device; normally p0 .. p0 + T - 1), 1 <= T <= 4096
  * (above 128 tokens the experts run as LDS-tiled MFMA grouped GEMMs).
  * Every token's k / v rows are written to sequence seq's cache (flat: batch
  * index seq; paged: block_table row seq) before the attention reads it, so

@@ -100,7 +100,7 @@ hipError_t pack_frag_launch(const uint16_t* src, uint16_t* dst, int G, int N, in
                             int interleave_half, hipStream_t s);
 
 // layer_mk.hip: persistent decoder layer (small batches, Qwen3 flow, bf16 experts)
-constexpr int kMaxPrefillT = 1024;   // tokens per prefill pass (mkd_qwen3_prefill_layers)
+constexpr int kMaxPrefillT = 4096;   // tokens per prefill pass (mkd_qwen3_prefill_layers)
 constexpr int kLkMaxB = 4;          // tokens per launch
 constexpr int kLkMaxNB = 1024;      // blocks (CUs) per launch
 constexpr int kLkBarWords = kLkMaxNB + 64;   // per-block flags + error word (zeroed once per step)

@@ -328,7 +328,7 @@ class GptOssMegakernelModel(nn.Module):
                                        self.lm_ws.numel(), s), "lm_head")
         return next_tokens
 
-    def prefill(self, input_ids: torch.Tensor, start_pos: int = 0, seq: int = 0, chunk: int = 512):
+    def prefill(self, input_ids: torch.Tensor, start_pos: int = 0, seq: int = 0, chunk: int = 4096):
         """Context encoding of one sequence: input_ids [T] fill the caches of sequence
         `seq` from start_pos, then the step epilogue on the last token: (logits [V]
         fp32, next id [1] int32).  The sliding-window layers' ring caches take one

@@ -341,10 +341,10 @@ class Qwen3MoeMegakernelModel(nn.Module):
                                        self.lm_ws.data_ptr(), self.lm_ws.numel(), s), "lm_head")
         return next_tokens
 
-    def prefill(self, input_ids: torch.Tensor, start_pos: int = 0, seq: int = 0, chunk: int = 512):
+    def prefill(self, input_ids: torch.Tensor, start_pos: int = 0, seq: int = 0, chunk: int = 4096):
         """Context encoding of one sequence (the reference's CTE layer path,
         qwen_with_megakernel.py:496-526): input_ids [T] fill cache rows start_pos ..
-        start_pos + T - 1 of sequence `seq`, in passes of up to `chunk` (<= 1024)
+        start_pos + T - 1 of sequence `seq`, in passes of up to `chunk` (<= 4096)
         tokens through all layers (mkd_qwen3_prefill_layers; passes above 128 tokens
         run the experts as LDS-tiled MFMA GEMMs), then the step epilogue on the last
         token: (logits [V] fp32, next id [1] int32)."""
@@ -372,7 +372,7 @@ def _prefill(model, input_ids, start_pos, seq, chunk, H, h_actual, norm_order, r
     T = ids.numel()
     if T < 1 or start_pos < 0 or start_pos + T > model.cfg.max_seq:
         raise ValueError(f"prompt of {T} tokens at {start_pos} does not fit max_seq {model.cfg.max_seq}")
-    chunk = max(1, min(int(chunk), 1024, T))
+    chunk = max(1, min(int(chunk), 4096, T))
     lib = L.load()
     ws = getattr(model, "_prefill_ws", None)
     need = max(lib.mkd_qwen3_workspace_bytes(model._model, chunk), 256)
