@@ -163,7 +163,8 @@ int check_mx_dims(int N, int K, int rb) {
   return MKD_OK;
 }
 
-// Dense launch with the token count split into tiles of <= 64 rows.
+// Dense launch: the tiled MFMA GEMM for many tokens, else one launch of 16..64-token
+// column tiles.
 int dense_gemm(GemmArgs a, int epi, bool xf32, hipStream_t s) {
   const int T = a.T;
   // many tokens (prefill passes): the LDS-tiled MFMA GEMM, fp32 out (+ bias)
@@ -171,6 +172,12 @@ int dense_gemm(GemmArgs a, int epi, bool xf32, hipStream_t s) {
       gemm_tile_supported(a.N, a.K, EPI_SCALE_F32)) {
     a.pair_scale = nullptr;
     MKD_TRY(gemm_tile_launch(a, EPI_SCALE_F32, 1, T, s), "tiled gemm");
+    return MKD_OK;
+  }
+  // more than one 64-token column of tiles: one launch over all of them (grid z
+  // holds the token tiles x the K split)
+  if (T > 64) {
+    MKD_TRY(gemm_launch(a, epi, xf32, 4, 1, T, s), "gemm launch");
     return MKD_OK;
   }
   for (int t0 = 0; t0 < T; t0 += 64) {
