@@ -34,3 +34,23 @@ def test_gpt_oss_converter_deinterleaves_and_folds_up_bias(mk):
     assert torch.equal(c["gate_up_bias"][:, 1].float(), (b[:, 1::2] + 1).bfloat16().float())
     assert torch.equal(c["down"][:, :96], hf["experts.down_proj"].transpose(1, 2))
     assert not c["w_qkv"][:, 96:].any() and not c["ln_in"][96:].any()
+
+
+def test_prefill_rejects_bad_requests_before_any_gpu_call(mk):
+    """model.prefill's host checks: the sequence slot must exist and the prompt must
+    fit the caches; a model without embedding / lm_head cannot prefill."""
+    from types import SimpleNamespace
+    from nki_moe_megakernel_amd.qwen_with_megakernel import _prefill
+    cfg = SimpleNamespace(max_seq=16, vocab_size=32)
+    m = SimpleNamespace(embed_tokens=torch.zeros(1), lm_head_packed=torch.zeros(1), batch=2, cfg=cfg,
+                        device=torch.device("cpu"))
+    ids = torch.arange(4, dtype=torch.int32)
+    with pytest.raises(ValueError, match="sequence 2"):
+        _prefill(m, ids, 0, 2, 128, 8, 8, 2, lambda p: (None, None))
+    with pytest.raises(ValueError, match="does not fit"):
+        _prefill(m, ids, 13, 0, 128, 8, 8, 2, lambda p: (None, None))
+    with pytest.raises(ValueError, match="does not fit"):
+        _prefill(m, ids[:0], 0, 0, 128, 8, 8, 2, lambda p: (None, None))
+    with pytest.raises(ValueError, match="embedding"):
+        _prefill(SimpleNamespace(**{**m.__dict__, "lm_head_packed": None}), ids, 0, 0, 128, 8, 8, 2,
+                 lambda p: (None, None))
