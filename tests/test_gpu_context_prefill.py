@@ -83,12 +83,12 @@ def test_qwen3_prefill_continues_into_decode_and_paged_matches_flat(mk, dev):
     assert max_abs_rel(outs[0][0], l1.cpu()) < TOL
 
 
-@pytest.mark.parametrize("T,short", [(300, 128), (1100, 512)])
-def test_qwen3_long_prefill_pass_matches_short_passes(mk, dev, T, short):
+@pytest.mark.parametrize("T,short,fmt", [(300, 128, "bf16"), (1100, 512, "bf16"), (300, 128, "mxfp8")])
+def test_qwen3_long_prefill_pass_matches_short_passes(mk, dev, T, short, fmt):
     """One T-token pass (router top-k on 16 tokens per block, expert groups from the
     indices, LDS-tiled MFMA expert / projection GEMMs) == passes of <= `short`
     tokens (to tolerance), caches included."""
-    print(f"qwen3 prefill T={T} one pass vs passes of {short}", flush=True)
+    print(f"qwen3 prefill T={T} one pass vs passes of {short}, {fmt} experts", flush=True)
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
     g = torch.Generator().manual_seed(12)
     ids = torch.randint(0, 1024, (T,), generator=g, dtype=torch.int32).to(dev)
@@ -96,8 +96,8 @@ def test_qwen3_long_prefill_pass_matches_short_passes(mk, dev, T, short):
     outs = []
     for chunk in (T, short):
         cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=2, max_batch=1, max_seq=(T + 255) // 256 * 256,
-                                 vocab_size=1024)
-        packed = [Q.pack_layer({k: v.to(dev) for k, v in Q.random_layer_hf(cfg, l, 29, "cpu").items()})
+                                 vocab_size=1024, expert_format=fmt)
+        packed = [Q.pack_layer({k: v.to(dev) for k, v in Q.random_layer_hf(cfg, l, 29, "cpu").items()}, fmt)
                   for l in range(2)]
         gg = torch.Generator().manual_seed(29)
         embed = (torch.randn(1024, cfg.hidden_size, generator=gg) * 0.5).to(torch.bfloat16).to(dev)
