@@ -308,10 +308,26 @@ typedef struct {
   /* Device copy of the per-layer pointers (mkd_qwen3_write_layer_table), read by
    * the persistent decode path; NULL: that path is not used.                   */
   const void* layer_table;
+  /* Routing log (no counterpart in the reference, whose router outputs stay on
+   * chip): when set, every decode / prefill call writes, for each layer l and
+   * each of its B tokens, what that layer's router actually produced, at
+   * route_log + l * stride (layout from mkd_qwen3_route_log_layout):
+   *   idx    int32 [B][K]  expert indices in rank order (as used by the experts)
+   *   w      fp32  [B][K]  routing weights of those slots
+   *   logits fp32  [B][E]  router logits (bias included) the top-k ran on
+   *   r      bf16  [B][H]  the post-attention residual the router norm read
+   * route_log_bytes must be >= mkd_qwen3_route_log_bytes(m, B).  NULL: no log. */
+  void* route_log;
+  size_t route_log_bytes;
 } mkd_qwen3_model;
 #define MKD_VARIANT_QWEN3 0
 #define MKD_VARIANT_GPT_OSS 1
 size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B);
+/* Routing log for B tokens per call: total bytes (all layers), and the byte
+ * offsets of the idx / w / logits / r arrays inside one layer's record and the
+ * record stride (offsets[0..4] = idx, w, logits, r, stride). */
+size_t mkd_qwen3_route_log_bytes(const mkd_qwen3_model* m, int B);
+int mkd_qwen3_route_log_layout(const mkd_qwen3_model* m, int B, size_t* offsets);
 /* hidden [B, H] bf16 in/out; position_ids [B] int32 (device); cos/sin [B, d]
  * fp32 or NULL (then generated from position_ids and inv_freq). */
 int mkd_qwen3_decode_layers(const mkd_qwen3_model* m, int B, void* hidden,

@@ -86,7 +86,7 @@ class Qwen3Model(C.Structure):
         ("sinks", C.POINTER(vp)), ("router_bias", C.POINTER(vp)), ("gate_up_bias", C.POINTER(vp)),
         ("down_bias", C.POINTER(vp)), ("window", C.POINTER(i32)), ("layer_s_max", C.POINTER(i32)),
         ("act_alpha", f32), ("gate_hi", f32), ("gate_lo", f32), ("up_hi", f32), ("up_lo", f32),
-        ("layer_table", vp),
+        ("layer_table", vp), ("route_log", vp), ("route_log_bytes", sz),
     ]
 
 
@@ -110,6 +110,8 @@ _SIGS = {
     "mkd_attention_workspace_bytes": (sz, [i32, i32, i32, i32, i32, i32]),
     "mkd_attention_block_tkg": (i32, [C.POINTER(AttentionArgs), vp, sz, vp]),
     "mkd_qwen3_workspace_bytes": (sz, [C.POINTER(Qwen3Model), i32]),
+    "mkd_qwen3_route_log_bytes": (sz, [C.POINTER(Qwen3Model), i32]),
+    "mkd_qwen3_route_log_layout": (i32, [C.POINTER(Qwen3Model), i32, C.POINTER(sz)]),
     "mkd_qwen3_decode_layers": (i32, [C.POINTER(Qwen3Model), i32, vp, vp, vp, vp, vp, sz, vp]),
     "mkd_qwen3_prefill_layers": (i32, [C.POINTER(Qwen3Model), i32, i32, vp, vp, vp, vp, vp, sz, vp]),
     "mkd_embed": (i32, [vp, vp, vp, i32, i32, i32, vp]),

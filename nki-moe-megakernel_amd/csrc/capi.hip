@@ -964,6 +964,11 @@ static int decode_layers_lk(const mkd_qwen3_model* m, int B, uint16_t* x, const 
   L.router_mode = MKD_ROUTER_QWEN;
   L.lds_a = p.lds_a; L.lds_b = p.lds_b; L.lds_c = p.lds_c; L.lds_s = p.lds_s;
   L.lds_total = p.lds_total;
+  if (m->route_log) {
+    const RouteLogLayout lo = route_log_layout(B, m->E, m->K, m->H);
+    L.route_log = static_cast<char*>(m->route_log);
+    L.log_stride = lo.stride; L.log_w = lo.w; L.log_logits = lo.logits; L.log_r = lo.r;
+  }
   const int ps = prof_begin(MKD_KCLASS_LAYER, s);
   MKD_TRY(layer_kernel_launch(L, s), "persistent decode kernel");
   prof_end(ps, s);
@@ -1016,6 +1021,11 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
   Carver c{static_cast<char*>(workspace), workspace_bytes};
   StepWs w = carve_step(c, m, B);
   MKD_REQUIRE(c.ok, MKD_ERR_WORKSPACE, "decode_layers: workspace %zu < %zu bytes", workspace_bytes, c.used);
+  if (m->route_log)
+    MKD_REQUIRE(m->route_log_bytes >= mkd_qwen3_route_log_bytes(m, B), MKD_ERR_WORKSPACE,
+                "decode_layers: route log %zu < %zu bytes", m->route_log_bytes,
+                mkd_qwen3_route_log_bytes(m, B));
+  const RouteLogLayout rlo = route_log_layout(B, m->E, m->K, m->H);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (!cos) {
     MKD_TRY(rope_table_launch(position_ids, m->inv_freq, B, m->d, w.cos, w.sin, s), "rope table");
@@ -1112,6 +1122,12 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
     ra.T = B; ra.E = m->E; ra.K = m->K; ra.mode = oss ? 0 : MKD_ROUTER_QWEN;
     ra.bias = static_cast<const uint16_t*>(at(m->router_bias, l));
     ra.idx_out = w.moe.idx; ra.slot_w = w.moe.slot_w;
+    char* rec = m->route_log ? static_cast<char*>(m->route_log) + (size_t)l * rlo.stride : nullptr;
+    if (rec) {   // this layer's routing record
+      ra.idx_out = reinterpret_cast<int*>(rec + rlo.idx);
+      ra.topk_out = reinterpret_cast<float*>(rec + rlo.w);
+      ra.logits_out = reinterpret_cast<float*>(rec + rlo.logits);
+    }
     ra.n_groups = w.moe.n_groups; ra.grp_expert = w.moe.grp_expert;
     ra.grp_count = w.moe.grp_count; ra.grp_offset = w.moe.grp_offset;
     ra.pair_token = w.moe.pair_token; ra.pair_slot = w.moe.pair_slot;
@@ -1171,10 +1187,13 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
       }
       prof_end(ps, s);
     }
+    if (rec)   // the post-attention residual the router norm read
+      MKD_TRY(hipMemcpyAsync(rec + rlo.r, w.r, (size_t)B * m->H * 2, hipMemcpyDeviceToDevice, s),
+              "route log residual");
     // > 128 tokens (prefill): groups from the indices, and with bf16 experts the
     // LDS-tiled grouped GEMMs (tens of tokens per expert)
     const bool long_pass = B > 128;
-    if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], long_pass ? w.moe.idx : nullptr, w.moe.slot_w,
+    if (int rc = moe_core(w.nbf, m->gate_up[l], m->down[l], long_pass ? ra.idx_out : nullptr, w.moe.slot_w,
                           static_cast<const uint16_t*>(at(m->gate_up_bias, l)),
                           static_cast<const uint16_t*>(at(m->down_bias, l)), w.r, x, nullptr, B,
                           m->H, m->E, m->I, m->K, oss ? MKD_ACT_SWISH : MKD_ACT_SILU,
@@ -1305,6 +1324,20 @@ int mkd_profile_events(int kernel_class, void* const* start_events, void* const*
 }
 
 int mkd_profile_count(void) { return g_prof.next; }
+
+size_t mkd_qwen3_route_log_bytes(const mkd_qwen3_model* m, int B) {
+  if (!m || m->num_layers <= 0 || B <= 0) return 0;
+  return (size_t)route_log_layout(B, m->E, m->K, m->H).stride * (size_t)m->num_layers;
+}
+
+int mkd_qwen3_route_log_layout(const mkd_qwen3_model* m, int B, size_t* offsets) {
+  MKD_REQUIRE(m && offsets, MKD_ERR_NULL, "route_log_layout: null pointer");
+  MKD_REQUIRE(B > 0, MKD_ERR_INVALID, "route_log_layout: B must be > 0");
+  const RouteLogLayout lo = route_log_layout(B, m->E, m->K, m->H);
+  offsets[0] = (size_t)lo.idx; offsets[1] = (size_t)lo.w; offsets[2] = (size_t)lo.logits;
+  offsets[3] = (size_t)lo.r; offsets[4] = (size_t)lo.stride;
+  return MKD_OK;
+}
 
 size_t mkd_qwen3_layer_table_bytes(const mkd_qwen3_model* m) {
   return m && m->num_layers > 0 ? sizeof(LkLayer) * (size_t)m->num_layers : 0;

@@ -1059,6 +1059,8 @@ __global__ void __launch_bounds__(kThreads) layer_kernel(LayerArgs L) {
             rvs[c][j] = pack2bf(r0, r1);
           }
           *reinterpret_cast<u32x4_t*>(xs + i) = rvs[c];
+          if (L.route_log && blk == 0)
+            st16(L.route_log + (long long)l * L.log_stride + L.log_r + (long long)i * 2, rvs[c]);
 #pragma unroll
           for (int q = 0; q < kLkMaxB; ++q)
             if (q == t) ss[q] += a;
@@ -1118,6 +1120,12 @@ __global__ void __launch_bounds__(kThreads) layer_kernel(LayerArgs L) {
       ra.grp_offset = sel->goff;
       ra.pair_token = sel->ptok;
       ra.pair_slot = sel->pslot;
+      if (L.route_log && blk == 0) {       // the routing record of this layer
+        char* rec = L.route_log + (long long)l * L.log_stride;
+        ra.idx_out = reinterpret_cast<int*>(rec);
+        ra.topk_out = reinterpret_cast<float*>(rec + L.log_w);
+        ra.logits_out = reinterpret_cast<float*>(rec + L.log_logits);
+      }
       select_small<PER>(ra, [&](int t, float (&lg)[PER]) {
 #pragma unroll
         for (int j = 0; j < PER; ++j) {

@@ -140,7 +140,25 @@ struct LayerArgs {
   unsigned* bar;                    // kLkBarWords barrier words
   int router_mode;                  // MKD_ROUTER_* bits
   int lds_a, lds_b, lds_c, lds_s, lds_total;   // dynamic LDS carve (bytes)
+  char* route_log;                  // per-layer routing records (RouteLogLayout) or null
+  long long log_stride, log_w, log_logits, log_r;
 };
+
+// One layer's routing record: idx int32 [B][K], w fp32 [B][K], logits fp32
+// [B][E], r bf16 [B][H], each 256-byte aligned; `stride` bytes per layer.
+struct RouteLogLayout {
+  long long idx, w, logits, r, stride;
+};
+inline RouteLogLayout route_log_layout(int B, int E, int K, int H) {
+  auto up = [](long long n) { return (n + 255) / 256 * 256; };
+  RouteLogLayout o;
+  o.idx = 0;
+  o.w = o.idx + up(4LL * B * K);
+  o.logits = o.w + up(4LL * B * K);
+  o.r = o.logits + up(4LL * B * E);
+  o.stride = o.r + up(2LL * B * H);
+  return o;
+}
 constexpr int kLkBarriers = 7;      // grid barriers per layer
 constexpr int kLkSelBytes = 4096;   // LDS of the selection results and small per-wave scratch
 constexpr int kLkStaticLds = 1024;  // static LDS of the kernel (router select_small), bound

@@ -32,7 +32,8 @@ from torch import nn
 
 from . import _lib as L
 from . import packing
-from .qwen_with_megakernel import EXPERT_FORMATS, _prefill, pack_experts_mx, randn_bf16, tensor_seed
+from .qwen_with_megakernel import (EXPERT_FORMATS, _LayerStack, _prefill, pack_experts_mx, randn_bf16,
+                                   tensor_seed)
 
 VARIANT_GPT_OSS = 1
 
@@ -221,7 +222,7 @@ class GptOssKVCache:
         return self.past_key_values[2 * l + 1]
 
 
-class GptOssMegakernelModel(nn.Module):
+class GptOssMegakernelModel(_LayerStack, nn.Module):
     """GPT-OSS decoder stack + decode-step epilogue on the MI355X library."""
 
     def __init__(self, cfg: GptOssMKConfig, layers: List[PackedGptOssLayer], batch: int, device,
@@ -295,8 +296,9 @@ class GptOssMegakernelModel(nn.Module):
             return cos, sin
         return c, s
 
-    def decode_layers(self, hidden: torch.Tensor, position_ids: torch.Tensor):
-        """All layers in place on hidden [B, hidden_pad] bf16 (padded columns zero)."""
+    def decode_layers(self, hidden: torch.Tensor, position_ids: torch.Tensor, layers=None):
+        """All layers (or the range `layers` = (lo, hi)) in place on hidden [B, hidden_pad]
+        bf16 (padded columns zero)."""
         B = hidden.shape[0]
         if B > self.batch:
             raise ValueError(f"batch {B} exceeds the configured max batch {self.batch}")
@@ -307,7 +309,7 @@ class GptOssMegakernelModel(nn.Module):
             raise ValueError("position_ids must be int32")
         cos, sin = self.rope_cos_sin(pos, self.cos[:B], self.sin[:B])
         rc = L.load().mkd_qwen3_decode_layers(
-            self._model, B, hidden.data_ptr(), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+            self._struct_for(layers), B, hidden.data_ptr(), pos.data_ptr(), cos.data_ptr(), sin.data_ptr(),
             self.ws.data_ptr(), self.ws.numel(), L.stream_ptr(self.device))
         L.check(rc, "gpt_oss decode_layers")
         return hidden

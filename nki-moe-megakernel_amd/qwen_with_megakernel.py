@@ -232,7 +232,91 @@ class KVCacheManager:
         return self.past_key_values[2 * l + 1]
 
 
-class Qwen3MoeMegakernelModel(nn.Module):
+_PTR_FIELDS = ("w_qkv", "w_o", "q_norm", "k_norm", "ln_in", "ln_post", "router", "gate_up", "down",
+               "k_cache", "v_cache", "gate_up_scales", "down_scales", "b_qkv", "b_o", "sinks",
+               "router_bias", "gate_up_bias", "down_bias")
+
+
+class _LayerStack:
+    """Shared by the Qwen3 and GPT-OSS models: a view of a contiguous range of
+    the layers, and the routing log (what each layer's router produced)."""
+
+    def _struct_for(self, layers):
+        """The model struct, or a copy covering layers [lo, hi) only (host pointer
+        arrays offset to lo; the persistent path's device table is left out)."""
+        if layers is None:
+            return self._model
+        lo, hi = layers
+        n = self._model.num_layers
+        if not 0 <= lo < hi <= n:
+            raise ValueError(f"layer range {layers} outside [0, {n})")
+        sub = L.Qwen3Model()
+        C.memmove(C.addressof(sub), C.addressof(self._model), C.sizeof(sub))
+        sub.num_layers = hi - lo
+        vsz = C.sizeof(L.vp)
+        for f in _PTR_FIELDS:
+            arr = getattr(self._model, f)
+            if arr:
+                setattr(sub, f, C.cast(C.cast(arr, C.c_void_p).value + lo * vsz, C.POINTER(L.vp)))
+        for f in ("window", "layer_s_max"):
+            arr = getattr(self._model, f)
+            if arr:
+                setattr(sub, f, C.cast(C.cast(arr, C.c_void_p).value + lo * C.sizeof(C.c_int),
+                                       C.POINTER(C.c_int)))
+        sub.layer_table = None
+        if self._model.route_log:
+            stride = self._route_log_offsets(self._route_log_batch)[4]
+            sub.route_log = self._model.route_log + lo * stride
+            sub.route_log_bytes = self._model.route_log_bytes - lo * stride
+        return sub
+
+    def _route_log_offsets(self, B):
+        offs = (C.c_size_t * 5)()
+        L.check(L.load().mkd_qwen3_route_log_layout(self._model, B, offs), "route_log_layout")
+        return list(offs)
+
+    def enable_route_log(self, batch: Optional[int] = None):
+        """Record, per layer, the expert indices / weights / router logits and the
+        post-attention residual of every decode call of up to `batch` tokens (the
+        record layout follows the batch of each call).  Capture a step graph after
+        this call for the graph to record too."""
+        B = batch or self.batch
+        n = L.load().mkd_qwen3_route_log_bytes(self._model, B)
+        self._route_log = torch.zeros(n, dtype=torch.uint8, device=self.device)
+        self._route_log_batch = B
+        self._model.route_log = self._route_log.data_ptr()
+        self._model.route_log_bytes = n
+
+    def disable_route_log(self):
+        self._model.route_log = None
+        self._model.route_log_bytes = 0
+        self._route_log = None
+
+    def route_log(self, B: int):
+        """Per-layer routing records of the last call of B tokens (synchronises):
+        a list of dicts idx [B, K] int32, w [B, K] fp32, logits [B, E] fp32,
+        r [B, H] bf16 (CPU tensors)."""
+        if getattr(self, "_route_log", None) is None:
+            raise ValueError("enable_route_log() first")
+        o_idx, o_w, o_lg, o_r, stride = self._route_log_offsets(B)
+        m = self._model
+        K, E, H = m.K, m.E, m.H
+        buf = self._route_log.cpu()
+        out = []
+        for l in range(m.num_layers):
+            b = l * stride
+            if b + stride > buf.numel():
+                break
+            out.append({
+                "idx": buf[b + o_idx: b + o_idx + 4 * B * K].view(torch.int32).reshape(B, K).clone(),
+                "w": buf[b + o_w: b + o_w + 4 * B * K].view(torch.float32).reshape(B, K).clone(),
+                "logits": buf[b + o_lg: b + o_lg + 4 * B * E].view(torch.float32).reshape(B, E).clone(),
+                "r": buf[b + o_r: b + o_r + 2 * B * H].view(torch.bfloat16).reshape(B, H).clone(),
+            })
+        return out
+
+
+class Qwen3MoeMegakernelModel(_LayerStack, nn.Module):
     """Decoder stack + decode-step epilogue on the MI355X library."""
 
     def __init__(self, cfg: Qwen3MoeMKConfig, layers: List[PackedLayer], batch: int, device,
@@ -301,8 +385,10 @@ class Qwen3MoeMegakernelModel(nn.Module):
         return emb.cos(), emb.sin()
 
     def decode_layers(self, hidden: torch.Tensor, position_ids: torch.Tensor,
-                      cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None):
-        """Run all layers in place on hidden [B, H] bf16 (the multilayer kernel call)."""
+                      cos: Optional[torch.Tensor] = None, sin: Optional[torch.Tensor] = None,
+                      layers=None):
+        """Run all layers (or the range `layers` = (lo, hi)) in place on hidden [B, H]
+        bf16 (the multilayer kernel call)."""
         B = hidden.shape[0]
         if B > self.batch:
             raise ValueError(f"batch {B} exceeds the configured max batch {self.batch}")
@@ -312,7 +398,7 @@ class Qwen3MoeMegakernelModel(nn.Module):
         if pos.dtype != torch.int32:
             raise ValueError("position_ids must be int32")
         rc = L.load().mkd_qwen3_decode_layers(
-            self._model, B, hidden.data_ptr(), pos.data_ptr(), L.ptr(cos), L.ptr(sin),
+            self._struct_for(layers), B, hidden.data_ptr(), pos.data_ptr(), L.ptr(cos), L.ptr(sin),
             self.ws.data_ptr(), self.ws.numel(), L.stream_ptr(self.device))
         L.check(rc, "qwen3_decode_layers")
         return hidden

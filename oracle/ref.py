@@ -112,7 +112,8 @@ def router_topk(x: torch.Tensor, w: torch.Tensor, w_bias: Optional[torch.Tensor]
     return logits, idx, aff, vals
 
 
-def qwen_router(x_f32: torch.Tensor, w_he: torch.Tensor, k: int, emulate_bf16: bool = True):
+def qwen_router(x_f32: torch.Tensor, w_he: torch.Tensor, k: int, emulate_bf16: bool = True,
+                force_idx: Optional[torch.Tensor] = None):
     """Qwen fused router (megakernels/qwen3_moe/moe_fused_nki.py:159-276, 404-418).
 
     fp32 normed input x [T, H], router weight [H, E] (bf16 values, fp32 math).
@@ -122,10 +123,26 @@ def qwen_router(x_f32: torch.Tensor, w_he: torch.Tensor, k: int, emulate_bf16: b
     bf16 values, reciprocal, product rounded to bf16 (:404-418).
     Returns (logits fp32 [T,E], idx [T,k], weights [T,k] fp32 holding bf16 values).
     """
-    logits = x_f32.float() @ w_he.float()
+    return qwen_router_from_logits(x_f32.float() @ w_he.float(), k, emulate_bf16, force_idx)
+
+
+def qwen_router_from_logits(logits: torch.Tensor, k: int, emulate_bf16: bool = True,
+                            force_idx: Optional[torch.Tensor] = None):
+    """The selection and weights of ``qwen_router`` given its fp32 logits [T, E]
+    (moe_fused_nki.py:241-272, 404-418).  Returns (logits, idx [T,k], weights [T,k]).
+
+    ``force_idx`` [T, k] replaces the top-k selection by the given experts (in
+    that rank order); the weights are then the same formula at those experts.
+    Tests use it to compare the continuous math of two flows whose routing a
+    near-tie decided differently (the selection itself is checked separately)."""
+    logits = logits.float()
     m = logits.max(-1, keepdim=True).values
     inv = 1.0 / torch.exp(logits - m).sum(-1, keepdim=True)
-    top, idx = stable_topk(logits, k)
+    if force_idx is not None:
+        idx = force_idx.long()
+        top = torch.gather(logits, -1, idx)
+    else:
+        top, idx = stable_topk(logits, k)
     vals = _bf(torch.exp(top - m) * inv, emulate_bf16)
     s = vals.sum(-1, keepdim=True)
     w = _bf(vals * (1.0 / s), emulate_bf16)
@@ -421,7 +438,7 @@ class QwenLayer:
 def qwen_decoder_layer(x_bf: torch.Tensor, lw: QwenLayer, k_cache: torch.Tensor,
                        v_cache: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                        pos: torch.Tensor, shape: QwenShape, emulate_bf16: bool = True,
-                       mx_experts: bool = False):
+                       mx_experts: bool = False, force_idx: Optional[torch.Tensor] = None):
     """Residual stream in bf16 (transformer_qwen.py:117-127, adds :332, :371).
 
     Pre-attn RMSNorm is fused in attention as (x*rinv)*gamma -> bf16
@@ -430,6 +447,8 @@ def qwen_decoder_layer(x_bf: torch.Tensor, lw: QwenLayer, k_cache: torch.Tensor,
     (moe_fused_nki.py:70-153).  mx_experts: lw.gate_up / lw.down hold the
     dequantised MX expert weights and the experts follow moe_tkg_mx (MXFP8
     activations) with the router's top-k weights as POST scales.
+    force_idx [B, K]: route to these experts instead of the top-k (weights from
+    the router formula at them; see qwen_router_from_logits).
     Returns (x_out, aux dict).
     """
     bf = lambda t: _bf(t, emulate_bf16)
@@ -442,7 +461,7 @@ def qwen_decoder_layer(x_bf: torch.Tensor, lw: QwenLayer, k_cache: torch.Tensor,
     r = bf(x + attn)
     n32 = rmsnorm_tkg(r, lw.ln_post, shape.eps)
     n_bf = bf(n32)
-    logits, idx, w = qwen_router(n32, lw.router.float().t(), shape.K, emulate_bf16)
+    logits, idx, w = qwen_router(n32, lw.router.float().t(), shape.K, emulate_bf16, force_idx)
     if mx_experts:
         aff = torch.zeros(logits.shape).scatter_(1, idx, w)
         moe = bf(moe_tkg_mx(n_bf, lw.gate_up, lw.down, aff, idx, scaling_mode="post"))
@@ -612,7 +631,8 @@ def gpt_oss_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch
 def gpt_oss_decoder_layer(x_bf: torch.Tensor, lw: GptOssLayer, k_cache: torch.Tensor,
                           v_cache: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
                           pos: torch.Tensor, window: int, shape: GptOssShape,
-                          mx_experts: bool = False, emulate_bf16: bool = True):
+                          mx_experts: bool = False, emulate_bf16: bool = True,
+                          force_idx: Optional[torch.Tensor] = None):
     """One decode token per sequence; residual in bf16 (transformer_gpt_oss.py:358-519).
 
     x [B, H] (bf16 values, unpadded H); caches [B, nkv, S, d] bf16, updated in
@@ -629,7 +649,9 @@ def gpt_oss_decoder_layer(x_bf: torch.Tensor, lw: GptOssLayer, k_cache: torch.Te
     over k (HF GptOssExperts).  mx_experts: the expert weights given are
     dequantised MX and the activations go through MXFP8 before each projection
     (as moe_tkg_mx).  emulate_bf16=False drops every bf16 rounding point (the
-    plain fp32 math the HF pin checks).  Returns (x_out [B, H], aux).
+    plain fp32 math the HF pin checks).  force_idx [B, K]: route to these
+    experts (softmax over their logits) instead of the top-k.  Returns
+    (x_out [B, H], aux).
     """
     bf = lambda t: _bf(t, emulate_bf16)
     B, H = x_bf.shape
@@ -666,7 +688,11 @@ def gpt_oss_decoder_layer(x_bf: torch.Tensor, lw: GptOssLayer, k_cache: torch.Te
     r = bf(x + o)
     n = bf(rmsnorm_tkg(r, lw.ln_post, shape.eps))
     logits = n @ lw.router_w.float().t() + lw.router_b.float()
-    top, idx = stable_topk(logits, shape.K)
+    if force_idx is not None:
+        idx = force_idx.long()
+        top = torch.gather(logits, -1, idx)
+    else:
+        top, idx = stable_topk(logits, shape.K)
     w = torch.softmax(top, -1)
     xin = mx_qdq(n) if mx_experts else n
     moe = torch.zeros(B, H)

@@ -81,13 +81,23 @@ def test_layer_kernel_vs_oracle_and_multi_kernel(mk, dev, persistent, B, S):
         p = int(pos[b])
         for new, old, other in ((k1, kc, k2), (v1, vc, v2)):
             changed = (new[b] != old[b]).any(-1).any(0).nonzero().flatten().tolist()
-            assert changed in ([p], [])
+            assert changed == [p], (b, p, changed[:8])
             assert max_abs_rel(new[b, :, p], other[b, :, p]) < TOL
 
 
 def test_layer_kernel_three_layers_one_launch(mk, dev, persistent):
     """Three full-shape layers in one persistent launch (the rows stay in LDS
-    between layers) vs the oracle applied layer by layer and the multi-kernel path."""
+    between layers) vs the oracle applied layer by layer and the multi-kernel path.
+
+    Each path's routing log is checked layer by layer (selection exact on its own
+    logits; oracle router on its own residual, near-ties < 1e-4 excepted) and the
+    oracle chain is routed to the experts that path chose: over chained layers
+    the residuals of the GPU and of the oracle differ by bf16 rounding (~5e-3),
+    and a near-tie at the 8th expert then picks a different expert, which moves
+    that token by ~2-3e-2 -- measured, a discrete flip rather than accumulated
+    rounding (the oracle's own bf16 and fp32 flows stay within 7e-3 over these
+    three layers)."""
+    from routing_checks import check_oracle_flips, check_qwen_routing
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
     B, S, Ln = 2, 512, 3
     cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=Ln, max_batch=B, max_seq=S)
@@ -99,6 +109,7 @@ def test_layer_kernel_three_layers_one_launch(mk, dev, persistent):
     vc = [bf(torch.randn(B, 4, S, 128, generator=g)) for _ in range(Ln)]
     layers = [Q.pack_layer({k: v.to(dev) for k, v in h.items()}, cfg.expert_format) for h in hf]
     model = Q.Qwen3MoeMegakernelModel(cfg, layers, B, dev)
+    model.enable_route_log(B)
     assert model.layer_kernel_status(B)[0]
 
     def run():
@@ -108,29 +119,36 @@ def test_layer_kernel_three_layers_one_launch(mk, dev, persistent):
         y = x.to(dev).contiguous()
         model.decode_layers(y, pos.to(dev))
         torch.cuda.synchronize()
-        return y.cpu(), [model.kv_mgr.k(l).cpu() for l in range(Ln)]
+        return y.cpu(), [model.kv_mgr.k(l).cpu() for l in range(Ln)], model.route_log(B)
 
-    y1, k1 = run()
+    y1, k1, log1 = run()
     assert not model.layer_kernel_status(B)[1]
     Q.set_decode_path("multi_kernel")
     try:
-        y2, k2 = run()
+        y2, k2, log2 = run()
     finally:
         Q.set_decode_path("persistent")
     cos, sin = ref.rope_cos_sin(pos, 128, cfg.rope_theta)
-    y_ref = x.float()
-    for l in range(Ln):
-        y_ref, _ = ref.qwen_decoder_layer(y_ref, _ref_layer(hf[l]), kc[l].clone(), vc[l].clone(), cos, sin,
-                                          pos, ref.QwenShape())
-    # The 2e-2 bar is per teacher-forced layer (the single-layer tests above);
-    # over 3 chained layers bf16 rounding differences compound (measured: both
-    # GPU paths ~2.5e-2 from the oracle, ~7e-3 apart), so the chain is held to
-    # 2e-2 against the per-layer-validated multi-kernel path and 4e-2 against
-    # the oracle.
-    e1, e2, e12 = max_abs_rel(y1, y_ref), max_abs_rel(y2, y_ref), max_abs_rel(y1, y2)
-    print(f"persistent vs oracle {e1:.4f}, multi-kernel vs oracle {e2:.4f}, between {e12:.4f}", flush=True)
-    assert e12 < TOL
-    assert e1 < 2 * TOL
+
+    def oracle_chain(logs):
+        y, own = x.float(), 0
+        for l in range(Ln):
+            lw = _ref_layer(hf[l])
+            check_qwen_routing(logs[l], lw, 1e-6, 8)
+            y_in = y
+            y, aux = ref.qwen_decoder_layer(y_in, lw, kc[l].clone(), vc[l].clone(), cos, sin, pos,
+                                            ref.QwenShape(), force_idx=logs[l]["idx"].long())
+            own += check_oracle_flips(logs[l]["idx"], logs[l]["logits"], aux["logits"], 8)[0]
+        return y, own
+
+    y_ref1, f1 = oracle_chain(log1)
+    y_ref2, f2 = oracle_chain(log2)
+    e1, e2, e12 = max_abs_rel(y1, y_ref1), max_abs_rel(y2, y_ref2), max_abs_rel(y1, y2)
+    print(f"persistent vs oracle {e1:.4f}, multi-kernel vs oracle {e2:.4f}, between {e12:.4f}; "
+          f"near-tie flips against the oracle's own routing: {f1}, {f2}", flush=True)
+    assert e1 < TOL and e2 < TOL
+    if all(torch.equal(a["idx"], b["idx"]) for a, b in zip(log1, log2)):
+        assert e12 < TOL
     for l in range(Ln):
         for b in range(B):
             p = int(pos[b])

@@ -414,3 +414,32 @@ def test_gpt_oss_layer_oracle_matches_hf(pos, window):
                                      sin[0, pos][None, : d // 2], torch.tensor([pos]), window, shape,
                                      emulate_bf16=False)
     torch.testing.assert_close(y[0], y_hf[0, pos], rtol=2e-5, atol=2e-5)
+
+
+def test_forced_routing_identity_and_pairing():
+    """force_idx (routing teacher-forcing in the GPU tests): forcing the oracle's own
+    top-k reproduces it exactly; forcing the same experts in another rank order
+    gives the same layer output in the fp32 flow (each weight stays with its
+    expert; only the order of the fp32 sum over k changes)."""
+    t, meta = _load_golden()
+    lw, shape = golden_layer(t, meta)
+    cos, sin = ref.rope_cos_sin(t["pos"], shape.d, shape.theta)
+    x = t["x"].float()
+
+    def run(force, emulate):
+        return ref.qwen_decoder_layer(x, lw, t["k_cache"].float().clone(), t["v_cache"].float().clone(),
+                                      cos, sin, t["pos"], shape, emulate_bf16=emulate, force_idx=force)
+
+    for emulate in (True, False):
+        y0, aux = run(None, emulate)
+        y1, aux1 = run(aux["idx"], emulate)
+        assert torch.equal(y0, y1) and torch.equal(aux["w"], aux1["w"])
+    y0, aux = run(None, False)
+    perm = aux["idx"].flip(-1)
+    y2, aux2 = run(perm, False)
+    assert torch.allclose(y2, y0, rtol=0, atol=1e-5)
+    assert torch.allclose(aux2["w"], aux["w"].flip(-1), atol=1e-7)
+    # a different expert set moves the output
+    other = (aux["idx"] + 1) % shape.E
+    y3, _ = run(other, False)
+    assert (y3 - y0).abs().max() > 1e-3
