@@ -110,6 +110,17 @@ int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_pack
                     int* expert_index, float* topk_affinities, int k, int mode, void* workspace,
                     size_t workspace_bytes, void* stream);
 
+/* router_topk with no workspace argument.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments, outputs and errors as mkd_router_topk; the split-K partial logits
+ * go to a device array inside the library (2 MiB + 256 B per GPU, held until
+ * the process ends), which covers every shape mkd_router_topk accepts.  Calls
+ * that overlap in time on one GPU share that array and race. */
+int mkd_router_topk_static(const void* x, int x_dtype, int T, int H, const void* w_packed, int E,
+                           const void* w_bias, float* router_logits, float* expert_affinities,
+                           int* expert_index, float* topk_affinities, int k, int mode, void* stream);
+
 /* ---------------------------------------------------------------------------
  * MX (OCP Microscaling v1.0) formats -- the reference's MXFP8 / MXFP4 expert
  * path (selective_expert_mx_impl.py:60-531, down_projection_mx_shard_H.py:

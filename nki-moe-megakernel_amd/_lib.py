@@ -100,6 +100,7 @@ _SIGS = {
     "mkd_linear": (i32, [vp, i32, i32, i32, vp, i32, i32, vp, vp, i32, i32, vp, vp]),
     "mkd_router_workspace_bytes": (sz, [i32, i32, i32]),
     "mkd_router_topk": (i32, [vp, i32, i32, i32, vp, i32, vp, vp, vp, vp, vp, i32, i32, vp, sz, vp]),
+    "mkd_router_topk_static": (i32, [vp, i32, i32, i32, vp, i32, vp, vp, vp, vp, vp, i32, i32, vp]),
     "mkd_quantize_mx": (i32, [vp, i32, i32, i32, i32, i32, vp, vp, i32, vp]),
     "mkd_packed_mx_bytes": (sz, [i32, i32, i32, i32]),
     "mkd_packed_mx_scale_bytes": (sz, [i32, i32, i32]),

@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <mutex>
 #include <vector>
 
 #include "common.h"
@@ -480,6 +481,57 @@ int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_pack
   r.topk_out = topk_affinities;
   return router_stage(x, x_dtype == MKD_DT_F32, H, w_packed, static_cast<float*>(workspace), r,
                       static_cast<hipStream_t>(stream));
+}
+
+// ---- router_topk without a caller workspace (mkd_router_topk_static) ----
+// The split-K partial logits live in this file-scope device array instead.
+// Each GPU the library runs on holds its own copy (2 MiB + 256 B: router_kgrid
+// keeps K-slices x experts below 4096, so 128 tokens need less) until the process
+// ends; host code must use the per-device address from hipGetSymbolAddress,
+// never the array's name.  Every call on one GPU shares that GPU's copy, so
+// calls that overlap in time on one GPU race.  Every partial the router GEMM
+// writes covers all T x E outputs of its K slice, so nothing needs clearing.
+constexpr size_t kRouterScratchFloats = ((size_t)1 << 19) + 64;   // 4096 x 128 partials + 256 B
+static __device__ __align__(256) float scratch[kRouterScratchFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch`, looked up once per device.
+int router_scratch(float** out) {
+  int dev = -1;
+  MKD_TRY(hipGetDevice(&dev), "router_topk_static: hipGetDevice");
+  MKD_REQUIRE(dev >= 0 && dev < kMaxDevices, MKD_ERR_UNSUPPORTED,
+              "router_topk_static: device %d beyond %d", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    MKD_TRY(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "router_topk_static: hipGetSymbolAddress");
+    MKD_REQUIRE(p, MKD_ERR_HIP, "router_topk_static: no device address for the scratch array");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = static_cast<float*>(g_scratch_ptr[dev]);
+  return MKD_OK;
+}
+}  // namespace
+
+int mkd_router_topk_static(const void* x, int x_dtype, int T, int H, const void* w_packed, int E,
+                           const void* w_bias, float* router_logits, float* expert_affinities,
+                           int* expert_index, float* topk_affinities, int k, int mode, void* stream) {
+  if (int rc = stale_check("mkd_router_topk_static")) return rc;
+  MKD_REQUIRE(T > 0 && T <= 128, MKD_ERR_INVALID, "router_topk_static: T %d must be in [1, 128]", T);
+  MKD_REQUIRE(E > 0 && E <= 512, MKD_ERR_INVALID, "router_topk_static: E %d must be in [1, 512]", E);
+  MKD_REQUIRE(H > 0, MKD_ERR_INVALID, "router_topk_static: H %d must be > 0", H);
+  const size_t need = mkd_router_workspace_bytes(T, H, E);
+  MKD_REQUIRE(need <= sizeof(scratch), MKD_ERR_UNSUPPORTED,
+              "router_topk_static: T=%d H=%d E=%d needs %zu bytes of scratch, above the %zu-byte maximum",
+              T, H, E, need, sizeof(scratch));
+  float* parts = nullptr;
+  if (int rc = router_scratch(&parts)) return rc;
+  return mkd_router_topk(x, x_dtype, T, H, w_packed, E, w_bias, router_logits, expert_affinities,
+                         expert_index, topk_affinities, k, mode, parts, sizeof(scratch), stream);
 }
 
 size_t mkd_moe_workspace_bytes(int T, int H, int E, int I, int K) {

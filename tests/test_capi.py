@@ -77,3 +77,16 @@ def test_packed_cache_is_per_tensor_and_version(mk):
     del b
     gc.collect()
     assert ident not in packing._cache
+
+
+def test_router_static_scratch_covers_every_accepted_shape():
+    """mkd_router_topk_static's scratch (2 MiB + 256 B) holds the split-K partial
+    logits of every shape mkd_router_topk accepts (T <= 128, E <= 512)."""
+    from nki_moe_megakernel_amd import _lib as L
+    lib = L.load()
+    cap = (1 << 21) + 256
+    worst = 0
+    for E in range(1, 513):
+        for H in (32, 64, 96, 512, 1024, 2048, 2880, 3072, 4096, 8192):
+            worst = max(worst, lib.mkd_router_workspace_bytes(128, H, E))
+    assert worst <= cap, worst
