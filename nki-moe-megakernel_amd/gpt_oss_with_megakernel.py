@@ -340,21 +340,72 @@ class GptOssMegakernelModel(_LayerStack, nn.Module):
         return _prefill(self, input_ids, start_pos, seq, chunk, self.cfg.hidden_pad, self.cfg.hidden_size,
                         1, lambda pos: self.rope_cos_sin(pos))
 
-    def get_model_output(self, input_ids: torch.Tensor, position_ids: torch.Tensor):
-        """(norm(Y) [B, 1, H], [K0, V0, K1, V1, ...]) -- NeuronGptOssModelV1's return
-        (gpt_oss_with_megakernel.py:577-690); caches updated in place."""
-        B = input_ids.shape[0]
-        Hp = self.cfg.hidden_pad
-        hidden = torch.empty(B, Hp, dtype=torch.bfloat16, device=self.device)
-        L.check(L.load().mkd_embed(input_ids.to(torch.int32).contiguous().data_ptr(),
-                                   self.embed_tokens.data_ptr(), hidden.data_ptr(), B, Hp,
-                                   self.embed_tokens.shape[0], L.stream_ptr(self.device)), "embed")
-        self.decode_layers(hidden, position_ids.reshape(-1).to(torch.int32).contiguous())
+    def get_model_output(self, input_ids: Optional[torch.Tensor] = None, seq_ids=None,
+                         attention_mask=None, position_ids: Optional[torch.Tensor] = None,
+                         past_key_values=None, active_mask=None, inputs_embeds=None, prev_hidden=None,
+                         adapter_ids=None, rotary_position_ids=None, update_cache: bool = False,
+                         is_for_context_encoding: bool = False, vision_embeddings=None,
+                         vision_mask=None, deepstack_vision_embeds=None, local_attn_mask=None,
+                         windowed_context_encoding_window_idx: int = -1, padding_mask=None, **kwargs):
+        """NeuronGptOssModelV1.get_model_output (gpt_oss_with_megakernel.py:577-690):
+        embed (or inputs_embeds [B, S, H]) -> all layers -> final norm; returns
+        (norm(Y) [B, S, H], [K0, V0, K1, V1, ...]) with the caches updated in place.
+        Token generation (S = 1) runs the decode layers at position_ids [B, 1];
+        context encoding runs each sequence's S tokens at consecutive
+        position_ids (one token per pass: the sliding-window layers' ring rows).
+        As in the reference's TKG path, attention masks, active_mask,
+        past_key_values (the model's own caches are used), update_cache and
+        rotary_position_ids carry no extra information; LoRA adapters, vision
+        inputs, windowed context encoding and cache slots other than the batch
+        rows (seq_ids != arange(B)) are not supported."""
+        for name, v in (("adapter_ids", adapter_ids), ("vision_embeddings", vision_embeddings),
+                        ("vision_mask", vision_mask), ("deepstack_vision_embeds", deepstack_vision_embeds),
+                        ("local_attn_mask", local_attn_mask), ("prev_hidden", prev_hidden)):
+            if v is not None:
+                raise NotImplementedError(f"get_model_output: {name} is not supported")
+        if windowed_context_encoding_window_idx != -1:
+            raise NotImplementedError("get_model_output: windowed context encoding is not supported")
+        if position_ids is None:
+            raise ValueError("get_model_output needs position_ids")
+        cfg, Hp = self.cfg, self.cfg.hidden_pad
+        if inputs_embeds is not None:
+            B, S = inputs_embeds.shape[:2]
+        else:
+            ids = input_ids.reshape(input_ids.shape[0], -1)
+            B, S = ids.shape
+        if seq_ids is not None and not torch.equal(seq_ids.reshape(-1).cpu().long(), torch.arange(B)):
+            raise NotImplementedError("get_model_output: seq_ids must be arange(B) (batch row b is cache slot b)")
+        if B > self.batch:
+            raise ValueError(f"batch {B} exceeds the configured max batch {self.batch}")
+        hidden = torch.zeros(B * S, Hp, dtype=torch.bfloat16, device=self.device)
+        s = L.stream_ptr(self.device)
+        if inputs_embeds is not None:
+            hidden[:, : cfg.hidden_size] = inputs_embeds.reshape(B * S, -1)[:, : cfg.hidden_size].to(torch.bfloat16)
+        else:
+            L.check(L.load().mkd_embed(ids.reshape(-1).to(device=self.device, dtype=torch.int32).contiguous().data_ptr(),
+                                       self.embed_tokens.data_ptr(), hidden.data_ptr(), B * S, Hp,
+                                       self.embed_tokens.shape[0], s), "embed")
+        pos = position_ids.reshape(B, S).to(device=self.device, dtype=torch.int32)
+        if not is_for_context_encoding:
+            if S != 1:
+                raise NotImplementedError("token generation takes one token per sequence")
+            self.decode_layers(hidden, pos.reshape(-1).contiguous())
+        else:
+            from .qwen_with_megakernel import prefill_rows
+            hv = hidden.reshape(B, S, Hp)
+            pc = pos.cpu().long()
+            for b in range(B):
+                if not torch.equal(pc[b], torch.arange(int(pc[b, 0]), int(pc[b, 0]) + S)):
+                    raise NotImplementedError("context encoding needs consecutive position_ids")
+                for t in range(S):   # sliding-window ring rows: one token per pass
+                    row = hv[b, t:t + 1].contiguous()
+                    prefill_rows(self, row, int(pc[b, t]), b, rope=lambda p: self.rope_cos_sin(p))
+                    hv[b, t] = row[0]
         normed = torch.empty_like(hidden)
         L.check(L.load().mkd_rmsnorm_tkg(hidden.data_ptr(), L.DT_BF16, self.ln_f.data_ptr(),
-                                         normed.data_ptr(), L.DT_BF16, B, Hp, self.cfg.hidden_size,
-                                         self.cfg.rms_norm_eps, L.stream_ptr(self.device)), "final norm")
-        return normed[:, None, : self.cfg.hidden_size], list(self.kv_mgr.past_key_values)
+                                         normed.data_ptr(), L.DT_BF16, B * S, Hp, cfg.hidden_size,
+                                         cfg.rms_norm_eps, s), "final norm")
+        return normed.reshape(B, S, Hp)[:, :, : cfg.hidden_size], list(self.kv_mgr.past_key_values)
 
 
 NeuronGptOssForCausalLM = GptOssMegakernelModel

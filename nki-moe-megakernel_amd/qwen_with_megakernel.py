@@ -448,6 +448,35 @@ class Qwen3MoeMegakernelModel(_LayerStack, nn.Module):
         return logits, nxt
 
 
+def prefill_rows(model, hidden: torch.Tensor, start_pos: int, seq: int = 0, layers=None, rope=None):
+    """Context encoding of rows already embedded: hidden [T, H] bf16 (contiguous,
+    T <= 4096) holds consecutive tokens of sequence `seq` at positions start_pos ..
+    start_pos + T - 1 and is run through all layers (or the range `layers` =
+    (lo, hi)) in one pass, in place; those layers' cache rows are written.
+    `rope(pos)` gives the (cos, sin) tables or (None, None)."""
+    T = hidden.shape[0]
+    if hidden.dtype != torch.bfloat16 or not hidden.is_contiguous() or hidden.dim() != 2:
+        raise ValueError("hidden must be a contiguous bf16 [T, H] tensor")
+    if not 1 <= T <= 4096:
+        raise ValueError(f"{T} tokens per pass; the library takes 1..4096")
+    if not 0 <= seq < model.batch:
+        raise ValueError(f"sequence {seq} outside the model's {model.batch} cache slots")
+    if start_pos < 0 or start_pos + T > model.cfg.max_seq:
+        raise ValueError(f"{T} tokens at {start_pos} do not fit max_seq {model.cfg.max_seq}")
+    lib = L.load()
+    st = model._struct_for(layers)
+    ws = getattr(model, "_prefill_ws", None)
+    need = max(lib.mkd_qwen3_workspace_bytes(st, T), 256)
+    if ws is None or ws.numel() < need:
+        ws = model._prefill_ws = torch.zeros(need, dtype=torch.uint8, device=model.device)
+    pos = torch.arange(start_pos, start_pos + T, dtype=torch.int32, device=model.device)
+    cos, sin = rope(pos) if rope is not None else (None, None)
+    L.check(lib.mkd_qwen3_prefill_layers(st, seq, T, hidden.data_ptr(), pos.data_ptr(), L.ptr(cos),
+                                         L.ptr(sin), ws.data_ptr(), ws.numel(),
+                                         L.stream_ptr(model.device)), "qwen3_prefill_layers")
+    return hidden
+
+
 def _prefill(model, input_ids, start_pos, seq, chunk, H, h_actual, norm_order, rope):
     """Shared prefill loop of the Qwen3 and GPT-OSS models (same C entry point)."""
     if model.embed_tokens is None or model.lm_head_packed is None:
@@ -504,12 +533,13 @@ class Qwen3MoeDecoderLayerMK(nn.Module):
     def forward(self, hidden_states: torch.Tensor, attention_mask=None, position_ids=None,
                 past_key_value=None, padding_mask=None, kv_mgr=None, idx: int = 0,
                 is_for_context_encoding: bool = True, **kwargs):
-        if is_for_context_encoding:
-            raise NotImplementedError("context encoding (prefill) is outside the decode path")
         parent = self._parent_model
         kv_mgr = kv_mgr if kv_mgr is not None else parent.kv_mgr
         if kv_mgr is not parent.kv_mgr:
             raise ValueError("kv_mgr must be the model's KVCacheManager (its caches are bound to the step)")
+        if is_for_context_encoding:
+            return self._context_encoding(hidden_states, attention_mask, position_ids, kv_mgr,
+                                          kwargs.get("seq_ids"))
         Ln = self._num_hidden_layers
         if self.layer_idx == 0:
             B, S, H = hidden_states.shape
@@ -525,6 +555,43 @@ class Qwen3MoeDecoderLayerMK(nn.Module):
             return (y.reshape(B, S, H), (K_out[0], V_out[0]), cos[:, None, :], sin[:, None, :], None)
         K_out, V_out = parent._tkg_kv_out
         return (hidden_states, (K_out[self.layer_idx], V_out[self.layer_idx]), None, None, None)
+
+    def _context_encoding(self, hidden_states, attention_mask, position_ids, kv_mgr, seq_ids):
+        """CTE through this one layer, as the reference's stock layer path
+        (qwen_with_megakernel.py:496-526): hidden_states [B, S, H] -> this layer's
+        output for every token, the layer's cache rows of each sequence written.
+        Sequence b's tokens are the positions where attention_mask[b] (a [B, S]
+        0/1 padding mask, default all ones) is 1 -- one contiguous run at
+        consecutive position_ids [B, S]; padded slots pass through unchanged."""
+        parent = self._parent_model
+        B, S, H = hidden_states.shape
+        if position_ids is None:
+            raise ValueError("context encoding needs position_ids [B, S]")
+        pos = position_ids.reshape(B, S).to(torch.int64).cpu()
+        if attention_mask is not None and attention_mask.dim() == 2:
+            keep = attention_mask.reshape(B, S).to(torch.bool).cpu()
+        elif attention_mask is None:
+            keep = torch.ones(B, S, dtype=torch.bool)
+        else:
+            raise NotImplementedError("context encoding takes a [B, S] padding mask (causal masking is implied)")
+        seqs = seq_ids.reshape(-1).tolist() if seq_ids is not None else list(range(B))
+        y = hidden_states.to(torch.bfloat16).clone()
+        l = self.layer_idx
+        for b in range(B):
+            cols = keep[b].nonzero().flatten()
+            if cols.numel() == 0:
+                continue
+            c0, c1 = int(cols[0]), int(cols[-1]) + 1
+            if cols.numel() != c1 - c0:
+                raise NotImplementedError("each sequence's tokens must be one contiguous run")
+            p = pos[b, c0:c1]
+            if not torch.equal(p, torch.arange(int(p[0]), int(p[0]) + p.numel())):
+                raise NotImplementedError("context encoding needs consecutive position_ids")
+            rows = y[b, c0:c1].contiguous()
+            prefill_rows(parent, rows, int(p[0]), int(seqs[b]), layers=(l, l + 1))
+            y[b, c0:c1] = rows
+        cos, sin = parent.rope_cos_sin(pos.reshape(-1).to(torch.int32).to(parent.device))
+        return (y, (kv_mgr.k(l), kv_mgr.v(l)), cos.reshape(B, S, -1), sin.reshape(B, S, -1), None)
 
 
 # Alias mirroring the reference module's export (qwen_with_megakernel.py:728).

@@ -3,20 +3,26 @@ of one sequence in multi-token passes fills that sequence's KV cache and gives
 the last token's logits as the token-by-token decode step does (the reference's
 CTE layer path, qwen_with_megakernel.py:496-526, produces the same context the
 TKG path then reads).  Tolerance 2e-2 (max-abs error relative to the max-abs of
-the decode result): the two paths run the GEMMs at different token counts, so
-bf16 roundings differ; other sequences' caches are left bit-identical."""
+the reference result).  Against the CPU oracle the prompt is decoded token by
+token, routed like the GPU's routing log (the routing itself is checked against
+the oracle router on the GPU's residual); against the GPU decode path the two
+runs sum in different fp32 orders, so a router near-tie may route a token
+differently, which the tests allow only where the two runs' logits show it."""
 import pytest
 import torch
 
 from conftest import max_abs_rel
+from oracle import ref
+from prompt_oracle import qwen_prompt_chain, qwen_ref_layers
+from routing_checks import check_oracle_flips, check_qwen_routing
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
 
 
-def _qwen(dev, batch, kv_block=0, layers=2, seed=23):
+def _qwen(dev, batch, kv_block=0, layers=2, seed=23, max_seq=256):
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
-    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=layers, max_batch=batch, max_seq=256, vocab_size=1024,
+    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=layers, max_batch=batch, max_seq=max_seq, vocab_size=1024,
                              kv_block_len=kv_block)
     packed = [Q.pack_layer({k: v.to(dev) for k, v in Q.random_layer_hf(cfg, l, seed, "cpu").items()})
               for l in range(layers)]
@@ -24,7 +30,9 @@ def _qwen(dev, batch, kv_block=0, layers=2, seed=23):
     embed = (torch.randn(1024, cfg.hidden_size, generator=g) * 0.5).to(torch.bfloat16).to(dev)
     ln_f = (1 + 0.02 * torch.randn(cfg.hidden_size, generator=g)).to(torch.bfloat16).to(dev)
     lm = (0.02 * torch.randn(1024, cfg.hidden_size, generator=g)).to(torch.bfloat16).to(dev)
-    return Q.Qwen3MoeMegakernelModel(cfg, packed, batch, dev, embed=embed, ln_f=ln_f, lm_head=lm)
+    m = Q.Qwen3MoeMegakernelModel(cfg, packed, batch, dev, embed=embed, ln_f=ln_f, lm_head=lm)
+    m.test_lm_head = lm.cpu()
+    return m
 
 
 def _decode_seq1(m, ids, dev):
@@ -61,6 +69,45 @@ def test_qwen3_prefill_matches_token_by_token_decode(mk, dev, chunk):
         assert not ka[0].any() and not va[0].any()                   # other sequence untouched
 
 
+@pytest.mark.parametrize("T", [37, 300])
+def test_qwen3_prefill_matches_oracle_chain(mk, dev, T):
+    """One T-token pass (300: the > 128-token path -- router top-k on 16 tokens per
+    block, groups from the indices, LDS-tiled MFMA projections and experts)
+    against the oracle decoding the prompt token by token: every K/V row of both
+    layers and the last token's logits within 2e-2; each layer's routing exact
+    on the GPU's own logits and equal to the oracle router on the GPU's residual
+    except near-ties < 1e-4."""
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    print(f"qwen3 prefill T={T} vs the oracle chain", flush=True)
+    g = torch.Generator().manual_seed(40 + T)
+    ids = torch.randint(0, 1024, (T,), generator=g, dtype=torch.int32)
+    m = _qwen(dev, 1, max_seq=512)
+    m.enable_route_log(T)
+    lo, _ = m.prefill(ids.to(dev), start_pos=0, seq=0, chunk=T)
+    torch.cuda.synchronize()
+    logs = m.route_log(T)
+    hfs = [Q.random_layer_hf(m.cfg, l, 23, "cpu") for l in range(2)]
+    lws = qwen_ref_layers(hfs)
+    for l in range(2):
+        check_qwen_routing(logs[l], lws[l], 1e-6, 8)
+    S = m.cfg.max_seq
+    kcs = [torch.zeros(1, 4, S, 128) for _ in range(2)]
+    vcs = [torch.zeros(1, 4, S, 128) for _ in range(2)]
+    x = m.embed_tokens.cpu()[ids.long()]
+    y, aux = qwen_prompt_chain(x, lws, kcs, vcs, 0, ref.QwenShape(), logs=logs)
+    for l in range(2):
+        own = torch.cat([a["logits"] for a in aux[l]], 0)
+        flips, _ = check_oracle_flips(logs[l]["idx"], logs[l]["logits"], own, 8)
+        ka, va = m.kv_mgr.k(l).cpu()[0, :, :T], m.kv_mgr.v(l).cpu()[0, :, :T]
+        ek, ev = max_abs_rel(ka, kcs[l][0, :, :T]), max_abs_rel(va, vcs[l][0, :, :T])
+        print(f"  layer {l}: K rows {ek:.2e}, V rows {ev:.2e}; oracle's own top-k differs in {flips}/{T}",
+              flush=True)
+        assert ek < TOL and ev < TOL
+        assert not m.kv_mgr.k(l).cpu()[0, :, T:].any()
+    lg_ref, _ = ref.final_norm_lm_head(y[-1:], m.ln_f.cpu(), m.test_lm_head, m.cfg.rms_norm_eps)
+    assert max_abs_rel(lo.cpu(), lg_ref[0]) < TOL
+
+
 def test_qwen3_prefill_continues_into_decode_and_paged_matches_flat(mk, dev):
     """Prefill 20 tokens at position 0 then 9 more at position 20 == one 29-token
     prefill (to tolerance); the paged cache gives bit-identical logits to the flat
@@ -83,11 +130,15 @@ def test_qwen3_prefill_continues_into_decode_and_paged_matches_flat(mk, dev):
     assert max_abs_rel(outs[0][0], l1.cpu()) < TOL
 
 
-@pytest.mark.parametrize("T,short,fmt", [(300, 128, "bf16"), (1100, 512, "bf16"), (300, 128, "mxfp8")])
+@pytest.mark.parametrize("T,short,fmt", [(300, 128, "bf16"), (1100, 128, "bf16"), (300, 128, "mxfp8")])
 def test_qwen3_long_prefill_pass_matches_short_passes(mk, dev, T, short, fmt):
     """One T-token pass (router top-k on 16 tokens per block, expert groups from the
     indices, LDS-tiled MFMA expert / projection GEMMs) == passes of <= `short`
-    tokens (to tolerance), caches included."""
+    tokens on the streaming decode kernels (to tolerance), caches included.
+    Layer 0's rows depend on the embeddings only and must all match; a layer-1
+    row may differ only for a token whose layer-0 routing differs between the two
+    runs at a near-tie their own logits show (gap within twice the logit
+    difference of the runs)."""
     print(f"qwen3 prefill T={T} one pass vs passes of {short}, {fmt} experts", flush=True)
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
     g = torch.Generator().manual_seed(12)
@@ -104,24 +155,36 @@ def test_qwen3_long_prefill_pass_matches_short_passes(mk, dev, T, short, fmt):
         ln_f = (1 + 0.02 * torch.randn(cfg.hidden_size, generator=gg)).to(torch.bfloat16).to(dev)
         lm = (0.02 * torch.randn(1024, cfg.hidden_size, generator=gg)).to(torch.bfloat16).to(dev)
         m = Q.Qwen3MoeMegakernelModel(cfg, packed, 1, dev, embed=embed, ln_f=ln_f, lm_head=lm)
-        lo, _ = m.prefill(ids, start_pos=0, seq=0, chunk=chunk)
+        m.enable_route_log(T)
+        idx0, lg0 = [], []
+        for c0 in range(0, T, chunk):
+            n = min(chunk, T - c0)
+            lo, _ = m.prefill(ids[c0:c0 + n], start_pos=c0, seq=0, chunk=n)
+            rec = m.route_log(n)[0]
+            idx0.append(rec["idx"])
+            lg0.append(rec["logits"])
         torch.cuda.synchronize()
-        outs.append((lo.cpu(), [m.kv_mgr.k(l).cpu() for l in range(2)], [m.kv_mgr.v(l).cpu() for l in range(2)]))
-    (la, ka, va), (lb, kb, vb) = outs
+        outs.append((lo.cpu(), [m.kv_mgr.k(l).cpu() for l in range(2)], [m.kv_mgr.v(l).cpu() for l in range(2)],
+                     torch.cat(idx0), torch.cat(lg0)))
+    (la, ka, va, ia, ga), (lb, kb, vb, ib, gb) = outs
     assert torch.isfinite(la).all()
     assert max_abs_rel(la, lb) < TOL
-    # per position: the two runs sum the expert GEMMs (tiled vs streaming) and the
-    # router inputs in different fp32 orders, so a token whose 8th / 9th router
-    # logits nearly tie (< 1e-4, the bar for router indices) may take another
-    # expert in layer 0 and carry different layer-1 K / V rows; at most 1 % of
-    # the positions may do so, every other row stays within the tolerance
+    # tokens whose layer-0 routing differs between the runs: near-ties only
+    dl = (ga - gb).abs().max().item()
+    order = torch.sort(-gb, dim=-1, stable=True).indices
+    differ = [t for t in range(T) if set(ia[t].tolist()) != set(ib[t].tolist())]
+    for t in differ:
+        kth = gb[t, order[t, 7]].item()
+        for e in set(ia[t].tolist()) - set(ib[t].tolist()):
+            assert kth - gb[t, e].item() <= 2 * dl + 1e-6, (t, e, kth, dl)
+    print(f"layer-0 routing differs at {differ} (logit difference of the runs {dl:.1e})", flush=True)
     for l in range(2):
         for new, old in ((ka[l][0], kb[l][0]), (va[l][0], vb[l][0])):
             scale = old[:, :T].abs().max()
             err = ((new[:, :T].float() - old[:, :T].float()).abs().amax(dim=(0, 2)) / scale)
             bad = (err >= TOL).nonzero().flatten().tolist()
             print(f"layer {l}: positions beyond tolerance {bad}", flush=True)
-            assert len(bad) <= (0 if l == 0 else T // 100)
+            assert set(bad) <= (set() if l == 0 else set(differ)), (bad, differ)
             assert not new[:, T:].any()
 
 
