@@ -88,7 +88,8 @@ int mkd_pack_weights(const void* src, void* dst, int groups, int n, int k, long 
  * output_projection_tkg, nki_kernels/attention/output_projection_tkg.py:66).
  * x [rows, k] (bf16, or fp32 for the router), w packed [n, k], bias [n] bf16
  * or NULL, y [rows, n] in y_dtype.  With `residual` (bf16 [rows, n], y_dtype
- * bf16) the result is bf16(residual + bf16(x @ W^T)).  rows <= 128.
+ * bf16) the result is bf16(residual + bf16(x @ W^T)).  rows <= 4096 (from 256
+ * rows, bf16 x and fp32 y without residual run on the LDS-tiled MFMA GEMM).
  * ------------------------------------------------------------------------- */
 int mkd_linear(const void* x, int x_dtype, int ldx, int rows, const void* w_packed, int n, int k,
                const void* bias, void* y, int y_dtype, int ldy, const void* residual,
@@ -101,7 +102,8 @@ int mkd_linear(const void* x, int x_dtype, int ldx, int rows, const void* w_pack
  * Outputs: router_logits [T, E] fp32, expert_index [T, k] int32,
  * expert_affinities [T, E] fp32 (scattered top-k, or full activation for the
  * (ACT1, topK) pipeline), topk_affinities [T, k] fp32 (may be NULL).
- * E <= 512, k <= 8, T <= 128.  Ties resolve to the lowest expert index.
+ * E <= 512, k <= 8, T <= 4096 (above 128 tokens the selection runs on 16
+ * tokens per block).  Ties resolve to the lowest expert index.
  * workspace: mkd_router_workspace_bytes(T, H, E) bytes (split-K partial logits).
  * ------------------------------------------------------------------------- */
 size_t mkd_router_workspace_bytes(int T, int H, int E);
@@ -113,10 +115,11 @@ int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_pack
 /* router_topk with no workspace argument.  No counterpart in the reference: it
  * is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
- * arguments, outputs and errors as mkd_router_topk; the split-K partial logits
- * go to a device array inside the library (2 MiB + 256 B per GPU, held until
- * the process ends), which covers every shape mkd_router_topk accepts.  Calls
- * that overlap in time on one GPU share that array and race. */
+ * arguments, outputs and errors as mkd_router_topk for T <= 128; the split-K
+ * partial logits go to a device array inside the library (2 MiB + 256 B per
+ * GPU, held until the process ends), which covers every such shape (T > 128 is
+ * rejected with MKD_ERR_INVALID).  Calls that overlap in time on one GPU share
+ * that array and race. */
 int mkd_router_topk_static(const void* x, int x_dtype, int T, int H, const void* w_packed, int E,
                            const void* w_bias, float* router_logits, float* expert_affinities,
                            int* expert_index, float* topk_affinities, int k, int mode, void* stream);

@@ -17,7 +17,7 @@ CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libmkd.so")
 SOURCES = ["capi.hip", "gemm.hip", "norm.hip", "attn_mfma.hip", "moe.hip",
-           "misc.hip", "mx.hip", "gemm_tile.hip", "layer_mk.hip", "qkv_norm.hip"]
+           "misc.hip", "mx.hip", "gemm_tile.hip", "layer_mk.hip", "qkv_norm.hip", "gemm_mid.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 

@@ -18,8 +18,12 @@ struct HeadPrep {
   static constexpr int HD = D / 2;
   // raw loads (converted in finish, so that a wave's loads for all its heads
   // are in flight together: a conversion inside a conditional would make the
-  // compiler wait for each load where it is issued)
+  // compiler wait for each load where it is issued).  fp32 projections may come
+  // as kMaxQkvParts split-K partials (a.qkv_nparts), summed in order.
+  static constexpr int kMaxQkvParts = 8;
   uint32_t xr[2], nr[2];
+  float xp[2][kMaxQkvParts];
+  int np;
   float cs[2], sn[2], invf[2];
   int posr;
   bool f32, has_nw, rope_tab;
@@ -38,12 +42,18 @@ struct HeadPrep {
     const float* sp = rope_tab ? a.sin + (long long)b * D : reinterpret_cast<const float*>(src);
     const int l = lane < HD ? lane : 0;
     off0 = (long long)b * a.ld_qkv + head * D + l;
+    np = (f32 && a.qkv_nparts > 1) ? min(a.qkv_nparts, kMaxQkvParts) : 1;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int i = l + e * HD;
       const long long off = off0 + e * HD;
       // one aligned dword: the fp32 element, or the pair holding the bf16 one
       xr[e] = *reinterpret_cast<const uint32_t*>(src + ((off << (f32 ? 2 : 1)) & ~3LL));
+      if (np > 1) {
+#pragma unroll
+        for (int q = 1; q < kMaxQkvParts; ++q)
+          xp[e][q] = a.qkv[(long long)min(q, np - 1) * a.qkv_part_stride + off];
+      }
       nr[e] = nwp[i];
       cs[e] = cp[i];
       sn[e] = sp[i];
@@ -60,7 +70,13 @@ struct HeadPrep {
     for (int e = 0; e < 2; ++e) {
       const long long off = off0 + e * HD;
       const uint32_t h16 = (off & 1) ? (xr[e] >> 16) : (xr[e] & 0xffffu);
-      x[e] = lane < HD ? (f32 ? __uint_as_float(xr[e]) : bf2f(h16)) : 0.f;
+      float v = f32 ? __uint_as_float(xr[e]) : bf2f(h16);
+      if (np > 1) {
+#pragma unroll
+        for (int q = 1; q < kMaxQkvParts; ++q)
+          if (q < np) v += xp[e][q];
+      }
+      x[e] = lane < HD ? v : 0.f;
       nw[e] = has_nw ? bf2f(nr[e]) : 1.f;
       if (!rope_tab) { cs[e] = 1.f; sn[e] = 0.f; }
       if (kind < 2 && rope_mode == 2) {

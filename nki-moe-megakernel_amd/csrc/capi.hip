@@ -164,13 +164,20 @@ int check_mx_dims(int N, int K, int rb) {
   return MKD_OK;
 }
 
+// The LDS-tiled GEMM addresses one expert's (or the dense) weight block and its
+// activation rows through 32-bit buffer offsets: both must stay below 2^31 bytes.
+bool tile_offsets_ok(long long x_rows, long long ldx, long long N, long long K) {
+  constexpr long long kLim = 1LL << 31;
+  return x_rows * ldx * 2 < kLim && padded_rows((int)N) * K * 2 < kLim;
+}
+
 // Dense launch: the tiled MFMA GEMM for many tokens, else one launch of 16..64-token
 // column tiles.
 int dense_gemm(GemmArgs a, int epi, bool xf32, hipStream_t s) {
   const int T = a.T;
   // many tokens (prefill passes): the LDS-tiled MFMA GEMM, fp32 out (+ bias)
   if (T >= 256 && epi == EPI_F32 && !xf32 && a.kgrid <= 1 && !a.residual && !a.grp_expert &&
-      gemm_tile_supported(a.N, a.K, EPI_SCALE_F32)) {
+      gemm_tile_supported(a.N, a.K, EPI_SCALE_F32) && tile_offsets_ok(T, a.ldx, a.N, a.K)) {
     a.pair_scale = nullptr;
     MKD_TRY(gemm_tile_launch(a, EPI_SCALE_F32, 1, T, s), "tiled gemm");
     return MKD_OK;
@@ -213,14 +220,30 @@ int router_stage(const void* x, bool xf32, int H, const void* w_packed, float* p
   a.KW = kg > 1 ? choose_kw_split(H, kg) : choose_kw(H);
   a.part_stride = (long long)r.T * r.E;
   MKD_REQUIRE(a.KW > 0, MKD_ERR_UNSUPPORTED, "router: no K split for H=%d", H);
-  if (int rc = dense_gemm(a, EPI_F32, xf32, s)) return rc;
+  // 17..128 tokens: the rows' K slices staged in LDS (gemm_mid), the same number
+  // of K-split partials when the split matches
+  if (gemm_mid_kgrid(r.E, H, r.T) == kg) {
+    MKD_TRY(gemm_mid_launch(a, kg, xf32, s), "router gemm (mid)");
+  } else if (int rc = dense_gemm(a, EPI_F32, xf32, s)) {
+    return rc;
+  }
   r.parts = parts;
   r.nparts = kg;
   r.part_stride = a.part_stride;
-  if (multi)
+  if (multi) {
     MKD_TRY(router_select_multi_launch(r, s), "router select (multi-block)");
-  else
+  } else if (r.n_groups && r.T > 16 && r.idx_out) {
+    // more tokens than one block's waves: one token per wave over several
+    // blocks, then the expert groups from the indices (one block serialising
+    // the tokens took 24 us at 64 tokens)
+    RouterArgs q = r;
+    q.n_groups = nullptr;
+    MKD_TRY(router_select_multi_launch(q, s), "router select (multi-block)");
+    MKD_TRY(moe_route_launch(r.idx_out, r.T, r.K, r.E, r.n_groups, r.grp_expert, r.grp_count,
+                             r.grp_offset, r.pair_token, r.pair_slot, s), "router groups");
+  } else {
     MKD_TRY(router_select_launch(r, s), "router select");
+  }
   return MKD_OK;
 }
 
@@ -442,7 +465,8 @@ int mkd_linear(const void* x, int x_dtype, int ldx, int rows, const void* w_pack
                void* stream) {
   if (int rc = stale_check("mkd_linear")) return rc;
   MKD_REQUIRE(x && w_packed && y, MKD_ERR_NULL, "linear: null pointer");
-  MKD_REQUIRE(rows > 0 && rows <= 128, MKD_ERR_INVALID, "linear: rows %d must be in [1, 128]", rows);
+  MKD_REQUIRE(rows > 0 && rows <= kMaxPrefillT, MKD_ERR_INVALID, "linear: rows %d must be in [1, %d]", rows,
+              kMaxPrefillT);
   if (int rc = check_gemm_dims(n, k, 1)) return rc;
   MKD_REQUIRE(ldx >= k && ldy >= n, MKD_ERR_INVALID, "linear: leading dims too small");
   MKD_REQUIRE(ldx % 8 == 0 && ldy % 4 == 0, MKD_ERR_INVALID, "linear: leading dims must be 16-byte aligned");
@@ -465,7 +489,8 @@ int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_pack
   if (int rc = stale_check("mkd_router_topk")) return rc;
   MKD_REQUIRE(x && w_packed && router_logits && expert_index && workspace, MKD_ERR_NULL,
               "router_topk: null pointer");
-  MKD_REQUIRE(T > 0 && T <= 128, MKD_ERR_INVALID, "router_topk: T %d must be in [1, 128]", T);
+  MKD_REQUIRE(T > 0 && T <= kMaxPrefillT, MKD_ERR_INVALID, "router_topk: T %d must be in [1, %d]", T,
+              kMaxPrefillT);
   MKD_REQUIRE(E > 0 && E <= 512, MKD_ERR_INVALID, "router_topk: E %d must be in [1, 512]", E);
   MKD_REQUIRE(k >= 1 && k <= 8 && k <= E, MKD_ERR_INVALID, "router_topk: k %d must be in [1, 8]", k);
   if (int rc = check_gemm_dims(E, H, 1)) return rc;
@@ -479,8 +504,9 @@ int mkd_router_topk(const void* x, int x_dtype, int T, int H, const void* w_pack
   r.T = T; r.E = E; r.K = k; r.mode = mode;
   r.logits_out = router_logits; r.aff_full = expert_affinities; r.idx_out = expert_index;
   r.topk_out = topk_affinities;
+  // above 128 tokens the selection runs on 16 tokens per block
   return router_stage(x, x_dtype == MKD_DT_F32, H, w_packed, static_cast<float*>(workspace), r,
-                      static_cast<hipStream_t>(stream));
+                      static_cast<hipStream_t>(stream), T > 128);
 }
 
 // ---- router_topk without a caller workspace (mkd_router_topk_static) ----
@@ -555,6 +581,11 @@ int moe_entry(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, vo
     MKD_REQUIRE(gemm_tile_supported(2 * p->I, p->H, EPI_SWIGLU_BF16) &&
                     gemm_tile_supported(p->H, p->I, EPI_SCALE_F32),
                 MKD_ERR_UNSUPPORTED, "moe_prefill: H (%d) and I (%d) must be multiples of 32", p->H, p->I);
+    MKD_REQUIRE(tile_offsets_ok(p->T, p->H, 2LL * p->I, p->H) &&
+                    tile_offsets_ok((long long)p->T * p->K, p->I, p->H, p->I),
+                MKD_ERR_UNSUPPORTED,
+                "moe_prefill: T=%d K=%d H=%d I=%d puts an operand past 2^31 bytes (32-bit buffer offsets)",
+                p->T, p->K, p->H, p->I);
   } else {
     MKD_REQUIRE(p->T > 0 && p->T <= 128, MKD_ERR_INVALID,
                 "moe_tkg: only T <= 128 tokens are supported in selective mode, got %d", p->T);
@@ -682,7 +713,9 @@ static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_
   w.chunk = attn_chunk_for(B, nkv, S_max);
   w.n_chunks = (S_max + 1 + w.chunk - 1) / w.chunk;
   w.hnorm = c.take<uint16_t>((size_t)B * H);
-  w.qkv = c.take<float>((size_t)B * (nq + 2 * nkv) * d);
+  // the QKV projection of 17..128 tokens comes as split-K partials
+  const int qparts = std::max(1, gemm_mid_kgrid((nq + 2 * nkv) * d, H, B));
+  w.qkv = c.take<float>((size_t)qparts * B * (nq + 2 * nkv) * d);
   w.attn = c.take<uint16_t>((size_t)B * nq * d);
   w.kvn = c.take<uint16_t>((size_t)B * 2 * nkv * d);
   w.prep = c.take<uint16_t>((size_t)B * (nq + 2 * nkv) * d);
@@ -704,6 +737,7 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
                           const float* inv_freq, hipStream_t s, float* o_parts = nullptr,
                           int o_kgrid = 1, const QkvNormArgs* qn = nullptr, bool prefill = false) {
   const int qkv_n = (p->nq + 2 * p->nkv) * p->d;
+  int qkv_parts = 1;
   // 1. optional RMSNorm
   const void* xin = p->X;
   if (p->rmsnorm_gamma) {
@@ -727,13 +761,23 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     GemmArgs g = dense_args(p->w_qkv_packed, xin, p->H, qkv_n, p->H, p->B, w.qkv, qkv_n);
     g.bias = static_cast<const uint16_t*>(p->bias_qkv);
     const int ps = prof_begin(MKD_KCLASS_QKV, s);
-    if (int rc = dense_gemm(g, EPI_F32, false, s)) return rc;
+    // the decode step at 17..128 tokens: activation slices in LDS, K-split partials
+    // that the head preparation adds in order
+    const int kq = o_parts ? gemm_mid_kgrid(qkv_n, p->H, p->B) : 0;
+    if (kq) {
+      g.part_stride = (long long)p->B * qkv_n;
+      MKD_TRY(gemm_mid_launch(g, kq, false, s), "qkv (mid)");
+      qkv_parts = kq;
+    } else if (int rc = dense_gemm(g, EPI_F32, false, s)) {
+      return rc;
+    }
     prof_end(ps, s);
   }
   // 3. q/k norm + RoPE + staging
   AttnArgs a;
   memset(&a, 0, sizeof(a));
   a.qkv = w.qkv; a.ld_qkv = qkv_n;
+  a.qkv_nparts = qkv_parts; a.qkv_part_stride = (long long)p->B * qkv_n;
   a.q_norm = static_cast<const uint16_t*>(p->q_norm);
   a.k_norm = static_cast<const uint16_t*>(p->k_norm);
   a.qk_eps = p->qk_eps;
@@ -785,11 +829,13 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     if (o_parts) {
       o.y = o_parts;
       o.residual = nullptr;
-      o.kgrid = o_kgrid;
-      o.KW = o_kgrid > 1 ? choose_kw_split(p->nq * p->d, o_kgrid)
-                         : choose_kw(p->nq * p->d, 512, (p->H_out + 15) / 16);
       o.part_stride = (long long)p->B * p->H_out;
-      if (int rc = dense_gemm(o, EPI_F32, false, s)) return rc;
+      if (o_kgrid > 1) {   // 17..128 tokens: K-split partials (gemm_mid_kgrid)
+        MKD_TRY(gemm_mid_launch(o, o_kgrid, false, s), "o_proj (mid)");
+      } else {
+        o.KW = choose_kw(p->nq * p->d, 512, (p->H_out + 15) / 16);
+        if (int rc = dense_gemm(o, EPI_F32, false, s)) return rc;
+      }
     } else if (int rc = dense_gemm(o, p->residual ? EPI_RESID_BF16 : EPI_BF16, false, s)) {
       return rc;
     }
@@ -961,6 +1007,12 @@ static LkWs carve_lk(Carver& c, const mkd_qwen3_model* m, int B) {
   return w;
 }
 
+// K split of the output projection in the decode step: the LDS-staged GEMM's at
+// 17..128 tokens (partials added by the post-attention norm), else none.
+static int o_proj_kgrid(const mkd_qwen3_model* m, int B) {
+  return std::max(1, gemm_mid_kgrid(m->H, m->nq * m->d, B));
+}
+
 struct StepWs {
   AttnWs attn;
   uint16_t *r, *nbf;
@@ -978,7 +1030,7 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.logits = c.take<float>((size_t)16 * B * m->E);  // split-K partials (<= 16)
   w.cos = c.take<float>((size_t)B * m->d);
   w.sin = c.take<float>((size_t)B * m->d);
-  w.oparts = c.take<float>((size_t)2 * B * m->H);      // o_proj split-K partials
+  w.oparts = c.take<float>((size_t)std::max(2, o_proj_kgrid(m, B)) * B * m->H);   // o_proj split-K partials
   w.moe = carve_moe(c, B, m->H, m->E, m->I, m->K);
   w.lk = carve_lk(c, m, B);
   return w;
@@ -1119,7 +1171,7 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
   if (!fuse_qn)
     MKD_TRY(rmsnorm_launch(x, 0, static_cast<const uint16_t*>(m->ln_in[0]), w.attn.hnorm, nullptr, B,
                            m->H, m->H, ha, m->eps, pre_order, s), "pre norm");
-  const int o_kgrid = 1;   // one block per 16 output rows, up to 16 waves over K
+  const int o_kgrid = o_proj_kgrid(m, B);
   for (int l = 0; l < m->num_layers; ++l) {
     const int wl = m->window ? m->window[l] : 0;
     mkd_attention_args ap;
@@ -1256,7 +1308,9 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
                           m->expert_format ? m->gate_up_scales[l] : nullptr,
                           m->expert_format ? m->down_scales[l] : nullptr,
                           long_pass && !m->expert_format && gemm_tile_supported(2 * m->I, m->H, EPI_SWIGLU_BF16) &&
-                              gemm_tile_supported(m->H, m->I, EPI_SCALE_F32),
+                              gemm_tile_supported(m->H, m->I, EPI_SCALE_F32) &&
+                              tile_offsets_ok(B, m->H, 2LL * m->I, m->H) &&
+                              tile_offsets_ok((long long)B * m->K, m->I, m->H, m->I),
                           defer_sel ? &sel : nullptr))
       return rc;
     // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention

@@ -1,0 +1,197 @@
+// Dense decode projection for 17..128 tokens (QKV and output projections at
+// batch 17-128): Y[t, n] = sum_k X[t, k] * W[n, k] in fp32 split-K partials
+// (qkv_tkg.py:71-363, output_projection_tkg.py:66-265 -- the same contraction as
+// the weight-streaming GEMM in gemm.hip, shaped for a wider token dimension).
+//
+// At these token counts the weight-streaming GEMM (one 16-row block per launch
+// block, waves splitting K) reads the activation tile of every token for every
+// weight fragment: at 64 tokens that is 4 bytes of activations per weight byte,
+// all through the issuing CU's vector L1 (64 B/clk).  Here a block of 4 waves
+// owns a K slice of KS and 4 * RBW row blocks: the slice's activations
+// X[0:T, k0:k0+KS] are copied to LDS once (in MFMA B-operand order, 16 bytes per
+// lane per fragment) and every wave reads them from there while streaming only
+// its own row blocks' weight fragments (frag layout, one 1 KiB
+// v_mfma_f32_16x16x32_bf16 A operand per fragment).  Waves own disjoint rows,
+// so there is no cross-wave reduction; block (row group, kb) writes partial kb
+// of the K split to y + kb * part_stride (bias in partial 0), which the
+// consumer (attention head preparation, post-attention norm) adds in order.
+#include "common.h"
+#include "mkd_internal.h"
+
+namespace mkd {
+
+namespace {
+constexpr int kMidWaves = 4;
+}
+
+// TT token tiles of 16; RBW row blocks per wave; NF = KS / 32 weight fragments
+// per row block (all issued before the first MFMA).  XF32: fp32 activations (the
+// router's normalised rows) carried as a bf16 hi + lo pair, two LDS slices and
+// two MFMAs per fragment (~2^-16 relative, as the weight-streaming GEMM).
+template <int TT, int RBW, int NF, bool XF32>
+__global__ void __launch_bounds__(256) gemm_mid_kernel(GemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) u32x4_t xs[];    // [hi/lo][TT][NF][64]
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int KB = a.K / 32;
+  const int kb = blockIdx.y;                      // K slice
+  const int kf0 = kb * NF;                        // first 32-wide k block of the slice
+  const int NRB = (a.N + 15) / 16;
+
+  // ---- weights of the wave's row blocks: every fragment in flight at once ----
+  u32x4_t wf[RBW][NF];
+#pragma unroll
+  for (int r = 0; r < RBW; ++r) {
+    const int rb = min((blockIdx.x * kMidWaves * RBW) + r * kMidWaves + w, NRB - 1);
+    const uint16_t* wp = a.w + ((long long)rb * KB + kf0) * 512 + lane * 8;
+#pragma unroll
+    for (int f = 0; f < NF; ++f)
+      wf[r][f] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp + f * 512));
+  }
+
+  // ---- the activation slice into LDS in B-operand order: chunk c = (tile tt,
+  // fragment f, lane l) holds token tt*16 + l%16, k = (kf0 + f)*32 + (l/16)*8 .. +8 ----
+  constexpr int NCH = TT * NF * 64;
+  for (int c = threadIdx.x; c < NCH; c += 256) {
+    const int l = c & 63, f = (c >> 6) % NF, tt = c / (64 * NF);
+    const int t = tt * 16 + (l & 15);
+    const long long k = (long long)(kf0 + f) * 32 + (l >> 4) * 8;
+    if constexpr (XF32) {
+      f32x4_t p = {0.f, 0.f, 0.f, 0.f}, q = {0.f, 0.f, 0.f, 0.f};
+      if (t < a.T) {
+        const float* xp = static_cast<const float*>(a.x) + (long long)t * a.ldx + k;
+        p = *reinterpret_cast<const f32x4_t*>(xp);
+        q = *reinterpret_cast<const f32x4_t*>(xp + 4);
+      }
+      const float v[8] = {p[0], p[1], p[2], p[3], q[0], q[1], q[2], q[3]};
+      u32x4_t hi, lo;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t h0 = f2bf(v[2 * j]), h1 = f2bf(v[2 * j + 1]);
+        hi[j] = h0 | (h1 << 16);
+        lo[j] = f2bf(v[2 * j] - bf2f(h0)) | (f2bf(v[2 * j + 1] - bf2f(h1)) << 16);
+      }
+      xs[c] = hi;
+      xs[NCH + c] = lo;
+    } else {
+      u32x4_t v = {0u, 0u, 0u, 0u};
+      if (t < a.T) v = ld16(static_cast<const uint16_t*>(a.x) + (long long)t * a.ldx + k);
+      xs[c] = v;
+    }
+  }
+  __syncthreads();
+
+  // ---- MFMAs: acc[r][tt] = rows of row block r x tokens of tile tt ----
+  f32x4_t acc[RBW][TT];
+#pragma unroll
+  for (int r = 0; r < RBW; ++r)
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[r][tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int f = 0; f < NF; ++f) {
+    u32x4_t xf[TT];
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) xf[tt] = xs[(tt * NF + f) * 64 + lane];
+#pragma unroll
+    for (int r = 0; r < RBW; ++r)
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) acc[r][tt] = mfma16x16x32(wf[r][f], xf[tt], acc[r][tt]);
+    if constexpr (XF32) {
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) xf[tt] = xs[NCH + (tt * NF + f) * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < RBW; ++r)
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) acc[r][tt] = mfma16x16x32(wf[r][f], xf[tt], acc[r][tt]);
+    }
+  }
+
+  // ---- partial kb: lane l holds rows 4*(l/16)+i of its row block, token l%16 ----
+  float* yb = static_cast<float*>(a.y) + (long long)kb * a.part_stride;
+#pragma unroll
+  for (int r = 0; r < RBW; ++r) {
+    const int rb = (blockIdx.x * kMidWaves * RBW) + r * kMidWaves + w;
+    if (rb >= NRB) continue;
+    const int n0 = rb * 16 + (lane >> 4) * 4;
+    float bb[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.bias && kb == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bb[i] = (n0 + i < a.N) ? bf2f(a.bias[n0 + i]) : 0.f;
+    }
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const int t = tt * 16 + (lane & 15);
+      if (t >= a.T) continue;
+      float* y = yb + (long long)t * a.ldy + n0;
+      if (n0 + 3 < a.N && (a.ldy & 3) == 0) {
+        *reinterpret_cast<f32x4_t*>(y) = f32x4_t{acc[r][tt][0] + bb[0], acc[r][tt][1] + bb[1],
+                                                 acc[r][tt][2] + bb[2], acc[r][tt][3] + bb[3]};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (n0 + i < a.N) y[i] = acc[r][tt][i] + bb[i];
+      }
+    }
+  }
+}
+
+// Fragments per K slice with a kernel instantiation.
+static bool mid_nf_ok(int nf) { return nf == 4 || nf == 6 || nf == 8 || nf == 12 || nf == 16; }
+
+// Row blocks per wave: 2 for narrow outputs (the router: 128 rows make one
+// block of 4 waves), else 1.
+static int mid_rbw(int N) { return N <= 256 ? 2 : 1; }
+
+// K split for N output rows, K contraction and T tokens: the number of slices
+// (a power of two <= 16 cutting K / 32 into NF whole fragments, NF instantiated)
+// that gives at least ~256 blocks of 4 * RBW row blocks, else the most slices;
+// 0 when no split fits.
+int gemm_mid_kgrid(int N, int K, int T) {
+  if (T < 17 || T > 128 || K % 32 || N <= 0) return 0;
+  const int rbw = mid_rbw(N);
+  const int KB = K / 32, groups = ((N + 15) / 16 + kMidWaves * rbw - 1) / (kMidWaves * rbw);
+  int best = 0;
+  for (int kg = 1; kg <= 16 && KB % kg == 0; kg *= 2) {
+    if (!mid_nf_ok(KB / kg)) continue;
+    best = kg;
+    if ((long long)groups * kg >= 256) break;
+  }
+  return best;
+}
+
+template <int TT, int RBW, int NF, bool XF32>
+static hipError_t mid_go(const GemmArgs& a, dim3 grid, size_t lds, hipStream_t s) {
+  if (lds > 65536)   // above the default dynamic LDS limit: raise the kernel's
+    if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_mid_kernel<TT, RBW, NF, XF32>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds))
+      return e;
+  return timed_launch(gemm_mid_kernel<TT, RBW, NF, XF32>, grid, dim3(256), lds, s, a);
+}
+
+hipError_t gemm_mid_launch(GemmArgs a, int kgrid, bool xf32, hipStream_t s) {
+  const int KB = a.K / 32;
+  if (kgrid < 1 || KB % kgrid || !mid_nf_ok(KB / kgrid) || a.T < 1 || a.T > 128 || a.grp_expert)
+    return hipErrorInvalidValue;
+  const int nf = KB / kgrid, rbw = mid_rbw(a.N);
+  const int TT = (a.T + 15) / 16;
+  const int groups = ((a.N + 15) / 16 + kMidWaves * rbw - 1) / (kMidWaves * rbw);
+  const dim3 grid(groups, kgrid);
+  // token tiles rounded up to 2 / 4 / 8 (fewer instantiations); the activation
+  // slice takes tt * nf KiB of LDS (twice that for fp32 activations)
+  const int tt = TT <= 2 ? 2 : (TT <= 4 ? 4 : 8);
+  const size_t lds = (size_t)tt * nf * 64 * 16 * (xf32 ? 2 : 1);
+#define MKD_MID(TT_, NF_)                                                           \
+  if (tt == TT_ && nf == NF_) {                                                      \
+    if (xf32) return rbw == 2 ? mid_go<TT_, 2, NF_, true>(a, grid, lds, s)          \
+                              : mid_go<TT_, 1, NF_, true>(a, grid, lds, s);         \
+    return rbw == 2 ? mid_go<TT_, 2, NF_, false>(a, grid, lds, s)                   \
+                    : mid_go<TT_, 1, NF_, false>(a, grid, lds, s);                  \
+  }
+  MKD_MID(2, 4) MKD_MID(2, 6) MKD_MID(2, 8) MKD_MID(2, 12) MKD_MID(2, 16)
+  MKD_MID(4, 4) MKD_MID(4, 6) MKD_MID(4, 8) MKD_MID(4, 12) MKD_MID(4, 16)
+  MKD_MID(8, 4) MKD_MID(8, 6) MKD_MID(8, 8) MKD_MID(8, 12) MKD_MID(8, 16)
+#undef MKD_MID
+  return hipErrorInvalidValue;
+}
+
+}  // namespace mkd

@@ -88,6 +88,10 @@ hipError_t mx_pack_launch(const uint8_t* codes, const uint8_t* scales, uint8_t* 
 hipError_t gemm_mx_launch(GemmArgs a, int fmt, int epi, int groups_max, int max_tokens_per_group,
                           hipStream_t s);
 int choose_kw_mx(int K_pad);
+// gemm_mid.hip: dense projection of 17..128 tokens, activation slices staged in
+// LDS, fp32 split-K partials (kgrid from gemm_mid_kgrid; 0 = shape not covered)
+int gemm_mid_kgrid(int N, int K, int T);
+hipError_t gemm_mid_launch(GemmArgs a, int kgrid, bool xf32, hipStream_t s);
 // gemm_tile.hip: LDS-tiled grouped GEMM (many tokens per expert)
 bool gemm_tile_supported(int N, int K, int epi);
 // total_rows: the sum of the group sizes (grouped mode: T*K pairs), else the rows.
@@ -207,6 +211,8 @@ hipError_t rmsnorm_launch(const void* x, int x_f32, const uint16_t* gamma, uint1
 // attention.hip
 struct AttnArgs {
   const float* qkv;           // [B, (nq + 2 nkv) * d] fp32 projections (or null)
+  int qkv_nparts;             // split-K partials of qkv (0 / 1: one), summed in order
+  long long qkv_part_stride;  // elements between the partials
   const uint16_t* qkv_bf16;   // same, bf16 (operator path) (or null)
   int ld_qkv;
   const uint16_t* q_norm;     // [d] or null

@@ -88,9 +88,9 @@ def router_topk(x: torch.Tensor, w: torch.Tensor, w_bias: Optional[torch.Tensor]
         mode |= L.ROUTER_NORM_TOPK
     bias = w_bias.reshape(-1).to(torch.bfloat16).contiguous() if w_bias is not None else None
     lib = L.load()
-    ws = _ws(lib.mkd_router_workspace_bytes(min(T, 128), H, E), dev)
-    for t0 in range(0, T, 128):
-        t1 = min(T, t0 + 128)
+    ws = _ws(lib.mkd_router_workspace_bytes(min(T, 4096), H, E), dev)
+    for t0 in range(0, T, 4096):     # one call per 4096 tokens (the library's bound)
+        t1 = min(T, t0 + 4096)
         rc = lib.mkd_router_topk(xt[t0:t1].data_ptr(), xdt, t1 - t0, H, wp.data_ptr(), E,
                                  L.ptr(bias), logits[t0:t1].data_ptr(), aff[t0:t1].data_ptr(),
                                  idx[t0:t1].data_ptr(), topk[t0:t1].data_ptr(), k, mode,

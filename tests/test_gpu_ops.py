@@ -105,6 +105,31 @@ def test_linear_bf16(mk, dev, T, n, k):
     assert torch.equal(wp, wp2)
 
 
+@pytest.mark.parametrize("T,n,k,y_dtype,bias,resid", [
+    (256, 1536, 2048, torch.float32, True, False),    # LDS-tiled MFMA GEMM (>= 256 rows)
+    (1000, 5120, 2048, torch.float32, True, False),   # tiled, partial last token tile
+    (200, 768, 512, torch.bfloat16, True, True),      # > 64 rows, one launch of column tiles
+])
+def test_linear_many_rows(mk, dev, T, n, k, y_dtype, bias, resid):
+    """Prefill-sized dense projections (the context pass's QKV / o_proj / router
+    GEMMs) against torch matmul in fp32."""
+    from nki_moe_megakernel_amd import packing
+    L = _lib(mk)
+    g = torch.Generator().manual_seed(T + n)
+    w = bf(0.05 * torch.randn(n, k, generator=g))
+    x = bf(torch.randn(T, k, generator=g))
+    b = bf(torch.randn(n, generator=g)) if bias else None
+    r = bf(torch.randn(T, n, generator=g)) if resid else None
+    y = linear(L, x.to(dev), packing.pack_out_in(w.to(dev)), n, k, y_dtype,
+               b.to(dev) if bias else None, r.to(dev) if resid else None)
+    y_ref = x.float() @ w.float().t() + (b.float() if bias else 0)
+    if resid:
+        y_ref = bf(r.float() + bf(y_ref).float())
+        assert max_abs_rel(y, y_ref) < 8e-3
+    else:
+        assert max_abs_rel(y, y_ref) < 1e-5
+
+
 def test_linear_fp32_input_split(mk, dev):
     """fp32 activations (router path) are carried as a hi/lo bf16 pair: ~2^-16 relative."""
     from nki_moe_megakernel_amd import packing
@@ -162,6 +187,28 @@ def test_router_topk(mk, dev, T, E, k, pre, norm, act, xdt):
     assert_topk_match(idx, key if pre else l_ref, k)
     if torch.equal(idx.cpu().long(), i_ref):
         assert (aff.cpu() - a_ref).abs().max().item() < 1e-5
+
+
+@pytest.mark.parametrize("T", [300, 1100])
+def test_router_topk_many_tokens(mk, dev, T):
+    """Above 128 tokens (a prefill pass) the selection runs on 16 tokens per block:
+    indices against the oracle's stable top-k (near-ties < 1e-4 excepted), the
+    Qwen3 pipeline (softmax, top-8, L1 renormalisation) on fp32 inputs."""
+    from nki_moe_megakernel_amd.common_types import RouterActFnType
+    g = torch.Generator().manual_seed(T)
+    H, E, k = 2048, 128, 8
+    x = torch.randn(T, H, generator=g)
+    w = bf(0.02 * torch.randn(H, E, generator=g)).float()
+    logits = torch.empty(T, E, dtype=torch.float32, device=dev)
+    aff = torch.empty(T, E, dtype=torch.float32, device=dev)
+    idx = torch.empty(T, k, dtype=torch.int32, device=dev)
+    mk.router_topk(x.to(dev), w.to(dev), None, logits, aff, idx, RouterActFnType.SOFTMAX, k, 1, 0,
+                   router_pre_norm=True, norm_topk_prob=True)
+    l_ref, i_ref, a_ref, _ = ref.router_topk(x, w, None, "softmax", k, True, True)
+    assert (logits.cpu() - l_ref).abs().max().item() < 5e-5
+    assert_topk_match(idx, a_ref, k)
+    same = (idx.cpu().long() == i_ref).all(-1)
+    assert (aff.cpu()[same] - a_ref[same]).abs().max().item() < 1e-5
 
 
 @pytest.mark.parametrize("T,E,k", [(1, 128, 8), (16, 128, 8), (3, 512, 8), (40, 64, 6)])
