@@ -222,7 +222,7 @@ int router_stage(const void* x, bool xf32, int H, const void* w_packed, float* p
   MKD_REQUIRE(a.KW > 0, MKD_ERR_UNSUPPORTED, "router: no K split for H=%d", H);
   // 17..128 tokens: the rows' K slices staged in LDS (gemm_mid), the same number
   // of K-split partials when the split matches
-  if (gemm_mid_kgrid(r.E, H, r.T) == kg) {
+  if (gemm_mid_kgrid(r.E, H, r.T, 16) == kg) {
     MKD_TRY(gemm_mid_launch(a, kg, xf32, s), "router gemm (mid)");
   } else if (int rc = dense_gemm(a, EPI_F32, xf32, s)) {
     return rc;

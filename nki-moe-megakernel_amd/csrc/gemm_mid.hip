@@ -22,6 +22,12 @@ namespace mkd {
 
 namespace {
 constexpr int kMidWaves = 4;
+// the largest divisor of n that is <= cap (the staging batch)
+constexpr int batch_of(int n, int cap) {
+  int b = n < cap ? n : cap;
+  while (n % b) --b;
+  return b;
+}
 }
 
 // TT token tiles of 16; RBW row blocks per wave; NF = KS / 32 weight fragments
@@ -51,32 +57,51 @@ __global__ void __launch_bounds__(256) gemm_mid_kernel(GemmArgs a) {
 
   // ---- the activation slice into LDS in B-operand order: chunk c = (tile tt,
   // fragment f, lane l) holds token tt*16 + l%16, k = (kf0 + f)*32 + (l/16)*8 .. +8 ----
+  // A thread's chunks are c = tid + 256 j; each batch of BJ chunks has all its
+  // loads in flight before the first LDS store (absent tokens read row 0 and
+  // store zeros).
   constexpr int NCH = TT * NF * 64;
-  for (int c = threadIdx.x; c < NCH; c += 256) {
-    const int l = c & 63, f = (c >> 6) % NF, tt = c / (64 * NF);
-    const int t = tt * 16 + (l & 15);
-    const long long k = (long long)(kf0 + f) * 32 + (l >> 4) * 8;
-    if constexpr (XF32) {
-      f32x4_t p = {0.f, 0.f, 0.f, 0.f}, q = {0.f, 0.f, 0.f, 0.f};
-      if (t < a.T) {
-        const float* xp = static_cast<const float*>(a.x) + (long long)t * a.ldx + k;
-        p = *reinterpret_cast<const f32x4_t*>(xp);
-        q = *reinterpret_cast<const f32x4_t*>(xp + 4);
-      }
-      const float v[8] = {p[0], p[1], p[2], p[3], q[0], q[1], q[2], q[3]};
-      u32x4_t hi, lo;
+  constexpr int PJ = NCH / 256;                    // chunks per thread
+  constexpr int BJ = batch_of(PJ, XF32 ? 8 : 16);
+  static_assert(NCH % 256 == 0 && PJ % BJ == 0, "chunk split");
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t h0 = f2bf(v[2 * j]), h1 = f2bf(v[2 * j + 1]);
-        hi[j] = h0 | (h1 << 16);
-        lo[j] = f2bf(v[2 * j] - bf2f(h0)) | (f2bf(v[2 * j + 1] - bf2f(h1)) << 16);
+  for (int j0 = 0; j0 < PJ; j0 += BJ) {
+    u32x4_t v[BJ][XF32 ? 2 : 1];
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+      const int c = threadIdx.x + (j0 + j) * 256;
+      const int l = c & 63, f = (c >> 6) % NF, tt = c / (64 * NF);
+      const int t = tt * 16 + (l & 15);
+      const long long off = (long long)(t < a.T ? t : 0) * a.ldx + (long long)(kf0 + f) * 32 + (l >> 4) * 8;
+      if constexpr (XF32) {
+        const float* xp = static_cast<const float*>(a.x) + off;
+        v[j][0] = ld16(xp);
+        v[j][1] = ld16(xp + 4);
+      } else {
+        v[j][0] = ld16(static_cast<const uint16_t*>(a.x) + off);
       }
-      xs[c] = hi;
-      xs[NCH + c] = lo;
-    } else {
-      u32x4_t v = {0u, 0u, 0u, 0u};
-      if (t < a.T) v = ld16(static_cast<const uint16_t*>(a.x) + (long long)t * a.ldx + k);
-      xs[c] = v;
+    }
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+      const int c = threadIdx.x + (j0 + j) * 256;
+      const bool live = (c / (64 * NF)) * 16 + (c & 15) < a.T;
+      if constexpr (XF32) {
+        const float x8[8] = {__uint_as_float(v[j][0][0]), __uint_as_float(v[j][0][1]),
+                             __uint_as_float(v[j][0][2]), __uint_as_float(v[j][0][3]),
+                             __uint_as_float(v[j][1][0]), __uint_as_float(v[j][1][1]),
+                             __uint_as_float(v[j][1][2]), __uint_as_float(v[j][1][3])};
+        u32x4_t hi, lo;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t h0 = f2bf(x8[2 * q]), h1 = f2bf(x8[2 * q + 1]);
+          hi[q] = h0 | (h1 << 16);
+          lo[q] = f2bf(x8[2 * q] - bf2f(h0)) | (f2bf(x8[2 * q + 1] - bf2f(h1)) << 16);
+        }
+        xs[c] = live ? hi : u32x4_t{0u, 0u, 0u, 0u};
+        xs[NCH + c] = live ? lo : u32x4_t{0u, 0u, 0u, 0u};
+      } else {
+        xs[c] = live ? v[j][0] : u32x4_t{0u, 0u, 0u, 0u};
+      }
     }
   }
   __syncthreads();
@@ -142,19 +167,26 @@ static bool mid_nf_ok(int nf) { return nf == 4 || nf == 6 || nf == 8 || nf == 12
 // block of 4 waves), else 1.
 static int mid_rbw(int N) { return N <= 256 ? 2 : 1; }
 
-// K split for N output rows, K contraction and T tokens: the number of slices
-// (a power of two <= 16 cutting K / 32 into NF whole fragments, NF instantiated)
-// that gives at least ~256 blocks of 4 * RBW row blocks, else the most slices;
-// 0 when no split fits.
-int gemm_mid_kgrid(int N, int K, int T) {
+// K split for N output rows, K contraction and T tokens: among the slice counts
+// (a power of two <= max_parts cutting K / 32 into NF whole fragments, NF
+// instantiated), the one with the least work on the busiest CU -- rounds of
+// blocks over the 256 CUs times the work of a block, ceil(blocks / 256) / kg --
+// the fewest slices on a tie; 0 when no split fits.  (A grid of 320 blocks left
+// a quarter of the CUs with two blocks and the launch waiting for them.)
+int gemm_mid_kgrid(int N, int K, int T, int max_parts) {
   if (T < 17 || T > 128 || K % 32 || N <= 0) return 0;
+  constexpr int kCUs = 256;
   const int rbw = mid_rbw(N);
   const int KB = K / 32, groups = ((N + 15) / 16 + kMidWaves * rbw - 1) / (kMidWaves * rbw);
   int best = 0;
-  for (int kg = 1; kg <= 16 && KB % kg == 0; kg *= 2) {
+  double best_load = 1e30;
+  for (int kg = 1; kg <= max_parts && kg <= 16 && KB % kg == 0; kg *= 2) {
     if (!mid_nf_ok(KB / kg)) continue;
-    best = kg;
-    if ((long long)groups * kg >= 256) break;
+    const double load = (double)((groups * kg + kCUs - 1) / kCUs) / kg;
+    if (load < best_load - 1e-9) {
+      best_load = load;
+      best = kg;
+    }
   }
   return best;
 }

@@ -90,7 +90,7 @@ hipError_t gemm_mx_launch(GemmArgs a, int fmt, int epi, int groups_max, int max_
 int choose_kw_mx(int K_pad);
 // gemm_mid.hip: dense projection of 17..128 tokens, activation slices staged in
 // LDS, fp32 split-K partials (kgrid from gemm_mid_kgrid; 0 = shape not covered)
-int gemm_mid_kgrid(int N, int K, int T);
+int gemm_mid_kgrid(int N, int K, int T, int max_parts = 8);
 hipError_t gemm_mid_launch(GemmArgs a, int kgrid, bool xf32, hipStream_t s);
 // gemm_tile.hip: LDS-tiled grouped GEMM (many tokens per expert)
 bool gemm_tile_supported(int N, int K, int epi);
