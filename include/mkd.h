@@ -415,11 +415,16 @@ int mkd_profile_count(void); /* launches recorded since the last mkd_profile_eve
  * Qwen3 flow with bf16 experts, B <= 4,
  * d in {64, 128}, gqa <= 16, no biases / sinks / windows, and the stage
  * buffers fit the LDS budget; other configurations keep the multi-kernel
- * sequence.  The workspace size does not depend on the mode.  Process-global.
+ * sequence.  In mode 0, where the router top-k runs inside the expert launch
+ * (a single token with bf16 experts), the gate/up and down projections share
+ * that launch, the down blocks waiting inside it for their expert's gate/up
+ * blocks.  Mode 2 is mode 0 with every stage a launch of its own.  The
+ * workspace size does not depend on the mode.  Process-global.
  * mkd_qwen3_layer_kernel_status reports (after a stream sync) whether the
  * workspace's plan uses the persistent kernel and whether any of its grid
- * barriers timed out (results of such a step are invalid; the barrier spins
- * are bounded so the kernel always completes).
+ * barriers, or any in-launch wait of the joined expert launch, timed out
+ * (results of such a step are invalid; the spins are bounded so every kernel
+ * completes).
  * ------------------------------------------------------------------------- */
 int mkd_set_decode_path(int mode);
 /* The per-layer weight and cache pointers of m as a device table (written once,

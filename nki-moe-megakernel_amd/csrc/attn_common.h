@@ -21,7 +21,7 @@ struct HeadPrep {
   // compiler wait for each load where it is issued).  fp32 projections may come
   // as kMaxQkvParts split-K partials (a.qkv_nparts), summed in order.
   static constexpr int kMaxQkvParts = 8;
-  uint32_t xr[2], nr[2];
+  uint32_t xr[2], nr[2];   // nr: the aligned dword holding the bf16 norm weight of element i
   float xp[2][kMaxQkvParts];
   int np;
   float cs[2], sn[2], invf[2];
@@ -54,7 +54,10 @@ struct HeadPrep {
         for (int q = 1; q < kMaxQkvParts; ++q)
           xp[e][q] = a.qkv[(long long)min(q, np - 1) * a.qkv_part_stride + off];
       }
-      nr[e] = nwp[i];
+      // the aligned dword holding the bf16 norm weight: a 16-bit load would be
+      // zero-extended where it is issued, making the wave wait for it before
+      // the next head's loads go out
+      nr[e] = *reinterpret_cast<const uint32_t*>(nwp + (i & ~1));
       cs[e] = cp[i];
       sn[e] = sp[i];
     }
@@ -77,7 +80,8 @@ struct HeadPrep {
           if (q < np) v += xp[e][q];
       }
       x[e] = lane < HD ? v : 0.f;
-      nw[e] = has_nw ? bf2f(nr[e]) : 1.f;
+      const int i = (lane < HD ? lane : 0) + e * HD;
+      nw[e] = has_nw ? ((i & 1) ? bf_hi(nr[e]) : bf_lo(nr[e])) : 1.f;
       if (!rope_tab) { cs[e] = 1.f; sn[e] = 0.f; }
       if (kind < 2 && rope_mode == 2) {
         const float ang = (float)posr * invf[e];

@@ -123,22 +123,27 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
-  const int n = prior_len(a, b);
-  const int total = n + 1;
   const int chunk0 = c * CP;
-  if (chunk0 >= total) return;                // whole block: uniform exit
 
   // ---- 0. the wave's K and V rows from the cache: they depend on nothing
-  // computed here, so their loads are issued first and overlap the prep.  With
-  // 4 tiles per wave (large grids) the registers cost more occupancy than the
-  // overlap gains, and the rows are loaded where they are used. ----
+  // computed here, so their loads are issued first and overlap the prep.  A
+  // flat cache's rows are loaded before the prior length n is known (rows of
+  // the chunk below S_max; rows at or past n are never used: their scores are
+  // masked and their V values zeroed where they are read), so that the length's
+  // own round trip is not in front of them; a block table's rows need the
+  // table and the length first.  With 4 tiles per wave (large grids) the
+  // registers cost more occupancy than the overlap gains, and the rows are
+  // loaded where they are used. ----
   constexpr bool PRE = TPW <= 2;
+  const bool flat = a.block_table == nullptr;
+  int n = a.S_max;                            // row bound until the prior length is read
   const int dq = (lane >> 4) * (D / 4);       // lane's d range in a 16-row tile
   const int wbase = chunk0 + w * TPW * 16;
   const int vc = (lane & 15) * (D / 16);      // lane's V row segment (d labels)
   // Row pointers first, then the loads: with a block table every pointer is
   // itself a load, and interleaving them would make each data load wait.
-  // V rows of tile `tile0` for the PV operand: position tile0 + 4*(l/16) + j.
+  // V rows of tile `tile0` for the PV operand: position tile0 + 4*(l/16) + j
+  // (rows below n; n is S_max until the prior length is known).
   auto v_ptrs = [&](int tile0, bool live, const uint16_t* (&p)[4]) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -171,7 +176,7 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   };
   u32x4_t kpre[PRE ? TPW : 1][NK];
   uint32_t vpre[PRE ? TPW : 1][4][VW];
-  if constexpr (PRE) {
+  auto pre_loads = [&]() {
     const uint16_t* kp[TPW];
     const uint16_t* vp[TPW][4];
 #pragma unroll
@@ -184,11 +189,32 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
       k_load(kp[tt], kpre[tt]);
       v_load(vp[tt], vpre[tt]);
     }
-  }
+  };
 
   // ---- 1. the kv group's prepared heads [q heads of g | k of g | v of g]:
   // copied from attn_prep_kernel's output (large grids), or prepared here --
-  // wave w takes heads w, w+4, ...; all loads first, then the math ----
+  // wave w takes heads w, w+4, ...: their loads go out first (a wave's vector
+  // loads complete in issue order, so the math need not wait for the cache
+  // rows behind them), then the prior length and the cache rows ----
+  constexpr int NR = (GQA + 2 + 3) / 4;
+  HeadPrep<D> hp[NR];
+  if (!a.prep) {
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int h = w + 4 * r;
+      if (h < GQA + 2) {
+        const int kind = h < GQA ? 0 : h - GQA + 1;
+        const int head = h < GQA ? g * GQA + h : (kind == 1 ? a.nq + g : a.nq + a.nkv + g);
+        hp[r].load(a, rope_mode, b, head, kind, lane);
+      }
+    }
+  }
+  const int n_read = prior_len(a, b);
+  if (PRE && flat) pre_loads();
+  n = n_read;
+  const int total = n + 1;
+  if (chunk0 >= total) return;                // whole block: uniform exit
+  if (PRE && !flat) pre_loads();
   if (a.prep) {
     const uint16_t* src = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
     for (int i = threadIdx.x * 8; i < (GQA + 2) * D; i += 256 * 8) {
@@ -197,7 +223,14 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
       *reinterpret_cast<u32x4_t*>(dst) = ld16(src + i);
     }
   } else {
-    prep_heads<D, GQA>(a, rope_mode, b, g, w, lane, q_s, kn_s, vn_s);
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+      const int h = w + 4 * r;
+      if (h < GQA + 2) {
+        const int kind = h < GQA ? 0 : h - GQA + 1;
+        hp[r].finish(a, rope_mode, kind, h < GQA ? q_s[h] : (kind == 1 ? kn_s : vn_s), lane);
+      }
+    }
   }
   __syncthreads();
 
@@ -294,12 +327,19 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
         if constexpr (PRE) v[j][e] = vpre[tt][j][e];
         else v[j][e] = vl[tt % LB][j][e];
       }
-    // the new token's row comes from LDS (at most one j per lane)
+    // the new token's row comes from LDS (at most one j per lane); rows past it
+    // (read before n was known) are zero
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (tile0 + (lane >> 4) * 4 + j == n)
+    for (int j = 0; j < 4; ++j) {
+      const int t = tile0 + (lane >> 4) * 4 + j;
+      if (t == n) {
 #pragma unroll
         for (int e = 0; e < VW; ++e) v[j][e] = *reinterpret_cast<const uint32_t*>(&vn_s[vc + 2 * e]);
+      } else if (t > n) {
+#pragma unroll
+        for (int e = 0; e < VW; ++e) v[j][e] = 0u;
+      }
+    }
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       const int e = dt >> 1;

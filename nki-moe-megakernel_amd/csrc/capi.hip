@@ -300,8 +300,10 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
              int K, int act, float alpha, float ghi, float glo, float uhi, float ulo, int round_qwen,
              MoeWs& w, hipStream_t s, bool do_finalize = true, int wfmt = 0,
              const void* gu_scales = nullptr, const void* dn_scales = nullptr, bool tiled = false,
-             const RouterArgs* sel = nullptr) {
+             const RouterArgs* sel = nullptr, unsigned* fused_flags = nullptr,
+             unsigned* fused_err = nullptr) {
   if (sel && (idx || wfmt || tiled)) return MKD_ERR_INVALID;
+  if (fused_flags && !sel) return MKD_ERR_INVALID;
   if (idx)  // otherwise the router stage already built the expert groups
     MKD_TRY(moe_route_launch(idx, T, K, E, w.n_groups, w.grp_expert, w.grp_count, w.grp_offset,
                              w.pair_token, w.pair_slot, s), "moe_route");
@@ -381,6 +383,30 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
   // Routed experts see few tokens each (T*K/E on average), so one 16-token
   // MFMA column tile per block; groups with more tokens use extra z-tiles.
   const int tn = 1;
+  if (fused_flags) {
+    // a few tokens: router top-k, gate/up and down in one launch (the down
+    // blocks wait for their group's gate/up blocks inside the launch)
+    MoeFusedArgs f = {};
+    f.gu = dense_args(gate_up, hidden, H, 2 * I, H, T, w.hbuf, I);
+    f.gu.KW = H / 8;
+    f.gu.w_group_stride = (long long)2 * I * H;
+    f.gu.bias = gu_bias; f.gu.bias_group_stride = 2LL * I;
+    f.gu.act = act; f.gu.alpha = alpha; f.gu.gate_hi = ghi; f.gu.gate_lo = glo;
+    f.gu.up_hi = uhi; f.gu.up_lo = ulo;
+    f.gu.round_qwen = round_qwen;
+    f.gu.grp_expert = w.grp_expert;      // replaced by the block's own tables
+    f.dn = dense_args(down, w.hbuf, I, H, I, T, w.ybuf, H);
+    f.dn.w_group_stride = padded_rows(H) * I;
+    f.dn.bias = dn_bias; f.dn.bias_group_stride = H;
+    f.r = *sel;
+    f.flags = fused_flags; f.err = fused_err;
+    const int ps = prof_begin(MKD_KCLASS_MOE_GATE_UP, s);
+    MKD_TRY(moe_fused_launch(f, gmax, s), "moe router select + gate_up + down");
+    prof_end(ps, s);
+    if (do_finalize)
+      MKD_TRY(moe_finalize_launch(w.ybuf, T, K, H, resid, out, out_f32, s), "moe finalize");
+    return MKD_OK;
+  }
   {  // gate/up + activation
     GemmArgs a = dense_args(gate_up, hidden, H, 2 * I, H, T, w.hbuf, I);
     a.KW = gate_up_kw(H, I, gmax);
@@ -896,6 +922,7 @@ int mkd_attention_block_tkg(const mkd_attention_args* p, void* workspace, size_t
 // allow (its buffers are then always part of the workspace); used when the
 // decode path is set to it, otherwise every layer runs the multi-kernel sequence.
 static int g_decode_path = 0;   // 0 multi-kernel layers, 1 persistent layer kernel where eligible
+static int g_inlaunch_sync = 1;  // 1: stages joined into one launch (in-launch waits) where eligible
 
 static int lk_device_cus() {
   static int cus = -1;
@@ -1009,6 +1036,8 @@ static LkWs carve_lk(Carver& c, const mkd_qwen3_model* m, int B) {
 
 // K split of the output projection in the decode step: the LDS-staged GEMM's at
 // 17..128 tokens (partials added by the post-attention norm), else none.
+// K split of the output projection in the decode step: the LDS-staged GEMM's at
+// 17..128 tokens (partials added by the post-attention norm), else none.
 static int o_proj_kgrid(const mkd_qwen3_model* m, int B) {
   return std::max(1, gemm_mid_kgrid(m->H, m->nq * m->d, B));
 }
@@ -1019,6 +1048,11 @@ struct StepWs {
   float *nf32, *logits, *cos, *sin, *oparts;
   MoeWs moe;
   LkWs lk;
+  // in-launch synchronisation of the joined expert launch: word 0 the timeout
+  // word, then per layer that launch's flags (sync_words in all, cleared once
+  // per call)
+  unsigned* sync;
+  int sync_words, layer_words, flag_words;
 };
 
 static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
@@ -1033,6 +1067,10 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.oparts = c.take<float>((size_t)std::max(2, o_proj_kgrid(m, B)) * B * m->H);   // o_proj split-K partials
   w.moe = carve_moe(c, B, m->H, m->E, m->I, m->K);
   w.lk = carve_lk(c, m, B);
+  w.flag_words = moe_fused_supported(B, m->K, m->E, m->H, m->I) ? moe_fused_flag_words(B, m->K, m->E, m->I) : 0;
+  w.layer_words = w.flag_words;
+  w.sync_words = w.layer_words ? 64 + m->num_layers * w.layer_words : 0;
+  w.sync = w.sync_words ? c.take<unsigned>(w.sync_words) : nullptr;
   return w;
 }
 
@@ -1172,6 +1210,15 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
     MKD_TRY(rmsnorm_launch(x, 0, static_cast<const uint16_t*>(m->ln_in[0]), w.attn.hnorm, nullptr, B,
                            m->H, m->H, ha, m->eps, pre_order, s), "pre norm");
   const int o_kgrid = o_proj_kgrid(m, B);
+  // the fused MoE launch (router select + gate/up + down) where the select is
+  // deferred into the gate/up blocks and the shapes fit it
+  const int gmax_all = m->E < B * m->K ? m->E : B * m->K;
+  const int gu_kw_all = gate_up_kw(m->H, m->I, gmax_all);
+  const bool defer_ok = router_fused_supported(B, m->E, m->H) && !m->expert_format && gu_kw_all > 0 &&
+                        gemm_sel_supported(B, m->K, m->E, m->H / gu_kw_all) &&
+                        (long long)((2 * m->I + 31) / 32) * gmax_all <= 2LL * lk_device_cus();
+  const bool fused_moe = defer_ok && w.flag_words > 0 && g_inlaunch_sync && gu_kw_all * 8 == m->H;
+  if (fused_moe) MKD_TRY(sync_clear_launch(w.sync, w.sync_words, s), "clear sync words");
   for (int l = 0; l < m->num_layers; ++l) {
     const int wl = m->window ? m->window[l] : 0;
     mkd_attention_args ap;
@@ -1215,6 +1262,7 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
       qn.eps = m->eps; qn.inv_h = 1.0f / (float)ha;
       qn.resid_out = l == 0 ? nullptr : x;
     }
+    unsigned* lsync = w.sync ? w.sync + 64 + (size_t)l * w.layer_words : nullptr;
     if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s, w.oparts, o_kgrid,
                                 fuse_qn ? &qn : nullptr, prefill && !wl))
       return rc;
@@ -1235,8 +1283,6 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
     ra.n_groups = w.moe.n_groups; ra.grp_expert = w.moe.grp_expert;
     ra.grp_count = w.moe.grp_count; ra.grp_offset = w.moe.grp_offset;
     ra.pair_token = w.moe.pair_token; ra.pair_slot = w.moe.pair_slot;
-    const int gmax_l = m->E < B * m->K ? m->E : B * m->K;
-    const int gu_kw = gate_up_kw(m->H, m->I, gmax_l);
     RouterArgs sel;
     bool defer_sel = false;
     if (router_fused_supported(B, m->E, m->H)) {
@@ -1244,9 +1290,7 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
       // before its weight loads, so only when the whole grid is resident at once
       // (two blocks per CU); measured at 4 tokens (1536 blocks) the select launch
       // is cheaper than three rounds of in-block selection
-      const long long gu_blocks = (long long)((2 * m->I + 31) / 32) * gmax_l;
-      defer_sel = !m->expert_format && gu_kw > 0 && gemm_sel_supported(B, m->K, m->E, m->H / gu_kw) &&
-                  gu_blocks <= 2LL * lk_device_cus();
+      defer_sel = defer_ok;
       // a few tokens: the residual add and post norm are folded into the router
       // GEMM (each block forms the row norms itself), then the select launch
       RouterFusedArgs fa = {};
@@ -1311,7 +1355,9 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
                               gemm_tile_supported(m->H, m->I, EPI_SCALE_F32) &&
                               tile_offsets_ok(B, m->H, 2LL * m->I, m->H) &&
                               tile_offsets_ok((long long)B * m->K, m->I, m->H, m->I),
-                          defer_sel ? &sel : nullptr))
+                          defer_sel ? &sel : nullptr,
+                          fused_moe ? lsync : nullptr,
+                          fused_moe ? w.sync : nullptr))
       return rc;
     // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention
     // norm (with fuse_qn: the next QKV kernel does both; after the last layer the
@@ -1469,8 +1515,9 @@ int mkd_qwen3_write_layer_table(const mkd_qwen3_model* m, void* table, size_t ta
 }
 
 int mkd_set_decode_path(int mode) {
-  MKD_REQUIRE(mode == 0 || mode == 1, MKD_ERR_INVALID, "set_decode_path: mode %d must be 0 or 1", mode);
-  g_decode_path = mode;
+  MKD_REQUIRE(mode >= 0 && mode <= 2, MKD_ERR_INVALID, "set_decode_path: mode %d must be 0, 1 or 2", mode);
+  g_decode_path = mode == 1 ? 1 : 0;
+  g_inlaunch_sync = mode == 2 ? 0 : 1;
   return MKD_OK;
 }
 
@@ -1486,6 +1533,11 @@ int mkd_qwen3_layer_kernel_status(const mkd_qwen3_model* m, int B, const void* w
     unsigned e = 0;
     MKD_TRY(hipMemcpy(&e, w.lk.bar + kLkMaxNB, sizeof(e), hipMemcpyDeviceToHost), "read error word");
     *barrier_timeout = e ? 1 : 0;
+  }
+  if (w.sync) {   // the fused MoE launch's in-launch waits
+    unsigned e = 0;
+    MKD_TRY(hipMemcpy(&e, w.sync, sizeof(e), hipMemcpyDeviceToHost), "read sync word");
+    if (e) *barrier_timeout = 1;
   }
   return MKD_OK;
 }

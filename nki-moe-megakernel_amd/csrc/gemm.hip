@@ -24,6 +24,7 @@
 #include "gemm_epi.h"
 #include "mkd_internal.h"
 #include "router_select.h"
+#include "coherent.h"
 
 namespace mkd {
 
@@ -146,15 +147,16 @@ MKD_DEV void stream_batch(const uint16_t* const (&wrow)[RB], int f, int kb0, int
 // ---------------------------------------------------------------------------
 // The GEMM.
 // ---------------------------------------------------------------------------
-template <int RB, int TN, bool XF32, int EPI>
-MKD_DEV void frag_body(const GemmArgs& a) {
+// (rbase, group, bz): the block's RB-row-block tile, routed group, and token
+// tile * kgrid + K block -- blockIdx in the plain launch.  COH: the outputs are
+// stored device-coherent (read by other blocks of the same launch).
+template <int RB, int TN, bool XF32, int EPI, bool COH = false>
+MKD_DEV void frag_body(const GemmArgs& a, int rbase, int group, int bz) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int rbase = blockIdx.x;          // index of the RB-row-block tile
-  const int group = blockIdx.y;
   const int kg = a.kgrid > 1 ? a.kgrid : 1;
-  const int ttile = blockIdx.z / kg;
-  const int kblk = blockIdx.z % kg;
+  const int ttile = bz / kg;
+  const int kblk = bz % kg;
 
   // ---- token columns of this block ----
   int count, base;                       // tokens in this group / first pair
@@ -222,12 +224,12 @@ MKD_DEV void frag_body(const GemmArgs& a) {
   if constexpr (UNROLL > 1)
     if (f < NF) stream_batch<RB, TN, XF32, 1>(wrow, f, kb0, koff, xrow, a, acc);
 
-  gemm_finish<RB, TN, EPI>(a, acc, lane, wave, rbase, group, t0, base, xrow, kblk);
+  gemm_finish<RB, TN, EPI, COH>(a, acc, lane, wave, rbase, group, t0, base, xrow, kblk);
 }
 
 template <int RB, int TN, bool XF32, int EPI>
 __global__ void __launch_bounds__(1024) gemm_frag_kernel(GemmArgs a) {
-  frag_body<RB, TN, XF32, EPI>(a);
+  frag_body<RB, TN, XF32, EPI>(a, blockIdx.x, blockIdx.y, blockIdx.z);
 }
 
 // Grouped gate/up + SwiGLU with the router top-k folded in, for a few tokens
@@ -251,7 +253,10 @@ __global__ void __launch_bounds__(1024) gemm_frag_sel_kernel(GemmArgs a, RouterA
   q.grp_expert = s_gexp; q.grp_count = s_gcnt; q.grp_offset = s_goff;
   q.pair_token = s_ptok; q.pair_slot = s_pslot; q.slot_w = s_w;
   if (!lead) q.logits_out = nullptr, q.aff_full = nullptr, q.idx_out = nullptr, q.topk_out = nullptr;
-  select_small<PER>(q, [&](int t, float (&l)[PER]) { load_logits<PER>(q, t, lane, l); });
+  if (r.T == 1 && r.E <= 128 && 4 * r.E <= (int)blockDim.x)
+    select_one(q, [&](int t, float (&l)[2]) { load_logits<2>(q, t, lane, l); });
+  else
+    select_small<PER>(q, [&](int t, float (&l)[PER]) { load_logits<PER>(q, t, lane, l); });
   __syncthreads();
   if (lead) {
     const int ng = s_ng, np = r.T * r.K;
@@ -271,7 +276,134 @@ __global__ void __launch_bounds__(1024) gemm_frag_sel_kernel(GemmArgs a, RouterA
   b.n_groups = &s_ng;
   b.grp_expert = s_gexp; b.grp_count = s_gcnt; b.grp_offset = s_goff;
   b.pair_row = s_ptok; b.pair_out_row = s_pslot;
-  frag_body<2, 1, false, EPI_SWIGLU_BF16>(b);
+  frag_body<2, 1, false, EPI_SWIGLU_BF16>(b, blockIdx.x, blockIdx.y, blockIdx.z);
+}
+
+// Gate/up and down of the routed experts in ONE launch for a few tokens
+// (moe_tkg.py selective experts; the router top-k as in gemm_frag_sel_kernel).
+// Blocks [0, ngu) are the gate/up tiles of gemm_frag_sel_kernel (tile =
+// bid % n_gu, group = bid / n_gu); they store their SwiGLU columns of h
+// device-coherent and then set their flag word.  Blocks [ngu, ngu + gmax * ndb)
+// take 64 output rows of one group's down projection: they form the routing
+// themselves like every block, issue their whole weight slice (8 waves = 4 row
+// blocks x 2 K halves, NFD fragments each) right away, then wait until all n_gu
+// flags of their group are set, read that group's h rows device-coherent and
+// finish -- the down weights stream while the gate/up blocks run, and the
+// kernel boundary between the two projections is gone.  Workgroups are
+// dispatched in index order and the gate/up blocks wait on nothing, so every
+// awaited block is already resident; the waits are bounded regardless
+// (coh_wait_all).
+template <int PER, int NFD>
+__global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(6))) moe_fused_kernel(MoeFusedArgs f) {
+  __shared__ int s_ng;
+  __shared__ int s_gexp[kSelMaxPairs], s_gcnt[kSelMaxPairs], s_goff[kSelMaxPairs];
+  __shared__ int s_ptok[kSelMaxPairs], s_pslot[kSelMaxPairs];
+  __shared__ float s_w[kSelMaxPairs];
+  __shared__ f32x4_t s_red[4][64];
+  __shared__ u32x4_t s_h[kFusedMaxRows][NFD * 8];   // h rows of a down block's group
+  const int bid = blockIdx.x;
+  const bool lead = bid == 0;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const RouterArgs& r = f.r;
+  RouterArgs q = r;
+  q.n_groups = &s_ng;
+  q.grp_expert = s_gexp; q.grp_count = s_gcnt; q.grp_offset = s_goff;
+  q.pair_token = s_ptok; q.pair_slot = s_pslot; q.slot_w = s_w;
+  if (!lead) q.logits_out = nullptr, q.aff_full = nullptr, q.idx_out = nullptr, q.topk_out = nullptr;
+  const bool gu_role = bid < f.ngu;
+  // a down block's weight slice does not depend on the routing: its row block
+  // and K half are fixed, only the expert offset is not -- so the routing comes
+  // first, then the loads
+  if (r.T == 1 && r.E <= 128 && 4 * r.E <= (int)blockDim.x)
+    select_one(q, [&](int t, float (&l)[2]) { load_logits<2>(q, t, lane, l); });
+  else
+    select_small<PER>(q, [&](int t, float (&l)[PER]) { load_logits<PER>(q, t, lane, l); });
+  __syncthreads();
+  if (lead) {
+    const int ng = s_ng, np = r.T * r.K;
+    if (threadIdx.x == 0) *r.n_groups = ng;
+    for (int i = threadIdx.x; i < ng; i += blockDim.x) {
+      r.grp_expert[i] = s_gexp[i];
+      r.grp_count[i] = s_gcnt[i];
+      r.grp_offset[i] = s_goff[i];
+    }
+    for (int i = threadIdx.x; i < np; i += blockDim.x) {
+      r.pair_token[i] = s_ptok[i];
+      r.pair_slot[i] = s_pslot[i];
+      if (r.slot_w) r.slot_w[i] = s_w[i];
+    }
+  }
+  if (gu_role) {
+    GemmArgs b = f.gu;
+    b.n_groups = &s_ng;
+    b.grp_expert = s_gexp; b.grp_count = s_gcnt; b.grp_offset = s_goff;
+    b.pair_row = s_ptok; b.pair_out_row = s_pslot;
+    frag_body<2, 1, false, EPI_SWIGLU_BF16, true>(b, bid % f.n_gu, bid / f.n_gu, 0);
+    coh_publish(f.flags + bid);
+    return;
+  }
+  // ---- down role ----
+  const GemmArgs& d = f.dn;
+  const int db = bid - f.ngu;
+  const int g = db / f.ndb, qd = db - g * f.ndb;
+  if (g >= s_ng) return;
+  const int ex = s_gexp[g], count = s_gcnt[g], base = s_goff[g];
+  const int KB = d.K / 32;
+  const int rbk = qd * 4 + (wave & 3);       // 16-row block of the output
+  const int kh = wave >> 2;                  // K half
+  const int kb0 = kh * NFD;
+  const uint16_t* wrow = d.w + (long long)ex * d.w_group_stride + ((long long)rbk * KB + kb0) * 512 + lane * 8;
+  u32x4_t wf[NFD];
+#pragma unroll
+  for (int u = 0; u < NFD; ++u)
+    wf[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + u * 512));
+  const int c = lane & 15;
+  const int prow = c < count ? s_pslot[base + c] : -1;   // h row and output row of the column
+  if (wave == 0) coh_wait_all(f.flags + g * f.n_gu, f.n_gu, f.err);
+  __syncthreads();
+  // the group's h rows (count <= kFusedMaxRows, K = 64 NFD) into LDS with one
+  // device-coherent 16-byte load per thread, then the B operands from LDS
+  {
+    const __amdgpu_buffer_rsrc_t hr = coh_rsrc(d.x);
+    const int per_row = d.K / 8;                       // 16-byte pieces per row
+    for (int i = threadIdx.x; i < count * per_row; i += blockDim.x) {
+      const int rr = i / per_row, pc = i - rr * per_row;
+      const int row = s_pslot[base + rr];
+      s_h[rr][pc] = coh_ld16(hr, (int)(((long long)row * d.ldx + pc * 8) * 2));
+    }
+  }
+  __syncthreads();
+  // B operands four at a time (the weights already hold NFD * 4 registers)
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u0 = 0; u0 < NFD; u0 += 4) {
+    u32x4_t xv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      xv[j] = c < count ? s_h[c][(kb0 + u0 + j) * 4 + (lane >> 4)] : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc = mfma16x16x32(wf[u0 + j], xv[j], acc);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (kh == 1) s_red[wave & 3][lane] = acc;
+  __syncthreads();
+  if (kh != 0 || prow < 0) return;
+  const f32x4_t hi = s_red[wave][lane];
+  const int n0 = rbk * 16 + (lane >> 4) * 4;
+  const float sc = s_w[prow];
+  float o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float v = acc[i] + hi[i];
+    if (d.bias) v += bf2f(d.bias[(long long)ex * d.bias_group_stride + n0 + i]);
+    o[i] = v * sc;
+  }
+  *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(d.y) + (long long)prow * d.ldy + n0) =
+      f32x4_t{o[0], o[1], o[2], o[3]};
+}
+
+__global__ void sync_clear_kernel(unsigned* p, int n) {
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -306,6 +438,48 @@ hipError_t gemm_sel_launch(const GemmArgs& a, const RouterArgs& r, int groups_ma
   if (per <= 1) return timed_launch(gemm_frag_sel_kernel<1>, grid, block, lds, s, a, r);
   if (per <= 2) return timed_launch(gemm_frag_sel_kernel<2>, grid, block, lds, s, a, r);
   return timed_launch(gemm_frag_sel_kernel<4>, grid, block, lds, s, a, r);
+}
+
+bool moe_fused_supported(int T, int K, int E, int H, int I) {
+  const int KB = I / 32;
+  return T >= 1 && T <= kFusedMaxRows && T * K <= kSelMaxPairs && K >= 1 && K <= 8 && K <= E && E <= 256 &&
+         H % 256 == 0 && H % 64 == 0 && I % 64 == 0 && (KB / 2 == 12 || KB / 2 == 8) &&
+         (2 * I) % 32 == 0 && (2 * I) / 32 <= 256;
+}
+
+int moe_fused_flag_words(int T, int K, int E, int I) {
+  const int gmax = E < T * K ? E : T * K;
+  return gmax * ((2 * I) / 32);
+}
+
+hipError_t moe_fused_launch(MoeFusedArgs f, int groups_max, hipStream_t s) {
+  const RouterArgs& r = f.r;
+  const GemmArgs& a = f.gu;
+  if (!moe_fused_supported(r.T, r.K, r.E, a.K, f.dn.K) || a.T != r.T || f.dn.N != a.K ||
+      a.N != 2 * f.dn.K || a.KW * 8 != a.K || a.kgrid > 1 || !r.parts || r.nparts < 1 ||
+      r.nparts > 16 || !r.n_groups || !r.grp_expert || !r.grp_count || !r.grp_offset ||
+      !r.pair_token || !r.pair_slot || !a.grp_expert || !f.flags || !f.err || groups_max < 1 ||
+      groups_max > kSelMaxPairs || (f.dn.ldx & 7) || (f.dn.ldy & 3))
+    return hipErrorInvalidValue;
+  f.n_gu = a.N / 32;
+  f.ngu = f.n_gu * groups_max;
+  f.ndb = f.dn.N / 64;
+  const dim3 grid(f.ngu + f.ndb * groups_max), block(512);
+  const size_t lds = (size_t)8 * 2 * 4 * 64 * sizeof(float);
+  const int per = (r.E + 63) / 64;
+  const int nfd = (f.dn.K / 32) / 2;
+#define MKD_FUSED(P, N) if (per <= P && nfd == N) return timed_launch(moe_fused_kernel<P, N>, grid, block, lds, s, f)
+  MKD_FUSED(1, 8); MKD_FUSED(1, 12);
+  MKD_FUSED(2, 8); MKD_FUSED(2, 12);
+  MKD_FUSED(4, 8); MKD_FUSED(4, 12);
+#undef MKD_FUSED
+  return hipErrorInvalidValue;
+}
+
+hipError_t sync_clear_launch(unsigned* p, int n, hipStream_t s) {
+  if (n <= 0) return hipSuccess;
+  hipLaunchKernelGGL(sync_clear_kernel, dim3((n + 255) / 256 < 64 ? (n + 255) / 256 : 64), dim3(256), 0, s, p, n);
+  return hipGetLastError();
 }
 
 int choose_kw(int K, int max_kw, long long blocks) {

@@ -13,6 +13,7 @@
 #pragma once
 #include "common.h"
 #include "mkd_internal.h"
+#include "coherent.h"
 
 namespace mkd {
 
@@ -30,7 +31,7 @@ MKD_DEV float swiglu_value(const GemmArgs& a, float gv, float uv) {
   return (g / (1.0f + expf(-z))) * u;
 }
 
-template <int RB, int TN, int EPI>
+template <int RB, int TN, int EPI, bool COH = false>
 MKD_DEV void gemm_finish(const GemmArgs& a, f32x4_t (&acc)[RB][TN], int lane, int wave, int rbase,
                          int group, int t0, int base, const int (&xrow)[TN], int kblk) {
   // ---- cross-wave reduction (fixed order) ----
@@ -113,7 +114,16 @@ MKD_DEV void gemm_finish(const GemmArgs& a, f32x4_t (&acc)[RB][TN], int lane, in
       }
     } else {
       uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n0;
-      if (vec) {
+      if (COH) {   // read back by other blocks of this launch
+        const __amdgpu_buffer_rsrc_t yr = coh_rsrc(a.y);
+        const int off = (int)(((long long)orow * a.ldy + n0) * 2);
+        if (vec) {
+          coh_st8(yr, off, pack2bf(o[0], o[1]), pack2bf(o[2], o[3]));
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) if (i < nv) coh_st2(yr, off + 2 * i, (uint16_t)f2bf(o[i]));
+        }
+      } else if (vec) {
         *reinterpret_cast<uint2*>(y) = uint2{pack2bf(o[0], o[1]), pack2bf(o[2], o[3])};
       } else {
 #pragma unroll

@@ -642,7 +642,7 @@ MKD_DEV void attn_unit(const LayerArgs& L, const LkLayer& ly, const AttnArgs& aa
         const int i = l + e * HD;
         const int row = head * D + i;
         q.xr[e] = __float_as_uint(part_sum1(L.q, cq, row >> 4, b, row & 15));
-        q.nr[e] = nw ? nw[i] : 0;
+        q.nr[e] = nw ? *reinterpret_cast<const uint32_t*>(nw + (i & ~1)) : 0;   // HeadPrep's dword
         q.cs[e] = L.cos[b * D + i];
         q.sn[e] = L.sin[b * D + i];
       }

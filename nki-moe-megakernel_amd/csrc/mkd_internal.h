@@ -305,6 +305,21 @@ hipError_t router_fused_launch(RouterFusedArgs a, hipStream_t s, RouterArgs* def
 // router top-k and expert groups themselves from r's partial logits; r's group
 // tables and slot weights are written for the down projection.
 constexpr int kSelMaxPairs = 64;
+// Gate/up + down in one launch (gemm.hip, moe_fused_kernel): the gate/up blocks
+// publish their h columns through flags[group * n_gu + tile] (zero at launch),
+// the down blocks wait on their group's flags; *err is set when a wait ran out.
+constexpr int kFusedMaxRows = 4;   // tokens of the fused expert launch (rows per group)
+struct MoeFusedArgs {
+  GemmArgs gu, dn;
+  RouterArgs r;
+  unsigned* flags;
+  unsigned* err;
+  int n_gu, ngu, ndb;   // set by moe_fused_launch
+};
+bool moe_fused_supported(int T, int K, int E, int H, int I);
+int moe_fused_flag_words(int T, int K, int E, int I);
+hipError_t moe_fused_launch(MoeFusedArgs f, int groups_max, hipStream_t s);
+hipError_t sync_clear_launch(unsigned* p, int n, hipStream_t s);
 bool gemm_sel_supported(int T, int K, int E, int nsplit);
 hipError_t gemm_sel_launch(const GemmArgs& a, const RouterArgs& r, int groups_max, hipStream_t s);
 hipError_t moe_route_launch(const int* idx, int T, int K, int E, int* n_groups, int* grp_expert,

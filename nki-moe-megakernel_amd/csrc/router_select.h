@@ -419,4 +419,118 @@ MKD_DEV void select_small(const RouterArgs& a, Load&& load) {
   }
 }
 
+
+// select_small for ONE token, spread over the whole block (blockDim.x >= 4 E,
+// a multiple of 64): wave 0 forms the logits, the softmax statistics and the
+// keys exactly as select_small does, the keys' order codes go to LDS, and every
+// expert's rank -- #{valid e' : code[e'] > code[e] or (code[e'] == code[e] and
+// e' < e)}, the order select_small's K rounds of wave-wide max produce -- is
+// counted by four threads over a quarter of the experts each, summed with two
+// DPP steps.  The expert of rank r < K lands in LDS slot r; wave 0 then forms
+// the routing weights as select_small does (same operations, same order).
+// With one token every pair is its own group, so the groups are listed in
+// rank order: group r = expert of rank r, one row (token 0), pair slot r --
+// no sort, and nothing downstream depends on the groups' order.  The caller
+// synchronises the block before reading the group tables.
+template <class Load>
+MKD_DEV void select_one(const RouterArgs& a, Load&& load) {
+  constexpr int PER = 2;                   // E <= 128
+  __shared__ __attribute__((aligned(16))) uint32_t code_s[128];
+  __shared__ float key_s[128];
+  __shared__ int sel_s[8];
+  __shared__ float stat_s[2];              // max, 1 / sum of exp
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int E = a.E, K = a.K;
+  const bool sigm = a.mode & 1, pre = a.mode & 2, norm = a.mode & 4, qwen = a.mode & 8;
+  if (wv == 0) {
+    float l[PER];
+    load(0, l);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E) {
+        if (a.logits_out) a.logits_out[e] = l[j];
+      } else {
+        l[j] = -INFINITY;
+      }
+      mx = fmaxf(mx, l[j]);
+    }
+    mx = wave_max(mx);
+    float sum = 0.f, ex[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      ex[j] = (lane + 64 * j < E) ? expf(l[j] - mx) : 0.f;
+      sum += ex[j];
+    }
+    sum = wave_sum(sum);
+    const float inv = 1.0f / sum;
+#pragma unroll
+    for (int j = 0; j < PER; ++j) {
+      const float key = (qwen || !pre) ? l[j] : (sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv);
+      code_s[lane + 64 * j] = order_code(key);
+      key_s[lane + 64 * j] = key;
+    }
+    if (lane == 0) {
+      stat_s[0] = mx;
+      stat_s[1] = inv;
+    }
+  }
+  __syncthreads();
+  {
+    // the quarter's 32 codes with eight 16-byte LDS reads issued together
+    const int e = tid >> 2, qtr = tid & 3;
+    int rank = 0;
+    if (e < E) {
+      const uint32_t ue = code_s[e];
+      const u32x4_t* cq = reinterpret_cast<const u32x4_t*>(code_s + qtr * 32);
+      u32x4_t c[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) c[i] = cq[i];
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int f = qtr * 32 + i * 4 + j;
+          rank += f < E && ((c[i][j] > ue) || (c[i][j] == ue && f < e));
+        }
+    }
+    rank += __builtin_amdgcn_update_dpp(0, rank, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+    rank += __builtin_amdgcn_update_dpp(0, rank, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+    if (e < E && qtr == 0 && rank < K) sel_s[rank] = e;
+  }
+  __syncthreads();
+  if (wv == 0) {
+    const float mx = stat_s[0], inv = stat_s[1];
+    const int my_e = lane < K ? sel_s[lane] : 0;
+    const float my_key = lane < K ? key_s[my_e] : 0.f;
+    const float k0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_key), 0));
+    float pv;
+    if (qwen) pv = rbf(expf(my_key - mx) * inv);
+    else if (pre) pv = my_key;
+    else if (sigm) pv = 1.0f / (1.0f + expf(-my_key));
+    else pv = expf(my_key - k0);
+    float w = pv;
+    if (qwen || (pre && norm) || (!pre && !sigm)) {
+      float s = 0.f;
+      for (int k = 0; k < K; ++k)
+        s += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), k));
+      w = qwen ? rbf(pv * (1.0f / s)) : pv * (1.0f / s);
+    }
+    if (lane < K) {
+      if (a.idx_out) a.idx_out[lane] = my_e;
+      if (a.topk_out) a.topk_out[lane] = w;
+      if (a.slot_w) a.slot_w[lane] = w;
+      if (a.n_groups) {
+        a.grp_expert[lane] = my_e;
+        a.grp_count[lane] = 1;
+        a.grp_offset[lane] = lane;
+        a.pair_token[lane] = 0;
+        a.pair_slot[lane] = lane;
+      }
+    }
+    if (lane == 0 && a.n_groups) *a.n_groups = K;
+  }
+}
+
 }  // namespace mkd

@@ -33,9 +33,13 @@ from . import packing
 
 def set_decode_path(mode: str = "multi_kernel") -> None:
     """Decode-layer execution (process-global): "multi_kernel" (default) runs
-    each layer as the per-stage kernel sequence; "persistent" runs each layer
-    as one persistent kernel launch where the model and batch allow it."""
-    modes = {"multi_kernel": 0, "persistent": 1}
+    each layer as a short kernel sequence (at one token with bf16 experts the
+    router top-k, gate/up and down projections share one launch, the down
+    blocks waiting inside it for their expert's gate/up blocks); "persistent"
+    runs each layer as one persistent kernel launch where the model and batch
+    allow it; "separate_launches" is "multi_kernel" with every stage a launch
+    of its own."""
+    modes = {"multi_kernel": 0, "persistent": 1, "separate_launches": 2}
     if mode not in modes:
         raise ValueError(f"decode path {mode!r} not in {sorted(modes)}")
     L.check(L.load().mkd_set_decode_path(modes[mode]), "set_decode_path")
