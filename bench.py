@@ -92,6 +92,18 @@ def prefill_kv(model, cfg, ctx, seed, dev):
                 t[:, :, :ctx].copy_(torch.randn(t[:, :, :ctx].shape, generator=g, device=dev))
 
 
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or None."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(cfg, lens, seconds_budget=20.0):
     """Time the CPU oracle's decode step on host cores (bounded sample).
 
@@ -160,7 +172,7 @@ def cpu_baseline(cfg, lens, seconds_budget=20.0):
         step_s = t_layers * L / n + t_lm
         sample = (f"one pass of {n} of {L} layers at bs={B} of the fp32 torch oracle, scaled by "
                   f"{L}/{n}, + lm_head")
-    return {"value": B / step_s, "unit": "tok/s", "cores": cores, "kind": "port",
+    return {"value": B / step_s, "unit": "tok/s", "cores": cores, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"{sample}, KV lengths mean {float(lens.float().mean()):.0f} "
                       f"({n_distinct} distinct layers' weights reused for all layer slots), "
                       f"{t_total:.1f} s on {cores} host threads"}
@@ -213,7 +225,7 @@ def cpu_baseline_gpt_oss(cfg, lens, seconds_budget=20.0):
     ref.final_norm_lm_head(x, torch.ones(cfg.hidden_size, dtype=torch.bfloat16), lm, cfg.rms_norm_eps)
     t_lm = time.perf_counter() - t0
     step_s = t_layers * L / n + t_lm
-    return {"value": B / step_s, "unit": "tok/s", "cores": cores, "kind": "port",
+    return {"value": B / step_s, "unit": "tok/s", "cores": cores, "kind": "port", "cpu_model": cpu_model(),
             "sample": f"{n} of {L} GPT-OSS layers at bs={B} of the fp32 torch oracle (bf16 experts), "
                       f"scaled by {L}/{n}, + lm_head; KV lengths mean {float(lens.float().mean()):.0f}; "
                       f"{t_layers + t_lm:.1f} s on {cores} host threads"}
@@ -333,28 +345,34 @@ def main():
         run = step
     for _ in range(args.warmup):
         run()
-    t_start = torch.cuda.Event(enable_timing=True)
-    t_end = torch.cuda.Event(enable_timing=True)
+    # one event between consecutive steps: the whole region and every step's own time
+    marks = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     torch.cuda.synchronize()
     w0 = time.perf_counter()
-    t_start.record()
+    marks[0].record()
     for i in range(args.steps):
         run()
-    t_end.record()
+        marks[i + 1].record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
-    ms_total = t_start.elapsed_time(t_end)
+    ms_total = marks[0].elapsed_time(marks[-1])
     ms_step = ms_total / args.steps
     tok_s = B * args.steps / (ms_total / 1e3)
+    per_step = sorted(a.elapsed_time(b) for a, b in zip(marks[:-1], marks[1:]))
+    ms_median = per_step[len(per_step) // 2] if len(per_step) % 2 else \
+        0.5 * (per_step[len(per_step) // 2 - 1] + per_step[len(per_step) // 2])
+    ms_p99 = per_step[min(len(per_step) - 1, int(math.ceil(0.99 * len(per_step))) - 1)]
 
     # Dominant kernel: the persistent layer kernel when the step runs one launch
     # per layer, else the MoE gate/up GEMM.  HIP events recorded by each of its
     # dispatch packets on the launch stream (hipExtLaunchKernel), so a pair
     # times the kernel alone, in one eager step right after the timed region (a
     # captured graph keeps no timing events).
-    layer_kernel = (not oss) and model.layer_kernel_status(B)[0]
-    if layer_kernel and model.layer_kernel_status(B)[1]:
-        raise RuntimeError("a grid barrier of the persistent layer kernel timed out")
+    plan = model.decode_plan(B)
+    layer_kernel = plan == "persistent"
+    joined = plan == "joined_experts"      # gate/up and down in one launch
+    if model.layer_kernel_status(B)[1]:
+        raise RuntimeError("an in-launch wait (grid barrier or expert flags) timed out")
     kcls = "layer" if layer_kernel else "moe_gate_up"
     n_prof = 1 if layer_kernel else n_ev      # the persistent kernel: one launch for all layers
     L.check(lib.mkd_profile_events(L.KCLASS[kcls], arr(ev_s), arr(ev_e), n_prof), "profile_events")
@@ -372,9 +390,10 @@ def main():
     distinct = E * (1 - (1 - K / E) ** B) if B > 1 else K
     # bytes per expert weight element: bf16 2; MX codes + one scale byte per 32
     wbytes = {"bf16": 2.0, "mxfp8": 1.0 + 1 / 32, "mxfp4": 0.5 + 1 / 32}[args.experts]
-    alg_bytes = distinct * 2 * I * H * wbytes
+    n_mats = 3 if joined else 2                       # gate + up (+ down when joined)
+    alg_bytes = distinct * n_mats * I * H * wbytes
     achieved = alg_bytes / (avg_ms / 1e3) / 1e9
-    gu_flops = 2.0 * B * K * 2 * I * H                 # one gate/up launch
+    gu_flops = 2.0 * B * K * n_mats * I * H            # one launch
     gu_tflops = gu_flops / (avg_ms / 1e3) / 1e12
     # dense MFMA peaks: bf16 2.5, MXFP8 5.0, MXFP4 10.1 PFLOP/s
     mfma_peak = {"bf16": MFMA_BF16_PEAK_TFLOPS, "mxfp8": 5000.0, "mxfp4": 10100.0}[args.experts]
@@ -409,7 +428,9 @@ def main():
     out = {
         "metric": "decode tok/s/GPU, Qwen3-30B-A3B shape bs=1/16/64; % of HBM & MFMA roofline",
         "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_step, 4), "higher_is_better": True,
+        "warmup": args.warmup, "ms_per_step": round(ms_step, 4),
+        "ms_per_step_median": round(ms_median, 4), "ms_per_step_p99": round(ms_p99, 4),
+        "higher_is_better": True,
         "scaling": "weak", "vs_baseline": vs_baseline(tok_s, cfg, B, ctx, args), "dtype": "bf16",
         "data": "synthetic (seeded random bf16 weights N(0,0.02)" +
                 (f", experts quantised to {args.experts}" if args.experts != "bf16" else "") +
@@ -428,13 +449,16 @@ def main():
         "roofline": {"bound": "hbm",
                      "kernel": ("persistent decoder (layer_kernel<%d,%d>), one launch for all layers"
                                 % (cfg.head_dim, 2 if cfg.num_experts <= 128 else 8)) if layer_kernel else
+                               ("moe_fused_kernel: router top-k, grouped gate/up + SwiGLU and down in one "
+                                "launch (down blocks wait in-launch for their expert's gate/up blocks)")
+                               if joined else
                                "moe gate_up grouped GEMM (" + (
                                    "gemm_mx_kernel<2,fmt,3>" if args.experts != "bf16" else
                                    "gemm_frag_sel_kernel<2>: router top-k formed in every block"
                                    if B == 1 and not oss else "gemm_frag_kernel<2,1,0,3>") + ")",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers, kcls)
+                     "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers, kcls, joined)
                      if (args.model == "qwen3" and args.experts == "bf16" and not args.ragged
                          and not args.kv_block) else None,
                      "avg_us": round(avg_ms * 1e3, 2), "bytes_per_launch": int(alg_bytes)},
@@ -622,10 +646,11 @@ def workload_name(cfg, B, ctx, lens, args):
             f"{args.experts} experts{tag}")
 
 
-def measured_traffic(B, ctx, layers, kcls="moe_gate_up"):
+def measured_traffic(B, ctx, layers, kcls="moe_gate_up", joined=False):
     """HBM bytes per launch of the dominant kernel from the committed counter
     summary for that kernel and workload, or None."""
-    name = "layer_kernel_traffic.json" if kcls == "layer" else "gate_up_traffic.json"
+    name = "layer_kernel_traffic.json" if kcls == "layer" else (
+        "moe_joined_traffic.json" if joined else "gate_up_traffic.json")
     path = os.path.join(ROOT, "profiles", name)
     try:
         with open(path) as f:

@@ -432,6 +432,13 @@ int mkd_set_decode_path(int mode);
  * bytes); set m->layer_table to it to enable the persistent decode path. */
 size_t mkd_qwen3_layer_table_bytes(const mkd_qwen3_model* m);
 int mkd_qwen3_write_layer_table(const mkd_qwen3_model* m, void* table, size_t table_bytes);
+/* Which decode path mkd_qwen3_decode_layers takes for m and B tokens under the
+ * current mode (no counterpart in the reference): *plan = MKD_PLAN_PERSISTENT
+ * (one persistent launch for all layers) or MKD_PLAN_JOINED_EXPERTS (the
+ * multi-kernel layers with gate/up and down in one launch), else 0. */
+#define MKD_PLAN_PERSISTENT 1
+#define MKD_PLAN_JOINED_EXPERTS 2
+int mkd_qwen3_decode_plan(const mkd_qwen3_model* m, int B, int* plan);
 int mkd_qwen3_layer_kernel_status(const mkd_qwen3_model* m, int B, const void* workspace,
                                   size_t workspace_bytes, int* used, int* barrier_timeout);
 

@@ -1132,6 +1132,22 @@ size_t mkd_qwen3_workspace_bytes(const mkd_qwen3_model* m, int B) {
 
 // prefill_seq >= 0: the B tokens are consecutive tokens of sequence prefill_seq
 // (context encoding); < 0: one token of each of B sequences (decode).
+// The router top-k formed inside the gate/up blocks (a few tokens, bf16 experts,
+// the whole gate/up grid resident at once) ...
+static bool defer_select_ok(const mkd_qwen3_model* m, int B) {
+  const int gmax = m->E < B * m->K ? m->E : B * m->K;
+  const int kw = gate_up_kw(m->H, m->I, gmax);
+  return router_fused_supported(B, m->E, m->H) && !m->expert_format && kw > 0 &&
+         gemm_sel_supported(B, m->K, m->E, m->H / kw) &&
+         (long long)((2 * m->I + 31) / 32) * gmax <= 2LL * lk_device_cus();
+}
+// ... and then gate/up and down joined in one launch (mode 0).
+static bool joined_experts_planned(const mkd_qwen3_model* m, int B) {
+  const int gmax = m->E < B * m->K ? m->E : B * m->K;
+  return g_inlaunch_sync && defer_select_ok(m, B) && moe_fused_supported(B, m->K, m->E, m->H, m->I) &&
+         gate_up_kw(m->H, m->I, gmax) * 8 == m->H;
+}
+
 static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const int* position_ids,
                          const float* cos, const float* sin, void* workspace,
                          size_t workspace_bytes, void* stream, int prefill_seq) {
@@ -1210,14 +1226,10 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
     MKD_TRY(rmsnorm_launch(x, 0, static_cast<const uint16_t*>(m->ln_in[0]), w.attn.hnorm, nullptr, B,
                            m->H, m->H, ha, m->eps, pre_order, s), "pre norm");
   const int o_kgrid = o_proj_kgrid(m, B);
-  // the fused MoE launch (router select + gate/up + down) where the select is
-  // deferred into the gate/up blocks and the shapes fit it
-  const int gmax_all = m->E < B * m->K ? m->E : B * m->K;
-  const int gu_kw_all = gate_up_kw(m->H, m->I, gmax_all);
-  const bool defer_ok = router_fused_supported(B, m->E, m->H) && !m->expert_format && gu_kw_all > 0 &&
-                        gemm_sel_supported(B, m->K, m->E, m->H / gu_kw_all) &&
-                        (long long)((2 * m->I + 31) / 32) * gmax_all <= 2LL * lk_device_cus();
-  const bool fused_moe = defer_ok && w.flag_words > 0 && g_inlaunch_sync && gu_kw_all * 8 == m->H;
+  // the joined expert launch (router select + gate/up + down) where the select
+  // is deferred into the gate/up blocks and the shapes fit it
+  const bool defer_ok = defer_select_ok(m, B);
+  const bool fused_moe = joined_experts_planned(m, B) && w.flag_words > 0;
   if (fused_moe) MKD_TRY(sync_clear_launch(w.sync, w.sync_words, s), "clear sync words");
   for (int l = 0; l < m->num_layers; ++l) {
     const int wl = m->window ? m->window[l] : 0;
@@ -1518,6 +1530,16 @@ int mkd_set_decode_path(int mode) {
   MKD_REQUIRE(mode >= 0 && mode <= 2, MKD_ERR_INVALID, "set_decode_path: mode %d must be 0, 1 or 2", mode);
   g_decode_path = mode == 1 ? 1 : 0;
   g_inlaunch_sync = mode == 2 ? 0 : 1;
+  return MKD_OK;
+}
+
+int mkd_qwen3_decode_plan(const mkd_qwen3_model* m, int B, int* plan) {
+  MKD_REQUIRE(m && plan, MKD_ERR_NULL, "decode_plan: null pointer");
+  MKD_REQUIRE(B > 0 && B <= 128, MKD_ERR_INVALID, "decode_plan: %d tokens must be in [1, 128]", B);
+  int p = 0;
+  if (g_decode_path == 1 && lk_plan(m, B).on) p |= MKD_PLAN_PERSISTENT;
+  else if (joined_experts_planned(m, B)) p |= MKD_PLAN_JOINED_EXPERTS;
+  *plan = p;
   return MKD_OK;
 }
 

@@ -155,7 +155,6 @@ MKD_DEV void frag_body(const GemmArgs& a, int rbase, int group, int bz) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int kg = a.kgrid > 1 ? a.kgrid : 1;
-  const int ttile = bz / kg;
   const int kblk = bz % kg;
 
   // ---- token columns of this block ----
@@ -175,8 +174,10 @@ MKD_DEV void frag_body(const GemmArgs& a, int rbase, int group, int bz) {
     count = a.T;
     base = 0;
   }
+  for (int ttile = bz / kg;; ++ttile) {
   const int t0 = ttile * 16 * TN;
   if (t0 >= count) return;
+  if (ttile > bz / kg) __syncthreads();   // the previous tile's reduction buffer is free
 
   // x row of each token column owned by this lane (one column per TN tile)
   int xrow[TN];
@@ -225,6 +226,8 @@ MKD_DEV void frag_body(const GemmArgs& a, int rbase, int group, int bz) {
     if (f < NF) stream_batch<RB, TN, XF32, 1>(wrow, f, kb0, koff, xrow, a, acc);
 
   gemm_finish<RB, TN, EPI, COH>(a, acc, lane, wave, rbase, group, t0, base, xrow, kblk);
+  if (!a.t_loop) return;
+  }
 }
 
 template <int RB, int TN, bool XF32, int EPI>
@@ -515,8 +518,12 @@ hipError_t gemm_launch(GemmArgs a, int epi, bool xf32, int tn, int groups_max,
                        int max_tokens_per_group, hipStream_t s) {
   const int RB = (epi == EPI_SWIGLU_BF16) ? 2 : 1;
   const int n_tiles = (a.N + 16 * RB - 1) / (16 * RB);
-  const int ttiles = (max_tokens_per_group + 16 * tn - 1) / (16 * tn);
+  int ttiles = (max_tokens_per_group + 16 * tn - 1) / (16 * tn);
   const int groups = a.grp_expert ? groups_max : 1;
+  if (a.grp_expert && ttiles > 1 && (a.kgrid <= 1)) {   // grouped: one tile per block, walking the group
+    a.t_loop = 1;
+    ttiles = 1;
+  }
 #define MKD_G(RB_, TN_, XF_, EPI_) \
   if (RB == RB_ && tn == TN_ && xf32 == XF_ && epi == EPI_) return launch_t<RB_, TN_, XF_, EPI_>(a, n_tiles, groups, ttiles, s);
   MKD_G(1, 1, false, EPI_F32) MKD_G(1, 2, false, EPI_F32) MKD_G(1, 4, false, EPI_F32)

@@ -181,9 +181,9 @@ MKD_DEV void grid_wait(const LayerArgs& L, int k) {
 // + 1 (Granlund-Montgomery, "Division by invariant integers using
 // multiplication", 1994).  m is formed in double precision: the numerator
 // (< 2^52) is exact, and for d < 2^20 the quotient lies at least one ulp from
-// an integer, so the rounded quotient floors to the exact one (checked on the
-// host for every d < 2^20 against integer arithmetic) -- far cheaper than an
-// emulated 64-bit integer division.
+// an integer, so the rounded quotient floors to the exact one
+// (tests/test_fdiv_magic.py checks every d < 2^20 against integer arithmetic)
+// -- far cheaper than an emulated 64-bit integer division.
 struct FDiv {
   uint32_t m, s, d;
 };

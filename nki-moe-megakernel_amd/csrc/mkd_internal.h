@@ -38,6 +38,11 @@ struct GemmArgs {
   // y + kb * part_stride; the consumer adds the kgrid partials in order.
   int kgrid;                  // 0 or 1: no split
   long long part_stride;      // elements between partial outputs
+  // grouped mode: the block walks every 16 * TN-token tile of its group in
+  // turn (launched with one token tile: most groups of a decode batch hold a
+  // few tokens, and a grid sized for the largest possible group would be
+  // mostly empty blocks)
+  int t_loop;
   // MX weights (mx.hip): `w` holds element codes in MX frag order and
   // w_group_stride counts bytes; x holds MXFP8 activation codes (ldx bytes per
   // row) with E8M0 scales x_scale (ldxs bytes per row, one per 32 along K).

@@ -245,6 +245,15 @@ class _LayerStack:
     """Shared by the Qwen3 and GPT-OSS models: a view of a contiguous range of
     the layers, and the routing log (what each layer's router produced)."""
 
+    def decode_plan(self, batch: Optional[int] = None) -> str:
+        """The decode path for this batch under the current mode: "persistent",
+        "joined_experts" (multi-kernel layers, gate/up and down in one launch) or
+        "multi_kernel"."""
+        plan = C.c_int32(0)
+        L.check(L.load().mkd_qwen3_decode_plan(self._model, batch or self.batch, C.byref(plan)),
+                "qwen3_decode_plan")
+        return "persistent" if plan.value & 1 else ("joined_experts" if plan.value & 2 else "multi_kernel")
+
     def _struct_for(self, layers):
         """The model struct, or a copy covering layers [lo, hi) only (host pointer
         arrays offset to lo; the persistent path's device table is left out)."""
