@@ -301,7 +301,6 @@ __global__ void __launch_bounds__(512) gemm_mx_kernel(GemmArgs a) {
   const int rbase = blockIdx.x;
   const int group = blockIdx.y;
   const int kg = a.kgrid > 1 ? a.kgrid : 1;
-  const int ttile = blockIdx.z / kg;
   const int kblk = blockIdx.z % kg;
 
   int count, base;
@@ -321,8 +320,11 @@ __global__ void __launch_bounds__(512) gemm_mx_kernel(GemmArgs a) {
     count = a.T;
     base = 0;
   }
+  // a.t_loop: the block walks every token tile of its group
+  for (int ttile = blockIdx.z / kg;; ++ttile) {
   const int t0 = ttile * 16;
   if (t0 >= count) return;
+  if (ttile > (int)blockIdx.z / kg) __syncthreads();   // the previous tile's reduction buffer is free
   int xrow[1];
   {
     const int c = t0 + (lane & 15);
@@ -358,6 +360,8 @@ __global__ void __launch_bounds__(512) gemm_mx_kernel(GemmArgs a) {
     if (f < NF) mx_batch<RB, FMT, 1>(wrow, srow, xrow[0], a, kb0, f, q, acc);
 
   gemm_finish<RB, 1, EPI>(a, acc, lane, wave, rbase, group, t0, base, xrow, kblk);
+  if (!a.t_loop) return;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -434,8 +438,12 @@ hipError_t gemm_mx_launch(GemmArgs a, int fmt, int epi, int groups_max, int max_
   if (a.kgrid > 1) return hipErrorInvalidValue;
   const int RB = (epi == EPI_SWIGLU_BF16) ? 2 : 1;
   const int n_tiles = (a.N + 16 * RB - 1) / (16 * RB);
-  const int ttiles = (max_tokens_per_group + 15) / 16;
+  int ttiles = (max_tokens_per_group + 15) / 16;
   const int groups = a.grp_expert ? groups_max : 1;
+  if (a.grp_expert && ttiles > 1) {   // grouped: one tile per block, walking the group (a.t_loop)
+    a.t_loop = 1;
+    ttiles = 1;
+  }
 #define MKD_M(RB_, F_, E_) \
   if (RB == RB_ && fmt == F_ && epi == E_) return launch_mx<RB_, F_, E_>(a, n_tiles, groups, ttiles, s);
   MKD_M(2, MX_E4M3, EPI_SWIGLU_BF16) MKD_M(2, MX_E2M1, EPI_SWIGLU_BF16)

@@ -254,6 +254,15 @@ class _LayerStack:
                 "qwen3_decode_plan")
         return "persistent" if plan.value & 1 else ("joined_experts" if plan.value & 2 else "multi_kernel")
 
+    def layer_kernel_status(self, batch: Optional[int] = None):
+        """(persistent layer kernel planned for this batch, an in-launch wait -- a grid
+        barrier or the joined expert launch's flags -- timed out).  Synchronises the device."""
+        used, timeout = C.c_int32(0), C.c_int32(0)
+        rc = L.load().mkd_qwen3_layer_kernel_status(self._model, batch or self.batch, self.ws.data_ptr(),
+                                                   self.ws.numel(), C.byref(used), C.byref(timeout))
+        L.check(rc, "qwen3_layer_kernel_status")
+        return bool(used.value), bool(timeout.value)
+
     def _struct_for(self, layers):
         """The model struct, or a copy covering layers [lo, hi) only (host pointer
         arrays offset to lo; the persistent path's device table is left out)."""
@@ -415,15 +424,6 @@ class Qwen3MoeMegakernelModel(_LayerStack, nn.Module):
             self.ws.data_ptr(), self.ws.numel(), L.stream_ptr(self.device))
         L.check(rc, "qwen3_decode_layers")
         return hidden
-
-    def layer_kernel_status(self, batch: Optional[int] = None):
-        """(persistent layer kernel planned for this batch, a grid barrier timed out).
-        Synchronises the device."""
-        used, timeout = C.c_int32(0), C.c_int32(0)
-        rc = L.load().mkd_qwen3_layer_kernel_status(self._model, batch or self.batch, self.ws.data_ptr(),
-                                                   self.ws.numel(), C.byref(used), C.byref(timeout))
-        L.check(rc, "qwen3_layer_kernel_status")
-        return bool(used.value), bool(timeout.value)
 
     def step(self, token_ids: torch.Tensor, position_ids: torch.Tensor, hidden: torch.Tensor,
              logits: torch.Tensor, next_tokens: torch.Tensor):
