@@ -17,18 +17,28 @@
 
 namespace mkd {
 
+// g * sigmoid(z) = g / (1 + e^-z) with the hardware exp2 and reciprocal
+// (v_exp_f32, v_rcp_f32: about 1 ulp each, so a few fp32 ulps in all -- far
+// below the bf16 rounding that follows); e^-z -> inf gives g * 0, e^-z -> 0
+// gives g.  The accurate expf and IEEE division cost ~40 instructions per
+// element, which dominated the epilogue of the MFMA-regime expert GEMM.
+MKD_DEV float gated_sigmoid(float g, float z) {
+  const float e = __builtin_amdgcn_exp2f(-z * 1.44269504088896341f);
+  return g * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // One gated activation value from the gate and up projections (fp32, bias
 // already added).  Qwen rounding: g, u -> bf16, silu(g) -> bf16, product;
 // otherwise clamps, then act(g) * u with act = silu or swish(alpha).
 MKD_DEV float swiglu_value(const GemmArgs& a, float gv, float uv) {
   if (a.round_qwen) {
     const float g = rbf(gv), u = rbf(uv);
-    return rbf(g / (1.0f + expf(-g))) * u;
+    return rbf(gated_sigmoid(g, g)) * u;
   }
   const float g = fmaxf(fminf(gv, a.gate_hi), a.gate_lo);
   const float u = fmaxf(fminf(uv, a.up_hi), a.up_lo);
   const float z = a.act ? a.alpha * g : g;
-  return (g / (1.0f + expf(-z))) * u;
+  return gated_sigmoid(g, z) * u;
 }
 
 template <int RB, int TN, int EPI, bool COH = false>
