@@ -29,7 +29,10 @@ namespace {
 constexpr int kTileRows = 256;           // packed weight rows per block
 constexpr int kTileTok = 256;            // tokens per block
 constexpr int kStageK = 32;              // k per stage (one fragment)
-constexpr int kStages = 4;               // LDS stage buffers (3 in flight)
+#ifndef MKD_TILE_STAGES
+#define MKD_TILE_STAGES 4
+#endif
+constexpr int kStages = MKD_TILE_STAGES;  // LDS stage buffers (kStages - 1 in flight)
 constexpr int kRB = kTileRows / 16;      // row blocks per block (16)
 constexpr int kTT = kTileTok / 16;       // token tiles per block (16)
 constexpr int kStageFrags = kRB + kTT;   // 1 KiB fragments per stage (32)
@@ -70,7 +73,10 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
   // contiguous run of logical tiles (n tile fastest, then item): the blocks
   // that share an expert's weight tiles and token rows run together on one
   // XCD's L2.
-  __shared__ int scan_s[8], item_s[3];
+  // the group scan's scratch lives in the first stage buffer (no copy is issued
+  // before every wave has read the scan's result)
+  int* scan_s = reinterpret_cast<int*>(lds);
+  int* item_s = scan_s + 8;
   const int gx = gridDim.x;
   const int total = gx * gridDim.y;
   const int L = blockIdx.x + gx * blockIdx.y;
@@ -113,6 +119,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
     base = a.grp_offset[g];
     expert = a.grp_expert[g];
     wp += (long long)expert * a.w_group_stride;
+    __syncthreads();                     // item_s read by every wave before the copies
   } else {
     count = a.T;
     base = 0;
@@ -163,6 +170,14 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
       voff[j] = (row * a.ldx + (lane >> 4) * 8) * 2;
     }
   }
+  // output rows of this lane's WT tokens, loaded ahead of the main loop (the
+  // epilogue's stores would otherwise wait on these loads one token at a time)
+  int orow[WT];
+#pragma unroll
+  for (int j = 0; j < WT; ++j) {
+    const int tc = min(t0 + (wn * WT + j) * 16 + (lane & 15), count - 1);
+    orow[j] = a.pair_out_row ? a.pair_out_row[base + tc] : base + tc;
+  }
   f32x4_t acc[8][WT];
 #pragma unroll
   for (int i = 0; i < 8; ++i)
@@ -171,11 +186,11 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
 
   for (int s = 0; s < kStages - 1; ++s) issue(min(s, S - 1), s);
   for (int s = 0; s < S; ++s) {
-    // this thread's loads of stage s have landed once at most the two later
-    // issued stages (4 loads each) are outstanding -- every iteration issues
-    // one stage, so the count is the same throughout; the barrier then makes
-    // every wave's stage s visible and frees the buffer of stage s - 1
-    wait_vmcnt<2 * FPW>();
+    // this thread's loads of stage s have landed once at most the kStages - 2
+    // later issued stages (FPW loads each) are outstanding -- every iteration
+    // issues one stage, so the count is the same throughout; the barrier then
+    // makes every wave's stage s visible and frees the buffer of stage s - 1
+    wait_vmcnt<(kStages - 2) * FPW>();
     asm volatile("s_barrier" ::: "memory");
     const u32x4_t* st = lds + (s % kStages) * kStageFrags * 64;
     // B first, then A in MFMA order: the MFMAs of row block i wait only for
@@ -186,7 +201,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) af[i] = st[(wm * 8 + i) * 64 + lane];
     __builtin_amdgcn_sched_barrier(0);     // all 12 operand reads in flight together
-    // the copies of stage s + 3 go out behind the reads (into the buffer that
+    // the copies of stage s + kStages - 1 go out behind the reads (into the buffer that
     // stage s - 1 used, which every wave has left: barrier above); past the
     // last stage the last stage is copied again into that dead buffer, which
     // keeps the loop free of branches and the wait count fixed
@@ -219,17 +234,21 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
       for (int j = 0; j < WT; ++j) {
         const int tc = t0 + (wn * WT + j) * 16 + (lane & 15);
         if (tc >= count) continue;
-        const int orow = a.pair_out_row ? a.pair_out_row[base + tc] : base + tc;
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           o[e] = swiglu_value(a, acc[2 * p][j][e] + gb[e], acc[2 * p + 1][j][e] + ub[e]);
-        uint16_t* y = static_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n;
+        uint16_t* y = static_cast<uint16_t*>(a.y) + (long long)orow[j] * a.ldy + n;
         *reinterpret_cast<uint2*>(y) = uint2{pack2bf(o[0], o[1]), pack2bf(o[2], o[3])};
       }
     }
   } else {   // EPI_SCALE_F32
     const uint16_t* bp = a.bias ? a.bias + (long long)expert * a.bias_group_stride : nullptr;
+    // all WT affinities up front (y is float too, so loads among the stores
+    // could not be moved past them)
+    float sc[WT];
+#pragma unroll
+    for (int j = 0; j < WT; ++j) sc[j] = a.pair_scale ? a.pair_scale[orow[j]] : 1.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int nb = nb0 + wm * 8 + i;
@@ -244,16 +263,15 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
       for (int j = 0; j < WT; ++j) {
         const int tc = t0 + (wn * WT + j) * 16 + (lane & 15);
         if (tc >= count) continue;
-        const int orow = a.pair_out_row ? a.pair_out_row[base + tc] : base + tc;
-        const float sc = a.pair_scale ? a.pair_scale[orow] : 1.0f;
-        float* y = static_cast<float*>(a.y) + (long long)orow * a.ldy + n;
+        float* y = static_cast<float*>(a.y) + (long long)orow[j] * a.ldy + n;
         if (n + 3 < a.N) {
-          *reinterpret_cast<f32x4_t*>(y) = f32x4_t{(acc[i][j][0] + bb[0]) * sc, (acc[i][j][1] + bb[1]) * sc,
-                                                   (acc[i][j][2] + bb[2]) * sc, (acc[i][j][3] + bb[3]) * sc};
+          *reinterpret_cast<f32x4_t*>(y) =
+              f32x4_t{(acc[i][j][0] + bb[0]) * sc[j], (acc[i][j][1] + bb[1]) * sc[j],
+                      (acc[i][j][2] + bb[2]) * sc[j], (acc[i][j][3] + bb[3]) * sc[j]};
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (n + e < a.N) y[e] = (acc[i][j][e] + bb[e]) * sc;
+            if (n + e < a.N) y[e] = (acc[i][j][e] + bb[e]) * sc[j];
         }
       }
     }
