@@ -441,6 +441,8 @@ def main():
                    "layers": cfg.num_hidden_layers, "experts": args.experts,
                    "kv_block": args.kv_block,
                    "graph": graph is not None,
+                   "attention_launch": "joined (attention + combine + o_proj)"
+                   if hasattr(model, "joined_attention") and model.joined_attention(B) else "separate",
                    "step_algorithmic_GB": round(step_b / 1e9, 4),
                    "step_GBps": round(step_gbs, 1),
                    "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),

@@ -418,7 +418,10 @@ int mkd_profile_count(void); /* launches recorded since the last mkd_profile_eve
  * sequence.  In mode 0, where the router top-k runs inside the expert launch
  * (a single token with bf16 experts), the gate/up and down projections share
  * that launch, the down blocks waiting inside it for their expert's gate/up
- * blocks.  Mode 2 is mode 0 with every stage a launch of its own.  The
+ * blocks; and at up to 4 tokens the attention, its chunk combine and the
+ * output projection run as one launch (the projection blocks load their
+ * weights while the attention runs, then wait for the combine blocks).
+ * Mode 2 is mode 0 with every stage a launch of its own.  The
  * workspace size does not depend on the mode.  Process-global.
  * mkd_qwen3_layer_kernel_status reports (after a stream sync) whether the
  * workspace's plan uses the persistent kernel and whether any of its grid
@@ -435,9 +438,12 @@ int mkd_qwen3_write_layer_table(const mkd_qwen3_model* m, void* table, size_t ta
 /* Which decode path mkd_qwen3_decode_layers takes for m and B tokens under the
  * current mode (no counterpart in the reference): *plan = MKD_PLAN_PERSISTENT
  * (one persistent launch for all layers) or MKD_PLAN_JOINED_EXPERTS (the
- * multi-kernel layers with gate/up and down in one launch), else 0. */
+ * multi-kernel layers with gate/up and down in one launch), else 0; plus
+ * MKD_PLAN_JOINED_ATTENTION when the multi-kernel layers run attention,
+ * combine and output projection as one launch. */
 #define MKD_PLAN_PERSISTENT 1
 #define MKD_PLAN_JOINED_EXPERTS 2
+#define MKD_PLAN_JOINED_ATTENTION 4
 int mkd_qwen3_decode_plan(const mkd_qwen3_model* m, int B, int* plan);
 int mkd_qwen3_layer_kernel_status(const mkd_qwen3_model* m, int B, const void* workspace,
                                   size_t workspace_bytes, int* used, int* barrier_timeout);

@@ -132,10 +132,26 @@ MKD_DEV const uint16_t* kv_row(const AttnArgs& a, const uint16_t* cache, int b, 
 }
 
 // Prior positions attended by sequence b (the new token sits at index n).
+MKD_DEV int prior_clamp(const AttnArgs& a, int raw) {
+  int n = max(raw, 0);
+  if (a.window > 0) n = min(n, a.window - 1);
+  return min(n, a.S_max);
+}
 MKD_DEV int prior_len(const AttnArgs& a, int b) {
   int n = max(a.n_prior[b], 0);
   if (a.window > 0) n = min(n, a.window - 1);
   return min(n, a.S_max);
+}
+
+// The raw count by a vector load, for prior_clamp once it is needed: a scalar
+// load would be waited for together with every scalar load before it
+// (lgkmcnt(0)), so address math issued after it that does not need the count
+// would wait for its round trip too.  (The zero offset comes from a VGPR so
+// that the uniform address is not turned into a scalar load.)
+MKD_DEV int prior_raw_vmem(const AttnArgs& a, int b) {
+  int zero;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
+  return a.n_prior[b + zero];
 }
 
 // Cache row that receives the new token of sequence b (-1: skip).

@@ -46,6 +46,7 @@
 #include "common.h"
 #include "mkd_internal.h"
 #include "attn_common.h"
+#include "coherent.h"
 
 namespace mkd {
 
@@ -109,8 +110,12 @@ __global__ void __launch_bounds__(D) attn_kv_write_kernel(AttnArgs a) {
   a.v_cache[off] = src[(GQA + 1) * D + d];
 }
 
-template <int D, int GQA, int TPW>
-__global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mode) {
+// One split-K chunk block (c, g, b).  COH: the block's outputs (partials and
+// staged k / v rows) are read by later blocks of the same launch -- they are
+// stored device-coherent and the block then sets *flag (also when the chunk
+// lies past the sequence and the block does nothing else).
+template <int D, int GQA, int TPW, bool COH>
+MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, int b, unsigned* flag) {
   constexpr int NK = D / 32;                  // QK MFMAs per tile (k = 32)
   constexpr int NDT = D / 16;                 // PV d-tiles
   constexpr int CP = 4 * TPW * 16;            // positions per block
@@ -122,7 +127,6 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   __shared__ __attribute__((aligned(16))) uint16_t vn_s[D];
 
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int c = blockIdx.x, g = blockIdx.y, b = blockIdx.z;
   const int chunk0 = c * CP;
 
   // ---- 0. the wave's K and V rows from the cache: they depend on nothing
@@ -177,6 +181,34 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
   u32x4_t kpre[PRE ? TPW : 1][NK];
   uint32_t vpre[PRE ? TPW : 1][4][VW];
   auto pre_loads = [&]() {
+    if (flat) {
+      // every row address valid (clamped below S_max), so the loads carry no
+      // condition and the wait for the prior length -- loaded before them --
+      // can count them out; the rows past n are masked where they are used
+      const uint16_t* kc = a.k_cache + b * a.cache_b_stride + g * a.cache_h_stride;
+      const uint16_t* vc0 = a.v_cache + b * a.cache_b_stride + g * a.cache_h_stride;
+#pragma unroll
+      for (int tt = 0; tt < TPW; ++tt) {
+        const int tk = min(wbase + tt * 16 + (lane & 15), a.S_max - 1);
+#pragma unroll
+        for (int kk = 0; kk < NK; ++kk) kpre[tt][kk] = ld16(kc + (long long)tk * D + dq + kk * 8);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const int tv = min(wbase + tt * 16 + (lane >> 4) * 4 + jj, a.S_max - 1);
+          const uint16_t* vr = vc0 + (long long)tv * D + vc;
+          if constexpr (VW == 4) {
+            const u32x4_t v = ld16(vr);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) vpre[tt][jj][e] = v[e];
+          } else {
+            const uint2 v = *reinterpret_cast<const uint2*>(vr);
+            vpre[tt][jj][0] = v.x;
+            vpre[tt][jj][1] = v.y;
+          }
+        }
+      }
+      return;
+    }
     const uint16_t* kp[TPW];
     const uint16_t* vp[TPW][4];
 #pragma unroll
@@ -209,11 +241,14 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
       }
     }
   }
-  const int n_read = prior_len(a, b);
+  const int n_raw = prior_raw_vmem(a, b);
   if (PRE && flat) pre_loads();
-  n = n_read;
+  n = __builtin_amdgcn_readfirstlane(prior_clamp(a, n_raw));
   const int total = n + 1;
-  if (chunk0 >= total) return;                // whole block: uniform exit
+  if (chunk0 >= total) {                      // whole block: uniform exit
+    if constexpr (COH) coh_publish(flag);
+    return;
+  }
   if (PRE && !flat) pre_loads();
   if (a.prep) {
     const uint16_t* src = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
@@ -363,33 +398,52 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
             f32x4_t{o[4 * q][i], o[4 * q + 1][i], o[4 * q + 2][i], o[4 * q + 3][i]};
   }
   __syncthreads();
-  for (int idx = threadIdx.x; idx < GQA * D; idx += 256) {
+  // four consecutive d of one head per thread (one 16-byte store)
+  for (int idx = threadIdx.x * 4; idx < GQA * D; idx += 1024) {
     const int h = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
     for (int q = 0; q < 4; ++q) M = fmaxf(M, m_s[q][h]);
-    float L = 0.f, O = 0.f;
+    float L = 0.f;
+    f32x4_t O = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
       const float f = (m_s[q][h] == -INFINITY) ? 0.f : expf(m_s[q][h] - M);
       L += l_s[q][h] * f;
-      O += o_s[q][h][d] * f;
+      O += *reinterpret_cast<const f32x4_t*>(&o_s[q][h][d]) * f;
     }
     const int hq = g * GQA + h;
-    a.part_o[(((long long)b * a.nq + hq) * a.n_chunks + c) * D + d] = O;
-    if (d == 0) {
-      float* ml = a.part_ml + (((long long)b * a.nq + hq) * a.n_chunks + c) * 2;
-      ml[0] = M;
-      ml[1] = L;
+    const long long po = (((long long)b * a.nq + hq) * a.n_chunks + c) * D + d;
+    const long long ml = (((long long)b * a.nq + hq) * a.n_chunks + c) * 2;
+    if constexpr (COH) {
+      coh_st16(coh_rsrc(a.part_o), (int)(po * 4), __builtin_bit_cast(u32x4_t, O));
+      if (d == 0) coh_st8(coh_rsrc(a.part_ml), (int)(ml * 4), __float_as_uint(M), __float_as_uint(L));
+    } else {
+      *reinterpret_cast<f32x4_t*>(a.part_o + po) = O;
+      if (d == 0) *reinterpret_cast<float2*>(a.part_ml + ml) = float2{M, L};
     }
   }
 
   // the chunk holding the new token stages its k / v rows for the scatter
   if (n >= chunk0 && n < chunk0 + CP)
     for (int i = threadIdx.x; i < D; i += 256) {
-      a.kv_new[(((long long)b * 2 + 0) * a.nkv + g) * D + i] = kn_s[i];
-      a.kv_new[(((long long)b * 2 + 1) * a.nkv + g) * D + i] = vn_s[i];
+      const long long ko = (((long long)b * 2 + 0) * a.nkv + g) * D + i;
+      const long long vo = (((long long)b * 2 + 1) * a.nkv + g) * D + i;
+      if constexpr (COH) {
+        const __amdgpu_buffer_rsrc_t kr = coh_rsrc(a.kv_new);
+        coh_st2(kr, (int)(ko * 2), kn_s[i]);
+        coh_st2(kr, (int)(vo * 2), vn_s[i]);
+      } else {
+        a.kv_new[ko] = kn_s[i];
+        a.kv_new[vo] = vn_s[i];
+      }
     }
+  if constexpr (COH) coh_publish(flag);
+}
+
+template <int D, int GQA, int TPW>
+__global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mode) {
+  attn_chunk_block<D, GQA, TPW, false>(a, rope_mode, blockIdx.x, blockIdx.y, blockIdx.z, nullptr);
 }
 
 // Combine: block (head h, sequence b), 4 waves; wave w takes chunks w, w+4, ...
@@ -397,18 +451,52 @@ __global__ void __launch_bounds__(256) attn_fused_kernel(AttnArgs a, int rope_mo
 // running (max, sum, O) per wave rescaled when a batch raises the max; the 4
 // wave results then merge in LDS in wave order, with the sink logit if any.
 // The new k / v rows of the scatter are loaded at the start as well.
-template <int D, int U>
-__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
+// COH: the chunk partials and staged rows come from earlier blocks of the same
+// launch -- one wave first waits for the n_wait flags at wait_fl (the kv group's
+// chunk blocks), every read of them is device-coherent, the bf16 output is
+// stored device-coherent and *flag is set at the end.
+template <int D, int U, bool COH>
+MKD_DEV void attn_combine_block(const AttnArgs& a, int h, int b, const unsigned* wait_fl, int n_wait,
+                                unsigned* flag, unsigned* err) {
   constexpr int EL = D / 64;
   __shared__ float m_s[4], l_s[4];
   __shared__ float acc_s[4][D];
-  const int h = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int CP = a.chunk;
   const int n = prior_len(a, b);
   const int nch = (n + 1 + CP - 1) / CP;
-  const float* ml = a.part_ml + ((long long)b * a.nq + h) * a.n_chunks * 2;
-  const float* po = a.part_o + ((long long)b * a.nq + h) * a.n_chunks * D;
+  const long long ml0 = ((long long)b * a.nq + h) * a.n_chunks * 2;   // floats
+  const long long po0 = ((long long)b * a.nq + h) * a.n_chunks * D;
+  const __amdgpu_buffer_rsrc_t mlr = coh_rsrc(a.part_ml), por = coh_rsrc(a.part_o);
+  // chunk k's (max, sum) and this lane's EL values of its O partial
+  auto ld_ml = [&](int k) -> float2 {
+    if constexpr (COH) {
+      const coh_u32x2 v = coh_ld8(mlr, (int)((ml0 + 2 * k) * 4));
+      return float2{__uint_as_float(v.x), __uint_as_float(v.y)};
+    } else {
+      return *reinterpret_cast<const float2*>(a.part_ml + ml0 + 2 * k);
+    }
+  };
+  auto ld_po = [&](int k, float (&dst)[EL]) {
+    const long long o = po0 + (long long)k * D + lane * EL;
+    if constexpr (COH) {
+      if constexpr (EL == 2) {
+        const coh_u32x2 v = coh_ld8(por, (int)(o * 4));
+        dst[0] = __uint_as_float(v.x);
+        dst[1] = __uint_as_float(v.y);
+      } else {
+#pragma unroll
+        for (int e = 0; e < EL; ++e) dst[e] = __uint_as_float(coh_ld4(por, (int)((o + e) * 4)));
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < EL; ++e) dst[e] = a.part_o[o + e];
+    }
+  };
+  if constexpr (COH) {
+    if (w == 0) coh_wait_all(wait_fl, n_wait, err);
+    __syncthreads();
+  }
 
   // scatter operands: the first query head of each kv group writes that group's rows
   const int gqa = a.nq / a.nkv;
@@ -416,8 +504,17 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
   uint16_t knew = 0, vnew = 0;
   if (scatter) {
     const int g = h / gqa;
-    knew = a.kv_new[(((long long)b * 2 + 0) * a.nkv + g) * D + threadIdx.x];
-    vnew = a.kv_new[(((long long)b * 2 + 1) * a.nkv + g) * D + threadIdx.x];
+    const long long ko = (((long long)b * 2 + 0) * a.nkv + g) * D + threadIdx.x;
+    const long long vo = (((long long)b * 2 + 1) * a.nkv + g) * D + threadIdx.x;
+    if constexpr (COH) {   // aligned dwords (a 16-bit load would be waited for at issue)
+      const __amdgpu_buffer_rsrc_t kr = coh_rsrc(a.kv_new);
+      const uint32_t kw = coh_ld4(kr, (int)((ko & ~1LL) * 2)), vw = coh_ld4(kr, (int)((vo & ~1LL) * 2));
+      knew = (uint16_t)((ko & 1) ? kw >> 16 : kw);
+      vnew = (uint16_t)((vo & 1) ? vw >> 16 : vw);
+    } else {
+      knew = a.kv_new[ko];
+      vnew = a.kv_new[vo];
+    }
   }
 
   float m = -INFINITY, L = 0.f, acc[EL];
@@ -429,10 +526,10 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
     for (int u = 0; u < U; ++u) {
       const int k = k0 + 4 * u;
       const int kc = k < nch ? k : k0;       // in-range address; masked below
-      mk[u] = ml[2 * kc];
-      lk[u] = ml[2 * kc + 1];
-#pragma unroll
-      for (int e = 0; e < EL; ++e) pv[u][e] = po[(long long)kc * D + lane * EL + e];
+      const float2 mlv = ld_ml(kc);
+      mk[u] = mlv.x;
+      lk[u] = mlv.y;
+      ld_po(kc, pv[u]);
       if (k >= nch) mk[u] = -INFINITY;
     }
     float bm = m;
@@ -468,7 +565,10 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
       o += acc_s[q][d] * f;
     }
     if (a.sink) Lt += expf(a.sink[h] - M);
-    a.attn_out[((long long)b * a.nq + h) * D + d] = (uint16_t)f2bf(Lt > 0.f ? o / Lt : 0.f);
+    const uint16_t ov = (uint16_t)f2bf(Lt > 0.f ? o / Lt : 0.f);
+    const long long oo = ((long long)b * a.nq + h) * D + d;
+    if constexpr (COH) coh_st2(coh_rsrc(a.attn_out), (int)(oo * 2), ov);
+    else a.attn_out[oo] = ov;
     // in-place KV scatter of the new rows (attention_block_tkg.py:1144-1470),
     // after every chunk has read the cache (kernels run in stream order)
     if (scatter) {
@@ -483,6 +583,151 @@ __global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
       }
     }
   }
+  if constexpr (COH) coh_publish(flag);
+}
+
+template <int D, int U>
+__global__ void __launch_bounds__(256) attn_combine_kernel(AttnArgs a) {
+  attn_combine_block<D, U, false>(a, blockIdx.x, blockIdx.y, nullptr, 0, nullptr, nullptr);
+}
+
+// ---- joined launch: chunk blocks | combine blocks | projection blocks ----
+constexpr int kJoinMaxF = 32;        // weight fragments per wave (nq * d <= 4096)
+// The projection blocks start their weight stream this long after they start
+// (wall clock, 100 MHz ticks): the chunk blocks' cache and projection loads,
+// which the whole launch waits on, are served first; the weights still arrive
+// long before the combine is done.  Measured at bs=1, Qwen3-30B-A3B shape,
+// KV 2048 (decode step tok/s): no delay 320.5, 1 us 321.9, 1.5 us 324.4,
+// 2.5 us 326.2, 4 us 324.7.
+constexpr unsigned kJoinWeightDelay = 250;
+
+// Output-projection block: 16 rows (row block rb) of y = attn_out . W_out^T for
+// the B tokens, 4 waves over K quarters.  The weight fragments do not depend on
+// the attention, so they are loaded first (after the start delay above); then
+// one wave waits for the ncf
+// combine flags, the B attention rows go to LDS (device-coherent loads), and
+// the MFMAs run (A = weight fragment, B = tokens: lane l holds token l%16, k
+// (l/16)*8 .. +8; D lane l holds rows 4*(l/16)+i of token l%16).  The wave
+// partials are added in wave order.
+MKD_DEV void oproj_block(const AttnArgs& a, const AttnJoinArgs& j, int rb, const unsigned* cfl, int ncf) {
+  extern __shared__ u32x4_t xs[];            // [B][K / 8]
+  __shared__ f32x4_t red[4][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int K = a.nq * a.d, KB = K / 32, nf = KB / 4, kb0 = w * nf;
+  // fragments past nf (K < 4096) repeat the last one and meet zero operands:
+  // no branch in the unrolled loop
+  {
+    const unsigned long long t0 = wall_clock64();
+    while (wall_clock64() - t0 < kJoinWeightDelay) __builtin_amdgcn_s_sleep(2);
+  }
+  const uint16_t* wrow = j.w_out + ((long long)rb * KB + kb0) * 512 + lane * 8;
+  u32x4_t wf[kJoinMaxF];
+#pragma unroll
+  for (int u = 0; u < kJoinMaxF; ++u)
+    wf[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + min(u, nf - 1) * 512));
+  if (w == 0) coh_wait_all(cfl, ncf, j.err);
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t xr = coh_rsrc(a.attn_out);
+  const int per_row = K / 8, n16 = a.B * per_row;
+  constexpr int kXs = kJoinMaxB * 4096 / 8 / 256;     // 16-byte pieces per thread at most
+  u32x4_t xt[kXs];
+#pragma unroll
+  for (int q = 0; q < kXs; ++q) {
+    const int i = threadIdx.x + 256 * q;
+    if (i < n16) xt[q] = coh_ld16(xr, i * 16);
+  }
+#pragma unroll
+  for (int q = 0; q < kXs; ++q) {
+    const int i = threadIdx.x + 256 * q;
+    if (i < n16) xs[i] = xt[q];
+  }
+  __syncthreads();
+  const int c = lane & 15;
+  const bool tok = c < a.B;
+  const u32x4_t* xrow = xs + (tok ? c : 0) * per_row + (lane >> 4);
+  f32x4_t acc[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // eight operand reads, then their eight MFMAs (masked, not branched)
+#pragma unroll
+  for (int u0 = 0; u0 < kJoinMaxF; u0 += 8) {
+    u32x4_t xv[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int u = u0 + q;
+      const uint32_t m = (tok && u < nf) ? 0xffffffffu : 0u;
+      const u32x4_t t = xrow[(kb0 + min(u, nf - 1)) * 4];
+      xv[q] = u32x4_t{t[0] & m, t[1] & m, t[2] & m, t[3] & m};
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q & 3] = mfma16x16x32(wf[u0 + q], xv[q], acc[q & 3]);
+  }
+  red[w][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  __syncthreads();
+  if (w != 0 || c >= a.B) return;
+  const f32x4_t v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+  const int n0 = rb * 16 + (lane >> 4) * 4;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (n0 + i < j.N) j.y[(long long)c * j.N + n0 + i] = v[i] + (j.bias ? bf2f(j.bias[n0 + i]) : 0.f);
+}
+
+template <int D, int GQA, int TPW>
+__global__ void __launch_bounds__(256) attn_joined_kernel(AttnArgs a, AttnJoinArgs j, int rope_mode) {
+  const int bid = blockIdx.x;
+  const int na = a.n_chunks * a.nkv * a.B, nc = a.nq * a.B;
+  if (bid < na) {
+    const int c = bid % a.n_chunks, gb = bid / a.n_chunks;
+    attn_chunk_block<D, GQA, TPW, true>(a, rope_mode, c, gb % a.nkv, gb / a.nkv, j.flags + bid);
+  } else if (bid < na + nc) {
+    const int hb = bid - na, h = hb % a.nq, b = hb / a.nq;
+    attn_combine_block<D, 16, true>(a, h, b, j.flags + ((long long)b * a.nkv + h / GQA) * a.n_chunks,
+                                    a.n_chunks, j.flags + bid, j.err);
+  } else {
+    oproj_block(a, j, bid - na - nc, j.flags + na, nc);
+  }
+}
+
+int attn_join_flag_words(int B, int nq, int nkv, int n_chunks) { return n_chunks * nkv * B + nq * B; }
+
+bool attn_join_supported(const AttnArgs& a, int N) {
+  const int gqa = a.nkv > 0 ? a.nq / a.nkv : 0;
+  const int K = a.nq * a.d;
+  return !a.prep && !a.prefill && a.B >= 1 && a.B <= kJoinMaxB && (a.chunk == 64 || a.chunk == 128) &&
+         (a.d == 64 || a.d == 128) && (gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8 || gqa == 16) &&
+         gqa * a.nkv == a.nq && K % 128 == 0 && K / 128 <= kJoinMaxF && N > 0 &&
+         (long long)a.B * K * 2 <= 32768;
+}
+
+template <int D, int GQA>
+static hipError_t launch_join(const AttnArgs& a, const AttnJoinArgs& j, int rope_mode, hipStream_t s) {
+  const int blocks = a.n_chunks * a.nkv * a.B + a.nq * a.B + (j.N + 15) / 16;
+  const size_t lds = (size_t)a.B * a.nq * a.d * 2;
+  if (a.chunk == 64) return timed_launch(attn_joined_kernel<D, GQA, 1>, dim3(blocks), dim3(256), lds, s, a, j, rope_mode);
+  return timed_launch(attn_joined_kernel<D, GQA, 2>, dim3(blocks), dim3(256), lds, s, a, j, rope_mode);
+}
+
+hipError_t attn_join_launch(const AttnArgs& a, const AttnJoinArgs& j, int rope_mode, hipStream_t s) {
+  if (!attn_join_supported(a, j.N) || !j.w_out || !j.y || !j.flags || !j.err) return hipErrorInvalidValue;
+  const int gqa = a.nq / a.nkv;
+  if (a.d == 128) {
+    switch (gqa) {
+      case 1: return launch_join<128, 1>(a, j, rope_mode, s);
+      case 2: return launch_join<128, 2>(a, j, rope_mode, s);
+      case 4: return launch_join<128, 4>(a, j, rope_mode, s);
+      case 8: return launch_join<128, 8>(a, j, rope_mode, s);
+      case 16: return launch_join<128, 16>(a, j, rope_mode, s);
+    }
+  } else {
+    switch (gqa) {
+      case 1: return launch_join<64, 1>(a, j, rope_mode, s);
+      case 2: return launch_join<64, 2>(a, j, rope_mode, s);
+      case 4: return launch_join<64, 4>(a, j, rope_mode, s);
+      case 8: return launch_join<64, 8>(a, j, rope_mode, s);
+      case 16: return launch_join<64, 16>(a, j, rope_mode, s);
+    }
+  }
+  return hipErrorInvalidValue;
 }
 
 template <int D, int GQA, int TPW>

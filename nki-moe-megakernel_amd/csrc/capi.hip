@@ -759,9 +759,13 @@ size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S
 // o_parts != null: the output projection writes fp32 split-K partials
 // [kgrid][B][H_out] there (the caller's next norm folds them into the residual)
 // instead of applying the bf16 / residual epilogue.
+// join != null (with o_parts, one partial): attention, chunk combine and the
+// output projection run as one launch where attn_join_supported allows,
+// synchronised through join's flag words.
 static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos_for_rope,
                           const float* inv_freq, hipStream_t s, float* o_parts = nullptr,
-                          int o_kgrid = 1, const QkvNormArgs* qn = nullptr, bool prefill = false) {
+                          int o_kgrid = 1, const QkvNormArgs* qn = nullptr, bool prefill = false,
+                          const AttnJoinArgs* join = nullptr) {
   const int qkv_n = (p->nq + 2 * p->nkv) * p->d;
   int qkv_parts = 1;
   // 1. optional RMSNorm
@@ -839,6 +843,17 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     a.prefill = 1;
   }
   const int rope_mode = p->cos ? 1 : (inv_freq ? 2 : 0);
+  if (join && o_parts && o_kgrid <= 1 && p->w_out_packed && attn_join_supported(a, p->H_out)) {
+    AttnJoinArgs j = *join;
+    j.w_out = static_cast<const uint16_t*>(p->w_out_packed);
+    j.bias = static_cast<const uint16_t*>(p->bias_out);
+    j.y = o_parts;
+    j.N = p->H_out;
+    const int ps = prof_begin(MKD_KCLASS_ATTN, s);
+    MKD_TRY(attn_join_launch(a, j, rope_mode, s), "attention + combine + o_proj");
+    prof_end(ps, s);
+    return MKD_OK;
+  }
   {  // q/k norm + RoPE and split-K attention in one launch
     const int ps = prof_begin(MKD_KCLASS_ATTN, s);
     MKD_TRY(attn_decode_launch(a, rope_mode, s), "attention");
@@ -1052,7 +1067,7 @@ struct StepWs {
   // word, then per layer that launch's flags (sync_words in all, cleared once
   // per call)
   unsigned* sync;
-  int sync_words, layer_words, flag_words;
+  int sync_words, layer_words, flag_words, attn_words;
 };
 
 static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
@@ -1068,7 +1083,9 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.moe = carve_moe(c, B, m->H, m->E, m->I, m->K);
   w.lk = carve_lk(c, m, B);
   w.flag_words = moe_fused_supported(B, m->K, m->E, m->H, m->I) ? moe_fused_flag_words(B, m->K, m->E, m->I) : 0;
-  w.layer_words = w.flag_words;
+  // the joined attention launch's flags (chunk and combine blocks)
+  w.attn_words = B <= kJoinMaxB ? attn_join_flag_words(B, m->nq, m->nkv, w.attn.n_chunks) : 0;
+  w.layer_words = w.flag_words + w.attn_words;
   w.sync_words = w.layer_words ? 64 + m->num_layers * w.layer_words : 0;
   w.sync = w.sync_words ? c.take<unsigned>(w.sync_words) : nullptr;
   return w;
@@ -1146,6 +1163,19 @@ static bool joined_experts_planned(const mkd_qwen3_model* m, int B) {
   const int gmax = m->E < B * m->K ? m->E : B * m->K;
   return g_inlaunch_sync && defer_select_ok(m, B) && moe_fused_supported(B, m->K, m->E, m->H, m->I) &&
          gate_up_kw(m->H, m->I, gmax) * 8 == m->H;
+}
+
+// ... and attention, combine and output projection in one launch (mode 0, a
+// few tokens): the same test attention_core applies, on the step's shapes.
+static bool joined_attention_planned(const mkd_qwen3_model* m, int B) {
+  if (!g_inlaunch_sync || B > kJoinMaxB || o_proj_kgrid(m, B) > 1 || !m->w_o) return false;
+  AttnArgs a;
+  memset(&a, 0, sizeof(a));
+  a.B = B; a.nq = m->nq; a.nkv = m->nkv; a.d = m->d; a.S_max = m->S_max;
+  a.chunk = attn_chunk_for(B, m->nkv, m->S_max);
+  a.n_chunks = (m->S_max + 1 + a.chunk - 1) / a.chunk;
+  if ((long long)a.n_chunks * m->nkv * B > 1024) return false;   // the large-grid prep launch
+  return attn_join_supported(a, m->H);
 }
 
 static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const int* position_ids,
@@ -1230,7 +1260,8 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
   // is deferred into the gate/up blocks and the shapes fit it
   const bool defer_ok = defer_select_ok(m, B);
   const bool fused_moe = joined_experts_planned(m, B) && w.flag_words > 0;
-  if (fused_moe) MKD_TRY(sync_clear_launch(w.sync, w.sync_words, s), "clear sync words");
+  const bool join_attn = g_inlaunch_sync && !prefill && w.attn_words > 0 && o_kgrid <= 1;
+  if (fused_moe || join_attn) MKD_TRY(sync_clear_launch(w.sync, w.sync_words, s), "clear sync words");
   for (int l = 0; l < m->num_layers; ++l) {
     const int wl = m->window ? m->window[l] : 0;
     mkd_attention_args ap;
@@ -1275,8 +1306,12 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
       qn.resid_out = l == 0 ? nullptr : x;
     }
     unsigned* lsync = w.sync ? w.sync + 64 + (size_t)l * w.layer_words : nullptr;
+    AttnJoinArgs ja = {};
+    ja.flags = lsync ? lsync + w.flag_words : nullptr;
+    ja.err = w.sync;
     if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s, w.oparts, o_kgrid,
-                                fuse_qn ? &qn : nullptr, prefill && !wl))
+                                fuse_qn ? &qn : nullptr, prefill && !wl,
+                                join_attn && lsync ? &ja : nullptr))
       return rc;
     // router (split-K GEMM) + top-k + expert groups in one select launch: Qwen
     // fp32 input and fused flow; GPT-OSS bf16 input, biased logits, top-k then
@@ -1537,8 +1572,12 @@ int mkd_qwen3_decode_plan(const mkd_qwen3_model* m, int B, int* plan) {
   MKD_REQUIRE(m && plan, MKD_ERR_NULL, "decode_plan: null pointer");
   MKD_REQUIRE(B > 0 && B <= 128, MKD_ERR_INVALID, "decode_plan: %d tokens must be in [1, 128]", B);
   int p = 0;
-  if (g_decode_path == 1 && lk_plan(m, B).on) p |= MKD_PLAN_PERSISTENT;
-  else if (joined_experts_planned(m, B)) p |= MKD_PLAN_JOINED_EXPERTS;
+  if (g_decode_path == 1 && lk_plan(m, B).on) {
+    p |= MKD_PLAN_PERSISTENT;
+  } else {
+    if (joined_experts_planned(m, B)) p |= MKD_PLAN_JOINED_EXPERTS;
+    if (joined_attention_planned(m, B)) p |= MKD_PLAN_JOINED_ATTENTION;
+  }
   *plan = p;
   return MKD_OK;
 }

@@ -45,6 +45,12 @@ MKD_DEV float coh_ldf(const float* p) {
 MKD_DEV void coh_stf(float* p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+MKD_DEV uint32_t coh_ld4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCohSc1);
+}
+MKD_DEV coh_u32x2 coh_ld8(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCohSc1);
+}
 MKD_DEV uint16_t coh_ld2(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, kCohSc1);
 }

@@ -267,6 +267,22 @@ struct AttnArgs {
 hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s);
 hipError_t attn_combine_launch(const AttnArgs& a, hipStream_t s);
 int attn_chunk_for(int B, int nkv, int S_max);   // positions per attention block (64/128/256)
+// Attention, chunk combine and output projection in one launch (attn_mfma.hip,
+// attn_joined_kernel): the chunk blocks, then the combine blocks, then the
+// projection blocks of one grid, each stage waiting on the flags of the blocks
+// it reads; the projection blocks load their weight slices before they wait.
+constexpr int kJoinMaxB = 4;         // tokens
+struct AttnJoinArgs {
+  const uint16_t* w_out;      // [N, nq * d] frag-packed
+  const uint16_t* bias;       // [N] or null
+  float* y;                   // [B, N] fp32 projection (bias added, no residual)
+  int N;
+  unsigned* flags;            // attn_join_flag_words() words, zero at launch
+  unsigned* err;              // set when a wait ran out
+};
+int attn_join_flag_words(int B, int nq, int nkv, int n_chunks);
+bool attn_join_supported(const AttnArgs& a, int N);
+hipError_t attn_join_launch(const AttnArgs& a, const AttnJoinArgs& j, int rope_mode, hipStream_t s);
 
 // moe.hip
 struct RouterArgs {

@@ -254,6 +254,14 @@ class _LayerStack:
                 "qwen3_decode_plan")
         return "persistent" if plan.value & 1 else ("joined_experts" if plan.value & 2 else "multi_kernel")
 
+    def joined_attention(self, batch: Optional[int] = None) -> bool:
+        """Whether the multi-kernel layers run attention, chunk combine and output
+        projection as one launch for this batch under the current mode."""
+        plan = C.c_int32(0)
+        L.check(L.load().mkd_qwen3_decode_plan(self._model, batch or self.batch, C.byref(plan)),
+                "qwen3_decode_plan")
+        return bool(plan.value & 4)
+
     def layer_kernel_status(self, batch: Optional[int] = None):
         """(persistent layer kernel planned for this batch, an in-launch wait -- a grid
         barrier or the joined expert launch's flags -- timed out).  Synchronises the device."""

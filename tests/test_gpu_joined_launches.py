@@ -1,6 +1,9 @@
-"""The joined expert launch of the one-token decode step (router top-k, gate/up
-and down in one kernel whose down blocks wait inside the launch for their
-expert's gate/up blocks), and the one-token router selection inside it.
+"""The joined launches of the few-token decode step: attention, chunk combine
+and output projection in one kernel (the combine blocks wait inside the launch
+for their kv group's chunk blocks, the projection blocks for every combine
+block), and the expert launch (router top-k, gate/up and down in one kernel
+whose down blocks wait for their expert's gate/up blocks) with the one-token
+router selection inside it.
 
 Checked, at full Qwen3-30B-A3B layer shapes (H 2048, 32 / 4 heads, 128 experts
 top-8, I 768), 3 layers chained:
@@ -70,7 +73,7 @@ def _run(model, x, kcs, vcs, pos, dev):
     return y.cpu(), [model.kv_mgr.k(l).cpu() for l in range(len(kcs))], model.route_log(x.shape[0])
 
 
-@pytest.mark.parametrize("B,S", [(1, 1024), (1, 4096)])
+@pytest.mark.parametrize("B,S", [(1, 1024), (1, 4096), (4, 2048)])
 def test_joined_launches_vs_separate_and_oracle(mk, dev, restore_path, B, S):
     Q = restore_path
     print(f"joined launches: B={B} S={S}", flush=True)
