@@ -468,7 +468,7 @@ MKD_DEV void select_one(const RouterArgs& a, Load&& load) {
 #pragma unroll
     for (int j = 0; j < PER; ++j) {
       const float key = (qwen || !pre) ? l[j] : (sigm ? 1.0f / (1.0f + expf(-l[j])) : ex[j] * inv);
-      code_s[lane + 64 * j] = order_code(key);
+      code_s[lane + 64 * j] = (lane + 64 * j < E) ? order_code(key) : 0u;   // padding ranks last
       key_s[lane + 64 * j] = key;
     }
     if (lane == 0) {
@@ -478,11 +478,17 @@ MKD_DEV void select_one(const RouterArgs& a, Load&& load) {
   }
   __syncthreads();
   {
-    // the quarter's 32 codes with eight 16-byte LDS reads issued together
+    // the quarter's 32 codes with eight 16-byte LDS reads issued together.
+    // f outranks e when code_f > code_e, or code_f == code_e and f < e: one
+    // unsigned compare against code_e - 1 below e and code_e from e on (every
+    // finite or infinite key codes to >= 0x7fffff; padding codes are 0) -- a
+    // select and a compare per code, no lane-mask logic.
     const int e = tid >> 2, qtr = tid & 3;
     int rank = 0;
     if (e < E) {
       const uint32_t ue = code_s[e];
+      const uint32_t ue1 = ue ? ue - 1 : 0u;
+      const int d = e - qtr * 32;          // codes i*4+j of the quarter below e: i*4+j < d
       const u32x4_t* cq = reinterpret_cast<const u32x4_t*>(code_s + qtr * 32);
       u32x4_t c[8];
 #pragma unroll
@@ -491,8 +497,8 @@ MKD_DEV void select_one(const RouterArgs& a, Load&& load) {
       for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const int f = qtr * 32 + i * 4 + j;
-          rank += f < E && ((c[i][j] > ue) || (c[i][j] == ue && f < e));
+          const uint32_t thr = (i * 4 + j < d) ? ue1 : ue;
+          rank += c[i][j] > thr ? 1 : 0;
         }
     }
     rank += __builtin_amdgcn_update_dpp(0, rank, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
