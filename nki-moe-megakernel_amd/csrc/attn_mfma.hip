@@ -14,9 +14,11 @@
 //                          (16 columns, >= gqa zero).  D lane l holds
 //                          S[pos 4*(l/16)+i][head l%16].
 //       p = exp(s - m_head) with the wave's per-head max.
-//       O += P . V        v_mfma_f32_16x16x16_bf16: the S layout above IS the A
-//                          layout of this MFMA (row = head l%16, k = positions
-//                          4*(l/16)+i), so P never leaves registers.  B = V
+//       O += P . V        v_mfma_f32_16x16x32_bf16 over two tiles (one 16x16x16
+//                          when a wave holds a single tile): the S layout above
+//                          IS the A layout (row = head l%16, k = positions
+//                          4*(l/16)+i; two tiles give a lane group's 8 k slots),
+//                          so P never leaves registers.  B = V
 //                          [pos 4*(l/16)+j][d label l%16]: the d labels are
 //                          permuted so that lane column c = l%16 owns the D/16
 //                          contiguous elements c*D/16.. of its four position
@@ -344,6 +346,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
 #pragma unroll
   for (int dt = 0; dt < NDT; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   uint32_t vl[LB][4][VW];
+  uint2 bprev[NDT];                           // an even tile's V operands (paired tiles)
 #pragma unroll
   for (int tt = 0; tt < TPW; ++tt) {
     const int tile0 = wbase + tt * 16;
@@ -375,13 +378,31 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
         for (int e = 0; e < VW; ++e) v[j][e] = 0u;
       }
     }
+    uint2 bop[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       const int e = dt >> 1;
-      const uint2 bop = (dt & 1)
+      bop[dt] = (dt & 1)
           ? uint2{(v[0][e] >> 16) | (v[1][e] & 0xffff0000u), (v[2][e] >> 16) | (v[3][e] & 0xffff0000u)}
           : uint2{(v[0][e] & 0xffffu) | (v[1][e] << 16), (v[2][e] & 0xffffu) | (v[3][e] << 16)};
-      o[dt] = mfma16x16x16(pa[tt], bop, o[dt]);
+    }
+    if constexpr (TPW % 2 == 0) {
+      // tiles in pairs on the 32-deep MFMA: lane group q's k slots 8q .. 8q+7
+      // are positions 4q .. 4q+3 of the even tile, then of the odd tile -- the
+      // same order in the P operand (its two 4-position halves) and in the V
+      // operand (its two row quads)
+      if (tt % 2 == 0) {
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) bprev[dt] = bop[dt];
+      } else {
+        const u32x4_t pp = {pa[tt - 1].x, pa[tt - 1].y, pa[tt].x, pa[tt].y};
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+          o[dt] = mfma16x16x32(pp, u32x4_t{bprev[dt].x, bprev[dt].y, bop[dt].x, bop[dt].y}, o[dt]);
+      }
+    } else {   // one tile per wave: the 16-deep MFMA
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) o[dt] = mfma16x16x16(pa[tt], bop[dt], o[dt]);
     }
   }
 

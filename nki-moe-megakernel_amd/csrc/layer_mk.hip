@@ -691,7 +691,9 @@ MKD_DEV void attn_unit(const LayerArgs& L, const LkLayer& ly, const AttnArgs& aa
   lsum += __shfl_xor(lsum, 32, 64);
 
   // ---- O = P V (V rows: d labels permuted so each lane holds D/16
-  // contiguous elements of its four position rows) ----
+  // contiguous elements of its four position rows).  One 16-position tile per
+  // wave, so the 16-deep MFMA: the 32-deep one would take a second tile's
+  // positions for its other k half ----
   uint32_t v[4][VW];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
