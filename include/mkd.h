@@ -207,8 +207,8 @@ int mkd_moe_prefill(const mkd_moe_args* args, void* workspace, size_t workspace_
 
 /* ---------------------------------------------------------------------------
  * attention_block_tkg -- replaces nki_kernels/attention/attention_block_tkg.py:83
- * for S_tkg = 1 (one new token per sequence), generalised from one kv head per
- * call to nkv >= 1 (GQA).  Stages (attention_block_tkg.py:359-583): optional
+ * for S_tkg <= 8 new tokens per sequence (s_tkg below), generalised from one kv
+ * head per call to nkv >= 1 (GQA).  Stages (attention_block_tkg.py:359-583): optional
  * RMSNorm(X) -> QKV projection (+bias) -> optional pre-RoPE per-head RMSNorm ->
  * RoPE (contiguous halves) -> decode attention over the cache window (+ the
  * active token) with optional 0/1 mask and sink -> in-place KV scatter at
@@ -257,8 +257,20 @@ typedef struct {
                                   window): min(n_prior, window-1) prior rows are
                                   attended and, with kv_cache_update_idx NULL, the
                                   new row goes to n_prior % (window-1)            */
+  /* New tokens per sequence, S_tkg of attention_block_tkg.py:151 (0 or 1: one).
+   * With s_tkg > 1 (<= 8; B * s_tkg <= 128): X, cos, sin and out hold B * s_tkg
+   * rows, row b * s_tkg + s being token s of sequence b; sequence b attends its
+   * n_prior[b] cache positions and then its s_tkg new tokens; mask is
+   * [S_ctx, B, nq, s_tkg] uint8 with new token i at slot S_ctx - s_tkg + i
+   * (attention_tkg.py: the active keys close the window); token s is written
+   * at kv_cache_update_idx[b] + s (attention_block_tkg.py:1365-1470, 1611-1685;
+   * a global row for a block cache), which is then required.  No ring cache
+   * (window) and no residual with s_tkg > 1. */
+  int s_tkg;
 } mkd_attention_args;
 size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S_max);
+/* The same for s_tkg new tokens per sequence (mkd_attention_args::s_tkg). */
+size_t mkd_attention_workspace_bytes_tkg(int B, int s_tkg, int H, int nq, int nkv, int d, int S_max);
 int mkd_attention_block_tkg(const mkd_attention_args* args, void* workspace,
                             size_t workspace_bytes, void* stream);
 

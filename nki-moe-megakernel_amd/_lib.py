@@ -68,7 +68,7 @@ class AttentionArgs(C.Structure):
         ("B", i32), ("H", i32), ("H_out", i32), ("nq", i32), ("nkv", i32), ("d", i32),
         ("S_max", i32), ("round_qwen", i32),
         ("active_blocks_table", vp), ("blocks_per_seq", i32), ("block_len", i32), ("num_blocks", i32),
-        ("hidden_actual", i32), ("window", i32),
+        ("hidden_actual", i32), ("window", i32), ("s_tkg", i32),
     ]
 
 
@@ -109,6 +109,7 @@ _SIGS = {
     "mkd_moe_tkg": (i32, [C.POINTER(MoeArgs), vp, sz, vp]),
     "mkd_moe_prefill": (i32, [C.POINTER(MoeArgs), vp, sz, vp]),
     "mkd_attention_workspace_bytes": (sz, [i32, i32, i32, i32, i32, i32]),
+    "mkd_attention_workspace_bytes_tkg": (sz, [i32, i32, i32, i32, i32, i32, i32]),
     "mkd_attention_block_tkg": (i32, [C.POINTER(AttentionArgs), vp, sz, vp]),
     "mkd_qwen3_workspace_bytes": (sz, [C.POINTER(Qwen3Model), i32]),
     "mkd_qwen3_route_log_bytes": (sz, [C.POINTER(Qwen3Model), i32]),

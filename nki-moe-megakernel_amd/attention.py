@@ -52,8 +52,13 @@ def attention_block_tkg(
     active token is mask slot S_ctx - 1, and kv_cache_update_idx holds global
     rows block * block_len + row (uint32 max = skip).
 
-    Supported: S_tkg = 1, flat or block caches, no quantisation.  Other
-    reference options raise NotImplementedError.  enable_fa_s_prior_tiling is a
+    S_tkg <= 8 new tokens per sequence (attention_block_tkg.py:151): the window
+    of sequence b is its first S_ctx - S_tkg cache positions followed by its
+    S_tkg new tokens (mask slot S_ctx - S_tkg + i = new token i; the active keys
+    close the window as in attention_tkg.py), and token s is written at
+    kv_cache_update_idx[b] + s (attention_block_tkg.py:1365-1470; a global row of
+    a block cache).  Flat or block caches, no quantisation.  Other reference
+    options raise NotImplementedError.  enable_fa_s_prior_tiling is a
     scheduling hint (the GPU path always tiles the KV length).
     """
     if KVDP != 1:
@@ -76,8 +81,10 @@ def attention_block_tkg(
         raise NotImplementedError("post-RoPE Q/K RMSNorm is not supported")
     L.require_gpu(X, W_qkv, K_cache, V_cache, attention_mask)
     B, S_tkg, H = X.shape
-    if S_tkg != 1:
-        raise NotImplementedError("only S_tkg = 1 (one new token per sequence) is supported")
+    if not 1 <= S_tkg <= 8:
+        raise ValueError(f"S_tkg must be in [1, 8] (attention_block_tkg.py:151), got {S_tkg}")
+    if B * S_tkg > 128:
+        raise ValueError(f"B * S_tkg = {B * S_tkg} must be <= 128")
     d = V_cache.shape[-1]
     if d % 2:
         raise ValueError(f"d_head must be even, got {d}")
@@ -116,8 +123,9 @@ def attention_block_tkg(
         raise ValueError(f"block KV: attention_mask covers S_ctx={S_ctx}, the table covers {S_max}")
     if tuple(attention_mask.shape) != (S_ctx, B, nq, S_tkg):
         raise ValueError(f"attention_mask shape mismatch: expected {(S_ctx, B, nq, S_tkg)}, got {tuple(attention_mask.shape)}")
-    if S_ctx - 1 > S_max:
-        raise ValueError(f"mask window S_ctx={S_ctx} exceeds cache capacity {S_max} + 1")
+    if S_ctx < S_tkg or S_ctx - S_tkg > S_max:
+        raise ValueError(f"mask window S_ctx={S_ctx} must hold the {S_tkg} new tokens after at most "
+                         f"{S_max} cache positions")
     if rmsnorm_X_enabled and rmsnorm_X_gamma is not None and tuple(rmsnorm_X_gamma.shape) not in ((1, H), (H,)):
         raise ValueError(f"rmsnorm_X_gamma must be (1, {H}), got {tuple(rmsnorm_X_gamma.shape)}")
     if (cos is None) != (sin is None):
@@ -133,7 +141,7 @@ def attention_block_tkg(
     wqkv = packing.packed_cached(W_qkv, packing.pack_in_out)
     wout = packing.packed_cached(W_out, packing.pack_in_out) if W_out is not None else None
     H_out = W_out.shape[1] if W_out is not None else 0
-    x = X.reshape(B, H).contiguous()
+    x = X.reshape(B * S_tkg, H).contiguous()
     gamma = rmsnorm_X_gamma.reshape(-1).to(torch.bfloat16).contiguous() \
         if (rmsnorm_X_enabled and rmsnorm_X_gamma is not None) else None
     qn = kn = None
@@ -144,11 +152,12 @@ def attention_block_tkg(
             if rmsnorm_QK_pre_rope_W_K is not None else torch.ones(d, dtype=torch.bfloat16, device=dev)
     cos_f = sin_f = None
     if cos is not None:
-        # [d/2, B, 1] -> [B, d] with the halves duplicated
-        cos_f = torch.cat([cos, cos], 0)[:, :, 0].t().float().contiguous()
-        sin_f = torch.cat([sin, sin], 0)[:, :, 0].t().float().contiguous()
-    mask_u8 = (attention_mask[:, :, :, 0] != 0).to(torch.uint8).contiguous()
-    n_prior = torch.full((B,), S_ctx - 1, dtype=torch.int32, device=dev)
+        # [d/2, B, S_tkg] -> [B * S_tkg, d] with the halves duplicated (row b * S_tkg + s)
+        cos_f = torch.cat([cos, cos], 0).permute(1, 2, 0).reshape(B * S_tkg, d).float().contiguous()
+        sin_f = torch.cat([sin, sin], 0).permute(1, 2, 0).reshape(B * S_tkg, d).float().contiguous()
+    # [S_ctx, B, nq, S_tkg] 0/1 (with S_tkg = 1 the kernel reads it as [S_ctx, B, nq])
+    mask_u8 = (attention_mask != 0).to(torch.uint8).contiguous()
+    n_prior = torch.full((B,), S_ctx - S_tkg, dtype=torch.int32, device=dev)
     wpos = None
     if update_cache:
         idx = kv_cache_update_idx.reshape(-1).to(torch.int64)
@@ -162,7 +171,7 @@ def attention_block_tkg(
     sink_f = sink.reshape(-1).float().contiguous() if sink is not None else None
     bqkv = bias_qkv.reshape(-1).to(torch.bfloat16).contiguous() if bias_qkv is not None else None
     bout = bias_out.reshape(-1).to(torch.bfloat16).contiguous() if bias_out is not None else None
-    out = torch.empty(B, H_out if W_out is not None else nq * d, dtype=torch.bfloat16, device=dev)
+    out = torch.empty(B * S_tkg, H_out if W_out is not None else nq * d, dtype=torch.bfloat16, device=dev)
     scale = float(softmax_scale) if softmax_scale is not None else 1.0 / math.sqrt(d)
     args = L.AttentionArgs(
         X=x.data_ptr(), rmsnorm_gamma=L.ptr(gamma),
@@ -175,12 +184,12 @@ def attention_block_tkg(
         w_out_packed=L.ptr(wout), bias_out=L.ptr(bout), residual=None, out=out.data_ptr(),
         B=B, H=H, H_out=H_out, nq=nq, nkv=nkv, d=d, S_max=S_max, round_qwen=0,
         active_blocks_table=L.ptr(table), blocks_per_seq=table.shape[1] if block else 0,
-        block_len=blk_len if block else 0, num_blocks=num_blocks if block else 0)
+        block_len=blk_len if block else 0, num_blocks=num_blocks if block else 0, s_tkg=S_tkg)
     lib = L.load()
-    ws = torch.zeros(max(lib.mkd_attention_workspace_bytes(B, H, nq, nkv, d, S_max), 256),
+    ws = torch.zeros(max(lib.mkd_attention_workspace_bytes_tkg(B, S_tkg, H, nq, nkv, d, S_max), 256),
                      dtype=torch.uint8, device=dev)
     rc = lib.mkd_attention_block_tkg(args, ws.data_ptr(), ws.numel(), L.stream_ptr(dev))
     L.check(rc, "attention_block_tkg")
-    if W_out is None:
-        out = out.reshape(B, nq, d, 1)
+    if W_out is None:   # [B, q_heads, d_head, S_tkg]
+        out = out.reshape(B, S_tkg, nq, d).permute(0, 2, 3, 1).contiguous()
     return out, K_cache, V_cache

@@ -24,7 +24,7 @@ ARCH = "gfx950"
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    "-Wno-unused-result", "-I", os.path.join(PKG_DIR, "..", "include"),
+    "-Wno-unused-result", "-Werror=uninitialized", "-I", os.path.join(PKG_DIR, "..", "include"),
 ]
 
 

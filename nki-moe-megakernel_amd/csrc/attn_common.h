@@ -121,10 +121,17 @@ struct HeadPrep {
   }
 };
 
-// Row t of kv head g of sequence b in a cache (flat or block layout); null when
-// the block table holds no valid block there (the row then reads as zero).
+// Sequence of row r and its token slot (several new tokens per sequence, AttnArgs::s_tkg).
+MKD_DEV int seq_of(const AttnArgs& a, int r) { return a.s_tkg > 1 ? r / a.s_tkg : r; }
+MKD_DEV int tok_of(const AttnArgs& a, int r) { return a.s_tkg > 1 ? r % a.s_tkg : 0; }
+MKD_DEV int new_tokens(const AttnArgs& a) { return a.s_tkg > 1 ? a.s_tkg : 1; }
+
+// Position t of kv head g in the cache of row b's sequence (flat or block
+// layout); null when the block table holds no valid block there (the row then
+// reads as zero).
 template <int D>
-MKD_DEV const uint16_t* kv_row(const AttnArgs& a, const uint16_t* cache, int b, int g, int t) {
+MKD_DEV const uint16_t* kv_row(const AttnArgs& a, const uint16_t* cache, int r, int g, int t) {
+  const int b = seq_of(a, r);
   if (!a.block_table) return cache + b * a.cache_b_stride + g * a.cache_h_stride + (long long)t * D;
   const int blk = a.block_table[(long long)b * a.tbl_stride + t / a.blk_len];
   if ((unsigned)blk >= (unsigned)a.num_blocks) return nullptr;
@@ -137,8 +144,8 @@ MKD_DEV int prior_clamp(const AttnArgs& a, int raw) {
   if (a.window > 0) n = min(n, a.window - 1);
   return min(n, a.S_max);
 }
-MKD_DEV int prior_len(const AttnArgs& a, int b) {
-  int n = max(a.n_prior[b], 0);
+MKD_DEV int prior_len(const AttnArgs& a, int r) {
+  int n = max(a.n_prior[seq_of(a, r)], 0);
   if (a.window > 0) n = min(n, a.window - 1);
   return min(n, a.S_max);
 }
@@ -148,22 +155,29 @@ MKD_DEV int prior_len(const AttnArgs& a, int b) {
 // (lgkmcnt(0)), so address math issued after it that does not need the count
 // would wait for its round trip too.  (The zero offset comes from a VGPR so
 // that the uniform address is not turned into a scalar load.)
-MKD_DEV int prior_raw_vmem(const AttnArgs& a, int b) {
+MKD_DEV int prior_raw_vmem(const AttnArgs& a, int r) {
   int zero;
   asm volatile("v_mov_b32 %0, 0" : "=v"(zero));
-  return a.n_prior[b + zero];
+  return a.n_prior[seq_of(a, r) + zero];
 }
 
-// Cache row that receives the new token of sequence b (-1: skip).
-MKD_DEV long long kv_write_row(const AttnArgs& a, int b) {
+// Cache row that receives row r's new token (-1: skip): token s of a sequence
+// goes s rows after the sequence's write position (a global row of a block
+// cache).
+MKD_DEV long long kv_write_row(const AttnArgs& a, int r) {
+  const int b = seq_of(a, r), s = tok_of(a, r);
   if (!a.block_table) {
     int wp = a.write_pos ? a.write_pos[b] : a.pos[b];
     if (a.window > 1 && !a.write_pos) wp = wp >= 0 ? wp % (a.window - 1) : -1;
-    return (wp >= 0 && wp < a.S_max) ? wp : -1;
+    if (wp < 0) return -1;
+    wp += s;
+    return wp < a.S_max ? wp : -1;
   }
   long long row;
   if (a.write_pos) {
     row = a.write_pos[b];
+    if (row < 0) return -1;
+    row += s;
   } else {
     const int p = a.pos[b];
     if (p < 0 || p >= a.S_max) return -1;

@@ -107,7 +107,7 @@ __global__ void __launch_bounds__(D) attn_kv_write_kernel(AttnArgs a) {
   if (row < 0) return;
   const uint16_t* src = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
   const long long off = a.block_table ? (row * a.nkv + g) * D + d
-                                      : b * a.cache_b_stride + g * a.cache_h_stride + row * D + d;
+                                      : seq_of(a, b) * a.cache_b_stride + g * a.cache_h_stride + row * D + d;
   a.k_cache[off] = src[GQA * D + d];
   a.v_cache[off] = src[(GQA + 1) * D + d];
 }
@@ -187,8 +187,8 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
       // every row address valid (clamped below S_max), so the loads carry no
       // condition and the wait for the prior length -- loaded before them --
       // can count them out; the rows past n are masked where they are used
-      const uint16_t* kc = a.k_cache + b * a.cache_b_stride + g * a.cache_h_stride;
-      const uint16_t* vc0 = a.v_cache + b * a.cache_b_stride + g * a.cache_h_stride;
+      const uint16_t* kc = a.k_cache + seq_of(a, b) * a.cache_b_stride + g * a.cache_h_stride;
+      const uint16_t* vc0 = a.v_cache + seq_of(a, b) * a.cache_b_stride + g * a.cache_h_stride;
 #pragma unroll
       for (int tt = 0; tt < TPW; ++tt) {
         const int tk = min(wbase + tt * 16 + (lane & 15), a.S_max - 1);
@@ -246,7 +246,13 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   const int n_raw = prior_raw_vmem(a, b);
   if (PRE && flat) pre_loads();
   n = __builtin_amdgcn_readfirstlane(prior_clamp(a, n_raw));
-  const int total = n + 1;
+  // the window: n cache positions, then the sequence's NT new tokens (NT = 1:
+  // this row's own, in LDS; more: every new row's prepared k / v in `prep`)
+  const int NT = new_tokens(a), seq = seq_of(a, b), tk = tok_of(a, b);
+  const uint16_t* act0 =                      // new token 0's prepared heads
+      NT > 1 ? a.prep + ((long long)seq * NT * a.nkv + g) * (GQA + 2) * D : nullptr;
+  const long long act_stride = (long long)a.nkv * (GQA + 2) * D;                     // per new token
+  const int total = n + NT;
   if (chunk0 >= total) {                      // whole block: uniform exit
     if constexpr (COH) coh_publish(flag);
     return;
@@ -303,7 +309,11 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
       u32x4_t kf;
       if constexpr (PRE) kf = kpre[tt][kk];
       else kf = kl[tt % LB][kk];
-      if (t == n) kf = *reinterpret_cast<const u32x4_t*>(&kn_s[dq + kk * 8]);
+      if (NT == 1) {
+        if (t == n) kf = *reinterpret_cast<const u32x4_t*>(&kn_s[dq + kk * 8]);
+      } else if (t >= n && t < total) {
+        kf = ld16(act0 + (t - n) * act_stride + GQA * D + dq + kk * 8);
+      }
       acc = mfma16x16x32(kf, qf[kk], acc);
     }
 #pragma unroll
@@ -312,8 +322,8 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
       float sc = a.round_qwen ? rbf(rbf(acc[i]) * a.scale) : acc[i] * a.scale;
       bool ok = tp < total && hcol < GQA;
       if (ok && a.mask) {
-        const int mt = (tp < n) ? tp : (a.mask_s_ctx - 1);
-        ok = a.mask[((long long)mt * a.B + b) * a.nq + g * GQA + hcol] != 0;
+        const int mt = (tp < n) ? tp : (a.mask_s_ctx - NT + (tp - n));
+        ok = a.mask[(((long long)mt * (a.B / NT) + seq) * a.nq + g * GQA + hcol) * NT + tk] != 0;
       }
       s[tt][i] = ok ? sc : -INFINITY;
     }
@@ -370,10 +380,14 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int t = tile0 + (lane >> 4) * 4 + j;
-      if (t == n) {
+      if (NT == 1 && t == n) {
 #pragma unroll
         for (int e = 0; e < VW; ++e) v[j][e] = *reinterpret_cast<const uint32_t*>(&vn_s[vc + 2 * e]);
-      } else if (t > n) {
+      } else if (NT > 1 && t >= n && t < total) {
+        const uint16_t* vr = act0 + (t - n) * act_stride + (GQA + 1) * D + vc;
+#pragma unroll
+        for (int e = 0; e < VW; ++e) v[j][e] = *reinterpret_cast<const uint32_t*>(vr + 2 * e);
+      } else if (t >= total) {
 #pragma unroll
         for (int e = 0; e < VW; ++e) v[j][e] = 0u;
       }
@@ -446,7 +460,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   }
 
   // the chunk holding the new token stages its k / v rows for the scatter
-  if (n >= chunk0 && n < chunk0 + CP)
+  if (NT == 1 && n >= chunk0 && n < chunk0 + CP)
     for (int i = threadIdx.x; i < D; i += 256) {
       const long long ko = (((long long)b * 2 + 0) * a.nkv + g) * D + i;
       const long long vo = (((long long)b * 2 + 1) * a.nkv + g) * D + i;
@@ -485,7 +499,7 @@ MKD_DEV void attn_combine_block(const AttnArgs& a, int h, int b, const unsigned*
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int CP = a.chunk;
   const int n = prior_len(a, b);
-  const int nch = (n + 1 + CP - 1) / CP;
+  const int nch = (n + new_tokens(a) + CP - 1) / CP;
   const long long ml0 = ((long long)b * a.nq + h) * a.n_chunks * 2;   // floats
   const long long po0 = ((long long)b * a.nq + h) * a.n_chunks * D;
   const __amdgpu_buffer_rsrc_t mlr = coh_rsrc(a.part_ml), por = coh_rsrc(a.part_o);
@@ -523,7 +537,12 @@ MKD_DEV void attn_combine_block(const AttnArgs& a, int h, int b, const unsigned*
   const int gqa = a.nq / a.nkv;
   const bool scatter = a.update_cache && h % gqa == 0 && threadIdx.x < D;
   uint16_t knew = 0, vnew = 0;
-  if (scatter) {
+  if (scatter && a.s_tkg > 1) {   // several new tokens: row b's prepared k / v
+    const int g = h / gqa;
+    const uint16_t* src = a.prep + ((long long)b * a.nkv + g) * (gqa + 2) * D;
+    knew = src[gqa * D + threadIdx.x];
+    vnew = src[(gqa + 1) * D + threadIdx.x];
+  } else if (scatter) {
     const int g = h / gqa;
     const long long ko = (((long long)b * 2 + 0) * a.nkv + g) * D + threadIdx.x;
     const long long vo = (((long long)b * 2 + 1) * a.nkv + g) * D + threadIdx.x;
@@ -598,7 +617,7 @@ MKD_DEV void attn_combine_block(const AttnArgs& a, int h, int b, const unsigned*
       if (row >= 0) {
         const long long off = a.block_table
                                   ? (row * a.nkv + g) * D + d
-                                  : b * a.cache_b_stride + g * a.cache_h_stride + row * D + d;
+                                  : seq_of(a, b) * a.cache_b_stride + g * a.cache_h_stride + row * D + d;
         a.k_cache[off] = knew;
         a.v_cache[off] = vnew;
       }
@@ -714,7 +733,7 @@ int attn_join_flag_words(int B, int nq, int nkv, int n_chunks) { return n_chunks
 bool attn_join_supported(const AttnArgs& a, int N) {
   const int gqa = a.nkv > 0 ? a.nq / a.nkv : 0;
   const int K = a.nq * a.d;
-  return !a.prep && !a.prefill && a.B >= 1 && a.B <= kJoinMaxB && (a.chunk == 64 || a.chunk == 128) &&
+  return !a.prep && !a.prefill && a.s_tkg <= 1 && a.B >= 1 && a.B <= kJoinMaxB && (a.chunk == 64 || a.chunk == 128) &&
          (a.d == 64 || a.d == 128) && (gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8 || gqa == 16) &&
          gqa * a.nkv == a.nq && K % 128 == 0 && K / 128 <= kJoinMaxF && N > 0 &&
          (long long)a.B * K * 2 <= 32768;
@@ -760,6 +779,7 @@ static hipError_t launch_attn(const AttnArgs& a, int rope_mode, hipStream_t s) {
 template <int D, int GQA>
 static hipError_t launch_tpw(const AttnArgs& a, int rope_mode, hipStream_t s) {
   if (a.prefill && (!a.prep || !a.update_cache)) return hipErrorInvalidValue;
+  if (a.s_tkg > 1 && (!a.prep || a.prefill || a.window > 0 || a.B % a.s_tkg)) return hipErrorInvalidValue;
   if (a.prep) {
     hipLaunchKernelGGL((attn_prep_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode);
     if (hipError_t e = hipGetLastError()) return e;

@@ -734,10 +734,12 @@ struct AttnWs {
   int chunk, n_chunks;
 };
 
-static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_max) {
+// B: query rows (sequences x new tokens each); s_tkg new tokens per sequence
+// (the attended window ends s_tkg - 1 positions past S_max at most)
+static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_max, int s_tkg = 1) {
   AttnWs w;
   w.chunk = attn_chunk_for(B, nkv, S_max);
-  w.n_chunks = (S_max + 1 + w.chunk - 1) / w.chunk;
+  w.n_chunks = (S_max + s_tkg + w.chunk - 1) / w.chunk;
   w.hnorm = c.take<uint16_t>((size_t)B * H);
   // the QKV projection of 17..128 tokens comes as split-K partials
   const int qparts = std::max(1, gemm_mid_kgrid((nq + 2 * nkv) * d, H, B));
@@ -751,8 +753,13 @@ static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_
 }
 
 size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S_max) {
+  return mkd_attention_workspace_bytes_tkg(B, 1, H, nq, nkv, d, S_max);
+}
+
+size_t mkd_attention_workspace_bytes_tkg(int B, int s_tkg, int H, int nq, int nkv, int d, int S_max) {
+  const int nt = s_tkg > 1 ? s_tkg : 1;
   Carver c{nullptr, 0};
-  carve_attn(c, B, H, nq, nkv, d, S_max);
+  carve_attn(c, B * nt, H, nq, nkv, d, S_max, nt);
   return c.used;
 }
 
@@ -767,12 +774,14 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
                           int o_kgrid = 1, const QkvNormArgs* qn = nullptr, bool prefill = false,
                           const AttnJoinArgs* join = nullptr) {
   const int qkv_n = (p->nq + 2 * p->nkv) * p->d;
+  const int NT = p->s_tkg > 1 ? p->s_tkg : 1;
+  const int rows = p->B * NT;            // query tokens: NT consecutive rows per sequence
   int qkv_parts = 1;
   // 1. optional RMSNorm
   const void* xin = p->X;
   if (p->rmsnorm_gamma) {
     MKD_TRY(rmsnorm_launch(p->X, 0, static_cast<const uint16_t*>(p->rmsnorm_gamma),
-                           w.hnorm, nullptr, p->B, p->H, p->H,
+                           w.hnorm, nullptr, rows, p->H, p->H,
                            p->hidden_actual > 0 ? p->hidden_actual : p->H, p->rmsnorm_eps,
                            p->rmsnorm_order, s), "attn rmsnorm");
     xin = w.hnorm;
@@ -782,20 +791,20 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   if (qn) {
     QkvNormArgs q = *qn;
     q.w = static_cast<const uint16_t*>(p->w_qkv_packed);
-    q.N = qkv_n; q.K = p->H; q.T = p->B;
+    q.N = qkv_n; q.K = p->H; q.T = rows;
     q.y = w.qkv; q.ldy = qkv_n;
     const int ps = prof_begin(MKD_KCLASS_QKV, s);
     MKD_TRY(qkv_norm_launch(q, s), "qkv + norm");
     prof_end(ps, s);
   } else {
-    GemmArgs g = dense_args(p->w_qkv_packed, xin, p->H, qkv_n, p->H, p->B, w.qkv, qkv_n);
+    GemmArgs g = dense_args(p->w_qkv_packed, xin, p->H, qkv_n, p->H, rows, w.qkv, qkv_n);
     g.bias = static_cast<const uint16_t*>(p->bias_qkv);
     const int ps = prof_begin(MKD_KCLASS_QKV, s);
     // the decode step at 17..128 tokens: activation slices in LDS, K-split partials
     // that the head preparation adds in order
-    const int kq = o_parts ? gemm_mid_kgrid(qkv_n, p->H, p->B) : 0;
+    const int kq = o_parts ? gemm_mid_kgrid(qkv_n, p->H, rows) : 0;
     if (kq) {
-      g.part_stride = (long long)p->B * qkv_n;
+      g.part_stride = (long long)rows * qkv_n;
       MKD_TRY(gemm_mid_launch(g, kq, false, s), "qkv (mid)");
       qkv_parts = kq;
     } else if (int rc = dense_gemm(g, EPI_F32, false, s)) {
@@ -807,7 +816,7 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   AttnArgs a;
   memset(&a, 0, sizeof(a));
   a.qkv = w.qkv; a.ld_qkv = qkv_n;
-  a.qkv_nparts = qkv_parts; a.qkv_part_stride = (long long)p->B * qkv_n;
+  a.qkv_nparts = qkv_parts; a.qkv_part_stride = (long long)rows * qkv_n;
   a.q_norm = static_cast<const uint16_t*>(p->q_norm);
   a.k_norm = static_cast<const uint16_t*>(p->k_norm);
   a.qk_eps = p->qk_eps;
@@ -822,12 +831,12 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   a.sink = p->sink;
   a.scale = p->softmax_scale > 0.f ? p->softmax_scale : 1.0f / sqrtf((float)p->d);
   a.round_qwen = p->round_qwen;
-  a.B = p->B; a.nq = p->nq; a.nkv = p->nkv; a.d = p->d; a.S_max = p->S_max;
+  a.B = rows; a.s_tkg = NT; a.nq = p->nq; a.nkv = p->nkv; a.d = p->d; a.S_max = p->S_max;
   a.chunk = w.chunk; a.n_chunks = w.n_chunks;
   a.part_o = w.po; a.part_ml = w.pml;
   // large grids prepare the q / k / v heads once per (sequence, kv head) in a
   // launch of their own; small ones inside every attention block
-  a.prep = (long long)w.n_chunks * p->nkv * p->B > 1024 ? w.prep : nullptr;
+  a.prep = (NT > 1 || (long long)w.n_chunks * p->nkv * rows > 1024) ? w.prep : nullptr;
   a.attn_out = w.attn;
   a.update_cache = p->update_cache;
   a.write_pos = p->kv_cache_update_idx;
@@ -862,7 +871,7 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   MKD_TRY(attn_combine_launch(a, s), "attention combine + kv scatter");
   // 5. output projection
   if (p->w_out_packed) {
-    GemmArgs o = dense_args(p->w_out_packed, w.attn, p->nq * p->d, p->H_out, p->nq * p->d, p->B,
+    GemmArgs o = dense_args(p->w_out_packed, w.attn, p->nq * p->d, p->H_out, p->nq * p->d, rows,
                             p->out, p->H_out);
     o.bias = static_cast<const uint16_t*>(p->bias_out);
     o.residual = static_cast<const uint16_t*>(p->residual);
@@ -870,7 +879,7 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     if (o_parts) {
       o.y = o_parts;
       o.residual = nullptr;
-      o.part_stride = (long long)p->B * p->H_out;
+      o.part_stride = (long long)rows * p->H_out;
       if (o_kgrid > 1) {   // 17..128 tokens: K-split partials (gemm_mid_kgrid)
         MKD_TRY(gemm_mid_launch(o, o_kgrid, false, s), "o_proj (mid)");
       } else {
@@ -882,7 +891,7 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     }
     prof_end(ps, s);
   } else {
-    MKD_TRY(hipMemcpyAsync(p->out, w.attn, (size_t)p->B * p->nq * p->d * 2, hipMemcpyDeviceToDevice, s),
+    MKD_TRY(hipMemcpyAsync(p->out, w.attn, (size_t)rows * p->nq * p->d * 2, hipMemcpyDeviceToDevice, s),
             "attn copy");
   }
   return MKD_OK;
@@ -893,6 +902,18 @@ static int validate_attn(const mkd_attention_args* p) {
   MKD_REQUIRE(p->X && p->w_qkv_packed && p->k_cache && p->v_cache && p->n_prior && p->out,
               MKD_ERR_NULL, "attention: null pointer");
   MKD_REQUIRE(p->B > 0 && p->B <= 128, MKD_ERR_INVALID, "attention: B %d must be in [1, 128]", p->B);
+  MKD_REQUIRE(p->s_tkg >= 0 && p->s_tkg <= 8, MKD_ERR_UNSUPPORTED, "attention: s_tkg %d must be in [0, 8]",
+              p->s_tkg);
+  if (p->s_tkg > 1) {
+    MKD_REQUIRE(p->B * p->s_tkg <= 128, MKD_ERR_INVALID, "attention: B * s_tkg = %d must be <= 128",
+                p->B * p->s_tkg);
+    MKD_REQUIRE(p->window == 0 && !p->residual, MKD_ERR_UNSUPPORTED,
+                "attention: several new tokens per sequence with a ring cache or a residual are not supported");
+    MKD_REQUIRE(!p->update_cache || p->kv_cache_update_idx, MKD_ERR_NULL,
+                "attention: several new tokens per sequence need kv_cache_update_idx");
+    MKD_REQUIRE(!p->mask || p->mask_s_ctx >= p->s_tkg, MKD_ERR_INVALID,
+                "attention: mask_s_ctx %d < s_tkg %d", p->mask_s_ctx, p->s_tkg);
+  }
   MKD_REQUIRE(p->d == 64 || p->d == 128, MKD_ERR_UNSUPPORTED, "attention: d_head %d must be 64 or 128", p->d);
   MKD_REQUIRE(p->nkv > 0 && p->nq % p->nkv == 0, MKD_ERR_INVALID, "attention: q_heads %d not a multiple of kv_heads %d", p->nq, p->nkv);
   const int g = p->nq / p->nkv;
@@ -924,7 +945,8 @@ int mkd_attention_block_tkg(const mkd_attention_args* p, void* workspace, size_t
   if (int rc = validate_attn(p)) return rc;
   MKD_REQUIRE(workspace, MKD_ERR_NULL, "attention: null workspace");
   Carver c{static_cast<char*>(workspace), workspace_bytes};
-  AttnWs w = carve_attn(c, p->B, p->H, p->nq, p->nkv, p->d, p->S_max);
+  const int nt = p->s_tkg > 1 ? p->s_tkg : 1;
+  AttnWs w = carve_attn(c, p->B * nt, p->H, p->nq, p->nkv, p->d, p->S_max, nt);
   MKD_REQUIRE(c.ok, MKD_ERR_WORKSPACE, "attention: workspace %zu < %zu bytes", workspace_bytes, c.used);
   return attention_core(p, w, nullptr, nullptr, static_cast<hipStream_t>(stream));
 }

@@ -262,6 +262,14 @@ struct AttnArgs {
   // k / v rows are written to the cache before the attention reads it, so each
   // token attends the rows of the earlier tokens of the same step
   int prefill;
+  // new tokens per sequence (0 / 1: one).  With s_tkg > 1 the B rows are
+  // s_tkg consecutive tokens of each of B / s_tkg sequences: row r is token
+  // r % s_tkg of sequence r / s_tkg, whose window is its n_prior cache positions
+  // followed by the sequence's s_tkg new tokens (their prepared k / v rows come
+  // from `prep`, which is then required); the mask is [S_ctx, B / s_tkg, nq,
+  // s_tkg] with new token i at slot S_ctx - s_tkg + i, and token s is written
+  // at write_pos[sequence] + s
+  int s_tkg;
 };
 // rope_mode: 0 none, 1 cos/sin tables, 2 from pos and inv_freq
 hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s);

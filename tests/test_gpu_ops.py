@@ -459,6 +459,139 @@ def test_attention_block_tkg_block_kv(mk, dev, B, nq, nkv, d, blk, n_act, num_bl
             assert max_abs_rel(Kn[r], newk[b]) < TOL
 
 
+def _multi_mask(g, P, B, nq, S, keep=0.75):
+    """[P + S, B, nq, S]: random prior slots, then causal among the S new tokens."""
+    prior = (torch.rand(P, B, nq, S, generator=g) < keep).to(torch.bfloat16)
+    causal = (torch.arange(S)[:, None] <= torch.arange(S)[None, :]).to(torch.bfloat16)
+    return torch.cat([prior, causal[:, None, None, :].expand(S, B, nq, S)], 0).contiguous()
+
+
+def _rope_rows(B, S, P, d):
+    cos, sin = ref.rope_cos_sin((torch.arange(S)[None, :] + P + 3 * torch.arange(B)[:, None]).reshape(-1), d, 1e6)
+    cos_r = cos[:, :d // 2].reshape(B, S, d // 2).permute(2, 0, 1).contiguous()   # [d/2, B, S]
+    sin_r = sin[:, :d // 2].reshape(B, S, d // 2).permute(2, 0, 1).contiguous()
+    return cos_r, sin_r
+
+
+@pytest.mark.parametrize("B,H,nq,nkv,d,S,P,S_max,qknorm,sink,wout", [
+    (1, 2048, 8, 1, 128, 4, 500, 640, True, False, True),
+    (2, 512, 8, 2, 64, 8, 40, 64, False, True, True),
+    (3, 256, 4, 1, 128, 2, 0, 8, False, False, False),
+    (2, 512, 16, 2, 128, 3, 300, 320, True, False, True),
+])
+def test_attention_block_tkg_multi_token(mk, dev, B, H, nq, nkv, d, S, P, S_max, qknorm, sink, wout):
+    """S_tkg > 1 (attention_block_tkg.py:151): each sequence attends its P cache
+    positions, then its S new tokens (causal among them here), against the
+    oracle per kv head; token s of sequence b lands at kv_cache_update_idx[b] + s
+    and nothing else changes; without W_out the output is [B, nq, d, S]."""
+    from nki_moe_megakernel_amd.common_types import QuantizationType
+    print(f"multi-token attention: B={B} S={S} P={P} nkv={nkv} d={d}", flush=True)
+    g = torch.Generator().manual_seed(B * 31 + S * 7 + P)
+    X = bf(torch.randn(B, S, H, generator=g))
+    W = bf(0.03 * torch.randn(H, d * (nq + 2 * nkv), generator=g))
+    Wo = bf(0.03 * torch.randn(nq * d, H, generator=g)) if wout else None
+    qn = bf(1 + 0.1 * torch.randn(1, d, generator=g)) if qknorm else None
+    kn = bf(1 + 0.1 * torch.randn(1, d, generator=g)) if qknorm else None
+    kshape = (B, S_max, d) if nkv == 1 else (B, nkv, S_max, d)
+    Kc = bf(torch.randn(*kshape, generator=g))
+    Vc = bf(torch.randn(*kshape, generator=g))
+    cos_r, sin_r = _rope_rows(B, S, P, d)
+    mask = _multi_mask(g, P, B, nq, S)
+    sk = torch.randn(nq, 1, generator=g) if sink else None
+    upd = torch.full((B, 1), P, dtype=torch.int64)
+    if B > 1:
+        upd[-1, 0] = 0xFFFFFFFF
+    Kg, Vg = Kc.to(dev), Vc.to(dev)
+    out, K2, V2 = mk.attention_block_tkg(
+        X.to(dev), None, False, 1e-6, None, W.to(dev), None,
+        QuantizationType.NONE, None, None, qknorm, 1e-6, qn.to(dev) if qknorm else None,
+        kn.to(dev) if qknorm else None, cos_r.to(dev), sin_r.to(dev), True, False, 1e-6, None,
+        None, False, None, Kg, Vg, mask.to(dev), sk.to(dev) if sink else None, True,
+        upd.to(dev), Wo.to(dev) if wout else None, None, QuantizationType.NONE, None, None, False, False)
+    gqa = nq // nkv
+    Kr4 = Kc.float().reshape(B, nkv, S_max, d) if nkv > 1 else Kc.float()[:, None]
+    Vr4 = Vc.float().reshape(B, nkv, S_max, d) if nkv > 1 else Vc.float()[:, None]
+    attn = torch.zeros(B * S, nq * d)
+    newk = torch.zeros(B, nkv, S, d)
+    for h in range(nkv):
+        cols = torch.cat([torch.arange(h * gqa * d, (h + 1) * gqa * d),
+                          nq * d + h * d + torch.arange(d),
+                          (nq + nkv) * d + h * d + torch.arange(d)])
+        Kh, Vh = Kr4[:, h].clone(), Vr4[:, h].clone()
+        o, Kh2, _ = ref.attention_block_tkg(
+            X.float(), W.float()[:, cols], None, 1e-6, None,
+            qn.float() if qknorm else None, kn.float() if qknorm else None, 1e-6, cos_r, sin_r,
+            Kh, Vh, mask[:, :, h * gqa:(h + 1) * gqa].float(),
+            sk[h * gqa:(h + 1) * gqa] if sink else None, True, torch.full((B, 1), P), None, None)
+        attn[:, h * gqa * d:(h + 1) * gqa * d] = o
+        newk[:, h] = Kh2[:, P:P + S]
+    if wout:
+        assert tuple(out.shape) == (B * S, H)
+        assert max_abs_rel(out, attn @ Wo.float()) < TOL
+    else:
+        assert tuple(out.shape) == (B, nq, d, S)
+        assert max_abs_rel(out, attn.reshape(B, S, nq, d).permute(0, 2, 3, 1)) < TOL
+    Kn = Kg.cpu().reshape(B, nkv, S_max, d) if nkv > 1 else Kg.cpu()[:, None]
+    K0 = Kc.reshape(B, nkv, S_max, d) if nkv > 1 else Kc[:, None]
+    for b in range(B):
+        changed = (Kn[b] != K0[b]).any(-1).any(0).nonzero().flatten().tolist()
+        if int(upd[b, 0]) == 0xFFFFFFFF:
+            assert changed == []
+        else:
+            assert changed == list(range(P, P + S)), (b, changed[:12])
+            assert max_abs_rel(Kn[b, :, P:P + S], newk[b]) < TOL
+
+
+def test_attention_block_tkg_multi_token_block_kv(mk, dev):
+    """S_tkg = 4 on a paged cache: the window's cache part through the block
+    table, token s written at global row kv_cache_update_idx[b] + s."""
+    from nki_moe_megakernel_amd.common_types import QuantizationType
+    B, nq, nkv, d, blk, n_act, num_blocks, S, H = 2, 8, 2, 64, 16, 5, 24, 4, 256
+    print("multi-token attention, block KV", flush=True)
+    g = torch.Generator().manual_seed(77)
+    X = bf(torch.randn(B, S, H, generator=g))
+    W = bf(0.05 * torch.randn(H, d * (nq + 2 * nkv), generator=g))
+    Wo = bf(0.05 * torch.randn(nq * d, H, generator=g))
+    Kb = bf(torch.randn(num_blocks, blk, nkv, d, generator=g))
+    Vb = bf(torch.randn(num_blocks, blk, nkv, d, generator=g))
+    table = torch.stack([torch.randperm(num_blocks, generator=g)[:n_act] for _ in range(B)]).to(torch.int32)
+    S_ctx = n_act * blk
+    P = S_ctx - S
+    mask = _multi_mask(g, P, B, nq, S)
+    cos_r, sin_r = _rope_rows(B, S, P, d)
+    # each sequence's new rows: the table's block of position P, rows P % blk .. + S (one block)
+    upd = torch.tensor([[int(table[b, P // blk]) * blk + P % blk] for b in range(B)], dtype=torch.int64)
+    Kg, Vg = Kb.to(dev), Vb.to(dev)
+    out, _, _ = mk.attention_block_tkg(
+        X.to(dev), None, False, 1e-6, None, W.to(dev), None, QuantizationType.NONE, None, None,
+        False, 1e-6, None, None, cos_r.to(dev), sin_r.to(dev), True, False, 1e-6, None, None,
+        False, table.to(dev), Kg, Vg, mask.to(dev), None, True, upd.to(dev), Wo.to(dev), None,
+        QuantizationType.NONE, None, None, False, False)
+    Kf = ref.block_kv_to_flat(Kb.float(), table)       # [B, S_ctx, nkv, d]
+    Vf = ref.block_kv_to_flat(Vb.float(), table)
+    gqa = nq // nkv
+    attn = torch.zeros(B * S, nq * d)
+    newk = torch.zeros(B, S, nkv, d)
+    for h in range(nkv):
+        cols = torch.cat([torch.arange(h * gqa * d, (h + 1) * gqa * d),
+                          nq * d + h * d + torch.arange(d),
+                          (nq + nkv) * d + h * d + torch.arange(d)])
+        Kh, Vh = Kf[:, :, h].clone(), Vf[:, :, h].clone()
+        o, K2, _ = ref.attention_block_tkg(
+            X.float(), W.float()[:, cols], None, 1e-6, None, None, None, 1e-6, cos_r, sin_r,
+            Kh, Vh, mask[:, :, h * gqa:(h + 1) * gqa].float(), None, True, torch.full((B, 1), P), None, None)
+        attn[:, h * gqa * d:(h + 1) * gqa * d] = o
+        newk[:, :, h] = K2[:, P:P + S]
+    assert max_abs_rel(out, attn @ Wo.float()) < TOL
+    Kn = Kg.cpu().reshape(num_blocks * blk, nkv, d)
+    K0 = Kb.reshape(num_blocks * blk, nkv, d)
+    changed = (Kn != K0).any(-1).any(-1).nonzero().flatten().tolist()
+    want = sorted(int(upd[b, 0]) + s for b in range(B) for s in range(S))
+    assert changed == want, (changed, want)
+    for b in range(B):
+        assert max_abs_rel(Kn[int(upd[b, 0]):int(upd[b, 0]) + S], newk[b]) < TOL
+
+
 # ---------------------------------------------------------------- Qwen layer / step
 def _model_from_hf(mk, hf, cfg, B, dev):
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q

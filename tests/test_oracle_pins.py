@@ -284,6 +284,40 @@ def test_kv_scatter_only_target_rows_change():
     assert torch.equal(Vc[0, 9], qkv[0, 160:])
 
 
+def test_multi_token_window_equals_token_by_token():
+    """S_tkg new tokens in one call (window = the cache positions, then the new
+    tokens; causal among them) equal S_tkg one-token calls that each write their
+    k / v row at the next position -- the multi-token form reduces to the
+    one-token form pinned above."""
+    g = torch.Generator().manual_seed(11)
+    B, S, H, nq, d, P, S_max = 2, 4, 64, 4, 32, 9, 16
+    X = torch.randn(B, S, H, generator=g)
+    W = 0.2 * torch.randn(H, d * (nq + 2), generator=g)
+    qn = 1 + 0.1 * torch.randn(d, generator=g)
+    kn = 1 + 0.1 * torch.randn(d, generator=g)
+    Kc = torch.randn(B, S_max, d, generator=g)
+    Vc = torch.randn(B, S_max, d, generator=g)
+    cos, sin = ref.rope_cos_sin(torch.arange(P, P + S).repeat(B), d, 1e4)
+    cos_r = cos[:, :d // 2].reshape(B, S, d // 2).permute(2, 0, 1).contiguous()   # [d/2, B, S]
+    sin_r = sin[:, :d // 2].reshape(B, S, d // 2).permute(2, 0, 1).contiguous()
+    prior = (torch.rand(P, B, nq, S, generator=g) > 0.3).float()
+    causal = (torch.arange(S)[:, None] <= torch.arange(S)[None, :]).float()     # [key i, query s]
+    mask = torch.cat([prior, causal[:, None, None, :].expand(S, B, nq, S)], 0)   # [P + S, B, nq, S]
+    idx = torch.full((B, 1), P, dtype=torch.int64)
+    K1, V1 = Kc.clone(), Vc.clone()
+    out, _, _ = ref.attention_block_tkg(X, W, None, None, None, qn, kn, 1e-6, cos_r, sin_r, K1, V1,
+                                        mask, None, True, idx, None, None)
+    K2, V2 = Kc.clone(), Vc.clone()
+    for i in range(S):
+        m_i = torch.cat([prior[:, :, :, i:i + 1], torch.ones(i + 1, B, nq, 1)], 0)
+        o_i, _, _ = ref.attention_block_tkg(X[:, i:i + 1], W, None, None, None, qn, kn, 1e-6,
+                                            cos_r[:, :, i:i + 1], sin_r[:, :, i:i + 1], K2, V2, m_i,
+                                            None, True, idx + i, None, None)
+        assert torch.allclose(out.reshape(B, S, -1)[:, i], o_i, atol=1e-5), i
+    assert torch.allclose(K1, K2, atol=1e-6) and torch.allclose(V1, V2, atol=1e-6)
+    assert (K1 != Kc).any(-1).nonzero()[:, 1].unique().tolist() == list(range(P, P + S))
+
+
 # ------------------------------------------------------------------ whole layer vs HF
 def _load_golden():
     from safetensors.torch import load_file
