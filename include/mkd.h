@@ -49,6 +49,8 @@ extern "C" {
 /* Expert activation (moe_tkg activation_fn) */
 #define MKD_ACT_SILU 0
 #define MKD_ACT_SWISH 1 /* g * sigmoid(alpha * g), GPT-OSS alpha = 1.702 */
+#define MKD_ACT_GELU 2       /* g/2 (1 + erf(g / sqrt 2))                        */
+#define MKD_ACT_GELU_TANH 3  /* g/2 (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3)))    */
 
 /* Affinity scaling (moe_tkg expert_affinities_scaling_mode) */
 #define MKD_SCALE_NONE 0

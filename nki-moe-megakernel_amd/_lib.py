@@ -24,7 +24,7 @@ MKD_ERR_HIP = -5
 DT_BF16, DT_F32 = 0, 1
 
 ROUTER_SIGMOID, ROUTER_PRE_NORM, ROUTER_NORM_TOPK, ROUTER_QWEN = 1, 2, 4, 8
-ACT_SILU, ACT_SWISH = 0, 1
+ACT_SILU, ACT_SWISH, ACT_GELU, ACT_GELU_TANH = 0, 1, 2, 3
 SCALE_NONE, SCALE_POST = 0, 1
 
 

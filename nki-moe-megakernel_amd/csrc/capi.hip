@@ -629,7 +629,7 @@ int moe_entry(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, vo
               MKD_ERR_UNSUPPORTED, "moe_tkg: only NO_SCALE and POST_SCALE affinity scaling are supported");
   MKD_REQUIRE(!(p->scaling_mode == MKD_SCALE_POST && !p->expert_affinities && !p->slot_weights),
               MKD_ERR_NULL, "moe_tkg: POST_SCALE needs expert_affinities");
-  MKD_REQUIRE(p->activation == MKD_ACT_SILU || p->activation == MKD_ACT_SWISH, MKD_ERR_UNSUPPORTED,
+  MKD_REQUIRE(p->activation >= MKD_ACT_SILU && p->activation <= MKD_ACT_GELU_TANH, MKD_ERR_UNSUPPORTED,
               "moe_tkg: unsupported activation %d", p->activation);
   MKD_REQUIRE(p->weight_format == 0 || p->weight_format == MKD_MX_E4M3 ||
                   p->weight_format == MKD_MX_E2M1, MKD_ERR_INVALID,

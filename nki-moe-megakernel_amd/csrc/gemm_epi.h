@@ -29,7 +29,8 @@ MKD_DEV float gated_sigmoid(float g, float z) {
 
 // One gated activation value from the gate and up projections (fp32, bias
 // already added).  Qwen rounding: g, u -> bf16, silu(g) -> bf16, product;
-// otherwise clamps, then act(g) * u with act = silu or swish(alpha).
+// otherwise clamps, then act(g) * u with act (kAct*) = silu, swish(alpha),
+// GELU (erf) or GELU's tanh approximation.
 MKD_DEV float swiglu_value(const GemmArgs& a, float gv, float uv) {
   if (a.round_qwen) {
     const float g = rbf(gv), u = rbf(uv);
@@ -37,7 +38,10 @@ MKD_DEV float swiglu_value(const GemmArgs& a, float gv, float uv) {
   }
   const float g = fmaxf(fminf(gv, a.gate_hi), a.gate_lo);
   const float u = fmaxf(fminf(uv, a.up_hi), a.up_lo);
-  const float z = a.act ? a.alpha * g : g;
+  if (a.act == kActGelu) return 0.5f * g * (1.0f + erff(g * 0.70710678118654752f)) * u;
+  if (a.act == kActGeluTanh)
+    return 0.5f * g * (1.0f + tanhf(0.79788456080286536f * (g + 0.044715f * g * g * g))) * u;
+  const float z = a.act == kActSwish ? a.alpha * g : g;
   return gated_sigmoid(g, z) * u;
 }
 

@@ -8,6 +8,9 @@ namespace mkd {
 
 enum Epi { EPI_F32 = 0, EPI_BF16 = 1, EPI_RESID_BF16 = 2, EPI_SWIGLU_BF16 = 3, EPI_SCALE_F32 = 4 };
 
+// Gated expert activations (GemmArgs::act; the values of the public MKD_ACT_*)
+constexpr int kActSilu = 0, kActSwish = 1, kActGelu = 2, kActGeluTanh = 3;
+
 struct GemmArgs {
   const uint16_t* w;          // frag-packed weights (group 0)
   long long w_group_stride;   // elements between experts
@@ -30,7 +33,7 @@ struct GemmArgs {
   const uint16_t* bias;       // bf16 bias per logical output column (null = none)
   long long bias_group_stride;  // elements between experts' biases
   // EPI_SWIGLU_BF16 options
-  int act;                    // 0 silu, 1 swish(alpha)
+  int act;                    // kActSilu, kActSwish (alpha), kActGelu, kActGeluTanh
   float alpha;
   float gate_hi, gate_lo, up_hi, up_lo;
   int round_qwen;             // Qwen rounding points (else one rounding of the product)

@@ -168,7 +168,8 @@ def moe_tkg(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
     if T > 128 and not _prefill:
         raise ValueError("Currently only batch size * seq len <= 128 is supported (except for all-expert mode)")
     K = expert_index.shape[-1]
-    act = {ActFnType.SiLU: L.ACT_SILU, ActFnType.Swish: L.ACT_SWISH}.get(activation_fn)
+    act = {ActFnType.SiLU: L.ACT_SILU, ActFnType.Swish: L.ACT_SWISH, ActFnType.GELU: L.ACT_GELU,
+           ActFnType.GELU_Tanh_Approx: L.ACT_GELU_TANH}.get(activation_fn)
     if act is None:
         raise NotImplementedError(f"activation {activation_fn} is not supported")
     gu = packing.packed_cached(expert_gate_up_weights, packing.pack_experts_gate_up_ref)

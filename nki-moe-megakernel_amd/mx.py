@@ -229,7 +229,8 @@ def moe_tkg_mx(hidden_input, expert_gate_up_weights, expert_down_weights, expert
     if dcodes.shape[0] != E or dcodes.shape[3] != H:
         raise ValueError(f"down weights {tuple(dcodes.shape)} do not match E={E}, H={H}")
     K = expert_index.shape[-1]
-    act = {ActFnType.SiLU: L.ACT_SILU, ActFnType.Swish: L.ACT_SWISH}.get(activation_fn)
+    act = {ActFnType.SiLU: L.ACT_SILU, ActFnType.Swish: L.ACT_SWISH, ActFnType.GELU: L.ACT_GELU,
+           ActFnType.GELU_Tanh_Approx: L.ACT_GELU_TANH}.get(activation_fn)
     if act is None:
         raise NotImplementedError(f"activation {activation_fn} is not supported")
 

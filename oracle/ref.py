@@ -159,8 +159,10 @@ def act_fn_apply(g: torch.Tensor, act: str) -> torch.Tensor:
         return g * torch.sigmoid(g)
     if act == "swish":          # GPT-OSS: g * sigmoid(1.702 g) (HF modeling_gpt_oss.py:82-88)
         return g * torch.sigmoid(1.702 * g)
-    if act == "gelu":
+    if act == "gelu":           # erf form (nl.gelu)
         return torch.nn.functional.gelu(g)
+    if act == "gelu_tanh":      # tanh approximation (nl.gelu_apprx_tanh)
+        return torch.nn.functional.gelu(g, approximate="tanh")
     raise ValueError(act)
 
 

@@ -254,6 +254,8 @@ def test_router_rejects_bad_pipeline(mk, dev):
     (37, 32, 4, 256, 64, "swish", True, True),
     (64, 128, 8, 256, 64, "silu", False, False),
     (128, 8, 2, 128, 32, "silu", False, True),
+    (3, 16, 4, 512, 128, "gelu", False, True),
+    (20, 32, 4, 256, 64, "gelu_tanh", True, False),
 ])
 def test_moe_tkg(mk, dev, T, E, K, H, I, act, clamp, bias):
     from nki_moe_megakernel_amd.common_types import ActFnType, ExpertAffinityScaleMode
@@ -271,7 +273,8 @@ def test_moe_tkg(mk, dev, T, E, K, H, I, act, clamp, bias):
                      expert_gate_up_bias=gub.to(dev) if bias else None,
                      expert_down_bias=dnb.to(dev) if bias else None,
                      expert_affinities_scaling_mode=ExpertAffinityScaleMode.POST_SCALE,
-                     activation_fn=ActFnType.Swish if act == "swish" else ActFnType.SiLU, **kw)
+                     activation_fn={"swish": ActFnType.Swish, "gelu": ActFnType.GELU,
+                                    "gelu_tanh": ActFnType.GELU_Tanh_Approx}.get(act, ActFnType.SiLU), **kw)
     y_ref = ref.moe_tkg(x, gu, dn, aff, idx.long(), gub, dnb, "post", act,
                         gate_clamp_upper=7.0 if clamp else None,
                         up_clamp_upper=7.0 if clamp else None, up_clamp_lower=-7.0 if clamp else None)

@@ -165,6 +165,28 @@ def test_one_hot_routing_is_dense_swiglu():
     assert torch.allclose(y, dense, rtol=1e-5, atol=1e-6)
 
 
+def test_moe_gelu_activations_closed_form():
+    """One expert per token with weight 1: the oracle's GELU-gated expert equals
+    g/2 (1 + erf(g / sqrt 2)) * u (math.erf) and the tanh form
+    g/2 (1 + tanh(sqrt(2/pi) (g + 0.044715 g^3))) (math.tanh), element by element."""
+    g = torch.Generator().manual_seed(5)
+    T, E, H, I = 3, 4, 32, 16
+    x = torch.randn(T, H, generator=g)
+    gu = 0.3 * torch.randn(E, H, 2, I, generator=g)
+    dn = 0.3 * torch.randn(E, I, H, generator=g)
+    idx = torch.tensor([[1], [3], [0]])
+    aff = torch.zeros(T, E).scatter_(1, idx, 1.0)
+    for act, f in [("gelu", lambda v: 0.5 * v * (1 + math.erf(v / math.sqrt(2)))),
+                   ("gelu_tanh", lambda v: 0.5 * v * (1 + math.tanh(math.sqrt(2 / math.pi) * (v + 0.044715 * v ** 3))))]:
+        y = ref.moe_tkg(x, gu, dn, aff, idx, None, None, "post", act, emulate_bf16=False)
+        for t in range(T):
+            e = int(idx[t, 0])
+            gv = x[t] @ gu[e, :, 0, :]
+            uv = x[t] @ gu[e, :, 1, :]
+            h = torch.tensor([f(float(a)) for a in gv]) * uv
+            assert torch.allclose(y[t], h @ dn[e], atol=1e-5), act
+
+
 def test_moe_clamps_and_swish():
     # GPT-OSS semantics: gate <= 7, up in [-7, 7], g * sigmoid(1.702 g) (HF modeling_gpt_oss.py:82-88)
     g = torch.Generator().manual_seed(8)
