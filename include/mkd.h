@@ -269,6 +269,14 @@ typedef struct {
    * a global row for a block cache), which is then required.  No ring cache
    * (window) and no residual with s_tkg > 1. */
   int s_tkg;
+  /* Post-RoPE per-head RMSNorm, rmsnorm_QK_post_rope_* of
+   * attention_block_tkg.py:107-110 (applied at :906-910, :1093-1138): after
+   * RoPE, each query head becomes x * rsqrt(mean(x^2) + qk_post_eps) *
+   * q_norm_post, each key head the same with k_norm_post, in fp32.  [d] bf16
+   * each, or NULL: that norm is not applied. */
+  const void* q_norm_post;
+  const void* k_norm_post;
+  float qk_post_eps;
 } mkd_attention_args;
 size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S_max);
 /* The same for s_tkg new tokens per sequence (mkd_attention_args::s_tkg). */

@@ -69,6 +69,7 @@ class AttentionArgs(C.Structure):
         ("S_max", i32), ("round_qwen", i32),
         ("active_blocks_table", vp), ("blocks_per_seq", i32), ("block_len", i32), ("num_blocks", i32),
         ("hidden_actual", i32), ("window", i32), ("s_tkg", i32),
+        ("q_norm_post", vp), ("k_norm_post", vp), ("qk_post_eps", f32),
     ]
 
 

@@ -57,7 +57,8 @@ def attention_block_tkg(
     S_tkg new tokens (mask slot S_ctx - S_tkg + i = new token i; the active keys
     close the window as in attention_tkg.py), and token s is written at
     kv_cache_update_idx[b] + s (attention_block_tkg.py:1365-1470; a global row of
-    a block cache).  Flat or block caches, no quantisation.  Other reference
+    a block cache).  Pre- and post-RoPE per-head Q/K RMSNorm (attention_block_tkg.py:
+    895-910; absent weights are ones).  Flat or block caches, no quantisation.  Other reference
     options raise NotImplementedError.  enable_fa_s_prior_tiling is a
     scheduling hint (the GPU path always tiles the KV length).
     """
@@ -77,8 +78,6 @@ def attention_block_tkg(
         raise NotImplementedError("quantized QKV / output projection / FP8 KV are not supported")
     if not rope_contiguous_layout and cos is not None:
         raise NotImplementedError("interleaved RoPE layout is not supported")
-    if rmsnorm_QK_post_rope_enabled:
-        raise NotImplementedError("post-RoPE Q/K RMSNorm is not supported")
     L.require_gpu(X, W_qkv, K_cache, V_cache, attention_mask)
     B, S_tkg, H = X.shape
     if not 1 <= S_tkg <= 8:
@@ -150,6 +149,12 @@ def attention_block_tkg(
             if rmsnorm_QK_pre_rope_W_Q is not None else torch.ones(d, dtype=torch.bfloat16, device=dev)
         kn = rmsnorm_QK_pre_rope_W_K.reshape(-1).to(torch.bfloat16).contiguous() \
             if rmsnorm_QK_pre_rope_W_K is not None else torch.ones(d, dtype=torch.bfloat16, device=dev)
+    qp = kp = None
+    if rmsnorm_QK_post_rope_enabled:   # after RoPE (attention_block_tkg.py:906-910)
+        qp = rmsnorm_QK_post_rope_W_Q.reshape(-1).to(torch.bfloat16).contiguous() \
+            if rmsnorm_QK_post_rope_W_Q is not None else torch.ones(d, dtype=torch.bfloat16, device=dev)
+        kp = rmsnorm_QK_post_rope_W_K.reshape(-1).to(torch.bfloat16).contiguous() \
+            if rmsnorm_QK_post_rope_W_K is not None else torch.ones(d, dtype=torch.bfloat16, device=dev)
     cos_f = sin_f = None
     if cos is not None:
         # [d/2, B, S_tkg] -> [B * S_tkg, d] with the halves duplicated (row b * S_tkg + s)
@@ -184,7 +189,9 @@ def attention_block_tkg(
         w_out_packed=L.ptr(wout), bias_out=L.ptr(bout), residual=None, out=out.data_ptr(),
         B=B, H=H, H_out=H_out, nq=nq, nkv=nkv, d=d, S_max=S_max, round_qwen=0,
         active_blocks_table=L.ptr(table), blocks_per_seq=table.shape[1] if block else 0,
-        block_len=blk_len if block else 0, num_blocks=num_blocks if block else 0, s_tkg=S_tkg)
+        block_len=blk_len if block else 0, num_blocks=num_blocks if block else 0, s_tkg=S_tkg,
+        q_norm_post=L.ptr(qp), k_norm_post=L.ptr(kp),
+        qk_post_eps=float(rmsnorm_QK_post_rope_eps) if rmsnorm_QK_post_rope_enabled else 0.0)
     lib = L.load()
     ws = torch.zeros(max(lib.mkd_attention_workspace_bytes_tkg(B, S_tkg, H, nq, nkv, d, S_max), 256),
                      dtype=torch.uint8, device=dev)

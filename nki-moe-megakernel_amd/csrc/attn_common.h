@@ -113,6 +113,19 @@ struct HeadPrep {
           x[e] = a.round_qwen ? rbf(rbf(x[e] * rbf(cs[e])) + rbf(rot[e] * rbf(sn[e])))
                               : x[e] * cs[e] + rot[e] * sn[e];
       }
+      // post-RoPE RMSNorm (attention_block_tkg.py:906-910, 1093-1138); its
+      // weights are loaded here only when present, so the default path issues
+      // no extra loads
+      const uint16_t* pw = kind == 0 ? a.q_norm_post : a.k_norm_post;
+      if (pw) {
+        const int i0 = lane < HD ? lane : 0;
+        const float w0 = bf2f(pw[i0]), w1 = bf2f(pw[i0 + HD]);
+        const float ss = wave_sum(x[0] * x[0] + x[1] * x[1]);
+        const float rinv = 1.0f / sqrtf(ss * (1.0f / D) + a.qk_post_eps);
+        x[0] = (x[0] * rinv) * w0;
+        x[1] = (x[1] * rinv) * w1;
+        if (a.round_qwen) { x[0] = rbf(x[0]); x[1] = rbf(x[1]); }
+      }
     }
     if (lane < HD) {
       dst[lane] = (uint16_t)f2bf(x[0]);

@@ -820,6 +820,9 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   a.q_norm = static_cast<const uint16_t*>(p->q_norm);
   a.k_norm = static_cast<const uint16_t*>(p->k_norm);
   a.qk_eps = p->qk_eps;
+  a.q_norm_post = static_cast<const uint16_t*>(p->q_norm_post);
+  a.k_norm_post = static_cast<const uint16_t*>(p->k_norm_post);
+  a.qk_post_eps = p->qk_post_eps;
   a.cos = p->cos; a.sin = p->sin; a.inv_freq = inv_freq; a.pos = pos_for_rope;
   a.kv_new = w.kvn;
   a.k_cache = static_cast<uint16_t*>(p->k_cache);

@@ -273,6 +273,12 @@ struct AttnArgs {
   // s_tkg] with new token i at slot S_ctx - s_tkg + i, and token s is written
   // at write_pos[sequence] + s
   int s_tkg;
+  // per-head RMSNorm after RoPE (x * rsqrt(mean(x^2) + qk_post_eps) * w) of
+  // the query heads with q_norm_post, of the key heads with k_norm_post; null:
+  // not applied
+  const uint16_t* q_norm_post;
+  const uint16_t* k_norm_post;
+  float qk_post_eps;
 };
 // rope_mode: 0 none, 1 cos/sin tables, 2 from pos and inv_freq
 hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s);

@@ -506,12 +506,15 @@ def block_kv_to_flat(cache: torch.Tensor, table: torch.Tensor) -> torch.Tensor:
 def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
                         q_norm_w, k_norm_w, qk_eps, cos, sin, K_cache, V_cache,
                         attention_mask, sink, update_cache, kv_cache_update_idx,
-                        W_out, bias_out, softmax_scale=None):
+                        W_out, bias_out, softmax_scale=None, q_norm_post_w=None,
+                        k_norm_post_w=None, qk_post_eps=None):
     """Generic attention block (fp32 math, kv_heads = 1 as in the reference :353).
 
     X [B, S_tkg, H]; W_qkv [H, d*(nq+2)] packed Q | K | V (:363-384);
     optional pre-attention RMSNorm (:359-366); pre-RoPE per-head RMSNorm
     (:880-900); RoPE with cos/sin [d/2, B, S_tkg] contiguous halves (:905);
+    optional post-RoPE per-head RMSNorm with q_norm_post_w / k_norm_post_w [d]
+    and qk_post_eps (:906-910, 1093-1138; a None weight skips that norm);
     scores over the cache window [0, S_ctx - S_tkg) followed by the S_tkg
     active tokens, uint8-style 0/1 mask [S_ctx, B, nq, S_tkg]
     (attention_tkg.py:1019-1046, 1892-1893); optional sink logit per head in
@@ -541,6 +544,10 @@ def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
         s_ = torch.cat([sin, sin], 0).permute(1, 2, 0).float()
         q = q * c[:, :, None, :] + rotate_half(q) * s_[:, :, None, :]
         k = k * c + rotate_half(k) * s_
+    if q_norm_post_w is not None:
+        q = head_rmsnorm(q, q_norm_post_w.reshape(-1), qk_post_eps)
+    if k_norm_post_w is not None:
+        k = head_rmsnorm(k, k_norm_post_w.reshape(-1), qk_post_eps)
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d)
     S_ctx = attention_mask.shape[0]
     Kc = K_cache.reshape(K_cache.shape[0], -1, d) if K_cache.dim() == 4 else K_cache

@@ -595,6 +595,64 @@ def test_attention_block_tkg_multi_token_block_kv(mk, dev):
         assert max_abs_rel(Kn[int(upd[b, 0]):int(upd[b, 0]) + S], newk[b]) < TOL
 
 
+@pytest.mark.parametrize("B,S,P,nq,nkv,d,pre,wq,wk", [
+    (2, 1, 300, 8, 1, 128, True, True, True),
+    (2, 3, 40, 8, 2, 64, False, True, False),
+    (1, 1, 0, 4, 1, 64, False, False, False),
+])
+def test_attention_block_tkg_post_rope_norm(mk, dev, B, S, P, nq, nkv, d, pre, wq, wk):
+    """rmsnorm_QK_post_rope_* (attention_block_tkg.py:906-910): a per-head RMSNorm
+    of Q and K after RoPE (a missing weight is ones), against the oracle per kv
+    head; the cache receives the post-normed K rows."""
+    from nki_moe_megakernel_amd.common_types import QuantizationType
+    print(f"post-RoPE norm attention: B={B} S={S} P={P} nkv={nkv} d={d}", flush=True)
+    H, S_max = 256, P + S + 8
+    g = torch.Generator().manual_seed(B * 5 + S * 11 + P)
+    X = bf(torch.randn(B, S, H, generator=g))
+    W = bf(0.05 * torch.randn(H, d * (nq + 2 * nkv), generator=g))
+    Wo = bf(0.05 * torch.randn(nq * d, H, generator=g))
+    qn = bf(1 + 0.1 * torch.randn(1, d, generator=g)) if pre else None
+    kn = bf(1 + 0.1 * torch.randn(1, d, generator=g)) if pre else None
+    qp = bf(1 + 0.3 * torch.randn(1, d, generator=g)) if wq else None
+    kp = bf(1 + 0.3 * torch.randn(1, d, generator=g)) if wk else None
+    kshape = (B, S_max, d) if nkv == 1 else (B, nkv, S_max, d)
+    Kc = bf(torch.randn(*kshape, generator=g))
+    Vc = bf(torch.randn(*kshape, generator=g))
+    cos_r, sin_r = _rope_rows(B, S, P, d)
+    mask = _multi_mask(g, P, B, nq, S)
+    upd = torch.full((B, 1), P, dtype=torch.int64)
+    Kg, Vg = Kc.to(dev), Vc.to(dev)
+    on = lambda t: t.to(dev) if t is not None else None
+    out, _, _ = mk.attention_block_tkg(
+        X.to(dev), None, False, 1e-6, None, W.to(dev), None,
+        QuantizationType.NONE, None, None, pre, 1e-6, on(qn), on(kn), cos_r.to(dev), sin_r.to(dev),
+        True, True, 1e-5, on(qp), on(kp), False, None, Kg, Vg, mask.to(dev), None, True,
+        upd.to(dev), Wo.to(dev), None, QuantizationType.NONE, None, None, False, False)
+    gqa = nq // nkv
+    Kr4 = Kc.float().reshape(B, nkv, S_max, d) if nkv > 1 else Kc.float()[:, None]
+    Vr4 = Vc.float().reshape(B, nkv, S_max, d) if nkv > 1 else Vc.float()[:, None]
+    one = torch.ones(d)
+    attn = torch.zeros(B * S, nq * d)
+    newk = torch.zeros(B, nkv, S, d)
+    for h in range(nkv):
+        cols = torch.cat([torch.arange(h * gqa * d, (h + 1) * gqa * d),
+                          nq * d + h * d + torch.arange(d),
+                          (nq + nkv) * d + h * d + torch.arange(d)])
+        Kh, Vh = Kr4[:, h].clone(), Vr4[:, h].clone()
+        o, Kh2, _ = ref.attention_block_tkg(
+            X.float(), W.float()[:, cols], None, 1e-6, None,
+            qn.float() if pre else None, kn.float() if pre else None, 1e-6, cos_r, sin_r,
+            Kh, Vh, mask[:, :, h * gqa:(h + 1) * gqa].float(), None, True, torch.full((B, 1), P),
+            None, None, q_norm_post_w=qp.float() if wq else one,
+            k_norm_post_w=kp.float() if wk else one, qk_post_eps=1e-5)
+        attn[:, h * gqa * d:(h + 1) * gqa * d] = o
+        newk[:, h] = Kh2[:, P:P + S]
+    assert max_abs_rel(out, attn @ Wo.float()) < TOL
+    Kn = Kg.cpu().reshape(B, nkv, S_max, d) if nkv > 1 else Kg.cpu()[:, None]
+    for b in range(B):
+        assert max_abs_rel(Kn[b, :, P:P + S], newk[b]) < TOL
+
+
 # ---------------------------------------------------------------- Qwen layer / step
 def _model_from_hf(mk, hf, cfg, B, dev):
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q

@@ -340,6 +340,60 @@ def test_multi_token_window_equals_token_by_token():
     assert (K1 != Kc).any(-1).nonzero()[:, 1].unique().tolist() == list(range(P, P + S))
 
 
+def test_post_rope_norm_reduces_to_pre_rope_norm():
+    """Post-RoPE per-head RMSNorm (attention_block_tkg.py:906-910) against the
+    pre-RoPE norm pinned above: the contiguous-halves rotation keeps the rms, so
+    with the identity rotation (cos 1, sin 0) the post norm with weights w is
+    the pre norm with w, and with the quarter turn (cos 0, sin 1: x -> [-x2, x1])
+    it is the pre norm with w's halves swapped -- a norm applied before RoPE, or
+    a weight index off by the half, fails the second.  With eps = 0 the post norm
+    also makes the block blind to the scale of the Q and K projections."""
+    g = torch.Generator().manual_seed(23)
+    B, S, H, nq, d, P, S_max = 2, 2, 48, 4, 16, 5, 10
+    X = torch.randn(B, S, H, generator=g)
+    W = 0.3 * torch.randn(H, d * (nq + 2), generator=g)
+    w_q = 1 + 0.5 * torch.randn(d, generator=g)
+    w_k = 1 + 0.5 * torch.randn(d, generator=g)
+    Kc = torch.randn(B, S_max, d, generator=g)
+    Vc = torch.randn(B, S_max, d, generator=g)
+    prior = (torch.rand(P, B, nq, S, generator=g) > 0.3).float()
+    causal = (torch.arange(S)[:, None] <= torch.arange(S)[None, :]).float()
+    mask = torch.cat([prior, causal[:, None, None, :].expand(S, B, nq, S)], 0)
+    idx = torch.full((B, 1), P, dtype=torch.int64)
+    swap = lambda w: torch.cat([w[d // 2:], w[:d // 2]])
+
+    def run(Wm, cosv, sinv, pre=None, post=None, eps=1e-5):
+        c = torch.full((d // 2, B, S), float(cosv))
+        s_ = torch.full((d // 2, B, S), float(sinv))
+        K1, V1 = Kc.clone(), Vc.clone()
+        o, K2, _ = ref.attention_block_tkg(
+            X, Wm, None, None, None, pre[0] if pre else None, pre[1] if pre else None, eps, c, s_,
+            K1, V1, mask, None, True, idx, None, None,
+            q_norm_post_w=post[0] if post else None, k_norm_post_w=post[1] if post else None,
+            qk_post_eps=eps)
+        return o, K2[:, P:P + S]
+
+    o_post, k_post = run(W, 1, 0, post=(w_q, w_k))
+    o_pre, k_pre = run(W, 1, 0, pre=(w_q, w_k))
+    assert torch.allclose(o_post, o_pre, atol=1e-5) and torch.allclose(k_post, k_pre, atol=1e-5)
+    o_post, k_post = run(W, 0, 1, post=(w_q, w_k))
+    o_pre, k_pre = run(W, 0, 1, pre=(swap(w_q), swap(w_k)))
+    assert torch.allclose(o_post, o_pre, atol=1e-5) and torch.allclose(k_post, k_pre, atol=1e-5)
+    o_wrong, _ = run(W, 0, 1, pre=(w_q, w_k))
+    assert not torch.allclose(o_post, o_wrong, atol=1e-3)
+    # scale blindness (eps = 0): Q columns x3, K columns x0.25
+    cs = torch.ones(d * (nq + 2))
+    cs[:nq * d] = 3.0
+    cs[nq * d:(nq + 1) * d] = 0.25
+    c0, s0 = 0.6, 0.8
+    o1, _ = run(W, c0, s0, post=(w_q, w_k), eps=0.0)
+    o2, _ = run(W * cs, c0, s0, post=(w_q, w_k), eps=0.0)
+    assert torch.allclose(o1, o2, atol=1e-5)
+    n1, _ = run(W, c0, s0, eps=0.0)
+    n2, _ = run(W * cs, c0, s0, eps=0.0)
+    assert not torch.allclose(n1, n2, atol=1e-3)
+
+
 # ------------------------------------------------------------------ whole layer vs HF
 def _load_golden():
     from safetensors.torch import load_file
