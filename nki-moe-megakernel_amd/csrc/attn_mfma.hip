@@ -648,8 +648,10 @@ constexpr unsigned kJoinWeightDelay = 250;
 // combine flags, the B attention rows go to LDS (device-coherent loads), and
 // the MFMAs run (A = weight fragment, B = tokens: lane l holds token l%16, k
 // (l/16)*8 .. +8; D lane l holds rows 4*(l/16)+i of token l%16).  The wave
-// partials are added in wave order.
-MKD_DEV void oproj_block(const AttnArgs& a, const AttnJoinArgs& j, int rb, const unsigned* cfl, int ncf) {
+// partials are added in wave order.  With a router stage the rows are stored
+// device-coherent and *oflag is set.
+MKD_DEV void oproj_block(const AttnArgs& a, const AttnJoinArgs& j, int rb, const unsigned* cfl, int ncf,
+                         unsigned* oflag) {
   extern __shared__ u32x4_t xs[];            // [B][K / 8]
   __shared__ f32x4_t red[4][64];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -704,12 +706,187 @@ MKD_DEV void oproj_block(const AttnArgs& a, const AttnJoinArgs& j, int rb, const
   }
   red[w][lane] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   __syncthreads();
-  if (w != 0 || c >= a.B) return;
-  const f32x4_t v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
-  const int n0 = rb * 16 + (lane >> 4) * 4;
+  if (w == 0 && c < a.B) {
+    const f32x4_t v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+    const int n0 = rb * 16 + (lane >> 4) * 4;
+    float o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-    if (n0 + i < j.N) j.y[(long long)c * j.N + n0 + i] = v[i] + (j.bias ? bf2f(j.bias[n0 + i]) : 0.f);
+    for (int i = 0; i < 4; ++i) o[i] = v[i] + ((j.bias && n0 + i < j.N) ? bf2f(j.bias[n0 + i]) : 0.f);
+    if (j.rw) {   // read back by the router blocks (N % 16 == 0)
+      coh_st16(coh_rsrc(j.y), (int)(((long long)c * j.N + n0) * 4),
+               u32x4_t{__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3])});
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (n0 + i < j.N) j.y[(long long)c * j.N + n0 + i] = o[i];
+    }
+  }
+  if (j.rw) coh_publish(oflag);
+}
+
+// ---- router stage: the post-attention residual, norm and router logits ----
+constexpr int kJoinRouterF = 8;      // router weight fragments per wave
+constexpr int kJoinRouterMaxN = 3072;
+
+__host__ __device__ static inline int router_parts_of(int N) { return (N / 32 + kJoinRouterF - 1) / kJoinRouterF; }
+int attn_join_router_parts(int N) { return router_parts_of(N); }
+
+static int router_join_blocks(int E, int N) { return ((E / 16) * router_parts_of(N) + 3) / 4; }
+
+bool attn_join_router_supported(int B, int E, int N) {
+  return B >= 1 && B <= kJoinMaxB && E >= 16 && E % 16 == 0 && E <= 512 && N % 32 == 0 &&
+         N <= kJoinRouterMaxN && router_parts_of(N) <= 16;
+}
+
+// Router block rbk (after the projection blocks): wave gw = 4 rbk + w computes
+// experts 16 erb .. +16 over the K part kp (kJoinRouterF fragments of 32) of
+// the router GEMM, as router_norm_gemm_kernel does (router_topk.py:69-1207 with
+// the Qwen fused post-attention norm, moe_fused_nki.py:159-276): the weights,
+// the residual rows and gamma are loaded first; one wave waits for the nof
+// projection flags; the block then reads the projection rows device-coherent,
+// forms r = bf16(x + bf16(y)) and each token's sum of squares (in a fixed
+// order: thread, wave, then waves 0..3), and writes y = (r * gamma) * rinv once
+// to LDS in B-operand order (bf16 hi + lo for an fp32 router input, one 16-byte
+// piece per thread and row chunk), from where every wave reads its operands.
+// Block 0 also writes r and bf16(y), the residual and expert input of the rest
+// of the layer.
+// RC = the row chunks (16 bytes) per thread, ceil(B N / 8 / 256).
+template <int RC>
+MKD_DEV void router_block(const AttnArgs& a, const AttnJoinArgs& j, int rbk, const unsigned* ofl, int nof) {
+  extern __shared__ u32x4_t xs[];             // [B][N / 8] y hi, [B][N / 8] y lo, [N / 8] gamma
+  __shared__ float ssw[4][kJoinMaxB];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int N = j.N, KB = N / 32, nkp = router_parts_of(N);
+  const int nwv = (j.E / 16) * nkp;
+  const int gw = min(rbk * 4 + w, nwv - 1);   // a wave past the last one repeats it, storing nothing
+  const bool wlive = rbk * 4 + w < nwv;
+  const int erb = gw / nkp, kp = gw % nkp;
+  const int kb0 = kp * kJoinRouterF, nf = min(kJoinRouterF, KB - kb0);
+  const int B = a.B, per_row = N / 8, nch = B * per_row;
+  constexpr int kRC = RC;
+  constexpr int kGC = kJoinRouterMaxN / 8 / 256 + 1;           // gamma chunks per thread at most
+  u32x4_t xr[kRC], gr[kGC];
+#pragma unroll
+  for (int q = 0; q < kRC; ++q) {
+    const int i = min((int)threadIdx.x + 256 * q, nch - 1);
+    xr[q] = ld16(j.rx + (long long)i * 8);
+  }
+#pragma unroll
+  for (int q = 0; q < kGC; ++q) gr[q] = ld16(j.rgamma + min((int)threadIdx.x + 256 * q, per_row - 1) * 8);
+  {
+    const unsigned long long t0 = wall_clock64();
+    while (wall_clock64() - t0 < kJoinWeightDelay) __builtin_amdgcn_s_sleep(2);
+  }
+  const uint16_t* wrow = j.rw + ((long long)erb * KB + kb0) * 512 + lane * 8;
+  u32x4_t wf[kJoinRouterF];
+#pragma unroll
+  for (int u = 0; u < kJoinRouterF; ++u)
+    wf[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + min(u, nf - 1) * 512));
+  if (w == 0) coh_wait_all(ofl, nof, j.err);
+  __syncthreads();
+
+  // r = bf16(x + bf16(y)) (kept in registers), per-token sums of squares
+  const __amdgpu_buffer_rsrc_t yr = coh_rsrc(j.y);
+  u32x4_t y0[kRC], y1[kRC];
+#pragma unroll
+  for (int q = 0; q < kRC; ++q) {
+    const int i = min((int)threadIdx.x + 256 * q, nch - 1);
+    y0[q] = coh_ld16(yr, i * 32);
+    y1[q] = coh_ld16(yr, i * 32 + 16);
+  }
+  u32x4_t* yhi = xs;
+  u32x4_t* ylo = xs + nch;
+  u32x4_t* gs = xs + 2 * nch;
+#pragma unroll
+  for (int q = 0; q < kGC; ++q) {
+    const int i = (int)threadIdx.x + 256 * q;
+    if (i < per_row) gs[i] = gr[q];
+  }
+  float ss[kJoinMaxB] = {0.f, 0.f, 0.f, 0.f};
+  u32x4_t rreg[kRC];
+#pragma unroll
+  for (int q = 0; q < kRC; ++q) {
+    const int i = (int)threadIdx.x + 256 * q;
+    const int t = i / per_row;
+    const float yv[8] = {__uint_as_float(y0[q][0]), __uint_as_float(y0[q][1]), __uint_as_float(y0[q][2]),
+                         __uint_as_float(y0[q][3]), __uint_as_float(y1[q][0]), __uint_as_float(y1[q][1]),
+                         __uint_as_float(y1[q][2]), __uint_as_float(y1[q][3])};
+    float s = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float r0 = rbf(bf_lo(xr[q][e]) + rbf(yv[2 * e]));
+      const float r1 = rbf(bf_hi(xr[q][e]) + rbf(yv[2 * e + 1]));
+      s += r0 * r0;
+      s += r1 * r1;
+      rreg[q][e] = pack2bf(r0, r1);
+    }
+#pragma unroll
+    for (int tt = 0; tt < kJoinMaxB; ++tt)
+      if (tt == t && i < nch) ss[tt] += s;
+  }
+#pragma unroll
+  for (int tt = 0; tt < kJoinMaxB; ++tt) {
+    const float v = wave_sum(ss[tt]);
+    if (lane == 0) ssw[w][tt] = v;
+  }
+  __syncthreads();
+  float rinv[kJoinMaxB];
+#pragma unroll
+  for (int tt = 0; tt < kJoinMaxB; ++tt)
+    rinv[tt] = 1.0f / sqrtf((((ssw[0][tt] + ssw[1][tt]) + ssw[2][tt]) + ssw[3][tt]) * j.rinv_h + j.reps);
+
+  // y = (r * gamma) * rinv of the thread's chunks -> LDS (hi, lo); block 0 also
+  // writes r and bf16(y)
+#pragma unroll
+  for (int q = 0; q < kRC; ++q) {
+    const int i = (int)threadIdx.x + 256 * q;
+    if (i >= nch) continue;
+    const int t = i / per_row;
+    float rv = rinv[0];
+#pragma unroll
+    for (int tt = 1; tt < kJoinMaxB; ++tt)
+      if (tt == t) rv = rinv[tt];
+    const u32x4_t gp = gs[i - t * per_row];
+    u32x4_t hi, lo;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v0 = (bf_lo(rreg[q][e]) * bf_lo(gp[e])) * rv;
+      float v1 = (bf_hi(rreg[q][e]) * bf_hi(gp[e])) * rv;
+      if (!j.rx_f32) { v0 = rbf(v0); v1 = rbf(v1); }
+      const uint32_t h0 = f2bf(v0), h1 = f2bf(v1);
+      hi[e] = h0 | (h1 << 16);
+      lo[e] = f2bf(v0 - bf2f(h0)) | (f2bf(v1 - bf2f(h1)) << 16);
+    }
+    yhi[i] = hi;
+    ylo[i] = lo;
+    if (rbk == 0) {
+      st16(j.rresid + (long long)i * 8, rreg[q]);
+      st16(j.rhnorm + (long long)i * 8, hi);
+    }
+  }
+  __syncthreads();
+
+  // MFMAs: lane l = token l%16, k (l/16)*8 .. +8 of each fragment (masked, not branched)
+  const int c = lane & 15;
+  const bool tok = c < B;
+  const int o0 = (tok ? c : 0) * per_row + (lane >> 4);
+  f32x4_t acc[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) acc[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int u = 0; u < kJoinRouterF; ++u) {
+    const int o = o0 + (kb0 + min(u, nf - 1)) * 4;
+    const uint32_t m = (tok && u < nf) ? 0xffffffffu : 0u;
+    const u32x4_t h = yhi[o], l = ylo[o];
+    acc[u & 1] = mfma16x16x32(wf[u], u32x4_t{h[0] & m, h[1] & m, h[2] & m, h[3] & m}, acc[u & 1]);
+    if (j.rx_f32)
+      acc[2 + (u & 1)] = mfma16x16x32(wf[u], u32x4_t{l[0] & m, l[1] & m, l[2] & m, l[3] & m}, acc[2 + (u & 1)]);
+  }
+  if (wlive && tok) {
+    const f32x4_t v = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+    float* pp = j.rparts + (long long)kp * B * j.E + (long long)c * j.E + erb * 16 + (lane >> 4) * 4;
+    *reinterpret_cast<f32x4_t*>(pp) = v;
+  }
 }
 
 template <int D, int GQA, int TPW>
@@ -723,12 +900,26 @@ __global__ void __launch_bounds__(256) attn_joined_kernel(AttnArgs a, AttnJoinAr
     const int hb = bid - na, h = hb % a.nq, b = hb / a.nq;
     attn_combine_block<D, 16, true>(a, h, b, j.flags + ((long long)b * a.nkv + h / GQA) * a.n_chunks,
                                     a.n_chunks, j.flags + bid, j.err);
+  } else if (bid < na + nc + (j.N + 15) / 16) {
+    const int rb = bid - na - nc;
+    oproj_block(a, j, rb, j.flags + na, nc, j.flags + na + nc + rb);
   } else {
-    oproj_block(a, j, bid - na - nc, j.flags + na, nc);
+    const int rbk = bid - na - nc - (j.N + 15) / 16, no = (j.N + 15) / 16;
+    switch ((a.B * j.N / 8 + 255) / 256) {   // row chunks per thread
+      case 1: router_block<1>(a, j, rbk, j.flags + na + nc, no); break;
+      case 2: router_block<2>(a, j, rbk, j.flags + na + nc, no); break;
+      case 3: router_block<3>(a, j, rbk, j.flags + na + nc, no); break;
+      case 4: router_block<4>(a, j, rbk, j.flags + na + nc, no); break;
+      case 5: router_block<5>(a, j, rbk, j.flags + na + nc, no); break;
+      default: router_block<6>(a, j, rbk, j.flags + na + nc, no); break;
+    }
   }
 }
 
-int attn_join_flag_words(int B, int nq, int nkv, int n_chunks) { return n_chunks * nkv * B + nq * B; }
+// chunk flags, combine flags, projection flags (router stage)
+int attn_join_flag_words(int B, int nq, int nkv, int n_chunks, int N) {
+  return n_chunks * nkv * B + nq * B + (N + 15) / 16;
+}
 
 bool attn_join_supported(const AttnArgs& a, int N) {
   const int gqa = a.nkv > 0 ? a.nq / a.nkv : 0;
@@ -741,14 +932,18 @@ bool attn_join_supported(const AttnArgs& a, int N) {
 
 template <int D, int GQA>
 static hipError_t launch_join(const AttnArgs& a, const AttnJoinArgs& j, int rope_mode, hipStream_t s) {
-  const int blocks = a.n_chunks * a.nkv * a.B + a.nq * a.B + (j.N + 15) / 16;
-  const size_t lds = (size_t)a.B * a.nq * a.d * 2;
+  const int blocks = a.n_chunks * a.nkv * a.B + a.nq * a.B + (j.N + 15) / 16 +
+                     (j.rw ? router_join_blocks(j.E, j.N) : 0);
+  const size_t lds = std::max((size_t)a.B * a.nq * a.d * 2, j.rw ? (size_t)(2 * a.B + 1) * j.N * 2 : 0);
   if (a.chunk == 64) return timed_launch(attn_joined_kernel<D, GQA, 1>, dim3(blocks), dim3(256), lds, s, a, j, rope_mode);
   return timed_launch(attn_joined_kernel<D, GQA, 2>, dim3(blocks), dim3(256), lds, s, a, j, rope_mode);
 }
 
 hipError_t attn_join_launch(const AttnArgs& a, const AttnJoinArgs& j, int rope_mode, hipStream_t s) {
   if (!attn_join_supported(a, j.N) || !j.w_out || !j.y || !j.flags || !j.err) return hipErrorInvalidValue;
+  if (j.rw && (!attn_join_router_supported(a.B, j.E, j.N) || j.N % 16 || !j.rx || !j.rgamma ||
+               !j.rparts || !j.rresid || !j.rhnorm))
+    return hipErrorInvalidValue;
   const int gqa = a.nq / a.nkv;
   if (a.d == 128) {
     switch (gqa) {

@@ -862,10 +862,14 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     j.y = o_parts;
     j.N = p->H_out;
     const int ps = prof_begin(MKD_KCLASS_ATTN, s);
-    MKD_TRY(attn_join_launch(a, j, rope_mode, s), "attention + combine + o_proj");
+    MKD_TRY(attn_join_launch(a, j, rope_mode, s), j.rw ? "attention + combine + o_proj + router"
+                                                        : "attention + combine + o_proj");
     prof_end(ps, s);
     return MKD_OK;
   }
+  // the caller left its router to the joined launch
+  MKD_REQUIRE(!(join && join->rw), MKD_ERR_UNSUPPORTED,
+              "attention: the joined launch with its router stage does not fit this layer");
   {  // q/k norm + RoPE and split-K attention in one launch
     const int ps = prof_begin(MKD_KCLASS_ATTN, s);
     MKD_TRY(attn_decode_launch(a, rope_mode, s), "attention");
@@ -963,6 +967,8 @@ int mkd_attention_block_tkg(const mkd_attention_args* p, void* workspace, size_t
 // decode path is set to it, otherwise every layer runs the multi-kernel sequence.
 static int g_decode_path = 0;   // 0 multi-kernel layers, 1 persistent layer kernel where eligible
 static int g_inlaunch_sync = 1;  // 1: stages joined into one launch (in-launch waits) where eligible
+// the router stage inside the joined attention launch where that launch runs
+static constexpr bool g_router_in_attention = true;
 
 static int lk_device_cus() {
   static int cus = -1;
@@ -1109,7 +1115,7 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.lk = carve_lk(c, m, B);
   w.flag_words = moe_fused_supported(B, m->K, m->E, m->H, m->I) ? moe_fused_flag_words(B, m->K, m->E, m->I) : 0;
   // the joined attention launch's flags (chunk and combine blocks)
-  w.attn_words = B <= kJoinMaxB ? attn_join_flag_words(B, m->nq, m->nkv, w.attn.n_chunks) : 0;
+  w.attn_words = B <= kJoinMaxB ? attn_join_flag_words(B, m->nq, m->nkv, w.attn.n_chunks, m->H) : 0;
   w.layer_words = w.flag_words + w.attn_words;
   w.sync_words = w.layer_words ? 64 + m->num_layers * w.layer_words : 0;
   w.sync = w.sync_words ? c.take<unsigned>(w.sync_words) : nullptr;
@@ -1201,6 +1207,15 @@ static bool joined_attention_planned(const mkd_qwen3_model* m, int B) {
   a.n_chunks = (m->S_max + 1 + a.chunk - 1) / a.chunk;
   if ((long long)a.n_chunks * m->nkv * B > 1024) return false;   // the large-grid prep launch
   return attn_join_supported(a, m->H);
+}
+
+// ... and with it the router stage (residual add, post-attention norm, router
+// GEMM) as that launch's last blocks, where the router's shapes fit both.
+static bool router_in_attention_planned(const mkd_qwen3_model* m, int B, int l) {
+  if (!g_router_in_attention || !joined_attention_planned(m, B) || !router_fused_supported(B, m->E, m->H) ||
+      !attn_join_router_supported(B, m->E, m->H) || m->H % 16)
+    return false;
+  return l < 0 || !m->layer_s_max || m->layer_s_max[l] == m->S_max;
 }
 
 static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const int* position_ids,
@@ -1334,6 +1349,18 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
     AttnJoinArgs ja = {};
     ja.flags = lsync ? lsync + w.flag_words : nullptr;
     ja.err = w.sync;
+    // the residual add, post-attention norm and router GEMM as the joined
+    // attention launch's last blocks (replacing the router launch)
+    const bool router_join = join_attn && lsync && router_in_attention_planned(m, B, l);
+    if (router_join) {
+      ja.rx = static_cast<const uint16_t*>(x);
+      ja.rgamma = static_cast<const uint16_t*>(m->ln_post[l]);
+      ja.rw = static_cast<const uint16_t*>(m->router[l]);
+      ja.rparts = w.logits;
+      ja.rresid = w.r; ja.rhnorm = w.nbf;
+      ja.reps = m->eps; ja.rinv_h = 1.0f / (float)ha;
+      ja.E = m->E; ja.rx_f32 = oss ? 0 : 1;
+    }
     if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s, w.oparts, o_kgrid,
                                 fuse_qn ? &qn : nullptr, prefill && !wl,
                                 join_attn && lsync ? &ja : nullptr))
@@ -1357,7 +1384,15 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
     ra.pair_token = w.moe.pair_token; ra.pair_slot = w.moe.pair_slot;
     RouterArgs sel;
     bool defer_sel = false;
-    if (router_fused_supported(B, m->E, m->H)) {
+    if (router_join) {
+      // the partial logits came from the attention launch
+      sel = ra;
+      sel.parts = w.logits;
+      sel.nparts = attn_join_router_parts(m->H);
+      sel.part_stride = (long long)B * m->E;
+      defer_sel = defer_ok;
+      if (!defer_sel) MKD_TRY(router_select_launch(sel, s), "router select");
+    } else if (router_fused_supported(B, m->E, m->H)) {
       // the router top-k inside the gate/up blocks: each block pays the selection
       // before its weight loads, so only when the whole grid is resident at once
       // (two blocks per CU); measured at 4 tokens (1536 blocks) the select launch

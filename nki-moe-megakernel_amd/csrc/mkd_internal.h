@@ -296,9 +296,25 @@ struct AttnJoinArgs {
   int N;
   unsigned* flags;            // attn_join_flag_words() words, zero at launch
   unsigned* err;              // set when a wait ran out
+  // Router stage (rw non-null): blocks after the projection blocks wait for
+  // every projection block (whose rows are then stored device-coherent and
+  // flagged), form r = bf16(x + bf16(y)), the post-attention RMSNorm of r and
+  // the router logits' K-split partials -- router_norm_gemm_kernel's work
+  // without its launch.
+  const uint16_t* rx;         // [B, N] bf16 residual stream (the layer input)
+  const uint16_t* rgamma;     // [N] post-attention norm weight
+  const uint16_t* rw;         // router weights [E, N], frag-packed
+  float* rparts;              // [attn_join_router_parts(N)][B][E] partial logits
+  uint16_t* rresid;           // [B, N] r
+  uint16_t* rhnorm;           // [B, N] bf16 normalised rows (the expert input)
+  float reps, rinv_h;         // norm epsilon, 1 / hidden size it averages over
+  int E;
+  int rx_f32;                 // 1: router operand fp32 (bf16 hi + lo), 0: bf16
 };
-int attn_join_flag_words(int B, int nq, int nkv, int n_chunks);
+int attn_join_flag_words(int B, int nq, int nkv, int n_chunks, int N);
 bool attn_join_supported(const AttnArgs& a, int N);
+int attn_join_router_parts(int N);
+bool attn_join_router_supported(int B, int E, int N);
 hipError_t attn_join_launch(const AttnArgs& a, const AttnJoinArgs& j, int rope_mode, hipStream_t s);
 
 // moe.hip
