@@ -462,11 +462,22 @@ int mkd_qwen3_write_layer_table(const mkd_qwen3_model* m, void* table, size_t ta
  * (one persistent launch for all layers) or MKD_PLAN_JOINED_EXPERTS (the
  * multi-kernel layers with gate/up and down in one launch), else 0; plus
  * MKD_PLAN_JOINED_ATTENTION when the multi-kernel layers run attention,
- * combine and output projection as one launch. */
+ * combine and output projection as one launch, and MKD_PLAN_ROUTER_IN_ATTENTION
+ * when (all layers of m having one cache length) the router stage joins it. */
 #define MKD_PLAN_PERSISTENT 1
 #define MKD_PLAN_JOINED_EXPERTS 2
 #define MKD_PLAN_JOINED_ATTENTION 4
+/* ... and the residual add, post-attention norm and router GEMM run as that
+ * launch's last blocks (no router launch of their own). */
+#define MKD_PLAN_ROUTER_IN_ATTENTION 8
 int mkd_qwen3_decode_plan(const mkd_qwen3_model* m, int B, int* plan);
+/* Self-check of the device's fp32 -> bf16 rounding, which every bf16 result of
+ * the library goes through (no counterpart in the reference): converts all
+ * 2^32 fp32 bit patterns with the library's conversion and with the integer
+ * round-to-nearest-even form, and adds the number of non-NaN patterns that
+ * differ (and of NaNs that do not stay NaN) to the device word *mismatches
+ * (8 bytes, zeroed by the caller).  Asynchronous on `stream`. */
+int mkd_selfcheck_bf16_round(unsigned long long* mismatches, void* stream);
 int mkd_qwen3_layer_kernel_status(const mkd_qwen3_model* m, int B, const void* workspace,
                                   size_t workspace_bytes, int* used, int* barrier_timeout);
 

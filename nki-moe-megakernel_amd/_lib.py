@@ -127,6 +127,7 @@ _SIGS = {
     "mkd_qwen3_layer_table_bytes": (sz, [C.POINTER(Qwen3Model)]),
     "mkd_qwen3_write_layer_table": (i32, [C.POINTER(Qwen3Model), vp, sz]),
     "mkd_qwen3_decode_plan": (i32, [C.POINTER(Qwen3Model), i32, C.POINTER(i32)]),
+    "mkd_selfcheck_bf16_round": (i32, [vp, vp]),
     "mkd_qwen3_layer_kernel_status": (i32, [C.POINTER(Qwen3Model), i32, vp, sz, C.POINTER(i32),
                                             C.POINTER(i32)]),
 }

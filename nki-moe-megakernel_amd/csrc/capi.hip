@@ -1621,6 +1621,31 @@ int mkd_qwen3_write_layer_table(const mkd_qwen3_model* m, void* table, size_t ta
   return MKD_OK;
 }
 
+__global__ void bf16_round_check_kernel(unsigned base_hi, unsigned long long* bad) {
+  const uint32_t u = (base_hi << 28) + blockIdx.x * blockDim.x + threadIdx.x;
+  const float f = __uint_as_float(u);
+  const uint32_t h = f2bf(f);
+  bool ok;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    ok = (h & 0x7f80u) == 0x7f80u && (h & 0x7fu) != 0u;   // a NaN stays a NaN
+  } else {
+    const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+    ok = h == r && __float_as_uint(rbf(f)) == (r << 16) &&
+         (pack2bf(f, -f) & 0xffffu) == r && (pack2bf(-f, f) >> 16) == r;
+  }
+  const unsigned long long m = __ballot(!ok);   // the grid covers its range exactly
+  if ((threadIdx.x & 63) == 0 && m) atomicAdd(bad, (unsigned long long)__popcll(m));
+}
+
+int mkd_selfcheck_bf16_round(unsigned long long* mismatches, void* stream) {
+  MKD_REQUIRE(mismatches, MKD_ERR_NULL, "selfcheck_bf16_round: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  for (unsigned hi = 0; hi < 16; ++hi)   // 2^28 patterns per launch
+    hipLaunchKernelGGL(bf16_round_check_kernel, dim3(1u << 20), dim3(256), 0, s, hi, mismatches);
+  MKD_TRY(hipGetLastError(), "selfcheck_bf16_round");
+  return MKD_OK;
+}
+
 int mkd_set_decode_path(int mode) {
   MKD_REQUIRE(mode >= 0 && mode <= 2, MKD_ERR_INVALID, "set_decode_path: mode %d must be 0, 1 or 2", mode);
   g_decode_path = mode == 1 ? 1 : 0;
@@ -1637,6 +1662,9 @@ int mkd_qwen3_decode_plan(const mkd_qwen3_model* m, int B, int* plan) {
   } else {
     if (joined_experts_planned(m, B)) p |= MKD_PLAN_JOINED_EXPERTS;
     if (joined_attention_planned(m, B)) p |= MKD_PLAN_JOINED_ATTENTION;
+    if (router_in_attention_planned(m, B, -1) && (!m->layer_s_max || m->num_layers < 1 ||
+                                                  m->layer_s_max[0] == m->S_max))
+      p |= MKD_PLAN_ROUTER_IN_ATTENTION;
   }
   *plan = p;
   return MKD_OK;

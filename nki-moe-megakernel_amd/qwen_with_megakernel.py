@@ -262,6 +262,14 @@ class _LayerStack:
                 "qwen3_decode_plan")
         return bool(plan.value & 4)
 
+    def router_in_attention(self, batch: Optional[int] = None) -> bool:
+        """Whether the joined attention launch also runs the residual add, the
+        post-attention norm and the router GEMM (no router launch) for this batch."""
+        plan = C.c_int32(0)
+        L.check(L.load().mkd_qwen3_decode_plan(self._model, batch or self.batch, C.byref(plan)),
+                "qwen3_decode_plan")
+        return bool(plan.value & 8)
+
     def layer_kernel_status(self, batch: Optional[int] = None):
         """(persistent layer kernel planned for this batch, an in-launch wait -- a grid
         barrier or the joined expert launch's flags -- timed out).  Synchronises the device."""

@@ -1,7 +1,8 @@
-"""The joined launches of the few-token decode step: attention, chunk combine
-and output projection in one kernel (the combine blocks wait inside the launch
-for their kv group's chunk blocks, the projection blocks for every combine
-block), and the expert launch (router top-k, gate/up and down in one kernel
+"""The joined launches of the few-token decode step: attention, chunk combine,
+output projection and router GEMM in one kernel (the combine blocks wait inside
+the launch for their kv group's chunk blocks, the projection blocks for every
+combine block, the router blocks -- residual add, post-attention norm, router
+logits -- for every projection block), and the expert launch (router top-k, gate/up and down in one kernel
 whose down blocks wait for their expert's gate/up blocks) with the one-token
 router selection inside it.
 
@@ -78,10 +79,12 @@ def test_joined_launches_vs_separate_and_oracle(mk, dev, restore_path, B, S):
     Q = restore_path
     print(f"joined launches: B={B} S={S}", flush=True)
     cfg, hfs, pos, x, kcs, vcs, model = _setup(dev, 3, B, S, 17 + B)
+    assert model.joined_attention(B) and model.router_in_attention(B)
     y_f, k_f, log_f = _run(model, x, kcs, vcs, pos, dev)
     y_f2, _, _ = _run(model, x, kcs, vcs, pos, dev)
     assert torch.equal(y_f, y_f2)                     # deterministic call to call
     Q.set_decode_path("separate_launches")
+    assert not model.router_in_attention(B)
     y_s, k_s, log_s = _run(model, x, kcs, vcs, pos, dev)
     e = max_abs_rel(y_f, y_s)
     print(f"joined vs separate launches, 3 layers: {e:.2e}", flush=True)

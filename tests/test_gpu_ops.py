@@ -326,6 +326,18 @@ def test_moe_tkg_rejects_large_T(mk, dev):
                    torch.zeros(4, 2, dtype=torch.int32, device=dev), True)
 
 
+def test_bf16_rounding_selfcheck(mk, dev):
+    """Every bf16 the library writes goes through the device's fp32 -> bf16
+    conversion (gfx950 v_cvt_pk_bf16_f32): all 2^32 fp32 patterns against the
+    integer round-to-nearest-even form torch's cast uses, NaN staying NaN."""
+    L = _lib(mk)
+    lib = L.load()
+    cnt = torch.zeros(1, dtype=torch.int64, device=dev)
+    L.check(lib.mkd_selfcheck_bf16_round(cnt.data_ptr(), L.stream_ptr(dev)), "selfcheck_bf16_round")
+    torch.cuda.synchronize()
+    assert int(cnt.item()) == 0
+
+
 # ---------------------------------------------------------------- attention_block_tkg
 @pytest.mark.parametrize("B,H,nq,nkv,d,S_ctx,S_max,qknorm,sink,norm", [
     (1, 2048, 8, 1, 128, 512, 640, True, False, True),
