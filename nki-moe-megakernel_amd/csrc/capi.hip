@@ -970,19 +970,7 @@ static int g_inlaunch_sync = 1;  // 1: stages joined into one launch (in-launch 
 // the router stage inside the joined attention launch where that launch runs
 static constexpr bool g_router_in_attention = true;
 
-static int lk_device_cus() {
-  static int cus = -1;
-  if (cus < 0) {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-      (void)hipGetLastError();
-      n = 0;
-    }
-    cus = n;
-  }
-  return cus;
-}
+static int lk_device_cus() { return device_cus(); }
 
 struct LkPlan {
   bool on = false;

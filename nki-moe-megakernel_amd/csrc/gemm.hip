@@ -300,13 +300,15 @@ __global__ void __launch_bounds__(1024) gemm_frag_sel_kernel(GemmArgs a, RouterA
 // measured at bs = 1 (Qwen3-30B-A3B shape): 25.5 us per launch against 27.5 us
 // with all 640 blocks resident at 6 waves per SIMD (80 VGPRs); 2, 3, 4 and 5
 // waves per SIMD are within 0.3 us of each other.
-template <int PER, int NFD>
+// DRB: row blocks per down wave (1: 64 output rows per down block, 2: 128), chosen
+// so that the whole grid is resident at once where it can be.
+template <int PER, int NFD, int DRB>
 __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) moe_fused_kernel(MoeFusedArgs f) {
   __shared__ int s_ng;
   __shared__ int s_gexp[kSelMaxPairs], s_gcnt[kSelMaxPairs], s_goff[kSelMaxPairs];
   __shared__ int s_ptok[kSelMaxPairs], s_pslot[kSelMaxPairs];
   __shared__ float s_w[kSelMaxPairs];
-  __shared__ f32x4_t s_red[4][64];
+  __shared__ f32x4_t s_red[DRB][4][64];
   __shared__ u32x4_t s_h[kFusedMaxRows][NFD * 8];   // h rows of a down block's group
   const int bid = blockIdx.x;
   const bool lead = bid == 0;
@@ -356,14 +358,18 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   if (g >= s_ng) return;
   const int ex = s_gexp[g], count = s_gcnt[g], base = s_goff[g];
   const int KB = d.K / 32;
-  const int rbk = qd * 4 + (wave & 3);       // 16-row block of the output
+  const int rbk = qd * 4 * DRB + (wave & 3); // 16-row blocks rbk + 4 i of the output
   const int kh = wave >> 2;                  // K half
   const int kb0 = kh * NFD;
-  const uint16_t* wrow = d.w + (long long)ex * d.w_group_stride + ((long long)rbk * KB + kb0) * 512 + lane * 8;
-  u32x4_t wf[NFD];
+  u32x4_t wf[DRB][NFD];
 #pragma unroll
-  for (int u = 0; u < NFD; ++u)
-    wf[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + u * 512));
+  for (int i = 0; i < DRB; ++i) {
+    const uint16_t* wrow =
+        d.w + (long long)ex * d.w_group_stride + ((long long)(rbk + 4 * i) * KB + kb0) * 512 + lane * 8;
+#pragma unroll
+    for (int u = 0; u < NFD; ++u)
+      wf[i][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + u * 512));
+  }
   const int c = lane & 15;
   const int prow = c < count ? s_pslot[base + c] : -1;   // h row and output row of the column
   if (wave == 0) coh_wait_all(f.flags + g * f.n_gu, f.n_gu, f.err);
@@ -380,8 +386,10 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
     }
   }
   __syncthreads();
-  // B operands four at a time (the weights already hold NFD * 4 registers)
-  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  // B operands four at a time (the weights already hold DRB * NFD * 4 registers)
+  f32x4_t acc[DRB];
+#pragma unroll
+  for (int i = 0; i < DRB; ++i) acc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int u0 = 0; u0 < NFD; u0 += 4) {
     u32x4_t xv[4];
@@ -389,24 +397,32 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
     for (int j = 0; j < 4; ++j)
       xv[j] = c < count ? s_h[c][(kb0 + u0 + j) * 4 + (lane >> 4)] : u32x4_t{0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int j = 0; j < 4; ++j) acc = mfma16x16x32(wf[u0 + j], xv[j], acc);
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < DRB; ++i) acc[i] = mfma16x16x32(wf[i][u0 + j], xv[j], acc[i]);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (kh == 1) s_red[wave & 3][lane] = acc;
+  if (kh == 1) {
+#pragma unroll
+    for (int i = 0; i < DRB; ++i) s_red[i][wave & 3][lane] = acc[i];
+  }
   __syncthreads();
   if (kh != 0 || prow < 0) return;
-  const f32x4_t hi = s_red[wave][lane];
-  const int n0 = rbk * 16 + (lane >> 4) * 4;
   const float sc = s_w[prow];
-  float o[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float v = acc[i] + hi[i];
-    if (d.bias) v += bf2f(d.bias[(long long)ex * d.bias_group_stride + n0 + i]);
-    o[i] = v * sc;
+  for (int i = 0; i < DRB; ++i) {
+    const f32x4_t hi = s_red[i][wave][lane];
+    const int n0 = (rbk + 4 * i) * 16 + (lane >> 4) * 4;
+    float o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float v = acc[i][e] + hi[e];
+      if (d.bias) v += bf2f(d.bias[(long long)ex * d.bias_group_stride + n0 + e]);
+      o[e] = v * sc;
+    }
+    *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(d.y) + (long long)prow * d.ldy + n0) =
+        f32x4_t{o[0], o[1], o[2], o[3]};
   }
-  *reinterpret_cast<f32x4_t*>(reinterpret_cast<float*>(d.y) + (long long)prow * d.ldy + n0) =
-      f32x4_t{o[0], o[1], o[2], o[3]};
 }
 
 __global__ void sync_clear_kernel(unsigned* p, int n) {
@@ -459,6 +475,20 @@ int moe_fused_flag_words(int T, int K, int E, int I) {
   return gmax * ((2 * I) / 32);
 }
 
+int device_cus() {
+  static int cus = -1;
+  if (cus < 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+      (void)hipGetLastError();
+      n = 0;
+    }
+    cus = n;
+  }
+  return cus;
+}
+
 hipError_t moe_fused_launch(MoeFusedArgs f, int groups_max, hipStream_t s) {
   const RouterArgs& r = f.r;
   const GemmArgs& a = f.gu;
@@ -470,12 +500,20 @@ hipError_t moe_fused_launch(MoeFusedArgs f, int groups_max, hipStream_t s) {
     return hipErrorInvalidValue;
   f.n_gu = a.N / 32;
   f.ngu = f.n_gu * groups_max;
-  f.ndb = f.dn.N / 64;
+  // 128 output rows per down block where that makes the whole grid resident at
+  // two blocks per CU (at one token: 384 gate/up + 128 down blocks); the last
+  // down blocks are otherwise dispatched only as gate/up blocks retire, and
+  // then stream their weights and form the routing after the gate/up work
+  const int drb = (f.dn.N % 128 == 0 && f.ngu + (f.dn.N / 128) * groups_max <= 2 * device_cus()) ? 2 : 1;
+  f.ndb = f.dn.N / (64 * drb);
   const dim3 grid(f.ngu + f.ndb * groups_max), block(512);
   const size_t lds = (size_t)8 * 2 * 4 * 64 * sizeof(float);
   const int per = (r.E + 63) / 64;
   const int nfd = (f.dn.K / 32) / 2;
-#define MKD_FUSED(P, N) if (per <= P && nfd == N) return timed_launch(moe_fused_kernel<P, N>, grid, block, lds, s, f)
+#define MKD_FUSED(P, N)                                                                      \
+  if (per <= P && nfd == N)                                                                  \
+    return drb == 2 ? timed_launch(moe_fused_kernel<P, N, 2>, grid, block, lds, s, f)       \
+                    : timed_launch(moe_fused_kernel<P, N, 1>, grid, block, lds, s, f)
   MKD_FUSED(1, 8); MKD_FUSED(1, 12);
   MKD_FUSED(2, 8); MKD_FUSED(2, 12);
   MKD_FUSED(4, 8); MKD_FUSED(4, 12);

@@ -362,6 +362,7 @@ constexpr int kSelMaxPairs = 64;
 // Gate/up + down in one launch (gemm.hip, moe_fused_kernel): the gate/up blocks
 // publish their h columns through flags[group * n_gu + tile] (zero at launch),
 // the down blocks wait on their group's flags; *err is set when a wait ran out.
+int device_cus();                   // compute units of the current device (0 if unknown)
 constexpr int kFusedMaxRows = 4;   // tokens of the fused expert launch (rows per group)
 struct MoeFusedArgs {
   GemmArgs gu, dn;
