@@ -724,6 +724,146 @@ MKD_DEV void oproj_block(const AttnArgs& a, const AttnJoinArgs& j, int rb, const
   if (j.rw) coh_publish(oflag);
 }
 
+// ---- merge + projection blocks (one token, d = 128, with the router stage) ----
+// Block (ks, nr) merges the chunk partials of query heads 4 ks .. +4 itself (one
+// wave per head, the combine's online log-sum-exp merge over every chunk of the
+// sequence) and projects them onto output rows 128 nr .. +128: the K-split
+// partial ks of y = attn . W_out^T.  This folds the combine stage into the
+// projection -- one flag hop and one device-coherent read of partials fewer
+// than combine blocks followed by projection blocks.  Wave w holds row tiles
+// 8 nr + 2 w, +1 over the block's whole 512-wide K slice (32 fragments), so no
+// cross-wave sum is needed; the router blocks add the nq / 4 partials in order.
+constexpr int kMpHeads = 4;                 // query heads per merge + projection block
+constexpr int kMpRows = 128;                // output rows per block (d = 128)
+constexpr int kMpBatch = 32;                // chunk partials in flight per wave
+constexpr int kMpMaxParts = 8;              // K slices (nq <= 32)
+
+int attn_join_y_parts(int nq) { return nq % kMpHeads == 0 ? std::min(nq / kMpHeads, kMpMaxParts) : 1; }
+
+__host__ __device__ static inline int attn_join_mp_blocks(int nq, int N) { return (nq / kMpHeads) * ((N + kMpRows - 1) / kMpRows); }
+
+bool attn_join_mp_ok(const AttnArgs& a, const AttnJoinArgs& j) {
+  return j.rw && a.B == 1 && a.d == 128 && a.nq % kMpHeads == 0 && a.s_tkg <= 1 && !a.prefill &&
+         a.nq / kMpHeads <= kMpMaxParts;
+}
+
+template <int GQA>
+MKD_DEV void mp_block(const AttnArgs& a, const AttnJoinArgs& j, int ks, int nr, unsigned* oflag) {
+  constexpr int D = 128, FT = kMpHeads * D / 32;    // fragments per row tile of the K slice (16)
+  __shared__ __attribute__((aligned(16))) uint32_t ob_s[kMpHeads * D / 2];   // bf16 pairs of the 4 heads
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int N = j.N, KB = a.nq * D / 32, NRB = (N + 15) / 16;
+  const int h0 = ks * kMpHeads, h = h0 + w;
+  {
+    const unsigned long long t0 = wall_clock64();
+    while (wall_clock64() - t0 < kJoinWeightDelay) __builtin_amdgcn_s_sleep(2);
+  }
+  u32x4_t wf[2][FT];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int rt = min(nr * (kMpRows / 16) + w * 2 + i, NRB - 1);
+    const uint16_t* wrow = j.w_out + ((long long)rt * KB + ks * FT) * 512 + lane * 8;
+#pragma unroll
+    for (int u = 0; u < FT; ++u)
+      wf[i][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + u * 512));
+  }
+  // the chunk flags of the kv groups of the block's heads
+  if (w == 0) {
+    const int g0 = h0 / GQA, g1 = (h0 + kMpHeads - 1) / GQA;
+    for (int g = g0; g <= g1; ++g) coh_wait_all(j.flags + (long long)g * a.n_chunks, a.n_chunks, j.err);
+  }
+  __syncthreads();
+
+  // ---- merge head h: lane l of the ml load holds chunk c0 + l % 32, the
+  // partial loads hold d = 2 l, 2 l + 1 of chunk c0 + u ----
+  const int CP = a.chunk;
+  const int n = prior_len(a, 0);
+  const int nch = (n + 1 + CP - 1) / CP;
+  const long long ml0 = (long long)h * a.n_chunks * 2, po0 = (long long)h * a.n_chunks * D;
+  const __amdgpu_buffer_rsrc_t mlr = coh_rsrc(a.part_ml), por = coh_rsrc(a.part_o);
+  float M = -INFINITY, Ls = 0.f, acc0 = 0.f, acc1 = 0.f;
+  for (int c0 = 0; c0 < nch; c0 += kMpBatch) {
+    const int cl = c0 + (lane & 31);
+    const coh_u32x2 mlv = coh_ld8(mlr, (int)((ml0 + 2 * min(cl, nch - 1)) * 4));
+    coh_u32x2 pv[kMpBatch];
+#pragma unroll
+    for (int u = 0; u < kMpBatch; ++u)
+      pv[u] = coh_ld8(por, (int)((po0 + (long long)min(c0 + u, nch - 1) * D + 2 * lane) * 4));
+    const bool live = cl < nch && lane < 32;
+    const float mk = live ? __uint_as_float(mlv.x) : -INFINITY;
+    const float lk = live ? __uint_as_float(mlv.y) : 0.f;
+    const float bm = fmaxf(M, wave_max(mk));
+    if (bm == -INFINITY) continue;               // nothing live yet (uniform)
+    const float r = M == -INFINITY ? 0.f : expf(M - bm);
+    const float fk = mk == -INFINITY ? 0.f : expf(mk - bm);
+    Ls = Ls * r + wave_sum(lk * fk);
+    acc0 *= r;
+    acc1 *= r;
+#pragma unroll
+    for (int u = 0; u < kMpBatch; ++u) {
+      const float f = lane_f(fk, u);             // 0 past the last chunk
+      acc0 += __uint_as_float(pv[u].x) * f;
+      acc1 += __uint_as_float(pv[u].y) * f;
+    }
+    M = bm;
+  }
+  if (a.sink) {
+    const float sk = a.sink[h];
+    const float M2 = fmaxf(M, sk);
+    const float r = M == -INFINITY ? 0.f : expf(M - M2);
+    Ls = Ls * r + expf(sk - M2);
+    acc0 *= r;
+    acc1 *= r;
+  }
+  ob_s[w * (D / 2) + lane] = Ls > 0.f ? pack2bf(acc0 / Ls, acc1 / Ls) : 0u;
+  __syncthreads();
+
+  // ---- MFMAs: B operand lane l = token l % 16 (token 0 only), k (l / 16) * 8 .. + 8 ----
+  const int c = lane & 15;
+  const uint32_t m = c == 0 ? 0xffffffffu : 0u;
+  const u32x4_t* xq = reinterpret_cast<const u32x4_t*>(ob_s) + (lane >> 4);
+  f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int u = 0; u < FT; ++u) {
+    const u32x4_t t = xq[u * 4];
+    const u32x4_t xv = u32x4_t{t[0] & m, t[1] & m, t[2] & m, t[3] & m};
+    acc[0] = mfma16x16x32(wf[0][u], xv, acc[0]);
+    acc[1] = mfma16x16x32(wf[1][u], xv, acc[1]);
+  }
+  if (c == 0) {
+    const __amdgpu_buffer_rsrc_t yr = coh_rsrc(j.y);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int rt = nr * (kMpRows / 16) + w * 2 + i;
+      const int n0 = rt * 16 + (lane >> 4) * 4;
+      if (rt >= NRB || n0 >= N) continue;
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = acc[i][e] + ((ks == 0 && j.bias) ? bf2f(j.bias[n0 + e]) : 0.f);
+      coh_st16(yr, (int)(((long long)ks * N + n0) * 4),
+               u32x4_t{__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3])});
+    }
+  }
+  coh_publish(oflag);
+  // in-place KV scatter of the new rows (attention_block_tkg.py:1144-1470): the
+  // first query head of each kv group, in the row-0 blocks, once every chunk of
+  // the group has read the cache (the flags above); nothing in this launch
+  // reads the new rows, so the stores go after the flag
+  if (nr == 0 && a.update_cache && h % GQA == 0) {
+    const int g = h / GQA;
+    const long long row = kv_write_row(a, 0);
+    if (row >= 0) {
+      const __amdgpu_buffer_rsrc_t kr = coh_rsrc(a.kv_new);
+      const long long ko = (long long)g * D + 2 * lane, vo = ((long long)a.nkv + g) * D + 2 * lane;
+      const uint32_t kw = coh_ld4(kr, (int)(ko * 2)), vw = coh_ld4(kr, (int)(vo * 2));
+      const long long off = a.block_table ? (row * a.nkv + g) * D + 2 * lane
+                                          : g * a.cache_h_stride + row * D + 2 * lane;
+      *reinterpret_cast<uint32_t*>(a.k_cache + off) = kw;
+      *reinterpret_cast<uint32_t*>(a.v_cache + off) = vw;
+    }
+  }
+}
+
 // ---- router stage: the post-attention residual, norm and router logits ----
 constexpr int kJoinRouterF = 8;      // router weight fragments per wave
 constexpr int kJoinRouterMaxN = 3072;
@@ -751,7 +891,7 @@ bool attn_join_router_supported(int B, int E, int N) {
 // Block 0 also writes r and bf16(y), the residual and expert input of the rest
 // of the layer.
 // RC = the row chunks (16 bytes) per thread, ceil(B N / 8 / 256).
-template <int RC>
+template <int RC, int PM>
 MKD_DEV void router_block(const AttnArgs& a, const AttnJoinArgs& j, int rbk, const unsigned* ofl, int nof) {
   extern __shared__ u32x4_t xs[];             // [B][N / 8] y hi, [B][N / 8] y lo, [N / 8] gamma
   __shared__ float ssw[4][kJoinMaxB];
@@ -785,14 +925,34 @@ MKD_DEV void router_block(const AttnArgs& a, const AttnJoinArgs& j, int rbk, con
   if (w == 0) coh_wait_all(ofl, nof, j.err);
   __syncthreads();
 
-  // r = bf16(x + bf16(y)) (kept in registers), per-token sums of squares
+  // r = bf16(x + bf16(y)) (kept in registers), per-token sums of squares; y is
+  // the sum of the j.o_parts K-split partials (PM at most), in order
   const __amdgpu_buffer_rsrc_t yr = coh_rsrc(j.y);
   u32x4_t y0[kRC], y1[kRC];
+  {
+    u32x4_t p0[kRC][PM], p1[kRC][PM];
 #pragma unroll
-  for (int q = 0; q < kRC; ++q) {
-    const int i = min((int)threadIdx.x + 256 * q, nch - 1);
-    y0[q] = coh_ld16(yr, i * 32);
-    y1[q] = coh_ld16(yr, i * 32 + 16);
+    for (int q = 0; q < kRC; ++q) {
+      const int i = min((int)threadIdx.x + 256 * q, nch - 1);
+#pragma unroll
+      for (int pp = 0; pp < PM; ++pp) {
+        const int off = (min(pp, j.o_parts - 1) * nch + i) * 32;
+        p0[q][pp] = coh_ld16(yr, off);
+        p1[q][pp] = coh_ld16(yr, off + 16);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kRC; ++q) {
+      f32x4_t s0 = __builtin_bit_cast(f32x4_t, p0[q][0]), s1 = __builtin_bit_cast(f32x4_t, p1[q][0]);
+#pragma unroll
+      for (int pp = 1; pp < PM; ++pp)
+        if (pp < j.o_parts) {
+          s0 += __builtin_bit_cast(f32x4_t, p0[q][pp]);
+          s1 += __builtin_bit_cast(f32x4_t, p1[q][pp]);
+        }
+      y0[q] = __builtin_bit_cast(u32x4_t, s0);
+      y1[q] = __builtin_bit_cast(u32x4_t, s1);
+    }
   }
   u32x4_t* yhi = xs;
   u32x4_t* ylo = xs + nch;
@@ -896,7 +1056,21 @@ __global__ void __launch_bounds__(256) attn_joined_kernel(AttnArgs a, AttnJoinAr
   if (bid < na) {
     const int c = bid % a.n_chunks, gb = bid / a.n_chunks;
     attn_chunk_block<D, GQA, TPW, true>(a, rope_mode, c, gb % a.nkv, gb / a.nkv, j.flags + bid);
-  } else if (bid < na + nc) {
+    return;
+  }
+  if (j.mp) {   // merge + projection blocks, then the router blocks
+    const int ksn = a.nq / kMpHeads, nmp = attn_join_mp_blocks(a.nq, j.N);
+    if (bid < na + nmp) {
+      const int q = bid - na;
+      if constexpr (D == 128) mp_block<GQA>(a, j, q % ksn, q / ksn, j.flags + na + nc + q);
+    } else {
+      const int rbk = bid - na - nmp;
+      if ((a.B * j.N / 8 + 255) / 256 == 1) router_block<1, kMpMaxParts>(a, j, rbk, j.flags + na + nc, nmp);
+      else router_block<2, kMpMaxParts>(a, j, rbk, j.flags + na + nc, nmp);
+    }
+    return;
+  }
+  if (bid < na + nc) {
     const int hb = bid - na, h = hb % a.nq, b = hb / a.nq;
     attn_combine_block<D, 16, true>(a, h, b, j.flags + ((long long)b * a.nkv + h / GQA) * a.n_chunks,
                                     a.n_chunks, j.flags + bid, j.err);
@@ -906,12 +1080,12 @@ __global__ void __launch_bounds__(256) attn_joined_kernel(AttnArgs a, AttnJoinAr
   } else {
     const int rbk = bid - na - nc - (j.N + 15) / 16, no = (j.N + 15) / 16;
     switch ((a.B * j.N / 8 + 255) / 256) {   // row chunks per thread
-      case 1: router_block<1>(a, j, rbk, j.flags + na + nc, no); break;
-      case 2: router_block<2>(a, j, rbk, j.flags + na + nc, no); break;
-      case 3: router_block<3>(a, j, rbk, j.flags + na + nc, no); break;
-      case 4: router_block<4>(a, j, rbk, j.flags + na + nc, no); break;
-      case 5: router_block<5>(a, j, rbk, j.flags + na + nc, no); break;
-      default: router_block<6>(a, j, rbk, j.flags + na + nc, no); break;
+      case 1: router_block<1, 1>(a, j, rbk, j.flags + na + nc, no); break;
+      case 2: router_block<2, 1>(a, j, rbk, j.flags + na + nc, no); break;
+      case 3: router_block<3, 1>(a, j, rbk, j.flags + na + nc, no); break;
+      case 4: router_block<4, 1>(a, j, rbk, j.flags + na + nc, no); break;
+      case 5: router_block<5, 1>(a, j, rbk, j.flags + na + nc, no); break;
+      default: router_block<6, 1>(a, j, rbk, j.flags + na + nc, no); break;
     }
   }
 }
@@ -932,14 +1106,18 @@ bool attn_join_supported(const AttnArgs& a, int N) {
 
 template <int D, int GQA>
 static hipError_t launch_join(const AttnArgs& a, const AttnJoinArgs& j, int rope_mode, hipStream_t s) {
-  const int blocks = a.n_chunks * a.nkv * a.B + a.nq * a.B + (j.N + 15) / 16 +
+  const int blocks = a.n_chunks * a.nkv * a.B +
+                     (j.mp ? attn_join_mp_blocks(a.nq, j.N) : a.nq * a.B + (j.N + 15) / 16) +
                      (j.rw ? router_join_blocks(j.E, j.N) : 0);
   const size_t lds = std::max((size_t)a.B * a.nq * a.d * 2, j.rw ? (size_t)(2 * a.B + 1) * j.N * 2 : 0);
   if (a.chunk == 64) return timed_launch(attn_joined_kernel<D, GQA, 1>, dim3(blocks), dim3(256), lds, s, a, j, rope_mode);
   return timed_launch(attn_joined_kernel<D, GQA, 2>, dim3(blocks), dim3(256), lds, s, a, j, rope_mode);
 }
 
-hipError_t attn_join_launch(const AttnArgs& a, const AttnJoinArgs& j, int rope_mode, hipStream_t s) {
+hipError_t attn_join_launch(const AttnArgs& a, const AttnJoinArgs& jin, int rope_mode, hipStream_t s) {
+  AttnJoinArgs j = jin;
+  j.mp = attn_join_mp_ok(a, j) ? 1 : 0;
+  j.o_parts = j.mp ? a.nq / kMpHeads : 1;
   if (!attn_join_supported(a, j.N) || !j.w_out || !j.y || !j.flags || !j.err) return hipErrorInvalidValue;
   if (j.rw && (!attn_join_router_supported(a.B, j.E, j.N) || j.N % 16 || !j.rx || !j.rgamma ||
                !j.rparts || !j.rresid || !j.rhnorm))

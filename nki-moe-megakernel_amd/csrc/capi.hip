@@ -1098,7 +1098,8 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.logits = c.take<float>((size_t)16 * B * m->E);  // split-K partials (<= 16)
   w.cos = c.take<float>((size_t)B * m->d);
   w.sin = c.take<float>((size_t)B * m->d);
-  w.oparts = c.take<float>((size_t)std::max(2, o_proj_kgrid(m, B)) * B * m->H);   // o_proj split-K partials
+  w.oparts = c.take<float>((size_t)std::max({2, o_proj_kgrid(m, B), B == 1 ? attn_join_y_parts(m->nq) : 1}) *
+                           B * m->H);   // o_proj split-K partials
   w.moe = carve_moe(c, B, m->H, m->E, m->I, m->K);
   w.lk = carve_lk(c, m, B);
   w.flag_words = moe_fused_supported(B, m->K, m->E, m->H, m->I) ? moe_fused_flag_words(B, m->K, m->E, m->I) : 0;

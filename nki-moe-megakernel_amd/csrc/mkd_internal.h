@@ -310,7 +310,13 @@ struct AttnJoinArgs {
   float reps, rinv_h;         // norm epsilon, 1 / hidden size it averages over
   int E;
   int rx_f32;                 // 1: router operand fp32 (bf16 hi + lo), 0: bf16
+  // set by attn_join_launch: one token with d = 128 and the router stage merges
+  // the chunk partials inside the projection blocks (no combine blocks), which
+  // then write o_parts K-split partials of y ([o_parts][B][N]); else 0 and 1
+  int mp, o_parts;
 };
+// size of y for attn_join_launch: K-split partials of the merge + projection form
+int attn_join_y_parts(int nq);
 int attn_join_flag_words(int B, int nq, int nkv, int n_chunks, int N);
 bool attn_join_supported(const AttnArgs& a, int N);
 int attn_join_router_parts(int N);
