@@ -1527,7 +1527,11 @@ int mkd_lm_head_greedy(const void* hidden, const void* ln_f, float eps, const vo
   GemmArgs a = dense_args(lm_head_packed, n, H, V, H, B, logits, V);
   {
     const int ps = prof_begin(MKD_KCLASS_LM_HEAD, s);
-    if (int rc = dense_gemm(a, EPI_F32, false, s)) return rc;
+    if (gemm_kloop_supported(V, H, B)) {   // 17..128 tokens: activation slices in LDS
+      MKD_TRY(gemm_kloop_launch(a, s), "lm_head (k-loop)");
+    } else if (int rc = dense_gemm(a, EPI_F32, false, s)) {
+      return rc;
+    }
     prof_end(ps, s);
   }
   MKD_TRY(argmax_launch(logits, B, V, next_tokens, sv, si, s), "argmax");

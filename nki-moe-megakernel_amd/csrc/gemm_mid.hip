@@ -191,6 +191,117 @@ int gemm_mid_kgrid(int N, int K, int T, int max_parts) {
   return best;
 }
 
+// The same contraction for very tall outputs (the vocabulary projection at
+// 17..128 tokens): each block owns 4 * RBW row blocks over the WHOLE K range,
+// looping over K slices of NF fragments -- the slice's activations staged in
+// LDS, the wave's weight fragments streamed -- and writes finished fp32 rows
+// (bias added), so there are no K-split partials to write and read back.  One
+// 16-row block per launch block instead (the weight-streaming GEMM) reads the
+// activations of every token for every weight fragment through the CU:
+// 4 bytes per weight byte at 64 tokens.
+template <int TT, int RBW, int NF>
+__global__ void __launch_bounds__(256) gemm_kloop_kernel(GemmArgs a) {
+  extern __shared__ __attribute__((aligned(16))) u32x4_t xs[];    // [TT][NF][64]
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int KB = a.K / 32, NRB = (a.N + 15) / 16, nsl = KB / NF;
+  constexpr int NCH = TT * NF * 64;
+  constexpr int PJ = NCH / 256;                    // staging chunks per thread
+  static_assert(NCH % 256 == 0, "chunk split");
+  f32x4_t acc[RBW][TT];
+#pragma unroll
+  for (int r = 0; r < RBW; ++r)
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) acc[r][tt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* wp[RBW];
+#pragma unroll
+  for (int r = 0; r < RBW; ++r) {
+    const int rb = min(blockIdx.x * kMidWaves * RBW + r * kMidWaves + w, NRB - 1);
+    wp[r] = a.w + (long long)rb * KB * 512 + lane * 8;
+  }
+  for (int sl = 0; sl < nsl; ++sl) {
+    const int kf0 = sl * NF;
+    // the slice's weight fragments, then its activation chunks (L2-resident)
+    u32x4_t wf[RBW][NF];
+#pragma unroll
+    for (int r = 0; r < RBW; ++r)
+#pragma unroll
+      for (int f = 0; f < NF; ++f)
+        wf[r][f] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp[r] + (kf0 + f) * 512));
+    u32x4_t v[PJ];
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      const int c = threadIdx.x + j * 256;
+      const int l = c & 63, f = (c >> 6) % NF, tt = c / (64 * NF);
+      const int t = tt * 16 + (l & 15);
+      v[j] = ld16(static_cast<const uint16_t*>(a.x) + (long long)(t < a.T ? t : 0) * a.ldx +
+                  (long long)(kf0 + f) * 32 + (l >> 4) * 8);
+    }
+    __syncthreads();                               // the previous slice's reads of xs are done
+#pragma unroll
+    for (int j = 0; j < PJ; ++j) {
+      const int c = threadIdx.x + j * 256;
+      const bool live = (c / (64 * NF)) * 16 + (c & 15) < a.T;
+      xs[c] = live ? v[j] : u32x4_t{0u, 0u, 0u, 0u};
+    }
+    __syncthreads();
+#pragma unroll
+    for (int f = 0; f < NF; ++f) {
+      u32x4_t xf[TT];
+#pragma unroll
+      for (int tt = 0; tt < TT; ++tt) xf[tt] = xs[(tt * NF + f) * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < RBW; ++r)
+#pragma unroll
+        for (int tt = 0; tt < TT; ++tt) acc[r][tt] = mfma16x16x32(wf[r][f], xf[tt], acc[r][tt]);
+    }
+  }
+  float* yb = static_cast<float*>(a.y);
+#pragma unroll
+  for (int r = 0; r < RBW; ++r) {
+    const int rb = blockIdx.x * kMidWaves * RBW + r * kMidWaves + w;
+    if (rb >= NRB) continue;
+    const int n0 = rb * 16 + (lane >> 4) * 4;
+    float bb[4] = {0.f, 0.f, 0.f, 0.f};
+    if (a.bias) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) bb[i] = (n0 + i < a.N) ? bf2f(a.bias[n0 + i]) : 0.f;
+    }
+#pragma unroll
+    for (int tt = 0; tt < TT; ++tt) {
+      const int t = tt * 16 + (lane & 15);
+      if (t >= a.T) continue;
+      float* y = yb + (long long)t * a.ldy + n0;
+      if (n0 + 3 < a.N && (a.ldy & 3) == 0) {
+        *reinterpret_cast<f32x4_t*>(y) = f32x4_t{acc[r][tt][0] + bb[0], acc[r][tt][1] + bb[1],
+                                                 acc[r][tt][2] + bb[2], acc[r][tt][3] + bb[3]};
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (n0 + i < a.N) y[i] = acc[r][tt][i] + bb[i];
+      }
+    }
+  }
+}
+
+constexpr int kKloopRBW = 2, kKloopNF = 8;
+
+bool gemm_kloop_supported(int N, int K, int T) {
+  return T >= 17 && T <= 128 && K % (32 * kKloopNF) == 0 && N > 0 &&
+         (long long)((N + 15) / 16 + kMidWaves * kKloopRBW - 1) / (kMidWaves * kKloopRBW) >= 1024;
+}
+
+hipError_t gemm_kloop_launch(const GemmArgs& a, hipStream_t s) {
+  if (!gemm_kloop_supported(a.N, a.K, a.T) || a.grp_expert || a.kgrid > 1) return hipErrorInvalidValue;
+  const int TT = (a.T + 15) / 16;
+  const int tt = TT <= 2 ? 2 : (TT <= 4 ? 4 : 8);
+  const dim3 grid(((a.N + 15) / 16 + kMidWaves * kKloopRBW - 1) / (kMidWaves * kKloopRBW));
+  const size_t lds = (size_t)tt * kKloopNF * 64 * 16;
+  if (tt == 2) return timed_launch(gemm_kloop_kernel<2, kKloopRBW, kKloopNF>, grid, dim3(256), lds, s, a);
+  if (tt == 4) return timed_launch(gemm_kloop_kernel<4, kKloopRBW, kKloopNF>, grid, dim3(256), lds, s, a);
+  return timed_launch(gemm_kloop_kernel<8, kKloopRBW, kKloopNF>, grid, dim3(256), lds, s, a);
+}
+
 template <int TT, int RBW, int NF, bool XF32>
 static hipError_t mid_go(const GemmArgs& a, dim3 grid, size_t lds, hipStream_t s) {
   if (lds > 65536)   // above the default dynamic LDS limit: raise the kernel's

@@ -100,6 +100,10 @@ int choose_kw_mx(int K_pad);
 // LDS, fp32 split-K partials (kgrid from gemm_mid_kgrid; 0 = shape not covered)
 int gemm_mid_kgrid(int N, int K, int T, int max_parts = 8);
 hipError_t gemm_mid_launch(GemmArgs a, int kgrid, bool xf32, hipStream_t s);
+// the vocabulary projection at 17..128 tokens: whole-K blocks of 128 rows
+// looping over K slices staged in LDS (fp32 rows, no partials)
+bool gemm_kloop_supported(int N, int K, int T);
+hipError_t gemm_kloop_launch(const GemmArgs& a, hipStream_t s);
 // gemm_tile.hip: LDS-tiled grouped GEMM (many tokens per expert)
 bool gemm_tile_supported(int N, int K, int epi);
 // total_rows: the sum of the group sizes (grouped mode: T*K pairs), else the rows.

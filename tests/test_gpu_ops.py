@@ -865,6 +865,38 @@ def test_decode_step_two_layers_greedy(mk, dev):
             assert int(nxt[b]) == int(nxt_ref[b])
 
 
+@pytest.mark.parametrize("B", [20, 64, 128])
+def test_lm_head_greedy_many_tokens(mk, dev, B):
+    """The vocabulary projection at 17..128 tokens (whole-K blocks looping over
+    LDS-staged activation slices) through mkd_lm_head_greedy: logits against the
+    oracle's final norm + projection in fp32, arg-max where the top two are
+    apart (main.py:390-398)."""
+    from nki_moe_megakernel_amd import packing
+    L = _lib(mk)
+    lib = L.load()
+    H, V = 512, 151936
+    print(f"lm_head: B={B} H={H} V={V}", flush=True)
+    g = torch.Generator().manual_seed(B)
+    x = bf(torch.randn(B, H, generator=g))
+    lnf = bf(1 + 0.1 * torch.randn(H, generator=g))
+    lm = bf(0.05 * torch.randn(V, H, generator=g))
+    packed = packing.pack_out_in(lm.to(dev))
+    logits = torch.empty(B, V, dtype=torch.float32, device=dev)
+    nxt = torch.empty(B, dtype=torch.int32, device=dev)
+    ws = torch.zeros(lib.mkd_lm_head_workspace_bytes(B, H, V), dtype=torch.uint8, device=dev)
+    xd, lnd = x.to(dev), lnf.to(dev)
+    L.check(lib.mkd_lm_head_greedy(xd.data_ptr(), lnd.data_ptr(), 1e-6, packed.data_ptr(), B, H, V, H, 2,
+                                   logits.data_ptr(), nxt.data_ptr(), ws.data_ptr(), ws.numel(),
+                                   L.stream_ptr(dev)), "lm_head")
+    torch.cuda.synchronize()
+    lg_ref, nxt_ref = ref.final_norm_lm_head(x.float(), lnf, lm, 1e-6)
+    assert max_abs_rel(logits, lg_ref) < TOL
+    top2 = torch.topk(lg_ref, 2, -1).values
+    for b in range(B):
+        if (top2[b, 0] - top2[b, 1]).item() > 1e-2 * lg_ref[b].abs().max().item():
+            assert int(nxt[b]) == int(nxt_ref[b]), b
+
+
 # ---------------------------------------------------------------- GPT-OSS layer
 def _dequant_mx_torch(codes, scales, fmt, k):
     """Independent dequantiser for the test: element value table x 2^(scale-127)."""
