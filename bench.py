@@ -441,8 +441,7 @@ def main():
                    "layers": cfg.num_hidden_layers, "experts": args.experts,
                    "kv_block": args.kv_block,
                    "graph": graph is not None,
-                   "attention_launch": "joined (attention + combine + o_proj)"
-                   if hasattr(model, "joined_attention") and model.joined_attention(B) else "separate",
+                   "attention_launch": attention_launch(model, B),
                    "step_algorithmic_GB": round(step_b / 1e9, 4),
                    "step_GBps": round(step_gbs, 1),
                    "step_hbm_frac": round(step_gbs / HBM_PEAK_GBS, 4),
@@ -646,6 +645,16 @@ def workload_name(cfg, B, ctx, lens, args):
                 f"full alternating, sinks), bs={B}, {kv}, {args.experts} experts{tag}")
     return (f"Qwen3-30B-A3B-shaped {cfg.num_hidden_layers}-layer greedy decode, bs={B}, {kv}, "
             f"{args.experts} experts{tag}")
+
+
+def attention_launch(model, B):
+    """How the decode step runs attention for this batch (the decode plan)."""
+    if not (hasattr(model, "joined_attention") and model.joined_attention(B)):
+        return "separate launches"
+    if model.router_in_attention(B):
+        return ("joined (attention, chunk merge + o_proj, residual + post norm + router GEMM)" if B == 1
+                else "joined (attention, combine, o_proj, residual + post norm + router GEMM)")
+    return "joined (attention + combine + o_proj)"
 
 
 def measured_traffic(B, ctx, layers, kcls="moe_gate_up", joined=False):
