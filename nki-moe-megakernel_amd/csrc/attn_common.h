@@ -42,7 +42,7 @@ struct HeadPrep {
     const float* sp = rope_tab ? a.sin + (long long)b * D : reinterpret_cast<const float*>(src);
     const int l = lane < HD ? lane : 0;
     off0 = (long long)b * a.ld_qkv + head * D + l;
-    np = (f32 && a.qkv_nparts > 1) ? min(a.qkv_nparts, kMaxQkvParts) : 1;
+    np = (f32 && a.qkv_nparts > 1 && head * D >= a.qkv_split_row) ? min(a.qkv_nparts, kMaxQkvParts) : 1;
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
       const int i = l + e * HD;

@@ -742,7 +742,9 @@ static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_
   w.n_chunks = (S_max + s_tkg + w.chunk - 1) / w.chunk;
   w.hnorm = c.take<uint16_t>((size_t)B * H);
   // the QKV projection of 17..128 tokens comes as split-K partials
-  const int qparts = std::max(1, gemm_mid_kgrid((nq + 2 * nkv) * d, H, B));
+  const int qparts = std::max({1, gemm_mid_kgrid((nq + 2 * nkv) * d, H, B),
+                               (qkv_norm_supported(B, (nq + 2 * nkv) * d, H) &&
+                                qkv_norm_extra_tiles((nq + 2 * nkv) * d, H)) ? 4 : 1});
   w.qkv = c.take<float>((size_t)qparts * B * (nq + 2 * nkv) * d);
   w.attn = c.take<uint16_t>((size_t)B * nq * d);
   w.kvn = c.take<uint16_t>((size_t)B * 2 * nkv * d);
@@ -776,7 +778,7 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   const int qkv_n = (p->nq + 2 * p->nkv) * p->d;
   const int NT = p->s_tkg > 1 ? p->s_tkg : 1;
   const int rows = p->B * NT;            // query tokens: NT consecutive rows per sequence
-  int qkv_parts = 1;
+  int qkv_parts = 1, qkv_split_row = 0;
   // 1. optional RMSNorm
   const void* xin = p->X;
   if (p->rmsnorm_gamma) {
@@ -793,9 +795,14 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     q.w = static_cast<const uint16_t*>(p->w_qkv_packed);
     q.N = qkv_n; q.K = p->H; q.T = rows;
     q.y = w.qkv; q.ldy = qkv_n;
+    q.part_stride = (long long)rows * qkv_n;
     const int ps = prof_begin(MKD_KCLASS_QKV, s);
     MKD_TRY(qkv_norm_launch(q, s), "qkv + norm");
     prof_end(ps, s);
+    if (const int xt = qkv_norm_extra_tiles(qkv_n, p->H)) {   // the last tiles as K quarters
+      qkv_parts = 4;
+      qkv_split_row = (qkv_n / 16 - xt) * 16;
+    }
   } else {
     GemmArgs g = dense_args(p->w_qkv_packed, xin, p->H, qkv_n, p->H, rows, w.qkv, qkv_n);
     g.bias = static_cast<const uint16_t*>(p->bias_qkv);
@@ -817,6 +824,7 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   memset(&a, 0, sizeof(a));
   a.qkv = w.qkv; a.ld_qkv = qkv_n;
   a.qkv_nparts = qkv_parts; a.qkv_part_stride = (long long)rows * qkv_n;
+  a.qkv_split_row = qkv_split_row;
   a.q_norm = static_cast<const uint16_t*>(p->q_norm);
   a.k_norm = static_cast<const uint16_t*>(p->k_norm);
   a.qk_eps = p->qk_eps;

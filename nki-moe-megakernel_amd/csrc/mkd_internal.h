@@ -196,9 +196,14 @@ struct QkvNormArgs {
   uint16_t* resid_out;        // [T, ld_r] x, the new residual stream (or null)
   float* y;                   // [T, ldy] fp32 projections
   int ldy;
+  long long part_stride;      // elements between the K-quarter partials of the extra tiles
+  int n_main, n_extra;        // set by qkv_norm_launch
 };
 bool qkv_norm_supported(int T, int N, int K);
 hipError_t qkv_norm_launch(const QkvNormArgs& a, hipStream_t s);
+// 16-row tiles past one per CU, written as 4 K-quarter partials (0: none); rows
+// from (N / 16 - extra) * 16 on then come as 4 partials at part_stride
+int qkv_norm_extra_tiles(int N, int K);
 
 // norm.hip
 struct NormArgs {
@@ -225,6 +230,7 @@ struct AttnArgs {
   const float* qkv;           // [B, (nq + 2 nkv) * d] fp32 projections (or null)
   int qkv_nparts;             // split-K partials of qkv (0 / 1: one), summed in order
   long long qkv_part_stride;  // elements between the partials
+  int qkv_split_row;          // rows of a token below this come as one partial (0: all split)
   const uint16_t* qkv_bf16;   // same, bf16 (operator path) (or null)
   int ld_qkv;
   const uint16_t* q_norm;     // [d] or null

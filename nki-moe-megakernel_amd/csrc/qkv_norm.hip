@@ -30,15 +30,30 @@ constexpr int kQnMaxDK = 8;      // partial rows per token
 // CU (4 waves per SIMD, <= 128 VGPRs) up to NF = 8: the grid (N / 16 blocks)
 // exceeds the CU count, and a second round of blocks would double the launch's
 // latency.  NF = 16 (K = 4096) keeps one block per CU, where the cap would spill.
-template <int NF>
-__global__ void __launch_bounds__(kQnThreads, NF <= 8 ? 4 : 2) qkv_norm_gemm_kernel(QkvNormArgs a) {
+//
+// XQ: more 16-row tiles than CUs (N = 5120: 320 tiles on 256 CUs) -- one block
+// per CU owns tile blockIdx.x, and two more waves take a K quarter of one of the
+// remaining tiles (tile nmain + blockIdx.x / 4, quarter blockIdx.x % 4), written
+// as partial quarter of those rows at y + quarter * part_stride; the head
+// preparation adds the quarters in order.  Every CU then streams the same bytes,
+// where a second block on a quarter of the CUs (the plain grid) made the launch
+// wait for those CUs (9.1 against 6.7 us with the extra tiles left out).
+template <int NF, bool XQ>
+__global__ void __launch_bounds__(kQnThreads + (XQ ? 128 : 0), XQ ? 1 : (NF <= 8 ? 4 : 2))
+qkv_norm_gemm_kernel(QkvNormArgs a) {
+  constexpr int NWV = kQnWaves + (XQ ? 2 : 0);
   extern __shared__ __attribute__((aligned(16))) uint16_t hs[];    // [T][K] x, then hn
-  __shared__ float ssr[kQnWaves * kQkvNormMaxT];
-  __shared__ __attribute__((aligned(16))) f32x4_t red[kQnWaves][64];
+  __shared__ float ssr[NWV * kQkvNormMaxT];
+  __shared__ __attribute__((aligned(16))) f32x4_t red[NWV][64];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int rb = blockIdx.x;
   const int K = a.K, T = a.T, KB = K / 32;
+  // the wave's tile and K slice (of eight)
+  const bool xw = XQ && w >= kQnWaves;
+  const int xq = blockIdx.x & 3;                              // extra waves: K quarter
+  const bool xlive = xw && (int)blockIdx.x / 4 < a.n_extra;
+  const int rb = xw ? a.n_main + min((int)blockIdx.x / 4, a.n_extra - 1) : (int)blockIdx.x;
+  const int ks = xw ? xq * 2 + (w - kQnWaves) : w;
 
   // ---- 1. the row loads (residual, partial rows) go out first, then the
   // wave's weight fragments: a wave's loads complete in issue order, so the
@@ -97,7 +112,7 @@ __global__ void __launch_bounds__(kQnThreads, NF <= 8 ? 4 : 2) qkv_norm_gemm_ker
   };
   load_chunk(0);
   u32x4_t wf[NF];
-  const uint16_t* wp = a.w + ((long long)rb * KB + w * NF) * 512 + lane * 8;
+  const uint16_t* wp = a.w + ((long long)rb * KB + ks * NF) * 512 + lane * 8;
 #pragma unroll
   for (int u = 0; u < NF; ++u)
     wf[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp + u * 512));
@@ -140,7 +155,7 @@ __global__ void __launch_bounds__(kQnThreads, NF <= 8 ? 4 : 2) qkv_norm_gemm_ker
 
   // ---- 4. the wave's MFMAs (B operand: token l%16, k 8*(l/16)..+8 of the slice) ----
   const int col = lane & 15;
-  const uint16_t* xrow = hs + (col < T ? col : 0) * K + w * NF * 32 + (lane >> 4) * 8;
+  const uint16_t* xrow = hs + (col < T ? col : 0) * K + ks * NF * 32 + (lane >> 4) * 8;
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int u = 0; u < NF; ++u) {
@@ -160,6 +175,14 @@ __global__ void __launch_bounds__(kQnThreads, NF <= 8 ? 4 : 2) qkv_norm_gemm_ker
     for (int i = 0; i < 4; ++i)
       if (n0 + i < a.N) y[i] = s[i];
   }
+  if (XQ && w == kQnWaves && xlive && col < T) {   // the extra tile's K quarter xq
+    const f32x4_t s = red[kQnWaves][lane] + red[kQnWaves + 1][lane];
+    const int n0 = rb * 16 + (lane >> 4) * 4;
+    float* y = a.y + (long long)xq * a.part_stride + (long long)col * a.ldy + n0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (n0 + i < a.N) y[i] = s[i];
+  }
 }
 
 bool qkv_norm_supported(int T, int N, int K) {
@@ -169,15 +192,29 @@ bool qkv_norm_supported(int T, int N, int K) {
          T * K <= kQnThreads * 8;
 }
 
-hipError_t qkv_norm_launch(const QkvNormArgs& a, hipStream_t s) {
+int qkv_norm_extra_tiles(int N, int K) {
+  const int tiles = N / 16, cus = device_cus(), nf = K / 32 / kQnWaves;
+  if (cus <= 0 || tiles <= cus || nf > 8) return 0;
+  const int extra = tiles - cus;
+  return extra * 4 <= cus ? extra : 0;
+}
+
+hipError_t qkv_norm_launch(const QkvNormArgs& ain, hipStream_t s) {
+  QkvNormArgs a = ain;
   if (!qkv_norm_supported(a.T, a.N, a.K) || (a.dsum && (a.dK < 1 || a.dK > kQnMaxDK)))
     return hipErrorInvalidValue;
-  const dim3 grid(a.N / 16), block(kQnThreads);
+  a.n_extra = qkv_norm_extra_tiles(a.N, a.K);
+  a.n_main = a.N / 16 - a.n_extra;
+  if (a.n_extra && a.part_stride < (long long)a.T * a.ldy) return hipErrorInvalidValue;
+  const dim3 grid(a.n_main), block(kQnThreads + (a.n_extra ? 128 : 0));
   const size_t lds = (size_t)a.T * a.K * 2;
-#define MKD_QN(NF_) \
-  case NF_: return timed_launch(qkv_norm_gemm_kernel<NF_>, grid, block, lds, s, a);
+#define MKD_QN(NF_)                                                                          \
+  case NF_:                                                                                  \
+    return a.n_extra ? timed_launch(qkv_norm_gemm_kernel<NF_, true>, grid, block, lds, s, a)  \
+                     : timed_launch(qkv_norm_gemm_kernel<NF_, false>, grid, block, lds, s, a);
   switch (a.K / 32 / kQnWaves) {
-    MKD_QN(1) MKD_QN(2) MKD_QN(4) MKD_QN(8) MKD_QN(16)
+    MKD_QN(1) MKD_QN(2) MKD_QN(4) MKD_QN(8)
+    case 16: return timed_launch(qkv_norm_gemm_kernel<16, false>, grid, block, lds, s, a);
     default: return hipErrorInvalidValue;
   }
 #undef MKD_QN
