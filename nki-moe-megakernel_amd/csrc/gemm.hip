@@ -323,10 +323,13 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   // a down block's weight slice does not depend on the routing: its row block
   // and K half are fixed, only the expert offset is not -- so the routing comes
   // first, then the loads
-  if (r.T == 1 && r.E <= 128 && 4 * r.E <= (int)blockDim.x)
-    select_one(q, [&](int t, float (&l)[2]) { load_logits<2>(q, t, lane, l); });
-  else
+  if (r.T == 1 && r.E <= 128 && 4 * r.E <= (int)blockDim.x) {
+    // the joined attention launch's router stage leaves 8 partial logits
+    if (r.nparts <= 8) select_one(q, [&](int t, float (&l)[2]) { load_logits<2, 8>(q, t, lane, l); });
+    else select_one(q, [&](int t, float (&l)[2]) { load_logits<2>(q, t, lane, l); });
+  } else {
     select_small<PER>(q, [&](int t, float (&l)[PER]) { load_logits<PER>(q, t, lane, l); });
+  }
   __syncthreads();
   if (lead) {
     const int ng = s_ng, np = r.T * r.K;

@@ -56,7 +56,9 @@ MKD_DEV int wave_excl_scan(int v, int lane) {
 // Sum of the split-K partial logits of token t for the lane's experts (+ the
 // bias): a whole batch of loads is issued (slots past nparts re-read the last
 // partial and are masked out) before summing in fixed order.
-template <int PER>
+// NPM: partial count the loads are unrolled for (a.nparts <= NPM; the partials
+// past a.nparts repeat the last one and are not added).
+template <int PER, int NPM = 16>
 MKD_DEV void load_logits(const RouterArgs& a, int t, int lane, float (&l)[PER]) {
   const int E = a.E;
   uint32_t braw[PER];                   // bias bits, loaded with the partials
@@ -66,9 +68,9 @@ MKD_DEV void load_logits(const RouterArgs& a, int t, int lane, float (&l)[PER]) 
   }
 #pragma unroll
   for (int j = 0; j < PER; ++j) l[j] = 0.f;
-  constexpr int PB = (PER <= 2) ? 16 : 4;
+  constexpr int PB = (PER <= 2) ? NPM : 4;
 #pragma unroll
-  for (int p0 = 0; p0 < 16; p0 += PB) {
+  for (int p0 = 0; p0 < NPM; p0 += PB) {
     float v[PB][PER];
 #pragma unroll
     for (int q = 0; q < PB; ++q) {
