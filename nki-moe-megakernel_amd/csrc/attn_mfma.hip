@@ -735,7 +735,8 @@ MKD_DEV void oproj_block(const AttnArgs& a, const AttnJoinArgs& j, int rb, const
 // cross-wave sum is needed; the router blocks add the nq / 4 partials in order.
 constexpr int kMpHeads = 4;                 // query heads per merge + projection block
 constexpr int kMpRows = 128;                // output rows per block (d = 128)
-constexpr int kMpBatch = 32;                // chunk partials in flight per wave
+constexpr int kMpBatch = 20;                // chunk partials in flight per wave (two waves per SIMD with the polling loop)
+static_assert(kMpBatch <= 32, "one (max, sum) load per lane covers a batch");
 constexpr int kMpMaxParts = 8;              // K slices (nq <= 32)
 
 int attn_join_y_parts(int nq) { return nq % kMpHeads == 0 ? std::min(nq / kMpHeads, kMpMaxParts) : 1; }
@@ -744,7 +745,7 @@ __host__ __device__ static inline int attn_join_mp_blocks(int nq, int N) { retur
 
 bool attn_join_mp_ok(const AttnArgs& a, const AttnJoinArgs& j) {
   return j.rw && a.B == 1 && a.d == 128 && a.nq % kMpHeads == 0 && a.s_tkg <= 1 && !a.prefill &&
-         a.nq / kMpHeads <= kMpMaxParts;
+         a.nq / kMpHeads <= kMpMaxParts && j.N <= 2048;
 }
 
 template <int GQA>
@@ -767,12 +768,15 @@ MKD_DEV void mp_block(const AttnArgs& a, const AttnJoinArgs& j, int ks, int nr, 
     for (int u = 0; u < FT; ++u)
       wf[i][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + u * 512));
   }
-  // the chunk flags of the kv groups of the block's heads
-  if (w == 0) {
-    const int g0 = h0 / GQA, g1 = (h0 + kMpHeads - 1) / GQA;
-    for (int g = g0; g <= g1; ++g) coh_wait_all(j.flags + (long long)g * a.n_chunks, a.n_chunks, j.err);
+  // the chunk flags of the kv groups of the block's heads (with the data-polled
+  // exchange the partials themselves are polled below)
+  if (!j.dpoll) {
+    if (w == 0) {
+      const int g0 = h0 / GQA, g1 = (h0 + kMpHeads - 1) / GQA;
+      for (int g = g0; g <= g1; ++g) coh_wait_all(j.flags + (long long)g * a.n_chunks, a.n_chunks, j.err);
+    }
+    __syncthreads();
   }
-  __syncthreads();
 
   // ---- merge head h: lane l of the ml load holds chunk c0 + l % 32, the
   // partial loads hold d = 2 l, 2 l + 1 of chunk c0 + u ----
@@ -784,12 +788,23 @@ MKD_DEV void mp_block(const AttnArgs& a, const AttnJoinArgs& j, int ks, int nr, 
   float M = -INFINITY, Ls = 0.f, acc0 = 0.f, acc1 = 0.f;
   for (int c0 = 0; c0 < nch; c0 += kMpBatch) {
     const int cl = c0 + (lane & 31);
-    const coh_u32x2 mlv = coh_ld8(mlr, (int)((ml0 + 2 * min(cl, nch - 1)) * 4));
+    const bool live = cl < nch && lane < kMpBatch;     // this batch's chunks only
+    coh_u32x2 mlv;
     coh_u32x2 pv[kMpBatch];
+    for (unsigned it = 0;; ++it) {
+      mlv = coh_ld8(mlr, (int)((ml0 + 2 * min(cl, nch - 1)) * 4));
 #pragma unroll
-    for (int u = 0; u < kMpBatch; ++u)
-      pv[u] = coh_ld8(por, (int)((po0 + (long long)min(c0 + u, nch - 1) * D + 2 * lane) * 4));
-    const bool live = cl < nch && lane < 32;
+      for (int u = 0; u < kMpBatch; ++u)
+        pv[u] = coh_ld8(por, (int)((po0 + (long long)min(c0 + u, nch - 1) * D + 2 * lane) * 4));
+      if (!j.dpoll) break;
+      // every word this wave reads written (kPollEmpty: not yet)
+      bool ok = !live || (mlv.x != kPollEmpty && mlv.y != kPollEmpty);
+#pragma unroll
+      for (int u = 0; u < kMpBatch; ++u)
+        ok = ok && (c0 + u >= nch || (pv[u].x != kPollEmpty && pv[u].y != kPollEmpty));
+      if (__all(ok) || coh_poll_giveup(it, j.err)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
     const float mk = live ? __uint_as_float(mlv.x) : -INFINITY;
     const float lk = live ? __uint_as_float(mlv.y) : 0.f;
     const float bm = fmaxf(M, wave_max(mk));
@@ -844,13 +859,14 @@ MKD_DEV void mp_block(const AttnArgs& a, const AttnJoinArgs& j, int ks, int nr, 
                u32x4_t{__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3])});
     }
   }
-  coh_publish(oflag);
+  if (!j.dpoll) coh_publish(oflag);
   // in-place KV scatter of the new rows (attention_block_tkg.py:1144-1470): the
   // first query head of each kv group, in the row-0 blocks, once every chunk of
-  // the group has read the cache (the flags above); nothing in this launch
-  // reads the new rows, so the stores go after the flag
+  // the group has read the cache (its flags); nothing in this launch reads the
+  // new rows, so the stores go after the block's results
   if (nr == 0 && a.update_cache && h % GQA == 0) {
     const int g = h / GQA;
+    if (j.dpoll) coh_wait_all(j.flags + (long long)g * a.n_chunks, a.n_chunks, j.err);
     const long long row = kv_write_row(a, 0);
     if (row >= 0) {
       const __amdgpu_buffer_rsrc_t kr = coh_rsrc(a.kv_new);
@@ -922,24 +938,40 @@ MKD_DEV void router_block(const AttnArgs& a, const AttnJoinArgs& j, int rbk, con
 #pragma unroll
   for (int u = 0; u < kJoinRouterF; ++u)
     wf[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + min(u, nf - 1) * 512));
-  if (w == 0) coh_wait_all(ofl, nof, j.err);
-  __syncthreads();
+  if (!j.dpoll) {
+    if (w == 0) coh_wait_all(ofl, nof, j.err);
+    __syncthreads();
+  }
 
   // r = bf16(x + bf16(y)) (kept in registers), per-token sums of squares; y is
-  // the sum of the j.o_parts K-split partials (PM at most), in order
+  // the sum of the j.o_parts K-split partials (PM at most), in order (with the
+  // data-polled exchange, loaded until no word reads kPollEmpty)
   const __amdgpu_buffer_rsrc_t yr = coh_rsrc(j.y);
   u32x4_t y0[kRC], y1[kRC];
   {
     u32x4_t p0[kRC][PM], p1[kRC][PM];
+    for (unsigned it = 0;; ++it) {
 #pragma unroll
-    for (int q = 0; q < kRC; ++q) {
-      const int i = min((int)threadIdx.x + 256 * q, nch - 1);
+      for (int q = 0; q < kRC; ++q) {
+        const int i = min((int)threadIdx.x + 256 * q, nch - 1);
 #pragma unroll
-      for (int pp = 0; pp < PM; ++pp) {
-        const int off = (min(pp, j.o_parts - 1) * nch + i) * 32;
-        p0[q][pp] = coh_ld16(yr, off);
-        p1[q][pp] = coh_ld16(yr, off + 16);
+        for (int pp = 0; pp < PM; ++pp) {
+          const int off = (min(pp, j.o_parts - 1) * nch + i) * 32;
+          p0[q][pp] = coh_ld16(yr, off);
+          p1[q][pp] = coh_ld16(yr, off + 16);
+        }
       }
+      if (!j.dpoll) break;
+      bool ok = true;
+#pragma unroll
+      for (int q = 0; q < kRC; ++q)
+#pragma unroll
+        for (int pp = 0; pp < PM; ++pp)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            ok = ok && p0[q][pp][e] != kPollEmpty && p1[q][pp][e] != kPollEmpty;
+      if (__all(ok) || coh_poll_giveup(it, j.err)) break;
+      __builtin_amdgcn_s_sleep(1);
     }
 #pragma unroll
     for (int q = 0; q < kRC; ++q) {
@@ -1064,9 +1096,8 @@ __global__ void __launch_bounds__(256) attn_joined_kernel(AttnArgs a, AttnJoinAr
       const int q = bid - na;
       if constexpr (D == 128) mp_block<GQA>(a, j, q % ksn, q / ksn, j.flags + na + nc + q);
     } else {
-      const int rbk = bid - na - nmp;
-      if ((a.B * j.N / 8 + 255) / 256 == 1) router_block<1, kMpMaxParts>(a, j, rbk, j.flags + na + nc, nmp);
-      else router_block<2, kMpMaxParts>(a, j, rbk, j.flags + na + nc, nmp);
+      // one token of N <= 2048 (attn_join_mp_ok): one row chunk per thread
+      router_block<1, kMpMaxParts>(a, j, bid - na - nmp, j.flags + na + nc, nmp);
     }
     return;
   }
@@ -1114,10 +1145,17 @@ static hipError_t launch_join(const AttnArgs& a, const AttnJoinArgs& j, int rope
   return timed_launch(attn_joined_kernel<D, GQA, 2>, dim3(blocks), dim3(256), lds, s, a, j, rope_mode);
 }
 
-hipError_t attn_join_launch(const AttnArgs& a, const AttnJoinArgs& jin, int rope_mode, hipStream_t s) {
+hipError_t attn_join_launch(const AttnArgs& ain, const AttnJoinArgs& jin, int rope_mode, hipStream_t s) {
   AttnJoinArgs j = jin;
+  AttnArgs a = ain;
   j.mp = attn_join_mp_ok(a, j) ? 1 : 0;
   j.o_parts = j.mp ? a.nq / kMpHeads : 1;
+  j.dpoll = (j.mp && j.poll_po && j.poll_pml && j.poll_y) ? 1 : 0;
+  if (j.dpoll) {   // this launch's own exchange buffers, filled with kPollEmpty
+    a.part_o = j.poll_po;
+    a.part_ml = j.poll_pml;
+    j.y = j.poll_y;
+  }
   if (!attn_join_supported(a, j.N) || !j.w_out || !j.y || !j.flags || !j.err) return hipErrorInvalidValue;
   if (j.rw && (!attn_join_router_supported(a.B, j.E, j.N) || j.N % 16 || !j.rx || !j.rgamma ||
                !j.rparts || !j.rresid || !j.rhnorm))
@@ -1175,7 +1213,7 @@ int attn_chunk_for(int B, int nkv, int S_max) {
     if (blocks >= 1024) return chunk;
   }
   // one token: 128, so that the joined launch's merge + projection blocks read
-  // the chunk partials of a head in one batch up to 4096 positions (measured at
+  // the chunk partials of a head in one batch up to 2560 positions (measured at
   // KV 2048, Qwen3-30B-A3B shape: 384.0 against 382.0 tok/s with 64)
   return B == 1 ? 128 : 64;
 }

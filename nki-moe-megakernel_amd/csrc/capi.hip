@@ -1095,6 +1095,11 @@ struct StepWs {
   // per call)
   unsigned* sync;
   int sync_words, layer_words, flag_words, attn_words;
+  // the joined attention launch's data-polled exchange at one token: per layer
+  // the chunk partials (O, then max / sum) and the projection partials, filled
+  // with kPollEmpty at the start of every decode call
+  float* poll;
+  long long poll_po, poll_pml, poll_y, poll_layer;
 };
 
 static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
@@ -1116,6 +1121,15 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.layer_words = w.flag_words + w.attn_words;
   w.sync_words = w.layer_words ? 64 + m->num_layers * w.layer_words : 0;
   w.sync = w.sync_words ? c.take<unsigned>(w.sync_words) : nullptr;
+  w.poll = nullptr;
+  w.poll_po = w.poll_pml = w.poll_y = w.poll_layer = 0;
+  if (B == 1 && w.attn_words > 0) {
+    w.poll_po = (long long)m->nq * w.attn.n_chunks * m->d;
+    w.poll_pml = (long long)m->nq * w.attn.n_chunks * 2;
+    w.poll_y = (long long)attn_join_y_parts(m->nq) * m->H;
+    w.poll_layer = w.poll_po + w.poll_pml + w.poll_y;
+    w.poll = c.take<float>((size_t)(w.poll_layer * m->num_layers));
+  }
   return w;
 }
 
@@ -1299,6 +1313,9 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
   const bool fused_moe = joined_experts_planned(m, B) && w.flag_words > 0;
   const bool join_attn = g_inlaunch_sync && !prefill && w.attn_words > 0 && o_kgrid <= 1;
   if (fused_moe || join_attn) MKD_TRY(sync_clear_launch(w.sync, w.sync_words, s), "clear sync words");
+  if (join_attn && w.poll)
+    MKD_TRY(fill_u32_launch(reinterpret_cast<uint32_t*>(w.poll), w.poll_layer * m->num_layers, kPollEmpty, s),
+            "fill the attention exchange");
   for (int l = 0; l < m->num_layers; ++l) {
     const int wl = m->window ? m->window[l] : 0;
     mkd_attention_args ap;
@@ -1357,6 +1374,12 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
       ja.rresid = w.r; ja.rhnorm = w.nbf;
       ja.reps = m->eps; ja.rinv_h = 1.0f / (float)ha;
       ja.E = m->E; ja.rx_f32 = oss ? 0 : 1;
+      if (w.poll) {
+        float* pl = w.poll + (size_t)l * w.poll_layer;
+        ja.poll_po = pl;
+        ja.poll_pml = pl + w.poll_po;
+        ja.poll_y = pl + w.poll_po + w.poll_pml;
+      }
     }
     if (int rc = attention_core(&ap, w.attn, position_ids, nullptr, s, w.oparts, o_kgrid,
                                 fuse_qn ? &qn : nullptr, prefill && !wl,

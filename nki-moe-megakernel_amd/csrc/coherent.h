@@ -65,6 +65,18 @@ MKD_DEV void coh_publish(unsigned* flag) {
   if (threadIdx.x == 0) coh_store(flag, 1u);
 }
 
+// A data-polling loop's bound (same as coh_wait_all's): true once *err is set
+// (another wait already gave up) or after kCohSpinLimit polls, when it sets
+// *err itself; the caller then goes on with whatever it read.
+MKD_DEV bool coh_poll_giveup(unsigned it, unsigned* err) {
+  if (coh_load(err) != 0u) return true;
+  if (it >= kCohSpinLimit) {
+    if ((threadIdx.x & 63) == 0) coh_store(err, 1u);
+    return true;
+  }
+  return false;
+}
+
 // One wave waits until the n flag words fl[0..n) are all non-zero.  Bounded:
 // after kCohSpinLimit polls (tens of milliseconds) it sets *err and gives up, and
 // a wave that finds *err already set does not wait at all, so the grid always

@@ -324,7 +324,18 @@ struct AttnJoinArgs {
   // the chunk partials inside the projection blocks (no combine blocks), which
   // then write o_parts K-split partials of y ([o_parts][B][N]); else 0 and 1
   int mp, o_parts;
+  // data-polled exchange (one token, merge + projection form): when poll_po is
+  // set, the chunk partials go to poll_po / poll_pml and the projection's
+  // partials to poll_y -- buffers of this launch alone, filled with kPollEmpty
+  // beforehand -- and the consumers poll the data words themselves instead of
+  // waiting for flags and then loading (one coherent round trip per stage fewer)
+  float* poll_po;
+  float* poll_pml;
+  float* poll_y;
+  int dpoll;                  // set by attn_join_launch
 };
+constexpr uint32_t kPollEmpty = 0xffffffffu;   // a NaN no bf16-derived fp32 math produces
+hipError_t fill_u32_launch(uint32_t* p, long long n, uint32_t v, hipStream_t s);
 // size of y for attn_join_launch: K-split partials of the merge + projection form
 int attn_join_y_parts(int nq);
 int attn_join_flag_words(int B, int nq, int nkv, int n_chunks, int N);

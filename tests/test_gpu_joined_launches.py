@@ -16,7 +16,10 @@ top-8, I 768), 3 layers chained:
   (router rows checked against the oracle router, near-tie flips against the
   oracle's logit gap), within 2e-2;
 * bit-identical from call to call and across graph replays (the flag words are
-  cleared at the start of every call, including inside a captured graph);
+  cleared, and at one token the data-polled exchange buffers filled with their
+  empty marker, at the start of every call, including inside a captured graph);
+* at one token up to 8192 positions: the merge + projection blocks read a head's
+  chunk partials in several batches;
 * no in-launch wait timed out."""
 import pytest
 import torch
@@ -74,7 +77,7 @@ def _run(model, x, kcs, vcs, pos, dev):
     return y.cpu(), [model.kv_mgr.k(l).cpu() for l in range(len(kcs))], model.route_log(x.shape[0])
 
 
-@pytest.mark.parametrize("B,S", [(1, 1024), (1, 4096), (4, 2048)])
+@pytest.mark.parametrize("B,S", [(1, 1024), (1, 4096), (1, 8192), (4, 2048)])
 def test_joined_launches_vs_separate_and_oracle(mk, dev, restore_path, B, S):
     Q = restore_path
     print(f"joined launches: B={B} S={S}", flush=True)
