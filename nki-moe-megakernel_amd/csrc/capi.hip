@@ -301,7 +301,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
              MoeWs& w, hipStream_t s, bool do_finalize = true, int wfmt = 0,
              const void* gu_scales = nullptr, const void* dn_scales = nullptr, bool tiled = false,
              const RouterArgs* sel = nullptr, unsigned* fused_flags = nullptr,
-             unsigned* fused_err = nullptr) {
+             unsigned* fused_err = nullptr, uint16_t* poll_h = nullptr) {
   if (sel && (idx || wfmt || tiled)) return MKD_ERR_INVALID;
   if (fused_flags && !sel) return MKD_ERR_INVALID;
   if (idx)  // otherwise the router stage already built the expert groups
@@ -400,6 +400,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
     f.dn.bias = dn_bias; f.dn.bias_group_stride = H;
     f.r = *sel;
     f.flags = fused_flags; f.err = fused_err;
+    f.poll_h = T == 1 ? poll_h : nullptr;
     const int ps = prof_begin(MKD_KCLASS_MOE_GATE_UP, s);
     MKD_TRY(moe_fused_launch(f, gmax, s), "moe router select + gate_up + down");
     prof_end(ps, s);
@@ -1099,7 +1100,7 @@ struct StepWs {
   // the chunk partials (O, then max / sum) and the projection partials, filled
   // with kPollEmpty at the start of every decode call
   float* poll;
-  long long poll_po, poll_pml, poll_y, poll_layer;
+  long long poll_po, poll_pml, poll_y, poll_h, poll_layer;   // words per layer
 };
 
 static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
@@ -1122,12 +1123,15 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.sync_words = w.layer_words ? 64 + m->num_layers * w.layer_words : 0;
   w.sync = w.sync_words ? c.take<unsigned>(w.sync_words) : nullptr;
   w.poll = nullptr;
-  w.poll_po = w.poll_pml = w.poll_y = w.poll_layer = 0;
-  if (B == 1 && w.attn_words > 0) {
-    w.poll_po = (long long)m->nq * w.attn.n_chunks * m->d;
-    w.poll_pml = (long long)m->nq * w.attn.n_chunks * 2;
-    w.poll_y = (long long)attn_join_y_parts(m->nq) * m->H;
-    w.poll_layer = w.poll_po + w.poll_pml + w.poll_y;
+  w.poll_po = w.poll_pml = w.poll_y = w.poll_h = w.poll_layer = 0;
+  if (B == 1 && (w.attn_words > 0 || w.flag_words > 0)) {
+    if (w.attn_words > 0) {
+      w.poll_po = (long long)m->nq * w.attn.n_chunks * m->d;
+      w.poll_pml = (long long)m->nq * w.attn.n_chunks * 2;
+      w.poll_y = (long long)attn_join_y_parts(m->nq) * m->H;
+    }
+    if (w.flag_words > 0) w.poll_h = ((long long)m->K * m->I + 1) / 2;   // h rows, bf16 pairs
+    w.poll_layer = w.poll_po + w.poll_pml + w.poll_y + w.poll_h;
     w.poll = c.take<float>((size_t)(w.poll_layer * m->num_layers));
   }
   return w;
@@ -1313,9 +1317,9 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
   const bool fused_moe = joined_experts_planned(m, B) && w.flag_words > 0;
   const bool join_attn = g_inlaunch_sync && !prefill && w.attn_words > 0 && o_kgrid <= 1;
   if (fused_moe || join_attn) MKD_TRY(sync_clear_launch(w.sync, w.sync_words, s), "clear sync words");
-  if (join_attn && w.poll)
+  if ((join_attn || fused_moe) && w.poll)
     MKD_TRY(fill_u32_launch(reinterpret_cast<uint32_t*>(w.poll), w.poll_layer * m->num_layers, kPollEmpty, s),
-            "fill the attention exchange");
+            "fill the data-polled exchange buffers");
   for (int l = 0; l < m->num_layers; ++l) {
     const int wl = m->window ? m->window[l] : 0;
     mkd_attention_args ap;
@@ -1374,7 +1378,7 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
       ja.rresid = w.r; ja.rhnorm = w.nbf;
       ja.reps = m->eps; ja.rinv_h = 1.0f / (float)ha;
       ja.E = m->E; ja.rx_f32 = oss ? 0 : 1;
-      if (w.poll) {
+      if (w.poll && w.poll_po) {
         float* pl = w.poll + (size_t)l * w.poll_layer;
         ja.poll_po = pl;
         ja.poll_pml = pl + w.poll_po;
@@ -1484,7 +1488,8 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
                               tile_offsets_ok((long long)B * m->K, m->I, m->H, m->I),
                           defer_sel ? &sel : nullptr,
                           fused_moe ? lsync : nullptr,
-                          fused_moe ? w.sync : nullptr))
+                          fused_moe ? w.sync : nullptr,
+                          fused_moe && w.poll_h ? reinterpret_cast<uint16_t*>(w.poll + (size_t)l * w.poll_layer + w.poll_po + w.poll_pml + w.poll_y) : nullptr))
       return rc;
     // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention
     // norm (with fuse_qn: the next QKV kernel does both; after the last layer the

@@ -351,7 +351,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
     b.grp_expert = s_gexp; b.grp_count = s_gcnt; b.grp_offset = s_goff;
     b.pair_row = s_ptok; b.pair_out_row = s_pslot;
     frag_body<2, 1, false, EPI_SWIGLU_BF16, true>(b, bid % f.n_gu, bid / f.n_gu, 0);
-    coh_publish(f.flags + bid);
+    if (!f.poll_h) coh_publish(f.flags + bid);
     return;
   }
   // ---- down role ----
@@ -375,17 +375,34 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   }
   const int c = lane & 15;
   const int prow = c < count ? s_pslot[base + c] : -1;   // h row and output row of the column
-  if (wave == 0) coh_wait_all(f.flags + g * f.n_gu, f.n_gu, f.err);
-  __syncthreads();
+  if (!f.poll_h) {
+    if (wave == 0) coh_wait_all(f.flags + g * f.n_gu, f.n_gu, f.err);
+    __syncthreads();
+  }
   // the group's h rows (count <= kFusedMaxRows, K = 64 NFD) into LDS with one
-  // device-coherent 16-byte load per thread, then the B operands from LDS
+  // device-coherent 16-byte load per thread, then the B operands from LDS; with
+  // the data-polled h, loaded until no 16-bit word reads 0xffff (the empty
+  // marker; bounded like the flag waits)
   {
     const __amdgpu_buffer_rsrc_t hr = coh_rsrc(d.x);
     const int per_row = d.K / 8;                       // 16-byte pieces per row
-    for (int i = threadIdx.x; i < count * per_row; i += blockDim.x) {
-      const int rr = i / per_row, pc = i - rr * per_row;
-      const int row = s_pslot[base + rr];
-      s_h[rr][pc] = coh_ld16(hr, (int)(((long long)row * d.ldx + pc * 8) * 2));
+    for (unsigned it = 0;; ++it) {
+      int miss = 0;
+      for (int i = threadIdx.x; i < count * per_row; i += blockDim.x) {
+        const int rr = i / per_row, pc = i - rr * per_row;
+        const int row = s_pslot[base + rr];
+        const u32x4_t v = coh_ld16(hr, (int)(((long long)row * d.ldx + pc * 8) * 2));
+        s_h[rr][pc] = v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) miss |= (v[e] & 0xffffu) == 0xffffu || (v[e] >> 16) == 0xffffu;
+      }
+      if (!f.poll_h) break;
+      if (!__syncthreads_or(miss)) break;
+      if (it >= kCohSpinLimit) {
+        if (threadIdx.x == 0) coh_store(f.err, 1u);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
     }
   }
   __syncthreads();
@@ -501,6 +518,10 @@ hipError_t moe_fused_launch(MoeFusedArgs f, int groups_max, hipStream_t s) {
       !r.pair_token || !r.pair_slot || !a.grp_expert || !f.flags || !f.err || groups_max < 1 ||
       groups_max > kSelMaxPairs || (f.dn.ldx & 7) || (f.dn.ldy & 3))
     return hipErrorInvalidValue;
+  if (f.poll_h) {   // h goes to the launch's own pre-filled buffer
+    f.gu.y = f.poll_h;
+    f.dn.x = f.poll_h;
+  }
   f.n_gu = a.N / 32;
   f.ngu = f.n_gu * groups_max;
   // 128 output rows per down block where that makes the whole grid resident at

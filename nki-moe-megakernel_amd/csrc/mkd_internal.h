@@ -397,6 +397,11 @@ struct MoeFusedArgs {
   unsigned* flags;
   unsigned* err;
   int n_gu, ngu, ndb;   // set by moe_fused_launch
+  // data-polled h (one token): when set, the gate/up blocks write h here -- a
+  // buffer of this launch alone, filled with kPollEmpty beforehand -- and set no
+  // flags; the down blocks poll their h row itself (one coherent round trip
+  // fewer than a flag wait followed by the loads)
+  uint16_t* poll_h;
 };
 bool moe_fused_supported(int T, int K, int E, int H, int I);
 int moe_fused_flag_words(int T, int K, int E, int I);
