@@ -277,7 +277,23 @@ typedef struct {
   const void* q_norm_post;
   const void* k_norm_post;
   float qk_post_eps;
+  /* KV cache format (0: bf16, K as [.., S_max, d]).  MKD_KV_FP8: both caches
+   * hold float8 e4m3 codes, one byte per element (k_scale / v_scale of
+   * attention_block_tkg.py:133-134, :213-218, :749-754): a new k row is stored
+   * as e4m3(clip(k * k_scale, -240, 240)) with round to nearest even
+   * (_quantize_to_fp8, :1694-1737), v likewise with v_scale, and the attention
+   * uses the stored values as they are -- no dequantisation (attention_tkg.py:
+   * 749-821); the new tokens attend their own quantised rows.
+   * MKD_KV_K_TRANSPOSED: the flat K cache is [B, nkv, d, S_max]
+   * (K_cache_transposed, attention_block_tkg.py:112, :197-202; not with a
+   * block table).  V keeps [.., S_max, d].  Neither with a ring cache.
+   * k_scale / v_scale: one fp32 value each in device memory (MKD_KV_FP8). */
+  int kv_format;
+  const float* k_scale;
+  const float* v_scale;
 } mkd_attention_args;
+#define MKD_KV_FP8 1
+#define MKD_KV_K_TRANSPOSED 2
 size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S_max);
 /* The same for s_tkg new tokens per sequence (mkd_attention_args::s_tkg). */
 size_t mkd_attention_workspace_bytes_tkg(int B, int s_tkg, int H, int nq, int nkv, int d, int S_max);

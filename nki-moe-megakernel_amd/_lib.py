@@ -70,7 +70,12 @@ class AttentionArgs(C.Structure):
         ("active_blocks_table", vp), ("blocks_per_seq", i32), ("block_len", i32), ("num_blocks", i32),
         ("hidden_actual", i32), ("window", i32), ("s_tkg", i32),
         ("q_norm_post", vp), ("k_norm_post", vp), ("qk_post_eps", f32),
+        ("kv_format", i32), ("k_scale", vp), ("v_scale", vp),
     ]
+
+
+KV_FP8 = 1            # MKD_KV_FP8
+KV_K_TRANSPOSED = 2   # MKD_KV_K_TRANSPOSED
 
 
 class Qwen3Model(C.Structure):

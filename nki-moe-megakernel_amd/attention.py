@@ -58,24 +58,37 @@ def attention_block_tkg(
     close the window as in attention_tkg.py), and token s is written at
     kv_cache_update_idx[b] + s (attention_block_tkg.py:1365-1470; a global row of
     a block cache).  Pre- and post-RoPE per-head Q/K RMSNorm (attention_block_tkg.py:
-    895-910; absent weights are ones).  Flat or block caches, no quantisation.  Other reference
-    options raise NotImplementedError.  enable_fa_s_prior_tiling is a
-    scheduling hint (the GPU path always tiles the KV length).
+    895-910; absent weights are ones).
+
+    K_cache_transposed (attention_block_tkg.py:112, :197-202): the flat K cache
+    is [B, d, S_max] (or [B, kv_heads, d, S_max]); V keeps [B, S_max, d]; not
+    with a block table (ValueError, as the reference).
+
+    FP8 KV cache (k_scale and v_scale both given, attention_block_tkg.py:133-134,
+    :213-218, :749-754): K_cache / V_cache are float8 e4m3 (torch.float8_e4m3fn,
+    or uint8 tensors of the codes); each scale is one value ((1, 1) or (PMAX, 1)
+    replicated: element 0 is read, on the device); the new rows are stored as
+    e4m3(clip(k * k_scale, +-240)) (_quantize_to_fp8, :1694-1737) and the
+    attention uses the stored values as they are, the new tokens' own rows
+    included -- the caller folds any dequantisation into softmax_scale / W_out.
+
+    Quantised QKV / output projections and the remaining reference options raise
+    NotImplementedError.  enable_fa_s_prior_tiling is a scheduling hint (the GPU
+    path always tiles the KV length).
     """
     if KVDP != 1:
         raise NotImplementedError("KV data parallelism spans several devices; one GPU only")
     if K_cache_transposed and active_blocks_table is not None:
         raise ValueError("K_cache_transposed must be False for block KV cache")
-    if K_cache_transposed:
-        raise NotImplementedError("K_cache_transposed=True is not supported (K is stored [.., S, d])")
     if transposed_out or out_in_sb or sbm is not None:
         raise NotImplementedError("transposed/SBUF outputs have no GPU equivalent")
     if skip_attention:
         raise NotImplementedError("skip_attention is a test hook of the reference")
     if quantization_type_qkv not in (None, QuantizationType.NONE) or \
-            quantization_type_out not in (None, QuantizationType.NONE) or \
-            k_scale is not None or v_scale is not None:
-        raise NotImplementedError("quantized QKV / output projection / FP8 KV are not supported")
+            quantization_type_out not in (None, QuantizationType.NONE):
+        raise NotImplementedError("quantized QKV / output projections are not supported")
+    # KV quantisation only when both scales are given (attention_block_tkg.py:749-754)
+    kv_quant = k_scale is not None and v_scale is not None
     if not rope_contiguous_layout and cos is not None:
         raise NotImplementedError("interleaved RoPE layout is not supported")
     L.require_gpu(X, W_qkv, K_cache, V_cache, attention_mask)
@@ -87,8 +100,14 @@ def attention_block_tkg(
     d = V_cache.shape[-1]
     if d % 2:
         raise ValueError(f"d_head must be even, got {d}")
-    if tuple(K_cache.shape) != tuple(V_cache.shape):
-        raise ValueError(f"KV cache shape mismatch: K={tuple(K_cache.shape)} vs V={tuple(V_cache.shape)}")
+    # a transposed K cache is compared in V's layout
+    k_shape = tuple(K_cache.shape[:-2]) + (K_cache.shape[-1], K_cache.shape[-2]) \
+        if K_cache_transposed else tuple(K_cache.shape)
+    if K_cache_transposed and K_cache.dim() < 3:
+        raise ValueError(f"transposed K_cache must be [B, d, S_max], got {tuple(K_cache.shape)}")
+    if k_shape != tuple(V_cache.shape):
+        raise ValueError(f"KV cache shape mismatch: K={tuple(K_cache.shape)} vs V={tuple(V_cache.shape)}"
+                         + (" (K transposed)" if K_cache_transposed else ""))
     block = active_blocks_table is not None
     if block:
         if K_cache.dim() == 3:
@@ -102,13 +121,13 @@ def attention_block_tkg(
             raise ValueError(f"active_blocks_table must be [B={B}, num_active_blocks], got {tuple(active_blocks_table.shape)}")
         n_active = active_blocks_table.shape[1]
         S_max = n_active * blk_len
-    else:
-        if K_cache.dim() == 3:
+    else:   # V_cache [B, S_max, d] or [B, kv_heads, S_max, d] (K matches it, maybe transposed)
+        if V_cache.dim() == 3:
             nkv = 1
-            S_max = K_cache.shape[1]
-        elif K_cache.dim() == 4:
-            nkv = K_cache.shape[1]
-            S_max = K_cache.shape[2]
+            S_max = V_cache.shape[1]
+        elif V_cache.dim() == 4:
+            nkv = V_cache.shape[1]
+            S_max = V_cache.shape[2]
         else:
             raise ValueError(f"K_cache must be 3-D or 4-D, got {tuple(K_cache.shape)}")
         if K_cache.shape[0] != B:
@@ -133,8 +152,20 @@ def attention_block_tkg(
         raise ValueError(f"cos shape mismatch: expected ({d // 2}, {B}, {S_tkg}), got {tuple(cos.shape)}")
     if update_cache and kv_cache_update_idx is None:
         raise ValueError("update_cache=True needs kv_cache_update_idx")
-    if K_cache.dtype != torch.bfloat16 or X.dtype != torch.bfloat16:
-        raise ValueError("X and the KV caches must be bfloat16")
+    if X.dtype != torch.bfloat16:
+        raise ValueError("X must be bfloat16")
+    fp8_types = (torch.float8_e4m3fn, torch.uint8)
+    if kv_quant:
+        if K_cache.dtype not in fp8_types or V_cache.dtype not in fp8_types:
+            raise ValueError(f"KV quantization requires float8_e4m3 K_cache / V_cache, got "
+                             f"{K_cache.dtype} / {V_cache.dtype}")
+        for nm, sc in (("k_scale", k_scale), ("v_scale", v_scale)):
+            if sc.numel() < 1 or sc.dim() != 2 or sc.shape[1] != 1:
+                raise ValueError(f"{nm} must be (1, 1) or (PMAX, 1), got {tuple(sc.shape)}")
+            if sc.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+                raise ValueError(f"{nm} dtype must be float32 / float16 / bfloat16, got {sc.dtype}")
+    elif K_cache.dtype != torch.bfloat16 or V_cache.dtype != torch.bfloat16:
+        raise ValueError("the KV caches must be bfloat16 (float8_e4m3 needs k_scale and v_scale)")
 
     dev = X.device
     wqkv = packing.packed_cached(W_qkv, packing.pack_in_out)
@@ -174,6 +205,10 @@ def attention_block_tkg(
         table = torch.where((t64 < 0) | (t64 >= num_blocks), torch.full_like(t64, -1), t64) \
             .to(torch.int32).contiguous()
     sink_f = sink.reshape(-1).float().contiguous() if sink is not None else None
+    ks = vs = None
+    if kv_quant:   # element 0 of each scale, as fp32 on the device (no host round trip)
+        ks = k_scale.reshape(-1)[:1].float().contiguous()
+        vs = v_scale.reshape(-1)[:1].float().contiguous()
     bqkv = bias_qkv.reshape(-1).to(torch.bfloat16).contiguous() if bias_qkv is not None else None
     bout = bias_out.reshape(-1).to(torch.bfloat16).contiguous() if bias_out is not None else None
     out = torch.empty(B * S_tkg, H_out if W_out is not None else nq * d, dtype=torch.bfloat16, device=dev)
@@ -191,7 +226,9 @@ def attention_block_tkg(
         active_blocks_table=L.ptr(table), blocks_per_seq=table.shape[1] if block else 0,
         block_len=blk_len if block else 0, num_blocks=num_blocks if block else 0, s_tkg=S_tkg,
         q_norm_post=L.ptr(qp), k_norm_post=L.ptr(kp),
-        qk_post_eps=float(rmsnorm_QK_post_rope_eps) if rmsnorm_QK_post_rope_enabled else 0.0)
+        qk_post_eps=float(rmsnorm_QK_post_rope_eps) if rmsnorm_QK_post_rope_enabled else 0.0,
+        kv_format=(L.KV_FP8 if kv_quant else 0) | (L.KV_K_TRANSPOSED if K_cache_transposed else 0),
+        k_scale=L.ptr(ks), v_scale=L.ptr(vs))
     lib = L.load()
     ws = torch.zeros(max(lib.mkd_attention_workspace_bytes_tkg(B, S_tkg, H, nq, nkv, d, S_max), 256),
                      dtype=torch.uint8, device=dev)

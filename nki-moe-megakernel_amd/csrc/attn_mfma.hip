@@ -1233,6 +1233,36 @@ hipError_t attn_combine_launch(const AttnArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+hipError_t attn_prep_launch(const AttnArgs& a, int rope_mode, hipStream_t s) {
+  if (!a.prep) return hipErrorInvalidValue;
+  const int gqa = a.nq / a.nkv;
+#define MKD_PREP(D, G) \
+  hipLaunchKernelGGL((attn_prep_kernel<D, G>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode)
+  if (a.d == 128) {
+    switch (gqa) {
+      case 1: MKD_PREP(128, 1); break;
+      case 2: MKD_PREP(128, 2); break;
+      case 4: MKD_PREP(128, 4); break;
+      case 8: MKD_PREP(128, 8); break;
+      case 16: MKD_PREP(128, 16); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else if (a.d == 64) {
+    switch (gqa) {
+      case 1: MKD_PREP(64, 1); break;
+      case 2: MKD_PREP(64, 2); break;
+      case 4: MKD_PREP(64, 4); break;
+      case 8: MKD_PREP(64, 8); break;
+      case 16: MKD_PREP(64, 16); break;
+      default: return hipErrorInvalidValue;
+    }
+  } else {
+    return hipErrorInvalidValue;
+  }
+#undef MKD_PREP
+  return hipGetLastError();
+}
+
 hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s) {
   const int gqa = a.nq / a.nkv;
   if (a.d == 128) {

@@ -863,8 +863,15 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     a.prep = w.prep;
     a.prefill = 1;
   }
+  // fp8 / transposed-K caches: the option path of attn_kvfmt.hip
+  a.kv_fp8 = (p->kv_format & MKD_KV_FP8) != 0;
+  a.k_transposed = (p->kv_format & MKD_KV_K_TRANSPOSED) != 0;
+  a.k_scale = p->k_scale;
+  a.v_scale = p->v_scale;
+  const bool kvfmt = a.kv_fp8 || a.k_transposed;
+  if (kvfmt) a.prep = w.prep;
   const int rope_mode = p->cos ? 1 : (inv_freq ? 2 : 0);
-  if (join && o_parts && o_kgrid <= 1 && p->w_out_packed && attn_join_supported(a, p->H_out)) {
+  if (join && !kvfmt && o_parts && o_kgrid <= 1 && p->w_out_packed && attn_join_supported(a, p->H_out)) {
     AttnJoinArgs j = *join;
     j.w_out = static_cast<const uint16_t*>(p->w_out_packed);
     j.bias = static_cast<const uint16_t*>(p->bias_out);
@@ -879,12 +886,24 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   // the caller left its router to the joined launch
   MKD_REQUIRE(!(join && join->rw), MKD_ERR_UNSUPPORTED,
               "attention: the joined launch with its router stage does not fit this layer");
-  {  // q/k norm + RoPE and split-K attention in one launch
+  if (kvfmt) {
+    MKD_REQUIRE(!prefill && a.window == 0, MKD_ERR_UNSUPPORTED,
+                "attention: fp8 / transposed-K caches are served by the operator path only");
     const int ps = prof_begin(MKD_KCLASS_ATTN, s);
-    MKD_TRY(attn_decode_launch(a, rope_mode, s), "attention");
+    MKD_TRY(attn_kvfmt_launch(a, rope_mode, s), "attention (fp8 / transposed-K cache)");
     prof_end(ps, s);
+    AttnArgs ac = a;
+    ac.update_cache = 0;               // the new rows are stored below, in the cache's format
+    MKD_TRY(attn_combine_launch(ac, s), "attention combine");
+    MKD_TRY(attn_kvfmt_store_launch(a, s), "kv store (fp8 / transposed-K cache)");
+  } else {
+    {  // q/k norm + RoPE and split-K attention in one launch
+      const int ps = prof_begin(MKD_KCLASS_ATTN, s);
+      MKD_TRY(attn_decode_launch(a, rope_mode, s), "attention");
+      prof_end(ps, s);
+    }
+    MKD_TRY(attn_combine_launch(a, s), "attention combine + kv scatter");
   }
-  MKD_TRY(attn_combine_launch(a, s), "attention combine + kv scatter");
   // 5. output projection
   if (p->w_out_packed) {
     GemmArgs o = dense_args(p->w_out_packed, w.attn, p->nq * p->d, p->H_out, p->nq * p->d, rows,
@@ -940,6 +959,15 @@ static int validate_attn(const mkd_attention_args* p) {
     if (int rc = check_gemm_dims(p->H_out, p->nq * p->d, 1)) return rc;
   }
   MKD_REQUIRE(!p->residual || p->w_out_packed, MKD_ERR_INVALID, "attention: residual needs W_out");
+  MKD_REQUIRE((p->kv_format & ~(MKD_KV_FP8 | MKD_KV_K_TRANSPOSED)) == 0, MKD_ERR_INVALID,
+              "attention: unknown kv_format bits 0x%x", p->kv_format);
+  if (p->kv_format) {
+    MKD_REQUIRE(p->window == 0, MKD_ERR_UNSUPPORTED, "attention: fp8 / transposed-K caches with a ring cache");
+    MKD_REQUIRE(!(p->kv_format & MKD_KV_K_TRANSPOSED) || !p->active_blocks_table, MKD_ERR_INVALID,
+                "attention: a transposed K cache must be flat (attention_block_tkg.py:197-202)");
+    MKD_REQUIRE(!(p->kv_format & MKD_KV_FP8) || (p->k_scale && p->v_scale), MKD_ERR_NULL,
+                "attention: fp8 KV needs k_scale and v_scale");
+  }
   MKD_REQUIRE(!p->mask || p->mask_s_ctx >= 1, MKD_ERR_INVALID, "attention: mask_s_ctx must be >= 1");
   MKD_REQUIRE(!(p->cos && !p->sin), MKD_ERR_NULL, "attention: cos without sin");
   if (p->active_blocks_table) {

@@ -289,11 +289,28 @@ struct AttnArgs {
   const uint16_t* q_norm_post;
   const uint16_t* k_norm_post;
   float qk_post_eps;
+  // KV cache formats of the operator's option path (attn_kvfmt.hip; flat or
+  // block caches, no ring, no prefill).  kv_fp8: both caches hold float8 e4m3
+  // codes (one byte per element, the element offsets above unchanged); a new
+  // row is stored as e4m3(clip(x * k_scale, +-240)) (v_scale for V) and the
+  // attention uses the stored values as they are.  k_transposed: the flat K
+  // cache is [B, nkv, d, S_max] (element (t, i) at i * S_max + t of its head).
+  int kv_fp8, k_transposed;
+  const float* k_scale;       // fp32 scalars in device memory (kv_fp8)
+  const float* v_scale;
 };
 // rope_mode: 0 none, 1 cos/sin tables, 2 from pos and inv_freq
 hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s);
 hipError_t attn_combine_launch(const AttnArgs& a, hipStream_t s);
 int attn_chunk_for(int B, int nkv, int S_max);   // positions per attention block (64/128/256)
+// q / k / v head preparation of every (row, kv head) into a.prep (required)
+hipError_t attn_prep_launch(const AttnArgs& a, int rope_mode, hipStream_t s);
+// Option-path attention over fp8 / transposed-K caches (attn_kvfmt.hip): the
+// head preparation, then split-K chunk partials in the layout attn_combine
+// merges; the new rows are stored afterwards by attn_kvfmt_store_launch, after
+// the combine (kernels run in stream order, so every chunk has read the cache).
+hipError_t attn_kvfmt_launch(const AttnArgs& a, int rope_mode, hipStream_t s);
+hipError_t attn_kvfmt_store_launch(const AttnArgs& a, hipStream_t s);
 // Attention, chunk combine and output projection in one launch (attn_mfma.hip,
 // attn_joined_kernel): the chunk blocks, then the combine blocks, then the
 // projection blocks of one grid, each stage waiting on the flags of the blocks

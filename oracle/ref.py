@@ -503,11 +503,25 @@ def block_kv_to_flat(cache: torch.Tensor, table: torch.Tensor) -> torch.Tensor:
     return out
 
 
+KV_FP8_MAX = 240.0   # _FP8_E4M3_MAX of the reference's float8_e4m3 (attention_block_tkg.py:1690)
+
+
+def kv_fp8_quant(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """FP8 KV quantisation (attention_block_tkg.py:1694-1737 _quantize_to_fp8):
+    e4m3(clip(x * scale, -240, 240)), round to nearest even, as a
+    torch.float8_e4m3fn tensor.  The reference's float8_e4m3 reserves the top
+    exponent for infinities (largest finite 240); on [-240, 240] its codes and
+    values equal float8_e4m3fn's, which torch implements."""
+    y = (x.float() * float(scale)).clamp(-KV_FP8_MAX, KV_FP8_MAX)
+    return y.to(torch.float8_e4m3fn)
+
+
 def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
                         q_norm_w, k_norm_w, qk_eps, cos, sin, K_cache, V_cache,
                         attention_mask, sink, update_cache, kv_cache_update_idx,
                         W_out, bias_out, softmax_scale=None, q_norm_post_w=None,
-                        k_norm_post_w=None, qk_post_eps=None):
+                        k_norm_post_w=None, qk_post_eps=None, k_scale=None, v_scale=None,
+                        K_cache_transposed=False):
     """Generic attention block (fp32 math, kv_heads = 1 as in the reference :353).
 
     X [B, S_tkg, H]; W_qkv [H, d*(nq+2)] packed Q | K | V (:363-384);
@@ -522,6 +536,13 @@ def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
     kv_cache_update_idx[b] + s after attention, uint32 max = skip
     (attention_block_tkg.py:1144-1470); output projection
     attn [B*S, nq*d] @ W_out [nq*d, H] (+ bias).
+
+    K_cache_transposed (:112, :197-202): K_cache is [B, d, S_max].  k_scale and
+    v_scale (floats) both given (:749-754): the caches are float8_e4m3fn, the
+    new k / v rows are taken in bf16 (their io dtype, :979-1084), quantised by
+    kv_fp8_quant, written as such, and the attention uses the stored values
+    as they are, the new tokens' own quantised rows included (:1073-1084;
+    attention_tkg.py:749-821).
     Returns (out [B*S_tkg, H] fp32, K_cache, V_cache).
     """
     B, S, H = X.shape
@@ -550,8 +571,14 @@ def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
         k = head_rmsnorm(k, k_norm_post_w.reshape(-1), qk_post_eps)
     scale = softmax_scale if softmax_scale is not None else 1.0 / math.sqrt(d)
     S_ctx = attention_mask.shape[0]
-    Kc = K_cache.reshape(K_cache.shape[0], -1, d) if K_cache.dim() == 4 else K_cache
+    # [B, S_max, d] views (a transposed K cache read through its transpose)
+    Kc = K_cache.transpose(1, 2) if K_cache_transposed else \
+        (K_cache.reshape(K_cache.shape[0], -1, d) if K_cache.dim() == 4 else K_cache)
     Vc = V_cache.reshape(V_cache.shape[0], -1, d) if V_cache.dim() == 4 else V_cache
+    kv_quant = k_scale is not None and v_scale is not None
+    if kv_quant:   # the new rows as stored
+        k = kv_fp8_quant(k.to(torch.bfloat16), k_scale).float()
+        v = kv_fp8_quant(v.to(torch.bfloat16), v_scale).float()
     n_prior = S_ctx - S
     out = torch.zeros(B, S, nq, d)
     for b in range(B):

@@ -1,0 +1,244 @@
+"""GPU parity of attention_block_tkg's optional KV cache formats against the CPU
+oracle (through the C ABI): the FP8 e4m3 KV cache (k_scale / v_scale,
+attention_block_tkg.py:133-134, :749-754, :1694-1737) and the transposed K
+cache (K_cache_transposed, :112, :197-202), flat and block caches, one and
+several new tokens per sequence.
+
+Tolerances: output max-abs-rel <= 2e-2 (the oracle runs the same stored fp8
+values in fp32).  Written cache rows: exactly the target rows change; bf16 rows
+within 2e-2 of the oracle's; e4m3 codes equal the oracle's except where the
+GPU's bf16 k / v differs from the oracle's fp32 one by a rounding and lands on
+the other side of an e4m3 rounding boundary -- such codes differ by one step
+(<= 1/8 relative, or one subnormal quantum 2^-9) and are at most 3 % of a row.
+"""
+import pytest
+import torch
+
+from conftest import max_abs_rel
+from oracle import ref
+
+pytestmark = pytest.mark.gpu
+
+TOL = 2e-2
+
+
+def bf(t):
+    return t.to(torch.bfloat16)
+
+
+def _rope_rows(B, S, P, d):
+    cos, sin = ref.rope_cos_sin((torch.arange(S)[None, :] + P + 3 * torch.arange(B)[:, None]).reshape(-1), d, 1e6)
+    cos_r = cos[:, :d // 2].reshape(B, S, d // 2).permute(2, 0, 1).contiguous()   # [d/2, B, S]
+    sin_r = sin[:, :d // 2].reshape(B, S, d // 2).permute(2, 0, 1).contiguous()
+    return cos_r, sin_r
+
+
+def _mask(g, P, B, nq, S, keep=0.8):
+    """[P + S, B, nq, S]: random prior slots, then causal among the S new tokens."""
+    prior = (torch.rand(P, B, nq, S, generator=g) < keep).to(torch.bfloat16)
+    causal = (torch.arange(S)[:, None] <= torch.arange(S)[None, :]).to(torch.bfloat16)
+    return torch.cat([prior, causal[:, None, None, :].expand(S, B, nq, S)], 0).contiguous()
+
+
+def _assert_codes_close(got, want):
+    """e4m3 rows: equal codes, or one rounding step apart on a small fraction."""
+    gb, wb = got.view(torch.uint8), want.view(torch.uint8)
+    diff = gb != wb
+    assert diff.float().mean().item() <= 0.03, f"{int(diff.sum())} of {diff.numel()} codes differ"
+    if diff.any():
+        gv, wv = got.float()[diff], want.float()[diff]
+        assert ((gv - wv).abs() <= wv.abs() / 8 + 2.0 ** -9 + 1e-12).all()
+
+
+def _call(mk, dev, X, W, Wo, qn, kn, cos_r, sin_r, Kg, Vg, mask, sk, upd, table, kt, ks, vs, scale):
+    from nki_moe_megakernel_amd.common_types import QuantizationType
+    return mk.attention_block_tkg(
+        X.to(dev), None, False, 1e-6, None, W.to(dev), None,
+        QuantizationType.NONE, None, None, qn is not None, 1e-6,
+        qn.to(dev) if qn is not None else None, kn.to(dev) if kn is not None else None,
+        cos_r.to(dev), sin_r.to(dev), True, False, 1e-6, None, None,
+        kt, table.to(dev) if table is not None else None, Kg, Vg, mask.to(dev),
+        sk.to(dev) if sk is not None else None, True, upd.to(dev),
+        Wo.to(dev) if Wo is not None else None, None, QuantizationType.NONE, None, None, False, False,
+        softmax_scale=scale, k_scale=ks.to(dev) if ks is not None else None,
+        v_scale=vs.to(dev) if vs is not None else None)
+
+
+@pytest.mark.parametrize("fp8,kt,B,H,nq,nkv,d,S,P,S_max,qknorm,sink,wout", [
+    (True, False, 2, 512, 8, 1, 128, 1, 300, 384, True, False, True),
+    (True, False, 3, 256, 8, 2, 64, 1, 70, 96, False, True, True),
+    (False, True, 2, 512, 8, 1, 128, 1, 500, 512, True, False, True),
+    (False, True, 2, 256, 16, 2, 64, 2, 40, 64, False, True, False),
+    (True, True, 1, 2048, 32, 4, 128, 1, 1000, 1024, True, False, True),
+    (True, False, 2, 512, 16, 2, 128, 4, 200, 256, True, True, True),
+    (True, True, 2, 256, 4, 1, 128, 3, 9, 16, False, False, True),
+])
+def test_attention_kv_formats_flat(mk, dev, fp8, kt, B, H, nq, nkv, d, S, P, S_max, qknorm, sink, wout):
+    """Flat caches ([B, S_max, d] / [B, kv_heads, S_max, d]; K as [.., d, S_max]
+    when transposed) against the oracle per kv head; the last sequence skips its
+    cache update (uint32 max)."""
+    print(f"kv formats flat: fp8={fp8} kt={kt} B={B} nq={nq} nkv={nkv} d={d} S={S} P={P}", flush=True)
+    g = torch.Generator().manual_seed(B * 131 + S * 17 + P + 7 * fp8 + 3 * kt)
+    X = bf(torch.randn(B, S, H, generator=g))
+    W = bf(0.03 * torch.randn(H, d * (nq + 2 * nkv), generator=g))
+    Wo = bf(0.03 * torch.randn(nq * d, H, generator=g)) if wout else None
+    qn = bf(1 + 0.1 * torch.randn(1, d, generator=g)) if qknorm else None
+    kn = bf(1 + 0.1 * torch.randn(1, d, generator=g)) if qknorm else None
+    k_val = 0.5 if fp8 else 1.0
+    v_val = 2.0 if fp8 else 1.0
+    # caches as [B, nkv, S_max, d] logical values
+    K4 = torch.randn(B, nkv, S_max, d, generator=g)
+    V4 = torch.randn(B, nkv, S_max, d, generator=g)
+    if fp8:
+        K4 = ref.kv_fp8_quant(K4, k_val)
+        V4 = ref.kv_fp8_quant(V4, v_val)
+        ks = torch.tensor([[k_val]], dtype=torch.float32)
+        vs = torch.full((128, 1), v_val, dtype=torch.bfloat16)     # (PMAX, 1) replicated
+    else:
+        K4, V4 = bf(K4), bf(V4)
+        ks = vs = None
+    Kst = K4.transpose(2, 3).contiguous() if kt else K4          # stored K layout
+    Kdev = Kst if nkv > 1 else Kst[:, 0]
+    Vdev = V4 if nkv > 1 else V4[:, 0]
+    cos_r, sin_r = _rope_rows(B, S, P, d)
+    mask = _mask(g, P, B, nq, S)
+    sk = torch.randn(nq, 1, generator=g) if sink else None
+    upd = torch.full((B, 1), P, dtype=torch.int64)
+    if B > 1:
+        upd[-1, 0] = 0xFFFFFFFF
+    scale = 1.0 / ((d ** 0.5) * k_val)
+    Kg, Vg = Kdev.contiguous().to(dev), Vdev.contiguous().to(dev)
+    out, K2, V2 = _call(mk, dev, X, W, Wo, qn, kn, cos_r, sin_r, Kg, Vg, mask, sk, upd, None, kt,
+                        ks, vs, scale)
+    assert K2 is Kg and V2 is Vg
+    gqa = nq // nkv
+    attn = torch.zeros(B * S, nq * d)
+    Kr, Vr = Kst.clone(), V4.clone()
+    for h in range(nkv):
+        cols = torch.cat([torch.arange(h * gqa * d, (h + 1) * gqa * d),
+                          nq * d + h * d + torch.arange(d),
+                          (nq + nkv) * d + h * d + torch.arange(d)])
+        Kh, Vh = Kr[:, h].clone(), Vr[:, h].clone()
+        o, Kh2, Vh2 = ref.attention_block_tkg(
+            X.float(), W.float()[:, cols], None, 1e-6, None,
+            qn.float() if qknorm else None, kn.float() if qknorm else None, 1e-6, cos_r, sin_r,
+            Kh, Vh, mask[:, :, h * gqa:(h + 1) * gqa].float(),
+            sk[h * gqa:(h + 1) * gqa] if sink else None, True, upd, None, None,
+            softmax_scale=scale, k_scale=k_val if fp8 else None, v_scale=v_val if fp8 else None,
+            K_cache_transposed=kt)
+        attn[:, h * gqa * d:(h + 1) * gqa * d] = o
+        Kr[:, h], Vr[:, h] = Kh2, Vh2
+    y_ref = attn @ Wo.float() if wout else attn.reshape(B, S, nq, d).permute(0, 2, 3, 1)
+    assert max_abs_rel(out, y_ref) < TOL
+    # the cache: exactly rows P .. P+S-1 of the updated sequences changed
+    Kn = Kg.cpu().reshape(Kst.shape)
+    Vn = Vg.cpu().reshape(V4.shape)
+    Kn_rows = Kn.transpose(2, 3) if kt else Kn                     # [B, nkv, S_max, d]
+    Kr_rows = Kr.transpose(2, 3) if kt else Kr
+    K0_rows = K4
+    for b in range(B):
+        ch = (Kn_rows[b].view(torch.uint8 if fp8 else torch.int16) !=
+              K0_rows[b].view(torch.uint8 if fp8 else torch.int16)).any(-1).any(0)
+        chv = (Vn[b].view(torch.uint8 if fp8 else torch.int16) !=
+               V4[b].view(torch.uint8 if fp8 else torch.int16)).any(-1).any(0)
+        expect = [] if int(upd[b, 0]) == 0xFFFFFFFF else list(range(P, P + S))
+        # a new row may equal the old one only by chance: compare against the oracle's rows
+        assert set(ch.nonzero().flatten().tolist()) <= set(expect)
+        assert set(chv.nonzero().flatten().tolist()) <= set(expect)
+        if not expect:
+            continue
+        if fp8:
+            _assert_codes_close(Kn_rows[b, :, P:P + S], Kr_rows[b, :, P:P + S])
+            _assert_codes_close(Vn[b, :, P:P + S], Vr[b, :, P:P + S])
+        else:
+            assert max_abs_rel(Kn_rows[b, :, P:P + S], Kr_rows[b, :, P:P + S]) < TOL
+            assert max_abs_rel(Vn[b, :, P:P + S], Vr[b, :, P:P + S]) < TOL
+        # every other row untouched (bitwise)
+        keep = torch.ones(S_max, dtype=torch.bool)
+        keep[P:P + S] = False
+        assert torch.equal(Kn_rows[b, :, keep].contiguous().view(torch.uint8),
+                           K0_rows[b, :, keep].contiguous().view(torch.uint8))
+
+
+def test_attention_fp8_block_kv(mk, dev):
+    """FP8 e4m3 block cache [num_blocks, block_len, kv_heads, d] through a block
+    table (one sequence's table with an invalid entry), global write rows."""
+    print("kv formats: fp8 block cache", flush=True)
+    B, H, nq, nkv, d, blk, n_act, nb = 2, 512, 8, 2, 128, 16, 5, 14
+    g = torch.Generator().manual_seed(99)
+    X = bf(torch.randn(B, 1, H, generator=g))
+    W = bf(0.03 * torch.randn(H, d * (nq + 2 * nkv), generator=g))
+    Wo = bf(0.03 * torch.randn(nq * d, H, generator=g))
+    Kc = ref.kv_fp8_quant(torch.randn(nb, blk, nkv, d, generator=g), 0.75)
+    Vc = ref.kv_fp8_quant(torch.randn(nb, blk, nkv, d, generator=g), 1.5)
+    perm = torch.randperm(nb, generator=g)                 # disjoint blocks per sequence
+    table = torch.stack([perm[b * n_act:(b + 1) * n_act] for b in range(B)]).to(torch.int32)
+    table[1, 4] = -1                                      # an absent block reads as zero rows
+    S_ctx = n_act * blk
+    P = S_ctx - 1 - 20                                     # the new token's slot index
+    cos_r, sin_r = _rope_rows(B, 1, P, d)
+    mask = torch.zeros(S_ctx, B, nq, 1, dtype=torch.bfloat16)
+    mask[:P] = (torch.rand(P, B, nq, 1, generator=g) < 0.8).to(torch.bfloat16)
+    mask[-1] = 1
+    # the new token of sequence b goes to its position P: block table[b, P // blk]
+    rows = [int(table[b, P // blk]) * blk + P % blk for b in range(B)]
+    upd = torch.tensor(rows, dtype=torch.int64).reshape(B, 1)
+    ks = torch.tensor([[0.75]], dtype=torch.float32)
+    vs = torch.tensor([[1.5]], dtype=torch.float16)
+    scale = 1.0 / (d ** 0.5 * 0.75)
+    Kg, Vg = Kc.to(dev), Vc.to(dev)
+    out, _, _ = _call(mk, dev, X, W, Wo, None, None, cos_r, sin_r, Kg, Vg, mask, None, upd, table,
+                      False, ks, vs, scale)
+    # oracle on the flat view (mask slots P .. S_ctx-2 are masked; slot S_ctx-1 is the new token)
+    Kf = ref.block_kv_to_flat(Kc, table)                   # [B, S_ctx, nkv, d]
+    Vf = ref.block_kv_to_flat(Vc, table)
+    gqa = nq // nkv
+    attn = torch.zeros(B, nq * d)
+    newk = torch.zeros(B, nkv, d, dtype=torch.float8_e4m3fn)
+    newv = torch.zeros(B, nkv, d, dtype=torch.float8_e4m3fn)
+    for h in range(nkv):
+        cols = torch.cat([torch.arange(h * gqa * d, (h + 1) * gqa * d),
+                          nq * d + h * d + torch.arange(d),
+                          (nq + nkv) * d + h * d + torch.arange(d)])
+        Kh = Kf[:, :, h].contiguous()
+        Vh = Vf[:, :, h].contiguous()
+        slot = torch.full((B, 1), S_ctx - 1)
+        o, Kh2, Vh2 = ref.attention_block_tkg(
+            X.float(), W.float()[:, cols], None, 1e-6, None, None, None, 1e-6, cos_r, sin_r,
+            Kh, Vh, mask[:, :, h * gqa:(h + 1) * gqa].float(), None, True, slot, None, None,
+            softmax_scale=scale, k_scale=0.75, v_scale=1.5)
+        attn[:, h * gqa * d:(h + 1) * gqa * d] = o
+        newk[:, h], newv[:, h] = Kh2[:, S_ctx - 1], Vh2[:, S_ctx - 1]
+    assert max_abs_rel(out, attn @ Wo.float()) < TOL
+    Kn, Vn = Kg.cpu(), Vg.cpu()
+    flat_rows = (Kn.view(torch.uint8) != Kc.view(torch.uint8)).reshape(nb * blk, -1).any(-1)
+    assert set(flat_rows.nonzero().flatten().tolist()) <= set(rows)
+    for b in range(B):
+        r = rows[b]
+        _assert_codes_close(Kn.reshape(nb * blk, nkv, d)[r], newk[b])
+        _assert_codes_close(Vn.reshape(nb * blk, nkv, d)[r], newv[b])
+
+
+def test_attention_kv_formats_reject(mk, dev):
+    """A transposed K cache with a block table, and an fp8 cache without both
+    scales, are rejected before any launch."""
+    from nki_moe_megakernel_amd.common_types import QuantizationType
+    B, H, nq, d, S_max = 1, 256, 4, 64, 32
+    X = torch.zeros(B, 1, H, dtype=torch.bfloat16, device=dev)
+    W = torch.zeros(H, d * (nq + 2), dtype=torch.bfloat16, device=dev)
+    mask = torch.ones(S_max, B, nq, 1, dtype=torch.bfloat16, device=dev)
+    upd = torch.zeros(B, 1, dtype=torch.int64, device=dev)
+    Kb = torch.zeros(4, 8, d, dtype=torch.bfloat16, device=dev)
+    table = torch.zeros(B, 4, dtype=torch.int32, device=dev)
+    with pytest.raises(ValueError, match="block KV"):
+        mk.attention_block_tkg(X, None, False, 1e-6, None, W, None, QuantizationType.NONE, None, None,
+                               False, 1e-6, None, None, None, None, True, False, 1e-6, None, None,
+                               True, table, Kb, Kb.clone(), mask, None, True, upd, None, None,
+                               QuantizationType.NONE, None, None, False, False)
+    K8 = torch.zeros(B, S_max, d, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    with pytest.raises(ValueError, match="float8_e4m3 needs k_scale"):
+        mk.attention_block_tkg(X, None, False, 1e-6, None, W, None, QuantizationType.NONE, None, None,
+                               False, 1e-6, None, None, None, None, True, False, 1e-6, None, None,
+                               False, None, K8, K8.clone(), mask, None, True, upd, None, None,
+                               QuantizationType.NONE, None, None, False, False,
+                               k_scale=torch.ones(1, 1, device=dev))

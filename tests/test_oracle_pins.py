@@ -553,3 +553,85 @@ def test_forced_routing_identity_and_pairing():
     other = (aux["idx"] + 1) % shape.E
     y3, _ = run(other, False)
     assert (y3 - y0).abs().max() > 1e-3
+
+
+# ------------------------------------------------------------ KV cache formats
+def test_kv_fp8_quant_matches_independent_e4m3_and_known_answers():
+    """kv_fp8_quant (torch's float8_e4m3fn cast after the clip) against the
+    independent numpy e4m3 quantiser of oracle/mx.py, over the whole range,
+    plus known answers: the +-240 clip, round-to-nearest-even ties, subnormals."""
+    import numpy as np
+    from oracle import mx
+    g = torch.Generator().manual_seed(11)
+    x = torch.cat([torch.randn(4096, generator=g) * 10 ** torch.empty(4096).uniform_(-4, 3, generator=g),
+                   torch.tensor([0.0, -0.0, 1e-12, 300.0, -1e4])])
+    for scale in (1.0, 0.37, 16.0):
+        q = ref.kv_fp8_quant(x, scale)
+        y = (x * scale).clamp(-240, 240).numpy().astype(np.float64)
+        codes = mx.quantize_elements(y, "e4m3")
+        assert np.array_equal(q.view(torch.uint8).numpy() & 0x7f, codes & 0x7f)
+        nz = y != 0
+        assert np.array_equal(q.view(torch.uint8).numpy()[nz], codes[nz])
+    kat = {1000.0: 240.0, -1000.0: -240.0, 239.0: 240.0, 1.0625: 1.0, 1.1875: 1.25,
+           2.0 ** -10: 0.0, 3 * 2.0 ** -10: 2.0 ** -8, 2.0 ** -9: 2.0 ** -9, 0.0: 0.0}
+    for xin, want in kat.items():
+        assert ref.kv_fp8_quant(torch.tensor([xin]), 1.0).float().item() == want, xin
+
+
+def _attn_case(seed, B=2, S=1, nq=4, d=64, H=128, P=20, S_max=40):
+    g = torch.Generator().manual_seed(seed)
+    X = torch.randn(B, S, H, generator=g).to(torch.bfloat16)
+    W = (0.05 * torch.randn(H, d * (nq + 2), generator=g))
+    Kc = torch.randn(B, S_max, d, generator=g)
+    Vc = torch.randn(B, S_max, d, generator=g)
+    mask = (torch.rand(P + S, B, nq, S, generator=g) > 0.2).float()
+    mask[P:] = 1
+    upd = torch.tensor([[P]] * B)
+    return X, W, Kc, Vc, mask, upd
+
+
+def _run_attn(X, W, Kc, Vc, mask, upd, **kw):
+    return ref.attention_block_tkg(X, W, None, None, None, None, None, 1e-6, None, None,
+                                   Kc, Vc, mask, None, True, upd, None, None, **kw)
+
+
+def test_transposed_k_cache_equals_row_layout():
+    """K_cache_transposed reads and writes the same logical cache: results and
+    the written column equal the [S, d] layout's on the same data."""
+    X, W, Kc, Vc, mask, upd = _attn_case(3, S=2)
+    K1, V1 = Kc.clone(), Vc.clone()
+    o1, _, _ = _run_attn(X, W, K1, V1, mask, upd)
+    Kt, V2 = Kc.transpose(1, 2).contiguous(), Vc.clone()
+    o2, _, _ = _run_attn(X, W, Kt, V2, mask, upd, K_cache_transposed=True)
+    assert torch.equal(o1, o2)
+    assert torch.equal(Kt.transpose(1, 2), K1) and torch.equal(V1, V2)
+    p = int(upd[0, 0])
+    assert not torch.equal(Kt[:, :, p], Kc.transpose(1, 2)[:, :, p])   # the column was written
+
+
+def test_fp8_kv_scales_multiply_and_are_not_undone():
+    """FP8 KV: the scales multiply the stored values and the attention does not
+    divide them out.  With power-of-two scales (no clipping, no subnormals),
+    quantisation commutes with the scale, so k_scale = 2 with softmax_scale / 2
+    equals k_scale = 1, and v_scale = 2 doubles the output (up to the few new
+    elements below 2^-6, whose subnormal quantum does not scale).  An oracle
+    that dequantised (or divided by the scale) is off by O(1) in both."""
+    X, W, Kc, Vc, mask, upd = _attn_case(5)
+    Kq = ref.kv_fp8_quant(Kc, 1.0)
+    Vq = ref.kv_fp8_quant(Vc, 1.0)
+    s = 1.0 / 8.0
+    o1, K1, V1 = _run_attn(X, W, Kq.clone(), Vq.clone(), mask, upd, k_scale=1.0, v_scale=1.0,
+                           softmax_scale=s)
+    # the cache doubled for K (exact in e4m3), scores rescaled back
+    o2, K2, _ = _run_attn(X, W, ref.kv_fp8_quant(Kq.float() * 2, 1.0), Vq.clone(), mask, upd,
+                          k_scale=2.0, v_scale=1.0, softmax_scale=s / 2)
+    assert torch.allclose(o1, o2, rtol=2e-3, atol=2e-4)
+    assert (o1 - o2).abs().max() < 1e-2 * o1.abs().max()
+    o3, _, V3 = _run_attn(X, W, Kq.clone(), ref.kv_fp8_quant(Vq.float() * 2, 1.0), mask, upd,
+                          k_scale=1.0, v_scale=2.0, softmax_scale=s)
+    assert torch.allclose(o3, 2 * o1, rtol=2e-3, atol=2e-4)
+    # the new row is stored quantised, and a fp8 cache of exactly representable
+    # values with unit scales gives the bf16-valued attention of those values
+    p = int(upd[0, 0])
+    assert K1.dtype == torch.float8_e4m3fn
+    assert not torch.equal(K1[:, p].float(), Kq[:, p].float())
