@@ -291,10 +291,31 @@ typedef struct {
   int kv_format;
   const float* k_scale;
   const float* v_scale;
+  /* Static FP8 quantisation of the projections (quantization_type_qkv / _out =
+   * STATIC, attention_block_tkg.py:94-97, :124-127, :179-183, :225-229; qkv_tkg.py:
+   * 289-305, 849-862, 946-986; output_projection_tkg.py:185-200, 549-566).  With
+   * quant_qkv = MKD_QUANT_STATIC, w_qkv_packed holds e4m3 weights packed by
+   * mkd_pack_fp8_weights; the (normalised) input is quantised as
+   * x_q = e4m3(clip(x * (1 / in_scale_qkv[0]), -240, 240)) and the projection is
+   * (x_q @ W) * (w_scale_qkv[j] * in_scale_qkv[0]) + bias, j = 0 / 1 / 2 for the
+   * Q / K / V columns.  quant_out likewise for the output projection with one
+   * weight scale w_scale_out[0] (no residual).  Scales: fp32 in device memory. */
+  int quant_qkv, quant_out;
+  const float* w_scale_qkv;    /* [3] */
+  const float* in_scale_qkv;   /* [1] */
+  const float* w_scale_out;    /* [1] */
+  const float* in_scale_out;   /* [1] */
 } mkd_attention_args;
+#define MKD_QUANT_NONE 0
+#define MKD_QUANT_STATIC 1
 #define MKD_KV_FP8 1
 #define MKD_KV_K_TRANSPOSED 2
 size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S_max);
+/* e4m3 weights for the static FP8 projections: src [K, N] codes (the
+ * reference's [in, out] layout: W_qkv [H, I], W_out [nq d, H]; N % 16 == 0,
+ * K % 32 == 0) -> dst of mkd_packed_fp8_bytes(N, K) bytes (device). */
+size_t mkd_packed_fp8_bytes(int N, int K);
+int mkd_pack_fp8_weights(const void* src, void* dst, int N, int K, void* stream);
 /* The same for s_tkg new tokens per sequence (mkd_attention_args::s_tkg). */
 size_t mkd_attention_workspace_bytes_tkg(int B, int s_tkg, int H, int nq, int nkv, int d, int S_max);
 int mkd_attention_block_tkg(const mkd_attention_args* args, void* workspace,

@@ -71,6 +71,8 @@ class AttentionArgs(C.Structure):
         ("hidden_actual", i32), ("window", i32), ("s_tkg", i32),
         ("q_norm_post", vp), ("k_norm_post", vp), ("qk_post_eps", f32),
         ("kv_format", i32), ("k_scale", vp), ("v_scale", vp),
+        ("quant_qkv", i32), ("quant_out", i32), ("w_scale_qkv", vp), ("in_scale_qkv", vp),
+        ("w_scale_out", vp), ("in_scale_out", vp),
     ]
 
 
@@ -117,6 +119,8 @@ _SIGS = {
     "mkd_attention_workspace_bytes": (sz, [i32, i32, i32, i32, i32, i32]),
     "mkd_attention_workspace_bytes_tkg": (sz, [i32, i32, i32, i32, i32, i32, i32]),
     "mkd_attention_block_tkg": (i32, [C.POINTER(AttentionArgs), vp, sz, vp]),
+    "mkd_packed_fp8_bytes": (sz, [i32, i32]),
+    "mkd_pack_fp8_weights": (i32, [vp, vp, i32, i32, vp]),
     "mkd_qwen3_workspace_bytes": (sz, [C.POINTER(Qwen3Model), i32]),
     "mkd_qwen3_route_log_bytes": (sz, [C.POINTER(Qwen3Model), i32]),
     "mkd_qwen3_route_log_layout": (i32, [C.POINTER(Qwen3Model), i32, C.POINTER(sz)]),

@@ -17,12 +17,9 @@
 // layout attn_combine_kernel merges, so the sink, the output and the output
 // projection are the default path's.
 //
-// e4m3 here: 1 sign, 4 exponent (bias 7), 3 mantissa bits, no infinities,
-// 0x7f / 0xff NaN (the OCP float8 e4m3 layout, torch.float8_e4m3fn).  The
-// reference's float8_e4m3 keeps the top exponent for infinities (largest
-// finite 240); every value its quantiser produces (clipped to +-240) has the
-// same code in both layouts.
+// e4m3 codes and their quantiser: fp8.h.
 #include "common.h"
+#include "fp8.h"
 #include "mkd_internal.h"
 #include "attn_common.h"
 
@@ -30,44 +27,11 @@ namespace mkd {
 
 namespace {
 
-constexpr float kKvFp8Max = 240.0f;   // _FP8_E4M3_MAX of the reference's float8_e4m3
 constexpr int kKvMaxChunk = 256;      // positions per block (attn_chunk_for: 64 / 128 / 256)
 constexpr int kKvMaxNew = 8;          // new tokens per sequence
 
-// floor(log2(a)) for finite a > 0, fp32 subnormals included
-MKD_DEV int kv_floor_log2(float a) {
-  const uint32_t b = __float_as_uint(a);
-  const int e = (int)((b >> 23) & 0xffu);
-  if (e) return e - 127;
-  return (31 - __clz(b & 0x7fffffu)) - 149;
-}
-
-// e4m3 code of v, round to nearest even, saturating at 448 (the caller clips
-// to +-240 first): the quantum at |v| is 2^(max(floor(log2|v|), -6) - 3).
-MKD_DEV uint32_t e4m3_encode(float v) {
-  const uint32_t sign = (__float_as_uint(v) >> 24) & 0x80u;
-  const float a = fabsf(v);
-  if (!(a > 0.f)) return sign;
-  const int e = max(kv_floor_log2(a), -6);
-  const float q = fminf(ldexpf(rintf(ldexpf(a, 3 - e)), e - 3), 448.0f);
-  if (q == 0.f) return sign;
-  const int qe = kv_floor_log2(q);
-  const uint32_t mag = qe >= -6 ? (((uint32_t)(qe + 7) << 3) | ((__float_as_uint(q) >> 20) & 7u))
-                                : (uint32_t)ldexpf(q, 9);   // subnormal: q / 2^-9
-  return sign | mag;
-}
-
-MKD_DEV float e4m3_decode(uint32_t c) {
-  const uint32_t e = (c >> 3) & 15u, m = c & 7u;
-  if ((c & 0x7fu) == 0x7fu) return __uint_as_float(0x7fc00000u);
-  const float mag = e ? __uint_as_float(((e + 120u) << 23) | (m << 20)) : (float)m * 0x1p-9f;
-  return (c & 0x80u) ? -mag : mag;
-}
-
 // the stored code of a new k / v element (attention_block_tkg.py:1694-1737)
-MKD_DEV uint32_t kv_quant(float x, float scale) {
-  return e4m3_encode(fminf(fmaxf(x * scale, -kKvFp8Max), kKvFp8Max));
-}
+MKD_DEV uint32_t kv_quant(float x, float scale) { return fp8_quant(x, scale); }
 
 // Element offset of position t, element 0 of kv head g in row r's sequence
 // (V, or K when it is not transposed); -1 where a block table holds no block.

@@ -732,6 +732,7 @@ struct AttnWs {
   float* qkv;
   uint16_t *attn, *kvn, *prep;
   float *po, *pml;
+  uint16_t* xq;               // statically quantised projection inputs (FP8 projections)
   int chunk, n_chunks;
 };
 
@@ -752,6 +753,7 @@ static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_
   w.prep = c.take<uint16_t>((size_t)B * (nq + 2 * nkv) * d);
   w.po = c.take<float>((size_t)B * nq * w.n_chunks * d);
   w.pml = c.take<float>((size_t)B * nq * w.n_chunks * 2);
+  w.xq = c.take<uint16_t>((size_t)B * std::max(H, nq * d));
   return w;
 }
 
@@ -804,6 +806,20 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
       qkv_parts = 4;
       qkv_split_row = (qkv_n / 16 - xt) * 16;
     }
+  } else if (p->quant_qkv == MKD_QUANT_STATIC) {
+    // e4m3 weights, statically quantised input, per-segment dequantisation
+    W8Args q;
+    memset(&q, 0, sizeof(q));
+    q.w = static_cast<const uint8_t*>(p->w_qkv_packed);
+    q.x_bf16 = static_cast<const uint16_t*>(xin);
+    q.ldx = p->H; q.T = rows; q.N = qkv_n; q.K = p->H;
+    q.w_scale = p->w_scale_qkv; q.in_scale = p->in_scale_qkv;
+    q.seg0 = p->nq * p->d; q.seg1 = (p->nq + p->nkv) * p->d;
+    q.bias = static_cast<const uint16_t*>(p->bias_qkv);
+    q.y_f32 = w.qkv; q.ldy = qkv_n;
+    const int ps = prof_begin(MKD_KCLASS_QKV, s);
+    MKD_TRY(gemm_w8_launch(q, w.xq, s), "qkv (fp8 static)");
+    prof_end(ps, s);
   } else {
     GemmArgs g = dense_args(p->w_qkv_packed, xin, p->H, qkv_n, p->H, rows, w.qkv, qkv_n);
     g.bias = static_cast<const uint16_t*>(p->bias_qkv);
@@ -905,7 +921,22 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     MKD_TRY(attn_combine_launch(a, s), "attention combine + kv scatter");
   }
   // 5. output projection
-  if (p->w_out_packed) {
+  if (p->w_out_packed && p->quant_out == MKD_QUANT_STATIC) {
+    MKD_REQUIRE(!o_parts && !p->residual, MKD_ERR_UNSUPPORTED,
+                "attention: the fp8 output projection writes bf16 rows without a residual");
+    W8Args q;
+    memset(&q, 0, sizeof(q));
+    q.w = static_cast<const uint8_t*>(p->w_out_packed);
+    q.x_bf16 = w.attn;
+    q.ldx = p->nq * p->d; q.T = rows; q.N = p->H_out; q.K = p->nq * p->d;
+    q.w_scale = p->w_scale_out; q.in_scale = p->in_scale_out;
+    q.seg0 = q.seg1 = p->H_out;
+    q.bias = static_cast<const uint16_t*>(p->bias_out);
+    q.y_bf16 = static_cast<uint16_t*>(p->out); q.ldy = p->H_out;
+    const int ps = prof_begin(MKD_KCLASS_OPROJ, s);
+    MKD_TRY(gemm_w8_launch(q, w.xq, s), "o_proj (fp8 static)");
+    prof_end(ps, s);
+  } else if (p->w_out_packed) {
     GemmArgs o = dense_args(p->w_out_packed, w.attn, p->nq * p->d, p->H_out, p->nq * p->d, rows,
                             p->out, p->H_out);
     o.bias = static_cast<const uint16_t*>(p->bias_out);
@@ -959,6 +990,15 @@ static int validate_attn(const mkd_attention_args* p) {
     if (int rc = check_gemm_dims(p->H_out, p->nq * p->d, 1)) return rc;
   }
   MKD_REQUIRE(!p->residual || p->w_out_packed, MKD_ERR_INVALID, "attention: residual needs W_out");
+  MKD_REQUIRE(p->quant_qkv == MKD_QUANT_NONE || p->quant_qkv == MKD_QUANT_STATIC, MKD_ERR_UNSUPPORTED,
+              "attention: quant_qkv %d must be NONE or STATIC", p->quant_qkv);
+  MKD_REQUIRE(p->quant_out == MKD_QUANT_NONE || p->quant_out == MKD_QUANT_STATIC, MKD_ERR_UNSUPPORTED,
+              "attention: quant_out %d must be NONE or STATIC", p->quant_out);
+  MKD_REQUIRE(!p->quant_qkv || (p->w_scale_qkv && p->in_scale_qkv), MKD_ERR_NULL,
+              "attention: the static fp8 QKV projection needs w_scale_qkv and in_scale_qkv");
+  MKD_REQUIRE(!p->quant_out || (p->w_out_packed && p->w_scale_out && p->in_scale_out && !p->residual),
+              MKD_ERR_INVALID,
+              "attention: the static fp8 output projection needs W_out, w_scale_out, in_scale_out, no residual");
   MKD_REQUIRE((p->kv_format & ~(MKD_KV_FP8 | MKD_KV_K_TRANSPOSED)) == 0, MKD_ERR_INVALID,
               "attention: unknown kv_format bits 0x%x", p->kv_format);
   if (p->kv_format) {
@@ -980,6 +1020,20 @@ static int validate_attn(const mkd_attention_args* p) {
     MKD_REQUIRE(!p->update_cache || p->kv_cache_update_idx, MKD_ERR_NULL,
                 "attention: update_cache needs kv_cache_update_idx");
   }
+  return MKD_OK;
+}
+
+size_t mkd_packed_fp8_bytes(int N, int K) {
+  return (N > 0 && K > 0) ? (size_t)N * K : 0;
+}
+
+int mkd_pack_fp8_weights(const void* src, void* dst, int N, int K, void* stream) {
+  if (int rc = stale_check("mkd_pack_fp8_weights")) return rc;
+  MKD_REQUIRE(src && dst, MKD_ERR_NULL, "pack_fp8_weights: null pointer");
+  MKD_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0, MKD_ERR_INVALID,
+              "pack_fp8_weights: N %d must be a multiple of 16 and K %d of 32", N, K);
+  MKD_TRY(w8_pack_launch(static_cast<const uint8_t*>(src), N, K, static_cast<uint8_t*>(dst),
+                         static_cast<hipStream_t>(stream)), "pack fp8 weights");
   return MKD_OK;
 }
 

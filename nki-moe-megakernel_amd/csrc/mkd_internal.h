@@ -311,6 +311,25 @@ hipError_t attn_prep_launch(const AttnArgs& a, int rope_mode, hipStream_t s);
 // the combine (kernels run in stream order, so every chunk has read the cache).
 hipError_t attn_kvfmt_launch(const AttnArgs& a, int rope_mode, hipStream_t s);
 hipError_t attn_kvfmt_store_launch(const AttnArgs& a, hipStream_t s);
+
+// gemm_w8.hip: dense projection with e4m3 weights and static activation
+// quantisation (the STATIC paths of qkv_tkg.py / output_projection_tkg.py)
+struct W8Args {
+  const uint8_t* w;           // frag-packed e4m3 [N/16][K/32][64][8] (w8_pack_launch)
+  const uint16_t* x_bf16;     // activations [T, ldx] bf16
+  const uint16_t* x;          // the quantised activations (set by the launch)
+  int ldx, T, N, K;
+  const float* w_scale;       // device: [3] Q / K / V weight scales, or [1]
+  const float* in_scale;      // device: [1] input scale
+  int seg0, seg1;             // columns < seg0 use w_scale[0], < seg1 [1], else [2]
+  const uint16_t* bias;       // [N] bf16 or null
+  float* y_f32;               // exactly one of y_f32 / y_bf16
+  uint16_t* y_bf16;
+  int ldy;
+};
+hipError_t w8_pack_launch(const uint8_t* src, int N, int K, uint8_t* dst, hipStream_t s);
+// quantises x into xq ([T, K] bf16 scratch), then the GEMM (T <= 128)
+hipError_t gemm_w8_launch(const W8Args& a, uint16_t* xq, hipStream_t s);
 // Attention, chunk combine and output projection in one launch (attn_mfma.hip,
 // attn_joined_kernel): the chunk blocks, then the combine blocks, then the
 // projection blocks of one grid, each stage waiting on the flags of the blocks

@@ -40,6 +40,21 @@ def pack(src: torch.Tensor, groups: int, n: int, k: int, g_stride: int, row_stri
     return out
 
 
+def pack_fp8_in_out(w: torch.Tensor) -> torch.Tensor:
+    """float8 e4m3 weights in the reference layout [k_in, n_out] (torch.float8_e4m3fn,
+    or uint8 codes) -> the frag-packed e4m3 layout of the static FP8 projections."""
+    L.require_gpu(w)
+    if w.dtype not in (torch.float8_e4m3fn, torch.uint8):
+        raise ValueError(f"FP8 weights must be float8_e4m3, got {w.dtype}")
+    k, n = w.shape
+    src = w.contiguous().view(torch.uint8)
+    lib = L.load()
+    out = torch.empty(lib.mkd_packed_fp8_bytes(n, k), dtype=torch.uint8, device=w.device)
+    rc = lib.mkd_pack_fp8_weights(src.data_ptr(), out.data_ptr(), n, k, L.stream_ptr(w.device))
+    L.check(rc, "pack_fp8_weights")
+    return out
+
+
 def pack_out_in(w: torch.Tensor) -> torch.Tensor:
     """HF / nn.Linear layout [n_out, k_in] -> packed."""
     n, k = w.shape

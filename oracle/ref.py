@@ -516,12 +516,28 @@ def kv_fp8_quant(x: torch.Tensor, scale: float) -> torch.Tensor:
     return y.to(torch.float8_e4m3fn)
 
 
+def static_fp8_linear(x: torch.Tensor, W: torch.Tensor, col_w_scale: torch.Tensor,
+                      in_scale: float, bias=None) -> torch.Tensor:
+    """Static FP8 projection (qkv_tkg.py:289-305, 849-862, 946-986, 1094-1098;
+    output_projection_tkg.py:185-200, 549-566): the bf16 input is quantised as
+    e4m3(clip(x * (1 / in_scale), +-240)), multiplied by the e4m3 weights
+    W [k_in, n_out] in fp32, each column dequantised by its weight scale times
+    in_scale (col_w_scale [n_out]), then the bias is added."""
+    inv = float(torch.tensor(1.0, dtype=torch.float32) / torch.tensor(in_scale, dtype=torch.float32))
+    xq = kv_fp8_quant(x.to(torch.bfloat16), inv).float()
+    comb = col_w_scale.float() * torch.tensor(in_scale, dtype=torch.float32)
+    y = (xq @ W.float()) * comb.reshape(1, -1)
+    if bias is not None:
+        y = y + bias.float().reshape(1, -1)
+    return y
+
+
 def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
                         q_norm_w, k_norm_w, qk_eps, cos, sin, K_cache, V_cache,
                         attention_mask, sink, update_cache, kv_cache_update_idx,
                         W_out, bias_out, softmax_scale=None, q_norm_post_w=None,
                         k_norm_post_w=None, qk_post_eps=None, k_scale=None, v_scale=None,
-                        K_cache_transposed=False):
+                        K_cache_transposed=False, qkv_static=None, out_static=None):
     """Generic attention block (fp32 math, kv_heads = 1 as in the reference :353).
 
     X [B, S_tkg, H]; W_qkv [H, d*(nq+2)] packed Q | K | V (:363-384);
@@ -542,7 +558,9 @@ def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
     new k / v rows are taken in bf16 (their io dtype, :979-1084), quantised by
     kv_fp8_quant, written as such, and the attention uses the stored values
     as they are, the new tokens' own quantised rows included (:1073-1084;
-    attention_tkg.py:749-821).
+    attention_tkg.py:749-821).  qkv_static = (w_scale [3] for the Q / K / V
+    columns, in_scale) and out_static = (w_scale, in_scale): the STATIC FP8
+    projections of static_fp8_linear with e4m3 W_qkv / W_out (:94-97, :124-127).
     Returns (out [B*S_tkg, H] fp32, K_cache, V_cache).
     """
     B, S, H = X.shape
@@ -551,9 +569,15 @@ def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
     x = X.float().reshape(B * S, H)
     if rmsnorm_X_gamma is not None:
         x = rmsnorm_tkg(x, rmsnorm_X_gamma, rmsnorm_X_eps)
-    qkv = x @ W_qkv.float()
-    if bias_qkv is not None:
-        qkv = qkv + bias_qkv.float().reshape(1, -1)
+    if qkv_static is not None:
+        ws, s_in = qkv_static
+        ws = torch.as_tensor(ws, dtype=torch.float32).reshape(-1)
+        seg = torch.cat([torch.full((nq * d,), 0), torch.full((d,), 1), torch.full((d,), 2)])
+        qkv = static_fp8_linear(x, W_qkv, ws[seg], s_in, bias_qkv)
+    else:
+        qkv = x @ W_qkv.float()
+        if bias_qkv is not None:
+            qkv = qkv + bias_qkv.float().reshape(1, -1)
     q = qkv[:, :nq * d].reshape(B, S, nq, d)
     k = qkv[:, nq * d:(nq + 1) * d].reshape(B, S, d)
     v = qkv[:, (nq + 1) * d:].reshape(B, S, d)
@@ -607,6 +631,10 @@ def attention_block_tkg(X, W_qkv, rmsnorm_X_gamma, rmsnorm_X_eps, bias_qkv,
     attn = out.reshape(B * S, nq * d)
     if W_out is None:
         return attn, K_cache, V_cache
+    if out_static is not None:
+        ws, s_in = out_static
+        o = static_fp8_linear(attn, W_out, torch.full((W_out.shape[1],), float(ws)), s_in, bias_out)
+        return o, K_cache, V_cache
     o = attn @ W_out.float()
     if bias_out is not None:
         o = o + bias_out.float().reshape(1, -1)

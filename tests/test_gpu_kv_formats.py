@@ -242,3 +242,77 @@ def test_attention_kv_formats_reject(mk, dev):
                                False, None, K8, K8.clone(), mask, None, True, upd, None, None,
                                QuantizationType.NONE, None, None, False, False,
                                k_scale=torch.ones(1, 1, device=dev))
+
+
+@pytest.mark.parametrize("B,H,nq,nkv,d,S,P,S_max,norm,bias,q_st,o_st,fp8kv", [
+    (2, 512, 8, 1, 128, 1, 100, 128, True, True, True, True, False),
+    (3, 256, 8, 2, 64, 2, 30, 64, False, False, True, False, True),
+    (1, 2048, 32, 4, 128, 1, 500, 512, True, True, False, True, False),
+    (48, 256, 4, 1, 64, 2, 10, 16, True, True, True, True, False),
+])
+def test_attention_static_fp8_projections(mk, dev, B, H, nq, nkv, d, S, P, S_max, norm, bias,
+                                          q_st, o_st, fp8kv):
+    """quantization_type_qkv / _out = STATIC: e4m3 weights, the input quantised
+    by 1 / input scale and clipped to +-240, per-segment (Q / K / V) weight
+    scales, bias after the dequantisation -- against the oracle per kv head."""
+    from nki_moe_megakernel_amd.common_types import QuantizationType
+    print(f"static fp8 projections: B={B} S={S} nq={nq} nkv={nkv} q={q_st} o={o_st} fp8kv={fp8kv}", flush=True)
+    g = torch.Generator().manual_seed(B * 7 + S * 3 + P + 11 * q_st + 5 * o_st)
+    X = bf(torch.randn(B, S, H, generator=g))
+    I = d * (nq + 2 * nkv)
+    gamma = bf(1 + 0.1 * torch.randn(1, H, generator=g)) if norm else None
+    wsq = torch.tensor([0.002, 0.003, 0.0025])
+    s_in_q, s_in_o, ws_o = 1.0 / 32, 1.0 / 16, 0.0015
+    if q_st:
+        Wq = ref.kv_fp8_quant(0.03 * torch.randn(H, I, generator=g), 1.0 / 0.0025)
+    else:
+        Wq = bf(0.03 * torch.randn(H, I, generator=g))
+    if o_st:
+        Wo = ref.kv_fp8_quant(0.03 * torch.randn(nq * d, H, generator=g), 1.0 / ws_o)
+    else:
+        Wo = bf(0.03 * torch.randn(nq * d, H, generator=g))
+    bq = bf(0.1 * torch.randn(1, I, generator=g)) if bias else None
+    bo = bf(0.1 * torch.randn(1, H, generator=g)) if bias else None
+    K4 = torch.randn(B, nkv, S_max, d, generator=g)
+    V4 = torch.randn(B, nkv, S_max, d, generator=g)
+    if fp8kv:
+        K4, V4 = ref.kv_fp8_quant(K4, 1.0), ref.kv_fp8_quant(V4, 1.0)
+    else:
+        K4, V4 = bf(K4), bf(V4)
+    cos_r, sin_r = _rope_rows(B, S, P, d)
+    mask = _mask(g, P, B, nq, S)
+    upd = torch.full((B, 1), P, dtype=torch.int64)
+    one = torch.ones(1, 1)
+    Kg = (K4 if nkv > 1 else K4[:, 0]).contiguous().to(dev)
+    Vg = (V4 if nkv > 1 else V4[:, 0]).contiguous().to(dev)
+    out, _, _ = mk.attention_block_tkg(
+        X.to(dev), None, norm, 1e-6, gamma.to(dev) if norm else None, Wq.to(dev),
+        bq.to(dev) if bias else None,
+        QuantizationType.STATIC if q_st else QuantizationType.NONE,
+        wsq.reshape(1, 3).expand(128, 3).contiguous().to(dev) if q_st else None,
+        torch.full((1, 1), s_in_q).to(dev) if q_st else None,
+        False, 1e-6, None, None, cos_r.to(dev), sin_r.to(dev), True, False, 1e-6, None, None,
+        False, None, Kg, Vg, mask.to(dev), None, True, upd.to(dev), Wo.to(dev),
+        bo.to(dev) if bias else None,
+        QuantizationType.STATIC if o_st else QuantizationType.NONE,
+        torch.full((128, 1), ws_o).to(dev) if o_st else None,
+        torch.full((128, 1), s_in_o).to(dev) if o_st else None, False, False,
+        k_scale=one.to(dev) if fp8kv else None, v_scale=one.to(dev) if fp8kv else None)
+    gqa = nq // nkv
+    attn = torch.zeros(B * S, nq * d)
+    for h in range(nkv):
+        cols = torch.cat([torch.arange(h * gqa * d, (h + 1) * gqa * d),
+                          nq * d + h * d + torch.arange(d),
+                          (nq + nkv) * d + h * d + torch.arange(d)])
+        o, _, _ = ref.attention_block_tkg(
+            X.float(), Wq[:, cols] if q_st else Wq.float()[:, cols], gamma.float() if norm else None,
+            1e-6, bq.reshape(-1)[cols] if bias else None, None, None, 1e-6, cos_r, sin_r,
+            K4[:, h].clone(), V4[:, h].clone(), mask[:, :, h * gqa:(h + 1) * gqa].float(), None, True,
+            upd, None, None, k_scale=1.0 if fp8kv else None, v_scale=1.0 if fp8kv else None,
+            qkv_static=(wsq, s_in_q) if q_st else None)
+        attn[:, h * gqa * d:(h + 1) * gqa * d] = o
+    if o_st:
+        y_ref = ref.static_fp8_linear(attn, Wo, torch.full((H,), ws_o), s_in_o, bo)
+    else:
+        y_ref = attn @ Wo.float() + (bo.float() if bias else 0.0)
+    assert max_abs_rel(out, y_ref) < TOL

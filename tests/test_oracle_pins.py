@@ -635,3 +635,63 @@ def test_fp8_kv_scales_multiply_and_are_not_undone():
     p = int(upd[0, 0])
     assert K1.dtype == torch.float8_e4m3fn
     assert not torch.equal(K1[:, p].float(), Kq[:, p].float())
+
+
+# ------------------------------------------------- static FP8 projections
+def _fp8_values(g, *shape, std=1.0):
+    return ref.kv_fp8_quant(std * torch.randn(*shape, generator=g), 1.0).float()
+
+
+def test_static_fp8_projection_reduces_to_plain_on_e4m3_values():
+    """Inputs and weights that are e4m3 values, unit scales: the static path is the
+    plain projection (quantisation is the identity there, the scales neutral);
+    power-of-two input scales that keep x / s_in in range do not change the
+    result (s_in divides the input and multiplies the output back); the weight
+    scale multiplies.  Clipping saturates at +-240."""
+    g = torch.Generator().manual_seed(21)
+    x = _fp8_values(g, 4, 64)
+    W = _fp8_values(g, 64, 48, std=0.1)
+    b = torch.randn(48, generator=g).to(torch.bfloat16)
+    plain = x @ W + b.float()
+    ones = torch.ones(48)
+    assert torch.allclose(ref.static_fp8_linear(x, W, ones, 1.0, b), plain, rtol=1e-6, atol=1e-5)
+    for s_in in (0.5, 0.25):    # x / s_in stays below 240 and normal
+        assert torch.allclose(ref.static_fp8_linear(x, W, ones, s_in, b), plain, rtol=1e-6, atol=1e-5)
+    assert torch.allclose(ref.static_fp8_linear(x, W, 3 * ones, 1.0), 3 * (x @ W), rtol=1e-6, atol=1e-5)
+    big = ref.static_fp8_linear(torch.full((1, 64), 1e4), torch.eye(64)[:, :16], torch.ones(16), 1.0)
+    assert torch.equal(big, torch.full((1, 16), 240.0))
+
+
+def test_static_fp8_qkv_segments_map_to_q_k_v():
+    """Weight scale j of the QKV projection scales the Q (j=0), K (1), V (2)
+    columns: doubling the V scale doubles the attention output (linear in V);
+    doubling the Q or the K scale with the softmax scale halved leaves it
+    unchanged.  A wrong segment order fails one of the three."""
+    g = torch.Generator().manual_seed(23)
+    B, nq, d, H, P, S_max = 2, 4, 32, 64, 12, 20
+    X = ref.kv_fp8_quant(torch.randn(B, 1, H, generator=g), 1.0).to(torch.bfloat16)
+    W = ref.kv_fp8_quant(0.1 * torch.randn(H, d * (nq + 2), generator=g), 1.0)
+    Kc = torch.randn(B, S_max, d, generator=g)
+    Vc = torch.randn(B, S_max, d, generator=g)
+    mask = torch.ones(P + 1, B, nq, 1)
+    upd = torch.tensor([[P]] * B)
+
+    def run(ws, sm):
+        o, _, _ = ref.attention_block_tkg(X, W, None, None, None, None, None, 1e-6, None, None,
+                                          Kc.clone(), Vc.clone(), mask, None, False, upd, None, None,
+                                          softmax_scale=sm, qkv_static=(ws, 1.0))
+        return o
+    s = 1.0 / math.sqrt(d)
+    base = run([1.0, 1.0, 1.0], s)
+    assert torch.allclose(run([2.0, 1.0, 1.0], s / 2), base, rtol=1e-4, atol=1e-5)
+    assert not torch.allclose(run([2.0, 1.0, 1.0], s), base, rtol=1e-3, atol=1e-4)
+    # K: only the new token's key is projected; the cache keys are not rescaled, so
+    # scale them by hand for the comparison
+    o_k, _, _ = ref.attention_block_tkg(X, W, None, None, None, None, None, 1e-6, None, None,
+                                        2 * Kc, Vc.clone(), mask, None, False, upd, None, None,
+                                        softmax_scale=s / 2, qkv_static=([1.0, 2.0, 1.0], 1.0))
+    assert torch.allclose(o_k, base, rtol=1e-4, atol=1e-5)
+    o_v, _, _ = ref.attention_block_tkg(X, W, None, None, None, None, None, 1e-6, None, None,
+                                        Kc.clone(), 2 * Vc, mask, None, False, upd, None, None,
+                                        softmax_scale=s, qkv_static=([1.0, 1.0, 2.0], 1.0))
+    assert torch.allclose(o_v, 2 * base, rtol=1e-4, atol=1e-5)
