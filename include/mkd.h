@@ -145,6 +145,7 @@ int mkd_router_topk_static(const void* x, int x_dtype, int T, int H, const void*
  * ------------------------------------------------------------------------- */
 #define MKD_MX_E4M3 1
 #define MKD_MX_E2M1 2
+#define MKD_FP8_E4M3 3   /* mkd_moe_args::weight_format: e4m3 experts, per-column scales */
 int mkd_quantize_mx(const void* x, int x_dtype, int rows, int k, int ldx, int fmt, void* codes,
                     void* scales, int k_pad, void* stream);
 size_t mkd_packed_mx_bytes(int groups, int n, int k, int fmt);
@@ -172,6 +173,16 @@ int mkd_pack_mx_weights(const void* codes, const void* scales, void* dst, void* 
  * the hidden rows and the bf16 SwiGLU output are quantised to MXFP8 (E4M3)
  * before each projection (selective_expert_mx_impl.py:143-149,
  * down_projection_mx_shard_H.py:74-79); round_qwen must be 0.
+ * weight_format MKD_FP8_E4M3: the FP8 ROW / STATIC experts (moe_tkg.py:119-131,
+ * 296-328): gate_up / down are e4m3 codes packed by mkd_pack_fp8_weights
+ * (G = E; gate/up [H, 2I] per expert with the gate columns first, down [I, H]);
+ * gate_up_scales / down_scales are fp32 dequantisation scales per expert and
+ * output column ([E, 2I]: ROW's [E, 2, I], or STATIC's [E, 2, 1] per half;
+ * [E, H]).  The activations stay bf16 (the reference's expert kernels read
+ * the input scales of STATIC mode only to select the mode,
+ * mlp_tkg_gate_up_projection.py:739, mlp_tkg_down_projection.py:498-502);
+ * each output is acc * scale + bias before the activation / affinity.
+ * Selective mode only (mkd_moe_tkg); round_qwen must be 0.
  * ------------------------------------------------------------------------- */
 typedef struct {
   const void* hidden;          /* [T, H] bf16                    */
@@ -191,9 +202,9 @@ typedef struct {
   float alpha;                 /* swish alpha                    */
   float gate_hi, gate_lo, up_hi, up_lo; /* +-INFINITY = no clamp */
   int round_qwen;
-  int weight_format;           /* 0 bf16, MKD_MX_E4M3, MKD_MX_E2M1 */
-  const void* gate_up_scales;  /* MX: packed scales of gate_up   */
-  const void* down_scales;     /* MX: packed scales of down      */
+  int weight_format;           /* 0 bf16, MKD_MX_E4M3, MKD_MX_E2M1, MKD_FP8_E4M3 */
+  const void* gate_up_scales;  /* MX: packed scales of gate_up; FP8: fp32 [E, 2 I]  */
+  const void* down_scales;     /* MX: packed scales of down; FP8: fp32 [E, H]       */
 } mkd_moe_args;
 size_t mkd_moe_workspace_bytes(int T, int H, int E, int I, int K);
 int mkd_moe_tkg(const mkd_moe_args* args, void* workspace, size_t workspace_bytes, void* stream);
@@ -311,11 +322,12 @@ typedef struct {
 #define MKD_KV_FP8 1
 #define MKD_KV_K_TRANSPOSED 2
 size_t mkd_attention_workspace_bytes(int B, int H, int nq, int nkv, int d, int S_max);
-/* e4m3 weights for the static FP8 projections: src [K, N] codes (the
- * reference's [in, out] layout: W_qkv [H, I], W_out [nq d, H]; N % 16 == 0,
- * K % 32 == 0) -> dst of mkd_packed_fp8_bytes(N, K) bytes (device). */
-size_t mkd_packed_fp8_bytes(int N, int K);
-int mkd_pack_fp8_weights(const void* src, void* dst, int N, int K, void* stream);
+/* e4m3 weights for the static FP8 projections and the FP8 experts: src G
+ * contiguous [K, N] code matrices (the reference's [in, out] layouts: W_qkv
+ * [H, I], W_out [nq d, H]; experts' gate/up [E, H, 2 I] and down [E, I, H];
+ * N % 16 == 0, K % 32 == 0) -> dst of mkd_packed_fp8_bytes(G, N, K) bytes. */
+size_t mkd_packed_fp8_bytes(int G, int N, int K);
+int mkd_pack_fp8_weights(const void* src, void* dst, int G, int N, int K, void* stream);
 /* The same for s_tkg new tokens per sequence (mkd_attention_args::s_tkg). */
 size_t mkd_attention_workspace_bytes_tkg(int B, int s_tkg, int H, int nq, int nkv, int d, int S_max);
 int mkd_attention_block_tkg(const mkd_attention_args* args, void* workspace,

@@ -26,6 +26,7 @@ DT_BF16, DT_F32 = 0, 1
 ROUTER_SIGMOID, ROUTER_PRE_NORM, ROUTER_NORM_TOPK, ROUTER_QWEN = 1, 2, 4, 8
 ACT_SILU, ACT_SWISH, ACT_GELU, ACT_GELU_TANH = 0, 1, 2, 3
 SCALE_NONE, SCALE_POST = 0, 1
+FP8_E4M3 = 3          # MKD_FP8_E4M3: mkd_moe_args::weight_format of e4m3 experts
 
 
 class MkdLibraryMissing(RuntimeError):
@@ -119,8 +120,8 @@ _SIGS = {
     "mkd_attention_workspace_bytes": (sz, [i32, i32, i32, i32, i32, i32]),
     "mkd_attention_workspace_bytes_tkg": (sz, [i32, i32, i32, i32, i32, i32, i32]),
     "mkd_attention_block_tkg": (i32, [C.POINTER(AttentionArgs), vp, sz, vp]),
-    "mkd_packed_fp8_bytes": (sz, [i32, i32]),
-    "mkd_pack_fp8_weights": (i32, [vp, vp, i32, i32, vp]),
+    "mkd_packed_fp8_bytes": (sz, [i32, i32, i32]),
+    "mkd_pack_fp8_weights": (i32, [vp, vp, i32, i32, i32, vp]),
     "mkd_qwen3_workspace_bytes": (sz, [C.POINTER(Qwen3Model), i32]),
     "mkd_qwen3_route_log_bytes": (sz, [C.POINTER(Qwen3Model), i32]),
     "mkd_qwen3_route_log_layout": (i32, [C.POINTER(Qwen3Model), i32, C.POINTER(sz)]),

@@ -308,6 +308,43 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
     MKD_TRY(moe_route_launch(idx, T, K, E, w.n_groups, w.grp_expert, w.grp_count, w.grp_offset,
                              w.pair_token, w.pair_slot, s), "moe_route");
   const int gmax = E < T * K ? E : T * K;
+  if (wfmt == MKD_FP8_E4M3) {
+    // e4m3 experts (FP8 ROW / STATIC): bf16 activations, per-column dequantisation
+    W8GroupArgs a;
+    memset(&a, 0, sizeof(a));
+    a.g.n_groups = w.n_groups; a.g.grp_expert = w.grp_expert; a.g.grp_count = w.grp_count;
+    a.g.grp_offset = w.grp_offset;
+    a.act.act = act; a.act.alpha = alpha; a.act.gate_hi = ghi; a.act.gate_lo = glo;
+    a.act.up_hi = uhi; a.act.up_lo = ulo;
+    a.w = static_cast<const uint8_t*>(gate_up);
+    a.w_group_stride = 2LL * I * H;
+    a.x = hidden; a.ldx = H; a.N = 2 * I; a.K = H;
+    a.x_row = w.pair_token; a.out_row = w.pair_slot;
+    a.col_scale = static_cast<const float*>(gu_scales);
+    a.bias = gu_bias;
+    a.h = w.hbuf; a.ldy = I;
+    {
+      const int ps = prof_begin(MKD_KCLASS_MOE_GATE_UP, s);
+      MKD_TRY(gemm_w8_grouped_launch(a, W8_SWIGLU, gmax, s), "moe gate_up (fp8)");
+      prof_end(ps, s);
+    }
+    a.w = static_cast<const uint8_t*>(down);
+    a.w_group_stride = (long long)H * I;
+    a.x = w.hbuf; a.ldx = I; a.N = H; a.K = I;
+    a.x_row = w.pair_slot;
+    a.col_scale = static_cast<const float*>(dn_scales);
+    a.bias = dn_bias;
+    a.pair_scale = slot_w;
+    a.h = nullptr; a.y = w.ybuf; a.ldy = H;
+    {
+      const int ps = prof_begin(MKD_KCLASS_MOE_DOWN, s);
+      MKD_TRY(gemm_w8_grouped_launch(a, W8_SCALE, gmax, s), "moe down (fp8)");
+      prof_end(ps, s);
+    }
+    if (do_finalize)
+      MKD_TRY(moe_finalize_launch(w.ybuf, T, K, H, resid, out, out_f32, s), "moe finalize");
+    return MKD_OK;
+  }
   if (wfmt) {
     // MX experts: hidden -> MXFP8, gate/up (scaled MFMA) + SwiGLU -> bf16 h,
     // h -> MXFP8, down (scaled MFMA) * slot affinity.
@@ -619,7 +656,11 @@ int moe_entry(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, vo
   }
   MKD_REQUIRE(p->E > 0 && p->E <= 512 && p->K >= 1 && p->K <= 8 && p->K <= p->E, MKD_ERR_INVALID,
               "moe_tkg: bad E=%d / K=%d", p->E, p->K);
-  if (p->weight_format) {
+  if (p->weight_format == MKD_FP8_E4M3) {
+    MKD_REQUIRE(!tiled, MKD_ERR_UNSUPPORTED, "moe_prefill: bf16 expert weights only");
+    MKD_REQUIRE(p->H % 32 == 0 && p->I % 32 == 0, MKD_ERR_INVALID,
+                "moe_tkg: fp8 experts need H (%d) and I (%d) multiples of 32", p->H, p->I);
+  } else if (p->weight_format) {
     if (int rc = check_mx_dims(2 * p->I, p->H, 2)) return rc;
     if (int rc = check_mx_dims(p->H, p->I, 1)) return rc;
   } else {
@@ -633,10 +674,11 @@ int moe_entry(const mkd_moe_args* p, void* workspace, size_t workspace_bytes, vo
   MKD_REQUIRE(p->activation >= MKD_ACT_SILU && p->activation <= MKD_ACT_GELU_TANH, MKD_ERR_UNSUPPORTED,
               "moe_tkg: unsupported activation %d", p->activation);
   MKD_REQUIRE(p->weight_format == 0 || p->weight_format == MKD_MX_E4M3 ||
-                  p->weight_format == MKD_MX_E2M1, MKD_ERR_INVALID,
+                  p->weight_format == MKD_MX_E2M1 || p->weight_format == MKD_FP8_E4M3, MKD_ERR_INVALID,
               "moe_tkg: unknown weight_format %d", p->weight_format);
   if (p->weight_format) {
-    MKD_REQUIRE(p->gate_up_scales && p->down_scales, MKD_ERR_NULL, "moe_tkg: MX weights need their scales");
+    MKD_REQUIRE(p->gate_up_scales && p->down_scales, MKD_ERR_NULL,
+                "moe_tkg: MX / fp8 weights need their scales");
     MKD_REQUIRE(!p->round_qwen, MKD_ERR_UNSUPPORTED, "moe_tkg: round_qwen applies to bf16 weights only");
   }
   MKD_REQUIRE(workspace, MKD_ERR_NULL, "moe_tkg: null workspace");
@@ -1023,16 +1065,16 @@ static int validate_attn(const mkd_attention_args* p) {
   return MKD_OK;
 }
 
-size_t mkd_packed_fp8_bytes(int N, int K) {
-  return (N > 0 && K > 0) ? (size_t)N * K : 0;
+size_t mkd_packed_fp8_bytes(int G, int N, int K) {
+  return (G > 0 && N > 0 && K > 0) ? (size_t)G * N * K : 0;
 }
 
-int mkd_pack_fp8_weights(const void* src, void* dst, int N, int K, void* stream) {
+int mkd_pack_fp8_weights(const void* src, void* dst, int G, int N, int K, void* stream) {
   if (int rc = stale_check("mkd_pack_fp8_weights")) return rc;
   MKD_REQUIRE(src && dst, MKD_ERR_NULL, "pack_fp8_weights: null pointer");
-  MKD_REQUIRE(N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0, MKD_ERR_INVALID,
-              "pack_fp8_weights: N %d must be a multiple of 16 and K %d of 32", N, K);
-  MKD_TRY(w8_pack_launch(static_cast<const uint8_t*>(src), N, K, static_cast<uint8_t*>(dst),
+  MKD_REQUIRE(G > 0 && N > 0 && K > 0 && N % 16 == 0 && K % 32 == 0, MKD_ERR_INVALID,
+              "pack_fp8_weights: G %d > 0, N %d a multiple of 16 and K %d of 32 required", G, N, K);
+  MKD_TRY(w8_pack_launch(static_cast<const uint8_t*>(src), G, N, K, static_cast<uint8_t*>(dst),
                          static_cast<hipStream_t>(stream)), "pack fp8 weights");
   return MKD_OK;
 }

@@ -26,6 +26,7 @@
 #include "common.h"
 #include "fp8.h"
 #include "mkd_internal.h"
+#include "gemm_epi.h"
 
 namespace mkd {
 
@@ -52,16 +53,19 @@ __global__ void __launch_bounds__(256) w8_quant_kernel(const uint16_t* __restric
   st16(xq + i, o);
 }
 
-// W [K, N] e4m3 codes (row-major, the reference's [in, out] layout) -> frag
-// packed [N/16][K/32][64][8]; one thread per lane-fragment (8 bytes).
-__global__ void __launch_bounds__(256) w8_pack_kernel(const uint8_t* __restrict__ src, int N, int K,
-                                                      uint8_t* __restrict__ dst) {
+// G x W [K, N] e4m3 codes (row-major, the reference's [in, out] layout) ->
+// frag packed [G][N/16][K/32][64][8]; one thread per lane-fragment (8 bytes).
+__global__ void __launch_bounds__(256) w8_pack_kernel(const uint8_t* __restrict__ src, int G, int N,
+                                                      int K, uint8_t* __restrict__ dst) {
   const long long i = (long long)blockIdx.x * 256 + threadIdx.x;
   const int KB = K / 32;
-  if (i >= (long long)(N / 16) * KB * 64) return;
-  const int l = (int)(i % 64);
-  const long long fk = i / 64;
+  const long long per = (long long)(N / 16) * KB * 64;
+  if (i >= per * G) return;
+  const long long gi = i / per, li = i % per;
+  const int l = (int)(li % 64);
+  const long long fk = li / 64;
   const int kb = (int)(fk % KB), rb = (int)(fk / KB);
+  src += gi * (long long)K * N;
   const int n = rb * 16 + (l & 15), k0 = kb * 32 + (l >> 4) * 8;
   uint32_t w0 = 0, w1 = 0;
 #pragma unroll
@@ -135,10 +139,10 @@ __global__ void __launch_bounds__(256) gemm_w8_kernel(W8Args a) {
   }
 }
 
-hipError_t w8_pack_launch(const uint8_t* src, int N, int K, uint8_t* dst, hipStream_t s) {
-  if (N % 16 || K % 32 || N <= 0 || K <= 0) return hipErrorInvalidValue;
-  const long long n = (long long)(N / 16) * (K / 32) * 64;
-  hipLaunchKernelGGL(w8_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, N, K, dst);
+hipError_t w8_pack_launch(const uint8_t* src, int G, int N, int K, uint8_t* dst, hipStream_t s) {
+  if (N % 16 || K % 32 || N <= 0 || K <= 0 || G <= 0) return hipErrorInvalidValue;
+  const long long n = (long long)G * (N / 16) * (K / 32) * 64;
+  hipLaunchKernelGGL(w8_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, src, G, N, K, dst);
   return hipGetLastError();
 }
 
@@ -159,6 +163,102 @@ hipError_t gemm_w8_launch(const W8Args& a, uint16_t* xq, hipStream_t s) {
   else if (tt == 2) hipLaunchKernelGGL((gemm_w8_kernel<2>), grid, dim3(256), 0, s, b);
   else if (tt <= 4) hipLaunchKernelGGL((gemm_w8_kernel<4>), grid, dim3(256), 0, s, b);
   else hipLaunchKernelGGL((gemm_w8_kernel<8>), grid, dim3(256), 0, s, b);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Routed experts with e4m3 weights (moe_tkg's FP8 ROW and STATIC modes,
+// moe_tkg.py:119-131, 296-328; mlp_tkg_gate_up_projection.py:188-275, 847-900;
+// mlp_tkg_down_projection.py:418-560): bf16 activations times e4m3 weights,
+// fp32 accumulation, each output column dequantised by its weight scale
+// (col_scale [E][N]: the per-column ROW scales, or a STATIC expert's scalar per
+// gate / up half) before the bias.  The reference's input scales of these
+// modes select the mode only; its expert kernels do not quantise the
+// activations.
+//
+// Block (i-block ib, routed group g), 4 waves over K quarters, token tiles of
+// 16 of the group in turn.  Gate / up (W8_SWIGLU): the block owns gate rows
+// 16 ib .. +16 and the matching up rows I + 16 ib .., so one lane holds the
+// gate and up values of an (i, token) pair; h = act(gate) * up (bf16) goes to
+// the pair's slot row.  Down (W8_SCALE): rows 16 ib .. +16 of H, times the
+// pair's affinity, fp32 into the slot row (moe_finalize sums the K slots).
+template <int EPI>
+__global__ void __launch_bounds__(256) gemm_w8_grouped_kernel(W8GroupArgs a) {
+  constexpr int RB = EPI == W8_SWIGLU ? 2 : 1;
+  __shared__ f32x4_t red[4][RB][64];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int ib = blockIdx.x, g = blockIdx.y;
+  if (g >= *a.g.n_groups) return;
+  const int e = a.g.grp_expert[g], count = a.g.grp_count[g], base = a.g.grp_offset[g];
+  const int KB = a.K / 32, kb0 = w * KB / 4, kb1 = (w + 1) * KB / 4;
+  const int rbs[2] = {ib, EPI == W8_SWIGLU ? ib + a.N / 32 : ib};   // gate / up row blocks
+  const uint8_t* we = a.w + (long long)e * a.w_group_stride;
+  const int c = lane & 15;
+  for (int t0 = 0; t0 < count; t0 += 16) {
+    if (t0) __syncthreads();               // the previous tile's reduction buffer is free
+    const int p = t0 + c < count ? base + t0 + c : -1;
+    const int xr = p >= 0 ? a.x_row[p] : 0;
+    const uint16_t* xp = a.x + (long long)xr * a.ldx + (lane >> 4) * 8;
+    f32x4_t acc[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int f0 = kb0; f0 < kb1; f0 += kW8MaxF) {
+      uint2 wf[RB][kW8MaxF];
+      u32x4_t xv[kW8MaxF];
+#pragma unroll
+      for (int u = 0; u < kW8MaxF; ++u) {
+        const int kb = min(f0 + u, kb1 - 1);
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+          wf[r][u] = *reinterpret_cast<const uint2*>(we + ((long long)rbs[r] * KB + kb) * 512 + lane * 8);
+        xv[u] = ld16(xp + kb * 32);
+      }
+#pragma unroll
+      for (int u = 0; u < kW8MaxF; ++u) {
+        if (f0 + u >= kb1) break;
+        const u32x4_t xu = p >= 0 ? xv[u] : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int r = 0; r < RB; ++r) acc[r] = mfma16x16x32(w8_widen(wf[r][u]), xu, acc[r]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) red[w][r][lane] = acc[r];
+    __syncthreads();
+    if (w == 0 && p >= 0) {
+      const int slot = a.out_row[p];
+      f32x4_t v[RB];
+#pragma unroll
+      for (int r = 0; r < RB; ++r) v[r] = ((red[0][r][lane] + red[1][r][lane]) + red[2][r][lane]) + red[3][r][lane];
+      const float* cs = a.col_scale + (long long)e * a.N;
+      const uint16_t* bp = a.bias ? a.bias + (long long)e * a.N : nullptr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int n = ib * 16 + (lane >> 4) * 4 + i;   // gate / down row (up: n + N / 2)
+        if constexpr (EPI == W8_SWIGLU) {
+          const int I = a.N / 2;
+          const float gv = v[0][i] * cs[n] + (bp ? bf2f(bp[n]) : 0.f);
+          const float uv = v[1][i] * cs[I + n] + (bp ? bf2f(bp[I + n]) : 0.f);
+          a.h[(long long)slot * a.ldy + n] = (uint16_t)f2bf(swiglu_value(a.act, gv, uv));
+        } else {
+          const float sc = a.pair_scale ? a.pair_scale[slot] : 1.0f;
+          a.y[(long long)slot * a.ldy + n] = (v[0][i] * cs[n] + (bp ? bf2f(bp[n]) : 0.f)) * sc;
+        }
+      }
+    }
+  }
+}
+
+hipError_t gemm_w8_grouped_launch(const W8GroupArgs& a, int epi, int groups_max, hipStream_t s) {
+  if (a.K % 32 || a.N % 16 || (epi == W8_SWIGLU && a.N % 32) || groups_max <= 0 || !a.w ||
+      !a.x || !a.col_scale || !a.g.n_groups || !a.x_row || !a.out_row || (a.ldx & 7))
+    return hipErrorInvalidValue;
+  if (epi == W8_SWIGLU) {
+    if (!a.h) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gemm_w8_grouped_kernel<W8_SWIGLU>, dim3(a.N / 32, groups_max), dim3(256), 0, s, a);
+  } else {
+    if (!a.y) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(gemm_w8_grouped_kernel<W8_SCALE>, dim3(a.N / 16, groups_max), dim3(256), 0, s, a);
+  }
   return hipGetLastError();
 }
 

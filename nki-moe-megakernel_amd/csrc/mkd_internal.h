@@ -327,9 +327,29 @@ struct W8Args {
   uint16_t* y_bf16;
   int ldy;
 };
-hipError_t w8_pack_launch(const uint8_t* src, int N, int K, uint8_t* dst, hipStream_t s);
+hipError_t w8_pack_launch(const uint8_t* src, int G, int N, int K, uint8_t* dst, hipStream_t s);
 // quantises x into xq ([T, K] bf16 scratch), then the GEMM (T <= 128)
 hipError_t gemm_w8_launch(const W8Args& a, uint16_t* xq, hipStream_t s);
+// routed experts with e4m3 weights (moe_tkg FP8 ROW / STATIC): gate/up + gated
+// activation -> bf16 h rows (W8_SWIGLU), down x affinity -> fp32 slot rows (W8_SCALE)
+enum { W8_SWIGLU = 0, W8_SCALE = 1 };
+struct W8GroupArgs {
+  const uint8_t* w;           // packed e4m3 [E][N/16][K/32][64][8]
+  long long w_group_stride;   // bytes per expert (N * K)
+  const uint16_t* x;          // bf16 rows [.., ldx]
+  int ldx, N, K;              // N: 2I (gate rows, then up rows) or H
+  const int* x_row;           // x row of pair p
+  const int* out_row;         // output row (slot) of pair p
+  GemmArgs g;                 // routing tables: n_groups, grp_expert, grp_count, grp_offset
+  GemmArgs act;               // activation fields (act, alpha, clamps; round_qwen 0)
+  const float* col_scale;     // [E][N] fp32 dequantisation scale per output column
+  const uint16_t* bias;       // [E][N] bf16 or null
+  const float* pair_scale;    // W8_SCALE: affinity per slot (null = 1)
+  uint16_t* h;                // W8_SWIGLU: [slots, ldy] bf16 (ldy = I)
+  float* y;                   // W8_SCALE: [slots, ldy] fp32 (ldy = H)
+  int ldy;
+};
+hipError_t gemm_w8_grouped_launch(const W8GroupArgs& a, int epi, int groups_max, hipStream_t s);
 // Attention, chunk combine and output projection in one launch (attn_mfma.hip,
 // attn_joined_kernel): the chunk blocks, then the combine blocks, then the
 // projection blocks of one grid, each stage waiting on the flags of the blocks

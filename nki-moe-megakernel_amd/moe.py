@@ -106,7 +106,7 @@ def router_topk(x: torch.Tensor, w: torch.Tensor, w_bias: Optional[torch.Tensor]
     return out
 
 
-def moe_tkg(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
+def _moe_selective(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
             expert_down_weights: torch.Tensor, expert_affinities: torch.Tensor,
             expert_index: torch.Tensor, is_all_expert: bool,
             rank_id: Optional[torch.Tensor] = None,
@@ -126,7 +126,7 @@ def moe_tkg(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
             up_clamp_upper_limit: Optional[float] = None,
             up_clamp_lower_limit: Optional[float] = None, output_in_sbuf: bool = False,
             is_all_expert_dynamic: bool = False, block_size: int = None,
-            name_prefix: str = "", _prefill: bool = False) -> torch.Tensor:
+            name_prefix: str = "", prefill: bool = False) -> torch.Tensor:
     """Selective-expert MoE for decode; returns output [T, H].
 
     hidden_input [T, H] bf16; expert_gate_up_weights [E, H, 2, I] bf16 (or
@@ -149,15 +149,23 @@ def moe_tkg(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
         raise ValueError("hidden_input_scale is only supported with MX weights in all-expert mode")
     if output_in_sbuf:
         raise NotImplementedError("output_in_sbuf has no GPU equivalent")
-    if _mx.is_mx_weight(expert_gate_up_weights):
+    # MX weights come in the reference's MX layouts (more than 4 dims); a 4-D
+    # float8 [E, H, 2, I] tensor with row scales is the FP8 row mode below
+    if _mx.is_mx_weight(expert_gate_up_weights) and expert_gate_up_weights.dim() != 4:
         return _mx.moe_tkg_mx(hidden_input, expert_gate_up_weights, expert_down_weights,
                               expert_affinities, expert_index, expert_gate_up_bias,
                               expert_down_bias, expert_gate_up_weights_scale,
                               expert_down_weights_scale, expert_affinities_scaling_mode,
                               activation_fn, output_dtype, gate_clamp_upper_limit,
                               gate_clamp_lower_limit, up_clamp_upper_limit, up_clamp_lower_limit)
-    if expert_gate_up_weights_scale is not None or expert_down_weights_scale is not None:
-        raise NotImplementedError("FP8 row quantization is not supported; use bf16 or MX weights")
+    # FP8 row quantisation (moe_tkg.py:119-123, 296-328): e4m3 weights, per-column scales
+    fp8 = expert_gate_up_weights_scale is not None and expert_down_weights_scale is not None
+    if (expert_gate_up_weights_scale is None) != (expert_down_weights_scale is None):
+        raise ValueError("FP8 row quantization needs expert_gate_up_weights_scale and expert_down_weights_scale")
+    if fp8 and prefill:
+        raise NotImplementedError("moe_prefill: bf16 expert weights only")
+    if not fp8 and expert_gate_up_weights.dtype in (torch.float8_e4m3fn, torch.uint8):
+        raise ValueError("float8 expert weights need expert_gate_up_weights_scale / expert_down_weights_scale")
     L.require_gpu(hidden_input, expert_gate_up_weights, expert_down_weights, expert_index)
     T, H = hidden_input.shape
     E, H2, two, I = expert_gate_up_weights.shape
@@ -165,15 +173,28 @@ def moe_tkg(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
         raise ValueError(f"gate_up weights {tuple(expert_gate_up_weights.shape)} do not match [E, {H}, 2, I]")
     if tuple(expert_down_weights.shape) != (E, I, H):
         raise ValueError(f"down weights {tuple(expert_down_weights.shape)} != {(E, I, H)}")
-    if T > 128 and not _prefill:
+    if T > 128 and not prefill:
         raise ValueError("Currently only batch size * seq len <= 128 is supported (except for all-expert mode)")
     K = expert_index.shape[-1]
     act = {ActFnType.SiLU: L.ACT_SILU, ActFnType.Swish: L.ACT_SWISH, ActFnType.GELU: L.ACT_GELU,
            ActFnType.GELU_Tanh_Approx: L.ACT_GELU_TANH}.get(activation_fn)
     if act is None:
         raise NotImplementedError(f"activation {activation_fn} is not supported")
-    gu = packing.packed_cached(expert_gate_up_weights, packing.pack_experts_gate_up_ref)
-    dn = packing.packed_cached(expert_down_weights, packing.pack_experts_down_ref)
+    gu_sc = dn_sc = None
+    if fp8:
+        if tuple(expert_gate_up_weights_scale.shape) != (E, 2, I):
+            raise ValueError(f"expert_gate_up_weights_scale must be [E, 2, I] = {(E, 2, I)} for FP8 row "
+                             f"quantization, got {tuple(expert_gate_up_weights_scale.shape)}")
+        if tuple(expert_down_weights_scale.shape) != (E, H):
+            raise ValueError(f"expert_down_weights_scale must be [E, H] = {(E, H)}, got "
+                             f"{tuple(expert_down_weights_scale.shape)}")
+        gu = packing.packed_cached(expert_gate_up_weights, packing.pack_fp8_experts_gate_up)
+        dn = packing.packed_cached(expert_down_weights, packing.pack_fp8_in_out)
+        gu_sc = expert_gate_up_weights_scale.float().reshape(E, 2 * I).contiguous()
+        dn_sc = expert_down_weights_scale.float().contiguous()
+    else:
+        gu = packing.packed_cached(expert_gate_up_weights, packing.pack_experts_gate_up_ref)
+        dn = packing.packed_cached(expert_down_weights, packing.pack_experts_down_ref)
     dev = hidden_input.device
     out_dtype = output_dtype if output_dtype is not None else hidden_input.dtype
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
@@ -197,15 +218,52 @@ def moe_tkg(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
         gate_lo=gate_clamp_lower_limit if gate_clamp_lower_limit is not None else -inf,
         up_hi=up_clamp_upper_limit if up_clamp_upper_limit is not None else inf,
         up_lo=up_clamp_lower_limit if up_clamp_lower_limit is not None else -inf,
-        round_qwen=0)
+        round_qwen=0, weight_format=L.FP8_E4M3 if fp8 else 0,
+        gate_up_scales=L.ptr(gu_sc), down_scales=L.ptr(dn_sc))
     lib = L.load()
     ws = _ws(lib.mkd_moe_workspace_bytes(T, H, E, I, K), dev)
-    entry = lib.mkd_moe_prefill if _prefill else lib.mkd_moe_tkg
+    entry = lib.mkd_moe_prefill if prefill else lib.mkd_moe_tkg
     rc = entry(args, ws.data_ptr(), ws.numel(), L.stream_ptr(dev))
-    L.check(rc, "moe_prefill" if _prefill else "moe_tkg")
+    L.check(rc, "moe_prefill" if prefill else "moe_tkg")
     if out32 is not None:
         return out32
     return out if out_dtype == torch.bfloat16 else out.to(out_dtype)
+
+
+def moe_tkg(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
+            expert_down_weights: torch.Tensor, expert_affinities: torch.Tensor,
+            expert_index: torch.Tensor, is_all_expert: bool,
+            rank_id: Optional[torch.Tensor] = None,
+            expert_gate_up_bias: Optional[torch.Tensor] = None,
+            expert_down_bias: Optional[torch.Tensor] = None,
+            expert_gate_up_weights_scale: Optional[torch.Tensor] = None,
+            expert_down_weights_scale: Optional[torch.Tensor] = None,
+            hidden_input_scale: Optional[torch.Tensor] = None,
+            gate_up_input_scale: Optional[torch.Tensor] = None,
+            down_input_scale: Optional[torch.Tensor] = None,
+            mask_unselected_experts: bool = False,
+            expert_affinities_eager: Optional[torch.Tensor] = None,
+            expert_affinities_scaling_mode: ExpertAffinityScaleMode = ExpertAffinityScaleMode.NO_SCALE,
+            activation_fn: ActFnType = ActFnType.SiLU, output_dtype=None,
+            gate_clamp_upper_limit: Optional[float] = None,
+            gate_clamp_lower_limit: Optional[float] = None,
+            up_clamp_upper_limit: Optional[float] = None,
+            up_clamp_lower_limit: Optional[float] = None, output_in_sbuf: bool = False,
+            is_all_expert_dynamic: bool = False, block_size: int = None,
+            name_prefix: str = "") -> torch.Tensor:
+    """moe_tkg (moe_tkg.py:56-293), the reference parameter list: selective experts,
+    bf16, MX (mx.py) or FP8 row-quantised e4m3 weights ([E, H, 2, I] / [E, I, H]
+    float8_e4m3 with expert_gate_up_weights_scale [E, 2, I] and
+    expert_down_weights_scale [E, H]: each projection column is dequantised by its
+    scale before the bias; the activations stay bf16).  See _moe_selective."""
+    return _moe_selective(
+        hidden_input, expert_gate_up_weights, expert_down_weights, expert_affinities, expert_index,
+        is_all_expert, rank_id, expert_gate_up_bias, expert_down_bias, expert_gate_up_weights_scale,
+        expert_down_weights_scale, hidden_input_scale, gate_up_input_scale, down_input_scale,
+        mask_unselected_experts, expert_affinities_eager, expert_affinities_scaling_mode,
+        activation_fn, output_dtype, gate_clamp_upper_limit, gate_clamp_lower_limit,
+        up_clamp_upper_limit, up_clamp_lower_limit, output_in_sbuf, is_all_expert_dynamic,
+        block_size, name_prefix)
 
 
 def moe_prefill(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor,
@@ -230,7 +288,7 @@ def moe_prefill(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor
     from . import mx as _mx
     if _mx.is_mx_weight(expert_gate_up_weights):
         raise NotImplementedError("moe_prefill: bf16 expert weights only")
-    return moe_tkg(hidden_input, expert_gate_up_weights, expert_down_weights, expert_affinities,
+    return _moe_selective(hidden_input, expert_gate_up_weights, expert_down_weights, expert_affinities,
                    expert_index, False, expert_gate_up_bias=expert_gate_up_bias,
                    expert_down_bias=expert_down_bias,
                    expert_affinities_scaling_mode=expert_affinities_scaling_mode,
@@ -238,4 +296,4 @@ def moe_prefill(hidden_input: torch.Tensor, expert_gate_up_weights: torch.Tensor
                    gate_clamp_upper_limit=gate_clamp_upper_limit,
                    gate_clamp_lower_limit=gate_clamp_lower_limit,
                    up_clamp_upper_limit=up_clamp_upper_limit,
-                   up_clamp_lower_limit=up_clamp_lower_limit, _prefill=True)
+                   up_clamp_lower_limit=up_clamp_lower_limit, prefill=True)

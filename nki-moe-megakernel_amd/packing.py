@@ -41,18 +41,27 @@ def pack(src: torch.Tensor, groups: int, n: int, k: int, g_stride: int, row_stri
 
 
 def pack_fp8_in_out(w: torch.Tensor) -> torch.Tensor:
-    """float8 e4m3 weights in the reference layout [k_in, n_out] (torch.float8_e4m3fn,
-    or uint8 codes) -> the frag-packed e4m3 layout of the static FP8 projections."""
+    """float8 e4m3 weights in the reference layout [k_in, n_out] (or G such
+    matrices [G, k_in, n_out]; torch.float8_e4m3fn, or uint8 codes) -> the
+    frag-packed e4m3 layout of the FP8 projections and experts."""
     L.require_gpu(w)
     if w.dtype not in (torch.float8_e4m3fn, torch.uint8):
         raise ValueError(f"FP8 weights must be float8_e4m3, got {w.dtype}")
-    k, n = w.shape
+    k, n = w.shape[-2], w.shape[-1]
+    g = w.numel() // (k * n)
     src = w.contiguous().view(torch.uint8)
     lib = L.load()
-    out = torch.empty(lib.mkd_packed_fp8_bytes(n, k), dtype=torch.uint8, device=w.device)
-    rc = lib.mkd_pack_fp8_weights(src.data_ptr(), out.data_ptr(), n, k, L.stream_ptr(w.device))
+    out = torch.empty(lib.mkd_packed_fp8_bytes(g, n, k), dtype=torch.uint8, device=w.device)
+    rc = lib.mkd_pack_fp8_weights(src.data_ptr(), out.data_ptr(), g, n, k, L.stream_ptr(w.device))
     L.check(rc, "pack_fp8_weights")
     return out
+
+
+def pack_fp8_experts_gate_up(w: torch.Tensor) -> torch.Tensor:
+    """FP8 experts' gate/up [E, H, 2, I] e4m3 -> E x packed [H, 2I] (gate columns first)."""
+    E, H, two, I = w.shape
+    assert two == 2
+    return pack_fp8_in_out(w.reshape(E, H, 2 * I))
 
 
 def pack_out_in(w: torch.Tensor) -> torch.Tensor:

@@ -215,6 +215,37 @@ def moe_tkg(hidden: torch.Tensor, gate_up: torch.Tensor, down: torch.Tensor,
     return out
 
 
+def moe_tkg_fp8_row(hidden, gate_up, down, gate_up_scale, down_scale, affinities, index,
+                    gate_up_bias=None, down_bias=None, scaling_mode="none", act="silu",
+                    emulate_bf16=True) -> torch.Tensor:
+    """FP8 row-quantised experts (moe_tkg.py:119-123, 296-328;
+    mlp_tkg_gate_up_projection.py:188-275; mlp_tkg_down_projection.py:418-560):
+    e4m3 weights gate_up [E,H,2,I] / down [E,I,H], fp32 scales gate_up_scale
+    [E,2,I] / down_scale [E,H].  Each projection is accumulated in fp32 over the
+    bf16 activations and the e4m3 weight values, every output column multiplied
+    by its scale, then the bias; the rest as moe_tkg.  Returns fp32 [T, H]."""
+    T, H = hidden.shape
+    K = index.shape[1]
+    x = hidden.float()
+    out = torch.zeros(T, H)
+    for t in range(T):
+        for j in range(K):
+            e = int(index[t, j])
+            g = (x[t] @ gate_up[e, :, 0, :].float()) * gate_up_scale[e, 0].float()
+            u = (x[t] @ gate_up[e, :, 1, :].float()) * gate_up_scale[e, 1].float()
+            if gate_up_bias is not None:
+                g = g + gate_up_bias[e, 0].float()
+                u = u + gate_up_bias[e, 1].float()
+            h = _bf(act_fn_apply(g, act) * u, emulate_bf16)
+            y = (h @ down[e].float()) * down_scale[e].float()
+            if down_bias is not None:
+                y = y + down_bias[e].float()
+            if scaling_mode == "post":
+                y = y * affinities[t, e].float()
+            out[t] += y
+    return out
+
+
 def mx_qdq(x: torch.Tensor, fmt: str = "e4m3") -> torch.Tensor:
     """Quantise the rows of x to MX (blocks of 32 along the last dim) and back to fp32."""
     from . import mx

@@ -316,3 +316,41 @@ def test_attention_static_fp8_projections(mk, dev, B, H, nq, nkv, d, S, P, S_max
     else:
         y_ref = attn @ Wo.float() + (bo.float() if bias else 0.0)
     assert max_abs_rel(out, y_ref) < TOL
+
+
+@pytest.mark.parametrize("T,E,K,H,I,act,bias", [
+    (1, 128, 8, 2048, 768, "silu", False),
+    (5, 16, 4, 512, 128, "silu", True),
+    (40, 32, 4, 256, 64, "swish", True),
+    (128, 8, 2, 128, 32, "gelu", False),
+])
+def test_moe_tkg_fp8_row(mk, dev, T, E, K, H, I, act, bias):
+    """moe_tkg with FP8 row-quantised experts (e4m3 [E, H, 2, I] / [E, I, H],
+    fp32 scales [E, 2, I] / [E, H]) against the oracle; STATIC (input scales)
+    is rejected as by the reference (moe_tkg.py:405-408)."""
+    from nki_moe_megakernel_amd.common_types import ActFnType, ExpertAffinityScaleMode
+    print(f"moe fp8 row: T={T} E={E} K={K} H={H} I={I} act={act}", flush=True)
+    g = torch.Generator().manual_seed(T * 13 + E + H)
+    x = bf(torch.randn(T, H, generator=g))
+    gs = 0.003 * (1 + torch.rand(E, 2, I, generator=g))
+    ds = 0.003 * (1 + torch.rand(E, H, generator=g))
+    gu = ref.kv_fp8_quant(0.03 * torch.randn(E, H, 2, I, generator=g) / gs[:, None, :, :], 1.0)
+    dn = ref.kv_fp8_quant(0.03 * torch.randn(E, I, H, generator=g) / ds[:, None, :], 1.0)
+    idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)]).to(torch.int32)
+    aff = torch.zeros(T, E).scatter_(1, idx.long(), torch.rand(T, K, generator=g))
+    gub = bf(0.1 * torch.randn(E, 2, I, generator=g)) if bias else None
+    dnb = bf(0.1 * torch.randn(E, H, generator=g)) if bias else None
+    actf = {"swish": ActFnType.Swish, "gelu": ActFnType.GELU}.get(act, ActFnType.SiLU)
+    out = mk.moe_tkg(x.to(dev), gu.to(dev), dn.to(dev), aff.to(dev), idx.to(dev), False,
+                     expert_gate_up_bias=gub.to(dev) if bias else None,
+                     expert_down_bias=dnb.to(dev) if bias else None,
+                     expert_gate_up_weights_scale=gs.to(dev), expert_down_weights_scale=ds.to(dev),
+                     expert_affinities_scaling_mode=ExpertAffinityScaleMode.POST_SCALE,
+                     activation_fn=actf)
+    y_ref = ref.moe_tkg_fp8_row(x, gu, dn, gs, ds, aff, idx.long(), gub, dnb, "post", act)
+    assert out.shape == (T, H)
+    assert max_abs_rel(out, y_ref) < TOL
+    with pytest.raises(ValueError, match="Static quantization"):
+        mk.moe_tkg(x.to(dev), gu.to(dev), dn.to(dev), aff.to(dev), idx.to(dev), False,
+                   expert_gate_up_weights_scale=gs[:, :, :1].to(dev), expert_down_weights_scale=ds[:, :1].to(dev),
+                   gate_up_input_scale=torch.ones(E, 1, device=dev), down_input_scale=torch.ones(E, 1, device=dev))

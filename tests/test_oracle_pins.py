@@ -695,3 +695,29 @@ def test_static_fp8_qkv_segments_map_to_q_k_v():
                                         Kc.clone(), 2 * Vc, mask, None, False, upd, None, None,
                                         softmax_scale=s, qkv_static=([1.0, 1.0, 2.0], 1.0))
     assert torch.allclose(o_v, 2 * base, rtol=1e-4, atol=1e-5)
+
+
+def test_fp8_row_experts_equal_experts_on_dequantised_weights():
+    """Per-column dequantisation commutes with the projection: the FP8 row-
+    quantised experts equal the bf16-flow experts on weights * column scale (the
+    gate and up halves scaled by their own [E, 2, I] rows, down by [E, H]).  With
+    unit scales they equal the experts on the e4m3 values.  A scale applied to
+    the wrong axis (rows instead of columns, or the gate scale on up) fails."""
+    g = torch.Generator().manual_seed(29)
+    T, E, K, H, I = 3, 6, 2, 64, 32
+    x = torch.randn(T, H, generator=g).to(torch.bfloat16)
+    gu = ref.kv_fp8_quant(10 * torch.randn(E, H, 2, I, generator=g), 1.0)
+    dn = ref.kv_fp8_quant(10 * torch.randn(E, I, H, generator=g), 1.0)
+    gs = 0.003 * (1 + torch.rand(E, 2, I, generator=g))
+    ds = 0.003 * (1 + torch.rand(E, H, generator=g))
+    idx = torch.stack([torch.randperm(E, generator=g)[:K] for _ in range(T)])
+    aff = torch.zeros(T, E).scatter_(1, idx, torch.rand(T, K, generator=g))
+    gub = 0.1 * torch.randn(E, 2, I, generator=g)
+    y = ref.moe_tkg_fp8_row(x, gu, dn, gs, ds, aff, idx, gub, None, "post")
+    y_deq = ref.moe_tkg(x, gu.float() * gs[:, None, :, :], dn.float() * ds[:, None, :], aff, idx,
+                        gub, None, "post")
+    assert torch.allclose(y, y_deq, rtol=1e-4, atol=1e-5 * y.abs().max().item())
+    y1 = ref.moe_tkg_fp8_row(x, gu, dn, torch.ones(E, 2, I), torch.ones(E, H), aff, idx)
+    assert torch.allclose(y1, ref.moe_tkg(x, gu.float(), dn.float(), aff, idx), rtol=1e-5, atol=1e-4)
+    y_swapped = ref.moe_tkg_fp8_row(x, gu, dn, gs.flip(1), ds, aff, idx, gub, None, "post")
+    assert not torch.allclose(y_swapped, y, rtol=1e-2, atol=1e-3 * y.abs().max().item())
