@@ -788,7 +788,7 @@ static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_
   // the QKV projection of 17..128 tokens comes as split-K partials
   const int qparts = std::max({1, gemm_mid_kgrid((nq + 2 * nkv) * d, H, B),
                                (qkv_norm_supported(B, (nq + 2 * nkv) * d, H) &&
-                                qkv_norm_extra_tiles((nq + 2 * nkv) * d, H)) ? 4 : 1});
+                                qkv_norm_extra_tiles((nq + 2 * nkv) * d, H, d)) ? 4 : 1});
   w.qkv = c.take<float>((size_t)qparts * B * (nq + 2 * nkv) * d);
   w.attn = c.take<uint16_t>((size_t)B * nq * d);
   w.kvn = c.take<uint16_t>((size_t)B * 2 * nkv * d);
@@ -838,13 +838,13 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
   if (qn) {
     QkvNormArgs q = *qn;
     q.w = static_cast<const uint16_t*>(p->w_qkv_packed);
-    q.N = qkv_n; q.K = p->H; q.T = rows;
+    q.N = qkv_n; q.K = p->H; q.T = rows; q.d = p->d;
     q.y = w.qkv; q.ldy = qkv_n;
     q.part_stride = (long long)rows * qkv_n;
     const int ps = prof_begin(MKD_KCLASS_QKV, s);
     MKD_TRY(qkv_norm_launch(q, s), "qkv + norm");
     prof_end(ps, s);
-    if (const int xt = qkv_norm_extra_tiles(qkv_n, p->H)) {   // the last tiles as K quarters
+    if (const int xt = qkv_norm_extra_tiles(qkv_n, p->H, p->d)) {   // the last tiles as K quarters
       qkv_parts = 4;
       qkv_split_row = (qkv_n / 16 - xt) * 16;
     }

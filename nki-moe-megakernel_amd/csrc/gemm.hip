@@ -25,6 +25,7 @@
 #include "mkd_internal.h"
 #include "router_select.h"
 #include "coherent.h"
+#include "poll_word.h"
 
 namespace mkd {
 
@@ -381,8 +382,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   }
   // the group's h rows (count <= kFusedMaxRows, K = 64 NFD) into LDS with one
   // device-coherent 16-byte load per thread, then the B operands from LDS; with
-  // the data-polled h, loaded until no 16-bit word reads 0xffff (the empty
-  // marker; bounded like the flag waits)
+  // the data-polled h, loaded until no 16-bit word reads the empty marker (the
+  // gate/up epilogue never stores it), bounded like the flag waits: the block
+  // gives up together once its own polls ran out or another wait already did
   {
     const __amdgpu_buffer_rsrc_t hr = coh_rsrc(d.x);
     const int per_row = d.K / 8;                       // 16-byte pieces per row
@@ -394,14 +396,11 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
         const u32x4_t v = coh_ld16(hr, (int)(((long long)row * d.ldx + pc * 8) * 2));
         s_h[rr][pc] = v;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) miss |= (v[e] & 0xffffu) == 0xffffu || (v[e] >> 16) == 0xffffu;
+        for (int e = 0; e < 4; ++e) miss |= poll_bf16x2_empty(v[e]);
       }
       if (!f.poll_h) break;
       if (!__syncthreads_or(miss)) break;
-      if (it >= kCohSpinLimit) {
-        if (threadIdx.x == 0) coh_store(f.err, 1u);
-        break;
-      }
+      if (__syncthreads_or(threadIdx.x == 0 && coh_poll_giveup(it, f.err))) break;
       __builtin_amdgcn_s_sleep(1);
     }
   }

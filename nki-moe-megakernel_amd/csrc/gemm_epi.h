@@ -14,6 +14,7 @@
 #include "common.h"
 #include "mkd_internal.h"
 #include "coherent.h"
+#include "poll_word.h"
 
 namespace mkd {
 
@@ -128,14 +129,16 @@ MKD_DEV void gemm_finish(const GemmArgs& a, f32x4_t (&acc)[RB][TN], int lane, in
       }
     } else {
       uint16_t* y = reinterpret_cast<uint16_t*>(a.y) + (long long)orow * a.ldy + n0;
-      if (COH) {   // read back by other blocks of this launch
+      if (COH) {   // read back by other blocks of this launch, which may poll these
+        // words for the empty marker: a NaN whose bits equal it is stored as the quiet NaN
         const __amdgpu_buffer_rsrc_t yr = coh_rsrc(a.y);
         const int off = (int)(((long long)orow * a.ldy + n0) * 2);
         if (vec) {
-          coh_st8(yr, off, pack2bf(o[0], o[1]), pack2bf(o[2], o[3]));
+          coh_st8(yr, off, poll_safe_bf16x2(pack2bf(o[0], o[1])), poll_safe_bf16x2(pack2bf(o[2], o[3])));
         } else {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) if (i < nv) coh_st2(yr, off + 2 * i, (uint16_t)f2bf(o[i]));
+          for (int i = 0; i < 4; ++i)
+            if (i < nv) coh_st2(yr, off + 2 * i, (uint16_t)poll_safe_bf16x2(f2bf(o[i])));
         }
       } else if (vec) {
         *reinterpret_cast<uint2*>(y) = uint2{pack2bf(o[0], o[1]), pack2bf(o[2], o[3])};

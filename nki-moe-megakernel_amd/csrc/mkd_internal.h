@@ -197,13 +197,14 @@ struct QkvNormArgs {
   float* y;                   // [T, ldy] fp32 projections
   int ldy;
   long long part_stride;      // elements between the K-quarter partials of the extra tiles
+  int d;                      // head size (the K-quarter split starts on a head boundary)
   int n_main, n_extra;        // set by qkv_norm_launch
 };
 bool qkv_norm_supported(int T, int N, int K);
 hipError_t qkv_norm_launch(const QkvNormArgs& a, hipStream_t s);
 // 16-row tiles past one per CU, written as 4 K-quarter partials (0: none); rows
 // from (N / 16 - extra) * 16 on then come as 4 partials at part_stride
-int qkv_norm_extra_tiles(int N, int K);
+int qkv_norm_extra_tiles(int N, int K, int d);   // launch_rules.h qkv_extra_tiles_rule on this device
 
 // norm.hip
 struct NormArgs {

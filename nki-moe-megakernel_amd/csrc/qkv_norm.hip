@@ -15,6 +15,7 @@
 // QKV projection of the next; block 0 also writes x, the new residual stream.
 #include "common.h"
 #include "mkd_internal.h"
+#include "launch_rules.h"
 
 namespace mkd {
 
@@ -192,18 +193,13 @@ bool qkv_norm_supported(int T, int N, int K) {
          T * K <= kQnThreads * 8;
 }
 
-int qkv_norm_extra_tiles(int N, int K) {
-  const int tiles = N / 16, cus = device_cus(), nf = K / 32 / kQnWaves;
-  if (cus <= 0 || tiles <= cus || nf > 8) return 0;
-  const int extra = tiles - cus;
-  return extra * 4 <= cus ? extra : 0;
-}
+int qkv_norm_extra_tiles(int N, int K, int d) { return qkv_extra_tiles_rule(N, K, d, device_cus()); }
 
 hipError_t qkv_norm_launch(const QkvNormArgs& ain, hipStream_t s) {
   QkvNormArgs a = ain;
   if (!qkv_norm_supported(a.T, a.N, a.K) || (a.dsum && (a.dK < 1 || a.dK > kQnMaxDK)))
     return hipErrorInvalidValue;
-  a.n_extra = qkv_norm_extra_tiles(a.N, a.K);
+  a.n_extra = qkv_norm_extra_tiles(a.N, a.K, a.d);
   a.n_main = a.N / 16 - a.n_extra;
   if (a.n_extra && a.part_stride < (long long)a.T * a.ldy) return hipErrorInvalidValue;
   const dim3 grid(a.n_main), block(kQnThreads + (a.n_extra ? 128 : 0));

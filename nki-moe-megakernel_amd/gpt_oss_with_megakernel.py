@@ -32,8 +32,8 @@ from torch import nn
 
 from . import _lib as L
 from . import packing
-from .qwen_with_megakernel import (EXPERT_FORMATS, _LayerStack, _prefill, pack_experts_mx, randn_bf16,
-                                   tensor_seed)
+from .qwen_with_megakernel import (EXPERT_FORMATS, _LayerStack, _prefill, check_waits, pack_experts_mx,
+                                   randn_bf16, tensor_seed)
 
 VARIANT_GPT_OSS = 1
 
@@ -390,6 +390,7 @@ class GptOssMegakernelModel(_LayerStack, nn.Module):
             if S != 1:
                 raise NotImplementedError("token generation takes one token per sequence")
             self.decode_layers(hidden, pos.reshape(-1).contiguous())
+            check_waits(self, B, self.ws)
         else:
             from .qwen_with_megakernel import prefill_rows
             hv = hidden.reshape(B, S, Hp)
@@ -401,6 +402,8 @@ class GptOssMegakernelModel(_LayerStack, nn.Module):
                     row = hv[b, t:t + 1].contiguous()
                     prefill_rows(self, row, int(pc[b, t]), b, rope=lambda p: self.rope_cos_sin(p))
                     hv[b, t] = row[0]
+                    if self.route_log_history is not None:
+                        self.route_log_history.append(self.route_log(1))
         normed = torch.empty_like(hidden)
         L.check(L.load().mkd_rmsnorm_tkg(hidden.data_ptr(), L.DT_BF16, self.ln_f.data_ptr(),
                                          normed.data_ptr(), L.DT_BF16, B * S, Hp, cfg.hidden_size,

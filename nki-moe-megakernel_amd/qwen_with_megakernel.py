@@ -245,6 +245,11 @@ class _LayerStack:
     """Shared by the Qwen3 and GPT-OSS models: a view of a contiguous range of
     the layers, and the routing log (what each layer's router produced)."""
 
+    # A list here (with the routing log enabled) collects route_log(1) after every
+    # one-token pass of a token-by-token context encoding, in pass order
+    # (synchronises per pass; for tests that route an oracle like the GPU).
+    route_log_history: Optional[list] = None
+
     def decode_plan(self, batch: Optional[int] = None) -> str:
         """The decode path for this batch under the current mode: "persistent",
         "joined_experts" (multi-kernel layers, gate/up and down in one launch) or
@@ -467,14 +472,36 @@ class Qwen3MoeMegakernelModel(_LayerStack, nn.Module):
                         self.cfg.hidden_size, 2, lambda pos: (None, None))
 
     def forward(self, input_ids: torch.Tensor, position_ids: torch.Tensor):
-        """Greedy decode step: input_ids [B] -> (logits [B, V] fp32, next ids [B] int32)."""
+        """Greedy decode step: input_ids [B] -> (logits [B, V] fp32, next ids [B] int32).
+        Synchronises and raises RuntimeError when an in-launch wait of the step ran
+        out (the step's results are then invalid); `step` is the graph-capturable
+        form without that check."""
         B = input_ids.shape[0]
         hidden = torch.empty(B, self.cfg.hidden_size, dtype=torch.bfloat16, device=self.device)
         logits = torch.empty(B, self.cfg.vocab_size, dtype=torch.float32, device=self.device)
         nxt = torch.empty(B, dtype=torch.int32, device=self.device)
         self.step(input_ids.to(torch.int32).contiguous(), position_ids.to(torch.int32).contiguous(),
                   hidden, logits, nxt)
+        check_waits(self, B, self.ws)
         return logits, nxt
+
+
+# Passes of more tokens than this plan no in-launch waits (the joined launches
+# and the persistent kernel take at most 4 tokens).
+_MAX_WAIT_TOKENS = 4
+
+
+def check_waits(model, B: int, ws: torch.Tensor, struct=None):
+    """Raise RuntimeError when an in-launch wait of the last decode / prefill call
+    of B tokens on workspace `ws` ran out of polls (a grid barrier, a flag or a
+    data-polled exchange): the kernels then drain but that call's results are
+    invalid.  Synchronises the device."""
+    used, timeout = C.c_int32(0), C.c_int32(0)
+    L.check(L.load().mkd_qwen3_layer_kernel_status(struct or model._model, B, ws.data_ptr(), ws.numel(),
+                                                   C.byref(used), C.byref(timeout)),
+            "qwen3_layer_kernel_status")
+    if timeout.value:
+        raise RuntimeError("an in-launch wait of the decode layers timed out: the step's results are invalid")
 
 
 def prefill_rows(model, hidden: torch.Tensor, start_pos: int, seq: int = 0, layers=None, rope=None):
@@ -503,6 +530,8 @@ def prefill_rows(model, hidden: torch.Tensor, start_pos: int, seq: int = 0, laye
     L.check(lib.mkd_qwen3_prefill_layers(st, seq, T, hidden.data_ptr(), pos.data_ptr(), L.ptr(cos),
                                          L.ptr(sin), ws.data_ptr(), ws.numel(),
                                          L.stream_ptr(model.device)), "qwen3_prefill_layers")
+    if T <= _MAX_WAIT_TOKENS:
+        check_waits(model, T, ws, st)
     return hidden
 
 
@@ -536,6 +565,8 @@ def _prefill(model, input_ids, start_pos, seq, chunk, H, h_actual, norm_order, r
         L.check(lib.mkd_qwen3_prefill_layers(model._model, seq, n, h.data_ptr(), pos.data_ptr(),
                                              L.ptr(cos), L.ptr(sin), ws.data_ptr(), ws.numel(), s),
                 "qwen3_prefill_layers")
+        if n <= _MAX_WAIT_TOKENS:
+            check_waits(model, n, ws)
     logits = torch.empty(1, V, dtype=torch.float32, device=model.device)
     nxt = torch.empty(1, dtype=torch.int32, device=model.device)
     L.check(lib.mkd_lm_head_greedy(hidden[n - 1:n].data_ptr(), model.ln_f.data_ptr(), model.cfg.rms_norm_eps,

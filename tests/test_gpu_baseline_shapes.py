@@ -403,3 +403,133 @@ def test_configs1_decode_step_48_layers(mk, dev):
     top2 = torch.topk(lg_ref[0], 2).values
     if (top2[0] - top2[1]).item() > 1e-2 * lg_ref.abs().max().item():
         assert int(nx_e[0]) == int(nx_ref[0])
+
+
+class _RoutedExperts:
+    """The routed experts of one layer (expert id -> weights [2I, H] or [H, I])
+    standing in for the [E, ...] expert tensor the oracle indexes by expert id."""
+
+    def __init__(self, full_shape, rows):
+        self.shape = full_shape
+        self.rows = rows
+
+    def __getitem__(self, e):
+        return self.rows[int(e)]
+
+
+def test_configs1_full_depth_parity(mk, dev):
+    """configs[1] through its whole depth, like the reference's whole-model logit
+    validation (main.py:559-640): one decode step of the bench's model (48
+    layers, V = 151936, bs = 1, KV context 2048) against the CPU oracle on the
+    same seeded weights (drawn on the GPU exactly as the bench draws them, then
+    copied to the host one layer at a time).
+
+    * Every one of the 48 layers teacher-forced: the GPU layer run alone on its
+      own chain's input, against both oracle flows on that input, routed like
+      the GPU, within 2e-2 -- with the routing contract on the GPU's residual
+      (check_qwen_routing) and every flip of the oracle's own top-k a near-tie.
+      The layer-by-layer GPU chain is bit-identical to the one-call step.
+    * The whole chain: the oracle's bf16-emulating and fp32 flows chained through
+      all 48 layers (routed like the GPU's routing log) against the step's final
+      hidden state and its V = 151936 logits.  With random-init weights a
+      rounding difference early in the chain grows layer by layer, and the
+      oracle's own two flows end ~9e-2 apart, so the bar here is relative: the
+      GPU may be no further from either flow than the flows are from each other
+      (x 1.5, + 5e-3).  The per-layer drift curve is printed."""
+    import bench
+    import __graft_entry__ as ge
+    ge.load_package()
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    B, ctx, seed, tok = 1, 2048, 1234, 77777
+    cfg = Q.Qwen3MoeMKConfig(num_hidden_layers=48, max_batch=B, max_seq=ctx + 128)
+    model = bench.build_model(Q, cfg, B, dev, seed)
+    bench.prefill_kv(model, cfg, ctx, seed, dev)
+    model.enable_route_log(B)
+    Ln = cfg.num_hidden_layers
+    k0 = [model.kv_mgr.k(l).clone() for l in range(Ln)]
+    v0 = [model.kv_mgr.v(l).clone() for l in range(Ln)]
+    ids = torch.tensor([tok], dtype=torch.int32, device=dev)
+    pos = torch.tensor([ctx], dtype=torch.int32, device=dev)
+    hidden = torch.empty(B, cfg.hidden_size, dtype=torch.bfloat16, device=dev)
+    logits = torch.empty(B, cfg.vocab_size, dtype=torch.float32, device=dev)
+    nxt = torch.empty(B, dtype=torch.int32, device=dev)
+    print("configs[1] full-depth step on the GPU", flush=True)
+    model.step(ids, pos, hidden, logits, nxt)
+    torch.cuda.synchronize()
+    assert not model.layer_kernel_status()[1]      # no in-launch wait timed out
+    lg_gpu, h_gpu = logits.cpu(), hidden.cpu()
+    logs = model.route_log(B)
+    assert len(logs) == Ln
+    for l in range(Ln):
+        model.kv_mgr.k(l).copy_(k0[l])
+        model.kv_mgr.v(l).copy_(v0[l])
+    x = model.embed_tokens[tok:tok + 1].clone()
+    x_bf = x.cpu()
+    x_32 = x_bf.float()
+    cos, sin = ref.rope_cos_sin(pos.cpu(), cfg.head_dim, cfg.rope_theta)
+    pc = pos.cpu()
+    shape = ref.QwenShape()
+    curve, tf = [], []
+    for l in range(Ln):
+        x_in = x.cpu()
+        model.decode_layers(x, pos, layers=(l, l + 1))
+        torch.cuda.synchronize()
+        rec = model.route_log(B)[l]
+        assert torch.equal(rec["idx"], logs[l]["idx"]) and torch.equal(rec["r"], logs[l]["r"])
+        hf = Q.random_layer_hf(cfg, l, seed, dev)
+        sel = sorted(set(rec["idx"][0].tolist()))
+        gu = _RoutedExperts(tuple(hf["gate_up_proj"].shape), {e: hf["gate_up_proj"][e].cpu() for e in sel})
+        dn = _RoutedExperts(tuple(hf["down_proj"].shape), {e: hf["down_proj"][e].cpu() for e in sel})
+        lw = ref.QwenLayer(wq=hf["q_proj"].cpu(), wk=hf["k_proj"].cpu(), wv=hf["v_proj"].cpu(),
+                           wo=hf["o_proj"].cpu(), q_norm=hf["q_norm"].cpu(), k_norm=hf["k_norm"].cpu(),
+                           ln_in=hf["input_layernorm"].cpu(), ln_post=hf["post_attention_layernorm"].cpu(),
+                           router=hf["gate"].cpu(), gate_up=gu, down=dn)
+        del hf
+        kc, vc = k0[l][:, :, :ctx + 1].cpu(), v0[l][:, :, :ctx + 1].cpu()
+        # teacher-forced: this layer on the GPU chain's own input (qwen_parity asserts 2e-2)
+        kr, _ = qwen_parity(x.cpu(), rec, x_in, lw, kc, vc, cos, sin, pc)
+        assert max_abs_rel(model.kv_mgr.k(l)[:, :, ctx].cpu(), kr[:, :, ctx]) < TOL
+        tf.append(max_abs_rel(x.cpu(), ref.qwen_decoder_layer(x_in, lw, kc.clone(), vc.clone(), cos, sin, pc,
+                                                              shape, force_idx=rec["idx"].long())[0]))
+        # the chains
+        force = logs[l]["idx"].long()
+        x_bf, aux = ref.qwen_decoder_layer(x_bf, lw, kc.clone(), vc.clone(), cos, sin, pc, shape,
+                                           force_idx=force)
+        x_32, aux32 = ref.qwen_decoder_layer(x_32, lw, kc.clone(), vc.clone(), cos, sin, pc, shape,
+                                             emulate_bf16=False, force_idx=force)
+        flips, dl = check_oracle_flips(logs[l]["idx"], logs[l]["logits"], aux["logits"], 8)
+        curve.append((max_abs_rel(logs[l]["r"], aux["r"]), max_abs_rel(logs[l]["r"], aux32["r"]),
+                      max_abs_rel(aux["r"], aux32["r"]), flips))
+        if l % 8 == 7:
+            print("  layers %2d-%2d teacher-forced: %s" % (l - 7, l, " ".join("%.1e" % e for e in tf[-8:])),
+                  flush=True)
+            print("                chained router input vs bf16 flow / fp32 flow / flows apart: %s" % (
+                "  ".join("%.1e/%.1e/%.1e%s" % (a, b, c, "*" if f else "") for a, b, c, f in curve[-8:])),
+                flush=True)
+    assert torch.equal(x.cpu(), h_gpu)             # layer by layer == the one-call step
+    e_bf, e_32, e_flows = max_abs_rel(h_gpu, x_bf), max_abs_rel(h_gpu, x_32), max_abs_rel(x_bf, x_32)
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed + 1)
+    torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g, device=dev)           # embedding draw
+    lm = (0.02 * torch.randn(cfg.vocab_size, cfg.hidden_size, generator=g, device=dev)).to(torch.bfloat16).cpu()
+    lnf = (1 + 0.02 * torch.randn(cfg.hidden_size, generator=g, device=dev)).to(torch.bfloat16).cpu()
+    lg_bf, nx_bf = ref.final_norm_lm_head(x_bf, lnf, lm, cfg.rms_norm_eps)
+    lg_32, nx_32 = ref.final_norm_lm_head(x_32, lnf, lm, cfg.rms_norm_eps, emulate_bf16=False)
+    l_bf, l_32, l_flows = max_abs_rel(lg_gpu, lg_bf), max_abs_rel(lg_gpu, lg_32), max_abs_rel(lg_bf, lg_32)
+    print(f"  after 48 layers: hidden vs bf16 flow {e_bf:.2e}, vs fp32 flow {e_32:.2e} (flows apart "
+          f"{e_flows:.2e}); logits vs bf16 flow {l_bf:.2e}, vs fp32 flow {l_32:.2e} (flows apart "
+          f"{l_flows:.2e}); greedy token gpu {int(nxt[0])}, oracle bf16 flow {int(nx_bf[0])}, "
+          f"fp32 flow {int(nx_32[0])}; teacher-forced layers max {max(tf):.2e}", flush=True)
+    assert max(tf) < TOL
+    for e in (e_bf, e_32):
+        assert e <= 1.5 * e_flows + 5e-3, (e, e_flows)
+    for e in (l_bf, l_32):
+        assert e <= 1.5 * l_flows + 5e-3, (e, l_flows)
+    # the step's own lm_head on its final hidden state (teacher-forced)
+    lg_tf, nx_tf = ref.final_norm_lm_head(h_gpu, lnf, lm, cfg.rms_norm_eps)
+    assert max_abs_rel(lg_gpu, lg_tf) < TOL
+    top2 = torch.topk(lg_tf[0], 2).values
+    if (top2[0] - top2[1]).item() > 1e-2 * lg_tf.abs().max().item():
+        assert int(nxt[0]) == int(nx_tf[0])
+    del model
+    torch.cuda.empty_cache()

@@ -18,7 +18,7 @@ import torch
 from conftest import max_abs_rel
 from oracle import ref
 from prompt_oracle import qwen_prompt_chain, qwen_ref_layers
-from routing_checks import check_qwen_routing
+from routing_checks import check_oracle_flips, check_qwen_routing
 
 pytestmark = pytest.mark.gpu
 TOL = 2e-2
@@ -147,6 +147,7 @@ def test_gpt_oss_get_model_output_reference_signature(mk, dev):
     cfg, hfs, model, embed, ln_f = _small_gpt_oss(dev, 2)
     B, S = 2, 5
     model.enable_route_log(B)
+    model.route_log_history = []     # every CTE pass's routing: pass b * S + t is token t of sequence b
     g = torch.Generator().manual_seed(21)
     ids = torch.randint(0, 1024, (B, S + 1), generator=g)
     pos = torch.arange(S).repeat(B, 1)
@@ -160,8 +161,12 @@ def test_gpt_oss_get_model_output_reference_signature(mk, dev):
                                       torch.full((B, 1), S).to(dev))
     torch.cuda.synchronize()
     logs = model.route_log(B)
+    hist = model.route_log_history
+    model.route_log_history = None
+    assert len(hist) == B * S
     # oracle: token by token through both layers (sliding window 128, full), routed like
-    # the GPU for the last (TKG) token
+    # the GPU -- the CTE tokens like their own passes, the last (TKG) token like the
+    # TKG call -- with every flip of the oracle's own top-k a near-tie
     from nki_moe_megakernel_amd import gpt_oss_with_megakernel as G
     lws = [_gpt_oss_ref_layer(h) for h in hfs]
     inv, scl = G.yarn_inv_freq(cfg)
@@ -175,9 +180,15 @@ def test_gpt_oss_get_model_output_reference_signature(mk, dev):
         cos, sin = fr.cos() * scl, fr.sin() * scl
         x = embed[ids[:, t]].float()
         for l in range(2):
-            force = logs[l]["idx"].long() if t == S else None
-            x, _ = ref.gpt_oss_decoder_layer(x, lws[l], caches[l][0], caches[l][1], cos, sin, p,
-                                             128 if cfg.is_sliding(l) else 0, shape, force_idx=force)
+            if t == S:
+                rec_idx, rec_lg = logs[l]["idx"], logs[l]["logits"]
+            else:
+                rec_idx = torch.cat([hist[b * S + t][l]["idx"] for b in range(B)])
+                rec_lg = torch.cat([hist[b * S + t][l]["logits"] for b in range(B)])
+            x, aux = ref.gpt_oss_decoder_layer(x, lws[l], caches[l][0], caches[l][1], cos, sin, p,
+                                               128 if cfg.is_sliding(l) else 0, shape,
+                                               force_idx=rec_idx.long())
+            check_oracle_flips(rec_idx, rec_lg, aux["logits"], 4)
         outs.append(ref._bf(ref.rmsnorm_tkg(x, ln_f, cfg.rms_norm_eps)))
     e_cte = max(max_abs_rel(y_cte[:, t], outs[t]) for t in range(S))
     e_tkg = max_abs_rel(y_tkg[:, 0], outs[S])
