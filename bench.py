@@ -462,6 +462,8 @@ def main():
                      "traffic": measured_traffic(B, ctx, cfg.num_hidden_layers, kcls, joined)
                      if (args.model == "qwen3" and args.experts == "bf16" and not args.ragged
                          and not args.kv_block) else None,
+                     "traffic_source": "committed rocprofv3 FETCH_SIZE + WRITE_SIZE summary of this kernel "
+                                       "and workload (profiles/), not measured in this run",
                      "avg_us": round(avg_ms * 1e3, 2), "bytes_per_launch": int(alg_bytes)},
         "cpu_baseline": cpu,
     }
@@ -658,8 +660,9 @@ def attention_launch(model, B):
 
 
 def measured_traffic(B, ctx, layers, kcls="moe_gate_up", joined=False):
-    """HBM bytes per launch of the dominant kernel from the committed counter
-    summary for that kernel and workload, or None."""
+    """HBM bytes per launch of the dominant kernel, read from the committed
+    counter summary for that kernel and workload (profiles/*_traffic.json, made
+    by two rocprofv3 --pmc runs of this bench), or None.  Not measured in this run."""
     name = "layer_kernel_traffic.json" if kcls == "layer" else (
         "moe_joined_traffic.json" if joined else "gate_up_traffic.json")
     path = os.path.join(ROOT, "profiles", name)

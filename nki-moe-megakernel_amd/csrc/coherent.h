@@ -57,6 +57,12 @@ MKD_DEV uint16_t coh_ld2(__amdgpu_buffer_rsrc_t r, int off) {
 // vmcnt(0): every load and store this wave issued has completed
 MKD_DEV void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0xF70); }
 
+// Block barrier for LDS data only: this wave's LDS accesses have completed,
+// then s_barrier.  Unlike __syncthreads (whose workgroup fence waits for every
+// outstanding vector-memory access, vmcnt(0)) it leaves loads in flight -- the
+// global -> LDS copies and the next round of polls.  A compiler barrier too.
+MKD_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // Publish a block's results: every wave waits for its own stores, then thread 0
 // sets the block's flag word.  Called by all threads of the block.
 MKD_DEV void coh_publish(unsigned* flag) {

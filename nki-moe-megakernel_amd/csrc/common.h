@@ -86,6 +86,14 @@ MKD_DEV float block_sum(float v, float* red) {
   return s;
 }
 
+// One 1 KiB fragment into LDS: lane l's 16 bytes from byte offset voff of the
+// buffer land at dst + 16 l (buffer_load_dwordx4 ... lds; dst is wave-uniform;
+// tracked by vmcnt alone).  A plain function so that the builtin stays out of
+// template instantiation.
+MKD_DEV void copy_frag_lds(__amdgpu_buffer_rsrc_t src, u32x4_t* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, voff,
+                                           0, 0, 0);
+}
 MKD_DEV u32x4_t ld16(const void* p) { return *reinterpret_cast<const u32x4_t*>(p); }
 MKD_DEV void st16(void* p, u32x4_t v) { *reinterpret_cast<u32x4_t*>(p) = v; }
 

@@ -22,6 +22,7 @@
 // w + expert * w_group_stride.
 #include "common.h"
 #include "gemm_epi.h"
+#include "gemm_frag.h"
 #include "mkd_internal.h"
 #include "router_select.h"
 #include "coherent.h"
@@ -66,168 +67,6 @@ __global__ void pack_frag_kernel(const uint16_t* __restrict__ src, uint16_t* __r
     uint16_t* d = dst + idx * 8;
 #pragma unroll
     for (int j = 0; j < 8; ++j) d[j] = v[j];
-  }
-}
-
-// B consecutive fragments of every row block: every weight and x load of the
-// batch is issued before the first MFMA.  Lanes of absent tokens (xrow < 0)
-// read x row 0 instead -- their output column is never written, and MFMA
-// columns are independent.  fp32 x rows are
-// carried as a bf16 hi + lo pair (two MFMAs).
-template <int RB, int TN, bool XF32, int B>
-MKD_DEV void stream_batch(const uint16_t* const (&wrow)[RB], int f, int kb0, int koff,
-                          const int (&xrow)[TN], const GemmArgs& a, f32x4_t (&acc)[RB][TN]) {
-  u32x4_t wf[RB][B];
-#pragma unroll
-  for (int u = 0; u < B; ++u)
-#pragma unroll
-    for (int r = 0; r < RB; ++r)
-      wf[r][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow[r] + (f + u) * 512));
-  // the weight loads go out before the x addresses are formed: in grouped mode
-  // the token rows come from a routing table whose load may still be in flight
-  __builtin_amdgcn_sched_barrier(0);
-  const void* xp[TN];
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) {
-    int xr = xrow[tn];
-    asm volatile("" : "+v"(xr));         // formed here, not hoisted out of the k loop
-    const long long off = (long long)(xr >= 0 ? xr : 0) * a.ldx + koff;
-    xp[tn] = XF32 ? static_cast<const void*>(static_cast<const float*>(a.x) + off)
-                  : static_cast<const void*>(static_cast<const uint16_t*>(a.x) + off);
-  }
-  if constexpr (XF32) {
-    f32x4_t xa[B][TN], xb[B][TN];
-#pragma unroll
-    for (int u = 0; u < B; ++u)
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const float* p = static_cast<const float*>(xp[tn]) + (kb0 + f + u) * 32;
-        xa[u][tn] = *reinterpret_cast<const f32x4_t*>(p);
-        xb[u][tn] = *reinterpret_cast<const f32x4_t*>(p + 4);
-      }
-    if constexpr (TN == 1) __builtin_amdgcn_sched_barrier(0);   // every load ahead of the MFMAs
-#pragma unroll
-    for (int u = 0; u < B; ++u)
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn) {
-        const float xs[8] = {xa[u][tn][0], xa[u][tn][1], xa[u][tn][2], xa[u][tn][3],
-                             xb[u][tn][0], xb[u][tn][1], xb[u][tn][2], xb[u][tn][3]};
-        u32x4_t hi, lo;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const uint32_t h0 = f2bf(xs[2 * j]), h1 = f2bf(xs[2 * j + 1]);
-          hi[j] = h0 | (h1 << 16);
-          lo[j] = f2bf(xs[2 * j] - bf2f(h0)) | (f2bf(xs[2 * j + 1] - bf2f(h1)) << 16);
-        }
-#pragma unroll
-        for (int r = 0; r < RB; ++r) {
-          acc[r][tn] = mfma16x16x32(wf[r][u], hi, acc[r][tn]);
-          acc[r][tn] = mfma16x16x32(wf[r][u], lo, acc[r][tn]);
-        }
-      }
-  } else {
-    u32x4_t xv[B][TN];
-#pragma unroll
-    for (int u = 0; u < B; ++u)
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn)
-        xv[u][tn] = ld16(static_cast<const uint16_t*>(xp[tn]) + (kb0 + f + u) * 32);
-    // one token tile: every load ahead of the MFMAs (a latency-bound launch);
-    // more tiles: MFMA work to hide, so the compiler interleaves (measured
-    // 46 -> 23 us for the QKV / o_proj GEMMs at 64 tokens)
-    if constexpr (TN == 1) __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int u = 0; u < B; ++u)
-#pragma unroll
-      for (int tn = 0; tn < TN; ++tn)
-#pragma unroll
-        for (int r = 0; r < RB; ++r) acc[r][tn] = mfma16x16x32(wf[r][u], xv[u][tn], acc[r][tn]);
-  }
-}
-
-// ---------------------------------------------------------------------------
-// The GEMM.
-// ---------------------------------------------------------------------------
-// (rbase, group, bz): the block's RB-row-block tile, routed group, and token
-// tile * kgrid + K block -- blockIdx in the plain launch.  COH: the outputs are
-// stored device-coherent (read by other blocks of the same launch).
-template <int RB, int TN, bool XF32, int EPI, bool COH = false, int UNR = 8 / RB>
-MKD_DEV void frag_body(const GemmArgs& a, int rbase, int group, int bz) {
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int kg = a.kgrid > 1 ? a.kgrid : 1;
-  const int kblk = bz % kg;
-
-  // ---- token columns of this block ----
-  int count, base;                       // tokens in this group / first pair
-  const uint16_t* w = a.w;
-  if (a.grp_expert) {
-    // the group's table entries are read together with the group count (one
-    // memory round trip; group < gridDim.y <= the tables' length)
-    const int ng = *a.n_groups;
-    count = a.grp_count[group];
-    base = a.grp_offset[group];
-    const int ex = a.grp_expert[group];
-    asm volatile("" ::"s"(ng), "s"(count), "s"(base), "s"(ex));   // no sinking past the exit
-    if (group >= ng) return;
-    w += (long long)ex * a.w_group_stride;
-  } else {
-    count = a.T;
-    base = 0;
-  }
-  for (int ttile = bz / kg;; ++ttile) {
-  const int t0 = ttile * 16 * TN;
-  if (t0 >= count) return;
-  if (ttile > bz / kg) __syncthreads();   // the previous tile's reduction buffer is free
-
-  // x row of each token column owned by this lane (one column per TN tile)
-  int xrow[TN];
-#pragma unroll
-  for (int tn = 0; tn < TN; ++tn) {
-    const int c = t0 + tn * 16 + (lane & 15);
-    if (c < count)
-      xrow[tn] = a.pair_row ? a.pair_row[base + c] : (base + c);
-    else
-      xrow[tn] = -1;
-  }
-
-  const int KB = a.K / 32;
-  const int NF = a.KW / 32;              // fragments per wave
-  const int kb0 = (kblk * (int)(blockDim.x >> 6) + wave) * NF;
-  const int koff = (lane >> 4) * 8;
-
-  f32x4_t acc[RB][TN];
-#pragma unroll
-  for (int r = 0; r < RB; ++r)
-#pragma unroll
-    for (int tn = 0; tn < TN; ++tn) acc[r][tn] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-
-  const uint16_t* wrow[RB];
-#pragma unroll
-  for (int r = 0; r < RB; ++r)
-    wrow[r] = w + ((long long)(rbase * RB + r) * KB + kb0) * 512 + lane * 8;
-
-  // Stream the fragments: a wave issues a batch of UNROLL*RB fragment loads
-  // (8 KiB) before the MFMAs that consume them; batches carry no guards so
-  // they stay in registers, and the remainder (< UNROLL) is taken as batches of
-  // 4/2/1 so short slices still keep several loads in flight.  (Measured at
-  // decode shapes: 8 fragments per batch with up to 16 waves per block beat
-  // 16- and 32-fragment batches with fewer waves.)
-  constexpr int UNROLL = UNR;
-  int f = 0;
-  for (; f + UNROLL <= NF; f += UNROLL)
-    stream_batch<RB, TN, XF32, UNROLL>(wrow, f, kb0, koff, xrow, a, acc);
-  if constexpr (UNROLL > 8)
-    if (f + 8 <= NF) { stream_batch<RB, TN, XF32, 8>(wrow, f, kb0, koff, xrow, a, acc); f += 8; }
-  if constexpr (UNROLL > 4)
-    if (f + 4 <= NF) { stream_batch<RB, TN, XF32, 4>(wrow, f, kb0, koff, xrow, a, acc); f += 4; }
-  if constexpr (UNROLL > 2)
-    if (f + 2 <= NF) { stream_batch<RB, TN, XF32, 2>(wrow, f, kb0, koff, xrow, a, acc); f += 2; }
-  if constexpr (UNROLL > 1)
-    if (f < NF) stream_batch<RB, TN, XF32, 1>(wrow, f, kb0, koff, xrow, a, acc);
-
-  gemm_finish<RB, TN, EPI, COH>(a, acc, lane, wave, rbase, group, t0, base, xrow, kblk);
-  if (!a.t_loop) return;
   }
 }
 
@@ -309,30 +148,66 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   __shared__ int s_gexp[kSelMaxPairs], s_gcnt[kSelMaxPairs], s_goff[kSelMaxPairs];
   __shared__ int s_ptok[kSelMaxPairs], s_pslot[kSelMaxPairs];
   __shared__ float s_w[kSelMaxPairs];
+  __shared__ OneTokenSel sel;
   __shared__ f32x4_t s_red[DRB][4][64];
   __shared__ u32x4_t s_h[kFusedMaxRows][NFD * 8];   // h rows of a down block's group
   const int bid = blockIdx.x;
-  const bool lead = bid == 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const RouterArgs& r = f.r;
+  // One token whose selection key is the logit (Qwen, or top-k on logits then a
+  // softmax over the top-k): the experts are ranked first and published to the
+  // group tables, and only the down blocks form the routing weights, after
+  // their weight loads are out (select_one_experts / select_one_weights) -- the
+  // gate/up blocks issue their weight loads without waiting for the softmax.
+  const bool one = r.T == 1 && r.E <= 128 && 4 * r.E <= (int)blockDim.x;
+  const bool split = one && r.nparts <= 8 &&
+                     ((r.mode & 8) || !(r.mode & 3));   // Qwen flow, or neither pre-norm nor sigmoid
+  const bool lead = split ? bid == f.ngu : bid == 0;   // writes the routing outputs
   RouterArgs q = r;
   q.n_groups = &s_ng;
   q.grp_expert = s_gexp; q.grp_count = s_gcnt; q.grp_offset = s_goff;
   q.pair_token = s_ptok; q.pair_slot = s_pslot; q.slot_w = s_w;
   if (!lead) q.logits_out = nullptr, q.aff_full = nullptr, q.idx_out = nullptr, q.topk_out = nullptr;
   const bool gu_role = bid < f.ngu;
+  // the block's routing tables (LDS)
+  int *t_ng = &s_ng, *t_gexp = s_gexp, *t_gcnt = s_gcnt, *t_goff = s_goff, *t_ptok = s_ptok, *t_pslot = s_pslot;
+  float* t_w = s_w;
+  float lg[2];
   // a down block's weight slice does not depend on the routing: its row block
   // and K half are fixed, only the expert offset is not -- so the routing comes
   // first, then the loads
-  if (r.T == 1 && r.E <= 128 && 4 * r.E <= (int)blockDim.x) {
-    // the joined attention launch's router stage leaves 8 partial logits
+  if (split) {
+    // the joined attention launch's router stage leaves <= 8 partial logits
+    float raw[8][2];
+    select_one_experts(q,
+        [&]() {
+#pragma unroll
+          for (int p = 0; p < 8; ++p)
+#pragma unroll
+            for (int j = 0; j < 2; ++j)
+              raw[p][j] = q.parts[min(p, q.nparts - 1) * q.part_stride + min(lane + 64 * j, q.E - 1)];
+        },
+        [&](float (&l)[2]) {
+#pragma unroll
+          for (int j = 0; j < 2; ++j) {
+            float v = 0.f;
+#pragma unroll
+            for (int p = 0; p < 8; ++p)
+              if (p < q.nparts) v += raw[p][j];
+            l[j] = q.bias ? v + bf2f(q.bias[min(lane + 64 * j, q.E - 1)]) : v;
+          }
+        },
+        [] {}, sel, lg);
+    t_ng = &sel.ng; t_gexp = sel.gexp; t_gcnt = sel.gcnt; t_goff = sel.goff;
+    t_ptok = sel.ptok; t_pslot = sel.pslot; t_w = sel.w;
+  } else if (one) {
     if (r.nparts <= 8) select_one(q, [&](int t, float (&l)[2]) { load_logits<2, 8>(q, t, lane, l); });
     else select_one(q, [&](int t, float (&l)[2]) { load_logits<2>(q, t, lane, l); });
   } else {
     select_small<PER>(q, [&](int t, float (&l)[PER]) { load_logits<PER>(q, t, lane, l); });
   }
   __syncthreads();
-  if (lead) {
+  if (lead && !split) {
     const int ng = s_ng, np = r.T * r.K;
     if (threadIdx.x == 0) *r.n_groups = ng;
     for (int i = threadIdx.x; i < ng; i += blockDim.x) {
@@ -348,9 +223,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   }
   if (gu_role) {
     GemmArgs b = f.gu;
-    b.n_groups = &s_ng;
-    b.grp_expert = s_gexp; b.grp_count = s_gcnt; b.grp_offset = s_goff;
-    b.pair_row = s_ptok; b.pair_out_row = s_pslot;
+    b.n_groups = t_ng;
+    b.grp_expert = t_gexp; b.grp_count = t_gcnt; b.grp_offset = t_goff;
+    b.pair_row = t_ptok; b.pair_out_row = t_pslot;
     frag_body<2, 1, false, EPI_SWIGLU_BF16, true>(b, bid % f.n_gu, bid / f.n_gu, 0);
     if (!f.poll_h) coh_publish(f.flags + bid);
     return;
@@ -359,8 +234,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   const GemmArgs& d = f.dn;
   const int db = bid - f.ngu;
   const int g = db / f.ndb, qd = db - g * f.ndb;
-  if (g >= s_ng) return;
-  const int ex = s_gexp[g], count = s_gcnt[g], base = s_goff[g];
+  if (g >= *t_ng) return;
+  const int ex = t_gexp[g], count = t_gcnt[g], base = t_goff[g];
   const int KB = d.K / 32;
   const int rbk = qd * 4 * DRB + (wave & 3); // 16-row blocks rbk + 4 i of the output
   const int kh = wave >> 2;                  // K half
@@ -374,8 +249,20 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
     for (int u = 0; u < NFD; ++u)
       wf[i][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + u * 512));
   }
+  if (split && wave == 0) {
+    q.slot_w = lead ? r.slot_w : nullptr;
+    select_one_weights(q, sel, lg);   // sel.w: read after the barriers below
+    if (lead && threadIdx.x < r.K) {   // the group tables too (one group per slot)
+      if (threadIdx.x == 0) *r.n_groups = r.K;
+      r.grp_expert[threadIdx.x] = sel.gexp[threadIdx.x];
+      r.grp_count[threadIdx.x] = 1;
+      r.grp_offset[threadIdx.x] = threadIdx.x;
+      r.pair_token[threadIdx.x] = 0;
+      r.pair_slot[threadIdx.x] = threadIdx.x;
+    }
+  }
   const int c = lane & 15;
-  const int prow = c < count ? s_pslot[base + c] : -1;   // h row and output row of the column
+  const int prow = c < count ? t_pslot[base + c] : -1;   // h row and output row of the column
   if (!f.poll_h) {
     if (wave == 0) coh_wait_all(f.flags + g * f.n_gu, f.n_gu, f.err);
     __syncthreads();
@@ -392,7 +279,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
       int miss = 0;
       for (int i = threadIdx.x; i < count * per_row; i += blockDim.x) {
         const int rr = i / per_row, pc = i - rr * per_row;
-        const int row = s_pslot[base + rr];
+        const int row = t_pslot[base + rr];
         const u32x4_t v = coh_ld16(hr, (int)(((long long)row * d.ldx + pc * 8) * 2));
         s_h[rr][pc] = v;
 #pragma unroll
@@ -427,7 +314,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   }
   __syncthreads();
   if (kh != 0 || prow < 0) return;
-  const float sc = s_w[prow];
+  const float sc = t_w[prow];
 #pragma unroll
   for (int i = 0; i < DRB; ++i) {
     const f32x4_t hi = s_red[i][wave][lane];

@@ -40,13 +40,6 @@ constexpr int kLdsBytes = kStages * kStageFrags * 1024;
 
 // s_waitcnt with only vmcnt = n (expcnt / lgkmcnt left at their maxima); gfx9
 // encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14.
-// One 1 KiB fragment into LDS: lane l's 16 bytes from byte offset voff of the
-// buffer land at dst + 16 l (buffer_load_dwordx4 ... lds; dst is wave-uniform).
-// A plain function so that the builtin stays out of template instantiation.
-MKD_DEV void copy_frag_lds(__amdgpu_buffer_rsrc_t src, u32x4_t* dst, int voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(src, (__attribute__((address_space(3))) void*)dst, 16, voff,
-                                           0, 0, 0);
-}
 
 template <int N>
 MKD_DEV void wait_vmcnt() {

@@ -3,6 +3,7 @@
 #pragma once
 #include "common.h"
 #include "mkd_internal.h"
+#include "coherent.h"
 
 namespace mkd {
 
@@ -538,6 +539,112 @@ MKD_DEV void select_one(const RouterArgs& a, Load&& load) {
       }
     }
     if (lane == 0 && a.n_groups) *a.n_groups = K;
+  }
+}
+
+// One-token routing split in two for blocks that need their experts before the
+// routing weights (flows whose selection key is the logit itself: Qwen's
+// logit top-k, or the top-k on logits with a softmax over the top-k).
+// select_one_experts: wave 0 loads the logits (kept in its registers, l) and
+// stores their order codes and values to LDS; after one block barrier every
+// expert's rank is counted as in select_one, and rank r < K goes straight into
+// the group tables (group r = expert r of the ranking, one row, pair slot r) --
+// no softmax statistics or weights on the way to the weight loads.  The caller
+// synchronises the block (LDS) before reading the tables.
+struct OneTokenSel {
+  uint32_t code[128];
+  float key[128];
+  int ng, gexp[8], gcnt[8], goff[8], ptok[8], pslot[8];
+  float w[8];
+};
+
+// `issue` (wave 0) issues the logit loads and `finish` (wave 0) forms l from
+// them; between the two every wave passes one plain barrier (no memory fence,
+// so wave 0's loads stay in flight) and runs `side` -- where the other waves
+// can issue loads of their own that then queue behind the logits.
+template <class Issue, class Finish, class Side>
+MKD_DEV void select_one_experts(const RouterArgs& a, Issue&& issue, Finish&& finish, Side&& side,
+                                OneTokenSel& s, float (&l)[2]) {
+  const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+  const int E = a.E, K = a.K;
+  if (wv == 0) issue();
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  side();
+  if (wv == 0) {
+    finish(l);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int e = lane + 64 * j;
+      if (e < E) {
+        if (a.logits_out) a.logits_out[e] = l[j];
+      } else {
+        l[j] = -INFINITY;
+      }
+      s.code[e] = e < E ? order_code(l[j]) : 0u;   // padding ranks last
+      s.key[e] = l[j];
+    }
+  }
+  lds_barrier();   // the loads `side` issued stay in flight
+  const int e = tid >> 2, qtr = tid & 3;
+  int rank = 0;
+  if (e < E) {
+    const uint32_t ue = s.code[e];
+    const uint32_t ue1 = ue ? ue - 1 : 0u;
+    const int d = e - qtr * 32;
+    const u32x4_t* cq = reinterpret_cast<const u32x4_t*>(s.code + qtr * 32);
+    u32x4_t c[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c[i] = cq[i];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t thr = (i * 4 + j < d) ? ue1 : ue;
+        rank += c[i][j] > thr ? 1 : 0;
+      }
+  }
+  rank += __builtin_amdgcn_update_dpp(0, rank, 0xB1, 0xF, 0xF, false);   // quad_perm [1,0,3,2]
+  rank += __builtin_amdgcn_update_dpp(0, rank, 0x4E, 0xF, 0xF, false);   // quad_perm [2,3,0,1]
+  if (e < E && qtr == 0 && rank < K) {
+    s.gexp[rank] = e;
+    s.gcnt[rank] = 1;
+    s.goff[rank] = rank;
+    s.ptok[rank] = 0;
+    s.pslot[rank] = rank;
+  }
+  if (tid == 0) s.ng = K;
+}
+
+// select_one_weights: wave 0, after the caller's barrier that follows
+// select_one_experts, forms the routing weights of the K slots (select_one's
+// formulas: Qwen softmax value at the expert -> bf16 -> bf16 L1 renormalisation,
+// or the softmax over the top-k logits) into s.w, and writes the optional
+// global outputs (idx_out, topk_out, slot_w).
+MKD_DEV void select_one_weights(const RouterArgs& a, OneTokenSel& s, const float (&l)[2]) {
+  const int lane = threadIdx.x & 63;
+  const int K = a.K;
+  const bool qwen = a.mode & 8;
+  float mx = fmaxf(l[0], l[1]);
+  mx = wave_max(mx);
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) sum += (lane + 64 * j < a.E) ? expf(l[j] - mx) : 0.f;
+  sum = wave_sum(sum);
+  const float inv = 1.0f / sum;
+  const int my_e = lane < K ? s.gexp[lane] : 0;
+  const float my_key = lane < K ? s.key[my_e] : 0.f;
+  const float k0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, my_key), 0));
+  const float pv = qwen ? rbf(expf(my_key - mx) * inv) : expf(my_key - k0);
+  float t = 0.f;
+  for (int k = 0; k < K; ++k)
+    t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pv), k));
+  const float w = qwen ? rbf(pv * (1.0f / t)) : pv * (1.0f / t);
+  if (lane < K) {
+    s.w[lane] = w;
+    if (a.idx_out) a.idx_out[lane] = my_e;
+    if (a.topk_out) a.topk_out[lane] = w;
+    if (a.slot_w) a.slot_w[lane] = w;
   }
 }
 
