@@ -116,14 +116,14 @@ __global__ void __launch_bounds__(D) attn_kv_write_kernel(AttnArgs a) {
 // staged k / v rows) are read by later blocks of the same launch -- they are
 // stored device-coherent and the block then sets *flag (also when the chunk
 // lies past the sequence and the block does nothing else).
-template <int D, int GQA, int TPW, bool COH>
+template <int D, int GQA, int TPW, bool COH, int NW = 4>
 MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, int b, unsigned* flag) {
   constexpr int NK = D / 32;                  // QK MFMAs per tile (k = 32)
   constexpr int NDT = D / 16;                 // PV d-tiles
-  constexpr int CP = 4 * TPW * 16;            // positions per block
+  constexpr int CP = NW * TPW * 16;           // positions per block (NW waves)
   constexpr int VW = D / 32;                  // dwords of a lane's V row segment
-  __shared__ float m_s[4][16], l_s[4][16];
-  __shared__ __attribute__((aligned(16))) float o_s[4][GQA][D];
+  __shared__ float m_s[NW][16], l_s[NW][16];
+  __shared__ __attribute__((aligned(16))) float o_s[NW][GQA][D];
   __shared__ __attribute__((aligned(16))) uint16_t q_s[GQA][D];
   __shared__ __attribute__((aligned(16))) uint16_t kn_s[D];
   __shared__ __attribute__((aligned(16))) uint16_t vn_s[D];
@@ -230,12 +230,12 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   // wave w takes heads w, w+4, ...: their loads go out first (a wave's vector
   // loads complete in issue order, so the math need not wait for the cache
   // rows behind them), then the prior length and the cache rows ----
-  constexpr int NR = (GQA + 2 + 3) / 4;
+  constexpr int NR = (GQA + 2 + NW - 1) / NW;
   HeadPrep<D> hp[NR];
   if (!a.prep) {
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      const int h = w + 4 * r;
+      const int h = w + NW * r;
       if (h < GQA + 2) {
         const int kind = h < GQA ? 0 : h - GQA + 1;
         const int head = h < GQA ? g * GQA + h : (kind == 1 ? a.nq + g : a.nq + a.nkv + g);
@@ -260,7 +260,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   if (PRE && !flat) pre_loads();
   if (a.prep) {
     const uint16_t* src = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
-    for (int i = threadIdx.x * 8; i < (GQA + 2) * D; i += 256 * 8) {
+    for (int i = threadIdx.x * 8; i < (GQA + 2) * D; i += NW * 64 * 8) {
       const int h = i / D, d = i % D;
       uint16_t* dst = h < GQA ? &q_s[h][d] : (h == GQA ? &kn_s[d] : &vn_s[d]);
       *reinterpret_cast<u32x4_t*>(dst) = ld16(src + i);
@@ -268,7 +268,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   } else {
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
-      const int h = w + 4 * r;
+      const int h = w + NW * r;
       if (h < GQA + 2) {
         const int kind = h < GQA ? 0 : h - GQA + 1;
         hp[r].finish(a, rope_mode, kind, h < GQA ? q_s[h] : (kind == 1 ? kn_s : vn_s), lane);
@@ -420,7 +420,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
     }
   }
 
-  // ---- merge the 4 waves into this chunk's partial ----
+  // ---- merge the NW waves into this chunk's partial ----
   if (lane < 16) { m_s[w][lane] = m; l_s[w][lane] = lsum; }
   // o[dt][i] = O[head 4*(l/16)+i][d = vc + dt]: NDT contiguous floats per head
 #pragma unroll
@@ -434,15 +434,15 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   }
   __syncthreads();
   // four consecutive d of one head per thread (one 16-byte store)
-  for (int idx = threadIdx.x * 4; idx < GQA * D; idx += 1024) {
+  for (int idx = threadIdx.x * 4; idx < GQA * D; idx += NW * 256) {
     const int h = idx / D, d = idx % D;
     float M = -INFINITY;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) M = fmaxf(M, m_s[q][h]);
+    for (int q = 0; q < NW; ++q) M = fmaxf(M, m_s[q][h]);
     float L = 0.f;
     f32x4_t O = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < NW; ++q) {
       const float f = (m_s[q][h] == -INFINITY) ? 0.f : expf(m_s[q][h] - M);
       L += l_s[q][h] * f;
       O += *reinterpret_cast<const f32x4_t*>(&o_s[q][h][d]) * f;
@@ -461,7 +461,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
 
   // the chunk holding the new token stages its k / v rows for the scatter
   if (NT == 1 && n >= chunk0 && n < chunk0 + CP)
-    for (int i = threadIdx.x; i < D; i += 256) {
+    for (int i = threadIdx.x; i < D; i += NW * 64) {
       const long long ko = (((long long)b * 2 + 0) * a.nkv + g) * D + i;
       const long long vo = (((long long)b * 2 + 1) * a.nkv + g) * D + i;
       if constexpr (COH) {
@@ -880,6 +880,274 @@ MKD_DEV void mp_block(const AttnArgs& a, const AttnJoinArgs& j, int ks, int nr, 
   }
 }
 
+// ---- one token, d = 128: the 512-thread form of the joined launch ----
+// (chunk blocks of 8 waves x 16 positions, merge + projection blocks whose
+// weight stream and merge polls run in different waves, K-sliced router blocks)
+//
+// A wave's vector loads complete in issue order, so a wave that streams 32
+// weight fragments and then polls the chunk partials sees the partials only
+// after its weights have arrived (measured: merged at 10.7 us, the chunk
+// partials written by ~6 us).  Here waves 0-3 of a merge + projection block
+// only stream the block's weights (the MFMA operands) and waves 4-7 only poll
+// and merge one query head each, handing the bf16 head rows over in LDS.
+template <int GQA>
+MKD_DEV void mp_block8(const AttnArgs& a, const AttnJoinArgs& j, int ks, int nr) {
+  constexpr int D = 128, FT = kMpHeads * D / 32;    // fragments per row tile of the K slice (16)
+  __shared__ __attribute__((aligned(16))) uint32_t ob_s[kMpHeads * D / 2];   // bf16 pairs of the 4 heads
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int N = j.N, KB = a.nq * D / 32, NRB = (N + 15) / 16;
+  const int h0 = ks * kMpHeads;
+  u32x4_t wf[2][FT];
+  if (w < 4) {
+    // the block's weights: they depend on nothing, but are needed only after
+    // the merge -- started after a short hold so that the chunk blocks' cache
+    // and head loads, which the whole launch waits on, are served first
+    {
+      const unsigned long long t0 = wall_clock64();
+      while (wall_clock64() - t0 < kJoinWeightDelay) __builtin_amdgcn_s_sleep(2);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int rt = min(nr * (kMpRows / 16) + w * 2 + i, NRB - 1);
+      const uint16_t* wrow = j.w_out + ((long long)rt * KB + ks * FT) * 512 + lane * 8;
+#pragma unroll
+      for (int u = 0; u < FT; ++u)
+        wf[i][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + u * 512));
+    }
+  } else {
+    // ---- merge head h = h0 + w - 4 (lane l of the ml load: chunk c0 + l % 32;
+    // the partial loads: d = 2 l, 2 l + 1 of chunk c0 + u), polled until no word
+    // holds the empty marker ----
+    const int h = h0 + w - 4;
+    const int CP = a.chunk;
+    const int n = prior_len(a, 0);
+    const int nch = (n + 1 + CP - 1) / CP;
+    const long long ml0 = (long long)h * a.n_chunks * 2, po0 = (long long)h * a.n_chunks * D;
+    const __amdgpu_buffer_rsrc_t mlr = coh_rsrc(a.part_ml), por = coh_rsrc(a.part_o);
+    float M = -INFINITY, Ls = 0.f, acc0 = 0.f, acc1 = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += kMpBatch) {
+      const int cl = c0 + (lane & 31);
+      const bool live = cl < nch && lane < kMpBatch;
+      coh_u32x2 mlv;
+      coh_u32x2 pv[kMpBatch];
+      for (unsigned it = 0;; ++it) {
+        mlv = coh_ld8(mlr, (int)((ml0 + 2 * min(cl, nch - 1)) * 4));
+#pragma unroll
+        for (int u = 0; u < kMpBatch; ++u)
+          pv[u] = coh_ld8(por, (int)((po0 + (long long)min(c0 + u, nch - 1) * D + 2 * lane) * 4));
+        bool ok = !live || (mlv.x != kPollEmpty && mlv.y != kPollEmpty);
+#pragma unroll
+        for (int u = 0; u < kMpBatch; ++u)
+          ok = ok && (c0 + u >= nch || (pv[u].x != kPollEmpty && pv[u].y != kPollEmpty));
+        if (__all(ok) || coh_poll_giveup(it, j.err)) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      const float mk = live ? __uint_as_float(mlv.x) : -INFINITY;
+      const float lk = live ? __uint_as_float(mlv.y) : 0.f;
+      const float bm = fmaxf(M, wave_max(mk));
+      if (bm == -INFINITY) continue;
+      const float r = M == -INFINITY ? 0.f : expf(M - bm);
+      const float fk = mk == -INFINITY ? 0.f : expf(mk - bm);
+      Ls = Ls * r + wave_sum(lk * fk);
+      acc0 *= r;
+      acc1 *= r;
+#pragma unroll
+      for (int u = 0; u < kMpBatch; ++u) {
+        const float f = lane_f(fk, u);
+        acc0 += __uint_as_float(pv[u].x) * f;
+        acc1 += __uint_as_float(pv[u].y) * f;
+      }
+      M = bm;
+    }
+    if (a.sink) {
+      const float sk = a.sink[h];
+      const float M2 = fmaxf(M, sk);
+      const float r = M == -INFINITY ? 0.f : expf(M - M2);
+      Ls = Ls * r + expf(sk - M2);
+      acc0 *= r;
+      acc1 *= r;
+    }
+    ob_s[(w - 4) * (D / 2) + lane] = Ls > 0.f ? pack2bf(acc0 / Ls, acc1 / Ls) : 0u;
+    // in-place KV scatter of the new rows (attention_block_tkg.py:1144-1470):
+    // the first query head of each kv group, in the row-0 blocks, once every
+    // chunk of the group has read the cache (its flags); nothing in this
+    // launch reads the new rows
+    if (nr == 0 && a.update_cache && h % GQA == 0) {
+      const int g = h / GQA;
+      coh_wait_all(j.flags + (long long)g * a.n_chunks, a.n_chunks, j.err);
+      const long long row = kv_write_row(a, 0);
+      if (row >= 0) {
+        const __amdgpu_buffer_rsrc_t kr = coh_rsrc(a.kv_new);
+        const long long ko = (long long)g * D + 2 * lane, vo = ((long long)a.nkv + g) * D + 2 * lane;
+        const uint32_t kw = coh_ld4(kr, (int)(ko * 2)), vw = coh_ld4(kr, (int)(vo * 2));
+        const long long off = a.block_table ? (row * a.nkv + g) * D + 2 * lane
+                                            : g * a.cache_h_stride + row * D + 2 * lane;
+        *reinterpret_cast<uint32_t*>(a.k_cache + off) = kw;
+        *reinterpret_cast<uint32_t*>(a.v_cache + off) = vw;
+      }
+    }
+  }
+  lds_barrier();   // ob_s; the weight waves' loads stay in flight
+  if (w >= 4) return;
+  // ---- MFMAs (waves 0-3): B operand lane l = token l % 16 (token 0 only) ----
+  const int c = lane & 15;
+  const uint32_t m = c == 0 ? 0xffffffffu : 0u;
+  const u32x4_t* xq = reinterpret_cast<const u32x4_t*>(ob_s) + (lane >> 4);
+  f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int u = 0; u < FT; ++u) {
+    const u32x4_t t = xq[u * 4];
+    const u32x4_t xv = u32x4_t{t[0] & m, t[1] & m, t[2] & m, t[3] & m};
+    acc[0] = mfma16x16x32(wf[0][u], xv, acc[0]);
+    acc[1] = mfma16x16x32(wf[1][u], xv, acc[1]);
+  }
+  if (c == 0) {
+    const __amdgpu_buffer_rsrc_t yr = coh_rsrc(j.y);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int rt = nr * (kMpRows / 16) + w * 2 + i;
+      const int n0 = rt * 16 + (lane >> 4) * 4;
+      if (rt >= NRB || n0 >= N) continue;
+      float o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = acc[i][e] + ((ks == 0 && j.bias) ? bf2f(j.bias[n0 + e]) : 0.f);
+      coh_st16(yr, (int)(((long long)ks * N + n0) * 4),
+               u32x4_t{__float_as_uint(o[0]), __float_as_uint(o[1]), __float_as_uint(o[2]), __float_as_uint(o[3])});
+    }
+  }
+}
+
+// K-sliced router block (one token): block kp owns the K slice [kp * KS, (kp
+// + 1) * KS) of the 2048-wide residual (KS = 256: 8 fragments of 32) and every
+// expert (wave w: expert row blocks w, w + 8, ...).  It reads only its slice of
+// the projection's K-split partials (8 KB instead of the whole 64 KB rows),
+// forms r = bf16(x + bf16(y)) there, stores that slice of r and the slice's
+// sum of squares, and the partial logits sum_k W[e, k] * (r_k * gamma_k) of
+// the slice (fp32 operand as bf16 hi + lo) -- the post-attention RMSNorm's
+// 1 / rms is one factor of every logit, which the expert launch applies once
+// it has added the slices' sums of squares (and with which it forms the
+// experts' bf16 input (r * gamma) * rinv itself).
+constexpr int kRsKb = 8;                      // fragments of 32 per K slice
+MKD_DEV void router_kslice_block(const AttnJoinArgs& j, int kp) {
+  __shared__ __attribute__((aligned(16))) u32x4_t ops[2][kRsKb * 4];   // hi / lo operands of the slice
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int N = j.N, KB = N / 32;
+  const int KS = kRsKb * 32, k0 = kp * KS;
+  const int nerb = j.E / 16;
+  // the weights of the wave's expert row blocks (at most 2 per wave: E <= 256)
+  u32x4_t wf[2][kRsKb];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (w + 8 * i >= nerb) break;               // wave-uniform
+    const uint16_t* wrow = j.rw + ((long long)(w + 8 * i) * KB + kp * kRsKb) * 512 + lane * 8;
+#pragma unroll
+    for (int u = 0; u < kRsKb; ++u)
+      wf[i][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + u * 512));
+  }
+  if (w == 0) {
+    // lane l: elements k0 + 4 l .. + 4 of the slice -- the residual, gamma and
+    // the o_parts partials of y (polled until no word holds the empty marker)
+    const int k = k0 + 4 * lane;
+    const uint2 xr = *reinterpret_cast<const uint2*>(j.rx + k);
+    const uint2 gr = *reinterpret_cast<const uint2*>(j.rgamma + k);
+    const __amdgpu_buffer_rsrc_t yr = coh_rsrc(j.y);
+    u32x4_t p[kMpMaxParts];
+    for (unsigned it = 0;; ++it) {
+#pragma unroll
+      for (int q = 0; q < kMpMaxParts; ++q) p[q] = coh_ld16(yr, (int)(((long long)min(q, j.o_parts - 1) * N + k) * 4));
+      bool ok = true;
+#pragma unroll
+      for (int q = 0; q < kMpMaxParts; ++q)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) ok = ok && p[q][e] != kPollEmpty;
+      if (__all(ok) || coh_poll_giveup(it, j.err)) break;
+      __builtin_amdgcn_s_sleep(1);
+    }
+    f32x4_t y = __builtin_bit_cast(f32x4_t, p[0]);
+#pragma unroll
+    for (int q = 1; q < kMpMaxParts; ++q)
+      if (q < j.o_parts) y += __builtin_bit_cast(f32x4_t, p[q]);
+    const float xv[4] = {bf_lo(xr.x), bf_hi(xr.x), bf_lo(xr.y), bf_hi(xr.y)};
+    const float gv[4] = {bf_lo(gr.x), bf_hi(gr.x), bf_lo(gr.y), bf_hi(gr.y)};
+    float r[4], ss = 0.f;
+    uint32_t hi[2], lo[2];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      r[e] = rbf(xv[e] + rbf(y[e]));
+      ss += r[e] * r[e];
+    }
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float v0 = r[2 * e] * gv[2 * e], v1 = r[2 * e + 1] * gv[2 * e + 1];
+      const uint32_t h0 = f2bf(v0), h1 = f2bf(v1);
+      hi[e] = h0 | (h1 << 16);
+      lo[e] = f2bf(v0 - bf2f(h0)) | (f2bf(v1 - bf2f(h1)) << 16);
+    }
+    *reinterpret_cast<uint2*>(j.rresid + k) = uint2{pack2bf(r[0], r[1]), pack2bf(r[2], r[3])};
+    // operands in B order: 16-byte piece lane / 2 (8 elements), half lane % 2
+    reinterpret_cast<uint2*>(ops[0])[lane] = uint2{hi[0], hi[1]};
+    reinterpret_cast<uint2*>(ops[1])[lane] = uint2{lo[0], lo[1]};
+    ss = wave_sum(ss);
+    if (lane == 0) j.rss[kp] = ss;
+  }
+  lds_barrier();   // the operands; the weight loads stay in flight
+  // MFMAs: B lane l = token l % 16 (token 0 only), k (l / 16) * 8 .. + 8 of each fragment
+  const int c = lane & 15;
+  const uint32_t m = c == 0 ? 0xffffffffu : 0u;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int erb = w + 8 * i;
+    if (erb >= nerb) break;                     // wave-uniform
+    f32x4_t acc[2] = {f32x4_t{0.f, 0.f, 0.f, 0.f}, f32x4_t{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int u = 0; u < kRsKb; ++u) {
+      const u32x4_t h = ops[0][u * 4 + (lane >> 4)], l = ops[1][u * 4 + (lane >> 4)];
+      acc[0] = mfma16x16x32(wf[i][u], u32x4_t{h[0] & m, h[1] & m, h[2] & m, h[3] & m}, acc[0]);
+      acc[1] = mfma16x16x32(wf[i][u], u32x4_t{l[0] & m, l[1] & m, l[2] & m, l[3] & m}, acc[1]);
+    }
+    if (c == 0)
+      *reinterpret_cast<f32x4_t*>(j.rparts + (long long)kp * j.E + erb * 16 + (lane >> 4) * 4) = acc[0] + acc[1];
+  }
+}
+
+// The 512-thread joined launch at one token (d = 128): chunk blocks (8 waves x
+// 16 positions: 128-position chunks), merge + projection blocks, K-sliced
+// router blocks.
+template <int GQA>
+__global__ void __launch_bounds__(512) attn_joined_mp_kernel(AttnArgs a, AttnJoinArgs j, int rope_mode) {
+  const int bid = blockIdx.x;
+  const int na = a.n_chunks * a.nkv;
+  if (bid < na) {
+    attn_chunk_block<128, GQA, 1, true, 8>(a, rope_mode, bid % a.n_chunks, bid / a.n_chunks, 0, j.flags + bid);
+    return;
+  }
+  const int ksn = a.nq / kMpHeads, nmp = attn_join_mp_blocks(a.nq, j.N);
+  if (bid < na + nmp) {
+    const int q = bid - na;
+    mp_block8<GQA>(a, j, q % ksn, q / ksn);
+  } else {
+    router_kslice_block(j, bid - na - nmp);
+  }
+}
+
+int attn_join_kslice_parts(int B, int nq, int nkv, int d, int S_max, int E, int N) {
+  const int gqa = nkv > 0 ? nq / nkv : 0;
+  if (B != 1 || d != 128 || nq % kMpHeads || nq / kMpHeads > kMpMaxParts || gqa * nkv != nq ||
+      (gqa != 1 && gqa != 2 && gqa != 4 && gqa != 8 && gqa != 16) || E % 16 || E > 256 ||
+      N % (kRsKb * 32) || N / (kRsKb * 32) > 8 || N > 2048 || attn_chunk_for(B, nkv, S_max) != 128)
+    return 0;
+  // one block per CU (512 threads, > 128 VGPRs): the whole grid resident at once
+  const int blocks = (S_max + 1 + 127) / 128 * nkv + attn_join_mp_blocks(nq, N) + N / (kRsKb * 32);
+  const int cus = device_cus();
+  if (cus <= 0 || blocks > cus) return 0;
+  return N / (kRsKb * 32);
+}
+
+bool attn_join_kslice_ok(const AttnArgs& a, const AttnJoinArgs& j) {
+  return attn_join_mp_ok(a, j) && a.chunk == 128 && j.E % 16 == 0 && j.E <= 256 && j.N % (kRsKb * 32) == 0 &&
+         j.N / (kRsKb * 32) <= 8 && j.rx_f32 && j.o_parts <= kMpMaxParts;
+}
+
 // ---- router stage: the post-attention residual, norm and router logits ----
 constexpr int kJoinRouterF = 8;      // router weight fragments per wave
 constexpr int kJoinRouterMaxN = 3072;
@@ -1160,6 +1428,18 @@ hipError_t attn_join_launch(const AttnArgs& ain, const AttnJoinArgs& jin, int ro
   if (j.rw && (!attn_join_router_supported(a.B, j.E, j.N) || j.N % 16 || !j.rx || !j.rgamma ||
                !j.rparts || !j.rresid || !j.rhnorm))
     return hipErrorInvalidValue;
+  if (j.rss) {   // the K-sliced router form (the 512-thread launch)
+    if (!j.dpoll || !attn_join_kslice_ok(a, j)) return hipErrorInvalidValue;
+    const int blocks = a.n_chunks * a.nkv + attn_join_mp_blocks(a.nq, j.N) + j.N / (kRsKb * 32);
+    switch (a.nq / a.nkv) {
+      case 1: return timed_launch(attn_joined_mp_kernel<1>, dim3(blocks), dim3(512), 0, s, a, j, rope_mode);
+      case 2: return timed_launch(attn_joined_mp_kernel<2>, dim3(blocks), dim3(512), 0, s, a, j, rope_mode);
+      case 4: return timed_launch(attn_joined_mp_kernel<4>, dim3(blocks), dim3(512), 0, s, a, j, rope_mode);
+      case 8: return timed_launch(attn_joined_mp_kernel<8>, dim3(blocks), dim3(512), 0, s, a, j, rope_mode);
+      case 16: return timed_launch(attn_joined_mp_kernel<16>, dim3(blocks), dim3(512), 0, s, a, j, rope_mode);
+    }
+    return hipErrorInvalidValue;
+  }
   const int gqa = a.nq / a.nkv;
   if (a.d == 128) {
     switch (gqa) {

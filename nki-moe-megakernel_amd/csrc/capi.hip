@@ -301,7 +301,8 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
              MoeWs& w, hipStream_t s, bool do_finalize = true, int wfmt = 0,
              const void* gu_scales = nullptr, const void* dn_scales = nullptr, bool tiled = false,
              const RouterArgs* sel = nullptr, unsigned* fused_flags = nullptr,
-             unsigned* fused_err = nullptr, uint16_t* poll_h = nullptr) {
+             unsigned* fused_err = nullptr, uint16_t* poll_h = nullptr,
+             const uint16_t* hn_r = nullptr, const uint16_t* hn_gamma = nullptr) {
   if (sel && (idx || wfmt || tiled)) return MKD_ERR_INVALID;
   if (fused_flags && !sel) return MKD_ERR_INVALID;
   if (idx)  // otherwise the router stage already built the expert groups
@@ -438,6 +439,11 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
     f.r = *sel;
     f.flags = fused_flags; f.err = fused_err;
     f.poll_h = T == 1 ? poll_h : nullptr;
+    if (sel->ss_parts) {   // the experts' input is formed in the launch (K-sliced router form)
+      f.hn_r = hn_r;
+      f.hn_gamma = hn_gamma;
+      f.hn_out = const_cast<uint16_t*>(hidden);
+    }
     const int ps = prof_begin(MKD_KCLASS_MOE_GATE_UP, s);
     MKD_TRY(moe_fused_launch(f, gmax, s), "moe router select + gate_up + down");
     prof_end(ps, s);
@@ -1225,6 +1231,7 @@ struct StepWs {
   // with kPollEmpty at the start of every decode call
   float* poll;
   long long poll_po, poll_pml, poll_y, poll_h, poll_layer;   // words per layer
+  float* rss;   // the K-sliced router form's slice sums of squares (one token)
 };
 
 static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
@@ -1234,6 +1241,7 @@ static StepWs carve_step(Carver& c, const mkd_qwen3_model* m, int B) {
   w.nbf = c.take<uint16_t>((size_t)B * m->H);
   w.nf32 = c.take<float>((size_t)B * m->H);
   w.logits = c.take<float>((size_t)16 * B * m->E);  // split-K partials (<= 16)
+  w.rss = c.take<float>(64);
   w.cos = c.take<float>((size_t)B * m->d);
   w.sin = c.take<float>((size_t)B * m->d);
   w.oparts = c.take<float>((size_t)std::max({2, o_proj_kgrid(m, B), B == 1 ? attn_join_y_parts(m->nq) : 1}) *
@@ -1494,6 +1502,13 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
     // the residual add, post-attention norm and router GEMM as the joined
     // attention launch's last blocks (replacing the router launch)
     const bool router_join = join_attn && lsync && router_in_attention_planned(m, B, l);
+    // one token: the router blocks each own a K slice (their partial logits lack
+    // the 1 / rms factor, applied -- with the experts' input -- by the expert
+    // launch), where that launch is the joined one with the split routing
+    const int kslice = (router_join && fused_moe && defer_ok && !oss && !m->router_bias && w.poll && w.poll_po)
+                           ? attn_join_kslice_parts(B, m->nq, m->nkv, m->d,
+                                                    m->layer_s_max ? m->layer_s_max[l] : m->S_max, m->E, m->H)
+                           : 0;
     if (router_join) {
       ja.rx = static_cast<const uint16_t*>(x);
       ja.rgamma = static_cast<const uint16_t*>(m->ln_post[l]);
@@ -1502,6 +1517,7 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
       ja.rresid = w.r; ja.rhnorm = w.nbf;
       ja.reps = m->eps; ja.rinv_h = 1.0f / (float)ha;
       ja.E = m->E; ja.rx_f32 = oss ? 0 : 1;
+      ja.rss = kslice ? w.rss : nullptr;
       if (w.poll && w.poll_po) {
         float* pl = w.poll + (size_t)l * w.poll_layer;
         ja.poll_po = pl;
@@ -1536,8 +1552,14 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
       // the partial logits came from the attention launch
       sel = ra;
       sel.parts = w.logits;
-      sel.nparts = attn_join_router_parts(m->H);
+      sel.nparts = kslice ? kslice : attn_join_router_parts(m->H);
       sel.part_stride = (long long)B * m->E;
+      if (kslice) {
+        sel.ss_parts = w.rss;
+        sel.nss = kslice;
+        sel.ss_eps = m->eps;
+        sel.ss_inv_h = 1.0f / (float)ha;
+      }
       defer_sel = defer_ok;
       if (!defer_sel) MKD_TRY(router_select_launch(sel, s), "router select");
     } else if (router_fused_supported(B, m->E, m->H)) {
@@ -1613,7 +1635,9 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
                           defer_sel ? &sel : nullptr,
                           fused_moe ? lsync : nullptr,
                           fused_moe ? w.sync : nullptr,
-                          fused_moe && w.poll_h ? reinterpret_cast<uint16_t*>(w.poll + (size_t)l * w.poll_layer + w.poll_po + w.poll_pml + w.poll_y) : nullptr))
+                          fused_moe && w.poll_h ? reinterpret_cast<uint16_t*>(w.poll + (size_t)l * w.poll_layer + w.poll_po + w.poll_pml + w.poll_y) : nullptr,
+                          kslice ? w.r : nullptr,
+                          kslice ? static_cast<const uint16_t*>(m->ln_post[l]) : nullptr))
       return rc;
     // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention
     // norm (with fuse_qn: the next QKV kernel does both; after the last layer the

@@ -149,6 +149,8 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   __shared__ int s_ptok[kSelMaxPairs], s_pslot[kSelMaxPairs];
   __shared__ float s_w[kSelMaxPairs];
   __shared__ OneTokenSel sel;
+  __shared__ float s_rinv;
+  __shared__ __attribute__((aligned(16))) uint16_t s_hn[kFusedHnMax];   // the experts' input (K-sliced router form)
   __shared__ f32x4_t s_red[DRB][4][64];
   __shared__ u32x4_t s_h[kFusedMaxRows][NFD * 8];   // h rows of a down block's group
   const int bid = blockIdx.x;
@@ -173,12 +175,22 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   int *t_ng = &s_ng, *t_gexp = s_gexp, *t_gcnt = s_gcnt, *t_goff = s_goff, *t_ptok = s_ptok, *t_pslot = s_pslot;
   float* t_w = s_w;
   float lg[2];
+  // K-sliced router form: the post-attention residual and gamma for the
+  // experts' input, loaded before the routing (4 elements per thread)
+  const bool hn_self = split && r.ss_parts && f.hn_r;
+  const int H = f.gu.K;
+  uint2 hr = {0u, 0u}, hg = {0u, 0u};
+  if (hn_self && (int)threadIdx.x * 4 < H) {
+    hr = *reinterpret_cast<const uint2*>(f.hn_r + threadIdx.x * 4);
+    hg = *reinterpret_cast<const uint2*>(f.hn_gamma + threadIdx.x * 4);
+  }
   // a down block's weight slice does not depend on the routing: its row block
   // and K half are fixed, only the expert offset is not -- so the routing comes
   // first, then the loads
   if (split) {
     // the joined attention launch's router stage leaves <= 8 partial logits
-    float raw[8][2];
+    // (and, K-sliced, <= 8 slice sums of squares: logits = rinv * sum)
+    float raw[8][2], ssr[8];
     select_one_experts(q,
         [&]() {
 #pragma unroll
@@ -186,18 +198,37 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
 #pragma unroll
             for (int j = 0; j < 2; ++j)
               raw[p][j] = q.parts[min(p, q.nparts - 1) * q.part_stride + min(lane + 64 * j, q.E - 1)];
+          if (q.ss_parts)
+#pragma unroll
+            for (int p = 0; p < 8; ++p) ssr[p] = q.ss_parts[min(p, q.nss - 1)];
         },
         [&](float (&l)[2]) {
+          float rinv = 1.f;
+          if (q.ss_parts) {
+            float t = 0.f;
+#pragma unroll
+            for (int p = 0; p < 8; ++p)
+              if (p < q.nss) t += ssr[p];
+            rinv = 1.0f / sqrtf(t * q.ss_inv_h + q.ss_eps);
+            if (lane == 0) s_rinv = rinv;
+          }
 #pragma unroll
           for (int j = 0; j < 2; ++j) {
             float v = 0.f;
 #pragma unroll
             for (int p = 0; p < 8; ++p)
               if (p < q.nparts) v += raw[p][j];
+            if (q.ss_parts) v *= rinv;
             l[j] = q.bias ? v + bf2f(q.bias[min(lane + 64 * j, q.E - 1)]) : v;
           }
         },
         [] {}, sel, lg);
+    if (hn_self && (int)threadIdx.x * 4 < H) {   // rinv in LDS since select_one_experts' barrier
+      const float ri = s_rinv;
+      *reinterpret_cast<uint2*>(s_hn + threadIdx.x * 4) =
+          uint2{pack2bf((bf_lo(hr.x) * bf_lo(hg.x)) * ri, (bf_hi(hr.x) * bf_hi(hg.x)) * ri),
+                pack2bf((bf_lo(hr.y) * bf_lo(hg.y)) * ri, (bf_hi(hr.y) * bf_hi(hg.y)) * ri)};
+    }
     t_ng = &sel.ng; t_gexp = sel.gexp; t_gcnt = sel.gcnt; t_goff = sel.goff;
     t_ptok = sel.ptok; t_pslot = sel.pslot; t_w = sel.w;
   } else if (one) {
@@ -223,6 +254,7 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   }
   if (gu_role) {
     GemmArgs b = f.gu;
+    if (hn_self) b.x = s_hn;             // the operand from LDS (generic loads)
     b.n_groups = t_ng;
     b.grp_expert = t_gexp; b.grp_count = t_gcnt; b.grp_offset = t_goff;
     b.pair_row = t_ptok; b.pair_out_row = t_pslot;
@@ -249,6 +281,9 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
     for (int u = 0; u < NFD; ++u)
       wf[i][u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wrow + u * 512));
   }
+  if (lead && hn_self && f.hn_out)
+    for (int i = threadIdx.x * 8; i < H; i += blockDim.x * 8)
+      *reinterpret_cast<u32x4_t*>(f.hn_out + i) = *reinterpret_cast<const u32x4_t*>(s_hn + i);
   if (split && wave == 0) {
     q.slot_w = lead ? r.slot_w : nullptr;
     select_one_weights(q, sel, lg);   // sel.w: read after the barriers below
@@ -404,6 +439,12 @@ hipError_t moe_fused_launch(MoeFusedArgs f, int groups_max, hipStream_t s) {
       !r.pair_token || !r.pair_slot || !a.grp_expert || !f.flags || !f.err || groups_max < 1 ||
       groups_max > kSelMaxPairs || (f.dn.ldx & 7) || (f.dn.ldy & 3))
     return hipErrorInvalidValue;
+  if (r.ss_parts) {   // the K-sliced router form: the kernel's split routing must apply
+    const bool split = r.T == 1 && r.E <= 128 && r.nparts <= 8 && ((r.mode & 8) || !(r.mode & 3));
+    if (!split || r.nss < 1 || r.nss > 8 || !f.hn_r || !f.hn_gamma || a.K > kFusedHnMax || a.K % 8 ||
+        a.K > 4 * 512)
+      return hipErrorInvalidValue;
+  }
   if (f.poll_h) {   // h goes to the launch's own pre-filled buffer
     f.gu.y = f.poll_h;
     f.dn.x = f.poll_h;

@@ -377,6 +377,13 @@ struct AttnJoinArgs {
   float reps, rinv_h;         // norm epsilon, 1 / hidden size it averages over
   int E;
   int rx_f32;                 // 1: router operand fp32 (bf16 hi + lo), 0: bf16
+  // K-sliced router form (one token, d = 128, the merge + projection blocks;
+  // attn_join_kslice_supported): rss set -> the router blocks each own a K
+  // slice of N / kRouterSlices and write rparts [kRouterSlices][E] as
+  // sum_k W[e,k] * (r_k * gamma_k) over their slice (no 1 / rms factor), rss
+  // [kRouterSlices] the slice's sum of r^2, and their slice of rresid; rhnorm is
+  // not written (the consumer forms rinv and the normalised rows itself)
+  float* rss;
   // set by attn_join_launch: one token with d = 128 and the router stage merges
   // the chunk partials inside the projection blocks (no combine blocks), which
   // then write o_parts K-split partials of y ([o_parts][B][N]); else 0 and 1
@@ -399,6 +406,9 @@ int attn_join_flag_words(int B, int nq, int nkv, int n_chunks, int N);
 bool attn_join_supported(const AttnArgs& a, int N);
 int attn_join_router_parts(int N);
 bool attn_join_router_supported(int B, int E, int N);
+// The K-sliced router form's slices (N / 256) when it applies to one token of
+// these shapes (d = 128, 128-position chunks), else 0.
+int attn_join_kslice_parts(int B, int nq, int nkv, int d, int S_max, int E, int N);
 hipError_t attn_join_launch(const AttnArgs& a, const AttnJoinArgs& j, int rope_mode, hipStream_t s);
 
 // moe.hip
@@ -415,6 +425,12 @@ struct RouterArgs {
   float* slot_w;              // [T*K] or null
   // expert grouping (all null = skip)
   int *n_groups, *grp_expert, *grp_count, *grp_offset, *pair_token, *pair_slot;
+  // one token, the K-sliced router form: the partials lack the post-attention
+  // norm's 1 / rms, formed here from nss slice sums of squares:
+  // rinv = 1 / sqrt(sum * ss_inv_h + ss_eps), logits = rinv * sum of the partials
+  const float* ss_parts;
+  int nss;
+  float ss_eps, ss_inv_h;
 };
 hipError_t router_select_launch(const RouterArgs& a, hipStream_t s);
 // Any number of tokens, no expert grouping (n_groups must be null): 16 tokens
@@ -448,6 +464,7 @@ constexpr int kSelMaxPairs = 64;
 // the down blocks wait on their group's flags; *err is set when a wait ran out.
 int device_cus();                   // compute units of the current device (0 if unknown)
 constexpr int kFusedMaxRows = 4;   // tokens of the fused expert launch (rows per group)
+constexpr int kFusedHnMax = 2048;  // hidden size of the experts' input formed in LDS (K-sliced router form)
 struct MoeFusedArgs {
   GemmArgs gu, dn;
   RouterArgs r;
@@ -459,6 +476,12 @@ struct MoeFusedArgs {
   // flags; the down blocks poll their h row itself (one coherent round trip
   // fewer than a flag wait followed by the loads)
   uint16_t* poll_h;
+  // with r.ss_parts (one token): every block forms the experts' input
+  // bf16((r * gamma) * rinv) from the post-attention residual itself (into LDS,
+  // the gate/up operand); the first down block also stores it to hn_out
+  const uint16_t* hn_r;
+  const uint16_t* hn_gamma;
+  uint16_t* hn_out;
 };
 bool moe_fused_supported(int T, int K, int E, int H, int I);
 int moe_fused_flag_words(int T, int K, int E, int I);

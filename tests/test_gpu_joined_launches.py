@@ -11,7 +11,8 @@ top-8, I 768), 3 layers chained:
 * against the same layers with every stage a launch of its own
   (set_decode_path("separate_launches")): identical routing in layer 0,
   hidden states and written K rows within 1e-2 (only fp32 summation orders
-  differ);
+  differ) unless a later layer's top-k differs at a near-tie of the two paths'
+  logits (asserted to be one);
 * against the fp32 oracle, teacher-forced on the decode path's own routing log
   (router rows checked against the oracle router, near-tie flips against the
   oracle's logit gap), within 2e-2;
@@ -90,16 +91,28 @@ def test_joined_launches_vs_separate_and_oracle(mk, dev, restore_path, B, S):
     assert not model.router_in_attention(B)
     y_s, k_s, log_s = _run(model, x, kcs, vcs, pos, dev)
     e = max_abs_rel(y_f, y_s)
-    print(f"joined vs separate launches, 3 layers: {e:.2e}", flush=True)
-    assert e < 1e-2
-    # layer 0 sees identical inputs on both paths: identical routing
-    assert torch.equal(log_f[0]["idx"], log_s[0]["idx"])
+    # the two paths add in different orders (one token: the attention's chunks
+    # span 8 waves of 16 positions, the router's K in slices), so a later
+    # layer's top-k may differ at a near-tie; then each expert the joined path
+    # chose beyond the other's top-k must sit within twice the two paths' logit
+    # difference of its K-th logit, and the hidden states are not compared
+    flipped = [l for l in range(3) if not torch.equal(log_f[l]["idx"], log_s[l]["idx"])]
+    print(f"joined vs separate launches, 3 layers: {e:.2e} (routing differs in layers {flipped})", flush=True)
+    for l in flipped:
+        check_oracle_flips(log_f[l]["idx"], log_f[l]["logits"], log_s[l]["logits"], 8)
+    if not flipped:
+        assert e < 1e-2
+    # layer 0 sees identical inputs on both paths: identical routing, and its
+    # post-attention residual within 1e-2
+    assert 0 not in flipped
+    assert max_abs_rel(log_f[0]["r"], log_s[0]["r"]) < 1e-2
     for l in range(3):
         for b in range(B):
             p = int(pos[b])
             changed = (k_f[l][b] != kcs[l][b]).any(-1).any(0).nonzero().flatten().tolist()
             assert changed == [p], (l, b, p, changed[:8])
-            assert max_abs_rel(k_f[l][b, :, p], k_s[l][b, :, p]) < 1e-2
+            if not any(f < l for f in flipped):
+                assert max_abs_rel(k_f[l][b, :, p], k_s[l][b, :, p]) < 1e-2
     # the joined path's layers against the oracle, teacher-forced on its routing log
     lws = [_ref_layer(h) for h in hfs]
     cos, sin = ref.rope_cos_sin(pos, 128, cfg.rope_theta)
