@@ -293,12 +293,30 @@ MKD_DEV void mx_batch(const uint8_t* const (&wrow)[RB], const uint8_t* const (&s
           (int)(ws[r][u] & 0xffu), 0, (int)(xsc[u] & 0xffu));
 }
 
-template <int RB, int FMT, int EPI>
+// Fragments per batch of one wave's loads for R streamed row tiles: as many as
+// fit 64 VGPRs (R x U weight fragments with their scale words, U x-code
+// fragments), rounded down to 8 / 4 / 2 / 1.  Small batches keep the kernel
+// near 100 VGPRs, i.e. 4 waves per SIMD: measured at bs=32 (MXFP8 gate/up
+// 84.6 -> 69.5 us, down 52.6 -> 38.5 us against 128-VGPR batches), the number
+// of waves in flight matters more than the bytes each has in flight.
+template <int FMT, int R>
+constexpr int mx_batch_frags() {
+  constexpr int per = 8 + (MxSpec<FMT>::BPL / 4 + 1) * R;
+  constexpr int u = 64 / per;
+  return u >= 8 ? 8 : u >= 4 ? 4 : u >= 2 ? 2 : 1;
+}
+
+// RT output tiles (16*RB rows each) per block: every wave streams the
+// fragments of all RT tiles of its K slice, so a block moves RT times the bytes
+// of a one-tile block for the same reduction and launch cost.
+template <int RB, int FMT, int EPI, int RT>
 __global__ void __launch_bounds__(512) gemm_mx_kernel(GemmArgs a) {
   constexpr int BPL = MxSpec<FMT>::BPL;
+  constexpr int R = RB * RT;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int rbase = blockIdx.x;
+  const int tile0 = blockIdx.x * RT;
+  const int n_tiles = (a.N + 16 * RB - 1) / (16 * RB);
   const int group = blockIdx.y;
   const int kg = a.kgrid > 1 ? a.kgrid : 1;
   const int kblk = blockIdx.z % kg;
@@ -336,30 +354,41 @@ __global__ void __launch_bounds__(512) gemm_mx_kernel(GemmArgs a) {
   const int kb0 = (kblk * (int)(blockDim.x >> 6) + wave) * NF;
   const int q = lane >> 4;
 
-  f32x4_t acc[RB][1];
+  f32x4_t acc[R][1];
 #pragma unroll
-  for (int r = 0; r < RB; ++r) acc[r][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  const uint8_t* wrow[RB];
-  const uint8_t* srow[RB];
+  for (int r = 0; r < R; ++r) acc[r][0] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // row tile t of the block, row block r of the tile -> stream row R*t + r;
+  // tiles past the last (a ragged final block) re-read the last one and are
+  // not stored
+  const uint8_t* wrow[R];
+  const uint8_t* srow[R];
 #pragma unroll
-  for (int r = 0; r < RB; ++r) {
-    const long long rb = rbase * RB + r;
-    wrow[r] = w + ((rb * KB + kb0) * 64 + lane) * BPL;
-    srow[r] = wsc + (rb * KB4 * 64 + lane) * 4;
-  }
-  // batches of U fragments per row block (<= 16 KiB of weight loads in flight
-  // per wave), remainder in batches of 4/2/1
-  constexpr int U = 8 / RB;
+  for (int t = 0; t < RT; ++t)
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const long long rb = (long long)min(tile0 + t, n_tiles - 1) * RB + r;
+      wrow[t * RB + r] = w + ((rb * KB + kb0) * 64 + lane) * BPL;
+      srow[t * RB + r] = wsc + (rb * KB4 * 64 + lane) * 4;
+    }
+  constexpr int U = mx_batch_frags<FMT, R>();
   int f = 0;
-  for (; f + U <= NF; f += U) mx_batch<RB, FMT, U>(wrow, srow, xrow[0], a, kb0, f, q, acc);
+  for (; f + U <= NF; f += U) mx_batch<R, FMT, U>(wrow, srow, xrow[0], a, kb0, f, q, acc);
   if constexpr (U > 4)
-    if (f + 4 <= NF) { mx_batch<RB, FMT, 4>(wrow, srow, xrow[0], a, kb0, f, q, acc); f += 4; }
+    if (f + 4 <= NF) { mx_batch<R, FMT, 4>(wrow, srow, xrow[0], a, kb0, f, q, acc); f += 4; }
   if constexpr (U > 2)
-    if (f + 2 <= NF) { mx_batch<RB, FMT, 2>(wrow, srow, xrow[0], a, kb0, f, q, acc); f += 2; }
+    if (f + 2 <= NF) { mx_batch<R, FMT, 2>(wrow, srow, xrow[0], a, kb0, f, q, acc); f += 2; }
   if constexpr (U > 1)
-    if (f < NF) mx_batch<RB, FMT, 1>(wrow, srow, xrow[0], a, kb0, f, q, acc);
+    if (f < NF) mx_batch<R, FMT, 1>(wrow, srow, xrow[0], a, kb0, f, q, acc);
 
-  gemm_finish<RB, 1, EPI>(a, acc, lane, wave, rbase, group, t0, base, xrow, kblk);
+#pragma unroll
+  for (int t = 0; t < RT; ++t) {
+    if (tile0 + t >= n_tiles) break;          // block-uniform
+    if (t > 0) __syncthreads();               // the previous tile's reduction buffer is free
+    f32x4_t at[RB][1];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) at[r][0] = acc[t * RB + r][0];
+    gemm_finish<RB, 1, EPI>(a, at, lane, wave, tile0 + t, group, t0, base, xrow, kblk);
+  }
   if (!a.t_loop) return;
   }
 }
@@ -411,8 +440,13 @@ hipError_t mx_pack_launch(const uint8_t* codes, const uint8_t* scales, uint8_t* 
 }
 
 int choose_kw_mx(int K_pad) {
-  // per-wave K slice (multiple of 128) splitting K_pad over <= 8 waves
-  for (int kw : {512, 384, 256, 128, 1024, 768, 1536, 2048})
+  // per-wave K slice (multiple of 128) splitting K_pad over <= 8 waves: 4 or 8
+  // waves per block first, so that whole blocks fill a CU's 16 wave slots
+  // (measured: MXFP4 gate/up at K_pad 3072, 6-wave blocks 83.8 us, 4-wave
+  // blocks 58.1 us), then slices of 2^i fragments (whole batches)
+  for (int nw : {4, 8})
+    if (K_pad % (128 * nw) == 0) return K_pad / nw;
+  for (int kw : {512, 256, 1024, 128, 384, 768, 1536, 2048})
     if (K_pad % kw == 0 && K_pad / kw <= 8) return kw;
   return -1;
 }
@@ -422,15 +456,25 @@ int mx_kpad(int K) {
   return choose_kw_mx(p) > 0 ? p : (K + 511) / 512 * 512;
 }
 
-template <int RB, int FMT, int EPI>
+template <int RB, int FMT, int EPI, int RT>
 static hipError_t launch_mx(const GemmArgs& a, int n_tiles, int groups, int ttiles, hipStream_t s) {
   const int nsplit = a.K / a.KW;
   if (a.KW <= 0 || a.KW % 128 || nsplit < 1 || nsplit > 8 || nsplit * a.KW != a.K)
     return hipErrorInvalidValue;
-  dim3 grid(n_tiles, groups, ttiles);
+  dim3 grid((n_tiles + RT - 1) / RT, groups, ttiles);
   dim3 block(64 * nsplit);
   const size_t lds = nsplit > 1 ? (size_t)nsplit * RB * 4 * 64 * sizeof(float) : 0;
-  return timed_launch(gemm_mx_kernel<RB, FMT, EPI>, grid, block, lds, s, a);
+  return timed_launch(gemm_mx_kernel<RB, FMT, EPI, RT>, grid, block, lds, s, a);
+}
+
+// Output tiles per block.  Measured at bs=32: one tile everywhere except the
+// MXFP4 down projection (a 1 KiB fragment per row tile), where four tiles per
+// block took 42.8 -> 39.3 us (GPT-OSS shape); for MXFP8 and for gate/up, more
+// tiles per block cost occupancy and were slower.
+int mx_tiles_per_block(int RB, int fmt, int n_tiles, int groups) {
+  constexpr long long kMxMinBlocks = 1024;
+  if (RB == 1 && fmt == MX_E2M1 && (long long)((n_tiles + 3) / 4) * groups >= kMxMinBlocks) return 4;
+  return 1;
 }
 
 hipError_t gemm_mx_launch(GemmArgs a, int fmt, int epi, int groups_max, int max_tokens_per_group,
@@ -444,8 +488,13 @@ hipError_t gemm_mx_launch(GemmArgs a, int fmt, int epi, int groups_max, int max_
     a.t_loop = 1;
     ttiles = 1;
   }
-#define MKD_M(RB_, F_, E_) \
-  if (RB == RB_ && fmt == F_ && epi == E_) return launch_mx<RB_, F_, E_>(a, n_tiles, groups, ttiles, s);
+  const int rt = mx_tiles_per_block(RB, fmt, n_tiles, groups);
+#define MKD_M(RB_, F_, E_)                                                                 \
+  if (RB == RB_ && fmt == F_ && epi == E_) {                                               \
+    if constexpr (RB_ == 1)                                                                \
+      if (rt == 4) return launch_mx<RB_, F_, E_, 4>(a, n_tiles, groups, ttiles, s);        \
+    return launch_mx<RB_, F_, E_, 1>(a, n_tiles, groups, ttiles, s);                       \
+  }
   MKD_M(2, MX_E4M3, EPI_SWIGLU_BF16) MKD_M(2, MX_E2M1, EPI_SWIGLU_BF16)
   MKD_M(1, MX_E4M3, EPI_SCALE_F32) MKD_M(1, MX_E2M1, EPI_SCALE_F32)
   MKD_M(1, MX_E4M3, EPI_F32) MKD_M(1, MX_E2M1, EPI_F32)
