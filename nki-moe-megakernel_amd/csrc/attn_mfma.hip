@@ -115,8 +115,11 @@ __global__ void __launch_bounds__(D) attn_kv_write_kernel(AttnArgs a) {
 // One split-K chunk block (c, g, b).  COH: the block's outputs (partials and
 // staged k / v rows) are read by later blocks of the same launch -- they are
 // stored device-coherent and the block then sets *flag (also when the chunk
-// lies past the sequence and the block does nothing else).
-template <int D, int GQA, int TPW, bool COH, int NW = 4>
+// lies past the sequence and the block does nothing else).  ONE: the caller
+// has established one new token per sequence, no mask, a flat cache and heads
+// prepared here (no a.prep), so those cases' code -- runtime branches around
+// conditional loads in the score and P.V loops -- is not compiled in.
+template <int D, int GQA, int TPW, bool COH, int NW = 4, bool ONE = false>
 MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, int b, unsigned* flag) {
   constexpr int NK = D / 32;                  // QK MFMAs per tile (k = 32)
   constexpr int NDT = D / 16;                 // PV d-tiles
@@ -141,7 +144,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   // registers cost more occupancy than the overlap gains, and the rows are
   // loaded where they are used. ----
   constexpr bool PRE = TPW <= 2;
-  const bool flat = a.block_table == nullptr;
+  const bool flat = ONE || a.block_table == nullptr;
   int n = a.S_max;                            // row bound until the prior length is read
   const int dq = (lane >> 4) * (D / 4);       // lane's d range in a 16-row tile
   const int wbase = chunk0 + w * TPW * 16;
@@ -232,7 +235,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   // rows behind them), then the prior length and the cache rows ----
   constexpr int NR = (GQA + 2 + NW - 1) / NW;
   HeadPrep<D> hp[NR];
-  if (!a.prep) {
+  if (ONE || !a.prep) {
 #pragma unroll
     for (int r = 0; r < NR; ++r) {
       const int h = w + NW * r;
@@ -248,17 +251,21 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   n = __builtin_amdgcn_readfirstlane(prior_clamp(a, n_raw));
   // the window: n cache positions, then the sequence's NT new tokens (NT = 1:
   // this row's own, in LDS; more: every new row's prepared k / v in `prep`)
-  const int NT = new_tokens(a), seq = seq_of(a, b), tk = tok_of(a, b);
+  const int NT = ONE ? 1 : new_tokens(a), seq = seq_of(a, b), tk = tok_of(a, b);
   const uint16_t* act0 =                      // new token 0's prepared heads
       NT > 1 ? a.prep + ((long long)seq * NT * a.nkv + g) * (GQA + 2) * D : nullptr;
   const long long act_stride = (long long)a.nkv * (GQA + 2) * D;                     // per new token
   const int total = n + NT;
-  if (chunk0 >= total) {                      // whole block: uniform exit
+  // a chunk past the sequence exits at once -- except in the ONE form: there
+  // the exit would depend on n, and the compiler then sinks the cache-row loads
+  // below it, behind n's round trip; the block instead runs with every
+  // position masked (its partial, M = -inf, L = 0, is never read)
+  if (!ONE && chunk0 >= total) {              // whole block: uniform exit
     if constexpr (COH) coh_publish(flag);
     return;
   }
   if (PRE && !flat) pre_loads();
-  if (a.prep) {
+  if (!ONE && a.prep) {
     const uint16_t* src = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
     for (int i = threadIdx.x * 8; i < (GQA + 2) * D; i += NW * 64 * 8) {
       const int h = i / D, d = i % D;
@@ -321,7 +328,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
       const int tp = wbase + tt * 16 + (lane >> 4) * 4 + i;   // position of acc[i]
       float sc = a.round_qwen ? rbf(rbf(acc[i]) * a.scale) : acc[i] * a.scale;
       bool ok = tp < total && hcol < GQA;
-      if (ok && a.mask) {
+      if (!ONE && ok && a.mask) {
         const int mt = (tp < n) ? tp : (a.mask_s_ctx - NT + (tp - n));
         ok = a.mask[(((long long)mt * (a.B / NT) + seq) * a.nq + g * GQA + hcol) * NT + tk] != 0;
       }
@@ -1118,7 +1125,10 @@ __global__ void __launch_bounds__(512) attn_joined_mp_kernel(AttnArgs a, AttnJoi
   const int bid = blockIdx.x;
   const int na = a.n_chunks * a.nkv;
   if (bid < na) {
-    attn_chunk_block<128, GQA, 1, true, 8>(a, rope_mode, bid % a.n_chunks, bid / a.n_chunks, 0, j.flags + bid);
+    if (!a.mask && !a.block_table && !a.prep)
+      attn_chunk_block<128, GQA, 1, true, 8, true>(a, rope_mode, bid % a.n_chunks, bid / a.n_chunks, 0, j.flags + bid);
+    else
+      attn_chunk_block<128, GQA, 1, true, 8>(a, rope_mode, bid % a.n_chunks, bid / a.n_chunks, 0, j.flags + bid);
     return;
   }
   const int ksn = a.nq / kMpHeads, nmp = attn_join_mp_blocks(a.nq, j.N);
