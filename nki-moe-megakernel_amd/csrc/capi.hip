@@ -1402,8 +1402,10 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
                 mkd_qwen3_route_log_bytes(m, B));
   const RouteLogLayout rlo = route_log_layout(B, m->E, m->K, m->H);
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (!cos) {
-    MKD_TRY(rope_table_launch(position_ids, m->inv_freq, B, m->d, w.cos, w.sin, s), "rope table");
+  // no tables given: this call forms them (in the persistent path's own launch,
+  // or in the one launch that starts the multi-kernel path)
+  const bool rope_here = !cos;
+  if (rope_here) {
     cos = w.cos;
     sin = w.sin;
   }
@@ -1413,8 +1415,11 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
                 m->k_cache[l] && m->v_cache[l] && m->ln_in[l] && m->ln_post[l] &&
                 (!m->expert_format || (m->gate_up_scales[l] && m->down_scales[l])),
                 MKD_ERR_NULL, "decode_layers: null weight in layer %d", l);
-  if (w.lk.plan.on && g_decode_path == 1 && !prefill)
+  if (w.lk.plan.on && g_decode_path == 1 && !prefill) {
+    if (rope_here)
+      MKD_TRY(rope_table_launch(position_ids, m->inv_freq, B, m->d, w.cos, w.sin, s), "rope table");
     return decode_layers_lk(m, B, x, position_ids, cos, sin, w, s);
+  }
   // Qwen3 flow: pre-attention norm (x*rinv)*g, Qwen rounding points, fp32 router
   // input.  GPT-OSS flow: rmsnorm_tkg's (x*g)*rinv with H_actual everywhere,
   // biases, sinks, sliding windows, bf16 router input with logit top-k.
@@ -1448,10 +1453,22 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
   const bool defer_ok = defer_select_ok(m, B);
   const bool fused_moe = joined_experts_planned(m, B) && w.flag_words > 0;
   const bool join_attn = g_inlaunch_sync && !prefill && w.attn_words > 0 && o_kgrid <= 1;
-  if (fused_moe || join_attn) MKD_TRY(sync_clear_launch(w.sync, w.sync_words, s), "clear sync words");
-  if ((join_attn || fused_moe) && w.poll)
-    MKD_TRY(fill_u32_launch(reinterpret_cast<uint32_t*>(w.poll), w.poll_layer * m->num_layers, kPollEmpty, s),
-            "fill the data-polled exchange buffers");
+  {
+    // the RoPE tables, the in-launch sync words and the data-polled exchange
+    // words (chunk partials only up to the position), one launch
+    DecodeBeginArgs db;
+    memset(&db, 0, sizeof(db));
+    db.pos = position_ids; db.inv_freq = m->inv_freq; db.B = B; db.d = m->d;
+    if (rope_here) { db.cos = w.cos; db.sin = w.sin; }
+    if (fused_moe || join_attn) { db.sync = w.sync; db.sync_words = w.sync_words; }
+    if ((join_attn || fused_moe) && w.poll) {
+      db.poll = reinterpret_cast<uint32_t*>(w.poll);
+      db.layer_words = w.poll_layer; db.po = w.poll_po; db.pml = w.poll_pml;
+      db.layers = m->num_layers; db.nq = w.poll_po ? m->nq : 0; db.n_chunks = w.attn.n_chunks; db.D = m->d;
+      db.chunk = w.attn.chunk; db.S_max = m->S_max;
+    }
+    MKD_TRY(decode_begin_launch(db, s), "decode begin (rope tables, sync words, exchange buffers)");
+  }
   for (int l = 0; l < m->num_layers; ++l) {
     const int wl = m->window ? m->window[l] : 0;
     mkd_attention_args ap;

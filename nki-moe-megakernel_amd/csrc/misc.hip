@@ -74,6 +74,56 @@ __global__ void rope_table_kernel(const int* __restrict__ pos, const float* __re
   sinv[b * d + i] = sinf(ang);
 }
 
+__global__ void decode_begin_kernel(DecodeBeginArgs d) {
+  const long long tid = blockIdx.x * (long long)blockDim.x + threadIdx.x;
+  const long long nth = (long long)gridDim.x * blockDim.x;
+  if (d.cos)
+    for (long long i = tid; i < (long long)d.B * d.d; i += nth) {
+      const int b = (int)(i / d.d), k = (int)(i % d.d);
+      const float ang = (float)d.pos[b] * d.inv_freq[k % (d.d / 2)];
+      d.cos[i] = cosf(ang);
+      d.sin[i] = sinf(ang);
+    }
+  for (long long i = tid; i < d.sync_words; i += nth) d.sync[i] = 0u;
+  if (!d.poll) return;
+  // chunks the attention can read: those holding positions 0 .. n (the prior
+  // rows and the new token), n the position clamped like the prior length
+  const int n = min(max(d.pos[0], 0), d.S_max);
+  const int nch = min((n + 1 + d.chunk - 1) / d.chunk, d.n_chunks);
+  const long long po_used = (long long)d.nq * nch * d.D, ml_used = (long long)d.nq * nch * 2;
+  const long long tail = d.layer_words - d.po - d.pml;
+  const long long used = po_used + ml_used + tail;
+  for (long long k = tid; k < used * d.layers; k += nth) {
+    const long long l = k / used, i = k % used;
+    long long off;
+    if (i < po_used) {
+      const long long h = i / ((long long)nch * d.D), r = i % ((long long)nch * d.D);
+      off = h * d.n_chunks * d.D + r;
+    } else if (i < po_used + ml_used) {
+      const long long j = i - po_used, h = j / (2LL * nch), r = j % (2LL * nch);
+      off = d.po + h * d.n_chunks * 2 + r;
+    } else {
+      off = d.po + d.pml + (i - po_used - ml_used);
+    }
+    d.poll[l * d.layer_words + off] = kPollEmpty;
+  }
+}
+
+hipError_t decode_begin_launch(const DecodeBeginArgs& d, hipStream_t s) {
+  long long work = d.cos ? (long long)d.B * d.d : 0;
+  work = max(work, (long long)d.sync_words);
+  if (d.poll) {
+    if (d.B != 1 || d.chunk <= 0 || d.n_chunks <= 0 || d.po != (long long)d.nq * d.n_chunks * d.D ||
+        d.pml != (long long)d.nq * d.n_chunks * 2 || d.layer_words < d.po + d.pml)
+      return hipErrorInvalidValue;
+    work = max(work, d.layer_words * d.layers);
+  }
+  if (work <= 0) return hipSuccess;
+  const long long blocks = min((work + 255) / 256, 1024LL);
+  hipLaunchKernelGGL(decode_begin_kernel, dim3((unsigned)blocks), dim3(256), 0, s, d);
+  return hipGetLastError();
+}
+
 hipError_t embed_launch(const int* ids, const uint16_t* table, uint16_t* out, int B, int H, int V,
                         hipStream_t s) {
   if (H % 8) return hipErrorInvalidValue;

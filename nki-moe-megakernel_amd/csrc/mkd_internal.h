@@ -400,6 +400,26 @@ struct AttnJoinArgs {
 };
 constexpr uint32_t kPollEmpty = 0xffffffffu;   // a NaN no bf16-derived fp32 math produces
 hipError_t fill_u32_launch(uint32_t* p, long long n, uint32_t v, hipStream_t s);
+
+// Start of a decode call, one launch (misc.hip): the RoPE tables (cos non-null),
+// the in-launch sync words cleared (sync non-null), and every layer's
+// data-polled exchange words set to kPollEmpty (poll non-null; one token):
+// of the chunk partials [nq][n_chunks][D] (then [nq][n_chunks][2]) only the
+// chunks up to the token's position -- the ones the call's attention reads --
+// and the rest of each layer's layer_words in full.
+struct DecodeBeginArgs {
+  const int* pos;             // [B] positions
+  const float* inv_freq;      // [d / 2]
+  int B, d;
+  float* cos;                 // [B, d] or null
+  float* sin;
+  unsigned* sync;
+  int sync_words;
+  uint32_t* poll;             // [layers][layer_words] or null
+  long long layer_words, po, pml;
+  int layers, nq, n_chunks, D, chunk, S_max;
+};
+hipError_t decode_begin_launch(const DecodeBeginArgs& d, hipStream_t s);
 // size of y for attn_join_launch: K-split partials of the merge + projection form
 int attn_join_y_parts(int nq);
 int attn_join_flag_words(int B, int nq, int nkv, int n_chunks, int N);

@@ -21,7 +21,9 @@ top-8, I 768), 3 layers chained:
   empty marker, at the start of every call, including inside a captured graph);
 * at one token up to 8192 positions: the merge + projection blocks read a head's
   chunk partials in several batches;
-* no in-launch wait timed out."""
+* no in-launch wait timed out;
+* a call at a short position between two at a long one (the exchange words are
+  reset only up to the position) changes nothing for the later call."""
 import pytest
 import torch
 
@@ -157,3 +159,28 @@ def test_joined_launches_graph_replays(mk, dev):
         assert torch.equal(y.cpu(), y_eager), rep
         assert torch.equal(model.kv_mgr.k(1).cpu(), k_eager[1]), rep
         assert model.layer_kernel_status(1) == (False, False)
+
+
+def test_one_token_positions_long_short_long(mk, dev, restore_path):
+    """The one-token exchange buffers are reset only up to the call's position:
+    a call at a long position, then a short one, then the long one again -- the
+    third call equals the first bit for bit, and the short call matches the
+    separate-launch path (which uses no exchange buffers)."""
+    Q = restore_path
+    cfg, hfs, pos, x, kcs, vcs, model = _setup(dev, 2, 1, 4096, 29)
+    p_long = torch.tensor([3900], dtype=torch.int32)
+    p_short = torch.tensor([100], dtype=torch.int32)
+    print("exchange reset: positions 3900, 100, 3900", flush=True)
+    y1, k1, log1 = _run(model, x, kcs, vcs, p_long, dev)
+    y2, k2, log2 = _run(model, x, kcs, vcs, p_short, dev)
+    y3, k3, _ = _run(model, x, kcs, vcs, p_long, dev)
+    assert torch.equal(y1, y3)
+    assert all(torch.equal(a, b) for a, b in zip(k1, k3))
+    Q.set_decode_path("separate_launches")
+    y2s, _, log2s = _run(model, x, kcs, vcs, p_short, dev)
+    flipped = [l for l in range(2) if not torch.equal(log2[l]["idx"], log2s[l]["idx"])]
+    for l in flipped:
+        check_oracle_flips(log2[l]["idx"], log2[l]["logits"], log2s[l]["logits"], 8)
+    assert 0 not in flipped
+    if not flipped:
+        assert max_abs_rel(y2, y2s) < 1e-2
