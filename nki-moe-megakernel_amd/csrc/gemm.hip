@@ -366,9 +366,6 @@ __global__ void __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4))) m
   }
 }
 
-__global__ void sync_clear_kernel(unsigned* p, int n) {
-  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = 0u;
-}
 
 // ---------------------------------------------------------------------------
 // host side
@@ -472,23 +469,6 @@ hipError_t moe_fused_launch(MoeFusedArgs f, int groups_max, hipStream_t s) {
   return hipErrorInvalidValue;
 }
 
-__global__ void fill_u32_kernel(uint32_t* p, long long n, uint32_t v) {
-  for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
-    p[i] = v;
-}
-
-hipError_t fill_u32_launch(uint32_t* p, long long n, uint32_t v, hipStream_t s) {
-  if (n <= 0) return hipSuccess;
-  const long long blocks = (n + 255) / 256;
-  hipLaunchKernelGGL(fill_u32_kernel, dim3(blocks < 1024 ? (unsigned)blocks : 1024u), dim3(256), 0, s, p, n, v);
-  return hipGetLastError();
-}
-
-hipError_t sync_clear_launch(unsigned* p, int n, hipStream_t s) {
-  if (n <= 0) return hipSuccess;
-  hipLaunchKernelGGL(sync_clear_kernel, dim3((n + 255) / 256 < 64 ? (n + 255) / 256 : 64), dim3(256), 0, s, p, n);
-  return hipGetLastError();
-}
 
 int choose_kw(int K, int max_kw, long long blocks) {
   // Per-wave K slice (a multiple of 32 dividing K into <= 16 waves, <= max_kw).

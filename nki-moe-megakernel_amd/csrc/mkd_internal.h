@@ -399,7 +399,6 @@ struct AttnJoinArgs {
   int dpoll;                  // set by attn_join_launch
 };
 constexpr uint32_t kPollEmpty = 0xffffffffu;   // a NaN no bf16-derived fp32 math produces
-hipError_t fill_u32_launch(uint32_t* p, long long n, uint32_t v, hipStream_t s);
 
 // Start of a decode call, one launch (misc.hip): the RoPE tables (cos non-null),
 // the in-launch sync words cleared (sync non-null), and every layer's
@@ -506,7 +505,6 @@ struct MoeFusedArgs {
 bool moe_fused_supported(int T, int K, int E, int H, int I);
 int moe_fused_flag_words(int T, int K, int E, int I);
 hipError_t moe_fused_launch(MoeFusedArgs f, int groups_max, hipStream_t s);
-hipError_t sync_clear_launch(unsigned* p, int n, hipStream_t s);
 bool gemm_sel_supported(int T, int K, int E, int nsplit);
 hipError_t gemm_sel_launch(const GemmArgs& a, const RouterArgs& r, int groups_max, hipStream_t s);
 hipError_t moe_route_launch(const int* idx, int T, int K, int E, int* n_groups, int* grp_expert,
