@@ -146,7 +146,10 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   constexpr bool PRE = TPW <= 2;
   const bool flat = ONE || a.block_table == nullptr;
   int n = a.S_max;                            // row bound until the prior length is read
-  const int dq = (lane >> 4) * (D / 4);       // lane's d range in a 16-row tile
+  // lane l's k elements of QK step kk: d = 32 kk + 8 (l / 16) .. + 8 -- the four
+  // lanes of a row read 64 consecutive bytes per step (half a cache line),
+  // not four 16-byte pieces 64 bytes apart
+  const int dq = (lane >> 4) * 8;
   const int wbase = chunk0 + w * TPW * 16;
   const int vc = (lane & 15) * (D / 16);      // lane's V row segment (d labels)
   // Row pointers first, then the loads: with a block table every pointer is
@@ -181,7 +184,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   };
   auto k_load = [&](const uint16_t* kr, u32x4_t (&dst)[NK]) {
 #pragma unroll
-    for (int kk = 0; kk < NK; ++kk) dst[kk] = kr ? ld16(kr + dq + kk * 8) : u32x4_t{0, 0, 0, 0};
+    for (int kk = 0; kk < NK; ++kk) dst[kk] = kr ? ld16(kr + dq + kk * 32) : u32x4_t{0, 0, 0, 0};
   };
   u32x4_t kpre[PRE ? TPW : 1][NK];
   uint32_t vpre[PRE ? TPW : 1][4][VW];
@@ -196,7 +199,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
       for (int tt = 0; tt < TPW; ++tt) {
         const int tk = min(wbase + tt * 16 + (lane & 15), a.S_max - 1);
 #pragma unroll
-        for (int kk = 0; kk < NK; ++kk) kpre[tt][kk] = ld16(kc + (long long)tk * D + dq + kk * 8);
+        for (int kk = 0; kk < NK; ++kk) kpre[tt][kk] = ld16(kc + (long long)tk * D + dq + kk * 32);
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const int tv = min(wbase + tt * 16 + (lane >> 4) * 4 + jj, a.S_max - 1);
@@ -289,7 +292,7 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
   u32x4_t qf[NK];
 #pragma unroll
   for (int kk = 0; kk < NK; ++kk)
-    qf[kk] = hcol < GQA ? *reinterpret_cast<const u32x4_t*>(&q_s[hcol][dq + kk * 8])
+    qf[kk] = hcol < GQA ? *reinterpret_cast<const u32x4_t*>(&q_s[hcol][dq + kk * 32])
                         : u32x4_t{0, 0, 0, 0};
 
   // ---- 2. scores for the wave's tiles (without the up-front copies: the K
@@ -317,9 +320,9 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
       if constexpr (PRE) kf = kpre[tt][kk];
       else kf = kl[tt % LB][kk];
       if (NT == 1) {
-        if (t == n) kf = *reinterpret_cast<const u32x4_t*>(&kn_s[dq + kk * 8]);
+        if (t == n) kf = *reinterpret_cast<const u32x4_t*>(&kn_s[dq + kk * 32]);
       } else if (t >= n && t < total) {
-        kf = ld16(act0 + (t - n) * act_stride + GQA * D + dq + kk * 8);
+        kf = ld16(act0 + (t - n) * act_stride + GQA * D + dq + kk * 32);
       }
       acc = mfma16x16x32(kf, qf[kk], acc);
     }
