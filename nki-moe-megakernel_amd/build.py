@@ -18,7 +18,7 @@ BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libmkd.so")
 SOURCES = ["capi.hip", "gemm.hip", "norm.hip", "attn_mfma.hip", "moe.hip",
            "misc.hip", "mx.hip", "gemm_tile.hip", "layer_mk.hip", "qkv_norm.hip", "gemm_mid.hip",
-           "attn_kvfmt.hip", "gemm_w8.hip"]
+           "attn_kvfmt.hip", "gemm_w8.hip", "attn_prefill.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 

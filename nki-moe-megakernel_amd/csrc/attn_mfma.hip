@@ -1556,6 +1556,31 @@ hipError_t attn_prep_launch(const AttnArgs& a, int rope_mode, hipStream_t s) {
   return hipGetLastError();
 }
 
+template <int D, int GQA>
+static hipError_t launch_prep_write(const AttnArgs& a, int rope_mode, hipStream_t s) {
+  hipLaunchKernelGGL((attn_prep_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode);
+  if (hipError_t e = hipGetLastError()) return e;
+  hipLaunchKernelGGL((attn_kv_write_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(D), 0, s, a);
+  return hipGetLastError();
+}
+
+hipError_t attn_prep_write_launch(const AttnArgs& a, int rope_mode, hipStream_t s) {
+  if (!a.prep || !a.prefill || !a.update_cache) return hipErrorInvalidValue;
+  const int gqa = a.nq / a.nkv;
+#define MKD_PW(D_)                                              \
+  switch (gqa) {                                                \
+    case 1: return launch_prep_write<D_, 1>(a, rope_mode, s);   \
+    case 2: return launch_prep_write<D_, 2>(a, rope_mode, s);   \
+    case 4: return launch_prep_write<D_, 4>(a, rope_mode, s);   \
+    case 8: return launch_prep_write<D_, 8>(a, rope_mode, s);   \
+    case 16: return launch_prep_write<D_, 16>(a, rope_mode, s); \
+  }
+  if (a.d == 128) { MKD_PW(128) }
+  else if (a.d == 64) { MKD_PW(64) }
+#undef MKD_PW
+  return hipErrorInvalidValue;
+}
+
 hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s) {
   const int gqa = a.nq / a.nkv;
   if (a.d == 128) {

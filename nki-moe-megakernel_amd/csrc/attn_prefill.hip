@@ -1,0 +1,211 @@
+// Prefill attention: the T new tokens of one sequence (a context-encoding pass,
+// attention_block_tkg's semantics per token: token b attends the cache rows
+// 0 .. n_prior[b] - 1 and then itself, attention_block_tkg.py:1473-1685 with
+// the new token's own k / v from its prepared heads) read each K / V row once
+// per 16-token query tile, instead of once per token as the split-K decode
+// kernel does.
+//
+// Block (query tile, kv group g, head slice): 16 consecutive tokens x up to 8
+// of the group's GQA query heads, one wave per head.  Per 32-position tile of the cache a wave forms
+// S^T = K Q^T (v_mfma_f32_16x16x32_bf16: A = 16 cache rows, B = the 16 tokens'
+// q; lane l holds positions 4(l/16) + i of token l % 16), the online softmax
+// per token (running max and sum, the token's own row first), then O += P V
+// with the two 16-position halves paired on the 32-deep MFMA (A = P, rows the
+// tokens; B = V, column l % 16 <-> d = 8 (l % 16) + dt).  The next tile's rows
+// are loaded while the current one is computed.  Rounding follows the decode
+// kernel: Qwen scores bf16(bf16(q.k) * scale), P rounded to bf16 for the MFMA,
+// sums in fp32.  An optional sink logit joins the normaliser at the end.
+#include "common.h"
+#include "mkd_internal.h"
+#include "attn_common.h"
+
+namespace mkd {
+
+constexpr int kPfTok = 16;    // query tokens per block (the MFMA's 16 columns)
+constexpr int kPfTile = 32;   // cache positions per step (two 16-row halves)
+
+template <int GQA, int HPB = (GQA < 8 ? GQA : 8)>
+__global__ void __launch_bounds__(64 * HPB) attn_prefill_kernel(AttnArgs a) {
+  constexpr int D = 128, NK = D / 32, NDT = D / 16;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int tl = lane & 15, q4 = lane >> 4;
+  const int nqt = (a.B + kPfTok - 1) / kPfTok;
+  const int t0 = (nqt - 1 - (int)blockIdx.x) * kPfTok;   // the longest tiles first
+  const int g = blockIdx.y, hg = blockIdx.z * HPB + w, h = g * GQA + hg;   // head in group / overall
+  const int tok = t0 + tl;
+  const bool live = tok < a.B;
+  const int tokc = live ? tok : a.B - 1;                 // in-range address for absent tokens
+  const long long hstride = (long long)(GQA + 2) * D;
+  const uint16_t* prep_t = a.prep + ((long long)tokc * a.nkv + g) * hstride;
+
+  // ---- the token's q (B operand, natural k order: d = 32 kk + 8 q4 .. + 8)
+  // and its own row's score ----
+  u32x4_t qf[NK], kown[NK];
+#pragma unroll
+  for (int kk = 0; kk < NK; ++kk) {
+    qf[kk] = live ? ld16(prep_t + hg * D + 32 * kk + 8 * q4) : u32x4_t{0u, 0u, 0u, 0u};
+    kown[kk] = ld16(prep_t + GQA * D + 32 * kk + 8 * q4);
+  }
+  const int n_b = live ? prior_len(a, tok) : 0;
+  int nmax = n_b;
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
+  nmax = __builtin_amdgcn_readfirstlane(nmax);
+  float dot = 0.f;
+#pragma unroll
+  for (int kk = 0; kk < NK; ++kk)
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      dot += bf_lo(qf[kk][e]) * bf_lo(kown[kk][e]) + bf_hi(qf[kk][e]) * bf_hi(kown[kk][e]);
+  dot += __shfl_xor(dot, 16, 64);
+  dot += __shfl_xor(dot, 32, 64);
+  const float sdiag = a.round_qwen ? rbf(rbf(dot) * a.scale) : dot * a.scale;
+
+  // ---- O starts as the own row's v (weight exp(0) = 1): rows are the tokens
+  // 4 q4 + i, column tl of d-tile dt is d = 8 tl + dt ----
+  f32x4_t o[NDT];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int ti = min(t0 + 4 * q4 + i, a.B - 1);
+    const u32x4_t v = ld16(a.prep + ((long long)ti * a.nkv + g) * hstride + (GQA + 1) * D + 8 * tl);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[2 * e][i] = bf_lo(v[e]);
+      o[2 * e + 1][i] = bf_hi(v[e]);
+    }
+  }
+  float m_run = sdiag, l_run = 1.f;
+
+  // ---- the cache rows, 32 positions per step ----
+  auto load_tile = [&](int p0, u32x4_t (&kf)[2][NK], u32x4_t (&vl)[2][4]) {
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const uint16_t* kr = kv_row<D>(a, a.k_cache, 0, g, min(p0 + 16 * s + tl, nmax - 1));
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) kf[s][kk] = kr ? ld16(kr + 32 * kk + 8 * q4) : u32x4_t{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint16_t* vr = kv_row<D>(a, a.v_cache, 0, g, min(p0 + 16 * s + 4 * q4 + j, nmax - 1));
+        vl[s][j] = vr ? ld16(vr + 8 * tl) : u32x4_t{0u, 0u, 0u, 0u};
+      }
+    }
+  };
+  auto compute_tile = [&](int p0, const u32x4_t (&kf)[2][NK], const u32x4_t (&vl)[2][4]) {
+    float sc[2][4];
+    float mt = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int kk = 0; kk < NK; ++kk) acc = mfma16x16x32(kf[s][kk], qf[kk], acc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int pos = p0 + 16 * s + 4 * q4 + i;
+        const float v = a.round_qwen ? rbf(rbf(acc[i]) * a.scale) : acc[i] * a.scale;
+        sc[s][i] = pos < n_b ? v : -INFINITY;
+        mt = fmaxf(mt, sc[s][i]);
+      }
+    }
+    mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+    mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+    const float m_new = fmaxf(m_run, mt);
+    const float alpha = expf(m_run - m_new);
+    float ls = 0.f;
+    uint2 pa[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        p[i] = sc[s][i] == -INFINITY ? 0.f : expf(sc[s][i] - m_new);
+        ls += p[i];
+      }
+      pa[s] = uint2{pack2bf(p[0], p[1]), pack2bf(p[2], p[3])};
+    }
+    ls += __shfl_xor(ls, 16, 64);
+    ls += __shfl_xor(ls, 32, 64);
+    l_run = l_run * alpha + ls;
+    m_run = m_new;
+    // O rows are tokens 4 q4 + i: their factors from the lanes holding them
+    float al[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * q4 + i, 64);
+    const u32x4_t pp = {pa[0].x, pa[0].y, pa[1].x, pa[1].y};
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const int e = dt >> 1;
+      uint2 bo[2];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        bo[s] = (dt & 1) ? uint2{(vl[s][0][e] >> 16) | (vl[s][1][e] & 0xffff0000u),
+                                 (vl[s][2][e] >> 16) | (vl[s][3][e] & 0xffff0000u)}
+                         : uint2{(vl[s][0][e] & 0xffffu) | (vl[s][1][e] << 16),
+                                 (vl[s][2][e] & 0xffffu) | (vl[s][3][e] << 16)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[dt][i] *= al[i];
+      o[dt] = mfma16x16x32(pp, u32x4_t{bo[0].x, bo[0].y, bo[1].x, bo[1].y}, o[dt]);
+    }
+  };
+  if (nmax > 0) {
+    u32x4_t kA[2][NK], vA[2][4], kB[2][NK], vB[2][4];
+    load_tile(0, kA, vA);
+    for (int p0 = 0; p0 < nmax; p0 += 2 * kPfTile) {
+      // the next tile's rows go out before this one's math (clamped addresses:
+      // past the last tile they re-read the last row and are never used)
+      load_tile(min(p0 + kPfTile, nmax - 1), kB, vB);
+      compute_tile(p0, kA, vA);
+      if (p0 + kPfTile >= nmax) break;
+      load_tile(min(p0 + 2 * kPfTile, nmax - 1), kA, vA);
+      compute_tile(p0 + kPfTile, kB, vB);
+    }
+  }
+  // ---- sink logit, normalisation, bf16 rows ----
+  if (a.sink) {
+    const float sk = a.sink[h];
+    const float m2 = fmaxf(m_run, sk);
+    const float r = expf(m_run - m2);
+    l_run = l_run * r + expf(sk - m2);
+    float rr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rr[i] = __shfl(r, 4 * q4 + i, 64);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[dt][i] *= rr[i];
+  }
+  const float inv = 1.f / l_run;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float f = __shfl(inv, 4 * q4 + i, 64);
+    const int ti = t0 + 4 * q4 + i;
+    if (ti >= a.B) continue;
+    u32x4_t out;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) out[e] = pack2bf(o[2 * e][i] * f, o[2 * e + 1][i] * f);
+    st16(a.attn_out + ((long long)ti * a.nq + h) * D + 8 * tl, out);
+  }
+}
+
+bool attn_prefill_ok(const AttnArgs& a) {
+  const int gqa = a.nkv > 0 ? a.nq / a.nkv : 0;
+  return a.prefill && a.prep && a.d == 128 && gqa * a.nkv == a.nq &&
+         (gqa == 1 || gqa == 2 || gqa == 4 || gqa == 8 || gqa == 16) && !a.mask && a.window == 0 &&
+         a.s_tkg <= 1 && !a.kv_fp8 && !a.k_transposed && a.B >= 1 && a.update_cache;
+}
+
+hipError_t attn_prefill_launch(const AttnArgs& a, int rope_mode, hipStream_t s) {
+  if (!attn_prefill_ok(a)) return hipErrorInvalidValue;
+  if (hipError_t e = attn_prep_write_launch(a, rope_mode, s)) return e;
+  const int gqa = a.nq / a.nkv, hpb = gqa < 8 ? gqa : 8;
+  const dim3 grid((a.B + kPfTok - 1) / kPfTok, a.nkv, gqa / hpb);
+  switch (gqa) {
+    case 1: return timed_launch(attn_prefill_kernel<1>, grid, dim3(64), 0, s, a);
+    case 2: return timed_launch(attn_prefill_kernel<2>, grid, dim3(128), 0, s, a);
+    case 4: return timed_launch(attn_prefill_kernel<4>, grid, dim3(256), 0, s, a);
+    case 8: return timed_launch(attn_prefill_kernel<8>, grid, dim3(512), 0, s, a);
+    case 16: return timed_launch(attn_prefill_kernel<16>, grid, dim3(512), 0, s, a);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace mkd

@@ -960,6 +960,11 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
     ac.update_cache = 0;               // the new rows are stored below, in the cache's format
     MKD_TRY(attn_combine_launch(ac, s), "attention combine");
     MKD_TRY(attn_kvfmt_store_launch(a, s), "kv store (fp8 / transposed-K cache)");
+  } else if (prefill && attn_prefill_ok(a)) {
+    // a context-encoding pass: query tiles read each cache row once per 16 tokens
+    const int ps = prof_begin(MKD_KCLASS_ATTN, s);
+    MKD_TRY(attn_prefill_launch(a, rope_mode, s), "prefill attention");
+    prof_end(ps, s);
   } else {
     {  // q/k norm + RoPE and split-K attention in one launch
       const int ps = prof_begin(MKD_KCLASS_ATTN, s);

@@ -302,6 +302,13 @@ struct AttnArgs {
 };
 // rope_mode: 0 none, 1 cos/sin tables, 2 from pos and inv_freq
 hipError_t attn_decode_launch(const AttnArgs& a, int rope_mode, hipStream_t s);
+// Prefill only: the prepared heads of every token (a.prep) and their k / v
+// rows written to the cache -- the first two launches of a prefill pass.
+hipError_t attn_prep_write_launch(const AttnArgs& a, int rope_mode, hipStream_t s);
+// Prefill attention by query tiles (attn_prefill.hip): the prep / write
+// launches, then one kernel writing a.attn_out; no split-K partials.
+bool attn_prefill_ok(const AttnArgs& a);
+hipError_t attn_prefill_launch(const AttnArgs& a, int rope_mode, hipStream_t s);
 hipError_t attn_combine_launch(const AttnArgs& a, hipStream_t s);
 int attn_chunk_for(int B, int nkv, int S_max);   // positions per attention block (64/128/256)
 // q / k / v head preparation of every (row, kv head) into a.prep (required)

@@ -69,19 +69,20 @@ def test_qwen3_prefill_matches_token_by_token_decode(mk, dev, chunk):
         assert not ka[0].any() and not va[0].any()                   # other sequence untouched
 
 
-@pytest.mark.parametrize("T", [37, 300])
+@pytest.mark.parametrize("T", [37, 300, 1100])
 def test_qwen3_prefill_matches_oracle_chain(mk, dev, T):
-    """One T-token pass (300: the > 128-token path -- router top-k on 16 tokens per
-    block, groups from the indices, LDS-tiled MFMA projections and experts)
-    against the oracle decoding the prompt token by token: every K/V row of both
-    layers and the last token's logits within 2e-2; each layer's routing exact
-    on the GPU's own logits and equal to the oracle router on the GPU's residual
-    except near-ties < 1e-4."""
+    """One T-token pass (300, 1100: the > 128-token path -- router top-k on 16
+    tokens per block, groups from the indices, LDS-tiled MFMA projections and
+    experts; every pass: the query-tiled prefill attention, 1100 tokens = 69
+    query tiles over up to 1100 cache rows) against the oracle decoding the
+    prompt token by token: every K/V row of both layers and the last token's
+    logits within 2e-2; each layer's routing exact on the GPU's own logits and
+    equal to the oracle router on the GPU's residual except near-ties < 1e-4."""
     from nki_moe_megakernel_amd import qwen_with_megakernel as Q
     print(f"qwen3 prefill T={T} vs the oracle chain", flush=True)
     g = torch.Generator().manual_seed(40 + T)
     ids = torch.randint(0, 1024, (T,), generator=g, dtype=torch.int32)
-    m = _qwen(dev, 1, max_seq=512)
+    m = _qwen(dev, 1, max_seq=max(512, (T + 16 + 127) // 128 * 128))
     m.enable_route_log(T)
     lo, _ = m.prefill(ids.to(dev), start_pos=0, seq=0, chunk=T)
     torch.cuda.synchronize()
@@ -156,19 +157,28 @@ def test_qwen3_long_prefill_pass_matches_short_passes(mk, dev, T, short, fmt):
         lm = (0.02 * torch.randn(1024, cfg.hidden_size, generator=gg)).to(torch.bfloat16).to(dev)
         m = Q.Qwen3MoeMegakernelModel(cfg, packed, 1, dev, embed=embed, ln_f=ln_f, lm_head=lm)
         m.enable_route_log(T)
-        idx0, lg0 = [], []
+        idx0, lg0, last1 = [], [], None
         for c0 in range(0, T, chunk):
             n = min(chunk, T - c0)
             lo, _ = m.prefill(ids[c0:c0 + n], start_pos=c0, seq=0, chunk=n)
-            rec = m.route_log(n)[0]
-            idx0.append(rec["idx"])
-            lg0.append(rec["logits"])
+            logs = m.route_log(n)
+            idx0.append(logs[0]["idx"])
+            lg0.append(logs[0]["logits"])
+            last1 = (logs[1]["idx"][-1], logs[1]["logits"][-1])   # the last token's layer-1 routing
         torch.cuda.synchronize()
         outs.append((lo.cpu(), [m.kv_mgr.k(l).cpu() for l in range(2)], [m.kv_mgr.v(l).cpu() for l in range(2)],
-                     torch.cat(idx0), torch.cat(lg0)))
-    (la, ka, va, ia, ga), (lb, kb, vb, ib, gb) = outs
+                     torch.cat(idx0), torch.cat(lg0), last1))
+    (la, ka, va, ia, ga, l1a), (lb, kb, vb, ib, gb, l1b) = outs
     assert torch.isfinite(la).all()
-    assert max_abs_rel(la, lb) < TOL
+    # the last token's logits: compared unless its layer-1 top-k differs between
+    # the runs, which must then be a near-tie of their logits
+    flip1 = set(l1a[0].tolist()) != set(l1b[0].tolist())
+    print(f"  last-token logits, one pass vs passes of {short}: {max_abs_rel(la, lb):.2e}"
+          f" (its layer-1 routing {'differs' if flip1 else 'agrees'})", flush=True)
+    if flip1:
+        check_oracle_flips(l1a[0][None], l1a[1][None], l1b[1][None], 8)
+    else:
+        assert max_abs_rel(la, lb) < TOL
     # tokens whose layer-0 routing differs between the runs: near-ties only
     dl = (ga - gb).abs().max().item()
     order = torch.sort(-gb, dim=-1, stable=True).indices
