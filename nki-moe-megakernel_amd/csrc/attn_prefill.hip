@@ -6,27 +6,38 @@
 // kernel does.
 //
 // Block (query tile, kv group g, head slice): 16 consecutive tokens x up to 8
-// of the group's GQA query heads, one wave per head.  Per 32-position tile of the cache a wave forms
+// of the group's GQA query heads, one wave per head.  Per 64-position step of the cache a wave forms
 // S^T = K Q^T (v_mfma_f32_16x16x32_bf16: A = 16 cache rows, B = the 16 tokens'
 // q; lane l holds positions 4(l/16) + i of token l % 16), the online softmax
 // per token (running max and sum, the token's own row first), then O += P V
-// with the two 16-position halves paired on the 32-deep MFMA (A = P, rows the
-// tokens; B = V, column l % 16 <-> d = 8 (l % 16) + dt).  The next tile's rows
-// are loaded while the current one is computed.  Rounding follows the decode
-// kernel: Qwen scores bf16(bf16(q.k) * scale), P rounded to bf16 for the MFMA,
-// sums in fp32.  An optional sink logit joins the normaliser at the end.
+// with 16-position quarters paired on the 32-deep MFMA (A = P, rows the
+// tokens; B = V, column l % 16 <-> d = 8 (l % 16) + dt).  The block stages each
+// 64-position step of K and V in LDS (double-buffered: the next step's rows are
+// loaded while the current one is computed), so a row is read from memory once
+// per block rather than once per head.  Rounding follows the decode kernel:
+// Qwen scores bf16(bf16(q.k) * scale), P rounded to bf16 for the MFMA, sums in
+// fp32; the exponentials use the hardware exp2 (__expf: 184 -> 148 us per
+// layer at 2048 tokens).  An optional sink logit joins the normaliser at the
+// end.  Four waves per SIMD (two 8-wave blocks per CU, <= 128 VGPRs).
 #include "common.h"
 #include "mkd_internal.h"
 #include "attn_common.h"
+#include "coherent.h"
 
 namespace mkd {
 
 constexpr int kPfTok = 16;    // query tokens per block (the MFMA's 16 columns)
-constexpr int kPfTile = 32;   // cache positions per step (two 16-row halves)
+constexpr int kPfStep = 64;   // cache positions per step (four 16-row quarters)
+constexpr int kPfLd = 136;    // LDS row stride in bf16 (256 B + 16 B: rows land on different banks)
 
 template <int GQA, int HPB = (GQA < 8 ? GQA : 8)>
-__global__ void __launch_bounds__(64 * HPB) attn_prefill_kernel(AttnArgs a) {
-  constexpr int D = 128, NK = D / 32, NDT = D / 16;
+__global__ void __launch_bounds__(64 * HPB) __attribute__((amdgpu_waves_per_eu(HPB >= 8 ? 4 : 1)))
+attn_prefill_kernel(AttnArgs a) {
+  constexpr int D = 128, NK = D / 32, NDT = D / 16, NT = 64 * HPB;
+  constexpr int CH = kPfStep * D / 8;                 // 16-byte chunks of one K (or V) step
+  constexpr int CPT = (CH + NT - 1) / NT;             // of them per thread
+  __shared__ __attribute__((aligned(16))) uint16_t k_s[2][kPfStep * kPfLd];
+  __shared__ __attribute__((aligned(16))) uint16_t v_s[2][kPfStep * kPfLd];
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int tl = lane & 15, q4 = lane >> 4;
   const int nqt = (a.B + kPfTok - 1) / kPfTok;
@@ -47,6 +58,8 @@ __global__ void __launch_bounds__(64 * HPB) attn_prefill_kernel(AttnArgs a) {
     kown[kk] = ld16(prep_t + GQA * D + 32 * kk + 8 * q4);
   }
   const int n_b = live ? prior_len(a, tok) : 0;
+  // the tile's largest prior length (every wave forms it: the step loop and
+  // its barriers are the same in all of them)
   int nmax = n_b;
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1) nmax = max(nmax, __shfl_xor(nmax, o, 64));
@@ -76,28 +89,42 @@ __global__ void __launch_bounds__(64 * HPB) attn_prefill_kernel(AttnArgs a) {
   }
   float m_run = sdiag, l_run = 1.f;
 
-  // ---- the cache rows, 32 positions per step ----
-  auto load_tile = [&](int p0, u32x4_t (&kf)[2][NK], u32x4_t (&vl)[2][4]) {
+  // ---- the cache rows, kPfStep positions per step, staged in LDS by the
+  // whole block (each row read from memory once per block), the next step's
+  // rows loaded while the current step is computed ----
+  u32x4_t kreg[CPT], vreg[CPT];
+  auto load_step = [&](int p0) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const uint16_t* kr = kv_row<D>(a, a.k_cache, 0, g, min(p0 + 16 * s + tl, nmax - 1));
+    for (int c = 0; c < CPT; ++c) {
+      const int ch = threadIdx.x + c * NT;
+      const int row = min(p0 + ch / 16, nmax - 1);     // clamped: rows past the tile re-read the last
+      const uint16_t* kr = kv_row<D>(a, a.k_cache, 0, g, row);
+      const uint16_t* vr = kv_row<D>(a, a.v_cache, 0, g, row);
+      kreg[c] = (ch < CH && kr) ? ld16(kr + (ch % 16) * 8) : u32x4_t{0u, 0u, 0u, 0u};
+      vreg[c] = (ch < CH && vr) ? ld16(vr + (ch % 16) * 8) : u32x4_t{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_step = [&](int buf) {
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk) kf[s][kk] = kr ? ld16(kr + 32 * kk + 8 * q4) : u32x4_t{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint16_t* vr = kv_row<D>(a, a.v_cache, 0, g, min(p0 + 16 * s + 4 * q4 + j, nmax - 1));
-        vl[s][j] = vr ? ld16(vr + 8 * tl) : u32x4_t{0u, 0u, 0u, 0u};
+    for (int c = 0; c < CPT; ++c) {
+      const int ch = threadIdx.x + c * NT;
+      if (ch < CH) {
+        st16(&k_s[buf][(ch / 16) * kPfLd + (ch % 16) * 8], kreg[c]);
+        st16(&v_s[buf][(ch / 16) * kPfLd + (ch % 16) * 8], vreg[c]);
       }
     }
   };
-  auto compute_tile = [&](int p0, const u32x4_t (&kf)[2][NK], const u32x4_t (&vl)[2][4]) {
-    float sc[2][4];
+  auto compute_step = [&](int p0, int buf) {
+    const uint16_t* ks = k_s[buf];
+    const uint16_t* vs = v_s[buf];
+    float sc[4][4];
     float mt = -INFINITY;
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int s = 0; s < 4; ++s) {
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int kk = 0; kk < NK; ++kk) acc = mfma16x16x32(kf[s][kk], qf[kk], acc);
+      for (int kk = 0; kk < NK; ++kk)
+        acc = mfma16x16x32(ld16(ks + (16 * s + tl) * kPfLd + 32 * kk + 8 * q4), qf[kk], acc);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int pos = p0 + 16 * s + 4 * q4 + i;
@@ -109,15 +136,15 @@ __global__ void __launch_bounds__(64 * HPB) attn_prefill_kernel(AttnArgs a) {
     mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
     mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
     const float m_new = fmaxf(m_run, mt);
-    const float alpha = expf(m_run - m_new);
+    const float alpha = __expf(m_run - m_new);
     float ls = 0.f;
-    uint2 pa[2];
+    uint2 pa[4];
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
+    for (int s = 0; s < 4; ++s) {
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        p[i] = sc[s][i] == -INFINITY ? 0.f : expf(sc[s][i] - m_new);
+        p[i] = sc[s][i] == -INFINITY ? 0.f : __expf(sc[s][i] - m_new);
         ls += p[i];
       }
       pa[s] = uint2{pack2bf(p[0], p[1]), pack2bf(p[2], p[3])};
@@ -130,33 +157,47 @@ __global__ void __launch_bounds__(64 * HPB) attn_prefill_kernel(AttnArgs a) {
     float al[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) al[i] = __shfl(alpha, 4 * q4 + i, 64);
-    const u32x4_t pp = {pa[0].x, pa[0].y, pa[1].x, pa[1].y};
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const int e = dt >> 1;
-      uint2 bo[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-        bo[s] = (dt & 1) ? uint2{(vl[s][0][e] >> 16) | (vl[s][1][e] & 0xffff0000u),
-                                 (vl[s][2][e] >> 16) | (vl[s][3][e] & 0xffff0000u)}
-                         : uint2{(vl[s][0][e] & 0xffffu) | (vl[s][1][e] << 16),
-                                 (vl[s][2][e] & 0xffffu) | (vl[s][3][e] << 16)};
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[dt][i] *= al[i];
-      o[dt] = mfma16x16x32(pp, u32x4_t{bo[0].x, bo[0].y, bo[1].x, bo[1].y}, o[dt]);
+    // P.V, the quarters in pairs on the 32-deep MFMA: lane group q4's k slots
+    // are positions 4 q4 .. 4 q4 + 3 of the even quarter, then of the odd one,
+    // in the P operand and in the V operand alike
+#pragma unroll
+    for (int sp = 0; sp < 2; ++sp) {
+      u32x4_t vq[2][4];
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) vq[s][j] = ld16(vs + (16 * (2 * sp + s) + 4 * q4 + j) * kPfLd + 8 * tl);
+      const u32x4_t pp = {pa[2 * sp].x, pa[2 * sp].y, pa[2 * sp + 1].x, pa[2 * sp + 1].y};
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int e = dt >> 1;
+        uint2 bo[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s)
+          bo[s] = (dt & 1) ? uint2{(vq[s][0][e] >> 16) | (vq[s][1][e] & 0xffff0000u),
+                                   (vq[s][2][e] >> 16) | (vq[s][3][e] & 0xffff0000u)}
+                           : uint2{(vq[s][0][e] & 0xffffu) | (vq[s][1][e] << 16),
+                                   (vq[s][2][e] & 0xffffu) | (vq[s][3][e] << 16)};
+        o[dt] = mfma16x16x32(pp, u32x4_t{bo[0].x, bo[0].y, bo[1].x, bo[1].y}, o[dt]);
+      }
     }
   };
   if (nmax > 0) {
-    u32x4_t kA[2][NK], vA[2][4], kB[2][NK], vB[2][4];
-    load_tile(0, kA, vA);
-    for (int p0 = 0; p0 < nmax; p0 += 2 * kPfTile) {
-      // the next tile's rows go out before this one's math (clamped addresses:
-      // past the last tile they re-read the last row and are never used)
-      load_tile(min(p0 + kPfTile, nmax - 1), kB, vB);
-      compute_tile(p0, kA, vA);
-      if (p0 + kPfTile >= nmax) break;
-      load_tile(min(p0 + 2 * kPfTile, nmax - 1), kA, vA);
-      compute_tile(p0 + kPfTile, kB, vB);
+    load_step(0);
+    store_step(0);
+    lds_barrier();
+    int buf = 0;
+    for (int p0 = 0; p0 < nmax; p0 += kPfStep) {
+      const bool more = p0 + kPfStep < nmax;        // block-uniform
+      if (more) load_step(p0 + kPfStep);
+      compute_step(p0, buf);
+      if (more) store_step(buf ^ 1);
+      lds_barrier();                                 // the next buffer written, this one read
+      buf ^= 1;
     }
   }
   // ---- sink logit, normalisation, bf16 rows ----
