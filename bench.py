@@ -568,8 +568,11 @@ def bench_context_prefill(args):
     --prefill-chunk tokens through all 48 layers), each step re-encoding the same prompt into
     cache rows 0..T-1.  Algorithmic HBM bytes per pass: the attention / router
     weights once, each expert's weights once if any token of the pass routes to
-    it (counted from the routing of a seeded uniform draw), and the K/V prefix each
-    token attends; reported against HBM peak for the whole pass (several kernels)."""
+    it (expected distinct experts under uniform routing), and the K/V rows each
+    16-token query tile of the prefill attention reads (every row up to the
+    tile's last position, once per tile); reported against HBM peak for the whole
+    pass (several kernels), with the pass's FLOPs against the bf16 MFMA peak
+    beside it (config.mfma_TFLOPs / mfma_frac)."""
     import torch
     import __graft_entry__ as ge
     ge.load_package()
@@ -602,18 +605,26 @@ def bench_context_prefill(args):
     expert_b = 2 * 3 * I * H
     passes = [(c0, min(CH, T - c0)) for c0 in range(0, T, CH)]
     alg = 0.0
+    flops = 0.0
     for c0, nt in passes:
         distinct = E * (1 - (1 - K / E) ** nt)
-        kv = sum(2 * nkv * (c0 + t + 1) * d * 2 for t in range(nt))
+        kv = sum(2 * nkv * min(c0 + 16 * (q + 1), c0 + nt) * d * 2 for q in range((nt + 15) // 16))
         alg += cfg.num_hidden_layers * (dense_b + distinct * expert_b + kv)
+        # dense projections + router, the experts' three matrices, and QK / PV
+        # over each token's prefix (itself included)
+        attn_f = sum(4 * nq * d * (c0 + t + 1) for t in range(nt))
+        flops += cfg.num_hidden_layers * (nt * (dense_b + K * expert_b) + attn_f)
     gbs = alg / (ms * 1e-3) / 1e9
+    tflops = flops / (ms * 1e-3) / 1e12
     line = {
         "metric": "context-encoding throughput (prefill of one sequence)", "value": round(T / (ms * 1e-3), 1),
         "unit": "tokens/s", "n_gpus": 1, "steps": n, "warmup": args.warmup, "ms_per_step": round(ms, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded random bf16 weights, random prompt ids)",
         "config": {"workload": f"Qwen3-30B-A3B shape, {cfg.num_hidden_layers} layers, {T}-token prompt "
-                               f"in {len(passes)} passes of <= {CH} tokens", "tokens": T, "chunk": CH},
+                               f"in {len(passes)} passes of <= {CH} tokens", "tokens": T, "chunk": CH,
+                   "flops_per_step": round(flops), "mfma_TFLOPs": round(tflops, 1),
+                   "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4)},
         "roofline": {"bound": "hbm", "kernel": "whole prefill pass (all kernels)",
                      "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
