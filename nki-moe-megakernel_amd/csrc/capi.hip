@@ -302,7 +302,8 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
              const void* gu_scales = nullptr, const void* dn_scales = nullptr, bool tiled = false,
              const RouterArgs* sel = nullptr, unsigned* fused_flags = nullptr,
              unsigned* fused_err = nullptr, uint16_t* poll_h = nullptr,
-             const uint16_t* hn_r = nullptr, const uint16_t* hn_gamma = nullptr) {
+             const uint16_t* hn_r = nullptr, const uint16_t* hn_gamma = nullptr,
+             bool x_mx_ready = false) {
   if (sel && (idx || wfmt || tiled)) return MKD_ERR_INVALID;
   if (fused_flags && !sel) return MKD_ERR_INVALID;
   if (idx)  // otherwise the router stage already built the expert groups
@@ -350,7 +351,8 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
     // MX experts: hidden -> MXFP8, gate/up (scaled MFMA) + SwiGLU -> bf16 h,
     // h -> MXFP8, down (scaled MFMA) * slot affinity.
     const int Hp = mx_pad(H), Ip = mx_pad(I);
-    MKD_TRY(mx_quantize_launch(hidden, false, T, H, H, MX_E4M3, w.xq, w.xs, Hp, s), "moe quantize hidden");
+    if (!x_mx_ready)   // else the norm that produced `hidden` wrote its MXFP8 form too
+      MKD_TRY(mx_quantize_launch(hidden, false, T, H, H, MX_E4M3, w.xq, w.xs, Hp, s), "moe quantize hidden");
     {
       GemmArgs a = dense_args(gate_up, w.xq, Hp, 2 * I, Hp, T, w.hbuf, I);
       a.KW = choose_kw_mx(Hp);
@@ -1476,6 +1478,8 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
   }
   for (int l = 0; l < m->num_layers; ++l) {
     const int wl = m->window ? m->window[l] : 0;
+    const bool mx_experts = m->expert_format == MKD_MX_E4M3 || m->expert_format == MKD_MX_E2M1;
+    bool x_mx_ready = false;   // the post-attention norm wrote the experts' MXFP8 input
     mkd_attention_args ap;
     memset(&ap, 0, sizeof(ap));
     ap.X = w.attn.hnorm;                       // already normalised
@@ -1615,6 +1619,10 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
         na.gamma = static_cast<const uint16_t*>(m->ln_post[l]);
         na.out_bf16 = w.nbf; na.out_f32 = oss ? nullptr : w.nf32;
         na.rows = B; na.H = m->H; na.hidden_actual = ha; na.eps = m->eps; na.order = 0;
+        if (mx_experts && m->H % 32 == 0 && g_inlaunch_sync) {   // the experts' MXFP8 input, same launch
+          na.mx_codes = w.moe.xq; na.mx_scales = w.moe.xs; na.mx_kpad = mx_pad(m->H);
+          x_mx_ready = true;
+        }
         MKD_TRY(norm_launch(na, s), "residual + post norm");
       }
       const int ps = prof_begin(MKD_KCLASS_ROUTER, s);
@@ -1659,7 +1667,7 @@ static int decode_layers(const mkd_qwen3_model* m, int B, void* hidden, const in
                           fused_moe ? w.sync : nullptr,
                           fused_moe && w.poll_h ? reinterpret_cast<uint16_t*>(w.poll + (size_t)l * w.poll_layer + w.poll_po + w.poll_pml + w.poll_y) : nullptr,
                           kslice ? w.r : nullptr,
-                          kslice ? static_cast<const uint16_t*>(m->ln_post[l]) : nullptr))
+                          kslice ? static_cast<const uint16_t*>(m->ln_post[l]) : nullptr, x_mx_ready))
       return rc;
     // x = bf16(r + bf16(sum_k expert_k)) fused with the next layer's pre-attention
     // norm (with fuse_qn: the next QKV kernel does both; after the last layer the

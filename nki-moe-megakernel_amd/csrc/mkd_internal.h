@@ -220,6 +220,12 @@ struct NormArgs {
   int rows, H, hidden_actual;
   float eps, inv_h;
   int order;                  // 0 (x*g)*rinv, 1 (x*rinv)*g, 2 g*bf16(x*rinv)
+  // optional: the bf16 output rows also as MXFP8 (the MX experts' input), codes
+  // [rows][mx_kpad] and E8M0 scales [rows][mx_kpad / 32], zero past H -- what
+  // mx_quantize_launch writes for out_bf16 (H % 32 == 0)
+  uint8_t* mx_codes;
+  uint8_t* mx_scales;
+  int mx_kpad;
 };
 hipError_t norm_launch(NormArgs a, hipStream_t s);
 hipError_t rmsnorm_launch(const void* x, int x_f32, const uint16_t* gamma, uint16_t* out_bf16,

@@ -11,11 +11,13 @@
 //
 // The fp32 partial rows are either the K expert outputs of a token (MoE
 // finalize: bf16 residual + bf16 sum) or the split-K partials of a projection
-// (o_proj -> residual add).  y is written as bf16 and/or fp32; gamma == null
-// skips the normalisation.  The row is held in registers (H <= 8192,
+// (o_proj -> residual add).  y is written as bf16 and/or fp32, and optionally
+// as MXFP8 codes + E8M0 scales of the bf16 values (a 32-element block is four
+// threads' 8 elements); gamma == null skips the normalisation.  The row is held in registers (H <= 8192,
 // H % 8 == 0); all global traffic is 16-byte vectors.
 #include "common.h"
 #include "mkd_internal.h"
+#include "mx_codec.h"
 
 namespace mkd {
 
@@ -107,6 +109,29 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(NormArgs a) {
         *reinterpret_cast<f32x4_t*>(op) = f32x4_t{y[0], y[1], y[2], y[3]};
         *reinterpret_cast<f32x4_t*>(op + 4) = f32x4_t{y[4], y[5], y[6], y[7]};
       }
+      if (a.mx_codes) {
+        // the block's amax over the four threads tid & ~3 .. +3 (H % 32 == 0:
+        // all four are in range together)
+        float q[8], amax = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          q[j] = rbf(y[j]);
+          amax = fmaxf(amax, fabsf(q[j]));
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 1, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 2, 64));
+        const uint32_t sb = mx_scale_byte<MX_E4M3>(amax);
+        const int sh = 127 - (int)sb;
+        uint2 c = {0u, 0u};
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          (j < 4 ? c.x : c.y) |= mx_encode<MX_E4M3>(ldexpf(q[j], sh)) << (8 * (j & 3));
+        *reinterpret_cast<uint2*>(a.mx_codes + (long long)row * a.mx_kpad + i) = c;
+        if ((tid & 3) == 0) a.mx_scales[(long long)row * (a.mx_kpad / 32) + i / 32] = (uint8_t)sb;
+      }
+    } else if (a.mx_codes && i < a.mx_kpad) {   // the padding blocks past H: zero codes and scales
+      *reinterpret_cast<uint2*>(a.mx_codes + (long long)row * a.mx_kpad + i) = uint2{0u, 0u};
+      if ((tid & 3) == 0) a.mx_scales[(long long)row * (a.mx_kpad / 32) + i / 32] = 0;
     }
   }
 }
@@ -114,6 +139,9 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(NormArgs a) {
 hipError_t norm_launch(NormArgs a, hipStream_t s) {
   if (a.H % 8 != 0 || a.H > kNormThreads * 8 * kNormMaxVec || a.rows <= 0 || a.hidden_actual <= 0 ||
       (a.dsum && (a.dK < 1 || a.dK > kNormMaxDK)))
+    return hipErrorInvalidValue;
+  if (a.mx_codes && (!a.mx_scales || !a.gamma || a.H % 32 || a.mx_kpad % 32 || a.mx_kpad < a.H ||
+                     a.mx_kpad > kNormThreads * 8 * kNormMaxVec))
     return hipErrorInvalidValue;
   a.inv_h = 1.0f / (float)a.hidden_actual;
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(a.rows), dim3(kNormThreads), 0, s, a);

@@ -199,6 +199,23 @@ def test_qwen_layer_mxfp8_batch32(mk, dev):
     kr, _ = qwen_parity(y, rec, x, lw, kc, vc, cos, sin, pos, mx=True)
     knew, _ = _read_kv(model, B, S)
     _check_kv_rows(knew, kc, pos, kr)
+    _check_mx_input_fusion(model, x, pos, dev, lambda: _fill_kv(model, kc, vc), y)
+
+
+def _check_mx_input_fusion(model, x_in, pos, dev, reload, y_fused):
+    """The experts' MXFP8 input written by the post-attention norm itself equals
+    the separate quantisation launch (set_decode_path("separate_launches") keeps
+    it): the layer's output bit for bit."""
+    from nki_moe_megakernel_amd import qwen_with_megakernel as Q
+    Q.set_decode_path("separate_launches")
+    try:
+        reload()
+        y2 = x_in.to(dev).contiguous()
+        model.decode_layers(y2, pos.to(dev))
+        torch.cuda.synchronize()
+    finally:
+        Q.set_decode_path("multi_kernel")
+    assert torch.equal(y_fused.cpu(), y2.cpu())
 
 
 def _dequant_mx_torch(codes, scales, fmt, k):
@@ -247,6 +264,11 @@ def test_gpt_oss_layer_baseline_shape(mk, dev, sliding):
     torch.cuda.synchronize()
     yc = y.cpu()
     assert torch.equal(yc[:, cfg.hidden_size:], torch.zeros(B, cfg.hidden_pad - cfg.hidden_size, dtype=torch.bfloat16))
+
+    def reload():
+        model.kv_mgr.k(0).copy_(kc.to(dev))
+        model.kv_mgr.v(0).copy_(vc.to(dev))
+    _check_mx_input_fusion(model, xp, pos, dev, reload, y)
     rec = model.route_log(B)[0]
     lw = ref.GptOssLayer(
         wq=hf["q_proj.weight"], bq=hf["q_proj.bias"], wk=hf["k_proj.weight"], bk=hf["k_proj.bias"],
