@@ -63,28 +63,35 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
   // holds an upper bound (ceil(T*K / 256) + groups) and the block finds its
   // group by a scan of the device-side group counts.  XCD-aware order: blocks
   // are dealt round-robin to the 8 XCDs by linear id, so each XCD is given a
-  // contiguous run of logical tiles (n tile fastest, then item): the blocks
-  // that share an expert's weight tiles and token rows run together on one
-  // XCD's L2.
+  // contiguous run of the LIVE logical tiles (n tile fastest, then item): the
+  // blocks that share an expert's weight tiles and token rows run together on
+  // one XCD's L2, and every XCD gets an eighth of the work.  (Dealing out the
+  // grid's upper bound instead put its dead items -- those past the last live
+  // token tile -- on the last XCDs: at 2048 tokens over 128 experts 128 of 192
+  // items are live, and two XCDs sat idle.)
   // the group scan's scratch lives in the first stage buffer (no copy is issued
   // before every wave has read the scan's result)
   int* scan_s = reinterpret_cast<int*>(lds);
   int* item_s = scan_s + 8;
   const int gx = gridDim.x;
-  const int total = gx * gridDim.y;
   const int L = blockIdx.x + gx * blockIdx.y;
   // XCD x (= L % 8) owns the contiguous logical range starting at x*q + min(x, r)
-  // of q or q + 1 tiles (total = 8q + r): a bijection of [0, total)
-  const int q8 = total / 8, r8 = total % 8, xcd = L % 8;
-  const int lt = xcd * q8 + min(xcd, r8) + L / 8;
-  const int nb0 = (lt % gx) * kRB;
-  const int item = lt / gx;
+  // of q or q + 1 tiles (live = 8q + r); its k-th block (k = L / 8) takes tile
+  // k of that range, and blocks past it have no work.  The grid holds at least
+  // `live` blocks, so each XCD holds at least as many blocks as tiles it owns.
+  const int xcd = L % 8, kx = L / 8;
+  auto deal = [&](int live, int& lt) {
+    const int q8 = live / 8, r8 = live % 8;
+    lt = xcd * q8 + min(xcd, r8) + kx;
+    return kx < q8 + (xcd < r8 ? 1 : 0);
+  };
+  int lt = 0;
 
   int count, base, t0, expert = 0;
   const uint16_t* wp = a.w;
   if (a.grp_expert) {
     // thread g holds group g's token-tile count (<= 512 groups); block-wide
-    // inclusive scan in group order; the owner of `item` publishes it
+    // inclusive scan in group order; the owner of the block's item publishes it
     const int ng = *a.n_groups;
     const int c = tid < ng ? a.grp_count[tid] : 0;
     const int tiles = (c + kTileTok - 1) / kTileTok;
@@ -97,10 +104,16 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
     if (lane == 63) scan_s[w] = x;
     if (tid == 0) item_s[0] = -1;
     __syncthreads();
-    int before = 0;
-    for (int q = 0; q < w; ++q) before += scan_s[q];
+    int before = 0, items = 0;
+    for (int q = 0; q < NW; ++q) {
+      const int v = scan_s[q];
+      if (q < w) before += v;
+      items += v;
+    }
+    const bool mine = deal(gx * items, lt);
+    const int item = lt / gx;
     const int incl = before + x, excl = incl - tiles;
-    if (tid < ng && item >= excl && item < incl) {
+    if (mine && tid < ng && item >= excl && item < incl) {
       item_s[0] = tid;
       item_s[1] = (item - excl) * kTileTok;
     }
@@ -114,11 +127,13 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
     wp += (long long)expert * a.w_group_stride;
     __syncthreads();                     // item_s read by every wave before the copies
   } else {
+    if (!deal(gx * (int)gridDim.y, lt)) return;   // (the grid is exact here)
     count = a.T;
     base = 0;
-    t0 = item * kTileTok;
+    t0 = (lt / gx) * kTileTok;
     if (t0 >= count) return;
   }
+  const int nb0 = (lt % gx) * kRB;
 
   const int KB = a.K / 32;
   const int NB = (a.N + 15) / 16;
