@@ -176,7 +176,8 @@ bool tile_offsets_ok(long long x_rows, long long ldx, long long N, long long K) 
 int dense_gemm(GemmArgs a, int epi, bool xf32, hipStream_t s) {
   const int T = a.T;
   // many tokens (prefill passes): the LDS-tiled MFMA GEMM, fp32 out (+ bias)
-  if (T >= 256 && epi == EPI_F32 && !xf32 && a.kgrid <= 1 && !a.residual && !a.grp_expert &&
+  if (T >= 256 && epi == EPI_F32 && !xf32 && (a.kgrid <= 1 || gemm_tile_kgrid_ok(a.K, a.kgrid)) &&
+      !a.residual && !a.grp_expert &&
       gemm_tile_supported(a.N, a.K, EPI_SCALE_F32) && tile_offsets_ok(T, a.ldx, a.N, a.K)) {
     a.pair_scale = nullptr;
     MKD_TRY(gemm_tile_launch(a, EPI_SCALE_F32, 1, T, s), "tiled gemm");
@@ -1001,10 +1002,11 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
       o.y = o_parts;
       o.residual = nullptr;
       o.part_stride = (long long)rows * p->H_out;
-      if (o_kgrid > 1) {   // 17..128 tokens: K-split partials (gemm_mid_kgrid)
+      if (o_kgrid > 1 && rows <= 128) {   // 17..128 tokens: K-split partials (gemm_mid_kgrid)
         MKD_TRY(gemm_mid_launch(o, o_kgrid, false, s), "o_proj (mid)");
       } else {
         o.KW = choose_kw(p->nq * p->d, 512, (p->H_out + 15) / 16);
+        o.kgrid = o_kgrid;   // prefill passes: K slices of the tiled GEMM (gemm_tile_kgrid)
         if (int rc = dense_gemm(o, EPI_F32, false, s)) return rc;
       }
     } else if (int rc = dense_gemm(o, p->residual ? EPI_RESID_BF16 : EPI_BF16, false, s)) {
@@ -1219,6 +1221,9 @@ static LkWs carve_lk(Carver& c, const mkd_qwen3_model* m, int B) {
 // K split of the output projection in the decode step: the LDS-staged GEMM's at
 // 17..128 tokens (partials added by the post-attention norm), else none.
 static int o_proj_kgrid(const mkd_qwen3_model* m, int B) {
+  // a prefill pass (the tiled GEMM): K slices where the output tiles leave CUs idle
+  if (B >= 256 && gemm_tile_supported(m->H, m->nq * m->d, EPI_SCALE_F32))
+    return gemm_tile_kgrid(m->H, m->nq * m->d, B);
   return std::max(1, gemm_mid_kgrid(m->H, m->nq * m->d, B));
 }
 

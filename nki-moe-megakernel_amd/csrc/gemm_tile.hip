@@ -87,7 +87,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
   };
   int lt = 0;
 
-  int count, base, t0, expert = 0;
+  int count, base, t0, expert = 0, kq = 0;
   const uint16_t* wp = a.w;
   if (a.grp_expert) {
     // thread g holds group g's token-tile count (<= 512 groups); block-wide
@@ -127,17 +127,24 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
     wp += (long long)expert * a.w_group_stride;
     __syncthreads();                     // item_s read by every wave before the copies
   } else {
+    // dense: gridDim.y = token tiles x K slices (kgrid > 1: fp32 partials, one
+    // per slice, at y + slice * part_stride; the slice is the slowest index, so
+    // an XCD's run shares one K slice of the weights)
     if (!deal(gx * (int)gridDim.y, lt)) return;   // (the grid is exact here)
+    const int items = (int)gridDim.y / (a.kgrid > 1 ? a.kgrid : 1);
+    const int r = lt / gx;
+    kq = r / items;
     count = a.T;
     base = 0;
-    t0 = (lt / gx) * kTileTok;
+    t0 = (r - kq * items) * kTileTok;
     if (t0 >= count) return;
   }
   const int nb0 = (lt % gx) * kRB;
 
   const int KB = a.K / 32;
   const int NB = (a.N + 15) / 16;
-  const int S = KB;                      // one 32-wide fragment per stage
+  const int S = a.grp_expert || a.kgrid <= 1 ? KB : KB / a.kgrid;   // one 32-wide fragment per stage
+  const int s0 = kq * S;                 // the block's first fragment of K
 
   // ---- loads: wave w moves fragments f = w + 8j (j < 4) of each stage, one
   // 1 KiB fragment per buffer_load_dwordx4 ... lds (lane l's 16 bytes land at
@@ -155,7 +162,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
   for (int j = 0; j < FPW; ++j) {
     const int f = w + NW * j;
     const int nb = min(nb0 + f, NB - 1);           // rows past N: any valid block
-    voff[j] = f < kRB ? ((nb * KB) * 512 + lane * 8) * 2 : 0;
+    voff[j] = f < kRB ? ((nb * KB + s0) * 512 + lane * 8) * 2 : 0;
   }
   auto issue = [&](int s, int buf) {
     u32x4_t* dst = lds + buf * kStageFrags * 64;
@@ -175,7 +182,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
     if (f >= kRB) {
       const int c = min(t0 + (f - kRB) * 16 + (lane & 15), count - 1);   // absent: any valid row
       const int row = a.pair_row ? a.pair_row[base + c] : base + c;
-      voff[j] = (row * a.ldx + (lane >> 4) * 8) * 2;
+      voff[j] = (row * a.ldx + s0 * 32 + (lane >> 4) * 8) * 2;
     }
   }
   // output rows of this lane's WT tokens, loaded ahead of the main loop (the
@@ -251,7 +258,8 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
       }
     }
   } else {   // EPI_SCALE_F32
-    const uint16_t* bp = a.bias ? a.bias + (long long)expert * a.bias_group_stride : nullptr;
+    // (K slices: the bias joins the first slice's partial)
+    const uint16_t* bp = a.bias && kq == 0 ? a.bias + (long long)expert * a.bias_group_stride : nullptr;
     // all WT affinities up front (y is float too, so loads among the stores
     // could not be moved past them)
     float sc[WT];
@@ -271,7 +279,7 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
       for (int j = 0; j < WT; ++j) {
         const int tc = t0 + (wn * WT + j) * 16 + (lane & 15);
         if (tc >= count) continue;
-        float* y = static_cast<float*>(a.y) + (long long)orow[j] * a.ldy + n;
+        float* y = static_cast<float*>(a.y) + kq * a.part_stride + (long long)orow[j] * a.ldy + n;
         if (n + 3 < a.N) {
           *reinterpret_cast<f32x4_t*>(y) =
               f32x4_t{(acc[i][j][0] + bb[0]) * sc[j], (acc[i][j][1] + bb[1]) * sc[j],
@@ -296,15 +304,40 @@ bool gemm_tile_supported(int N, int K, int epi) {
   return epi == EPI_SCALE_F32;
 }
 
+bool gemm_tile_kgrid_ok(int K, int kgrid) {
+  const int KB = K / kStageK;
+  return kgrid >= 1 && kgrid <= 8 && K % kStageK == 0 && KB % kgrid == 0;
+}
+
+// K slices for a dense tiled GEMM whose output tiles leave CUs idle (a short
+// prefill pass: the attention output projection at 2048 tokens has 64 tiles):
+// the largest of 2, 4, 8 that keeps tiles x slices within one block per CU and
+// at least 16 stages per slice.  The partials cost T * N * 4 bytes per slice
+// written and read again by the consumer.
+int gemm_tile_kgrid(int N, int K, int T) {
+  const int cus = device_cus() > 0 ? device_cus() : 256;
+  const long long tiles = (long long)((N + kTileRows - 1) / kTileRows) * ((T + kTileTok - 1) / kTileTok);
+  const int KB = K / kStageK;
+  int kg = 1;
+  for (int c = 2; c <= 8; c *= 2)
+    if (gemm_tile_kgrid_ok(K, c) && KB / c >= 16 && tiles * c <= cus) kg = c;
+  return kg;
+}
+
 hipError_t gemm_tile_launch(const GemmArgs& a, int epi, int groups_max, long long total_rows,
                             hipStream_t s) {
   if (!gemm_tile_supported(a.N, a.K, epi) || groups_max <= 0 || total_rows <= 0)
     return hipErrorInvalidValue;
+  // K slices: dense fp32 partials only, each slice's rows clear of the next's
+  const int kg = a.kgrid > 1 ? a.kgrid : 1;
+  if (kg > 1 && (a.grp_expert || epi != EPI_SCALE_F32 || a.pair_scale || !gemm_tile_kgrid_ok(a.K, kg) ||
+                 a.part_stride < total_rows * a.ldy))
+    return hipErrorInvalidValue;
   // work items: every group's token tiles; with total_rows = sum of the group
   // sizes, sum_g ceil(c_g / 256) <= ceil(total_rows / 256) + groups
   const long long items = (total_rows + kTileTok - 1) / kTileTok + (a.grp_expert ? groups_max : 0);
-  if (items > 65535) return hipErrorInvalidValue;
-  const dim3 grid((a.N + kTileRows - 1) / kTileRows, (unsigned)items);
+  if (items * kg > 65535) return hipErrorInvalidValue;
+  const dim3 grid((a.N + kTileRows - 1) / kTileRows, (unsigned)(items * kg));
   // 128 KiB of dynamic LDS is above the default launch limit (set per kernel)
   if (epi == EPI_SWIGLU_BF16) {
     if (hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(gemm_tile_kernel<EPI_SWIGLU_BF16>),

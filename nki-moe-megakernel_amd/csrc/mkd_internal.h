@@ -107,6 +107,9 @@ hipError_t gemm_kloop_launch(const GemmArgs& a, hipStream_t s);
 // gemm_tile.hip: LDS-tiled grouped GEMM (many tokens per expert)
 bool gemm_tile_supported(int N, int K, int epi);
 // total_rows: the sum of the group sizes (grouped mode: T*K pairs), else the rows.
+// Dense mode with a.kgrid > 1: fp32 partials of K slices at y + slice * part_stride.
+bool gemm_tile_kgrid_ok(int K, int kgrid);
+int gemm_tile_kgrid(int N, int K, int T);   // K slices that fill the CUs (1: none)
 hipError_t gemm_tile_launch(const GemmArgs& a, int epi, int groups_max, long long total_rows,
                             hipStream_t s);
 int mx_kpad(int K);   // contraction padding of the packed MX layout
