@@ -794,8 +794,10 @@ static AttnWs carve_attn(Carver& c, int B, int H, int nq, int nkv, int d, int S_
   w.chunk = attn_chunk_for(B, nkv, S_max);
   w.n_chunks = (S_max + s_tkg + w.chunk - 1) / w.chunk;
   w.hnorm = c.take<uint16_t>((size_t)B * H);
-  // the QKV projection of 17..128 tokens comes as split-K partials
+  // the QKV projection of 17..128 tokens comes as split-K partials, and of a
+  // prefill pass as the tiled GEMM's K slices where its tiles leave CUs idle
   const int qparts = std::max({1, gemm_mid_kgrid((nq + 2 * nkv) * d, H, B),
+                               B >= 256 ? gemm_tile_kgrid((nq + 2 * nkv) * d, H, B) : 1,
                                (qkv_norm_supported(B, (nq + 2 * nkv) * d, H) &&
                                 qkv_norm_extra_tiles((nq + 2 * nkv) * d, H, d)) ? 4 : 1});
   w.qkv = c.take<float>((size_t)qparts * B * (nq + 2 * nkv) * d);
@@ -882,8 +884,16 @@ static int attention_core(const mkd_attention_args* p, AttnWs& w, const int* pos
       g.part_stride = (long long)rows * qkv_n;
       MKD_TRY(gemm_mid_launch(g, kq, false, s), "qkv (mid)");
       qkv_parts = kq;
-    } else if (int rc = dense_gemm(g, EPI_F32, false, s)) {
-      return rc;
+    } else {
+      if (rows >= 256 && gemm_tile_supported(qkv_n, p->H, EPI_SCALE_F32)) {
+        const int kt = gemm_tile_kgrid(qkv_n, p->H, rows);   // a short prefill pass: K slices
+        if (kt > 1) {
+          g.kgrid = kt;
+          g.part_stride = (long long)rows * qkv_n;
+          qkv_parts = kt;
+        }
+      }
+      if (int rc = dense_gemm(g, EPI_F32, false, s)) return rc;
     }
     prof_end(ps, s);
   }
