@@ -41,8 +41,19 @@ attn_prefill_kernel(AttnArgs a) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int tl = lane & 15, q4 = lane >> 4;
   const int nqt = (a.B + kPfTok - 1) / kPfTok;
-  const int t0 = (nqt - 1 - (int)blockIdx.x) * kPfTok;   // the longest tiles first
-  const int g = blockIdx.y, hg = blockIdx.z * HPB + w, h = g * GQA + hg;   // head in group / overall
+  // Work units (query tile, kv group, head slice), longest tiles first: unit u
+  // is tile nqt - 1 - u / nsets of set u % nsets.  Block L takes unit L, except
+  // where the whole grid is resident at two blocks per CU: there block L >= CUs,
+  // which shares a CU with block L - CUs, takes unit total - 1 - (L - CUs), so
+  // the two tiles on a CU have complementary lengths (2048 tokens: 65.7k ->
+  // 70.6k tokens/s for the pass; with two tiles of the same length on every
+  // CU, the CUs of the longest tiles set the launch's length).
+  const int nsets = gridDim.y * gridDim.z, total = nqt * nsets;
+  const int L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+  const int u = (a.pf_pair > 0 && L >= a.pf_pair) ? total - 1 - (L - a.pf_pair) : L;
+  const int t0 = (nqt - 1 - u / nsets) * kPfTok;
+  const int set = u % nsets;
+  const int g = set % gridDim.y, hg = (set / gridDim.y) * HPB + w, h = g * GQA + hg;   // head in group / overall
   const int tok = t0 + tl;
   const bool live = tok < a.B;
   const int tokc = live ? tok : a.B - 1;                 // in-range address for absent tokens
@@ -239,12 +250,19 @@ hipError_t attn_prefill_launch(const AttnArgs& a, int rope_mode, hipStream_t s) 
   if (hipError_t e = attn_prep_write_launch(a, rope_mode, s)) return e;
   const int gqa = a.nq / a.nkv, hpb = gqa < 8 ? gqa : 8;
   const dim3 grid((a.B + kPfTok - 1) / kPfTok, a.nkv, gqa / hpb);
+  // tile pairing for the 8-wave blocks (two per CU: 128 VGPRs, 68 KiB of LDS
+  // each) when the whole grid is resident: workgroups go round-robin to the
+  // XCDs and fill each XCD's CUs in order, so block L + CUs lands beside block L
+  AttnArgs b = a;
+  const long long total = (long long)grid.x * grid.y * grid.z;
+  const int cus = device_cus();
+  b.pf_pair = (hpb == 8 && cus > 0 && total > cus && total <= 2LL * cus) ? cus : 0;
   switch (gqa) {
-    case 1: return timed_launch(attn_prefill_kernel<1>, grid, dim3(64), 0, s, a);
-    case 2: return timed_launch(attn_prefill_kernel<2>, grid, dim3(128), 0, s, a);
-    case 4: return timed_launch(attn_prefill_kernel<4>, grid, dim3(256), 0, s, a);
-    case 8: return timed_launch(attn_prefill_kernel<8>, grid, dim3(512), 0, s, a);
-    case 16: return timed_launch(attn_prefill_kernel<16>, grid, dim3(512), 0, s, a);
+    case 1: return timed_launch(attn_prefill_kernel<1>, grid, dim3(64), 0, s, b);
+    case 2: return timed_launch(attn_prefill_kernel<2>, grid, dim3(128), 0, s, b);
+    case 4: return timed_launch(attn_prefill_kernel<4>, grid, dim3(256), 0, s, b);
+    case 8: return timed_launch(attn_prefill_kernel<8>, grid, dim3(512), 0, s, b);
+    case 16: return timed_launch(attn_prefill_kernel<16>, grid, dim3(512), 0, s, b);
   }
   return hipErrorInvalidValue;
 }

@@ -285,6 +285,10 @@ struct AttnArgs {
   // k / v rows are written to the cache before the attention reads it, so each
   // token attends the rows of the earlier tokens of the same step
   int prefill;
+  // prefill attention, set by its launch: the CU count when the whole grid is
+  // resident at two blocks per CU (block L then shares a CU with block L + CUs),
+  // else 0
+  int pf_pair;
   // new tokens per sequence (0 / 1: one).  With s_tkg > 1 the B rows are
   // s_tkg consecutive tokens of each of B / s_tkg sequences: row r is token
   // r % s_tkg of sequence r / s_tkg, whose window is its n_prior cache positions
