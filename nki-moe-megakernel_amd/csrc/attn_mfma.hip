@@ -402,13 +402,14 @@ MKD_DEV void attn_chunk_block(const AttnArgs& a, int rope_mode, int c, int g, in
         for (int e = 0; e < VW; ++e) v[j][e] = 0u;
       }
     }
+    // the B operand's 16-bit halves from two V rows: one byte permute per
+    // dword (selector 0x05040100: bytes 0-1 of each row; 0x07060302: bytes 2-3)
     uint2 bop[NDT];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       const int e = dt >> 1;
-      bop[dt] = (dt & 1)
-          ? uint2{(v[0][e] >> 16) | (v[1][e] & 0xffff0000u), (v[2][e] >> 16) | (v[3][e] & 0xffff0000u)}
-          : uint2{(v[0][e] & 0xffffu) | (v[1][e] << 16), (v[2][e] & 0xffffu) | (v[3][e] << 16)};
+      const uint32_t sel = (dt & 1) ? 0x07060302u : 0x05040100u;
+      bop[dt] = uint2{__builtin_amdgcn_perm(v[1][e], v[0][e], sel), __builtin_amdgcn_perm(v[3][e], v[2][e], sel)};
     }
     if constexpr (TPW % 2 == 0) {
       // tiles in pairs on the 32-deep MFMA: lane group q's k slots 8q .. 8q+7
