@@ -90,22 +90,34 @@ __global__ void decode_begin_kernel(DecodeBeginArgs d) {
   // rows and the new token), n the position clamped like the prior length
   const int n = min(max(d.pos[0], 0), d.S_max);
   const int nch = min((n + 1 + d.chunk - 1) / d.chunk, d.n_chunks);
-  const long long po_used = (long long)d.nq * nch * d.D, ml_used = (long long)d.nq * nch * 2;
+  // per layer: one run of nch * D words per head (chunk partials), one of
+  // nch * 2 per head (their max / sum), and the whole tail; one block per run
+  // at a time, 16-byte stores where the run starts 16-byte aligned
   const long long tail = d.layer_words - d.po - d.pml;
-  const long long used = po_used + ml_used + tail;
-  for (long long k = tid; k < used * d.layers; k += nth) {
-    const long long l = k / used, i = k % used;
-    long long off;
-    if (i < po_used) {
-      const long long h = i / ((long long)nch * d.D), r = i % ((long long)nch * d.D);
-      off = h * d.n_chunks * d.D + r;
-    } else if (i < po_used + ml_used) {
-      const long long j = i - po_used, h = j / (2LL * nch), r = j % (2LL * nch);
-      off = d.po + h * d.n_chunks * 2 + r;
+  const long long runs = 2LL * d.nq + 1;
+  for (long long ru = blockIdx.x; ru < runs * d.layers; ru += gridDim.x) {
+    const long long l = ru / runs;
+    const int j = (int)(ru % runs);
+    long long off, len;
+    if (j < d.nq) {
+      off = (long long)j * d.n_chunks * d.D;
+      len = (long long)nch * d.D;
+    } else if (j < 2 * d.nq) {
+      off = d.po + (long long)(j - d.nq) * d.n_chunks * 2;
+      len = 2LL * nch;
     } else {
-      off = d.po + d.pml + (i - po_used - ml_used);
+      off = d.po + d.pml;
+      len = tail;
     }
-    d.poll[l * d.layer_words + off] = kPollEmpty;
+    uint32_t* p = d.poll + l * d.layer_words + off;
+    long long done = 0;
+    if ((reinterpret_cast<uintptr_t>(p) & 15) == 0) {
+      const long long n4 = len / 4;
+      for (long long i = threadIdx.x; i < n4; i += blockDim.x)
+        reinterpret_cast<u32x4_t*>(p)[i] = u32x4_t{kPollEmpty, kPollEmpty, kPollEmpty, kPollEmpty};
+      done = n4 * 4;
+    }
+    for (long long i = done + threadIdx.x; i < len; i += blockDim.x) p[i] = kPollEmpty;
   }
 }
 
