@@ -16,7 +16,11 @@
 // [32q, 32q+32) (one 16-byte run, low nibble first); the scale byte a lane
 // supplies is the E8M0 of row r, k-block q (k in [32q, 32q+32)).  The B
 // operand (16 token columns x 128 k) uses the same per-lane layout.  Packed:
-//   codes [G][NB][KB][64 lanes][32 B (e4m3) | 16 B (e2m1)]   KB = K_pad/128
+//   codes [G][NB][KB][2 halves][64 lanes][16 B] (e4m3) | [G][NB][KB][64 lanes][16 B] (e2m1)
+//   KB = K_pad/128; an e4m3 fragment's two 16-byte halves per lane lie 1 KiB
+//   apart, so each of its two loads reads 1 KiB contiguous (with the halves
+//   adjacent per lane, each load touched twice the cache lines it used and the
+//   address unit ran ~80 % busy)
 //   scales[G][NB][ceil(KB/4)][64 lanes][4 B]  byte i = fragment 4*kb4 + i
 // Rows past N and k past K are zero codes with scale byte 0.  K_pad (mx_kpad)
 // is K rounded up to 128, or to 512 when that leaves no even split of the
@@ -150,9 +154,9 @@ __global__ void mx_pack_kernel(const uint8_t* __restrict__ codes, const uint8_t*
           for (int j = 0; j < 16; ++j) out[j] = src[k0 / 2 + j];
       }
     }
-    uint8_t* d = dst + ((((long long)g * NB + nb) * KB + kb) * 64 + lane) * BPL;
+    uint8_t* d = dst + (((long long)g * NB + nb) * KB + kb) * 64 * BPL + lane * 16;
 #pragma unroll
-    for (int j = 0; j < BPL; ++j) d[j] = out[j];
+    for (int j = 0; j < BPL; ++j) d[(j / 16) * 1024 + (j % 16)] = out[j];
     if ((kb & 3) == 0) {
       uint32_t sv = 0;
 #pragma unroll
@@ -171,12 +175,13 @@ __global__ void mx_pack_kernel(const uint8_t* __restrict__ codes, const uint8_t*
 // ---------------------------------------------------------------------------
 // A fragment registers: 8 dwords for 8-bit elements, 4 for 4-bit ones (the
 // MFMA reads only the low 4 dwords of a 4-bit operand).
+// p: the lane's 16 bytes of the fragment's first half (the second half 1 KiB on)
 template <int FMT>
 struct WFrag {
   u32x4_t lo, hi;
   MKD_DEV void load(const uint8_t* p) {
     lo = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
-    hi = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p + 16));
+    hi = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p + 1024));
   }
   MKD_DEV i32x8_t op() const {
     return i32x8_t{(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3],
@@ -340,7 +345,7 @@ __global__ void __launch_bounds__(512) gemm_mx_kernel(GemmArgs a) {
 #pragma unroll
     for (int r = 0; r < RB; ++r) {
       const long long rb = (long long)min(tile0 + t, n_tiles - 1) * RB + r;
-      wrow[t * RB + r] = w + ((rb * KB + kb0) * 64 + lane) * BPL;
+      wrow[t * RB + r] = w + (rb * KB + kb0) * 64 * BPL + lane * 16;
       srow[t * RB + r] = wsc + (rb * KB4 * 64 + lane) * 4;
     }
   constexpr int U = mx_batch_frags<FMT, R>();
