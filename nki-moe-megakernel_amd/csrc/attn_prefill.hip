@@ -21,6 +21,7 @@
 // end.  Four waves per SIMD (two 8-wave blocks per CU, <= 128 VGPRs).
 #include "common.h"
 #include "mkd_internal.h"
+#include "launch_rules.h"
 #include "attn_common.h"
 #include "coherent.h"
 
@@ -50,7 +51,7 @@ attn_prefill_kernel(AttnArgs a) {
   // CU, the CUs of the longest tiles set the launch's length).
   const int nsets = gridDim.y * gridDim.z, total = nqt * nsets;
   const int L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
-  const int u = (a.pf_pair > 0 && L >= a.pf_pair) ? total - 1 - (L - a.pf_pair) : L;
+  const int u = prefill_unit_rule(L, total, a.pf_pair);
   const int t0 = (nqt - 1 - u / nsets) * kPfTok;
   const int set = u % nsets;
   const int g = set % gridDim.y, hg = (set / gridDim.y) * HPB + w, h = g * GQA + hg;   // head in group / overall
@@ -261,7 +262,7 @@ hipError_t attn_prefill_launch(const AttnArgs& a, int rope_mode, hipStream_t s) 
   AttnArgs b = a;
   const long long total = (long long)grid.x * grid.y * grid.z;
   const int cus = device_cus();
-  b.pf_pair = (hpb == 8 && cus > 0 && total > cus && total <= 2LL * cus) ? cus : 0;
+  b.pf_pair = prefill_pair_rule(total, cus, hpb);
   switch (gqa) {
     case 1: return timed_launch(attn_prefill_kernel<1>, grid, dim3(64), 0, s, b);
     case 2: return timed_launch(attn_prefill_kernel<2>, grid, dim3(128), 0, s, b);

@@ -21,6 +21,7 @@
 #include "common.h"
 #include "gemm_epi.h"
 #include "mkd_internal.h"
+#include "launch_rules.h"
 
 namespace mkd {
 
@@ -75,16 +76,10 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
   int* item_s = scan_s + 8;
   const int gx = gridDim.x;
   const int L = blockIdx.x + gx * blockIdx.y;
-  // XCD x (= L % 8) owns the contiguous logical range starting at x*q + min(x, r)
-  // of q or q + 1 tiles (live = 8q + r); its k-th block (k = L / 8) takes tile
-  // k of that range, and blocks past it have no work.  The grid holds at least
-  // `live` blocks, so each XCD holds at least as many blocks as tiles it owns.
-  const int xcd = L % 8, kx = L / 8;
-  auto deal = [&](int live, int& lt) {
-    const int q8 = live / 8, r8 = live % 8;
-    lt = xcd * q8 + min(xcd, r8) + kx;
-    return kx < q8 + (xcd < r8 ? 1 : 0);
-  };
+  // (tile_deal_rule: XCD L % 8 owns a contiguous run of the live tiles, its
+  // k-th block takes tile k of it, blocks past the run have no work; the grid
+  // holds at least `live` blocks, so every tile is taken)
+  auto deal = [&](int live, int& lt) { return tile_deal_rule(live, L, &lt); };
   int lt = 0;
 
   int count, base, t0, expert = 0, kq = 0;
@@ -315,13 +310,8 @@ bool gemm_tile_kgrid_ok(int K, int kgrid) {
 // at least 16 stages per slice.  The partials cost T * N * 4 bytes per slice
 // written and read again by the consumer.
 int gemm_tile_kgrid(int N, int K, int T) {
-  const int cus = device_cus() > 0 ? device_cus() : 256;
-  const long long tiles = (long long)((N + kTileRows - 1) / kTileRows) * ((T + kTileTok - 1) / kTileTok);
-  const int KB = K / kStageK;
-  int kg = 1;
-  for (int c = 2; c <= 8; c *= 2)
-    if (gemm_tile_kgrid_ok(K, c) && KB / c >= 16 && tiles * c <= cus) kg = c;
-  return kg;
+  static_assert(kTileRows == 256 && kTileTok == 256 && kStageK == 32, "tile_kgrid_rule's tile shape");
+  return tile_kgrid_rule(N, K, T, device_cus());
 }
 
 hipError_t gemm_tile_launch(const GemmArgs& a, int epi, int groups_max, long long total_rows,

@@ -3,6 +3,12 @@
 // them over many device sizes.
 #pragma once
 
+#if defined(__HIPCC__)
+#define MKD_RULE __host__ __device__ __forceinline__
+#else
+#define MKD_RULE inline
+#endif
+
 namespace mkd {
 
 // QKV projection + norm at one block per CU (qkv_norm.hip): N / 16 row tiles of
@@ -23,6 +29,46 @@ inline int qkv_extra_tiles_rule(int N, int K, int d, int cus) {
   const int extra = tiles - cus;
   if (extra * 4 > cus) return 0;
   return ((tiles - extra) * 16) % d == 0 ? extra : 0;
+}
+
+// The LDS-tiled GEMM (gemm_tile.hip) deals its `live` logical tiles to the 8
+// XCDs (workgroups go round-robin to the XCDs by linear id L): XCD x = L % 8 owns
+// the contiguous run starting at x * q + min(x, r) of q or q + 1 tiles (live =
+// 8q + r), and its k-th block (k = L / 8) takes tile k of the run.  Returns
+// whether block L has a tile (then *lt); with a grid of at least `live` blocks
+// every tile is taken exactly once.
+MKD_RULE bool tile_deal_rule(int live, int L, int* lt) {
+  const int xcd = L % 8, k = L / 8, q = live / 8, r = live % 8;
+  *lt = xcd * q + (xcd < r ? xcd : r) + k;
+  return k < q + (xcd < r ? 1 : 0);
+}
+
+// K slices for a dense tiled GEMM (256 x 256 output tiles, 32-wide stages) whose
+// tiles leave CUs idle: the largest of 2, 4, 8 that divides the stage count,
+// keeps at least 16 stages per slice and tiles x slices within the CU count
+// (cus <= 0: taken as 256).
+MKD_RULE int tile_kgrid_rule(int N, int K, int T, int cus) {
+  if (cus <= 0) cus = 256;
+  if (K <= 0 || K % 32 != 0 || N <= 0 || T <= 0) return 1;
+  const long long tiles = (long long)((N + 255) / 256) * ((T + 255) / 256);
+  const int KB = K / 32;
+  int kg = 1;
+  for (int c = 2; c <= 8; c *= 2)
+    if (KB % c == 0 && KB / c >= 16 && tiles * c <= cus) kg = c;
+  return kg;
+}
+
+// Prefill attention work units, longest query tiles first (unit u = tile
+// nqt - 1 - u / sets of set u % sets).  Where the grid of `total` blocks is
+// resident at two blocks per CU (cus < total <= 2 cus, pair_cus = cus, else 0),
+// block L >= cus -- on the CU of block L - cus -- takes unit total - 1 - (L -
+// cus), so the two tiles of a CU have complementary lengths; a bijection of
+// [0, total) either way.
+MKD_RULE int prefill_unit_rule(int L, int total, int pair_cus) {
+  return (pair_cus > 0 && L >= pair_cus) ? total - 1 - (L - pair_cus) : L;
+}
+MKD_RULE int prefill_pair_rule(long long total, int cus, int heads_per_block) {
+  return (heads_per_block == 8 && cus > 0 && total > cus && total <= 2LL * cus) ? cus : 0;
 }
 
 }  // namespace mkd

@@ -10,7 +10,17 @@
   1..1024 and the model shapes (Qwen3-30B-A3B, GPT-OSS-20B and head sizes 64 /
   128 / 256), a split is only taken with more tiles than CUs, at most one extra
   tile per four CUs, and with its split row on a head boundary; known answers on
-  gfx950's 256 / 304-CU parts.
+  gfx950's 256 / 304-CU parts;
+* the tiled GEMM's XCD dealing: for every live tile count up to 3000 and grids of
+  `live` to `live + 300` blocks, every tile is taken by exactly one block, each
+  XCD's tiles form one contiguous run, and no block has more than one;
+* the tiled GEMM's K slices: the slice count divides the stage count, leaves
+  >= 16 stages, fits tiles x slices in the CUs and is the largest such of 2 / 4 /
+  8, over shapes, token counts and CU counts; known answers for the Qwen3
+  projections;
+* the prefill attention's work units: a bijection of [0, total) for every grid
+  size and CU count, and where paired, the two blocks of a CU (L, L + CUs) take
+  units summing to total - 1 (complementary tile lengths).
 """
 import os
 import shutil
@@ -78,6 +88,69 @@ int main() {
     printf("known answers\n");
     return 1;
   }
+  // 3. XCD dealing of the tiled GEMM
+  static int owner[4096];
+  for (int live = 0; live <= 3000; live += (live < 100 ? 1 : 37)) {
+    for (int grid = live; grid <= live + 300; grid += 61) {
+      for (int t = 0; t < live; ++t) owner[t] = -1;
+      int first[8], last[8], cnt[8];
+      for (int x = 0; x < 8; ++x) { first[x] = 1 << 30; last[x] = -1; cnt[x] = 0; }
+      for (int L = 0; L < grid; ++L) {
+        int lt = -1;
+        if (!tile_deal_rule(live, L, &lt)) continue;
+        if (lt < 0 || lt >= live || owner[lt] != -1) { printf("deal live=%d grid=%d L=%d lt=%d\n", live, grid, L, lt); return 1; }
+        owner[lt] = L;
+        const int x = L % 8;
+        first[x] = lt < first[x] ? lt : first[x];
+        last[x] = lt > last[x] ? lt : last[x];
+        ++cnt[x];
+      }
+      for (int t = 0; t < live; ++t)
+        if (owner[t] < 0) { printf("deal untaken live=%d grid=%d t=%d\n", live, grid, t); return 1; }
+      for (int x = 0; x < 8; ++x)
+        if (cnt[x] && last[x] - first[x] + 1 != cnt[x]) { printf("deal run live=%d x=%d\n", live, x); return 1; }
+    }
+  }
+  // 4. K slices of the dense tiled GEMM
+  const int NK[][2] = {{5120, 2048}, {2048, 4096}, {128, 2048}, {2880, 4096}, {4096, 64}, {256, 96}};
+  for (const auto& nk : NK)
+    for (int T = 1; T <= 8192; T = T * 2 + 1)
+      for (int cus = 0; cus <= 512; cus += 32) {
+        const int kg = tile_kgrid_rule(nk[0], nk[1], T, cus);
+        const int KB = nk[1] / 32, c = cus > 0 ? cus : 256;
+        const long long tiles = (long long)((nk[0] + 255) / 256) * ((T + 255) / 256);
+        if (kg < 1 || kg > 8 || KB % kg || (kg > 1 && (KB / kg < 16 || tiles * kg > c))) {
+          printf("kgrid N=%d K=%d T=%d cus=%d kg=%d\n", nk[0], nk[1], T, cus, kg); return 1;
+        }
+        if (kg < 8 && KB % (2 * kg) == 0 && KB / (2 * kg) >= 16 && tiles * 2 * kg <= c) {
+          printf("kgrid not largest N=%d K=%d T=%d cus=%d kg=%d\n", nk[0], nk[1], T, cus, kg); return 1;
+        }
+      }
+  // o_proj (N 2048, K 4096) at 2048 tokens: 64 tiles -> 4 slices; QKV (N 5120,
+  // K 2048) at 2048 tokens: 160 tiles -> none; at 512: 40 tiles -> 4
+  if (tile_kgrid_rule(2048, 4096, 2048, 256) != 4 || tile_kgrid_rule(5120, 2048, 2048, 256) != 1 ||
+      tile_kgrid_rule(5120, 2048, 512, 256) != 4 || tile_kgrid_rule(2048, 4096, 4096, 256) != 2) {
+    printf("kgrid known answers\n"); return 1;
+  }
+  // 5. prefill attention work units
+  static int seen[4096];
+  for (int cus = 1; cus <= 320; cus += 7)
+    for (int total = 1; total <= 2 * cus + 40 && total <= 4096; total += 3) {
+      const int pair = prefill_pair_rule(total, cus, 8);
+      if (pair && !(total > cus && total <= 2 * cus)) { printf("pair rule\n"); return 1; }
+      for (int i = 0; i < total; ++i) seen[i] = 0;
+      for (int L = 0; L < total; ++L) {
+        const int u = prefill_unit_rule(L, total, pair);
+        if (u < 0 || u >= total || seen[u]++) { printf("units cus=%d total=%d L=%d\n", cus, total, L); return 1; }
+        if (pair && L >= cus && u + prefill_unit_rule(L - cus, total, pair) != total - 1) {
+          printf("pairing cus=%d total=%d L=%d\n", cus, total, L); return 1;
+        }
+      }
+    }
+  if (prefill_pair_rule(512, 256, 8) != 256 || prefill_pair_rule(1024, 256, 8) != 0 ||
+      prefill_pair_rule(256, 256, 8) != 0 || prefill_pair_rule(512, 256, 4) != 0) {
+    printf("pair known answers\n"); return 1;
+  }
   printf("ok %lld\n", taken);
   return 0;
 }
@@ -96,7 +169,7 @@ def rules_binary(tmp_path_factory):
     return str(exe)
 
 
-def test_poll_word_and_qkv_split_rules(rules_binary):
+def test_poll_word_split_deal_kgrid_and_unit_rules(rules_binary):
     r = subprocess.run([rules_binary], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert r.stdout.startswith("ok ")
