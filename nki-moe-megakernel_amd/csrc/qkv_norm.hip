@@ -16,6 +16,7 @@
 #include "common.h"
 #include "mkd_internal.h"
 #include "launch_rules.h"
+#include "coherent.h"
 
 namespace mkd {
 
@@ -112,23 +113,26 @@ qkv_norm_gemm_kernel(QkvNormArgs a) {
       if (tt == t) ss[tt] += q;
   };
   load_chunk(0);
+  // gamma before the weights too: a wave's loads complete in issue order, so
+  // the norm (which needs gamma) then runs while the weight fragments stream
+#pragma unroll
+  for (int c = 0; c < NC; ++c)
+    gm[c] = ld16(a.gamma + (min((c * kQnThreads + (int)threadIdx.x) * 8, T * K - 8) % K));
   u32x4_t wf[NF];
   const uint16_t* wp = a.w + ((long long)rb * KB + ks * NF) * 512 + lane * 8;
 #pragma unroll
   for (int u = 0; u < NF; ++u)
     wf[u] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(wp + u * 512));
   form_chunk(0);
-  // gamma (L2-resident) is fetched under the block reduction below
-#pragma unroll
-  for (int c = 0; c < NC; ++c)
-    gm[c] = ld16(a.gamma + (min((c * kQnThreads + (int)threadIdx.x) * 8, T * K - 8) % K));
   // per-token sums over the block (fixed order)
 #pragma unroll
   for (int t = 0; t < kQkvNormMaxT; ++t) {
     const float v = wave_sum(ss[t]);
     if (lane == 0) ssr[w * kQkvNormMaxT + t] = v;
   }
-  __syncthreads();
+  // (the block barriers here order LDS only -- ssr, hs, red -- so they wait for
+  // LDS, not for the weight loads still in flight as __syncthreads' fence would)
+  lds_barrier();
   float rinv[kQkvNormMaxT];
 #pragma unroll
   for (int t = 0; t < kQkvNormMaxT; ++t) {
@@ -152,7 +156,7 @@ qkv_norm_gemm_kernel(QkvNormArgs a) {
       o[j] = pack2bf((bf_lo(rv[c][j]) * ri) * bf_lo(gm[c][j]), (bf_hi(rv[c][j]) * ri) * bf_hi(gm[c][j]));
     *reinterpret_cast<u32x4_t*>(hs + t * K + h) = o;
   }
-  __syncthreads();
+  lds_barrier();
 
   // ---- 4. the wave's MFMAs (B operand: token l%16, k 8*(l/16)..+8 of the slice) ----
   const int col = lane & 15;
@@ -164,7 +168,7 @@ qkv_norm_gemm_kernel(QkvNormArgs a) {
     acc = mfma16x16x32(wf[u], xf, acc);
   }
   red[w][lane] = acc;
-  __syncthreads();
+  lds_barrier();
   // ---- 5. the 8 waves' tiles in wave order; rows 4*(l/16).. of token l%16 ----
   if (w == 0 && col < T) {
     f32x4_t s = red[0][lane];
