@@ -37,7 +37,13 @@ constexpr int kStages = MKD_TILE_STAGES;  // LDS stage buffers (kStages - 1 in f
 constexpr int kRB = kTileRows / 16;      // row blocks per block (16)
 constexpr int kTT = kTileTok / 16;       // token tiles per block (16)
 constexpr int kStageFrags = kRB + kTT;   // 1 KiB fragments per stage (32)
-constexpr int kLdsBytes = kStages * kStageFrags * 1024;
+constexpr int kRingBytes = kStages * kStageFrags * 1024;
+// the fp32 epilogue stages half of the output tile in LDS, [256 tokens][128 + 4
+// rows] (the 4 floats of padding spread a lane group's 16 rows over the banks),
+// then the block's output row indices
+constexpr int kStgLd = 132;
+constexpr int kStgBytes = kTileTok * kStgLd * 4 + kTileTok * 4;
+constexpr int kLdsBytes = kRingBytes > kStgBytes ? kRingBytes : kStgBytes;
 
 // s_waitcnt with only vmcnt = n (expcnt / lgkmcnt left at their maxima); gfx9
 // encoding: vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14.
@@ -260,31 +266,56 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
     float sc[WT];
 #pragma unroll
     for (int j = 0; j < WT; ++j) sc[j] = a.pair_scale ? a.pair_scale[orow[j]] : 1.0f;
+    // The tile goes out through LDS, half (128 rows) at a time: the waves of
+    // that half store their scaled accumulators as [token][row], then every
+    // thread writes 16 contiguous bytes of a token's 512-byte row segment --
+    // directly, a store instruction wrote 64 bytes into each of 16 scattered
+    // output rows, and the stores took ~40 % of the down projection's time.
+    wait_vmcnt<0>();                     // the ring's last copies have landed
+    float* stg = reinterpret_cast<float*>(lds);
+    int* orow_s = reinterpret_cast<int*>(stg + kTileTok * kStgLd);
+    if (tid < kTileTok) {
+      const int tc = min(t0 + tid, count - 1);
+      orow_s[tid] = a.pair_out_row ? a.pair_out_row[base + tc] : base + tc;
+    }
+    __syncthreads();                     // every wave is past its last operand reads
+    float* ybase = static_cast<float*>(a.y) + kq * a.part_stride;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int nb = nb0 + wm * 8 + i;
-      if (nb >= NB) continue;
-      const int n = nb * 16 + q4;
-      float bb[4] = {0.f, 0.f, 0.f, 0.f};
-      if (bp) {
+    for (int half = 0; half < 2; ++half) {
+      if (wm == half) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) bb[e] = (n + e < a.N) ? bf2f(bp[n + e]) : 0.f;
+        for (int i = 0; i < 8; ++i) {
+          const int n = (nb0 + wm * 8 + i) * 16 + q4;
+          float bb[4] = {0.f, 0.f, 0.f, 0.f};
+          if (bp) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bb[e] = (n + e < a.N) ? bf2f(bp[n + e]) : 0.f;
+          }
+#pragma unroll
+          for (int j = 0; j < WT; ++j) {
+            const int tl = (wn * WT + j) * 16 + (lane & 15);
+            *reinterpret_cast<f32x4_t*>(stg + tl * kStgLd + i * 16 + q4) =
+                f32x4_t{(acc[i][j][0] + bb[0]) * sc[j], (acc[i][j][1] + bb[1]) * sc[j],
+                        (acc[i][j][2] + bb[2]) * sc[j], (acc[i][j][3] + bb[3]) * sc[j]};
+          }
+        }
       }
-#pragma unroll
-      for (int j = 0; j < WT; ++j) {
-        const int tc = t0 + (wn * WT + j) * 16 + (lane & 15);
-        if (tc >= count) continue;
-        float* y = static_cast<float*>(a.y) + kq * a.part_stride + (long long)orow[j] * a.ldy + n;
+      __syncthreads();
+      const int c4 = (tid & 31) * 4;                  // row offset within the half
+      const int n = (nb0 + half * 8) * 16 + c4;
+      for (int tl = tid >> 5; tl < kTileTok; tl += 16) {
+        if (t0 + tl >= count) break;
+        const f32x4_t v = *reinterpret_cast<const f32x4_t*>(stg + tl * kStgLd + c4);
+        float* y = ybase + (long long)orow_s[tl] * a.ldy + n;
         if (n + 3 < a.N) {
-          *reinterpret_cast<f32x4_t*>(y) =
-              f32x4_t{(acc[i][j][0] + bb[0]) * sc[j], (acc[i][j][1] + bb[1]) * sc[j],
-                      (acc[i][j][2] + bb[2]) * sc[j], (acc[i][j][3] + bb[3]) * sc[j]};
+          *reinterpret_cast<f32x4_t*>(y) = v;
         } else {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            if (n + e < a.N) y[e] = (acc[i][j][e] + bb[e]) * sc[j];
+            if (n + e < a.N) y[e] = v[e];
         }
       }
+      __syncthreads();                   // the half is read before the next one is written
     }
   }
   wait_vmcnt<0>();                       // no copy into LDS outlives the block
