@@ -12,8 +12,9 @@
 // run of the packed weights) and 16 B fragments (16 tokens x 32 k, gathered
 // through the routing table), copied global -> LDS directly in MFMA operand
 // order (buffer_load_dwordx4 ... lds), three stages ahead in a ring of four LDS
-// buffers (128 KiB); one barrier per stage.  Per stage a wave issues 32 MFMAs
-// against 12 contiguous 1 KiB LDS reads.
+// buffers (128 KiB).  Per stage a wave issues 32 MFMAs against 12 contiguous
+// 1 KiB LDS reads; the two halves of the block's waves run half a stage apart
+// (two barriers per stage), one group reading while the other multiplies.
 //
 // Epilogues: EPI_SWIGLU_BF16 (gate / up row blocks interleaved in the packing,
 // so both halves of a pair sit in the same wave) and EPI_SCALE_F32 (affinity
@@ -201,34 +202,55 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
     for (int j = 0; j < WT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
   for (int s = 0; s < kStages - 1; ++s) issue(min(s, S - 1), s);
-  for (int s = 0; s < S; ++s) {
-    // this thread's loads of stage s have landed once at most the kStages - 2
-    // later issued stages (FPW loads each) are outstanding -- every iteration
-    // issues one stage, so the count is the same throughout; the barrier then
-    // makes every wave's stage s visible and frees the buffer of stage s - 1
-    wait_vmcnt<(kStages - 2) * FPW>();
-    asm volatile("s_barrier" ::: "memory");
-    const u32x4_t* st = lds + (s % kStages) * kStageFrags * 64;
-    // B first, then A in MFMA order: the MFMAs of row block i wait only for
-    // the reads up to af[i] (LDS returns in order), so they start early
-    u32x4_t af[8], bf[WT];
-#pragma unroll
-    for (int j = 0; j < WT; ++j) bf[j] = st[(kRB + wn * WT + j) * 64 + lane];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) af[i] = st[(wm * 8 + i) * 64 + lane];
-    __builtin_amdgcn_sched_barrier(0);     // all 12 operand reads in flight together
-    // the copies of stage s + kStages - 1 go out behind the reads (into the buffer that
-    // stage s - 1 used, which every wave has left: barrier above); past the
-    // last stage the last stage is copied again into that dead buffer, which
-    // keeps the loop free of branches and the wait count fixed
-    issue(min(s + kStages - 1, S - 1), (s + kStages - 1) % kStages);
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-#pragma unroll
-      for (int j = 0; j < WT; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
-      __builtin_amdgcn_sched_barrier(0);   // row-block order: group i waits for af[i] only
+  // Two wave groups run half a stage apart: waves 0-3 (group 0) and 4-7 (group
+  // 1), one of each per SIMD.  Group 1 takes one barrier before the loop and
+  // group 0 one after it, so between two barriers one group reads its operands
+  // of a stage from LDS while the other runs the previous stage's MFMAs, and the
+  // SIMD's matrix core has work in both halves.  Every wave executes the same
+  // loop: wait for its copies of stage s, barrier, 12 operand reads, the copies
+  // of stage s + kStages - 1, barrier, 32 MFMAs.  Ordering:
+  //  * a stage is read only after every wave's copies of it landed: group 0
+  //    waits for stage s before its first barrier of iteration s; group 1, which
+  //    reads it one barrier later, waits for stage s + 1 before its second
+  //    barrier of iteration s (the barrier after which group 0 reads s + 1), and
+  //    for stage 0 before its extra barrier;
+  //  * a buffer is refilled (stage s + kStages - 1 into the buffer of s - 1)
+  //    only after both groups' reads of it completed: each wave waits for its
+  //    operand reads (lgkmcnt 0) before the barrier that starts its MFMAs.
+  // Each accumulator sums its stages in the same order as a one-group loop.
+  {
+    const bool g1 = w >= 4;
+    if (g1) {
+      wait_vmcnt<(kStages - 2) * FPW>();
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_barrier" ::: "memory");
     }
+    for (int s = 0; s < S; ++s) {
+      wait_vmcnt<(kStages - 2) * FPW>();
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      const u32x4_t* st = lds + (s % kStages) * kStageFrags * 64;
+      u32x4_t af[8], bf[WT];
+#pragma unroll
+      for (int j = 0; j < WT; ++j) bf[j] = st[(kRB + wn * WT + j) * 64 + lane];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) af[i] = st[(wm * 8 + i) * 64 + lane];
+      __builtin_amdgcn_sched_barrier(0);
+      issue(min(s + kStages - 1, S - 1), (s + kStages - 1) % kStages);
+      __builtin_amdgcn_sched_barrier(0);
+      if (g1) wait_vmcnt<(kStages - 2) * FPW>();
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+#pragma unroll
+        for (int j = 0; j < WT; ++j) acc[i][j] = mfma16x16x32(af[i], bf[j], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+    if (!g1) asm volatile("s_barrier" ::: "memory");
   }
 
   // ---- epilogue: lane holds rows 4*(lane/16)+e of each row block, token lane%16 ----
