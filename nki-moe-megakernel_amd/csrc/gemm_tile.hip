@@ -44,6 +44,10 @@ constexpr int kRingBytes = kStages * kStageFrags * 1024;
 // then the block's output row indices
 constexpr int kStgLd = 132;
 constexpr int kStgBytes = kTileTok * kStgLd * 4 + kTileTok * 4;
+// the SwiGLU epilogue stages the whole h tile, [256 tokens][128 + 8 columns]
+// bf16 (the padding shifts each token row by 4 banks), then the row indices
+constexpr int kHsLd = 136;
+static_assert(kTileTok * kHsLd * 2 + kTileTok * 4 <= kStgBytes, "h staging fits the fp32 staging area");
 constexpr int kLdsBytes = kRingBytes > kStgBytes ? kRingBytes : kStgBytes;
 
 // s_waitcnt with only vmcnt = n (expcnt / lgkmcnt left at their maxima); gfx9
@@ -256,13 +260,26 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
   // ---- epilogue: lane holds rows 4*(lane/16)+e of each row block, token lane%16 ----
   const int q4 = (lane >> 4) * 4;
   if (EPI == EPI_SWIGLU_BF16) {
+    // The h tile goes out through LDS: the waves store their SwiGLU values as
+    // [token][128 h columns + 8] bf16, then 16 threads write each token's
+    // 256-byte row segment in 16-byte stores -- directly, a store instruction
+    // wrote 8 bytes into each of 16 scattered rows per lane group.
     const int I = a.N / 2;
     const uint16_t* bp = a.bias ? a.bias + (long long)expert * a.bias_group_stride : nullptr;
+    wait_vmcnt<0>();                     // the ring's last copies have landed
+    uint16_t* hs = reinterpret_cast<uint16_t*>(lds);
+    int* orow_s = reinterpret_cast<int*>(hs + kTileTok * kHsLd);
+    if (tid < kTileTok) {
+      const int tc = min(t0 + tid, count - 1);
+      orow_s[tid] = a.pair_out_row ? a.pair_out_row[base + tc] : base + tc;
+    }
+    __syncthreads();                     // every wave is past its last operand reads
 #pragma unroll
     for (int p = 0; p < 4; ++p) {
       const int nbg = nb0 + wm * 8 + 2 * p;           // gate row block (even), up = nbg + 1
-      if (nbg + 1 >= NB) continue;
+      if (nbg + 1 >= NB) continue;                    // h columns past I (never stored)
       const int n = (nbg >> 1) * 16 + q4;             // logical intermediate index
+      const int nl = (wm * 4 + p) * 16 + q4;          // its column in the tile's 128
       float gb[4] = {0.f, 0.f, 0.f, 0.f}, ub[4] = {0.f, 0.f, 0.f, 0.f};
       if (bp) {
 #pragma unroll
@@ -270,14 +287,23 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
       }
 #pragma unroll
       for (int j = 0; j < WT; ++j) {
-        const int tc = t0 + (wn * WT + j) * 16 + (lane & 15);
-        if (tc >= count) continue;
+        const int tl = (wn * WT + j) * 16 + (lane & 15);
         float o[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           o[e] = swiglu_value(a, acc[2 * p][j][e] + gb[e], acc[2 * p + 1][j][e] + ub[e]);
-        uint16_t* y = static_cast<uint16_t*>(a.y) + (long long)orow[j] * a.ldy + n;
-        *reinterpret_cast<uint2*>(y) = uint2{pack2bf(o[0], o[1]), pack2bf(o[2], o[3])};
+        *reinterpret_cast<uint2*>(hs + tl * kHsLd + nl) = uint2{pack2bf(o[0], o[1]), pack2bf(o[2], o[3])};
+      }
+    }
+    __syncthreads();
+    // N % 32 == 0, so I % 16 == 0: an 8-column piece is all below I or all past it
+    const int c8 = (tid & 15) * 8;
+    const int n = (nb0 >> 1) * 16 + c8;
+    if (n < I) {
+      for (int tl = tid >> 4; tl < kTileTok; tl += 32) {
+        if (t0 + tl >= count) break;
+        const u32x4_t v = *reinterpret_cast<const u32x4_t*>(hs + tl * kHsLd + c8);
+        *reinterpret_cast<u32x4_t*>(static_cast<uint16_t*>(a.y) + (long long)orow_s[tl] * a.ldy + n) = v;
       }
     }
   } else {   // EPI_SCALE_F32
@@ -370,6 +396,9 @@ int gemm_tile_kgrid(int N, int K, int T) {
 hipError_t gemm_tile_launch(const GemmArgs& a, int epi, int groups_max, long long total_rows,
                             hipStream_t s) {
   if (!gemm_tile_supported(a.N, a.K, epi) || groups_max <= 0 || total_rows <= 0)
+    return hipErrorInvalidValue;
+  // the SwiGLU epilogue writes h in 16-byte pieces
+  if (epi == EPI_SWIGLU_BF16 && ((a.ldy & 7) || (reinterpret_cast<uintptr_t>(a.y) & 15)))
     return hipErrorInvalidValue;
   // K slices: dense fp32 partials only, each slice's rows clear of the next's
   const int kg = a.kgrid > 1 ? a.kgrid : 1;
