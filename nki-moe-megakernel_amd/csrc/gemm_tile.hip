@@ -205,14 +205,24 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < WT; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int s = 0; s < kStages - 1; ++s) issue(min(s, S - 1), s);
+  // this wave's copies of a stage have landed once at most `after` stages
+  // issued later are outstanding (FPW copies each); after <= kStages - 2
+  static_assert(kStages >= 3 && kStages <= 5, "wait_landed covers 0 .. 3 later stages");
+  auto wait_landed = [&](int after) {
+    if (after >= 3) wait_vmcnt<3 * FPW>();
+    else if (after == 2) wait_vmcnt<2 * FPW>();
+    else if (after == 1) wait_vmcnt<FPW>();
+    else wait_vmcnt<0>();
+  };
+  for (int s = 0; s < kStages - 1 && s < S; ++s) issue(s, s);
   // Two wave groups run half a stage apart: waves 0-3 (group 0) and 4-7 (group
   // 1), one of each per SIMD.  Group 1 takes one barrier before the loop and
   // group 0 one after it, so between two barriers one group reads its operands
   // of a stage from LDS while the other runs the previous stage's MFMAs, and the
   // SIMD's matrix core has work in both halves.  Every wave executes the same
   // loop: wait for its copies of stage s, barrier, 12 operand reads, the copies
-  // of stage s + kStages - 1, barrier, 32 MFMAs.  Ordering:
+  // of stage s + kStages - 1 (none past the last stage: the waits count the
+  // stages actually issued after the awaited one), barrier, 32 MFMAs.  Ordering:
   //  * a stage is read only after every wave's copies of it landed: group 0
   //    waits for stage s before its first barrier of iteration s; group 1, which
   //    reads it one barrier later, waits for stage s + 1 before its second
@@ -225,12 +235,12 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
   {
     const bool g1 = w >= 4;
     if (g1) {
-      wait_vmcnt<(kStages - 2) * FPW>();
+      wait_landed(min(S - 1, kStages - 2));                  // stage 0
       __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_barrier" ::: "memory");
     }
     for (int s = 0; s < S; ++s) {
-      wait_vmcnt<(kStages - 2) * FPW>();
+      wait_landed(min(S - 1 - s, kStages - 2));              // stage s
       __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_barrier" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
@@ -241,9 +251,9 @@ __global__ void __launch_bounds__(512) gemm_tile_kernel(GemmArgs a) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) af[i] = st[(wm * 8 + i) * 64 + lane];
       __builtin_amdgcn_sched_barrier(0);
-      issue(min(s + kStages - 1, S - 1), (s + kStages - 1) % kStages);
+      if (s + kStages - 1 < S) issue(s + kStages - 1, (s + kStages - 1) % kStages);
       __builtin_amdgcn_sched_barrier(0);
-      if (g1) wait_vmcnt<(kStages - 2) * FPW>();
+      if (g1 && s + 1 < S) wait_landed(min(S - 2 - s, kStages - 2));   // stage s + 1
       __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
