@@ -11,8 +11,9 @@
 //   Outputs: expert index [T,K] (int32), top-k affinities [T,K] fp32, per-slot
 //   weights [T*K] (same values), and optionally the scattered / full
 //   affinities [T,E].
-// moe_route: single block; counting sort of the T*K (token, k) slots by expert
-//   into compact groups (live experts in ascending id order).
+// moe_route: single block of 1024 threads; counting sort of the T*K (token, k)
+//   slots by expert into compact groups (live experts in ascending id order;
+//   the slots within a group in any order -- every consumer indexes by slot).
 // moe_finalize: out[t] = bf16(sum_k y[t*K + k]) (fp32 sum in k order), then the
 //   bf16 residual add.
 #include "common.h"
@@ -74,48 +75,75 @@ moe_route_kernel(const int* __restrict__ idx, int T, int K, int E, int* __restri
                  int* __restrict__ grp_expert, int* __restrict__ grp_count,
                  int* __restrict__ grp_offset, int* __restrict__ pair_token,
                  int* __restrict__ pair_slot) {
-  __shared__ int cnt[kMaxE], off[kMaxE], gid[kMaxE], cursor[kMaxE];
-  __shared__ int scan[1024];
-  const int tid = threadIdx.x;
+  __shared__ int cnt[kMaxE], off[kMaxE], cursor[kMaxE];
+  __shared__ int wtot[16];
+  // Each pass takes CH slots per thread whose expert indices are all loaded
+  // before any is used (one memory round trip per pass, not per slot).
+  constexpr int CH = 16;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nt = (int)blockDim.x;
   const int TK = T * K;
-  for (int e = tid; e < E; e += blockDim.x) { cnt[e] = 0; cursor[e] = 0; }
+  for (int e = tid; e < E; e += nt) { cnt[e] = 0; cursor[e] = 0; }
   __syncthreads();
-  for (int p = tid; p < TK; p += blockDim.x) {
-    const int e = idx[p];
-    if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+  for (int p0 = 0; p0 < TK; p0 += CH * nt) {
+    int ev[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int p = p0 + u * nt + tid;
+      ev[u] = p < TK ? idx[p] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u)
+      if (ev[u] >= 0 && ev[u] < E) atomicAdd(&cnt[ev[u]], 1);
   }
   __syncthreads();
-  // exclusive scans over experts: pair offsets and live-group ids (E <= blockDim)
-  int c = (tid < E) ? cnt[tid] : 0;
-  int live = c > 0 ? 1 : 0;
-  scan[tid] = c | (live << 20);        // pack (count, live) -- counts < 2^20
-  __syncthreads();
-  for (int o = 1; o < (int)blockDim.x; o <<= 1) {
-    const int v = (tid >= o) ? scan[tid - o] : 0;
-    __syncthreads();
-    scan[tid] += v;
-    __syncthreads();
+  // exclusive scans over the experts (E <= 512, the first 8 waves) of the pair
+  // counts and the live-group ids, packed as count | live << 20 (counts < 2^20):
+  // a wave scan, then the totals of the waves before
+  const int c = tid < E ? cnt[tid] : 0;
+  const int live = c > 0 ? 1 : 0;
+  int x = c | (live << 20);
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(x, o, 64);
+    if (lane >= o) x += y;
   }
-  const int incl = scan[tid];
+  if (lane == 63) wtot[w] = x;
+  __syncthreads();
+  int before = 0, total = 0;
+  for (int q = 0; q < nt / 64; ++q) {
+    const int v = wtot[q];
+    if (q < w) before += v;
+    total += v;
+  }
+  const int incl = before + x;
   if (tid < E) {
     const int excl_cnt = (incl & 0xfffff) - c;
     const int excl_live = (incl >> 20) - live;
     off[tid] = excl_cnt;
-    gid[tid] = excl_live;
     if (live) {
       grp_expert[excl_live] = tid;
       grp_count[excl_live] = c;
       grp_offset[excl_live] = excl_cnt;
     }
   }
-  if (tid == blockDim.x - 1) *n_groups = incl >> 20;
+  if (tid == 0) *n_groups = total >> 20;
   __syncthreads();
-  for (int p = tid; p < TK; p += blockDim.x) {
-    const int e = idx[p];
-    if (e < 0 || e >= E) continue;
-    const int q = off[e] + atomicAdd(&cursor[e], 1);
-    pair_token[q] = p / K;
-    pair_slot[q] = p;
+  for (int p0 = 0; p0 < TK; p0 += CH * nt) {
+    int ev[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int p = p0 + u * nt + tid;
+      ev[u] = p < TK ? idx[p] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int e = ev[u];
+      if (e < 0 || e >= E) continue;
+      const int p = p0 + u * nt + tid;
+      const int q = off[e] + atomicAdd(&cursor[e], 1);
+      pair_token[q] = p / K;
+      pair_slot[q] = p;
+    }
   }
 }
 
