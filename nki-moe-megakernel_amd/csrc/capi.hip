@@ -250,6 +250,7 @@ int router_stage(const void* x, bool xf32, int H, const void* w_packed, float* p
 
 struct MoeWs {
   int *n_groups, *grp_expert, *grp_count, *grp_offset, *pair_token, *pair_slot, *idx;
+  int* route_off;               // per-chunk slot offsets of the split routing
   float *slot_w, *ybuf;
   uint16_t* hbuf;
   uint8_t *xq, *xs, *hq, *hs;   // MXFP8 codes / scales of the hidden rows and of hbuf
@@ -266,6 +267,7 @@ MoeWs carve_moe(Carver& c, int T, int H, int E, int I, int K) {
   w.pair_token = c.take<int>((size_t)T * K);
   w.pair_slot = c.take<int>((size_t)T * K);
   w.idx = c.take<int>((size_t)T * K);
+  w.route_off = c.take<int>(kRouteChunkCounts);
   w.slot_w = c.take<float>((size_t)T * K);
   w.hbuf = c.take<uint16_t>((size_t)T * K * I);
   w.ybuf = c.take<float>((size_t)T * K * H);
@@ -309,7 +311,7 @@ int moe_core(const uint16_t* hidden, const void* gate_up, const void* down, cons
   if (fused_flags && !sel) return MKD_ERR_INVALID;
   if (idx)  // otherwise the router stage already built the expert groups
     MKD_TRY(moe_route_launch(idx, T, K, E, w.n_groups, w.grp_expert, w.grp_count, w.grp_offset,
-                             w.pair_token, w.pair_slot, s), "moe_route");
+                             w.pair_token, w.pair_slot, s, w.route_off), "moe_route");
   const int gmax = E < T * K ? E : T * K;
   if (wfmt == MKD_FP8_E4M3) {
     // e4m3 experts (FP8 ROW / STATIC): bf16 activations, per-column dequantisation

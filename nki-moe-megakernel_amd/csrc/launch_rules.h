@@ -71,4 +71,18 @@ MKD_RULE int prefill_pair_rule(long long total, int cus, int heads_per_block) {
   return (heads_per_block == 8 && cus > 0 && total > cus && total <= 2LL * cus) ? cus : 0;
 }
 
+// Split routing of tk slots over e experts: slots per placing block (a multiple
+// of 256, at least min_chunk), such that the chunks number at most max_chunks
+// and chunks x e counts fit max_counts; 0 when one block places them all (tk
+// <= min_chunk, or fewer than two chunks fit).
+MKD_RULE int route_chunk_rule(int tk, int e, int min_chunk, int max_chunks, int max_counts) {
+  if (tk <= min_chunk || e <= 0) return 0;
+  const int by_counts = max_counts / e;
+  const int max_nc = max_chunks < by_counts ? max_chunks : by_counts;
+  if (max_nc < 2) return 0;
+  int cs = (tk + max_nc - 1) / max_nc;
+  cs = (cs + 255) / 256 * 256;
+  return cs > min_chunk ? cs : min_chunk;
+}
+
 }  // namespace mkd

@@ -527,9 +527,16 @@ int moe_fused_flag_words(int T, int K, int E, int I);
 hipError_t moe_fused_launch(MoeFusedArgs f, int groups_max, hipStream_t s);
 bool gemm_sel_supported(int T, int K, int E, int nsplit);
 hipError_t gemm_sel_launch(const GemmArgs& a, const RouterArgs& r, int groups_max, hipStream_t s);
+// Expert groups of T*K routed slots.  With chunk_off (kRouteChunkCounts ints of
+// workspace) and more than kRouteChunk slots, the slots are placed by one block
+// per chunk of slots (moe_route_scatter_kernel) instead of by the one block.
+constexpr int kRouteChunk = 2048;          // slots per placing block, at least
+constexpr int kRouteMaxChunks = 64;
+constexpr int kRouteChunkCounts = 8192;    // per-chunk counts: chunks x E <= this
+int moe_route_chunk(int TK, int E);        // slots per chunk, 0 = the one-block form
 hipError_t moe_route_launch(const int* idx, int T, int K, int E, int* n_groups, int* grp_expert,
                             int* grp_count, int* grp_offset, int* pair_token, int* pair_slot,
-                            hipStream_t s);
+                            hipStream_t s, int* chunk_off = nullptr);
 hipError_t moe_finalize_launch(const float* ybuf, int T, int K, int H, const uint16_t* resid,
                                uint16_t* out, float* out_f32, hipStream_t s);
 

@@ -19,6 +19,7 @@
 #include "common.h"
 #include "mkd_internal.h"
 #include "router_select.h"
+#include "launch_rules.h"
 
 namespace mkd {
 
@@ -74,15 +75,20 @@ __global__ void __launch_bounds__(1024)
 moe_route_kernel(const int* __restrict__ idx, int T, int K, int E, int* __restrict__ n_groups,
                  int* __restrict__ grp_expert, int* __restrict__ grp_count,
                  int* __restrict__ grp_offset, int* __restrict__ pair_token,
-                 int* __restrict__ pair_slot) {
+                 int* __restrict__ pair_slot, int cs, int nc, int* __restrict__ chunk_off) {
   __shared__ int cnt[kMaxE], off[kMaxE], cursor[kMaxE];
   __shared__ int wtot[16];
+  // split form (chunk_off set): per-chunk counts [nc][E] of the cs-slot chunks
+  __shared__ int cntc[kRouteChunkCounts];
+  const bool split = chunk_off != nullptr;
   // Each pass takes CH slots per thread whose expert indices are all loaded
   // before any is used (one memory round trip per pass, not per slot).
   constexpr int CH = 16;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, nt = (int)blockDim.x;
   const int TK = T * K;
   for (int e = tid; e < E; e += nt) { cnt[e] = 0; cursor[e] = 0; }
+  if (split)
+    for (int i = tid; i < nc * E; i += nt) cntc[i] = 0;
   __syncthreads();
   for (int p0 = 0; p0 < TK; p0 += CH * nt) {
     int ev[CH];
@@ -92,10 +98,21 @@ moe_route_kernel(const int* __restrict__ idx, int T, int K, int E, int* __restri
       ev[u] = p < TK ? idx[p] : -1;
     }
 #pragma unroll
-    for (int u = 0; u < CH; ++u)
-      if (ev[u] >= 0 && ev[u] < E) atomicAdd(&cnt[ev[u]], 1);
+    for (int u = 0; u < CH; ++u) {
+      if (ev[u] < 0 || ev[u] >= E) continue;
+      if (split) atomicAdd(&cntc[((p0 + u * nt + tid) / cs) * E + ev[u]], 1);
+      else atomicAdd(&cnt[ev[u]], 1);
+    }
   }
   __syncthreads();
+  if (split) {   // the experts' totals, chunk by chunk in order
+    for (int e = tid; e < E; e += nt) {
+      int t = 0;
+      for (int c = 0; c < nc; ++c) t += cntc[c * E + e];
+      cnt[e] = t;
+    }
+    __syncthreads();
+  }
   // exclusive scans over the experts (E <= 512, the first 8 waves) of the pair
   // counts and the live-group ids, packed as count | live << 20 (counts < 2^20):
   // a wave scan, then the totals of the waves before
@@ -127,6 +144,16 @@ moe_route_kernel(const int* __restrict__ idx, int T, int K, int E, int* __restri
     }
   }
   if (tid == 0) *n_groups = total >> 20;
+  if (split) {   // chunk c's slots of expert e start at its group offset plus the earlier chunks' counts
+    if (tid < E) {
+      int run = (incl & 0xfffff) - c;
+      for (int q = 0; q < nc; ++q) {
+        chunk_off[q * E + tid] = run;
+        run += cntc[q * E + tid];
+      }
+    }
+    return;      // moe_route_scatter_kernel places the slots
+  }
   __syncthreads();
   for (int p0 = 0; p0 < TK; p0 += CH * nt) {
     int ev[CH];
@@ -141,6 +168,40 @@ moe_route_kernel(const int* __restrict__ idx, int T, int K, int E, int* __restri
       if (e < 0 || e >= E) continue;
       const int p = p0 + u * nt + tid;
       const int q = off[e] + atomicAdd(&cursor[e], 1);
+      pair_token[q] = p / K;
+      pair_slot[q] = p;
+    }
+  }
+}
+
+// Split routing, second half: block c places the slots of chunk c (cs slots
+// from c * cs) at chunk_off[c][e] onwards, ranked by LDS atomics.
+__global__ void __launch_bounds__(256)
+moe_route_scatter_kernel(const int* __restrict__ idx, int TK, int K, int E, int cs,
+                         const int* __restrict__ chunk_off, int* __restrict__ pair_token,
+                         int* __restrict__ pair_slot) {
+  __shared__ int base_s[kMaxE], cursor[kMaxE];
+  constexpr int CH = 8;
+  const int tid = threadIdx.x, nt = (int)blockDim.x;
+  const int c = blockIdx.x, p_lo = c * cs, p_hi = min(TK, p_lo + cs);
+  for (int e = tid; e < E; e += nt) {
+    base_s[e] = chunk_off[c * E + e];
+    cursor[e] = 0;
+  }
+  __syncthreads();
+  for (int p0 = p_lo; p0 < p_hi; p0 += CH * nt) {
+    int ev[CH];
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int p = p0 + u * nt + tid;
+      ev[u] = p < p_hi ? idx[p] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int e = ev[u];
+      if (e < 0 || e >= E) continue;
+      const int p = p0 + u * nt + tid;
+      const int q = base_s[e] + atomicAdd(&cursor[e], 1);
       pair_token[q] = p / K;
       pair_slot[q] = p;
     }
@@ -350,12 +411,27 @@ hipError_t router_select_launch(const RouterArgs& a, hipStream_t s) {
   return hipGetLastError();
 }
 
+// Chunking of the split form: chunks of at least kRouteChunk slots, at most
+// kRouteMaxChunks of them and nc * E counts within the LDS table; 0 = one block.
+int moe_route_chunk(int TK, int E) {
+  if (E > kMaxE) return 0;
+  return route_chunk_rule(TK, E, kRouteChunk, kRouteMaxChunks, kRouteChunkCounts);
+}
+
 hipError_t moe_route_launch(const int* idx, int T, int K, int E, int* n_groups, int* grp_expert,
                             int* grp_count, int* grp_offset, int* pair_token, int* pair_slot,
-                            hipStream_t s) {
-  if (E > kMaxE) return hipErrorInvalidValue;
+                            hipStream_t s, int* chunk_off) {
+  if (E > kMaxE || T < 0 || K < 1) return hipErrorInvalidValue;
+  const int TK = T * K;
+  const int cs = chunk_off ? moe_route_chunk(TK, E) : 0;
+  const int nc = cs ? (TK + cs - 1) / cs : 0;
   hipLaunchKernelGGL(moe_route_kernel, dim3(1), dim3(1024), 0, s, idx, T, K, E, n_groups,
-                     grp_expert, grp_count, grp_offset, pair_token, pair_slot);
+                     grp_expert, grp_count, grp_offset, pair_token, pair_slot, cs ? cs : 1, nc,
+                     cs ? chunk_off : nullptr);
+  if (hipError_t e = hipGetLastError()) return e;
+  if (cs)
+    hipLaunchKernelGGL(moe_route_scatter_kernel, dim3(nc), dim3(256), 0, s, idx, TK, K, E, cs,
+                       chunk_off, pair_token, pair_slot);
   return hipGetLastError();
 }
 

@@ -20,7 +20,9 @@
   projections;
 * the prefill attention's work units: a bijection of [0, total) for every grid
   size and CU count, and where paired, the two blocks of a CU (L, L + CUs) take
-  units summing to total - 1 (complementary tile lengths).
+  units summing to total - 1 (complementary tile lengths);
+* the split routing's chunks: multiples of 256 of at least the minimum, every
+  slot covered by at most the chunk limit, chunk counts within the table.
 """
 import os
 import shutil
@@ -151,6 +153,28 @@ int main() {
       prefill_pair_rule(256, 256, 8) != 0 || prefill_pair_rule(512, 256, 4) != 0) {
     printf("pair known answers\n"); return 1;
   }
+  // 6. split routing chunks: multiples of 256, >= the minimum, covering every
+  // slot in at most max_chunks chunks whose counts fit the table; one block
+  // (0) at or below the minimum
+  const int es[] = {1, 8, 32, 128, 256, 512};
+  for (int e : es)
+    for (int tk = 1; tk <= 600000; tk = tk * 3 / 2 + 7) {
+      const int cs = route_chunk_rule(tk, e, 2048, 64, 8192);
+      const int max_nc = 64 < 8192 / e ? 64 : 8192 / e;
+      if (tk <= 2048 || max_nc < 2) {
+        if (cs != 0) { printf("route one block tk=%d e=%d cs=%d\n", tk, e, cs); return 1; }
+        continue;
+      }
+      const long long nc = (tk + (long long)cs - 1) / cs;
+      if (cs < 2048 || cs % 256 || nc > max_nc || nc * e > 8192 || nc * cs < tk) {
+        printf("route chunk tk=%d e=%d cs=%d nc=%lld\n", tk, e, cs, nc); return 1;
+      }
+    }
+  // 16384 tokens x top-8 over 128 experts: 64 chunks of 2048; 2048 x 8: 8 chunks
+  if (route_chunk_rule(131072, 128, 2048, 64, 8192) != 2048 || route_chunk_rule(16384, 128, 2048, 64, 8192) != 2048 ||
+      route_chunk_rule(512, 128, 2048, 64, 8192) != 0 || route_chunk_rule(131072, 512, 2048, 64, 8192) != 8192) {
+    printf("route known answers\n"); return 1;
+  }
   printf("ok %lld\n", taken);
   return 0;
 }
@@ -169,7 +193,7 @@ def rules_binary(tmp_path_factory):
     return str(exe)
 
 
-def test_poll_word_split_deal_kgrid_and_unit_rules(rules_binary):
+def test_poll_word_split_deal_kgrid_unit_and_route_rules(rules_binary):
     r = subprocess.run([rules_binary], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert r.stdout.startswith("ok ")
