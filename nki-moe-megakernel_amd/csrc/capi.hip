@@ -225,6 +225,10 @@ int router_stage(const void* x, bool xf32, int H, const void* w_packed, float* p
   // of K-split partials when the split matches
   if (gemm_mid_kgrid(r.E, H, r.T, 16) == kg) {
     MKD_TRY(gemm_mid_launch(a, kg, xf32, s), "router gemm (mid)");
+  } else if (r.T > 128 && gemm_mid_chunked_ok(H, kg)) {
+    // a prefill pass: the same, over chunks of 128 tokens, each chunk's activation
+    // slice staged once per block instead of re-read for every 16-row block
+    MKD_TRY(gemm_mid_launch(a, kg, xf32, s), "router gemm (mid, token chunks)");
   } else if (int rc = dense_gemm(a, EPI_F32, xf32, s)) {
     return rc;
   }

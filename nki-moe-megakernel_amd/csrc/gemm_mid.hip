@@ -37,6 +37,14 @@ constexpr int batch_of(int n, int cap) {
 template <int TT, int RBW, int NF, bool XF32>
 __global__ void __launch_bounds__(256) gemm_mid_kernel(GemmArgs a) {
   extern __shared__ __attribute__((aligned(16))) u32x4_t xs[];    // [hi/lo][TT][NF][64]
+  // grid z: chunks of 128 tokens (more than 128 tokens), each a call of its own
+  // on rows z * 128 .. of x and of every partial
+  if (gridDim.z > 1) {
+    const int t0 = (int)blockIdx.z * 128;
+    a.x = static_cast<const char*>(a.x) + (long long)t0 * a.ldx * (XF32 ? 4 : 2);
+    a.y = static_cast<char*>(a.y) + (long long)t0 * a.ldy * 4;
+    a.T = min(a.T - t0, 128);
+  }
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int KB = a.K / 32;
@@ -311,14 +319,20 @@ static hipError_t mid_go(const GemmArgs& a, dim3 grid, size_t lds, hipStream_t s
   return timed_launch(gemm_mid_kernel<TT, RBW, NF, XF32>, grid, dim3(256), lds, s, a);
 }
 
+bool gemm_mid_chunked_ok(int K, int kgrid) {
+  return K > 0 && K % 32 == 0 && kgrid >= 1 && (K / 32) % kgrid == 0 && mid_nf_ok(K / 32 / kgrid);
+}
+
 hipError_t gemm_mid_launch(GemmArgs a, int kgrid, bool xf32, hipStream_t s) {
   const int KB = a.K / 32;
-  if (kgrid < 1 || KB % kgrid || !mid_nf_ok(KB / kgrid) || a.T < 1 || a.T > 128 || a.grp_expert)
+  if (kgrid < 1 || KB % kgrid || !mid_nf_ok(KB / kgrid) || a.T < 1 || a.grp_expert)
     return hipErrorInvalidValue;
+  const int chunks = (a.T + 127) / 128;     // > 1: token chunks of 128 over grid z
+  if (chunks > 65535) return hipErrorInvalidValue;
   const int nf = KB / kgrid, rbw = mid_rbw(a.N);
-  const int TT = (a.T + 15) / 16;
+  const int TT = chunks > 1 ? 8 : (a.T + 15) / 16;
   const int groups = ((a.N + 15) / 16 + kMidWaves * rbw - 1) / (kMidWaves * rbw);
-  const dim3 grid(groups, kgrid);
+  const dim3 grid(groups, kgrid, chunks);
   // token tiles rounded up to 2 / 4 / 8 (fewer instantiations); the activation
   // slice takes tt * nf KiB of LDS (twice that for fp32 activations)
   const int tt = TT <= 2 ? 2 : (TT <= 4 ? 4 : 8);

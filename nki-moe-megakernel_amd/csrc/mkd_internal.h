@@ -99,6 +99,8 @@ int choose_kw_mx(int K_pad);
 // gemm_mid.hip: dense projection of 17..128 tokens, activation slices staged in
 // LDS, fp32 split-K partials (kgrid from gemm_mid_kgrid; 0 = shape not covered)
 int gemm_mid_kgrid(int N, int K, int T, int max_parts = 8);
+// K split of gemm_mid_launch valid for any token count (more than 128: chunks of 128)
+bool gemm_mid_chunked_ok(int K, int kgrid);
 hipError_t gemm_mid_launch(GemmArgs a, int kgrid, bool xf32, hipStream_t s);
 // the vocabulary projection at 17..128 tokens: whole-K blocks of 128 rows
 // looping over K slices staged in LDS (fp32 rows, no partials)
