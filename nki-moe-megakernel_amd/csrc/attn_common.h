@@ -13,14 +13,15 @@ namespace mkd {
 // holds elements l and l + D/2 -- the pair that rotate-half RoPE mixes -- so
 // the rotation stays inside the lane; lanes >= D/2 (D = 64) hold zeros.  Split
 // into load and finish so a wave can issue the loads of all its heads first.
-template <int D>
+template <int D, int MP = 8>
 struct HeadPrep {
   static constexpr int HD = D / 2;
   // raw loads (converted in finish, so that a wave's loads for all its heads
   // are in flight together: a conversion inside a conditional would make the
   // compiler wait for each load where it is issued).  fp32 projections may come
-  // as kMaxQkvParts split-K partials (a.qkv_nparts), summed in order.
-  static constexpr int kMaxQkvParts = 8;
+  // as up to kMaxQkvParts = MP split-K partials (a.qkv_nparts), summed in order
+  // (MP = 1: the caller has established a.qkv_nparts <= 1).
+  static constexpr int kMaxQkvParts = MP;
   uint32_t xr[2], nr[2];   // nr: the aligned dword holding the bf16 norm weight of element i
   float xp[2][kMaxQkvParts];
   int np;

@@ -62,11 +62,11 @@ MKD_DEV f32x4_t mfma16x16x16(uint2 a, uint2 b, f32x4_t c) {
 // The GQA + 2 heads of kv group g of sequence b, prepared (attention_block_tkg.py:
 // 915-1138) by the 4 waves of a block: wave w takes heads w, w+4, ... of
 // [q heads of g | k of g | v of g]; all loads first, then the math.
-template <int D, int GQA>
+template <int D, int GQA, int MP = 8>
 MKD_DEV void prep_heads(const AttnArgs& a, int rope_mode, int b, int g, int w, int lane,
                         uint16_t (*q_dst)[D], uint16_t* k_dst, uint16_t* v_dst) {
   constexpr int NR = (GQA + 2 + 3) / 4;
-  HeadPrep<D> hp[NR];
+  HeadPrep<D, MP> hp[NR];
 #pragma unroll
   for (int r = 0; r < NR; ++r) {
     const int h = w + 4 * r;
@@ -88,13 +88,27 @@ MKD_DEV void prep_heads(const AttnArgs& a, int rope_mode, int b, int g, int w, i
 
 // Large grids: the heads of (b, g) are prepared once here, block (g, b), into
 // a.prep [B, nkv, gqa + 2, d], instead of in every one of its chunk blocks.
-template <int D, int GQA>
-__global__ void __launch_bounds__(256) attn_prep_kernel(AttnArgs a, int rope_mode) {
+// MP = 1 (the projection comes whole, a.qkv_nparts <= 1): without the partial
+// sums' registers the kernel fits 8 waves per SIMD -- a prefill pass's grid of
+// (kv heads x tokens) small blocks is a chain of load round trips, and twice the
+// resident blocks halve their number.
+template <int D, int GQA, int MP = 8>
+__global__ void __launch_bounds__(256, MP == 1 ? 8 : 1) attn_prep_kernel(AttnArgs a, int rope_mode) {
   const int g = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   uint16_t* dst = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
-  prep_heads<D, GQA>(a, rope_mode, b, g, w, lane, reinterpret_cast<uint16_t(*)[D]>(dst),
-                     dst + GQA * D, dst + (GQA + 1) * D);
+  prep_heads<D, GQA, MP>(a, rope_mode, b, g, w, lane, reinterpret_cast<uint16_t(*)[D]>(dst),
+                         dst + GQA * D, dst + (GQA + 1) * D);
+}
+
+// the one-part form wherever the projection comes whole (bf16, or fp32 without
+// K-slice partials: HeadPrep then sums exactly one part)
+template <int D, int GQA>
+static void launch_prep(const AttnArgs& a, int rope_mode, hipStream_t s) {
+  if (!a.qkv || a.qkv_nparts <= 1)
+    hipLaunchKernelGGL((attn_prep_kernel<D, GQA, 1>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode);
+  else
+    hipLaunchKernelGGL((attn_prep_kernel<D, GQA, 8>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode);
 }
 
 // Prefill (tokens of one sequence in one step): block (g, b) writes token b's
@@ -1486,7 +1500,7 @@ static hipError_t launch_tpw(const AttnArgs& a, int rope_mode, hipStream_t s) {
   if (a.prefill && (!a.prep || !a.update_cache)) return hipErrorInvalidValue;
   if (a.s_tkg > 1 && (!a.prep || a.prefill || a.window > 0 || a.B % a.s_tkg)) return hipErrorInvalidValue;
   if (a.prep) {
-    hipLaunchKernelGGL((attn_prep_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode);
+    launch_prep<D, GQA>(a, rope_mode, s);
     if (hipError_t e = hipGetLastError()) return e;
   }
   if (a.prefill) {
@@ -1530,8 +1544,7 @@ hipError_t attn_combine_launch(const AttnArgs& a, hipStream_t s) {
 hipError_t attn_prep_launch(const AttnArgs& a, int rope_mode, hipStream_t s) {
   if (!a.prep) return hipErrorInvalidValue;
   const int gqa = a.nq / a.nkv;
-#define MKD_PREP(D, G) \
-  hipLaunchKernelGGL((attn_prep_kernel<D, G>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode)
+#define MKD_PREP(D, G) launch_prep<D, G>(a, rope_mode, s)
   if (a.d == 128) {
     switch (gqa) {
       case 1: MKD_PREP(128, 1); break;
@@ -1559,7 +1572,7 @@ hipError_t attn_prep_launch(const AttnArgs& a, int rope_mode, hipStream_t s) {
 
 template <int D, int GQA>
 static hipError_t launch_prep_write(const AttnArgs& a, int rope_mode, hipStream_t s) {
-  hipLaunchKernelGGL((attn_prep_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode);
+  launch_prep<D, GQA>(a, rope_mode, s);
   if (hipError_t e = hipGetLastError()) return e;
   hipLaunchKernelGGL((attn_kv_write_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(D), 0, s, a);
   return hipGetLastError();
