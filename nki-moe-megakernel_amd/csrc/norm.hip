@@ -25,16 +25,20 @@ constexpr int kNormThreads = 256;
 constexpr int kNormMaxVec = 4;  // 4 x 8 elements x 256 threads = 8192
 constexpr int kNormMaxDK = 8;   // partial rows summed per element (experts / split-K)
 
+// VEC slices of 2048 elements per row (1, 2 or 4: the row's span, H or the MX
+// padding past it); one slice keeps the kernel near 60 VGPRs, so a prefill
+// pass's one-block-per-row grid is resident in one round
+template <int VEC>
 __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(NormArgs a) {
   __shared__ float red[16];
   const int row = blockIdx.x;
   const int tid = threadIdx.x;
   const int H = a.H;
-  float v[kNormMaxVec][8];
-  u32x4_t gp[kNormMaxVec];
+  float v[VEC][8];
+  u32x4_t gp[VEC];
   float ss = 0.f;
 #pragma unroll
-  for (int c = 0; c < kNormMaxVec; ++c) {
+  for (int c = 0; c < VEC; ++c) {
     const int i = (c * kNormThreads + tid) * 8;
     if (i < H) {
       if (a.gamma) gp[c] = ld16(a.gamma + i);
@@ -87,7 +91,7 @@ __global__ void __launch_bounds__(kNormThreads) rmsnorm_kernel(NormArgs a) {
   ss = block_sum(ss, red);
   const float rinv = 1.0f / sqrtf(ss * a.inv_h + a.eps);
 #pragma unroll
-  for (int c = 0; c < kNormMaxVec; ++c) {
+  for (int c = 0; c < VEC; ++c) {
     const int i = (c * kNormThreads + tid) * 8;
     if (i < H) {
       float y[8];
@@ -144,7 +148,11 @@ hipError_t norm_launch(NormArgs a, hipStream_t s) {
                      a.mx_kpad > kNormThreads * 8 * kNormMaxVec))
     return hipErrorInvalidValue;
   a.inv_h = 1.0f / (float)a.hidden_actual;
-  hipLaunchKernelGGL(rmsnorm_kernel, dim3(a.rows), dim3(kNormThreads), 0, s, a);
+  const int span = a.mx_codes && a.mx_kpad > a.H ? a.mx_kpad : a.H;
+  constexpr int kSlice = kNormThreads * 8;
+  if (span <= kSlice) hipLaunchKernelGGL(rmsnorm_kernel<1>, dim3(a.rows), dim3(kNormThreads), 0, s, a);
+  else if (span <= 2 * kSlice) hipLaunchKernelGGL(rmsnorm_kernel<2>, dim3(a.rows), dim3(kNormThreads), 0, s, a);
+  else hipLaunchKernelGGL(rmsnorm_kernel<kNormMaxVec>, dim3(a.rows), dim3(kNormThreads), 0, s, a);
   return hipGetLastError();
 }
 
