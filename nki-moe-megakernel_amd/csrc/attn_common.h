@@ -91,7 +91,10 @@ struct HeadPrep {
       }
     }
   }
-  MKD_DEV void finish(const AttnArgs& a, int rope_mode, int kind, uint16_t* dst, int lane) {
+  // dst2 (optional): a second copy of the prepared row (a prefill pass's KV
+  // cache row, stored here rather than by a launch of its own)
+  MKD_DEV void finish(const AttnArgs& a, int rope_mode, int kind, uint16_t* dst, int lane,
+                      uint16_t* dst2 = nullptr) {
     convert(rope_mode, kind, lane);
 #pragma unroll
     for (int e = 0; e < 2; ++e)
@@ -129,8 +132,13 @@ struct HeadPrep {
       }
     }
     if (lane < HD) {
-      dst[lane] = (uint16_t)f2bf(x[0]);
-      dst[lane + HD] = (uint16_t)f2bf(x[1]);
+      const uint16_t o0 = (uint16_t)f2bf(x[0]), o1 = (uint16_t)f2bf(x[1]);
+      dst[lane] = o0;
+      dst[lane + HD] = o1;
+      if (dst2) {
+        dst2[lane] = o0;
+        dst2[lane + HD] = o1;
+      }
     }
   }
 };

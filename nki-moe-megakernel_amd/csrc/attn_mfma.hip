@@ -64,7 +64,8 @@ MKD_DEV f32x4_t mfma16x16x16(uint2 a, uint2 b, f32x4_t c) {
 // [q heads of g | k of g | v of g]; all loads first, then the math.
 template <int D, int GQA, int MP = 8>
 MKD_DEV void prep_heads(const AttnArgs& a, int rope_mode, int b, int g, int w, int lane,
-                        uint16_t (*q_dst)[D], uint16_t* k_dst, uint16_t* v_dst) {
+                        uint16_t (*q_dst)[D], uint16_t* k_dst, uint16_t* v_dst,
+                        uint16_t* k_dst2 = nullptr, uint16_t* v_dst2 = nullptr) {
   constexpr int NR = (GQA + 2 + 3) / 4;
   HeadPrep<D, MP> hp[NR];
 #pragma unroll
@@ -81,7 +82,8 @@ MKD_DEV void prep_heads(const AttnArgs& a, int rope_mode, int b, int g, int w, i
     const int h = w + 4 * r;
     if (h < GQA + 2) {
       const int kind = h < GQA ? 0 : h - GQA + 1;
-      hp[r].finish(a, rope_mode, kind, h < GQA ? q_dst[h] : (kind == 1 ? k_dst : v_dst), lane);
+      hp[r].finish(a, rope_mode, kind, h < GQA ? q_dst[h] : (kind == 1 ? k_dst : v_dst), lane,
+                   kind == 1 ? k_dst2 : (kind == 2 ? v_dst2 : nullptr));
     }
   }
 }
@@ -92,38 +94,37 @@ MKD_DEV void prep_heads(const AttnArgs& a, int rope_mode, int b, int g, int w, i
 // sums' registers the kernel fits 8 waves per SIMD -- a prefill pass's grid of
 // (kv heads x tokens) small blocks is a chain of load round trips, and twice the
 // resident blocks halve their number.
+// kv_write (a prefill pass): token b's prepared k / v rows of kv head g also go
+// to their cache row, before any attention block reads it (the combine
+// kernel later stores the same values again).
 template <int D, int GQA, int MP = 8>
-__global__ void __launch_bounds__(256, MP == 1 ? 8 : 1) attn_prep_kernel(AttnArgs a, int rope_mode) {
+__global__ void __launch_bounds__(256, MP == 1 ? 8 : 1) attn_prep_kernel(AttnArgs a, int rope_mode, int kv_write) {
   const int g = blockIdx.x, b = blockIdx.y;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   uint16_t* dst = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
+  uint16_t *k2 = nullptr, *v2 = nullptr;
+  if (kv_write) {
+    const long long row = kv_write_row(a, b);
+    if (row >= 0) {
+      const long long off = a.block_table ? (row * a.nkv + g) * D
+                                          : seq_of(a, b) * a.cache_b_stride + g * a.cache_h_stride + row * D;
+      k2 = a.k_cache + off;
+      v2 = a.v_cache + off;
+    }
+  }
   prep_heads<D, GQA, MP>(a, rope_mode, b, g, w, lane, reinterpret_cast<uint16_t(*)[D]>(dst),
-                         dst + GQA * D, dst + (GQA + 1) * D);
+                         dst + GQA * D, dst + (GQA + 1) * D, k2, v2);
 }
 
 // the one-part form wherever the projection comes whole (bf16, or fp32 without
 // K-slice partials: HeadPrep then sums exactly one part)
 template <int D, int GQA>
-static void launch_prep(const AttnArgs& a, int rope_mode, hipStream_t s) {
+static void launch_prep(const AttnArgs& a, int rope_mode, hipStream_t s, bool kv_write = false) {
+  const int kw = kv_write ? 1 : 0;
   if (!a.qkv || a.qkv_nparts <= 1)
-    hipLaunchKernelGGL((attn_prep_kernel<D, GQA, 1>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode);
+    hipLaunchKernelGGL((attn_prep_kernel<D, GQA, 1>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode, kw);
   else
-    hipLaunchKernelGGL((attn_prep_kernel<D, GQA, 8>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode);
-}
-
-// Prefill (tokens of one sequence in one step): block (g, b) writes token b's
-// prepared k / v rows of kv head g to the cache before any attention block
-// reads it; the combine kernel later stores the same values again.
-template <int D, int GQA>
-__global__ void __launch_bounds__(D) attn_kv_write_kernel(AttnArgs a) {
-  const int g = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
-  const long long row = kv_write_row(a, b);
-  if (row < 0) return;
-  const uint16_t* src = a.prep + ((long long)b * a.nkv + g) * (GQA + 2) * D;
-  const long long off = a.block_table ? (row * a.nkv + g) * D + d
-                                      : seq_of(a, b) * a.cache_b_stride + g * a.cache_h_stride + row * D + d;
-  a.k_cache[off] = src[GQA * D + d];
-  a.v_cache[off] = src[(GQA + 1) * D + d];
+    hipLaunchKernelGGL((attn_prep_kernel<D, GQA, 8>), dim3(a.nkv, a.B), dim3(256), 0, s, a, rope_mode, kw);
 }
 
 // One split-K chunk block (c, g, b).  COH: the block's outputs (partials and
@@ -1499,12 +1500,8 @@ template <int D, int GQA>
 static hipError_t launch_tpw(const AttnArgs& a, int rope_mode, hipStream_t s) {
   if (a.prefill && (!a.prep || !a.update_cache)) return hipErrorInvalidValue;
   if (a.s_tkg > 1 && (!a.prep || a.prefill || a.window > 0 || a.B % a.s_tkg)) return hipErrorInvalidValue;
-  if (a.prep) {
-    launch_prep<D, GQA>(a, rope_mode, s);
-    if (hipError_t e = hipGetLastError()) return e;
-  }
-  if (a.prefill) {
-    hipLaunchKernelGGL((attn_kv_write_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(D), 0, s, a);
+  if (a.prep) {   // (a prefill pass: the prepared k / v rows go to the cache as well)
+    launch_prep<D, GQA>(a, rope_mode, s, a.prefill);
     if (hipError_t e = hipGetLastError()) return e;
   }
   const int chunk = a.chunk;
@@ -1572,9 +1569,7 @@ hipError_t attn_prep_launch(const AttnArgs& a, int rope_mode, hipStream_t s) {
 
 template <int D, int GQA>
 static hipError_t launch_prep_write(const AttnArgs& a, int rope_mode, hipStream_t s) {
-  launch_prep<D, GQA>(a, rope_mode, s);
-  if (hipError_t e = hipGetLastError()) return e;
-  hipLaunchKernelGGL((attn_kv_write_kernel<D, GQA>), dim3(a.nkv, a.B), dim3(D), 0, s, a);
+  launch_prep<D, GQA>(a, rope_mode, s, true);
   return hipGetLastError();
 }
 
